@@ -1,0 +1,260 @@
+"""Throughput of the gradtrack training step (forward + backward + Adam::step)
+on one MI355X, on BASELINE config 5: batch 8192, six Linear(4096, 4096) layers
+with bias, ReLU after layers 1-5, MSE loss, fp32, Adam(lr 1e-3).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c5|c4|c1]
+                    [--no-cpu-baseline] [--cpu-sample-rows R]
+
+Prints one JSON line.  `value` is steps/s measured over exactly K steps with
+all inputs resident in HBM.  `roofline` is the fp32-MFMA roofline of the
+dominant kernel class (the GEMMs): algorithmic FLOPs of every GEMM launch in
+the timed region over their summed device-event durations, on the library
+stream.  `cpu_baseline` times the CPU restatement of the reference (oracle/,
+one core) on a bounded sample of the same step and extrapolates to steps/s.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import pathlib
+import sys
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_FP32_MFMA_TFLOPS = 157.3   # MI355X dense fp32 matrix peak (published)
+PEAK_HBM_GBS = 8000.0           # MI355X HBM3E (published)
+
+CONFIGS = {
+    # name: (batch, layer widths, init, relu on the last layer)
+    "c5": (8192, [4096] * 7, "normal"),
+    "c4": (1024, [784, 1024, 10], "kaiming"),
+    "c1": (32, [784, 128], "readme"),
+}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def make_params(TS, widths, init, rng):
+    ps = []
+    for i in range(len(widths) - 1):
+        fan_in, fan_out = widths[i], widths[i + 1]
+        if init == "normal":        # N(0, 1/fan_in)
+            w = rng.standard_normal((fan_in, fan_out), dtype=np.float32) * np.float32(1.0 / np.sqrt(fan_in))
+        elif init == "kaiming":     # Kaiming-uniform U(+-sqrt(6/fan_in))
+            bound = np.float32(np.sqrt(6.0 / fan_in))
+            w = rng.uniform(-bound, bound, (fan_in, fan_out)).astype(np.float32)
+        else:                       # README: W ~ N(0, 1)
+            w = rng.standard_normal((fan_in, fan_out), dtype=np.float32)
+        ps.append(TS.Tensor.from_slice(w, w.shape).with_requires_grad())
+        ps.append(TS.Tensor.zeros([fan_out]).with_requires_grad())
+    return ps
+
+
+def forward_loss(x, t, ps, readme: bool):
+    h = x
+    n = len(ps) // 2
+    for i in range(n):
+        h = h.matmul(ps[2 * i]).add_tensor(ps[2 * i + 1])
+        if i < n - 1 or readme:
+            h = h.relu()
+    if readme:                                   # README.md:71-79: loss = sum(relu(xW + b))
+        return h.sum()
+    return h.sub_tensor(t).pow_scalar(2.0).mean()   # feedforward_network.rs:478-479
+
+
+def step_flops(batch, widths, readme):
+    """Algorithmic GEMM FLOPs of one step: forward, dW for every layer, dX for
+    every layer but the first (x does not require grad)."""
+    f = 0
+    for i in range(len(widths) - 1):
+        mnk = 2.0 * batch * widths[i] * widths[i + 1]
+        f += mnk * (3 if i > 0 else 2)
+    return f
+
+
+def cpu_baseline(cfg_name: str, sample_rows: int):
+    """Single-core CPU restatement (oracle/) of one config-5 step, timed on a
+    bounded sample and scaled: the three GEMM layouts on `sample_rows` output
+    rows, the step's elementwise/reduction passes on 1/64 of the activations,
+    Adam on 1/16 of the parameters."""
+    import oracle as O
+
+    batch, widths, _ = CONFIGS[cfg_name]
+    rng = np.random.default_rng(7)
+    D = widths[1]
+    layers = len(widths) - 1
+    R = min(sample_rows, batch)
+    timings = {}
+
+    X = rng.standard_normal((R, widths[0]), dtype=np.float32)
+    W = rng.standard_normal((widths[0], D), dtype=np.float32)
+    dY = rng.standard_normal((R, D), dtype=np.float32)
+    Xfull_T = rng.standard_normal((batch, R), dtype=np.float32)      # X for the dW slab: [K=batch, M=R]
+    dYfull = rng.standard_normal((batch, D), dtype=np.float32)
+    t0 = time.perf_counter(); O.gemm_f32(X, W); t_nn = time.perf_counter() - t0            # X.W
+    t0 = time.perf_counter(); O.gemm_f32(dY, W, tb=True); t_nt = time.perf_counter() - t0  # dY.W^T
+    t0 = time.perf_counter(); O.gemm_f32(Xfull_T, dYfull, ta=True); t_tn = time.perf_counter() - t0  # X^T.dY
+    scale = batch / R
+    gemm_s = layers * (t_nn * scale) + (layers - 1) * (t_nt * scale) + layers * (t_tn * D / R)
+    timings["gemm_s"] = gemm_s
+
+    # elementwise + reductions of one step on 1/64 of each activation
+    n = batch * D // 64
+    a = rng.standard_normal(n, dtype=np.float32)
+    b = rng.standard_normal(n, dtype=np.float32)
+    bias = rng.standard_normal(D, dtype=np.float32)
+    t0 = time.perf_counter()
+    for _ in range(layers):
+        z = O.bias_add(a.reshape(-1, D), bias)        # forward bias add
+        r = O.relu(z)                                  # forward relu
+        O.relu_bwd(r, b)                               # relu mask gradient
+        O.sum_dim0(b.reshape(-1, D))                   # bias gradient
+        O.add(a, b)                                    # gradient accumulation
+    d = O.sub(a, b); p2 = O.pow2(d); O.mean(p2)        # MSE forward
+    O.pow_bwd(d, b, 2.0); O.fill(n, 1.0)               # MSE backward
+    elem_s = (time.perf_counter() - t0) * 64
+    timings["elementwise_s"] = elem_s
+
+    P = layers * (widths[0] * D + D)
+    ns = P // 16
+    p = rng.standard_normal(ns, dtype=np.float32)
+    g = rng.standard_normal(ns, dtype=np.float32) * np.float32(0.1)
+    m = np.zeros(ns, np.float32)
+    v = np.zeros(ns, np.float32)
+    t0 = time.perf_counter()
+    O.adam_step(p, g, m, v, 1)
+    adam_s = (time.perf_counter() - t0) * 16
+    timings["adam_s"] = adam_s
+    total = gemm_s + elem_s + adam_s
+    sample = (f"GEMM layouts NN/NT/TN on {R} of {batch} output rows (TN: {R} of {D}), "
+              f"elementwise/reduction passes on 1/64 of the activations, Adam on 1/16 of "
+              f"{P} params; scaled to one full step ({total:.1f} s)")
+    return {"value": 1.0 / total, "unit": "steps/s", "cores": 1, "kind": "port",
+            "sample": sample, "breakdown_s": {k: round(v, 3) for k, v in timings.items()}}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c5", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-rows", type=int, default=512)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one GPU: the path is built and measured on "
+                          "a single MI355X (how it would shard is described in DESIGN.md); "
+                          "run with --gpus 1"}))
+        return 2
+
+    import train_station_amd as TS
+    from train_station_amd._ffi import hip, hip_check
+
+    batch, widths, init = CONFIGS[args.config]
+    readme = init == "readme"
+    rng = np.random.default_rng(0)
+    log(f"config {args.config}: batch {batch}, widths {widths}; uploading inputs")
+    ps = make_params(TS, widths, init, rng)
+    x = TS.Tensor.from_slice(rng.standard_normal((batch, widths[0]), dtype=np.float32), [batch, widths[0]])
+    t = TS.Tensor.from_slice(rng.standard_normal((batch, widths[-1]), dtype=np.float32), [batch, widths[-1]])
+    opt = TS.Adam.with_learning_rate(1e-3)
+    opt.add_parameters(ps)
+
+    def step():
+        loss = forward_loss(x, t, ps, readme)
+        loss.backward()
+        opt.step(ps)
+        opt.zero_grad(ps)
+        return loss
+
+    for i in range(args.warmup):
+        loss = step()
+        log(f"warmup step {i}: loss {loss.value():.6f}")
+    TS.synchronize()
+
+    stream = TS.stream()
+    ev0, ev1 = ctypes.c_void_p(), ctypes.c_void_p()
+    hip_check(hip.ts_hip_event_create(ctypes.byref(ev0)))
+    hip_check(hip.ts_hip_event_create(ctypes.byref(ev1)))
+    TS.Profile.reset()
+    TS.Profile.enable(True)
+    TS.synchronize()
+    t0 = time.perf_counter()
+    hip_check(hip.ts_hip_event_record(ev0, stream))
+    for _ in range(args.steps):
+        loss = step()
+    hip_check(hip.ts_hip_event_record(ev1, stream))
+    TS.synchronize()
+    t1 = time.perf_counter()
+    TS.Profile.enable(False)
+    ev_ms = ctypes.c_float()
+    hip_check(hip.ts_hip_event_elapsed_ms(ctypes.byref(ev_ms), ev0, ev1))
+    final_loss = loss.value()
+
+    wall_ms = (t1 - t0) * 1000.0 / args.steps
+    classes = {"gemm": TS.Profile.GEMM, "elementwise": TS.Profile.ELEMENTWISE,
+               "reduction": TS.Profile.REDUCTION, "adam": TS.Profile.ADAM}
+    prof = {k: TS.Profile.read(v) for k, v in classes.items()}
+    g = prof["gemm"]
+    gemm_tflops = g["work"] / (g["ms"] * 1e-3) / 1e12 if g["ms"] > 0 else 0.0
+    kernels = {}
+    for k, s in prof.items():
+        if s["launches"] == 0:
+            continue
+        rate = s["work"] / (s["ms"] * 1e-3) if s["ms"] > 0 else 0.0
+        if k == "gemm":
+            kernels[k] = {"ms_per_step": round(s["ms"] / args.steps, 3), "launches_per_step": s["launches"] // args.steps,
+                          "TFLOP/s": round(rate / 1e12, 2), "frac_mfma_peak": round(rate / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)}
+        else:
+            kernels[k] = {"ms_per_step": round(s["ms"] / args.steps, 3), "launches_per_step": s["launches"] // args.steps,
+                          "GB/s": round(rate / 1e9, 1), "frac_hbm_peak": round(rate / 1e9 / PEAK_HBM_GBS, 4)}
+    per_launch_flops = g["work"] / g["launches"] if g["launches"] else 0.0
+
+    result = {
+        "metric": "fwd+bwd+Adam steps/sec (1 GPU); % fp32 MFMA peak and % HBM GB/s roofline",
+        "value": round(1000.0 / wall_ms, 4),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (numpy default_rng(0); N(0,1/fan_in) weights, N(0,1) inputs and targets)",
+        "config": {"workload": {"c5": "BASELINE config 5: deep wide MLP, batch 8192, 6 x Linear(4096,4096)+bias, "
+                                      "ReLU on layers 1-5, MSE, fwd+bwd+Adam(lr 1e-3)",
+                                "c4": "BASELINE config 4: MLP batch 1024, 784->1024->10, MSE, fwd+bwd+Adam",
+                                "c1": "BASELINE config 1: README step x[32,784] W[784,128], relu, sum, Adam"}[args.config],
+                   "batch": batch, "widths": widths, "gemm_flop_per_step": step_flops(batch, widths, readme)},
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None,
+                     "kernel": "gemm_f32_mfma (all 3 layouts, every launch of the timed region)",
+                     "flop_per_launch": per_launch_flops,
+                     "avg_launch_ms": round(g["ms"] / g["launches"], 4) if g["launches"] else None},
+        "kernels": kernels,
+        "event_ms_per_step": round(ev_ms.value / args.steps, 3),
+        "final_loss": final_loss,
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline (oracle port, one core, bounded sample)")
+        result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_sample_rows) if args.config == "c5" else None
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

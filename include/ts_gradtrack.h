@@ -1,0 +1,117 @@
+/*
+ * ts_gradtrack.h -- C handle API of the host-side mirror of train-station's
+ * Tensor / gradtrack / Adam (libts_gradtrack.so), for callers that are not
+ * C++ (Python ctypes tests and bench, or a foreign host).  Each entry names
+ * the reference method it mirrors.  The library reaches the device only
+ * through include/ts_hip.h.
+ *
+ * Errors: calls returning a pointer return NULL, calls returning int return
+ * -1; ts_last_error() then holds the message (the reference panics with the
+ * same text).  Handles are owned by the caller and released with
+ * ts_tensor_free / ts_adam_free.
+ */
+#ifndef TS_GRADTRACK_H
+#define TS_GRADTRACK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ts_tensor ts_tensor;
+typedef struct ts_adam ts_adam;
+
+const char *ts_last_error(void);
+
+/* Tensor::new (tensor/core/utils.rs:120-171), uninitialised */
+ts_tensor *ts_tensor_new(const size_t *dims, size_t rank);
+/* Tensor::zeros / ones (init/basic.rs:136-180) */
+ts_tensor *ts_tensor_zeros(const size_t *dims, size_t rank);
+ts_tensor *ts_tensor_ones(const size_t *dims, size_t rank);
+/* Tensor::from_slice (init/data.rs:227-247) */
+ts_tensor *ts_tensor_from_slice(const float *data, size_t len, const size_t *dims, size_t rank);
+/* Tensor::clone (core/mod.rs:344-378): new buffer, new id, no grad */
+ts_tensor *ts_tensor_clone(const ts_tensor *t);
+void ts_tensor_free(ts_tensor *t);
+
+uint64_t ts_tensor_id(const ts_tensor *t);
+size_t ts_tensor_rank(const ts_tensor *t);
+size_t ts_tensor_dims(const ts_tensor *t, size_t *dims_out, size_t cap);
+size_t ts_tensor_size(const ts_tensor *t);
+const float *ts_tensor_device_ptr(const ts_tensor *t);
+
+/* with_requires_grad / set_requires_grad / requires_grad (utils.rs:412-450) */
+int ts_tensor_with_requires_grad(ts_tensor *t);
+int ts_tensor_set_requires_grad(ts_tensor *t, int requires_grad);
+int ts_tensor_requires_grad(const ts_tensor *t);
+
+/* recorded ops (tensor/ops/{add,sub,mul,div,relu,pow}.rs, ops/matmul/mod.rs,
+ * tensor/reductions/{sum,mean}.rs) */
+ts_tensor *ts_tensor_add_tensor(const ts_tensor *a, const ts_tensor *b);
+ts_tensor *ts_tensor_sub_tensor(const ts_tensor *a, const ts_tensor *b);
+ts_tensor *ts_tensor_mul_tensor(const ts_tensor *a, const ts_tensor *b);
+ts_tensor *ts_tensor_div_tensor(const ts_tensor *a, const ts_tensor *b);
+ts_tensor *ts_tensor_add_scalar(const ts_tensor *a, float s);
+ts_tensor *ts_tensor_sub_scalar(const ts_tensor *a, float s);
+ts_tensor *ts_tensor_mul_scalar(const ts_tensor *a, float s);
+ts_tensor *ts_tensor_div_scalar(const ts_tensor *a, float s);
+ts_tensor *ts_tensor_relu(const ts_tensor *a);
+ts_tensor *ts_tensor_pow_scalar(const ts_tensor *a, float exponent);
+ts_tensor *ts_tensor_matmul(const ts_tensor *a, const ts_tensor *b);
+ts_tensor *ts_tensor_sum(const ts_tensor *a);
+ts_tensor *ts_tensor_mean(const ts_tensor *a);
+
+/* Tensor::backward(Option<Tensor>) (utils.rs:634-636); grad_output may be NULL */
+int ts_tensor_backward(ts_tensor *t, const ts_tensor *grad_output);
+/* grad_by_value (utils.rs:525-534): a copy, or NULL with ts_last_error() ""
+ * when there is no gradient */
+ts_tensor *ts_tensor_grad_by_value(const ts_tensor *t);
+/* set_grad / zero_grad (utils.rs:766-790) */
+int ts_tensor_set_grad(ts_tensor *t, const ts_tensor *grad);
+int ts_tensor_zero_grad(ts_tensor *t);
+/* data() / value(): device -> host, synchronises (utils.rs:1251-1260) */
+int ts_tensor_data(const ts_tensor *t, float *out, size_t len);
+int ts_tensor_value(const ts_tensor *t, float *out);
+
+/* gradtrack (engine.rs:812-816, no_grad_track.rs:80-235) */
+void ts_clear_gradients(void);
+void ts_no_grad_push(void);
+void ts_no_grad_pop(void);
+int ts_is_grad_enabled(void);
+
+/* Adam (optimizers/adam/mod.rs:227-320, :1036-1068) */
+ts_adam *ts_adam_new(void);
+ts_adam *ts_adam_with_config(float learning_rate, float beta1, float beta2, float eps,
+                             float weight_decay, int amsgrad);
+ts_adam *ts_adam_with_learning_rate(float learning_rate);
+void ts_adam_free(ts_adam *opt);
+int ts_adam_add_parameter(ts_adam *opt, const ts_tensor *param);
+int ts_adam_step(ts_adam *opt, ts_tensor *const *params, size_t count);
+int ts_adam_zero_grad(ts_adam *opt, ts_tensor *const *params, size_t count);
+float ts_adam_learning_rate(const ts_adam *opt);
+void ts_adam_set_learning_rate(ts_adam *opt, float lr);
+uint64_t ts_adam_step_count(const ts_adam *opt);
+/* copy a linked parameter's m or v (which 0 / 1) to the host */
+int ts_adam_state(const ts_adam *opt, const ts_tensor *param, int which, float *out, size_t len);
+
+/* runtime: wait for queued work (reports a recorded division by zero) */
+int ts_synchronize(void);
+/* library stream (for timing events on the stream the kernels run on) */
+void *ts_stream(void);
+/* device pool statistics and cache release */
+size_t ts_pool_live_bytes(void);
+size_t ts_pool_cached_bytes(void);
+void ts_pool_empty_cache(void);
+
+/* kernel timing with device events: class 0 GEMM (work = FLOP), 1 elementwise,
+ * 2 reduction, 3 Adam (work = algorithmic bytes) */
+void ts_profile_enable(int on);
+void ts_profile_reset(void);
+int ts_profile_read(int kernel_class, double *ms, double *work, uint64_t *launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TS_GRADTRACK_H */

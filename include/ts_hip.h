@@ -1,0 +1,204 @@
+/*
+ * ts_hip.h -- C-ABI of the MI355X (gfx950) backend for train-station's
+ * gradtrack training step.
+ *
+ * This is the drop-in replacement for the `extern "C"` block that
+ * train-station binds behind its `cuda` feature
+ * (train-station/src/cuda/mod.rs:139-208, implemented today by the host-only
+ * stub train-station/src/cuda/cuda_wrapper.cpp:19-94).  Conventions kept from
+ * that block:
+ *   - buffer sizes are ELEMENT counts of f32 (cuda/memory.rs:62-76);
+ *   - a NULL stream means the device's default stream (cuda/kernels.rs:37);
+ *   - memcpy kinds are 0 = host->device, 1 = device->host, 2 = device->device.
+ * Changed on purpose: every call returns an int status (0 = success, a HIP
+ * error code, or one of the TS_HIP_E* codes below) instead of a bool, so the
+ * caller can panic with a message from ts_hip_error_string().
+ *
+ * All tensor pointers are device pointers to contiguous row-major f32 data.
+ * Launchers are asynchronous on `stream` and never allocate.
+ * No torch or HIP types appear in these signatures.
+ */
+#ifndef TS_HIP_H
+#define TS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TS_HIP_OK 0
+#define TS_HIP_EINVAL 100001      /* bad argument (shape, NULL pointer, kind) */
+#define TS_HIP_ENODEVICE 100002   /* no gfx950 device visible */
+#define TS_HIP_EWORKSPACE 100003  /* workspace smaller than *_workspace_floats() */
+
+/* ---- runtime -------------------------------------------------------------- */
+
+/* cuda_ffi_initialize (cuda/mod.rs:141): selects device 0, checks it is gfx950 */
+int ts_hip_initialize(void);
+/* cuda_ffi_cleanup (cuda/mod.rs:144) */
+void ts_hip_cleanup(void);
+/* get_cuda_device_count (cuda/mod.rs:147) */
+int ts_hip_get_device_count(int *count);
+/* set_cuda_device (cuda/mod.rs:150) */
+int ts_hip_set_device(int device_id);
+/* get_current_cuda_device (cuda/mod.rs:154) */
+int ts_hip_get_device(int *device_id);
+/* cuda_malloc (cuda/mod.rs:157): *ptr receives room for n_floats f32 values */
+int ts_hip_malloc(float **ptr, size_t n_floats);
+/* cuda_free (cuda/mod.rs:160) */
+int ts_hip_free(float *ptr);
+/* cuda_memcpy (cuda/mod.rs:163): synchronous copy of n_floats values */
+int ts_hip_memcpy(float *dst, const float *src, size_t n_floats, int kind);
+/* hipMemcpyAsync wrapper (no counterpart in the stub; required by the
+ * device Allocation of tensor/core/allocation.rs:43-187) */
+int ts_hip_memcpy_async(float *dst, const float *src, size_t n_floats, int kind, void *stream);
+/* pinned host memory for asynchronous device->host copies */
+int ts_hip_host_malloc(void **ptr, size_t bytes);
+int ts_hip_host_free(void *ptr);
+/* create_cuda_stream / destroy_cuda_stream (cuda/mod.rs:166, 169); streams
+ * are created non-blocking at the default priority */
+int ts_hip_stream_create(void **stream);
+int ts_hip_stream_destroy(void *stream);
+int ts_hip_stream_synchronize(void *stream);
+int ts_hip_device_synchronize(void);
+/* events for timing on a stream (no counterpart in the reference) */
+int ts_hip_event_create(void **event);
+int ts_hip_event_destroy(void *event);
+int ts_hip_event_record(void *event, void *stream);
+int ts_hip_event_synchronize(void *event);
+int ts_hip_event_elapsed_ms(float *ms, void *start, void *stop);
+/* message for a status returned by any ts_hip_* call */
+const char *ts_hip_error_string(int status);
+/* free / total device memory in bytes */
+int ts_hip_mem_info(size_t *free_bytes, size_t *total_bytes);
+
+/* ---- elementwise forward (bit-exact with the reference) -------------------- */
+
+/* launch_add_kernel (cuda/mod.rs:172); ops/add.rs:276-379: out = a + b */
+int ts_hip_add(const float *a, const float *b, float *out, size_t n, void *stream);
+/* launch_sub_kernel (cuda/mod.rs:181); ops/sub.rs:311: out = a - b */
+int ts_hip_sub(const float *a, const float *b, float *out, size_t n, void *stream);
+/* launch_mul_kernel (cuda/mod.rs:190); ops/mul.rs:289-409: out = a * b */
+int ts_hip_mul(const float *a, const float *b, float *out, size_t n, void *stream);
+/* ops/div.rs:291-418: out = a / b (IEEE division).  The reference panics on a
+ * zero divisor at indices i >= zero_check_start (32*floor(n/32) there).  If
+ * zero_index is not NULL it must point to a device uint64 holding UINT64_MAX;
+ * the kernel lowers it to the smallest such index (atomic min). */
+int ts_hip_div(const float *a, const float *b, float *out, size_t n,
+               size_t zero_check_start, unsigned long long *zero_index, void *stream);
+/* ops/{add,sub,mul,div}.rs scalar variants: out = x op s */
+int ts_hip_add_scalar(const float *x, float s, float *out, size_t n, void *stream);
+int ts_hip_sub_scalar(const float *x, float s, float *out, size_t n, void *stream);
+int ts_hip_mul_scalar(const float *x, float s, float *out, size_t n, void *stream);
+int ts_hip_div_scalar(const float *x, float s, float *out, size_t n, void *stream);
+/* core/utils.rs:802-871 negate_inplace: out = 0 - x for i < tail_start,
+ * -x after (tail_start = 8*floor(n/8) reproduces the reference). out may be x. */
+int ts_hip_neg(const float *x, float *out, size_t n, size_t tail_start, void *stream);
+/* ops/relu.rs:117-273: out = x > 0 ? x : +0 */
+int ts_hip_relu(const float *x, float *out, size_t n, void *stream);
+/* ops/pow.rs:79-236 pow_scalar: e == 2 -> x*x, e == 0.5 -> sqrt(x), else powf */
+int ts_hip_pow_scalar(const float *x, float e, float *out, size_t n, void *stream);
+/* ops/add.rs:106-146 with ops/broadcasting.rs:299-478, the row broadcast
+ * [rows,cols] + [cols]: out[r][c] = x[r][c] + bias[c] (bias[c] + x[r][c] when
+ * bias_first), without materialising the broadcast bias. */
+int ts_hip_bias_add(const float *x, const float *bias, float *out, size_t rows, size_t cols,
+                    int bias_first, void *stream);
+/* Row broadcast for the other binary ops (ops/{sub,mul,div}.rs broadcast
+ * paths): op 0 add, 1 sub, 2 mul, 3 div.  out[r][c] = x[r][c] op v[c], or
+ * v[c] op x[r][c] when vec_first.  For div, zero_index as in ts_hip_div over
+ * the flat [rows*cols] index from zero_check_start on. */
+int ts_hip_row_broadcast(int op, const float *x, const float *v, float *out, size_t rows,
+                         size_t cols, int vec_first, size_t zero_check_start,
+                         unsigned long long *zero_index, void *stream);
+/* init/basic.rs:136-326 zeros/ones/fill: out[i] = value */
+int ts_hip_fill(float *out, float value, size_t n, void *stream);
+/* Fill from a device scalar without a host round trip (the upstream gradient
+ * of a scalar loss): out[i] = src[0] (grad_fn/reductions/sum.rs:4-16), or
+ * multiplier * src[0] when use_multiplier (grad_fn/reductions/mean.rs:4-30). */
+int ts_hip_fill_from_device(float *out, const float *src, float multiplier, int use_multiplier,
+                            size_t n, void *stream);
+/* Tensor::clone for contiguous data (core/mod.rs:344-355) */
+int ts_hip_copy(const float *src, float *dst, size_t n, void *stream);
+
+/* ---- elementwise backward -------------------------------------------------- */
+
+/* grad_fn/ops/relu.rs:4-17: gi = x > 0 ? go : 0.  A saved relu OUTPUT may be
+ * passed as x: relu(x) > 0 exactly when x > 0. */
+int ts_hip_relu_backward(const float *x, const float *go, float *gi, size_t n, void *stream);
+/* grad_fn/ops/pow.rs:5-27: gi = go * (e * powf(x, e - 1)) (0 when e == 0) */
+int ts_hip_pow_backward(const float *x, const float *go, float *gi, size_t n, float e,
+                        void *stream);
+/* grad_fn/ops/mul.rs:4-49 same-shape case in one pass: ga = go*b, gb = go*a.
+ * Either output may be NULL. */
+int ts_hip_mul_backward(const float *go, const float *a, const float *b, float *ga, float *gb,
+                        size_t n, void *stream);
+/* grad_fn/ops/div.rs:4-49 same-shape case in one pass:
+ *   ga = go / b;   gb = neg((go * a) / (b * b))   (neg as in ts_hip_neg)
+ * zero_index as in ts_hip_div, covering both divisions of the reference
+ * (divisor b, then b*b) from zero_check_start on.  Either output may be NULL. */
+int ts_hip_div_backward(const float *go, const float *a, const float *b, float *ga, float *gb,
+                        size_t n, size_t tail_start, size_t zero_check_start,
+                        unsigned long long *zero_index, void *stream);
+
+/* ---- reductions ------------------------------------------------------------- */
+
+/* Workspace (device floats) needed by ts_hip_sum / ts_hip_mean for n inputs. */
+size_t ts_hip_sum_workspace_floats(size_t n);
+/* reductions/sum.rs:80-141: out[0] = sum(x).  Deterministic two-pass tree with
+ * f64 partials (not the reference's sequential fp32 order; within 1e-4). */
+int ts_hip_sum(const float *x, size_t n, float *out, float *workspace, size_t workspace_floats,
+               void *stream);
+/* reductions/mean.rs:48-109: out[0] = sum(x) / (float)n */
+int ts_hip_mean(const float *x, size_t n, float *out, float *workspace, size_t workspace_floats,
+                void *stream);
+/* Workspace (device floats) needed by ts_hip_sum_dim0 for [rows,cols]. */
+size_t ts_hip_sum_dim0_workspace_floats(size_t rows, size_t cols);
+/* reductions/sum.rs:225-306 sum_dims(&[0]) on [rows,cols] -> [cols]; the
+ * bias-gradient column reduction of grad_fn/utils.rs:23-60. */
+int ts_hip_sum_dim0(const float *x, size_t rows, size_t cols, float *out, float *workspace,
+                    size_t workspace_floats, void *stream);
+
+/* ---- contractions (fp32 MFMA) ------------------------------------------------ */
+
+/* launch_matmul_kernel (cuda/mod.rs:199): row-major C[m,n] = A[m,k] . B[k,n] */
+int ts_hip_matmul(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,
+                  void *stream);
+/* General form used by matmul forward and backward (ops/matmul/mod.rs:572-611,
+ * grad_fn/ops/matmul.rs:68-80) with the transposes folded into the operand
+ * loads instead of the reference's t().contiguous() copies:
+ *   C[M,N] = op(A)[M,K] . op(B)[K,N]
+ *   trans_a == 0: A(i,k) = A[i*lda + k]   (A stored [M][lda])
+ *   trans_a == 1: A(i,k) = A[k*lda + i]   (A stored [K][lda], i.e. A^T view)
+ *   trans_b == 0: B(k,j) = B[k*ldb + j]   (B stored [K][ldb])
+ *   trans_b == 1: B(k,j) = B[j*ldb + k]   (B stored [N][ldb], i.e. B^T view)
+ *   C(i,j) = C[i*ldc + j]
+ * fp32 inputs, fp32 MFMA accumulation (v_mfma_f32_32x32x2_f32). */
+int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
+                size_t lda, const float *B, size_t ldb, float *C, size_t ldc, void *stream);
+
+/* ---- optimizer ------------------------------------------------------------------ */
+
+/* optimizers/adam/mod.rs:485-1007, one parameter, fused into one pass that
+ * reads p, g, m, v once and writes p, m, v once.  step_count is the
+ * optimizer's global count after its increment (:1036-1044); the bias
+ * corrections are computed on the host exactly as :524-531 (f64 powf, cast to
+ * f32, 1.0f/bc).  Per element, in the reference's fp32 order:
+ *   m = b1*m + (1-b1)*g
+ *   v = b2*v + (1-b2)*(g*g)       i <  tail_start (AVX2 body)
+ *   v = b2*v + ((1-b2)*g)*g       i >= tail_start (scalar tail)
+ *   p = p - (lr*(m*cf1)) / (sqrt(v*cf2) + eps)
+ * tail_start = 8*floor(n/8) reproduces the reference.  weight_decay > 0
+ * first forms g + weight_decay*p (adam/mod.rs:511-518).  AMSGrad
+ * (:534-541): when v_hat_max is not NULL it is set to v*cf2 on the
+ * parameter's first step (amsgrad_first != 0), else to
+ * (v_hat_max > v*cf2 ? v_hat_max : v*cf2), and the update uses it. */
+int ts_hip_adam_step(float *p, const float *g, float *m, float *v, float *v_hat_max, size_t n,
+                     float lr, float beta1, float beta2, float eps, float weight_decay,
+                     uint64_t step_count, size_t tail_start, int amsgrad_first, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TS_HIP_H */

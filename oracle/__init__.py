@@ -1,0 +1,263 @@
+"""CPU oracle for train-station's gradtrack training step.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
+the ``cpu_baseline`` leg of ``bench.py`` may import this package, and only as
+the checker or as the reported CPU baseline.  The product path
+(``train-station_amd/``) never imports, links or calls it.
+
+``libts_oracle.so`` (built from ``ts_oracle.c`` by ``make -C oracle``) holds
+the fp32 arithmetic restated from the reference in its operation order;
+``gradtrack.py`` restates the reference's graph recording, LIFO backward
+worklist and Adam on top of it.  Arrays are numpy float32, C-contiguous.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+
+import numpy as np
+
+_HERE = pathlib.Path(__file__).resolve().parent
+_LIB: ctypes.CDLL | None = None
+
+_F = ctypes.POINTER(ctypes.c_float)
+_D = ctypes.POINTER(ctypes.c_double)
+_SZ = ctypes.c_size_t
+
+
+def lib() -> ctypes.CDLL:
+    """Load libts_oracle.so (built by ``make -C oracle``)."""
+    global _LIB
+    if _LIB is None:
+        path = _HERE / "libts_oracle.so"
+        if not path.exists():
+            raise RuntimeError(f"{path} is missing: run `make -C oracle` (or __graft_entry__.build())")
+        L = ctypes.CDLL(str(path))
+        for name in ("o_add", "o_sub", "o_mul"):
+            getattr(L, name).argtypes = [_F, _F, _F, _SZ]
+        L.o_div.argtypes = [_F, _F, _F, _SZ]
+        L.o_div.restype = ctypes.c_longlong
+        for name in ("o_add_scalar", "o_sub_scalar", "o_mul_scalar", "o_div_scalar"):
+            getattr(L, name).argtypes = [_F, ctypes.c_float, _F, _SZ]
+        L.o_neg.argtypes = [_F, _F, _SZ]
+        L.o_relu.argtypes = [_F, _F, _SZ]
+        L.o_pow2.argtypes = [_F, _F, _SZ]
+        L.o_bias_add.argtypes = [_F, _F, _F, _SZ, _SZ, ctypes.c_int]
+        L.o_fill.argtypes = [_F, ctypes.c_float, _SZ]
+        L.o_relu_bwd.argtypes = [_F, _F, _F, _SZ]
+        L.o_pow_bwd.argtypes = [_F, _F, _F, _SZ, ctypes.c_float]
+        L.o_sum.argtypes = [_F, _SZ]
+        L.o_sum.restype = ctypes.c_float
+        L.o_mean.argtypes = [_F, _SZ]
+        L.o_mean.restype = ctypes.c_float
+        L.o_sum_f64.argtypes = [_F, _SZ]
+        L.o_sum_f64.restype = ctypes.c_double
+        L.o_sum_dim0.argtypes = [_F, _SZ, _SZ, _F]
+        L.o_sum_dim0_f64.argtypes = [_F, _SZ, _SZ, _D]
+        L.o_gemm_f64.argtypes = [ctypes.c_int, ctypes.c_int, _SZ, _SZ, _SZ, _F, _SZ, _F, _SZ, _D]
+        L.o_gemm_f32.argtypes = [ctypes.c_int, ctypes.c_int, _SZ, _SZ, _SZ, _F, _SZ, _F, _SZ, _F, _F, _F]
+        L.o_adam_correction_factor.argtypes = [ctypes.c_float, ctypes.c_uint64]
+        L.o_adam_correction_factor.restype = ctypes.c_float
+        L.o_adam_step.argtypes = [_F, _F, _F, _F, _F, _SZ, ctypes.c_float, ctypes.c_float,
+                                  ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_uint64,
+                                  ctypes.c_int]
+        _LIB = L
+    return _LIB
+
+
+def _f32(x) -> np.ndarray:
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    return a
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(_F)
+
+
+def _binary(name: str, a, b) -> np.ndarray:
+    a, b = _f32(a), _f32(b)
+    assert a.shape == b.shape, (a.shape, b.shape)
+    out = np.empty_like(a)
+    getattr(lib(), name)(_p(a), _p(b), _p(out), a.size)
+    return out
+
+
+def add(a, b):
+    return _binary("o_add", a, b)
+
+
+def sub(a, b):
+    return _binary("o_sub", a, b)
+
+
+def mul(a, b):
+    return _binary("o_mul", a, b)
+
+
+class DivisionByZero(ArithmeticError):
+    """Raised where the reference panics on a zero divisor (ops/div.rs:378-417)."""
+
+
+def div(a, b):
+    a, b = _f32(a), _f32(b)
+    assert a.shape == b.shape
+    out = np.empty_like(a)
+    idx = lib().o_div(_p(a), _p(b), _p(out), a.size)
+    if idx >= 0:
+        raise DivisionByZero(f"Division by zero detected at index {idx}")
+    return out
+
+
+def _scalar(name, x, s):
+    x = _f32(x)
+    out = np.empty_like(x)
+    getattr(lib(), name)(_p(x), ctypes.c_float(s), _p(out), x.size)
+    return out
+
+
+def add_scalar(x, s):
+    return _scalar("o_add_scalar", x, s)
+
+
+def sub_scalar(x, s):
+    return _scalar("o_sub_scalar", x, s)
+
+
+def mul_scalar(x, s):
+    return _scalar("o_mul_scalar", x, s)
+
+
+def div_scalar(x, s):
+    if np.float32(s) == 0:
+        raise DivisionByZero("Division by zero: cannot divide tensor by zero scalar")
+    return _scalar("o_div_scalar", x, s)
+
+
+def _unary(name, x):
+    x = _f32(x)
+    out = np.empty_like(x)
+    getattr(lib(), name)(_p(x), _p(out), x.size)
+    return out
+
+
+def neg(x):
+    return _unary("o_neg", x)
+
+
+def relu(x):
+    return _unary("o_relu", x)
+
+
+def pow2(x):
+    return _unary("o_pow2", x)
+
+
+def bias_add(x, bias, bias_first=False):
+    x, bias = _f32(x), _f32(bias)
+    rows, cols = x.shape
+    assert bias.shape == (cols,)
+    out = np.empty_like(x)
+    lib().o_bias_add(_p(x), _p(bias), _p(out), rows, cols, int(bias_first))
+    return out
+
+
+def fill(shape, v):
+    out = np.empty(shape, dtype=np.float32)
+    lib().o_fill(_p(out), ctypes.c_float(v), out.size)
+    return out
+
+
+def relu_bwd(x, go):
+    x, go = _f32(x), _f32(go)
+    gi = np.empty_like(x)
+    lib().o_relu_bwd(_p(x), _p(go), _p(gi), x.size)
+    return gi
+
+
+def pow_bwd(x, go, exponent):
+    x, go = _f32(x), _f32(go)
+    gi = np.empty_like(x)
+    lib().o_pow_bwd(_p(x), _p(go), _p(gi), x.size, ctypes.c_float(exponent))
+    return gi
+
+
+def sum_(x) -> np.float32:
+    x = _f32(x)
+    return np.float32(lib().o_sum(_p(x), x.size))
+
+
+def mean(x) -> np.float32:
+    x = _f32(x)
+    return np.float32(lib().o_mean(_p(x), x.size))
+
+
+def sum_f64(x) -> float:
+    x = _f32(x)
+    return float(lib().o_sum_f64(_p(x), x.size))
+
+
+def sum_dim0(x):
+    x = _f32(x)
+    rows, cols = x.shape
+    out = np.empty(cols, dtype=np.float32)
+    lib().o_sum_dim0(_p(x), rows, cols, _p(out))
+    return out
+
+
+def sum_dim0_f64(x):
+    x = _f32(x)
+    rows, cols = x.shape
+    out = np.empty(cols, dtype=np.float64)
+    lib().o_sum_dim0_f64(_p(x), rows, cols, out.ctypes.data_as(_D))
+    return out
+
+
+def gemm_f64(a, b, ta=False, tb=False) -> np.ndarray:
+    """op(a) @ op(b) with f64 accumulation; op transposes a [K,M] / b [N,K] view."""
+    a, b = _f32(a), _f32(b)
+    M = a.shape[1] if ta else a.shape[0]
+    K = a.shape[0] if ta else a.shape[1]
+    N = b.shape[0] if tb else b.shape[1]
+    Kb = b.shape[1] if tb else b.shape[0]
+    assert K == Kb, (a.shape, b.shape, ta, tb)
+    out = np.empty((M, N), dtype=np.float64)
+    lib().o_gemm_f64(int(ta), int(tb), M, N, K, _p(a), a.shape[1], _p(b), b.shape[1],
+                     out.ctypes.data_as(_D))
+    return out
+
+
+def gemm_f32(a, b, ta=False, tb=False) -> np.ndarray:
+    """op(a) @ op(b) in fp32 with the reference's sequential-k FMA order."""
+    a, b = _f32(a), _f32(b)
+    M = a.shape[1] if ta else a.shape[0]
+    K = a.shape[0] if ta else a.shape[1]
+    N = b.shape[0] if tb else b.shape[1]
+    out = np.empty((M, N), dtype=np.float32)
+    sa = np.empty(M * K if ta else 1, dtype=np.float32)
+    sb = np.empty(K * N if tb else 1, dtype=np.float32)
+    lib().o_gemm_f32(int(ta), int(tb), M, N, K, _p(a), a.shape[1], _p(b), b.shape[1],
+                     _p(out), _p(sa), _p(sb))
+    return out
+
+
+def adam_correction_factor(beta: float, step_count: int) -> np.float32:
+    return np.float32(lib().o_adam_correction_factor(ctypes.c_float(beta), step_count))
+
+
+def adam_step(p, g, m, v, step_count, lr=1e-3, b1=0.9, b2=0.999, eps=1e-8, weight_decay=0.0,
+              vmax=None, amsgrad_first=False):
+    """In-place Adam update of float32 arrays p, m, v (and vmax under AMSGrad)."""
+    for arr in (p, g, m, v) + ((vmax,) if vmax is not None else ()):
+        assert arr.dtype == np.float32 and arr.flags.c_contiguous
+    lib().o_adam_step(_p(p), _p(g), _p(m), _p(v), _p(vmax) if vmax is not None else None, p.size,
+                      ctypes.c_float(lr), ctypes.c_float(b1), ctypes.c_float(b2),
+                      ctypes.c_float(eps), ctypes.c_float(weight_decay), step_count,
+                      int(amsgrad_first))
+
+
+def build() -> None:
+    """Compile libts_oracle.so in place."""
+    import subprocess
+    subprocess.run(["make", "-B", "-C", str(_HERE)], check=True,
+                   stdout=subprocess.DEVNULL if not os.environ.get("TS_VERBOSE") else None)

@@ -1,0 +1,359 @@
+"""Restatement of train-station's gradtrack engine and Adam on the CPU oracle.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
+
+The control flow follows the reference so that gradient accumulation happens
+in the same order:
+
+* ``OTensor`` ids come from one global counter (tensor/core/mod.rs:131); the
+  recorded graph is ``operations: id -> (input_ids, grad_fn)`` and
+  ``gradients: id -> array`` (gradtrack/engine.rs:175-187, 265-267, 359-361).
+* Tensor ops record a node only when an operand requires grad and gradtrack
+  is enabled; elementwise ops list only the operands that require grad in
+  ``input_ids`` while the backward returns gradients by operand position
+  (ops/add.rs:127-143, ops/sub.rs:149-156); matmul always lists both operands
+  (ops/matmul/mod.rs:291-307); sum/mean record whenever the input requires
+  grad, ignoring the no-grad switch (reductions/sum.rs:131-138).
+* ``backward`` seeds ``ones`` (or the given gradient), then runs the LIFO
+  worklist of engine.rs:962-1047: pop, take the node's gradient, apply its
+  GradFn, accumulate ``existing + new`` into each input
+  (engine.rs:514-524) and push inputs that have an operation.
+* Leaf gradients stay in the map; ``grad_by_value`` returns ``self.grad`` if
+  set, else the map entry (core/utils.rs:525-534).
+* ``OAdam`` follows optimizers/adam/mod.rs:485-553 and :1036-1068.
+
+Matmul uses the f64-accumulated GEMM rounded to fp32 (the reference's blocked
+fp32 kernel is wrong at the configuration shapes, kernels.rs:1092-1133).
+"""
+from __future__ import annotations
+
+import itertools
+import warnings
+from dataclasses import dataclass, field
+from typing import Optional
+
+import numpy as np
+
+import oracle as O
+
+_ids = itertools.count(1)
+
+# thread-local GradGraph of the reference (engine.rs:697-699); one per process here
+_operations: dict[int, tuple[list[int], "GradFn"]] = {}
+_gradients: dict[int, np.ndarray] = {}
+_grad_enabled: list[bool] = [True]
+
+
+def clear_gradients() -> None:
+    """engine.rs:812-816: drops every recorded operation and gradient."""
+    _operations.clear()
+    _gradients.clear()
+
+
+def is_grad_enabled() -> bool:
+    return _grad_enabled[-1]
+
+
+class NoGradTrack:
+    """Context manager form of gradtrack/no_grad_track.rs:80-130."""
+
+    def __enter__(self):
+        _grad_enabled.append(False)
+
+    def __exit__(self, *exc):
+        _grad_enabled.pop()
+
+
+@dataclass
+class GradFn:
+    kind: str
+    saved: list = field(default_factory=list)      # saved arrays (reference clones)
+    shapes: Optional[tuple] = None                  # original_shapes for broadcasting
+    scalar: Optional[float] = None
+    requires: tuple = (True, True)                  # MatMul requires_grad pair
+    numel: int = 0
+
+
+class OTensor:
+    def __init__(self, data: np.ndarray, requires_grad: bool = False):
+        self.data = np.ascontiguousarray(data, dtype=np.float32)
+        self.id = next(_ids)
+        self.requires_grad = requires_grad
+        self.grad: Optional[np.ndarray] = None
+
+    # -- construction ------------------------------------------------------
+    @staticmethod
+    def from_slice(values, dims) -> "OTensor":
+        arr = np.asarray(values, dtype=np.float32).reshape(dims)
+        return OTensor(arr.copy())
+
+    def with_requires_grad(self) -> "OTensor":
+        self.requires_grad = True
+        return self
+
+    @property
+    def shape(self):
+        return self.data.shape
+
+    def size(self) -> int:
+        return self.data.size
+
+    # -- helpers -----------------------------------------------------------
+    def _record(self, out: "OTensor", input_ids: list[int], fn: GradFn) -> "OTensor":
+        out.requires_grad = True
+        _operations[out.id] = (input_ids, fn)
+        return out
+
+    def _elementwise(self, other: "OTensor", kind: str, same, bias_fn) -> "OTensor":
+        if self.shape == other.shape:
+            out = OTensor(same(self.data, other.data))
+            shapes = None
+        else:
+            out = OTensor(bias_fn(self.data, other.data))
+            shapes = (self.shape, other.shape)
+        if (self.requires_grad or other.requires_grad) and is_grad_enabled():
+            ids = [t.id for t in (self, other) if t.requires_grad]
+            saved = [self.data, other.data] if kind in ("mul", "div") else []
+            self._record(out, ids, GradFn(kind, saved=saved, shapes=shapes))
+        return out
+
+    # -- recorded ops (forward) --------------------------------------------
+    def add_tensor(self, other):
+        return self._elementwise(other, "add", O.add, _broadcast(O.add))
+
+    def sub_tensor(self, other):
+        return self._elementwise(other, "sub", O.sub, _broadcast(O.sub))
+
+    def mul_tensor(self, other):
+        return self._elementwise(other, "mul", O.mul, _broadcast(O.mul))
+
+    def div_tensor(self, other):
+        return self._elementwise(other, "div", O.div, _broadcast(O.div))
+
+    def _scalar_op(self, kind, fn, s):
+        out = OTensor(fn(self.data, s))
+        if self.requires_grad and is_grad_enabled():
+            self._record(out, [self.id], GradFn(kind + "_scalar", scalar=s))
+        return out
+
+    def add_scalar(self, s):
+        return self._scalar_op("add", O.add_scalar, s)
+
+    def sub_scalar(self, s):
+        return self._scalar_op("sub", O.sub_scalar, s)
+
+    def mul_scalar(self, s):
+        return self._scalar_op("mul", O.mul_scalar, s)
+
+    def div_scalar(self, s):
+        return self._scalar_op("div", O.div_scalar, s)
+
+    def relu(self):
+        out = OTensor(O.relu(self.data))
+        if self.requires_grad and is_grad_enabled():
+            self._record(out, [self.id], GradFn("relu", saved=[self.data]))
+        return out
+
+    def pow_scalar(self, e: float):
+        if np.float32(e) != 2.0:
+            raise NotImplementedError("the oracle restates exponent 2.0 only (ops/pow.rs:124-162)")
+        out = OTensor(O.pow2(self.data))
+        if self.requires_grad and is_grad_enabled():
+            self._record(out, [self.id], GradFn("pow", saved=[self.data], scalar=float(e)))
+        return out
+
+    def matmul(self, other):
+        assert self.data.ndim == 2 and other.data.ndim == 2
+        out = OTensor(O.gemm_f64(self.data, other.data).astype(np.float32))
+        if (self.requires_grad or other.requires_grad) and is_grad_enabled():
+            self._record(out, [self.id, other.id],
+                         GradFn("matmul", saved=[self.data, other.data],
+                                requires=(self.requires_grad, other.requires_grad)))
+        return out
+
+    def sum(self):
+        out = OTensor(np.array([O.sum_(self.data)], dtype=np.float32))
+        if self.requires_grad:
+            self._record(out, [self.id], GradFn("sum", shapes=(self.shape,)))
+        return out
+
+    def mean(self):
+        out = OTensor(np.array([O.mean(self.data)], dtype=np.float32))
+        if self.requires_grad:
+            self._record(out, [self.id], GradFn("mean", shapes=(self.shape,), numel=self.size()))
+        return out
+
+    # -- autograd ------------------------------------------------------------
+    def backward(self, grad_output: Optional[np.ndarray] = None) -> None:
+        backward(self, grad_output)
+
+    def grad_by_value(self) -> Optional[np.ndarray]:
+        if self.grad is not None:
+            return self.grad.copy()
+        g = _gradients.get(self.id)
+        return None if g is None else g.copy()
+
+    def zero_grad(self) -> None:
+        self.grad = None
+
+    def value(self) -> float:
+        assert self.size() == 1
+        return float(self.data.reshape(-1)[0])
+
+
+def _broadcast(fn):
+    """[B,N] op [N] (or [N] op [B,N]) after materialising the 1-D operand
+    (ops/broadcasting.rs:299-478); only the row-broadcast case is restated."""
+
+    def apply(a, b):
+        if a.ndim == 2 and b.ndim == 1 and b.shape[0] == a.shape[1]:
+            return fn(a, np.broadcast_to(b, a.shape).copy())
+        if a.ndim == 1 and b.ndim == 2 and a.shape[0] == b.shape[1]:
+            return fn(np.broadcast_to(a, b.shape).copy(), b)
+        raise ValueError(f"Cannot broadcast tensor shapes {a.shape} and {b.shape}")
+
+    return apply
+
+
+def _reduce_to(g: np.ndarray, shape) -> np.ndarray:
+    """grad_fn/utils.rs:23-60 for the row-broadcast case: sum_dims(&[0])."""
+    if g.shape == tuple(shape):
+        return g
+    assert g.ndim == 2 and len(shape) == 1, (g.shape, shape)
+    return O.sum_dim0(g)
+
+
+def _apply(fn: GradFn, go: np.ndarray) -> list[Optional[np.ndarray]]:
+    """GradFn::apply (grad_fn/mod.rs:490-789) for the variants on the path."""
+    k = fn.kind
+    if k == "add":                                   # grad_fn/ops/add.rs:4-28
+        if fn.shapes is None:
+            return [go, go]
+        return [_reduce_to(go, fn.shapes[0]), _reduce_to(go, fn.shapes[1])]
+    if k == "sub":                                   # grad_fn/ops/sub.rs:4-33
+        if fn.shapes is None:
+            return [go, O.neg(go)]
+        return [_reduce_to(go, fn.shapes[0]), O.neg(_reduce_to(go, fn.shapes[1]))]
+    if k == "mul":                                   # grad_fn/ops/mul.rs:4-49
+        a, b = fn.saved
+        if fn.shapes is None:
+            return [O.mul(go, b), O.mul(go, a)]
+        ab, bb = np.broadcast_arrays(a, b)
+        return [_reduce_to(O.mul(go, np.ascontiguousarray(bb)), fn.shapes[0]),
+                _reduce_to(O.mul(go, np.ascontiguousarray(ab)), fn.shapes[1])]
+    if k == "div":                                   # grad_fn/ops/div.rs:4-49
+        a, b = fn.saved
+        if fn.shapes is not None:
+            ab, bb = np.broadcast_arrays(a, b)
+            a, b = np.ascontiguousarray(ab), np.ascontiguousarray(bb)
+        ga = O.div(go, b)
+        gb = O.neg(O.div(O.mul(go, a), O.mul(b, b)))
+        if fn.shapes is None:
+            return [ga, gb]
+        return [_reduce_to(ga, fn.shapes[0]), _reduce_to(gb, fn.shapes[1])]
+    if k in ("add_scalar", "sub_scalar"):
+        return [go]
+    if k == "mul_scalar":
+        return [O.mul_scalar(go, fn.scalar)]
+    if k == "div_scalar":
+        return [O.div_scalar(go, fn.scalar)]
+    if k == "relu":                                  # grad_fn/ops/relu.rs:4-17
+        return [O.relu_bwd(fn.saved[0], go)]
+    if k == "pow":                                   # grad_fn/ops/pow.rs:5-27
+        return [O.pow_bwd(fn.saved[0], go, fn.scalar)]
+    if k == "matmul":                                # grad_fn/ops/matmul.rs:68-80
+        a, b = fn.saved
+        gl = O.gemm_f64(go, b, tb=True).astype(np.float32) if fn.requires[0] else None
+        gr = O.gemm_f64(a, go, ta=True).astype(np.float32) if fn.requires[1] else None
+        return [gl, gr]
+    if k == "sum":                                   # grad_fn/reductions/sum.rs:4-16
+        shape = fn.shapes[0]
+        if go.size == 1:
+            return [O.fill(shape, float(go.reshape(-1)[0]))]
+        return [O.fill(shape, 1.0)]
+    if k == "mean":                                  # grad_fn/reductions/mean.rs:4-30
+        shape = fn.shapes[0]
+        base = np.float32(1.0) / np.float32(fn.numel) if fn.numel > 0 else np.float32(0.0)
+        if go.size == 1:
+            return [O.fill(shape, float(base * np.float32(go.reshape(-1)[0])))]
+        return [O.fill(shape, float(base))]
+    raise NotImplementedError(k)
+
+
+def backward(t: OTensor, grad_output: Optional[np.ndarray] = None) -> None:
+    """GradEngine::backward (engine.rs:962-1047)."""
+    init = O.fill(t.shape, 1.0) if grad_output is None else np.ascontiguousarray(grad_output, np.float32)
+    if t.requires_grad:                                            # utils.rs:735 accumulate_grad
+        t.grad = init if t.grad is None else O.add(t.grad, init)
+    _gradients[t.id] = init
+    work = [t.id]
+    while work:
+        node = work.pop()
+        op = _operations.get(node)
+        if op is None:
+            continue
+        current = _gradients.pop(node, None)
+        if current is None:
+            continue
+        input_ids, fn = op
+        grads = _apply(fn, current)
+        for idx, iid in enumerate(input_ids):
+            if idx < len(grads) and grads[idx] is not None:
+                g = grads[idx]
+                if iid in _gradients:                              # engine.rs:514-524
+                    _gradients[iid] = O.add(_gradients[iid], g)
+                else:
+                    _gradients[iid] = g
+                if iid in _operations:
+                    work.append(iid)
+
+
+@dataclass
+class _AdamState:
+    m: np.ndarray
+    v: np.ndarray
+    step: int = 0
+    vmax: Optional[np.ndarray] = None
+
+
+class OAdam:
+    """optimizers/adam/mod.rs (AdamConfig of :90-117)."""
+
+    def __init__(self, learning_rate=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0,
+                 amsgrad=False):
+        self.lr, self.b1, self.b2, self.eps = learning_rate, beta1, beta2, eps
+        self.weight_decay, self.amsgrad = weight_decay, amsgrad
+        self.states: dict[int, _AdamState] = {}
+        self.step_count = 0
+
+    def add_parameter(self, p: OTensor) -> None:
+        assert p.requires_grad, "Parameter must require gradients"
+        self.states[p.id] = _AdamState(np.zeros(p.size(), np.float32), np.zeros(p.size(), np.float32))
+
+    def add_parameters(self, ps) -> None:
+        for p in ps:
+            self.add_parameter(p)
+
+    def step(self, params) -> None:
+        self.step_count += 1                                          # :1036-1044
+        for p in params:
+            assert p.id in self.states, "Parameter must be linked to optimizer before stepping"
+            g = p.grad_by_value()
+            if g is None:
+                warnings.warn(f"Failed to update parameter: Parameter {p.id} has no gradient")
+                continue
+            st = self.states[p.id]
+            st.step += 1
+            first = False
+            if self.amsgrad and st.vmax is None:
+                st.vmax = np.zeros_like(st.m)
+                first = True
+            flat = p.data.reshape(-1)
+            O.adam_step(flat, np.ascontiguousarray(g.reshape(-1)), st.m, st.v, self.step_count,
+                        self.lr, self.b1, self.b2, self.eps, self.weight_decay,
+                        st.vmax if self.amsgrad else None, first)
+
+    def zero_grad(self, params) -> None:
+        for p in params:
+            p.zero_grad()
+        clear_gradients()

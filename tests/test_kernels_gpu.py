@@ -1,0 +1,284 @@
+"""Kernel-level parity of libts_hip.so against the CPU oracle, through the
+C-ABI of include/ts_hip.h.  Bit-exact for elementwise ops, ReLU masks and
+Adam; <= 1e-4 normwise relative error (max|d| / max|ref|) for GEMMs and
+reductions, as the parity bar for this path states."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import assert_bits_equal, max_rel, normal, uniform
+from gpu_util import Dev, ZeroIndex, hip, hip_check, sync
+
+pytestmark = pytest.mark.gpu
+
+SIZES = [1, 3, 7, 8, 31, 32, 33, 1000, (1 << 20) + 5]
+SPECIAL = np.array([0.0, -0.0, 1.0, -1.0, 1e-45, -1e-45, 1e-38, 3.4e38, -3.4e38, np.inf,
+                    -np.inf, np.nan, 0.5, 2.0, 1e30, -1e-30], dtype=np.float32)
+
+
+def _with_special(x):
+    x = x.copy()
+    k = min(x.size, SPECIAL.size)
+    x.reshape(-1)[:k] = SPECIAL[:k]
+    return x
+
+
+def _run(name, *args):
+    hip_check(getattr(hip, name)(*args), name)
+    sync()
+
+
+@pytest.mark.parametrize("offset", [0, 1])
+@pytest.mark.parametrize("n", SIZES)
+def test_binary_elementwise_bit_exact(oracle, n, offset):
+    print(f"[binary] n={n} offset={offset}", flush=True)
+    a = _with_special(normal(n, 1))
+    b = _with_special(normal(n, 2))[::-1].copy()
+    da, db, do = Dev.of(a, offset), Dev.of(b, offset), Dev(n, offset)
+    for name, ref in (("ts_hip_add", oracle.add), ("ts_hip_sub", oracle.sub), ("ts_hip_mul", oracle.mul)):
+        _run(name, da.ptr, db.ptr, do.ptr, n, None)
+        assert_bits_equal(do.get(), ref(a, b), name)
+    bz = b.copy()
+    bz[bz == 0] = 1.5
+    dbz = Dev.of(bz, offset)
+    _run("ts_hip_div", da.ptr, dbz.ptr, do.ptr, n, (n // 32) * 32, None, None)
+    assert_bits_equal(do.get(), oracle.div(a, bz), "ts_hip_div")
+
+
+@pytest.mark.parametrize("n", [1, 9, 1000, (1 << 20) + 3])
+def test_unary_and_scalar_bit_exact(oracle, n):
+    print(f"[unary] n={n}", flush=True)
+    x = _with_special(normal(n, 3))
+    dx, do = Dev.of(x), Dev(n)
+    _run("ts_hip_relu", dx.ptr, do.ptr, n, None)
+    assert_bits_equal(do.get(), oracle.relu(x), "relu")
+    _run("ts_hip_neg", dx.ptr, do.ptr, n, (n // 8) * 8, None)
+    assert_bits_equal(do.get(), oracle.neg(x), "neg")
+    _run("ts_hip_pow_scalar", dx.ptr, 2.0, do.ptr, n, None)
+    assert_bits_equal(do.get(), oracle.pow2(x), "pow2")
+    ax = np.abs(x)
+    dax = Dev.of(ax)
+    _run("ts_hip_pow_scalar", dax.ptr, 0.5, do.ptr, n, None)
+    assert_bits_equal(do.get(), np.sqrt(ax), "pow 0.5 (IEEE sqrt)")
+    for s in (2.0, -0.5, 1e-3):
+        for name, ref in (("ts_hip_add_scalar", oracle.add_scalar), ("ts_hip_sub_scalar", oracle.sub_scalar),
+                          ("ts_hip_mul_scalar", oracle.mul_scalar), ("ts_hip_div_scalar", oracle.div_scalar)):
+            _run(name, dx.ptr, s, do.ptr, n, None)
+            assert_bits_equal(do.get(), ref(x, s), f"{name}({s})")
+    _run("ts_hip_fill", do.ptr, -2.5, n, None)
+    assert np.all(do.get() == np.float32(-2.5))
+    _run("ts_hip_copy", dx.ptr, do.ptr, n, None)
+    assert_bits_equal(do.get(), x, "copy")
+    src = Dev.of(np.array([0.75], np.float32))
+    _run("ts_hip_fill_from_device", do.ptr, src.ptr, 0.0, 0, n, None)
+    assert np.all(do.get() == np.float32(0.75))
+    base = np.float32(1.0) / np.float32(n)
+    _run("ts_hip_fill_from_device", do.ptr, src.ptr, float(base), 1, n, None)
+    assert np.all(do.get() == np.float32(base * np.float32(0.75)))
+
+
+def test_negate_tail_zero_sign():
+    z = np.zeros(13, np.float32)
+    dz, do = Dev.of(z), Dev(13)
+    _run("ts_hip_neg", dz.ptr, do.ptr, 13, 8, None)
+    out = do.get()
+    assert not np.any(np.signbit(out[:8])) and np.all(np.signbit(out[8:]))
+
+
+@pytest.mark.parametrize("n", [5, 64, 1000, (1 << 20) + 7])
+def test_backward_elementwise_bit_exact(oracle, n):
+    print(f"[backward] n={n}", flush=True)
+    x = _with_special(normal(n, 4))
+    go = normal(n, 5)
+    a = normal(n, 6)
+    b = uniform(n, 0.5, 2.0, 7) * np.where(np.arange(n) % 3 == 0, -1, 1).astype(np.float32)
+    dx, dgo, da, db = Dev.of(x), Dev.of(go), Dev.of(a), Dev.of(b)
+    o1, o2 = Dev(n), Dev(n)
+    _run("ts_hip_relu_backward", dx.ptr, dgo.ptr, o1.ptr, n, None)
+    assert_bits_equal(o1.get(), oracle.relu_bwd(x, go), "relu_backward")
+    # a saved relu OUTPUT gives the same mask as its input
+    dy = Dev.of(oracle.relu(x))
+    _run("ts_hip_relu_backward", dy.ptr, dgo.ptr, o1.ptr, n, None)
+    assert_bits_equal(o1.get(), oracle.relu_bwd(x, go), "relu_backward from output")
+    _run("ts_hip_pow_backward", dx.ptr, dgo.ptr, o1.ptr, n, 2.0, None)
+    assert_bits_equal(o1.get(), oracle.pow_bwd(x, go, 2.0), "pow_backward")
+    _run("ts_hip_mul_backward", dgo.ptr, da.ptr, db.ptr, o1.ptr, o2.ptr, n, None)
+    assert_bits_equal(o1.get(), oracle.mul(go, b), "mul_backward ga")
+    assert_bits_equal(o2.get(), oracle.mul(go, a), "mul_backward gb")
+    _run("ts_hip_div_backward", dgo.ptr, da.ptr, db.ptr, o1.ptr, o2.ptr, n, (n // 8) * 8,
+         (n // 32) * 32, None, None)
+    assert_bits_equal(o1.get(), oracle.div(go, b), "div_backward ga")
+    want_gb = oracle.neg(oracle.div(oracle.mul(go, a), oracle.mul(b, b)))
+    assert_bits_equal(o2.get(), want_gb, "div_backward gb")
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (32, 128), (1024, 10), (33, 7), (8192, 4096)])
+def test_row_broadcast_bit_exact(oracle, rows, cols):
+    print(f"[row_broadcast] {rows}x{cols}", flush=True)
+    x = normal((rows, cols), 8)
+    v = uniform(cols, 0.5, 2.0, 9)
+    dx, dv, do = Dev.of(x), Dev.of(v), Dev(rows * cols)
+    _run("ts_hip_bias_add", dx.ptr, dv.ptr, do.ptr, rows, cols, 0, None)
+    assert_bits_equal(do.get((rows, cols)), oracle.bias_add(x, v), "bias_add")
+    vb = np.broadcast_to(v, x.shape)
+    refs = {0: oracle.add, 1: oracle.sub, 2: oracle.mul, 3: oracle.div}
+    for op, ref in refs.items():
+        for vec_first in (0, 1):
+            _run("ts_hip_row_broadcast", op, dx.ptr, dv.ptr, do.ptr, rows, cols, vec_first, 0, None, None)
+            want = ref(vb, x) if vec_first else ref(x, vb)
+            assert_bits_equal(do.get((rows, cols)), want, f"row_broadcast op={op} vec_first={vec_first}")
+
+
+def test_division_zero_index_reports_tail_only():
+    n = 40
+    a = np.ones(n, np.float32)
+    b = np.ones(n, np.float32)
+    b[3] = 0.0      # inside the reference's unchecked 32-wide body
+    da, db, do = Dev.of(a), Dev.of(b), Dev(n)
+    zi = ZeroIndex()
+    _run("ts_hip_div", da.ptr, db.ptr, do.ptr, n, 32, zi.ptr, None)
+    assert zi.value() is None
+    b[37] = 0.0
+    b[35] = 0.0
+    db.put(b)
+    _run("ts_hip_div", da.ptr, db.ptr, do.ptr, n, 32, zi.ptr, None)
+    assert zi.value() == 35
+
+
+@pytest.mark.parametrize("n", [0, 1, 5, 4096, 100003, 1 << 26])
+def test_sum_and_mean(oracle, n):
+    print(f"[sum] n={n}", flush=True)
+    x = normal(n, 10)
+    dx = Dev.of(x)
+    ws = hip.ts_hip_sum_workspace_floats(n)
+    dws, dout = Dev(ws), Dev(1)
+    _run("ts_hip_sum", dx.ptr if n else None, n, dout.ptr, dws.ptr, ws, None)
+    exact = oracle.sum_f64(x)
+    scale = max(float(np.sum(np.abs(x), dtype=np.float64)), 1e-30)
+    assert abs(float(dout.get()[0]) - exact) <= 1e-6 * scale + 1e-30
+    _run("ts_hip_mean", dx.ptr if n else None, n, dout.ptr, dws.ptr, ws, None)
+    if n:
+        assert abs(float(dout.get()[0]) - exact / n) <= 1e-6 * scale / n
+    else:
+        assert float(dout.get()[0]) == 0.0
+    if n:  # too small a workspace is refused, not overrun
+        assert hip.ts_hip_sum(dx.ptr, n, dout.ptr, dws.ptr, ws - 1, None) == 100003
+
+
+def test_sum_known_answers():
+    for xs, want in (([i * 0.5 for i in range(6)], 7.5), ([1, 2, 3, 4, 5, 6], 21.0),
+                     (list(range(24)), 276.0)):
+        x = np.array(xs, np.float32)
+        dx, dws, dout = Dev.of(x), Dev(hip.ts_hip_sum_workspace_floats(x.size)), Dev(1)
+        _run("ts_hip_sum", dx.ptr, x.size, dout.ptr, dws.ptr, dws.n, None)
+        assert float(dout.get()[0]) == want
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (2, 4), (32, 128), (1024, 10), (33, 7), (1024, 1024),
+                                       (8192, 4096)])
+def test_sum_dim0(oracle, rows, cols):
+    print(f"[sum_dim0] {rows}x{cols}", flush=True)
+    x = normal((rows, cols), 11)
+    ws = hip.ts_hip_sum_dim0_workspace_floats(rows, cols)
+    dx, dws, do = Dev.of(x), Dev(ws), Dev(cols)
+    _run("ts_hip_sum_dim0", dx.ptr, rows, cols, do.ptr, dws.ptr, ws, None)
+    want = oracle.sum_dim0_f64(x)
+    got = do.get()
+    assert max_rel(got, want) <= 1e-6
+    if rows * cols <= 1 << 16:
+        assert max_rel(got, oracle.sum_dim0(x)) <= 1e-4   # the reference's fp32 row order
+
+
+GEMM_SHAPES = [(1, 1, 1), (2, 2, 2), (32, 128, 784), (784, 128, 32), (129, 127, 33), (1024, 10, 1024),
+               (1024, 1024, 10), (1024, 1024, 784), (784, 1024, 1024), (300, 200, 4096)]
+
+
+def _gemm_case(oracle, ta, tb, M, N, K, seed, check_rows=None):
+    a = normal((K, M) if ta else (M, K), seed)
+    b = normal((N, K) if tb else (K, N), seed + 1)
+    da, db, dc = Dev.of(a), Dev.of(b), Dev(M * N)
+    lda = M if ta else K
+    ldb = K if tb else N
+    _run("ts_hip_gemm", int(ta), int(tb), M, N, K, da.ptr, lda, db.ptr, ldb, dc.ptr, N, None)
+    got = dc.get((M, N))
+    if check_rows is None:
+        want = oracle.gemm_f64(a, b, ta=ta, tb=tb)
+        return got, want
+    rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(seed).integers(0, M, check_rows)]))
+    a_rows = (a[:, rows].T if ta else a[rows, :]).copy()
+    want = oracle.gemm_f64(a_rows, b, ta=False, tb=tb)
+    return got[rows], want
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+def test_gemm_layouts(oracle, ta, tb, M, N, K):
+    print(f"[gemm] ta={ta} tb={tb} M={M} N={N} K={K}", flush=True)
+    got, want = _gemm_case(oracle, ta, tb, M, N, K, seed=M + N + K)
+    assert max_rel(got, want) <= 1e-4, (M, N, K, ta, tb)
+
+
+def test_gemm_known_answer():
+    a = np.array([[1, 2], [3, 4]], np.float32)
+    b = np.array([[5, 6], [7, 8]], np.float32)
+    da, db, dc = Dev.of(a), Dev.of(b), Dev(4)
+    _run("ts_hip_matmul", da.ptr, db.ptr, dc.ptr, 2, 2, 2, None)
+    assert dc.get().tolist() == [19.0, 22.0, 43.0, 50.0]
+
+
+@pytest.mark.parametrize("ta,tb,M,N,K", [(0, 0, 8192, 4096, 4096), (0, 1, 8192, 4096, 4096),
+                                         (1, 0, 4096, 4096, 8192)])
+def test_gemm_full_size_sampled_rows(oracle, ta, tb, M, N, K):
+    # BASELINE config 5 contractions at their real shape: forward X.W, dX = dY.W^T,
+    # dW = X^T.dY; f64 check on 24 sampled rows of C
+    print(f"[gemm full] ta={ta} tb={tb} M={M} N={N} K={K}", flush=True)
+    got, want = _gemm_case(oracle, bool(ta), bool(tb), M, N, K, seed=5, check_rows=24)
+    assert max_rel(got, want) <= 1e-4
+
+
+def test_gemm_rejects_bad_leading_dimension():
+    d = Dev(64)
+    assert hip.ts_hip_gemm(0, 0, 8, 8, 8, d.ptr, 4, d.ptr, 8, d.ptr, 8, None) == 100001
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 9, 1000, (1 << 20) + 3])
+@pytest.mark.parametrize("mode", ["plain", "weight_decay", "amsgrad"])
+def test_adam_bit_exact(oracle, n, mode):
+    print(f"[adam] n={n} mode={mode}", flush=True)
+    p = normal(n, 12)
+    g = normal(n, 13, 0.1)
+    m = np.zeros(n, np.float32)
+    v = np.zeros(n, np.float32)
+    wd = 0.01 if mode == "weight_decay" else 0.0
+    vm = np.zeros(n, np.float32) if mode == "amsgrad" else None
+    dp, dg, dm, dv = Dev.of(p), Dev.of(g), Dev.of(m), Dev.of(v)
+    dvm = Dev.of(vm) if vm is not None else None
+    for step in range(1, 11):
+        g = normal(n, 100 + step, 0.1)
+        dg.put(g)
+        _run("ts_hip_adam_step", dp.ptr, dg.ptr, dm.ptr, dv.ptr, dvm.ptr if dvm else None, n, 1e-3,
+             0.9, 0.999, 1e-8, wd, step, (n // 8) * 8, int(step == 1), None)
+        oracle.adam_step(p, g, m, v, step, weight_decay=wd, vmax=vm, amsgrad_first=(step == 1))
+    assert_bits_equal(dp.get(), p, "p")
+    assert_bits_equal(dm.get(), m, "m")
+    assert_bits_equal(dv.get(), v, "v")
+    if vm is not None:
+        assert_bits_equal(dvm.get(), vm, "v_hat_max")
+
+
+def test_adam_100_steps_bit_exact(oracle):
+    # BASELINE config 3 (Adam alone, constant gradient set once, m = v = 0) at 2^22 params
+    n = 1 << 22
+    p = normal(n, 14)
+    g = normal(n, 15, 0.1)
+    m = np.zeros(n, np.float32)
+    v = np.zeros(n, np.float32)
+    dp, dg, dm, dv = Dev.of(p), Dev.of(g), Dev.of(m), Dev.of(v)
+    for step in range(1, 101):
+        hip_check(hip.ts_hip_adam_step(dp.ptr, dg.ptr, dm.ptr, dv.ptr, None, n, 1e-3, 0.9, 0.999, 1e-8,
+                                       0.0, step, n, 0, None), "adam")
+        oracle.adam_step(p, g, m, v, step)
+    sync()
+    assert_bits_equal(dp.get(), p, "p after 100 steps")
+    assert_bits_equal(dv.get(), v, "v after 100 steps")

@@ -1,0 +1,222 @@
+"""Pins the CPU oracle (oracle/ts_oracle.c) against checks that do not restate it:
+the reference's own known answers, torch CPU (an independent IEEE fp32 /
+float64 implementation), closed forms and brute force.  CPU only."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_bits_equal, golden, max_rel, normal, uniform
+
+SPECIAL = np.array([0.0, -0.0, 1.0, -1.0, 1e-45, -1e-45, 1e-38, 3.4e38, -3.4e38, np.inf, -np.inf,
+                    0.5, 2.0, 1e30, -1e-30, 7.0], dtype=np.float32)
+
+
+def _inputs(n, seed):
+    a = normal(n, seed)
+    b = normal(n, seed + 1)
+    a[: SPECIAL.size] = SPECIAL
+    b[: SPECIAL.size] = SPECIAL[::-1]
+    return a, b
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 33, 1000])
+def test_binary_ops_match_torch_bits(oracle, n):
+    a, b = _inputs(max(n, 16), 3)
+    a, b = a[:n], b[:n]
+    ta, tb = torch.from_numpy(a), torch.from_numpy(b)
+    assert_bits_equal(oracle.add(a, b), (ta + tb).numpy(), "add")
+    assert_bits_equal(oracle.sub(a, b), (ta - tb).numpy(), "sub")
+    assert_bits_equal(oracle.mul(a, b), (ta * tb).numpy(), "mul")
+    nz = b.copy()
+    nz[nz == 0] = 3.0
+    assert_bits_equal(oracle.div(a, nz), (ta / torch.from_numpy(nz)).numpy(), "div")
+
+
+def test_scalar_ops_match_torch_bits(oracle):
+    x = normal(257, 5)
+    tx = torch.from_numpy(x)
+    for s in (2.0, -0.5, 1e-3, 3.0):
+        sf = torch.tensor(s, dtype=torch.float32)
+        assert_bits_equal(oracle.add_scalar(x, s), (tx + sf).numpy(), "add_scalar")
+        assert_bits_equal(oracle.sub_scalar(x, s), (tx - sf).numpy(), "sub_scalar")
+        assert_bits_equal(oracle.mul_scalar(x, s), (tx * sf).numpy(), "mul_scalar")
+        assert_bits_equal(oracle.div_scalar(x, s), (tx / sf).numpy(), "div_scalar")
+
+
+def test_pow2_and_bias_add_match_torch_bits(oracle):
+    x = normal((37, 41), 7)
+    x.reshape(-1)[:SPECIAL.size] = SPECIAL
+    assert_bits_equal(oracle.pow2(x), (torch.from_numpy(x) * torch.from_numpy(x)).numpy(), "pow2")
+    bias = normal(41, 8)
+    want = (torch.from_numpy(x) + torch.from_numpy(bias)).numpy()
+    assert_bits_equal(oracle.bias_add(x, bias), want, "bias_add")
+    assert_bits_equal(oracle.bias_add(x, bias, bias_first=True), want, "bias_add (bias first)")
+
+
+def test_relu_known_answers_and_ieee_cases(oracle):
+    ka = golden("known_answers.json")["relu_forward"]          # relu.rs:280-291
+    assert_bits_equal(oracle.relu(np.array(ka["x"], np.float32)), np.array(ka["out"], np.float32))
+    lt = golden("ltv_patterns.json")["relu"]                   # LibTorch pattern, x[5] == 0
+    x = np.array(lt["x"], np.float32)
+    assert x[5] == 0.0
+    assert_bits_equal(oracle.relu(x), np.array(lt["out"], np.float32), "relu pattern")
+    # `if v > 0.0 { v } else { 0.0 }`: -0 and NaN give +0 (both fail the comparison)
+    out = oracle.relu(np.array([-0.0, np.nan, -np.inf, np.inf, 1e-45], np.float32))
+    assert_bits_equal(out, np.array([0.0, 0.0, 0.0, np.inf, 1e-45], np.float32), "relu ieee")
+
+
+def test_negate_zero_sign_rule(oracle):
+    # utils.rs:847-870: 0.0 - x on the 8-wide body gives +0 for +/-0; -x on the tail flips the sign
+    z = np.zeros(11, np.float32)
+    out = oracle.neg(z)
+    assert np.all(np.signbit(out[8:])) and not np.any(np.signbit(out[:8]))
+    nz = -np.zeros(11, np.float32)
+    out = oracle.neg(nz)
+    assert not np.any(np.signbit(out))
+    x = normal(1003, 9)
+    assert_bits_equal(oracle.neg(x), (-torch.from_numpy(x)).numpy(), "neg of nonzero values")
+
+
+def test_division_by_zero_only_outside_unrolled_body(oracle):
+    # ops/div.rs:378-417: the 32-wide unrolled body divides without checking
+    a = np.ones(40, np.float32)
+    b = np.ones(40, np.float32)
+    b[3] = 0.0
+    out = oracle.div(a, b)
+    assert np.isinf(out[3])
+    b[35] = 0.0
+    with pytest.raises(oracle.DivisionByZero, match="index 35"):
+        oracle.div(a, b)
+    with pytest.raises(oracle.DivisionByZero):
+        oracle.div_scalar(a, 0.0)
+
+
+def test_backward_elementwise_match_torch_autograd(oracle):
+    x = normal(513, 11)
+    x[:4] = [0.0, -0.0, 1e-45, -1e-45]
+    go = normal(513, 12)
+    tx = torch.from_numpy(x.copy()).requires_grad_()
+    torch.relu(tx).backward(torch.from_numpy(go))
+    assert_bits_equal(oracle.relu_bwd(x, go), tx.grad.numpy(), "relu backward")
+    tx = torch.from_numpy(x.copy()).requires_grad_()
+    tx.pow(2.0).backward(torch.from_numpy(go))        # torch: go * (2 * x.pow(1))
+    got = oracle.pow_bwd(x, go, 2.0)                   # pow.rs: go * (2 * powf(x, 1))
+    assert_bits_equal(got, tx.grad.numpy(), "pow2 backward")
+
+
+def test_sum_known_answers(oracle):
+    ka = golden("known_answers.json")
+    for key in ("sum_forward", "sum_21", "sum_276"):
+        case = ka[key]
+        got = oracle.sum_(np.array(case["x"], np.float32))
+        assert abs(float(got) - case["sum"]) <= case.get("tol", 0.0), key
+    for key in ("mean_forward", "mean_3_5"):
+        case = ka[key]
+        got = oracle.mean(np.array(case["x"], np.float32))
+        assert abs(float(got) - case["mean"]) <= case["tol"], key
+
+
+def test_sum_grouping_of_four(oracle):
+    # sum.rs:94-105 adds each group of four before touching the accumulator:
+    # acc = 1e8 + (((2+2)+2)+2) = 100000008, while a plain running sum loses every 2.
+    x = np.array([1e8, 0, 0, 0, 2, 2, 2, 2], np.float32)
+    assert float(oracle.sum_(x)) == 100000008.0
+    running = np.float32(0)
+    for v in x:
+        running = np.float32(running + v)
+    assert float(running) == 1e8
+
+
+@pytest.mark.parametrize("n", [0, 1, 3, 4, 5, 4096, 100003])
+def test_sum_error_bound_against_fsum(oracle, n):
+    x = normal(n, 13)
+    exact = math.fsum(float(v) for v in x)
+    bound = (n + 1) * np.finfo(np.float32).eps * float(np.sum(np.abs(x), dtype=np.float64)) + 1e-30
+    assert abs(float(oracle.sum_(x)) - exact) <= bound
+    assert abs(oracle.sum_f64(x) - exact) <= 1e-9 * (1 + abs(exact)) + 1e-6 * n * 1e-10
+
+
+def test_sum_dim0_against_torch(oracle):
+    x = normal((300, 67), 14)
+    want = torch.from_numpy(x).double().sum(0).numpy()
+    assert max_rel(oracle.sum_dim0(x), want) < 1e-5
+    assert max_rel(oracle.sum_dim0_f64(x), want) < 1e-12
+    ints = np.arange(12, dtype=np.float32).reshape(4, 3)
+    assert oracle.sum_dim0(ints).tolist() == [18.0, 22.0, 26.0]
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_gemm_layouts_against_torch_and_brute_force(oracle, ta, tb):
+    M, N, K = 13, 7, 19
+    a = normal((K, M) if ta else (M, K), 15)
+    b = normal((N, K) if tb else (K, N), 16)
+    A = torch.from_numpy(a).double()
+    B = torch.from_numpy(b).double()
+    want = (A.T if ta else A) @ (B.T if tb else B)
+    got = oracle.gemm_f64(a, b, ta=ta, tb=tb)
+    assert np.allclose(got, want.numpy(), rtol=1e-12, atol=1e-12)
+    # brute force on a corner
+    Am = a.T if ta else a
+    Bm = b.T if tb else b
+    for i, j in ((0, 0), (M - 1, N - 1), (5, 3)):
+        s = sum(float(Am[i, k]) * float(Bm[k, j]) for k in range(K))
+        assert abs(got[i, j] - s) < 1e-9
+    got32 = oracle.gemm_f32(a, b, ta=ta, tb=tb)
+    assert max_rel(got32, want.numpy()) < 1e-5
+
+
+def test_gemm_known_answer(oracle):
+    ka = golden("known_answers.json")["matmul_2x2"]   # matmul/mod.rs:1145-1195
+    a = np.array(ka["a"], np.float32).reshape(2, 2)
+    b = np.array(ka["b"], np.float32).reshape(2, 2)
+    assert oracle.gemm_f64(a, b).reshape(-1).tolist() == ka["out"]
+    g = np.array(ka["grad_output"], np.float32).reshape(2, 2)
+    assert oracle.gemm_f64(g, b, tb=True).reshape(-1).tolist() == ka["grad_a"]
+    assert oracle.gemm_f64(a, g, ta=True).reshape(-1).tolist() == ka["grad_b"]
+
+
+def test_adam_correction_factor_closed_form(oracle):
+    for beta in (0.9, 0.999):
+        for t in (1, 2, 10, 100, 1000):
+            exact = 1.0 / (1.0 - float(np.float32(beta)) ** t)
+            assert abs(float(oracle.adam_correction_factor(beta, t)) - exact) <= 4e-7 * exact
+
+
+def test_adam_constant_gradient_closed_form(oracle):
+    # m0 = v0 = 0, constant g: m_hat = g and v_hat = g^2 exactly in real
+    # arithmetic, so every step moves p by lr * g / (|g| + eps).
+    n = 37
+    g = uniform(n, 0.1, 2.0, 17) * np.where(np.arange(n) % 2 == 0, 1, -1).astype(np.float32)
+    p = normal(n, 18)
+    p0 = p.copy()
+    m = np.zeros(n, np.float32)
+    v = np.zeros(n, np.float32)
+    for t in range(1, 21):
+        oracle.adam_step(p, g, m, v, t)
+        step = 1e-3 * g.astype(np.float64) / (np.abs(g.astype(np.float64)) + 1e-8)
+        want = p0.astype(np.float64) - t * step
+        assert np.max(np.abs(p - want)) < 2e-6, t
+
+
+def test_adam_velocity_tail_association(oracle):
+    # adam/mod.rs:736-773: c2*(g*g) on the 8-wide AVX2 body, (c2*g)*g on the
+    # scalar tail.  Pick g where the two roundings differ and check each
+    # position uses its own rule (reading of the reference; no reference
+    # vector distinguishes the two, see the oracle header).
+    c2 = np.float32(1.0) - np.float32(0.999)
+    cand = uniform(4096, 0.5, 2.0, 19)
+    body = (c2 * (cand * cand)).astype(np.float32)
+    tail = ((c2 * cand) * cand).astype(np.float32)
+    g_diff = cand[body != tail][0]
+    g = np.full(9, g_diff, np.float32)
+    p = np.zeros(9, np.float32)
+    m = np.zeros(9, np.float32)
+    v = np.zeros(9, np.float32)
+    oracle.adam_step(p, g, m, v, 1)
+    assert v[0] == np.float32(c2 * np.float32(g_diff * g_diff))
+    assert v[8] == np.float32(np.float32(c2 * g_diff) * g_diff)
+    assert v[0] != v[8]

@@ -1,0 +1,177 @@
+"""ctypes bindings of the two native libraries of this package.
+
+``libts_hip.so``       -- the C-ABI of ``include/ts_hip.h`` (HIP kernels for gfx950)
+``libts_gradtrack.so`` -- the C handle API of ``include/ts_gradtrack.h``
+
+Both are built in place by ``make -C train-station_amd`` (or
+``__graft_entry__.build()``).  There is no fallback: if a library is missing
+or fails to load, importing the package raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+
+HERE = pathlib.Path(__file__).resolve().parent
+
+_c = ctypes
+F = _c.POINTER(_c.c_float)
+SZ = _c.c_size_t
+VP = _c.c_void_p
+U64P = _c.POINTER(_c.c_ulonglong)
+
+
+class TsError(RuntimeError):
+    """A panic of the reference (or a HIP error) raised by the native library."""
+
+
+def _load(name: str) -> ctypes.CDLL:
+    path = HERE / name
+    if not path.exists():
+        raise ImportError(f"{path} is missing: build it with `make -C {HERE}` "
+                          "or __graft_entry__.build(); there is no CPU fallback")
+    return ctypes.CDLL(str(path), mode=ctypes.RTLD_GLOBAL)
+
+
+# --- include/ts_hip.h ------------------------------------------------------------
+
+# name -> (restype, argtypes); every symbol declared in include/ts_hip.h
+HIP_SIGNATURES = {
+    "ts_hip_initialize": (_c.c_int, []),
+    "ts_hip_cleanup": (None, []),
+    "ts_hip_get_device_count": (_c.c_int, [_c.POINTER(_c.c_int)]),
+    "ts_hip_set_device": (_c.c_int, [_c.c_int]),
+    "ts_hip_get_device": (_c.c_int, [_c.POINTER(_c.c_int)]),
+    "ts_hip_malloc": (_c.c_int, [_c.POINTER(F), SZ]),
+    "ts_hip_free": (_c.c_int, [F]),
+    "ts_hip_memcpy": (_c.c_int, [VP, VP, SZ, _c.c_int]),
+    "ts_hip_memcpy_async": (_c.c_int, [VP, VP, SZ, _c.c_int, VP]),
+    "ts_hip_host_malloc": (_c.c_int, [_c.POINTER(VP), SZ]),
+    "ts_hip_host_free": (_c.c_int, [VP]),
+    "ts_hip_stream_create": (_c.c_int, [_c.POINTER(VP)]),
+    "ts_hip_stream_destroy": (_c.c_int, [VP]),
+    "ts_hip_stream_synchronize": (_c.c_int, [VP]),
+    "ts_hip_device_synchronize": (_c.c_int, []),
+    "ts_hip_event_create": (_c.c_int, [_c.POINTER(VP)]),
+    "ts_hip_event_destroy": (_c.c_int, [VP]),
+    "ts_hip_event_record": (_c.c_int, [VP, VP]),
+    "ts_hip_event_synchronize": (_c.c_int, [VP]),
+    "ts_hip_event_elapsed_ms": (_c.c_int, [_c.POINTER(_c.c_float), VP, VP]),
+    "ts_hip_error_string": (_c.c_char_p, [_c.c_int]),
+    "ts_hip_mem_info": (_c.c_int, [_c.POINTER(SZ), _c.POINTER(SZ)]),
+    "ts_hip_add": (_c.c_int, [VP, VP, VP, SZ, VP]),
+    "ts_hip_sub": (_c.c_int, [VP, VP, VP, SZ, VP]),
+    "ts_hip_mul": (_c.c_int, [VP, VP, VP, SZ, VP]),
+    "ts_hip_div": (_c.c_int, [VP, VP, VP, SZ, SZ, VP, VP]),
+    "ts_hip_add_scalar": (_c.c_int, [VP, _c.c_float, VP, SZ, VP]),
+    "ts_hip_sub_scalar": (_c.c_int, [VP, _c.c_float, VP, SZ, VP]),
+    "ts_hip_mul_scalar": (_c.c_int, [VP, _c.c_float, VP, SZ, VP]),
+    "ts_hip_div_scalar": (_c.c_int, [VP, _c.c_float, VP, SZ, VP]),
+    "ts_hip_neg": (_c.c_int, [VP, VP, SZ, SZ, VP]),
+    "ts_hip_relu": (_c.c_int, [VP, VP, SZ, VP]),
+    "ts_hip_pow_scalar": (_c.c_int, [VP, _c.c_float, VP, SZ, VP]),
+    "ts_hip_bias_add": (_c.c_int, [VP, VP, VP, SZ, SZ, _c.c_int, VP]),
+    "ts_hip_row_broadcast": (_c.c_int, [_c.c_int, VP, VP, VP, SZ, SZ, _c.c_int, SZ, VP, VP]),
+    "ts_hip_fill": (_c.c_int, [VP, _c.c_float, SZ, VP]),
+    "ts_hip_fill_from_device": (_c.c_int, [VP, VP, _c.c_float, _c.c_int, SZ, VP]),
+    "ts_hip_copy": (_c.c_int, [VP, VP, SZ, VP]),
+    "ts_hip_relu_backward": (_c.c_int, [VP, VP, VP, SZ, VP]),
+    "ts_hip_pow_backward": (_c.c_int, [VP, VP, VP, SZ, _c.c_float, VP]),
+    "ts_hip_mul_backward": (_c.c_int, [VP, VP, VP, VP, VP, SZ, VP]),
+    "ts_hip_div_backward": (_c.c_int, [VP, VP, VP, VP, VP, SZ, SZ, SZ, VP, VP]),
+    "ts_hip_sum_workspace_floats": (SZ, [SZ]),
+    "ts_hip_sum": (_c.c_int, [VP, SZ, VP, VP, SZ, VP]),
+    "ts_hip_mean": (_c.c_int, [VP, SZ, VP, VP, SZ, VP]),
+    "ts_hip_sum_dim0_workspace_floats": (SZ, [SZ, SZ]),
+    "ts_hip_sum_dim0": (_c.c_int, [VP, SZ, SZ, VP, VP, SZ, VP]),
+    "ts_hip_matmul": (_c.c_int, [VP, VP, VP, SZ, SZ, SZ, VP]),
+    "ts_hip_gemm": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, SZ, VP]),
+    "ts_hip_adam_step": (_c.c_int, [VP, VP, VP, VP, VP, SZ, _c.c_float, _c.c_float, _c.c_float,
+                                    _c.c_float, _c.c_float, _c.c_uint64, SZ, _c.c_int, VP]),
+}
+
+TP = VP  # opaque ts_tensor* / ts_adam*
+
+# name -> (restype, argtypes); every symbol declared in include/ts_gradtrack.h
+GRADTRACK_SIGNATURES = {
+    "ts_last_error": (_c.c_char_p, []),
+    "ts_tensor_new": (TP, [_c.POINTER(SZ), SZ]),
+    "ts_tensor_zeros": (TP, [_c.POINTER(SZ), SZ]),
+    "ts_tensor_ones": (TP, [_c.POINTER(SZ), SZ]),
+    "ts_tensor_from_slice": (TP, [F, SZ, _c.POINTER(SZ), SZ]),
+    "ts_tensor_clone": (TP, [TP]),
+    "ts_tensor_free": (None, [TP]),
+    "ts_tensor_id": (_c.c_uint64, [TP]),
+    "ts_tensor_rank": (SZ, [TP]),
+    "ts_tensor_dims": (SZ, [TP, _c.POINTER(SZ), SZ]),
+    "ts_tensor_size": (SZ, [TP]),
+    "ts_tensor_device_ptr": (VP, [TP]),
+    "ts_tensor_with_requires_grad": (_c.c_int, [TP]),
+    "ts_tensor_set_requires_grad": (_c.c_int, [TP, _c.c_int]),
+    "ts_tensor_requires_grad": (_c.c_int, [TP]),
+    "ts_tensor_add_tensor": (TP, [TP, TP]),
+    "ts_tensor_sub_tensor": (TP, [TP, TP]),
+    "ts_tensor_mul_tensor": (TP, [TP, TP]),
+    "ts_tensor_div_tensor": (TP, [TP, TP]),
+    "ts_tensor_add_scalar": (TP, [TP, _c.c_float]),
+    "ts_tensor_sub_scalar": (TP, [TP, _c.c_float]),
+    "ts_tensor_mul_scalar": (TP, [TP, _c.c_float]),
+    "ts_tensor_div_scalar": (TP, [TP, _c.c_float]),
+    "ts_tensor_relu": (TP, [TP]),
+    "ts_tensor_pow_scalar": (TP, [TP, _c.c_float]),
+    "ts_tensor_matmul": (TP, [TP, TP]),
+    "ts_tensor_sum": (TP, [TP]),
+    "ts_tensor_mean": (TP, [TP]),
+    "ts_tensor_backward": (_c.c_int, [TP, TP]),
+    "ts_tensor_grad_by_value": (TP, [TP]),
+    "ts_tensor_set_grad": (_c.c_int, [TP, TP]),
+    "ts_tensor_zero_grad": (_c.c_int, [TP]),
+    "ts_tensor_data": (_c.c_int, [TP, F, SZ]),
+    "ts_tensor_value": (_c.c_int, [TP, F]),
+    "ts_clear_gradients": (None, []),
+    "ts_no_grad_push": (None, []),
+    "ts_no_grad_pop": (None, []),
+    "ts_is_grad_enabled": (_c.c_int, []),
+    "ts_adam_new": (TP, []),
+    "ts_adam_with_config": (TP, [_c.c_float, _c.c_float, _c.c_float, _c.c_float, _c.c_float, _c.c_int]),
+    "ts_adam_with_learning_rate": (TP, [_c.c_float]),
+    "ts_adam_free": (None, [TP]),
+    "ts_adam_add_parameter": (_c.c_int, [TP, TP]),
+    "ts_adam_step": (_c.c_int, [TP, _c.POINTER(TP), SZ]),
+    "ts_adam_zero_grad": (_c.c_int, [TP, _c.POINTER(TP), SZ]),
+    "ts_adam_learning_rate": (_c.c_float, [TP]),
+    "ts_adam_set_learning_rate": (None, [TP, _c.c_float]),
+    "ts_adam_step_count": (_c.c_uint64, [TP]),
+    "ts_adam_state": (_c.c_int, [TP, TP, _c.c_int, F, SZ]),
+    "ts_synchronize": (_c.c_int, []),
+    "ts_stream": (VP, []),
+    "ts_pool_live_bytes": (SZ, []),
+    "ts_pool_cached_bytes": (SZ, []),
+    "ts_pool_empty_cache": (None, []),
+    "ts_profile_enable": (None, [_c.c_int]),
+    "ts_profile_reset": (None, []),
+    "ts_profile_read": (_c.c_int, [_c.c_int, _c.POINTER(_c.c_double), _c.POINTER(_c.c_double),
+                                   _c.POINTER(_c.c_uint64)]),
+}
+
+
+def _bind(lib: ctypes.CDLL, sigs: dict) -> ctypes.CDLL:
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)  # AttributeError if the library lacks a declared symbol
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+hip = _bind(_load("libts_hip.so"), HIP_SIGNATURES)
+gradtrack = _bind(_load("libts_gradtrack.so"), GRADTRACK_SIGNATURES)
+
+
+def hip_check(status: int, what: str = "ts_hip") -> None:
+    if status != 0:
+        msg = hip.ts_hip_error_string(status).decode()
+        raise TsError(f"{what}: {msg} (status {status})")
+
+
+def last_error() -> str:
+    return gradtrack.ts_last_error().decode()

@@ -1,0 +1,94 @@
+// Adam optimizer over device parameters (optimizers/adam/mod.rs).  Per-param
+// state m / v (and v_hat_max under AMSGrad) lives in pooled device buffers;
+// each step is one fused kernel per parameter.
+#include <cstdio>
+
+#include "ts_hip.h"
+#include "ts_host.h"
+
+namespace ts {
+
+Adam Adam::with_config(AdamConfig c) {
+    Adam a;
+    a.config_ = c;
+    return a;
+}
+
+Adam Adam::with_learning_rate(float lr) {
+    AdamConfig c;
+    c.learning_rate = lr;
+    return with_config(c);
+}
+
+// adam/mod.rs:287-307
+void Adam::add_parameter(const Tensor &p) {
+    if (!p.requires_grad()) throw Error("Parameter must require gradients");
+    if (states_.count(p.id())) return;
+    State s;
+    s.n = p.size();
+    if (s.n) {
+        s.m = std::make_shared<Allocation>(s.n);
+        s.v = std::make_shared<Allocation>(s.n);
+        void *st = Runtime::get().stream();
+        check(ts_hip_fill(s.m->ptr, 0.0f, s.n, st), "ts_hip_fill");
+        check(ts_hip_fill(s.v->ptr, 0.0f, s.n, st), "ts_hip_fill");
+    }
+    states_.emplace(p.id(), std::move(s));
+    insertion_order_.push_back(p.id());
+}
+
+void Adam::add_parameters(const std::vector<const Tensor *> &ps) {
+    for (const Tensor *p : ps) add_parameter(*p);
+}
+
+void Adam::step(const std::vector<Tensor *> &params) {
+    step_count_ += 1;  // adam/mod.rs:1037
+    for (Tensor *p : params) {
+        auto it = states_.find(p->id());
+        if (it == states_.end())  // adam/mod.rs:489-492
+            throw Error(
+                "Parameter must be linked to optimizer before stepping. Use add_parameter() first.");
+        const Tensor *g = p->grad_ref();
+        if (!g) {  // adam/mod.rs:1040-1042
+            std::fprintf(stderr, "Warning: Failed to update parameter: Parameter %zu has no gradient\n",
+                         p->id());
+            continue;
+        }
+        State &s = it->second;
+        if (g->size() != p->size() || s.n != p->size())
+            throw Error("Momentum and gradient size mismatch");
+        s.step += 1;
+        int first = 0;
+        if (config_.amsgrad && !s.v_hat_max && s.n) {
+            s.v_hat_max = std::make_shared<Allocation>(s.n);
+            first = 1;
+        }
+        if (!s.n) continue;
+        Profiler &P = Profiler::get();
+        P.begin();
+        check(ts_hip_adam_step(p->dev_mut(), g->dev(), s.m->ptr, s.v->ptr,
+                               config_.amsgrad ? s.v_hat_max->ptr : nullptr, s.n,
+                               config_.learning_rate, config_.beta1, config_.beta2, config_.eps,
+                               config_.weight_decay, step_count_, (s.n / 8) * 8, first,
+                               Runtime::get().stream()),
+              "ts_hip_adam_step");
+        P.end(KernelClass::Adam, 28.0 * s.n + (config_.amsgrad ? 8.0 * s.n : 0.0));
+    }
+}
+
+void Adam::zero_grad(const std::vector<Tensor *> &params) {
+    for (Tensor *p : params) p->zero_grad();
+    clear_gradients();
+}
+
+const float *Adam::state_m(size_t id) const {
+    auto it = states_.find(id);
+    return (it == states_.end() || !it->second.m) ? nullptr : it->second.m->ptr;
+}
+
+const float *Adam::state_v(size_t id) const {
+    auto it = states_.find(id);
+    return (it == states_.end() || !it->second.v) ? nullptr : it->second.v->ptr;
+}
+
+}  // namespace ts

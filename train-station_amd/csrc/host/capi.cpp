@@ -1,0 +1,303 @@
+// C handle API (include/ts_gradtrack.h) over the C++ host classes.
+#include <cstring>
+#include <exception>
+#include <string>
+
+#include "ts_gradtrack.h"
+#include "ts_hip.h"
+#include "ts_host.h"
+
+struct ts_tensor {
+    ts::Tensor t;
+};
+struct ts_adam {
+    ts::Adam a;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <class F>
+auto guard_ptr(F &&f) -> decltype(f()) {
+    try {
+        g_last_error.clear();
+        return f();
+    } catch (const std::exception &e) {
+        g_last_error = e.what();
+    } catch (...) {
+        g_last_error = "unknown error";
+    }
+    return nullptr;
+}
+
+template <class F>
+int guard_int(F &&f) {
+    try {
+        g_last_error.clear();
+        f();
+        return 0;
+    } catch (const std::exception &e) {
+        g_last_error = e.what();
+    } catch (...) {
+        g_last_error = "unknown error";
+    }
+    return -1;
+}
+
+ts_tensor *wrap(ts::Tensor &&t) { return new ts_tensor{std::move(t)}; }
+
+std::vector<size_t> dims_of(const size_t *dims, size_t rank) {
+    if (rank && !dims) throw ts::Error("dims pointer is NULL");
+    return std::vector<size_t>(dims, dims + rank);
+}
+
+const ts::Tensor &T(const ts_tensor *h) {
+    if (!h) throw ts::Error("tensor handle is NULL");
+    return h->t;
+}
+
+std::vector<ts::Tensor *> param_list(ts_tensor *const *params, size_t count) {
+    if (count && !params) throw ts::Error("parameter list is NULL");
+    std::vector<ts::Tensor *> v;
+    v.reserve(count);
+    for (size_t i = 0; i < count; ++i) {
+        if (!params[i]) throw ts::Error("parameter handle is NULL");
+        v.push_back(&params[i]->t);
+    }
+    return v;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *ts_last_error(void) { return g_last_error.c_str(); }
+
+ts_tensor *ts_tensor_new(const size_t *dims, size_t rank) {
+    return guard_ptr([&] { return wrap(ts::Tensor::new_uninit(dims_of(dims, rank))); });
+}
+ts_tensor *ts_tensor_zeros(const size_t *dims, size_t rank) {
+    return guard_ptr([&] { return wrap(ts::Tensor::zeros(dims_of(dims, rank))); });
+}
+ts_tensor *ts_tensor_ones(const size_t *dims, size_t rank) {
+    return guard_ptr([&] { return wrap(ts::Tensor::ones(dims_of(dims, rank))); });
+}
+ts_tensor *ts_tensor_from_slice(const float *data, size_t len, const size_t *dims, size_t rank) {
+    return guard_ptr([&] {
+        if (len && !data) throw ts::Error("data pointer is NULL");
+        return wrap(ts::Tensor::from_slice(data, len, dims_of(dims, rank)));
+    });
+}
+ts_tensor *ts_tensor_clone(const ts_tensor *t) {
+    return guard_ptr([&] { return wrap(T(t).clone()); });
+}
+void ts_tensor_free(ts_tensor *t) { delete t; }
+
+uint64_t ts_tensor_id(const ts_tensor *t) { return t ? t->t.id() : 0; }
+size_t ts_tensor_rank(const ts_tensor *t) { return t ? t->t.dims().size() : 0; }
+size_t ts_tensor_dims(const ts_tensor *t, size_t *out, size_t cap) {
+    if (!t) return 0;
+    const auto &d = t->t.dims();
+    for (size_t i = 0; i < d.size() && i < cap; ++i) out[i] = d[i];
+    return d.size();
+}
+size_t ts_tensor_size(const ts_tensor *t) { return t ? t->t.size() : 0; }
+const float *ts_tensor_device_ptr(const ts_tensor *t) { return t ? t->t.dev() : nullptr; }
+
+int ts_tensor_with_requires_grad(ts_tensor *t) {
+    return guard_int([&] {
+        if (!t) throw ts::Error("tensor handle is NULL");
+        t->t.with_requires_grad();
+    });
+}
+int ts_tensor_set_requires_grad(ts_tensor *t, int r) {
+    return guard_int([&] {
+        if (!t) throw ts::Error("tensor handle is NULL");
+        t->t.set_requires_grad(r != 0);
+    });
+}
+int ts_tensor_requires_grad(const ts_tensor *t) { return t && t->t.requires_grad() ? 1 : 0; }
+
+#define TS_BINARY(name, method)                                                   \
+    ts_tensor *name(const ts_tensor *a, const ts_tensor *b) {                     \
+        return guard_ptr([&] { return wrap(T(a).method(T(b))); });                \
+    }
+TS_BINARY(ts_tensor_add_tensor, add_tensor)
+TS_BINARY(ts_tensor_sub_tensor, sub_tensor)
+TS_BINARY(ts_tensor_mul_tensor, mul_tensor)
+TS_BINARY(ts_tensor_div_tensor, div_tensor)
+TS_BINARY(ts_tensor_matmul, matmul)
+#undef TS_BINARY
+
+#define TS_SCALAR(name, method)                                                   \
+    ts_tensor *name(const ts_tensor *a, float s) {                                \
+        return guard_ptr([&] { return wrap(T(a).method(s)); });                   \
+    }
+TS_SCALAR(ts_tensor_add_scalar, add_scalar)
+TS_SCALAR(ts_tensor_sub_scalar, sub_scalar)
+TS_SCALAR(ts_tensor_mul_scalar, mul_scalar)
+TS_SCALAR(ts_tensor_div_scalar, div_scalar)
+TS_SCALAR(ts_tensor_pow_scalar, pow_scalar)
+#undef TS_SCALAR
+
+ts_tensor *ts_tensor_relu(const ts_tensor *a) {
+    return guard_ptr([&] { return wrap(T(a).relu()); });
+}
+ts_tensor *ts_tensor_sum(const ts_tensor *a) {
+    return guard_ptr([&] { return wrap(T(a).sum()); });
+}
+ts_tensor *ts_tensor_mean(const ts_tensor *a) {
+    return guard_ptr([&] { return wrap(T(a).mean()); });
+}
+
+int ts_tensor_backward(ts_tensor *t, const ts_tensor *grad_output) {
+    return guard_int([&] {
+        if (!t) throw ts::Error("tensor handle is NULL");
+        t->t.backward(grad_output ? &grad_output->t : nullptr);
+    });
+}
+
+ts_tensor *ts_tensor_grad_by_value(const ts_tensor *t) {
+    return guard_ptr([&]() -> ts_tensor * {
+        auto g = T(t).grad_by_value();
+        if (!g) return nullptr;
+        return wrap(std::move(*g));
+    });
+}
+
+int ts_tensor_set_grad(ts_tensor *t, const ts_tensor *grad) {
+    return guard_int([&] {
+        if (!t) throw ts::Error("tensor handle is NULL");
+        t->t.set_grad(T(grad).clone());
+    });
+}
+int ts_tensor_zero_grad(ts_tensor *t) {
+    return guard_int([&] {
+        if (!t) throw ts::Error("tensor handle is NULL");
+        t->t.zero_grad();
+    });
+}
+
+int ts_tensor_data(const ts_tensor *t, float *out, size_t len) {
+    return guard_int([&] {
+        if (len && !out) throw ts::Error("output pointer is NULL");
+        T(t).copy_to_host(out, len);
+    });
+}
+int ts_tensor_value(const ts_tensor *t, float *out) {
+    return guard_int([&] {
+        if (!out) throw ts::Error("output pointer is NULL");
+        *out = T(t).value();
+    });
+}
+
+void ts_clear_gradients(void) { ts::clear_gradients(); }
+void ts_no_grad_push(void) { ts::push_grad_enabled(false); }
+void ts_no_grad_pop(void) { ts::pop_grad_enabled(); }
+int ts_is_grad_enabled(void) { return ts::is_grad_enabled() ? 1 : 0; }
+
+ts_adam *ts_adam_new(void) {
+    return guard_ptr([&] { return new ts_adam{ts::Adam()}; });
+}
+ts_adam *ts_adam_with_config(float lr, float b1, float b2, float eps, float wd, int amsgrad) {
+    return guard_ptr([&] {
+        ts::AdamConfig c;
+        c.learning_rate = lr;
+        c.beta1 = b1;
+        c.beta2 = b2;
+        c.eps = eps;
+        c.weight_decay = wd;
+        c.amsgrad = amsgrad != 0;
+        return new ts_adam{ts::Adam::with_config(c)};
+    });
+}
+ts_adam *ts_adam_with_learning_rate(float lr) {
+    return guard_ptr([&] { return new ts_adam{ts::Adam::with_learning_rate(lr)}; });
+}
+void ts_adam_free(ts_adam *opt) { delete opt; }
+
+int ts_adam_add_parameter(ts_adam *opt, const ts_tensor *param) {
+    return guard_int([&] {
+        if (!opt) throw ts::Error("optimizer handle is NULL");
+        opt->a.add_parameter(T(param));
+    });
+}
+int ts_adam_step(ts_adam *opt, ts_tensor *const *params, size_t count) {
+    return guard_int([&] {
+        if (!opt) throw ts::Error("optimizer handle is NULL");
+        opt->a.step(param_list(params, count));
+    });
+}
+int ts_adam_zero_grad(ts_adam *opt, ts_tensor *const *params, size_t count) {
+    return guard_int([&] {
+        if (!opt) throw ts::Error("optimizer handle is NULL");
+        opt->a.zero_grad(param_list(params, count));
+    });
+}
+float ts_adam_learning_rate(const ts_adam *opt) { return opt ? opt->a.learning_rate() : 0.0f; }
+void ts_adam_set_learning_rate(ts_adam *opt, float lr) {
+    if (opt) opt->a.set_learning_rate(lr);
+}
+uint64_t ts_adam_step_count(const ts_adam *opt) { return opt ? opt->a.step_count() : 0; }
+
+int ts_adam_state(const ts_adam *opt, const ts_tensor *param, int which, float *out, size_t len) {
+    return guard_int([&] {
+        if (!opt) throw ts::Error("optimizer handle is NULL");
+        const ts::Tensor &p = T(param);
+        const float *src = which == 0 ? opt->a.state_m(p.id()) : opt->a.state_v(p.id());
+        if (!src) throw ts::Error("parameter is not linked to this optimizer");
+        if (len != p.size()) throw ts::Error("state buffer length mismatch");
+        ts::check(ts_hip_memcpy_async(out, src, len, 1, ts::Runtime::get().stream()),
+                  "ts_hip_memcpy_async");
+        ts::Runtime::get().sync();
+    });
+}
+
+int ts_synchronize(void) {
+    return guard_int([&] { ts::Runtime::get().sync(); });
+}
+void *ts_stream(void) {
+    try {
+        return ts::Runtime::get().stream();
+    } catch (...) {
+        return nullptr;
+    }
+}
+size_t ts_pool_live_bytes(void) { return ts::DevicePool::get().live_bytes(); }
+size_t ts_pool_cached_bytes(void) { return ts::DevicePool::get().cached_bytes(); }
+void ts_pool_empty_cache(void) {
+    try {
+        ts::Runtime::get().sync();
+    } catch (...) {
+    }
+    ts::DevicePool::get().empty_cache();
+}
+
+void ts_profile_enable(int on) {
+    try {
+        ts::Profiler::get().enable(on != 0);
+    } catch (const std::exception &e) {
+        g_last_error = e.what();
+    }
+}
+void ts_profile_reset(void) {
+    try {
+        ts::Profiler::get().reset();
+    } catch (const std::exception &e) {
+        g_last_error = e.what();
+    }
+}
+int ts_profile_read(int k, double *ms, double *work, uint64_t *launches) {
+    return guard_int([&] {
+        if (k < 0 || k >= static_cast<int>(ts::KernelClass::kCount))
+            throw ts::Error("kernel class out of range");
+        ts::Profiler::get().collect();
+        ts::ClassStats s = ts::Profiler::get().stats(static_cast<ts::KernelClass>(k));
+        if (ms) *ms = s.ms;
+        if (work) *work = s.work;
+        if (launches) *launches = s.launches;
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,107 @@
+// gradtrack engine: the recorded graph, the no-grad switch and the backward
+// worklist (gradtrack/engine.rs, gradtrack/no_grad_track.rs).
+#include <unordered_map>
+#include <utility>
+#include <vector>
+
+#include "ts_hip.h"
+#include "ts_host.h"
+
+namespace ts {
+
+namespace {
+
+// engine.rs:175-187: operations id -> (input ids, GradFn); gradients id -> Tensor.
+struct Graph {
+    std::unordered_map<size_t, std::pair<std::vector<size_t>, GradFn>> operations;
+    std::unordered_map<size_t, Tensor> gradients;
+};
+
+// Thread-local, as GRADTRACK_GRAPH (engine.rs:697-699).
+Graph &graph() {
+    thread_local Graph g;
+    return g;
+}
+
+// no_grad_track.rs:16-22: thread-local stack, enabled by default.
+std::vector<bool> &grad_stack() {
+    thread_local std::vector<bool> s{true};
+    return s;
+}
+
+// engine.rs:514-524: existing + new, in a new buffer.
+void accumulate_gradient(size_t id, Tensor g) {
+    auto &grads = graph().gradients;
+    auto it = grads.find(id);
+    if (it == grads.end()) {
+        grads.emplace(id, std::move(g));
+        return;
+    }
+    Tensor &existing = it->second;
+    Tensor sum = Tensor::new_uninit(existing.dims());
+    const size_t n = sum.size();
+    Profiler &P = Profiler::get();
+    P.begin();
+    check(ts_hip_add(existing.dev(), g.dev(), sum.dev_mut(), n, Runtime::get().stream()),
+          "ts_hip_add(accumulate)");
+    P.end(KernelClass::Elementwise, 12.0 * n);
+    existing = std::move(sum);
+}
+
+}  // namespace
+
+bool is_grad_enabled() { return grad_stack().back(); }
+void push_grad_enabled(bool on) { grad_stack().push_back(on); }
+void pop_grad_enabled() {
+    if (grad_stack().size() > 1) grad_stack().pop_back();
+}
+
+void clear_gradients() {
+    graph().operations.clear();
+    graph().gradients.clear();
+}
+
+void register_operation(size_t output_id, std::vector<size_t> input_ids, GradFn fn) {
+    graph().operations.insert_or_assign(output_id, std::make_pair(std::move(input_ids), std::move(fn)));
+}
+
+const Tensor *accumulated_gradient(size_t id) {
+    auto &grads = graph().gradients;
+    auto it = grads.find(id);
+    return it == grads.end() ? nullptr : &it->second;
+}
+
+// engine.rs:962-1047
+void engine_backward(Tensor &root, const Tensor *grad_output) {
+    Tensor init = grad_output ? grad_output->alias() : Tensor::ones(root.dims());
+    if (init.dims() != root.dims() && init.size() != root.size())
+        throw Error("backward: gradient shape does not match the tensor");
+    root.accumulate_grad(init.alias());
+    graph().gradients.insert_or_assign(root.id(), init.alias());  // store_gradient overwrites
+
+    std::vector<size_t> worklist;
+    worklist.reserve(128);
+    worklist.push_back(root.id());
+    while (!worklist.empty()) {
+        const size_t node = worklist.back();
+        worklist.pop_back();
+        auto op = graph().operations.find(node);
+        if (op == graph().operations.end()) continue;  // leaf: keep its gradient
+        auto git = graph().gradients.find(node);
+        if (git == graph().gradients.end()) continue;
+        Tensor current = std::move(git->second);
+        graph().gradients.erase(git);
+        // operations is not modified below, so the reference stays valid
+        const std::vector<size_t> &input_ids = op->second.first;
+        std::vector<std::optional<Tensor>> grads = op->second.second.apply(current);
+        for (size_t idx = 0; idx < input_ids.size(); ++idx) {
+            if (idx >= grads.size() || !grads[idx]) continue;
+            const size_t input_id = input_ids[idx];
+            accumulate_gradient(input_id, std::move(*grads[idx]));
+            grads[idx].reset();
+            if (graph().operations.count(input_id)) worklist.push_back(input_id);
+        }
+    }
+}
+
+}  // namespace ts

@@ -1,0 +1,167 @@
+// Runtime pieces of the host library: status checking, the library stream,
+// the division-by-zero word, the device buffer pool and the event profiler.
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "ts_hip.h"
+#include "ts_host.h"
+
+namespace ts {
+
+void check(int status, const char *what) {
+    if (status != TS_HIP_OK)
+        throw Error(std::string(what) + ": " + ts_hip_error_string(status) + " (status " +
+                    std::to_string(status) + ")");
+}
+
+static const unsigned long long kNoZero = ~0ull;
+
+Runtime::Runtime() {
+    check(ts_hip_initialize(), "ts_hip_initialize");
+    check(ts_hip_stream_create(&stream_), "ts_hip_stream_create");
+    float *w = nullptr;
+    check(ts_hip_malloc(&w, 2), "ts_hip_malloc(zero index)");
+    zero_index_ = reinterpret_cast<unsigned long long *>(w);
+    check(ts_hip_memcpy(w, reinterpret_cast<const float *>(&kNoZero), 2, 0), "ts_hip_memcpy");
+}
+
+Runtime &Runtime::get() {
+    // Never destroyed: tensors may outlive static destruction order.
+    static Runtime *rt = new Runtime();
+    return *rt;
+}
+
+void Runtime::sync() {
+    check(ts_hip_stream_synchronize(stream_), "ts_hip_stream_synchronize");
+    unsigned long long idx = kNoZero;
+    check(ts_hip_memcpy(reinterpret_cast<float *>(&idx),
+                        reinterpret_cast<const float *>(zero_index_), 2, 1),
+          "ts_hip_memcpy");
+    if (idx != kNoZero) {
+        check(ts_hip_memcpy(reinterpret_cast<float *>(zero_index_),
+                            reinterpret_cast<const float *>(&kNoZero), 2, 0),
+              "ts_hip_memcpy");
+        // ops/div.rs:383-416
+        throw Error("Division by zero detected at index " + std::to_string(idx));
+    }
+}
+
+// ---- pool ---------------------------------------------------------------------
+
+static std::mutex g_pool_mutex;
+
+static size_t round_floats(size_t n) {
+    if (n <= 1024) return (n + 63) & ~size_t(63);            // 256-byte granules
+    if (n <= (size_t(1) << 20)) return (n + 1023) & ~size_t(1023);
+    return (n + 65535) & ~size_t(65535);                      // 256 KiB granules
+}
+
+DevicePool &DevicePool::get() {
+    static DevicePool *p = new DevicePool();
+    return *p;
+}
+
+float *DevicePool::acquire(size_t n_floats, size_t *rounded) {
+    Runtime::get();
+    const size_t r = round_floats(n_floats == 0 ? 1 : n_floats);
+    *rounded = r;
+    {
+        std::lock_guard<std::mutex> lock(g_pool_mutex);
+        auto it = free_.find(r);
+        if (it != free_.end() && !it->second.empty()) {
+            float *p = it->second.back();
+            it->second.pop_back();
+            cached_ -= r * sizeof(float);
+            live_ += r * sizeof(float);
+            return p;
+        }
+    }
+    float *p = nullptr;
+    int st = ts_hip_malloc(&p, r);
+    if (st != TS_HIP_OK) {  // return cached blocks to the device and retry once
+        Runtime::get().sync();
+        empty_cache();
+        st = ts_hip_malloc(&p, r);
+    }
+    check(st, "ts_hip_malloc");
+    std::lock_guard<std::mutex> lock(g_pool_mutex);
+    live_ += r * sizeof(float);
+    return p;
+}
+
+void DevicePool::release(float *p, size_t rounded) {
+    if (!p) return;
+    std::lock_guard<std::mutex> lock(g_pool_mutex);
+    free_[rounded].push_back(p);
+    live_ -= rounded * sizeof(float);
+    cached_ += rounded * sizeof(float);
+}
+
+void DevicePool::empty_cache() {
+    std::lock_guard<std::mutex> lock(g_pool_mutex);
+    for (auto &kv : free_)
+        for (float *p : kv.second) ts_hip_free(p);
+    free_.clear();
+    cached_ = 0;
+}
+
+Allocation::Allocation(size_t n_floats) : n(n_floats) {
+    ptr = DevicePool::get().acquire(n_floats, &rounded);
+}
+
+Allocation::~Allocation() { DevicePool::get().release(ptr, rounded); }
+
+// ---- profiler -----------------------------------------------------------------
+
+Profiler &Profiler::get() {
+    static Profiler *p = new Profiler();
+    return *p;
+}
+
+void Profiler::enable(bool on) {
+    if (!on && enabled_) collect();
+    enabled_ = on;
+}
+
+void Profiler::begin() {
+    if (!enabled_) return;
+    void *ev = nullptr;
+    if (!spare_.empty()) { ev = spare_.back(); spare_.pop_back(); }
+    else check(ts_hip_event_create(&ev), "ts_hip_event_create");
+    check(ts_hip_event_record(ev, Runtime::get().stream()), "ts_hip_event_record");
+    open_ = ev;
+}
+
+void Profiler::end(KernelClass k, double work) {
+    if (!enabled_ || !open_) return;
+    void *ev = nullptr;
+    if (!spare_.empty()) { ev = spare_.back(); spare_.pop_back(); }
+    else check(ts_hip_event_create(&ev), "ts_hip_event_create");
+    check(ts_hip_event_record(ev, Runtime::get().stream()), "ts_hip_event_record");
+    pending_.push_back(Pending{open_, ev, k, work});
+    open_ = nullptr;
+}
+
+void Profiler::collect() {
+    if (pending_.empty()) return;
+    check(ts_hip_stream_synchronize(Runtime::get().stream()), "ts_hip_stream_synchronize");
+    for (auto &p : pending_) {
+        float ms = 0.0f;
+        check(ts_hip_event_elapsed_ms(&ms, p.start, p.stop), "ts_hip_event_elapsed_ms");
+        auto &t = totals_[static_cast<int>(p.k)];
+        t.ms += ms;
+        t.work += p.work;
+        t.launches += 1;
+        spare_.push_back(p.start);
+        spare_.push_back(p.stop);
+    }
+    pending_.clear();
+}
+
+void Profiler::reset() {
+    collect();
+    for (auto &t : totals_) t = ClassStats{};
+}
+
+}  // namespace ts

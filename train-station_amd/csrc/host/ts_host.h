@@ -1,0 +1,282 @@
+// Host side of the MI355X backend: train-station's Tensor / gradtrack /
+// Adam API restated in C++ over the C-ABI of include/ts_hip.h.
+//
+// This library plays the part of train-station's Rust host code
+// (train-station/src/tensor, gradtrack, optimizers) for callers without a
+// Rust toolchain; it calls the device only through ts_hip.h, exactly as the
+// Rust crate would through its FFI block.  Names, argument meaning and error
+// behaviour follow the reference:
+//   Tensor::{new, zeros, ones, from_slice, with_requires_grad, add_tensor,
+//            sub_tensor, mul_tensor, div_tensor, *_scalar, relu, pow_scalar,
+//            matmul, sum, mean, backward, grad_by_value, zero_grad, data,
+//            value}   (tensor/core/utils.rs, tensor/ops/*, tensor/reductions/*)
+//   GradEngine backward worklist                  (gradtrack/engine.rs:962-1047)
+//   Adam::{new, with_config, with_learning_rate, add_parameter(s), step,
+//          zero_grad}                             (optimizers/adam/mod.rs)
+// Reference panics become ts::Error exceptions.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace ts {
+
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+// ---- runtime ----------------------------------------------------------------
+
+// Throws ts::Error("<what>: <message>") for a non-zero ts_hip status.
+void check(int status, const char *what);
+
+// Library state shared by every tensor of the process: the device stream all
+// work is queued on, and the device word where division kernels record the
+// first zero divisor (reported at the next synchronisation, see sync()).
+class Runtime {
+  public:
+    static Runtime &get();
+    void *stream() const { return stream_; }
+    unsigned long long *zero_index() const { return zero_index_; }
+    // Waits for queued work; throws the reference's division-by-zero panic
+    // message if a division kernel recorded a zero divisor.
+    void sync();
+
+  private:
+    Runtime();
+    void *stream_ = nullptr;
+    unsigned long long *zero_index_ = nullptr;
+};
+
+// Size-bucketed caching allocator for device buffers.  All work runs on the
+// one library stream, so a block released after its last use was queued can
+// be handed to later work without waiting.
+class DevicePool {
+  public:
+    static DevicePool &get();
+    float *acquire(size_t n_floats, size_t *rounded);
+    void release(float *p, size_t rounded);
+    void empty_cache();
+    size_t live_bytes() const { return live_; }
+    size_t cached_bytes() const { return cached_; }
+
+  private:
+    std::unordered_map<size_t, std::vector<float *>> free_;
+    size_t live_ = 0, cached_ = 0;
+};
+
+// Device variant of tensor/core/allocation.rs:43-187: owns one pooled device
+// buffer; shared (Arc-like) by tensors, saved graph operands and gradients.
+struct Allocation {
+    explicit Allocation(size_t n_floats);
+    ~Allocation();
+    Allocation(const Allocation &) = delete;
+    Allocation &operator=(const Allocation &) = delete;
+    float *ptr = nullptr;
+    size_t n = 0, rounded = 0;
+};
+
+// ---- profiling ----------------------------------------------------------------
+
+// Optional per-launch timing with device events on the library stream,
+// grouped by kernel class, with each launch's algorithmic work (FLOPs for
+// GEMMs, bytes for the bandwidth-bound kernels).
+enum class KernelClass : int { Gemm = 0, Elementwise = 1, Reduction = 2, Adam = 3, kCount = 4 };
+
+struct ClassStats {
+    double ms = 0.0;
+    double work = 0.0;  // FLOPs (Gemm) or bytes (others)
+    uint64_t launches = 0;
+};
+
+class Profiler {
+  public:
+    static Profiler &get();
+    void enable(bool on);
+    bool enabled() const { return enabled_; }
+    void begin();
+    void end(KernelClass k, double work);
+    // Synchronises and folds every recorded launch into the totals.
+    void collect();
+    ClassStats stats(KernelClass k) const { return totals_[static_cast<int>(k)]; }
+    void reset();
+
+  private:
+    struct Pending {
+        void *start, *stop;
+        KernelClass k;
+        double work;
+    };
+    bool enabled_ = false;
+    void *open_ = nullptr;
+    std::vector<Pending> pending_;
+    std::vector<void *> spare_;
+    ClassStats totals_[static_cast<int>(KernelClass::kCount)];
+};
+
+// ---- tensors --------------------------------------------------------------------
+
+class Tensor;
+
+struct SavedTensor {
+    std::shared_ptr<Allocation> alloc;
+    std::vector<size_t> dims;
+    const float *ptr() const { return alloc ? alloc->ptr : nullptr; }
+};
+
+// GradFn variants on the training-step path (gradtrack/grad_fn/mod.rs:127-450).
+struct GradFn {
+    enum class Kind {
+        Add, Sub, Mul, Div, AddScalar, SubScalar, MulScalar, DivScalar,
+        Relu, PowScalar, MatMul, ReduceSum, ReduceMean
+    };
+    explicit GradFn(Kind k) : kind(k) {}
+    Kind kind;
+    bool has_shapes = false;           // original_shapes: Some((a, b))
+    std::vector<size_t> shape_a, shape_b;
+    float scalar = 0.0f;               // scalar operand or exponent
+    std::vector<SavedTensor> saved;    // saved operands, shared not copied
+    bool req_left = false, req_right = false;
+    std::vector<size_t> input_shape;   // reductions
+    size_t numel = 0;
+
+    // GradFn::apply (grad_fn/mod.rs:490-789): gradients by operand position.
+    std::vector<std::optional<Tensor>> apply(const Tensor &grad_output) const;
+};
+
+class Tensor {
+  public:
+    Tensor() = default;
+    Tensor(Tensor &&) = default;
+    Tensor &operator=(Tensor &&) = default;
+    Tensor(const Tensor &) = delete;
+    Tensor &operator=(const Tensor &) = delete;
+
+    // construction (tensor/core/utils.rs:120-171, init/basic.rs, init/data.rs)
+    static Tensor new_uninit(std::vector<size_t> dims);
+    static Tensor zeros(std::vector<size_t> dims);
+    static Tensor ones(std::vector<size_t> dims);
+    static Tensor filled(std::vector<size_t> dims, float v);
+    static Tensor from_slice(const float *data, size_t len, std::vector<size_t> dims);
+
+    // Tensor::clone: new buffer with the same values, new id, no grad
+    Tensor clone() const;
+    // Handle on the same buffer with a new id (graph-internal sharing).
+    Tensor alias() const;
+
+    size_t id() const { return id_; }
+    const std::vector<size_t> &dims() const { return dims_; }
+    size_t size() const { return size_; }
+    const float *dev() const { return alloc_ ? alloc_->ptr : nullptr; }
+    float *dev_mut() { return alloc_ ? alloc_->ptr : nullptr; }
+    SavedTensor saved() const { return SavedTensor{alloc_, dims_}; }
+    static Tensor from_saved(const SavedTensor &s);
+
+    // gradient API (tensor/core/utils.rs:412-790)
+    bool requires_grad() const { return requires_grad_; }
+    Tensor &with_requires_grad() { requires_grad_ = true; return *this; }
+    void set_requires_grad(bool r);
+    void backward(const Tensor *grad_output = nullptr);
+    std::optional<Tensor> grad_by_value() const;
+    // The gradient Adam reads: self.grad, else the graph's map entry; no copy.
+    const Tensor *grad_ref() const;
+    void set_grad(Tensor g);
+    void zero_grad() { grad_.reset(); }
+    void accumulate_grad(Tensor g);
+
+    // recorded ops
+    Tensor add_tensor(const Tensor &o) const;
+    Tensor sub_tensor(const Tensor &o) const;
+    Tensor mul_tensor(const Tensor &o) const;
+    Tensor div_tensor(const Tensor &o) const;
+    Tensor add_scalar(float s) const;
+    Tensor sub_scalar(float s) const;
+    Tensor mul_scalar(float s) const;
+    Tensor div_scalar(float s) const;
+    Tensor relu() const;
+    Tensor pow_scalar(float e) const;
+    Tensor matmul(const Tensor &o) const;
+    Tensor sum() const;
+    Tensor mean() const;
+
+    // host access (synchronises)
+    std::vector<float> data() const;
+    void copy_to_host(float *out, size_t len) const;
+    float value() const;
+
+  private:
+    friend struct GradFn;
+    Tensor binary(const Tensor &o, GradFn::Kind kind) const;
+    Tensor scalar_op(float s, GradFn::Kind kind) const;
+    void record(Tensor &out, std::vector<size_t> input_ids, GradFn fn) const;
+
+    std::shared_ptr<Allocation> alloc_;
+    std::vector<size_t> dims_;
+    size_t size_ = 0;
+    size_t id_ = 0;
+    bool requires_grad_ = false;
+    std::shared_ptr<Tensor> grad_;
+};
+
+size_t next_tensor_id();
+
+// ---- gradtrack -------------------------------------------------------------------
+
+bool is_grad_enabled();
+void push_grad_enabled(bool on);   // NoGradTrack::new / with_no_grad (no_grad_track.rs)
+void pop_grad_enabled();
+void clear_gradients();            // engine.rs:812-816
+void register_operation(size_t output_id, std::vector<size_t> input_ids, GradFn fn);
+const Tensor *accumulated_gradient(size_t id);
+void engine_backward(Tensor &root, const Tensor *grad_output);
+
+// ---- optimizer -----------------------------------------------------------------------
+
+struct AdamConfig {
+    float learning_rate = 1e-3f;
+    float beta1 = 0.9f;
+    float beta2 = 0.999f;
+    float eps = 1e-8f;
+    float weight_decay = 0.0f;
+    bool amsgrad = false;
+};
+
+class Adam {
+  public:
+    Adam() = default;
+    static Adam with_config(AdamConfig c);
+    static Adam with_learning_rate(float lr);
+    void add_parameter(const Tensor &p);
+    void add_parameters(const std::vector<const Tensor *> &ps);
+    // Optimizer::step (adam/mod.rs:1036-1044); warns and skips params without grads.
+    void step(const std::vector<Tensor *> &params);
+    // Optimizer::zero_grad (adam/mod.rs:1061-1068)
+    void zero_grad(const std::vector<Tensor *> &params);
+    float learning_rate() const { return config_.learning_rate; }
+    void set_learning_rate(float lr) { config_.learning_rate = lr; }
+    const AdamConfig &config() const { return config_; }
+    uint64_t step_count() const { return step_count_; }
+    size_t parameter_count() const { return states_.size(); }
+    // m / v of a linked parameter (device), for checkpoint and tests.
+    const float *state_m(size_t param_id) const;
+    const float *state_v(size_t param_id) const;
+
+  private:
+    struct State {
+        std::shared_ptr<Allocation> m, v, v_hat_max;
+        size_t n = 0;
+        uint64_t step = 0;
+    };
+    AdamConfig config_;
+    std::unordered_map<size_t, State> states_;
+    std::vector<size_t> insertion_order_;
+    uint64_t step_count_ = 0;
+};
+
+}  // namespace ts

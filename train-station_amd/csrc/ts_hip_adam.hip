@@ -1,0 +1,102 @@
+// Fused Adam::step for one parameter tensor: one read of p, g, m, v and one
+// write of p, m, v per element (28 bytes), replacing the reference's five
+// passes and three temporary clones (optimizers/adam/mod.rs:485-1007) while
+// keeping its per-element fp32 operation order bit for bit.
+#include <cmath>
+
+#include "ts_hip_internal.h"
+
+namespace tship {
+
+struct AdamArgs {
+    float *p;
+    const float *g;
+    float *m;
+    float *v;
+    float *vmax;  // AMSGrad running max of v_hat, or nullptr
+    size_t n, n4, tail_start;
+    int amsgrad_first;
+    float b1, c1, b2, c2, cf1, cf2, lr, eps, wd;
+};
+
+__device__ inline void adam_elem(const AdamArgs &a, size_t i, float &p, float g, float &m,
+                                 float &v, float *vmax) {
+    if (a.wd > 0.0f) g = g + a.wd * p;                        // adam/mod.rs:567-620
+    m = a.b1 * m + a.c1 * g;                                  // :634-696
+    v = (i < a.tail_start) ? a.b2 * v + a.c2 * (g * g)        // :709-774 AVX2 body
+                           : a.b2 * v + (a.c2 * g) * g;       //          scalar tail
+    const float mh = m * a.cf1;                               // :790-833 bias_correct
+    float vh = v * a.cf2;
+    if (vmax) {                                               // :534-541 AMSGrad
+        const float old = a.amsgrad_first ? vh : *vmax;
+        vh = old > vh ? old : vh;
+        *vmax = vh;
+    }
+    const float den = sqrtf(vh) + a.eps;                      // :913-1007
+    p = p - (a.lr * mh) / den;
+}
+
+__global__ __launch_bounds__(kBlock) void adam_kernel(AdamArgs a) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    float4 *p4 = reinterpret_cast<float4 *>(a.p);
+    const float4 *g4 = reinterpret_cast<const float4 *>(a.g);
+    float4 *m4 = reinterpret_cast<float4 *>(a.m);
+    float4 *v4 = reinterpret_cast<float4 *>(a.v);
+    for (size_t q = t; q < a.n4; q += stride) {
+        float4 p = p4[q], g = g4[q], m = m4[q], v = v4[q];
+        float4 vm = a.vmax ? reinterpret_cast<const float4 *>(a.vmax)[q] : make_float4(0, 0, 0, 0);
+        float *vmp = a.vmax ? reinterpret_cast<float *>(&vm) : nullptr;
+        adam_elem(a, 4 * q + 0, p.x, g.x, m.x, v.x, vmp ? vmp + 0 : nullptr);
+        adam_elem(a, 4 * q + 1, p.y, g.y, m.y, v.y, vmp ? vmp + 1 : nullptr);
+        adam_elem(a, 4 * q + 2, p.z, g.z, m.z, v.z, vmp ? vmp + 2 : nullptr);
+        adam_elem(a, 4 * q + 3, p.w, g.w, m.w, v.w, vmp ? vmp + 3 : nullptr);
+        p4[q] = p;
+        m4[q] = m;
+        v4[q] = v;
+        if (a.vmax) reinterpret_cast<float4 *>(a.vmax)[q] = vm;
+    }
+    for (size_t i = 4 * a.n4 + t; i < a.n; i += stride) {
+        float p = a.p[i], m = a.m[i], v = a.v[i];
+        adam_elem(a, i, p, a.g[i], m, v, a.vmax ? a.vmax + i : nullptr);
+        a.p[i] = p;
+        a.m[i] = m;
+        a.v[i] = v;
+    }
+}
+
+// adam/mod.rs:524-531: (1 - (beta as f64).powf(step as f32 as f64)) as f32,
+// then bias_correct's 1.0 / bc in f32.
+static float correction_factor(float beta, uint64_t step_count) {
+    const float t = static_cast<float>(step_count);
+    const double bc = 1.0 - std::pow(static_cast<double>(beta), static_cast<double>(t));
+    return 1.0f / static_cast<float>(bc);
+}
+
+}  // namespace tship
+
+using namespace tship;
+
+extern "C" int ts_hip_adam_step(float *p, const float *g, float *m, float *v, float *v_hat_max,
+                                size_t n, float lr, float beta1, float beta2, float eps,
+                                float weight_decay, uint64_t step_count, size_t tail_start,
+                                int amsgrad_first, void *stream) {
+    if (n == 0) return TS_HIP_OK;
+    if (!p || !g || !m || !v || step_count == 0) return TS_HIP_EINVAL;
+    AdamArgs a{};
+    a.p = p; a.g = g; a.m = m; a.v = v; a.vmax = v_hat_max;
+    a.n = n;
+    a.amsgrad_first = amsgrad_first;
+    const bool vec = aligned16(p) && aligned16(g) && aligned16(m) && aligned16(v) &&
+                     (!v_hat_max || aligned16(v_hat_max));
+    a.n4 = vec ? n / 4 : 0;
+    a.tail_start = tail_start;
+    a.b1 = beta1; a.c1 = 1.0f - beta1;
+    a.b2 = beta2; a.c2 = 1.0f - beta2;
+    a.cf1 = correction_factor(beta1, step_count);
+    a.cf2 = correction_factor(beta2, step_count);
+    a.lr = lr; a.eps = eps; a.wd = weight_decay;
+    unsigned grid = grid_for(a.n4 ? a.n4 : n);
+    hipLaunchKernelGGL(adam_kernel, dim3(grid), dim3(kBlock), 0, as_stream(stream), a);
+    return launch_status();
+}

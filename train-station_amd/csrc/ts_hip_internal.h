@@ -1,0 +1,38 @@
+// Shared helpers of the gfx950 backend (device code and launchers).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ts_hip.h"
+
+namespace tship {
+
+constexpr int kBlock = 256;  // 4 wave64 per workgroup
+
+// Status of a launch: the error the runtime recorded for it, if any.
+inline int launch_status() {
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TS_HIP_OK : static_cast<int>(e);
+}
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+// Grid size for a grid-stride kernel covering `units` work items with
+// kBlock threads each handling `per_thread` items: enough workgroups to fill
+// every CU several times over, never more than the work needs.
+inline unsigned grid_for(size_t units, size_t per_thread = 1) {
+    size_t per_block = static_cast<size_t>(kBlock) * per_thread;
+    size_t need = (units + per_block - 1) / per_block;
+    size_t cap = static_cast<size_t>(device_cu_count()) * 16;
+    if (need > cap) need = cap;
+    return static_cast<unsigned>(need < 1 ? 1 : need);
+}
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace tship

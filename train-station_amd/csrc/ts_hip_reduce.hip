@@ -1,0 +1,177 @@
+// Reductions of the gradtrack step: the scalar loss (sum / mean) and the
+// bias-gradient column reduction sum_dims(&[0]).  Both are deterministic
+// two-pass trees: per-thread f64 accumulation over a fixed slice, a wave64
+// shuffle reduction, an LDS combine across the workgroup's four waves, one
+// f64 partial per workgroup, then a single-workgroup pass in fixed order.
+// No floating-point atomics, so every run gives the same bits.
+#include "ts_hip_internal.h"
+
+namespace tship {
+
+constexpr size_t kSumChunk = 8192;  // inputs per first-pass workgroup (minimum)
+constexpr size_t kSumMaxBlocks = 2048;
+
+static size_t sum_blocks(size_t n) {
+    size_t b = (n + kSumChunk - 1) / kSumChunk;
+    if (b > kSumMaxBlocks) b = kSumMaxBlocks;
+    return b < 1 ? 1 : b;
+}
+
+__device__ inline double wave_sum(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Sum of a workgroup's per-thread values, returned to thread 0.
+__device__ inline double block_sum(double v) {
+    __shared__ double lds[kBlock / 64];
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) lds[wave] = v;
+    __syncthreads();
+    double r = 0.0;
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int w = 0; w < kBlock / 64; ++w) r += lds[w];
+    }
+    return r;
+}
+
+// Pass 1: workgroup b sums the float4 groups b, b+G, b+2G, ... (all threads
+// of the grid stride together) and writes one f64 partial.
+__global__ __launch_bounds__(kBlock) void sum_partial(const float *__restrict__ x, size_t n,
+                                                      size_t n4, double *__restrict__ partial) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    double acc = 0.0;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    for (size_t v = t; v < n4; v += stride) {
+        float4 q = x4[v];
+        acc += (double)q.x + (double)q.y + (double)q.z + (double)q.w;
+    }
+    for (size_t i = 4 * n4 + t; i < n; i += stride) acc += (double)x[i];
+    double r = block_sum(acc);
+    if (threadIdx.x == 0) partial[blockIdx.x] = r;
+}
+
+// Pass 2: one workgroup adds the partials in a fixed order.  MEAN divides the
+// fp32 sum by (float)n, as reductions/mean.rs:104 does.
+template <bool MEAN>
+__global__ __launch_bounds__(kBlock) void sum_final(const double *__restrict__ partial,
+                                                    size_t nparts, size_t n, float *out) {
+    double acc = 0.0;
+    for (size_t i = threadIdx.x; i < nparts; i += kBlock) acc += partial[i];
+    double r = block_sum(acc);
+    if (threadIdx.x == 0) {
+        float s = static_cast<float>(r);
+        out[0] = MEAN ? s / static_cast<float>(n) : s;
+    }
+}
+
+template <bool MEAN>
+static int launch_sum(const float *x, size_t n, float *out, float *workspace, size_t ws,
+                      void *stream) {
+    if (!out) return TS_HIP_EINVAL;
+    hipStream_t s = as_stream(stream);
+    if (n == 0) {  // sum.rs:82-83 / mean.rs:51-53: empty input gives 0
+        return ts_hip_fill(out, 0.0f, 1, stream);
+    }
+    if (!x) return TS_HIP_EINVAL;
+    const size_t blocks = sum_blocks(n);
+    if (!workspace || ws < 2 * blocks) return TS_HIP_EWORKSPACE;
+    if ((reinterpret_cast<uintptr_t>(workspace) & 7u) != 0) return TS_HIP_EINVAL;
+    double *partial = reinterpret_cast<double *>(workspace);
+    size_t n4 = aligned16(x) ? n / 4 : 0;
+    hipLaunchKernelGGL(sum_partial, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, n,
+                       n4, partial);
+    int st = launch_status();
+    if (st) return st;
+    hipLaunchKernelGGL(sum_final<MEAN>, dim3(1), dim3(kBlock), 0, s, partial, blocks, n, out);
+    return launch_status();
+}
+
+// ---- column reduction [rows, cols] -> [cols] --------------------------------
+
+// Row chunks of the first pass: enough workgroups to cover the device, at
+// least 8 rows per chunk, at most 256 chunks.
+static size_t dim0_chunks(size_t rows, size_t cols) {
+    size_t col_blocks = (cols + kBlock - 1) / kBlock;
+    size_t want = 2048 / (col_blocks ? col_blocks : 1);
+    size_t by_rows = (rows + 7) / 8;
+    size_t c = want < by_rows ? want : by_rows;
+    if (c > 256) c = 256;
+    return c < 1 ? 1 : c;
+}
+
+// Pass 1: thread = one column, workgroup (x) = 256 columns, blockIdx.y = a
+// contiguous chunk of rows.  Coalesced: a wave reads 64 adjacent floats of
+// one row per step.
+__global__ __launch_bounds__(kBlock) void dim0_partial(const float *__restrict__ x, size_t rows,
+                                                       size_t cols, size_t rows_per_chunk,
+                                                       double *__restrict__ partial) {
+    const size_t c = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (c >= cols) return;
+    const size_t r0 = static_cast<size_t>(blockIdx.y) * rows_per_chunk;
+    size_t r1 = r0 + rows_per_chunk;
+    if (r1 > rows) r1 = rows;
+    double acc = 0.0;
+    for (size_t r = r0; r < r1; ++r) acc += (double)x[r * cols + c];
+    partial[static_cast<size_t>(blockIdx.y) * cols + c] = acc;
+}
+
+// Pass 2: thread = one column, adds the chunk partials in chunk order.
+__global__ __launch_bounds__(kBlock) void dim0_final(const double *__restrict__ partial,
+                                                     size_t chunks, size_t cols,
+                                                     float *__restrict__ out) {
+    const size_t c = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (c >= cols) return;
+    double acc = 0.0;
+    for (size_t k = 0; k < chunks; ++k) acc += partial[k * cols + c];
+    out[c] = static_cast<float>(acc);
+}
+
+}  // namespace tship
+
+using namespace tship;
+
+extern "C" {
+
+size_t ts_hip_sum_workspace_floats(size_t n) { return 2 * sum_blocks(n); }
+
+int ts_hip_sum(const float *x, size_t n, float *out, float *workspace, size_t workspace_floats,
+               void *stream) {
+    return launch_sum<false>(x, n, out, workspace, workspace_floats, stream);
+}
+
+int ts_hip_mean(const float *x, size_t n, float *out, float *workspace, size_t workspace_floats,
+                void *stream) {
+    return launch_sum<true>(x, n, out, workspace, workspace_floats, stream);
+}
+
+size_t ts_hip_sum_dim0_workspace_floats(size_t rows, size_t cols) {
+    return 2 * dim0_chunks(rows, cols) * cols;
+}
+
+int ts_hip_sum_dim0(const float *x, size_t rows, size_t cols, float *out, float *workspace,
+                    size_t workspace_floats, void *stream) {
+    if (cols == 0) return TS_HIP_OK;
+    if (!out) return TS_HIP_EINVAL;
+    if (rows == 0) return ts_hip_fill(out, 0.0f, cols, stream);
+    if (!x) return TS_HIP_EINVAL;
+    const size_t chunks = dim0_chunks(rows, cols);
+    if (!workspace || workspace_floats < 2 * chunks * cols) return TS_HIP_EWORKSPACE;
+    if ((reinterpret_cast<uintptr_t>(workspace) & 7u) != 0) return TS_HIP_EINVAL;
+    const size_t rows_per_chunk = (rows + chunks - 1) / chunks;
+    double *partial = reinterpret_cast<double *>(workspace);
+    hipStream_t s = as_stream(stream);
+    unsigned gx = static_cast<unsigned>((cols + kBlock - 1) / kBlock);
+    hipLaunchKernelGGL(dim0_partial, dim3(gx, static_cast<unsigned>(chunks)), dim3(kBlock), 0, s,
+                       x, rows, cols, rows_per_chunk, partial);
+    int st = launch_status();
+    if (st) return st;
+    hipLaunchKernelGGL(dim0_final, dim3(gx), dim3(kBlock), 0, s, partial, chunks, cols, out);
+    return launch_status();
+}
+
+}  // extern "C"

@@ -1,0 +1,183 @@
+// Runtime half of the C-ABI: device selection, memory, copies, streams,
+// events.  Replaces the host-only stub train-station/src/cuda/cuda_wrapper.cpp
+// (whose "device" memory is host `new float[]`, :37-52) with real HIP calls.
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "ts_hip_internal.h"
+
+namespace tship {
+
+static std::mutex g_cu_mutex;
+static std::vector<int> g_cu_count;  // per device, 0 = not queried yet
+
+int device_cu_count() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lock(g_cu_mutex);
+    if (static_cast<size_t>(dev) >= g_cu_count.size()) g_cu_count.resize(dev + 1, 0);
+    if (g_cu_count[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            cus = 256;
+        g_cu_count[dev] = cus;
+    }
+    return g_cu_count[dev];
+}
+
+static hipMemcpyKind copy_kind(int kind, bool *ok) {
+    *ok = true;
+    switch (kind) {
+        case 0: return hipMemcpyHostToDevice;
+        case 1: return hipMemcpyDeviceToHost;
+        case 2: return hipMemcpyDeviceToDevice;
+        default: *ok = false; return hipMemcpyDefault;
+    }
+}
+
+}  // namespace tship
+
+using namespace tship;
+
+extern "C" {
+
+int ts_hip_initialize(void) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (count <= 0) return TS_HIP_ENODEVICE;
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, 0);
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return TS_HIP_ENODEVICE;
+    e = hipSetDevice(0);
+    if (e != hipSuccess) return static_cast<int>(e);
+    device_cu_count();
+    return TS_HIP_OK;
+}
+
+void ts_hip_cleanup(void) { (void)hipDeviceSynchronize(); }
+
+int ts_hip_get_device_count(int *count) {
+    if (!count) return TS_HIP_EINVAL;
+    *count = 0;
+    hipError_t e = hipGetDeviceCount(count);
+    if (e == hipErrorNoDevice) { *count = 0; return TS_HIP_OK; }
+    return static_cast<int>(e);
+}
+
+int ts_hip_set_device(int device_id) { return static_cast<int>(hipSetDevice(device_id)); }
+
+int ts_hip_get_device(int *device_id) {
+    if (!device_id) return TS_HIP_EINVAL;
+    return static_cast<int>(hipGetDevice(device_id));
+}
+
+int ts_hip_malloc(float **ptr, size_t n_floats) {
+    if (!ptr) return TS_HIP_EINVAL;
+    *ptr = nullptr;
+    if (n_floats == 0) return TS_HIP_OK;
+    return static_cast<int>(hipMalloc(reinterpret_cast<void **>(ptr), n_floats * sizeof(float)));
+}
+
+int ts_hip_free(float *ptr) {
+    if (!ptr) return TS_HIP_OK;
+    return static_cast<int>(hipFree(ptr));
+}
+
+int ts_hip_memcpy(float *dst, const float *src, size_t n_floats, int kind) {
+    bool ok;
+    hipMemcpyKind k = copy_kind(kind, &ok);
+    if (!ok || (n_floats && (!dst || !src))) return TS_HIP_EINVAL;
+    if (n_floats == 0) return TS_HIP_OK;
+    return static_cast<int>(hipMemcpy(dst, src, n_floats * sizeof(float), k));
+}
+
+int ts_hip_memcpy_async(float *dst, const float *src, size_t n_floats, int kind, void *stream) {
+    bool ok;
+    hipMemcpyKind k = copy_kind(kind, &ok);
+    if (!ok || (n_floats && (!dst || !src))) return TS_HIP_EINVAL;
+    if (n_floats == 0) return TS_HIP_OK;
+    return static_cast<int>(
+        hipMemcpyAsync(dst, src, n_floats * sizeof(float), k, as_stream(stream)));
+}
+
+int ts_hip_host_malloc(void **ptr, size_t bytes) {
+    if (!ptr) return TS_HIP_EINVAL;
+    *ptr = nullptr;
+    if (bytes == 0) return TS_HIP_OK;
+    return static_cast<int>(hipHostMalloc(ptr, bytes, hipHostMallocDefault));
+}
+
+int ts_hip_host_free(void *ptr) {
+    if (!ptr) return TS_HIP_OK;
+    return static_cast<int>(hipHostFree(ptr));
+}
+
+int ts_hip_stream_create(void **stream) {
+    if (!stream) return TS_HIP_EINVAL;
+    hipStream_t s = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    *stream = s;
+    return static_cast<int>(e);
+}
+
+int ts_hip_stream_destroy(void *stream) {
+    if (!stream) return TS_HIP_OK;
+    return static_cast<int>(hipStreamDestroy(as_stream(stream)));
+}
+
+int ts_hip_stream_synchronize(void *stream) {
+    return static_cast<int>(hipStreamSynchronize(as_stream(stream)));
+}
+
+int ts_hip_device_synchronize(void) { return static_cast<int>(hipDeviceSynchronize()); }
+
+int ts_hip_event_create(void **event) {
+    if (!event) return TS_HIP_EINVAL;
+    hipEvent_t ev = nullptr;
+    hipError_t e = hipEventCreate(&ev);
+    *event = ev;
+    return static_cast<int>(e);
+}
+
+int ts_hip_event_destroy(void *event) {
+    if (!event) return TS_HIP_OK;
+    return static_cast<int>(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)));
+}
+
+int ts_hip_event_record(void *event, void *stream) {
+    if (!event) return TS_HIP_EINVAL;
+    return static_cast<int>(hipEventRecord(reinterpret_cast<hipEvent_t>(event), as_stream(stream)));
+}
+
+int ts_hip_event_synchronize(void *event) {
+    if (!event) return TS_HIP_EINVAL;
+    return static_cast<int>(hipEventSynchronize(reinterpret_cast<hipEvent_t>(event)));
+}
+
+int ts_hip_event_elapsed_ms(float *ms, void *start, void *stop) {
+    if (!ms || !start || !stop) return TS_HIP_EINVAL;
+    return static_cast<int>(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start),
+                                                reinterpret_cast<hipEvent_t>(stop)));
+}
+
+const char *ts_hip_error_string(int status) {
+    switch (status) {
+        case TS_HIP_OK: return "success";
+        case TS_HIP_EINVAL: return "invalid argument (shape, pointer, alignment or copy kind)";
+        case TS_HIP_ENODEVICE: return "no gfx950 device visible";
+        case TS_HIP_EWORKSPACE: return "workspace smaller than the size the kernel needs";
+        default: return hipGetErrorString(static_cast<hipError_t>(status));
+    }
+}
+
+int ts_hip_mem_info(size_t *free_bytes, size_t *total_bytes) {
+    if (!free_bytes || !total_bytes) return TS_HIP_EINVAL;
+    return static_cast<int>(hipMemGetInfo(free_bytes, total_bytes));
+}
+
+}  // extern "C"

@@ -1,0 +1,298 @@
+"""Python face of train-station's Tensor / gradtrack / Adam API on the MI355X.
+
+Every method is one call into ``libts_gradtrack.so`` (``include/ts_gradtrack.h``),
+whose C++ host code launches the gfx950 kernels of ``libts_hip.so``.  Method
+names and meaning follow the reference (tensor/core/utils.rs, tensor/ops/*,
+tensor/reductions/{sum,mean}.rs, gradtrack/, optimizers/adam/mod.rs); its
+panics surface as ``TsError``.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Iterable, Optional, Sequence
+
+import numpy as np
+
+from ._ffi import F, SZ, TsError, gradtrack as _G, last_error
+
+
+def _dims(shape: Sequence[int]):
+    shape = [int(d) for d in shape]
+    arr = (SZ * max(len(shape), 1))(*shape)
+    return arr, len(shape)
+
+
+def _wrap(handle) -> "Tensor":
+    if not handle:
+        raise TsError(last_error() or "native call returned no tensor")
+    return Tensor(handle)
+
+
+def _ok(status: int) -> None:
+    if status != 0:
+        raise TsError(last_error())
+
+
+class Tensor:
+    """Handle on a device tensor owned by the native host library."""
+
+    __slots__ = ("_h",)
+
+    def __init__(self, handle):
+        self._h = ctypes.c_void_p(handle)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            _G.ts_tensor_free(h)
+            self._h = None
+
+    # -- construction (utils.rs:120-171, init/basic.rs, init/data.rs) -----------
+    @staticmethod
+    def new(shape: Sequence[int]) -> "Tensor":
+        d, r = _dims(shape)
+        return _wrap(_G.ts_tensor_new(d, r))
+
+    @staticmethod
+    def zeros(shape: Sequence[int]) -> "Tensor":
+        d, r = _dims(shape)
+        return _wrap(_G.ts_tensor_zeros(d, r))
+
+    @staticmethod
+    def ones(shape: Sequence[int]) -> "Tensor":
+        d, r = _dims(shape)
+        return _wrap(_G.ts_tensor_ones(d, r))
+
+    @staticmethod
+    def from_slice(data, shape: Sequence[int]) -> "Tensor":
+        a = np.ascontiguousarray(np.asarray(data, dtype=np.float32).reshape(-1))
+        d, r = _dims(shape)
+        return _wrap(_G.ts_tensor_from_slice(a.ctypes.data_as(F), a.size, d, r))
+
+    def clone(self) -> "Tensor":
+        return _wrap(_G.ts_tensor_clone(self._h))
+
+    # -- metadata -----------------------------------------------------------------
+    def id(self) -> int:
+        return int(_G.ts_tensor_id(self._h))
+
+    @property
+    def shape(self) -> tuple:
+        rank = _G.ts_tensor_rank(self._h)
+        out = (SZ * max(rank, 1))()
+        _G.ts_tensor_dims(self._h, out, rank)
+        return tuple(int(out[i]) for i in range(rank))
+
+    def size(self) -> int:
+        return int(_G.ts_tensor_size(self._h))
+
+    def device_ptr(self) -> int:
+        return int(_G.ts_tensor_device_ptr(self._h) or 0)
+
+    # -- autograd flags (utils.rs:412-450) ------------------------------------------
+    def with_requires_grad(self) -> "Tensor":
+        _ok(_G.ts_tensor_with_requires_grad(self._h))
+        return self
+
+    def set_requires_grad(self, flag: bool) -> None:
+        _ok(_G.ts_tensor_set_requires_grad(self._h, int(bool(flag))))
+
+    def requires_grad(self) -> bool:
+        return bool(_G.ts_tensor_requires_grad(self._h))
+
+    # -- recorded ops -------------------------------------------------------------------
+    def add_tensor(self, other: "Tensor") -> "Tensor":
+        return _wrap(_G.ts_tensor_add_tensor(self._h, other._h))
+
+    def sub_tensor(self, other: "Tensor") -> "Tensor":
+        return _wrap(_G.ts_tensor_sub_tensor(self._h, other._h))
+
+    def mul_tensor(self, other: "Tensor") -> "Tensor":
+        return _wrap(_G.ts_tensor_mul_tensor(self._h, other._h))
+
+    def div_tensor(self, other: "Tensor") -> "Tensor":
+        return _wrap(_G.ts_tensor_div_tensor(self._h, other._h))
+
+    def add_scalar(self, s: float) -> "Tensor":
+        return _wrap(_G.ts_tensor_add_scalar(self._h, s))
+
+    def sub_scalar(self, s: float) -> "Tensor":
+        return _wrap(_G.ts_tensor_sub_scalar(self._h, s))
+
+    def mul_scalar(self, s: float) -> "Tensor":
+        return _wrap(_G.ts_tensor_mul_scalar(self._h, s))
+
+    def div_scalar(self, s: float) -> "Tensor":
+        return _wrap(_G.ts_tensor_div_scalar(self._h, s))
+
+    def relu(self) -> "Tensor":
+        return _wrap(_G.ts_tensor_relu(self._h))
+
+    def pow_scalar(self, e: float) -> "Tensor":
+        return _wrap(_G.ts_tensor_pow_scalar(self._h, e))
+
+    def matmul(self, other: "Tensor") -> "Tensor":
+        return _wrap(_G.ts_tensor_matmul(self._h, other._h))
+
+    def sum(self) -> "Tensor":
+        return _wrap(_G.ts_tensor_sum(self._h))
+
+    def mean(self) -> "Tensor":
+        return _wrap(_G.ts_tensor_mean(self._h))
+
+    # -- gradients (utils.rs:525-790) --------------------------------------------------
+    def backward(self, grad_output: Optional["Tensor"] = None) -> None:
+        _ok(_G.ts_tensor_backward(self._h, grad_output._h if grad_output is not None else None))
+
+    def grad_by_value(self) -> Optional["Tensor"]:
+        h = _G.ts_tensor_grad_by_value(self._h)
+        if not h:
+            err = last_error()
+            if err:
+                raise TsError(err)
+            return None
+        return Tensor(h)
+
+    def set_grad(self, grad: "Tensor") -> None:
+        _ok(_G.ts_tensor_set_grad(self._h, grad._h))
+
+    def zero_grad(self) -> None:
+        _ok(_G.ts_tensor_zero_grad(self._h))
+
+    # -- host access ------------------------------------------------------------------------
+    def data(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=np.float32)
+        _ok(_G.ts_tensor_data(self._h, out.ctypes.data_as(F), out.size))
+        return out
+
+    def value(self) -> float:
+        v = ctypes.c_float()
+        _ok(_G.ts_tensor_value(self._h, ctypes.byref(v)))
+        return float(v.value)
+
+    def __repr__(self) -> str:
+        return f"Tensor(id={self.id()}, shape={list(self.shape)}, requires_grad={self.requires_grad()})"
+
+
+def _handles(params: Iterable[Tensor]):
+    ps = list(params)
+    arr = (ctypes.c_void_p * max(len(ps), 1))(*[p._h.value for p in ps])
+    return arr, len(ps)
+
+
+class Adam:
+    """optimizers/adam/mod.rs (AdamConfig defaults: lr 1e-3, betas 0.9/0.999,
+    eps 1e-8, weight_decay 0, amsgrad off)."""
+
+    __slots__ = ("_h",)
+
+    def __init__(self, _handle=None):
+        h = _handle if _handle is not None else _G.ts_adam_new()
+        if not h:
+            raise TsError(last_error())
+        self._h = ctypes.c_void_p(h)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            _G.ts_adam_free(h)
+            self._h = None
+
+    @staticmethod
+    def new() -> "Adam":
+        return Adam()
+
+    @staticmethod
+    def with_config(learning_rate=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0,
+                    amsgrad=False) -> "Adam":
+        return Adam(_G.ts_adam_with_config(learning_rate, beta1, beta2, eps, weight_decay,
+                                           int(bool(amsgrad))))
+
+    @staticmethod
+    def with_learning_rate(lr: float) -> "Adam":
+        return Adam(_G.ts_adam_with_learning_rate(lr))
+
+    def add_parameter(self, p: Tensor) -> None:
+        _ok(_G.ts_adam_add_parameter(self._h, p._h))
+
+    def add_parameters(self, ps: Iterable[Tensor]) -> None:
+        for p in ps:
+            self.add_parameter(p)
+
+    def step(self, params: Iterable[Tensor]) -> None:
+        arr, n = _handles(params)
+        _ok(_G.ts_adam_step(self._h, arr, n))
+
+    def zero_grad(self, params: Iterable[Tensor]) -> None:
+        arr, n = _handles(params)
+        _ok(_G.ts_adam_zero_grad(self._h, arr, n))
+
+    def learning_rate(self) -> float:
+        return float(_G.ts_adam_learning_rate(self._h))
+
+    def set_learning_rate(self, lr: float) -> None:
+        _G.ts_adam_set_learning_rate(self._h, lr)
+
+    def step_count(self) -> int:
+        return int(_G.ts_adam_step_count(self._h))
+
+    def state(self, p: Tensor, which: str) -> np.ndarray:
+        out = np.empty(p.size(), dtype=np.float32)
+        _ok(_G.ts_adam_state(self._h, p._h, {"m": 0, "v": 1}[which], out.ctypes.data_as(F), out.size))
+        return out
+
+
+class NoGradTrack:
+    """gradtrack/no_grad_track.rs:80-130 as a context manager."""
+
+    def __enter__(self):
+        _G.ts_no_grad_push()
+        return self
+
+    def __exit__(self, *exc):
+        _G.ts_no_grad_pop()
+        return False
+
+
+def is_grad_enabled() -> bool:
+    return bool(_G.ts_is_grad_enabled())
+
+
+def clear_gradients() -> None:
+    _G.ts_clear_gradients()
+
+
+def synchronize() -> None:
+    _ok(_G.ts_synchronize())
+
+
+def stream() -> int:
+    return int(_G.ts_stream() or 0)
+
+
+class Profile:
+    """Device-event timing of every kernel the host library launches, by class."""
+
+    GEMM, ELEMENTWISE, REDUCTION, ADAM = 0, 1, 2, 3
+
+    @staticmethod
+    def enable(on: bool = True) -> None:
+        _G.ts_profile_enable(int(bool(on)))
+
+    @staticmethod
+    def reset() -> None:
+        _G.ts_profile_reset()
+
+    @staticmethod
+    def read(kernel_class: int):
+        ms, work, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_uint64()
+        _ok(_G.ts_profile_read(kernel_class, ctypes.byref(ms), ctypes.byref(work), ctypes.byref(n)))
+        return {"ms": ms.value, "work": work.value, "launches": int(n.value)}
+
+
+def pool_stats() -> dict:
+    return {"live_bytes": int(_G.ts_pool_live_bytes()), "cached_bytes": int(_G.ts_pool_cached_bytes())}
+
+
+def empty_cache() -> None:
+    _G.ts_pool_empty_cache()
