@@ -148,10 +148,16 @@ class OTensor:
     def div_scalar(self, s):
         return self._scalar_op("div", O.div_scalar, s)
 
-    def relu(self):
+    def relu(self, mask_source: Optional[np.ndarray] = None):
+        """ops/relu.rs:77-90.  ``mask_source`` (test hook) replaces the saved
+        input whose sign decides the backward mask, so a comparison with
+        another implementation can condition on that implementation's masks
+        where a pre-activation lies within rounding of zero."""
         out = OTensor(O.relu(self.data))
         if self.requires_grad and is_grad_enabled():
-            self._record(out, [self.id], GradFn("relu", saved=[self.data]))
+            saved = self.data if mask_source is None else np.ascontiguousarray(mask_source, np.float32)
+            assert saved.shape == self.data.shape
+            self._record(out, [self.id], GradFn("relu", saved=[saved]))
         return out
 
     def pow_scalar(self, e: float):

@@ -52,9 +52,13 @@ def bits(a) -> np.ndarray:
 
 
 def assert_bits_equal(got, want, what=""):
+    """Bit-for-bit equality, except that any two NaNs match: IEEE 754 leaves
+    the sign and payload of a generated NaN to the implementation (x86 SSE/AVX
+    produce 0xFFC00000 for inf - inf, gfx950 produces 0x7FC00000)."""
     g, w = bits(got), bits(want)
     assert g.shape == w.shape, (what, g.shape, w.shape)
-    bad = np.flatnonzero(g.reshape(-1) != w.reshape(-1))
+    both_nan = np.isnan(np.asarray(got, np.float32)) & np.isnan(np.asarray(want, np.float32))
+    bad = np.flatnonzero((g != w).reshape(-1) & ~both_nan.reshape(-1))
     assert bad.size == 0, (
         f"{what}: {bad.size} of {g.size} elements differ in bits; first at {bad[0]}: "
         f"got {np.asarray(got).reshape(-1)[bad[0]]!r} want {np.asarray(want).reshape(-1)[bad[0]]!r}")
@@ -66,3 +70,14 @@ def max_rel(got, want) -> float:
     want = np.asarray(want, dtype=np.float64)
     den = max(np.max(np.abs(want)), 1e-30)
     return float(np.max(np.abs(got - want)) / den)
+
+
+def rel_l2(got, want) -> float:
+    """Normwise L2 relative error ||got - want||_2 / ||want||_2.  Used for
+    parameters after many optimizer steps: a ReLU pre-activation within GEMM
+    rounding of zero can flip its mask in one of two correct GEMMs, moving a
+    single element by about one Adam step (~lr), which a max-norm measure
+    would report as the whole tensor's error."""
+    got = np.asarray(got, dtype=np.float64).reshape(-1)
+    want = np.asarray(want, dtype=np.float64).reshape(-1)
+    return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))

@@ -4,7 +4,9 @@ libts_hip.so) against the oracle's restatement of the reference
 
 Bars: elementwise ops, ReLU masks and Adam arithmetic bit-exact; matmul-derived
 gradients and reductions <= 1e-4 normwise relative error (max|d| / max|ref|);
-parameters after 100 Adam steps <= 1e-4 relative (normwise).  Loss values are
+parameters after many Adam steps <= 1e-4 normwise L2 relative error (see
+_train_both), with ReLU masks teacher-forced where a pre-activation is within
+rounding of zero (see _relu_both).  Loss values are
 compared with the f64 value (the reference's own sequential fp32 sum drifts,
 see tests/test_oracle.py)."""
 from __future__ import annotations
@@ -12,7 +14,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import assert_bits_equal, golden, max_rel, normal, uniform
+from conftest import assert_bits_equal, golden, max_rel, normal, rel_l2, uniform
 
 pytestmark = pytest.mark.gpu
 
@@ -109,37 +111,83 @@ def test_adam_libtorch_cases_on_device(TS, G, case):
         assert ((d <= c["rtol"] * np.abs(want)) | (d <= c["atol"])).all(), (case, step)
 
 
+# ---- teacher-forced ReLU masks -------------------------------------------------------------------
+#
+# Two correct fp32 GEMMs with different summation orders can put a
+# pre-activation that lies within rounding of zero on opposite sides of it;
+# the ReLU backward then routes an O(1) gradient differently.  The MLP tests
+# therefore (1) assert that device and oracle masks differ only where
+# |z| <= 1e-5 * max|z| and (2) hand the device's masks to the oracle's ReLU
+# backward, so every remaining difference is arithmetic.
+
+def _relu_both(z, zo, stats):
+    zg = z.data()
+    mism = (zg > 0) != (zo.data > 0)
+    if mism.any():
+        scale = float(np.max(np.abs(zo.data)))
+        assert np.all(np.abs(zo.data[mism]) <= 1e-5 * scale), "mask differs away from zero"
+        stats["flips"] = stats.get("flips", 0) + int(mism.sum())
+    return z.relu(), zo.relu(mask_source=zg)
+
+
+def _mlp_both(xd, td, pd, xo, to, po, stats, readme=False):
+    h, ho = xd, xo
+    n = len(pd) // 2
+    for i in range(n):
+        z = h.matmul(pd[2 * i]).add_tensor(pd[2 * i + 1])
+        zo = ho.matmul(po[2 * i]).add_tensor(po[2 * i + 1])
+        if i < n - 1 or readme:
+            h, ho = _relu_both(z, zo, stats)
+        else:
+            h, ho = z, zo
+    if readme:
+        return h.sum(), ho.sum()
+    return h.sub_tensor(td).pow_scalar(2.0).mean(), ho.sub_tensor(to).pow_scalar(2.0).mean()
+
+
+def _train_both(TS, G, ws, x, t, steps, readme=False, lr=1e-3):
+    pd = [TS.Tensor.from_slice(v, v.shape).with_requires_grad() for v in ws]
+    po = [G.OTensor(v.copy()).with_requires_grad() for v in ws]
+    opt, oopt = TS.Adam.with_learning_rate(lr), G.OAdam(lr)
+    opt.add_parameters(pd)
+    oopt.add_parameters(po)
+    xd, xo = TS.Tensor.from_slice(x, x.shape), G.OTensor(x)
+    td = TS.Tensor.from_slice(t, t.shape) if t is not None else None
+    to = G.OTensor(t) if t is not None else None
+    stats = {}
+    for step in range(steps):
+        loss, lo = _mlp_both(xd, td, pd, xo, to, po, stats, readme)
+        loss.backward()
+        lo.backward()
+        if step == 0:
+            for d, o in zip(pd, po):
+                assert max_rel(d.grad_by_value().data(), o.grad_by_value()) <= 1e-4
+        exact = lo.value()
+        assert abs(loss.value() - exact) <= 1e-4 * abs(exact), (step, loss.value(), exact)
+        opt.step(pd)
+        opt.zero_grad(pd)
+        oopt.step(po)
+        oopt.zero_grad(po)
+    # Parameters after several steps: normwise L2.  Adam's first steps move
+    # each element by about lr * sign(g); an element whose gradient cancels to
+    # the GEMM's rounding level has no fp32-determined sign, so a single
+    # element may differ by up to ~lr per step between two correct GEMMs.
+    worst = 0.0
+    for d, o in zip(pd, po):
+        got = d.data()
+        print(f"[train {steps} steps] max_rel {max_rel(got, o.data):.2e} rel_l2 {rel_l2(got, o.data):.2e}")
+        worst = max(worst, rel_l2(got, o.data))
+    print(f"[train] mask flips conditioned on: {stats.get('flips', 0)}")
+    return worst
+
+
 # ---- config 1: README quick-start step ---------------------------------------------------------
 
 def test_config1_readme_step(TS, G):
+    # x[32,784] ~ N(0,1), W[784,128] ~ N(0,1), b = 0; y = relu(x.W + b); loss = sum(y); 100 Adam steps
     x = normal((32, 784), 0)
-    w = normal((784, 128), 1)
-    b = np.zeros(128, np.float32)
-    pd = [TS.Tensor.from_slice(w, w.shape).with_requires_grad(), TS.Tensor.from_slice(b, b.shape).with_requires_grad()]
-    po = [G.OTensor(w.copy()).with_requires_grad(), G.OTensor(b.copy()).with_requires_grad()]
-    opt, oopt = TS.Adam.with_learning_rate(1e-3), G.OAdam(1e-3)
-    opt.add_parameters(pd)
-    oopt.add_parameters(po)
-    xd = TS.Tensor.from_slice(x, x.shape)
-    for step in range(100):
-        y = xd.matmul(pd[0]).add_tensor(pd[1]).relu()
-        loss = y.sum()
-        loss.backward()
-        if step == 0:
-            gw, gb = pd[0].grad_by_value().data(), pd[1].grad_by_value().data()
-        opt.step(pd)
-        opt.zero_grad(pd)
-        yo = G.OTensor(x).matmul(po[0]).add_tensor(po[1]).relu()
-        lo = yo.sum()
-        lo.backward()
-        if step == 0:
-            assert max_rel(gw, po[0].grad_by_value()) <= 1e-4
-            assert max_rel(gb, po[1].grad_by_value()) <= 1e-4
-            assert abs(loss.value() - float(np.sum(yo.data, dtype=np.float64))) <= 1e-4 * abs(loss.value())
-        oopt.step(po)
-        oopt.zero_grad(po)
-    for d, o in zip(pd, po):
-        assert max_rel(d.data(), o.data) <= 1e-4
+    ws = [normal((784, 128), 1), np.zeros(128, np.float32)]
+    assert _train_both(TS, G, ws, x, None, 100, readme=True) <= 1e-4
 
 
 # ---- config 2: elementwise autograd chain ------------------------------------------------------
@@ -202,17 +250,7 @@ def test_config3_adam_100_steps_via_api(TS, G):
 
 # ---- config 4 and a scaled config 5: MLP training steps ------------------------------------------
 
-def _mlp(lib_tensor, x, t, params, relu_last=False):
-    h = x
-    n = len(params) // 2
-    for i in range(n):
-        h = h.matmul(params[2 * i]).add_tensor(params[2 * i + 1])
-        if i < n - 1 or relu_last:
-            h = h.relu()
-    return h.sub_tensor(t).pow_scalar(2.0).mean()
-
-
-def _mlp_parity(TS, G, dims, batch, steps, seed, init):
+def _mlp_weights(dims, seed, init):
     rng = np.random.default_rng(seed)
     ws = []
     for i in range(len(dims) - 1):
@@ -223,66 +261,79 @@ def _mlp_parity(TS, G, dims, batch, steps, seed, init):
         else:
             w = (rng.standard_normal((dims[i], dims[i + 1])) / np.sqrt(fan_in)).astype(np.float32)
         ws += [w, np.zeros(dims[i + 1], np.float32)]
-    x = rng.standard_normal((batch, dims[0])).astype(np.float32)
-    t = rng.standard_normal((batch, dims[-1])).astype(np.float32)
-    pd = [TS.Tensor.from_slice(v, v.shape).with_requires_grad() for v in ws]
-    po = [G.OTensor(v.copy()).with_requires_grad() for v in ws]
-    opt, oopt = TS.Adam.new(), G.OAdam()
-    opt.add_parameters(pd)
-    oopt.add_parameters(po)
-    xd, td = TS.Tensor.from_slice(x, x.shape), TS.Tensor.from_slice(t, t.shape)
-    xo, to = G.OTensor(x), G.OTensor(t)
-    worst = 0.0
-    for step in range(steps):
-        loss = _mlp(TS, xd, td, pd)
-        loss.backward()
-        lo = _mlp(G, xo, to, po)
-        lo.backward()
-        if step == 0:
-            for d, o in zip(pd, po):
-                assert max_rel(d.grad_by_value().data(), o.grad_by_value()) <= 1e-4
-        assert abs(loss.value() - lo.value()) <= 1e-4 * abs(lo.value())
-        opt.step(pd)
-        opt.zero_grad(pd)
-        oopt.step(po)
-        oopt.zero_grad(po)
-    for d, o in zip(pd, po):
-        worst = max(worst, max_rel(d.data(), o.data))
-    return worst
+    return ws, rng
 
 
 def test_config4_mlp(TS, G):
     # batch 1024, 784 -> 1024 -> 10, Kaiming-uniform, MSE; 10 steps against the oracle
-    worst = _mlp_parity(TS, G, [784, 1024, 10], 1024, 10, seed=0, init="kaiming")
-    assert worst <= 1e-4
+    ws, rng = _mlp_weights([784, 1024, 10], 0, "kaiming")
+    x = rng.standard_normal((1024, 784)).astype(np.float32)
+    t = rng.standard_normal((1024, 10)).astype(np.float32)
+    assert _train_both(TS, G, ws, x, t, 10) <= 1e-4
 
 
 def test_config5_scaled_mlp(TS, G):
     # config 5 structure (6 layers, N(0, 1/fan_in) weights, ReLU on layers 1-5, MSE) at width 256
-    worst = _mlp_parity(TS, G, [256] * 7, 512, 5, seed=1, init="normal")
-    assert worst <= 1e-4
+    ws, rng = _mlp_weights([256] * 7, 1, "normal")
+    x = rng.standard_normal((512, 256)).astype(np.float32)
+    t = rng.standard_normal((512, 256)).astype(np.float32)
+    assert _train_both(TS, G, ws, x, t, 5) <= 1e-4
 
 
-def test_config5_full_size_step_runs(TS):
-    # the bench workload itself: two steps at B = 8192, 6 x 4096^2; finite and
-    # the loss moves (the contraction kernels at this shape are checked in
-    # test_kernels_gpu.py::test_gemm_full_size_sampled_rows)
+def _mlp(lib_tensor, x, t, params, relu_last=False):
+    h = x
+    n = len(params) // 2
+    for i in range(n):
+        h = h.matmul(params[2 * i]).add_tensor(params[2 * i + 1])
+        if i < n - 1 or relu_last:
+            h = h.relu()
+    return h.sub_tensor(t).pow_scalar(2.0).mean()
+
+
+def test_config5_full_size_step(TS, oracle):
+    # The bench workload at its real size (B = 8192, 6 x 4096^2, ReLU on 1-5,
+    # MSE), checked through size-independent properties: sampled output rows
+    # against an f64 forward pass, the loss against f64 over the downloaded
+    # output, the last bias gradient against 2/n * colsum(y - t) in f64, and
+    # Adam's first step, which moves every weight by lr * |g| / (|g| + eps).
     rng = np.random.default_rng(2)
-    D, B = 4096, 8192
+    D, B, L = 4096, 8192, 6
+    ws = [rng.standard_normal((D, D), dtype=np.float32) * np.float32(1 / 64) for _ in range(L)]
+    x = rng.standard_normal((B, D), dtype=np.float32)
+    t = rng.standard_normal((B, D), dtype=np.float32)
     ps = []
-    for _ in range(6):
-        w = (rng.standard_normal((D, D), dtype=np.float32) / np.float32(64.0))
-        ps += [TS.Tensor.from_slice(w, w.shape).with_requires_grad(),
-               TS.Tensor.zeros([D]).with_requires_grad()]
-    x = TS.Tensor.from_slice(rng.standard_normal((B, D), dtype=np.float32), [B, D])
-    t = TS.Tensor.from_slice(rng.standard_normal((B, D), dtype=np.float32), [B, D])
+    for w in ws:
+        ps += [TS.Tensor.from_slice(w, w.shape).with_requires_grad(), TS.Tensor.zeros([D]).with_requires_grad()]
+    xd, td = TS.Tensor.from_slice(x, [B, D]), TS.Tensor.from_slice(t, [B, D])
     opt = TS.Adam.new()
     opt.add_parameters(ps)
-    losses = []
-    for _ in range(2):
-        loss = _mlp(TS, x, t, ps)
-        loss.backward()
-        opt.step(ps)
-        opt.zero_grad(ps)
-        losses.append(loss.value())
-    assert all(np.isfinite(losses)) and losses[1] < losses[0]
+    h = xd
+    for i in range(L):
+        h = h.matmul(ps[2 * i]).add_tensor(ps[2 * i + 1])
+        if i < L - 1:
+            h = h.relu()
+    y = h
+    loss = y.sub_tensor(td).pow_scalar(2.0).mean()
+    loss.backward()
+    yg = y.data()
+    rows = np.array([0, 1, 4095, 8191])
+    hr = x[rows]
+    for i, w in enumerate(ws):
+        hr = oracle.gemm_f64(hr, w).astype(np.float32)
+        if i < L - 1:
+            hr = oracle.relu(hr)
+    assert max_rel(yg[rows], hr) <= 1e-4
+    d = yg.astype(np.float64) - t.astype(np.float64)
+    want_loss = float(np.mean(d * d))
+    assert abs(loss.value() - want_loss) <= 1e-5 * want_loss
+    want_db = 2.0 / (B * D) * d.sum(axis=0)
+    assert max_rel(ps[-1].grad_by_value().data(), want_db) <= 1e-4
+    g1 = ps[0].grad_by_value().data().astype(np.float64)
+    opt.step(ps)
+    # first step: m_hat = g and v_hat = g^2 (to a few ulp), so each weight
+    # moves by lr * |g| / (|g| + eps); the remaining error is the f32 rounding
+    # of the updated weight (|w| < 0.1, ulp <= 7.5e-9)
+    moved = np.abs(ps[0].data().astype(np.float64) - ws[0].astype(np.float64))
+    expected = 1e-3 * np.abs(g1) / (np.abs(g1) + 1e-8)
+    assert float(np.max(np.abs(moved - expected))) <= 2e-8
+    opt.zero_grad(ps)
