@@ -80,6 +80,19 @@ def step_flops(batch, widths, readme):
     return f
 
 
+def pmc_traffic(cfg_name: str):
+    """HBM bytes per GEMM launch from the committed rocprofv3 --pmc summary of
+    this workload (FETCH_SIZE and WRITE_SIZE runs, each scaled by the copy-kernel
+    calibration recorded in the same file), or None."""
+    import re
+
+    path = ROOT / "profiles" / f"{cfg_name}_gemm_pmc.md"
+    if not path.exists():
+        return None, None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+-]+)", path.read_text())
+    return (float(m.group(1)), str(path.relative_to(ROOT))) if m else (None, None)
+
+
 def cpu_baseline(cfg_name: str, sample_rows: int):
     """Single-core CPU restatement (oracle/) of one config-5 step, timed on a
     bounded sample and scaled: the three GEMM layouts on `sample_rows` output
@@ -149,6 +162,9 @@ def main() -> int:
     ap.add_argument("--config", default="c5", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-rows", type=int, default=512)
+    ap.add_argument("--copy-probe", type=int, default=0,
+                    help="first launch a plain copy kernel (x * 1.0 -> out, 8 bytes per float) over "
+                         "this many floats three times, as the calibration point of HBM byte counters")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -159,6 +175,16 @@ def main() -> int:
 
     import train_station_amd as TS
     from train_station_amd._ffi import hip, hip_check
+
+    if args.copy_probe:
+        n = args.copy_probe
+        src, dst = TS.Tensor.zeros([n]), TS.Tensor.zeros([n])
+        TS.synchronize()
+        for _ in range(3):
+            hip_check(hip.ts_hip_mul_scalar(src.device_ptr(), 1.0, dst.device_ptr(), n, TS.stream()))
+        TS.synchronize()
+        log(f"copy probe: 3 launches over {n} floats ({8 * n} bytes each)")
+        del src, dst
 
     batch, widths, init = CONFIGS[args.config]
     readme = init == "readme"
@@ -219,6 +245,7 @@ def main() -> int:
             kernels[k] = {"ms_per_step": round(s["ms"] / args.steps, 3), "launches_per_step": s["launches"] // args.steps,
                           "GB/s": round(rate / 1e9, 1), "frac_hbm_peak": round(rate / 1e9 / PEAK_HBM_GBS, 4)}
     per_launch_flops = g["work"] / g["launches"] if g["launches"] else 0.0
+    traffic, traffic_src = pmc_traffic(args.config)
 
     result = {
         "metric": "fwd+bwd+Adam steps/sec (1 GPU); % fp32 MFMA peak and % HBM GB/s roofline",
@@ -239,7 +266,8 @@ def main() -> int:
                                 "c1": "BASELINE config 1: README step x[32,784] W[784,128], relu, sum, Adam"}[args.config],
                    "batch": batch, "widths": widths, "gemm_flop_per_step": step_flops(batch, widths, readme)},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "kernel": "gemm_f32_mfma (all 3 layouts, every launch of the timed region)",
                      "flop_per_launch": per_launch_flops,
                      "avg_launch_ms": round(g["ms"] / g["launches"], 4) if g["launches"] else None},
