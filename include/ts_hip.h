@@ -174,7 +174,8 @@ int ts_hip_matmul(const float *a, const float *b, float *c, size_t m, size_t n, 
  *   trans_b == 0: B(k,j) = B[k*ldb + j]   (B stored [K][ldb])
  *   trans_b == 1: B(k,j) = B[j*ldb + k]   (B stored [N][ldb], i.e. B^T view)
  *   C(i,j) = C[i*ldc + j]
- * fp32 inputs, fp32 MFMA accumulation (v_mfma_f32_32x32x2_f32). */
+ * fp32 inputs, fp32 MFMA accumulation (v_mfma_f32_32x32x2_f32).  M, N, K and
+ * the leading dimensions must be below 2^31 (TS_HIP_EINVAL otherwise). */
 int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
                 size_t lda, const float *B, size_t ldb, float *C, size_t ldc, void *stream);
 

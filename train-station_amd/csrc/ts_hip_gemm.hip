@@ -8,15 +8,21 @@
 // here the transpose is only a different index order in the global->LDS
 // staging, so no transposed copy ever exists.
 //
-// Tiling: a 256-thread workgroup (4 wave64, 2x2) owns a 128x128 tile of C and
-// walks K in steps of 16.  Each wave owns 64x64 = 2x2 blocks of
-// v_mfma_f32_32x32x2_f32 accumulators (64 fp32 per lane).  Operand tiles live
-// in LDS k-major (As[k][m], Bs[k][n]) so that the MFMA operand read of a
-// wave is two rows of 32 consecutive floats; odd k rows are stored with the
-// two 32-column halves swapped so those two rows fall in different banks.
-// LDS is double buffered: global loads for tile k+1 are issued before the
-// MFMAs of tile k and written to the other buffer after them, with one
-// barrier per K step.
+// Tiling.  A workgroup owns a BM x BN tile of C and walks K in steps of BK=16.
+// Its waves form a WM x WN grid; each wave owns (BM/WM) x (BN/WN) of C as a
+// grid of 32x32 v_mfma_f32_32x32x2_f32 accumulators.  Two shapes:
+//   large problems: 256x256 tiles, 8 waves (2 per SIMD), 128x64 per wave;
+//   small problems: 128x128 tiles, 4 waves, 64x64 per wave.
+// LDS holds each operand tile k-major (As[k][m], Bs[k][n]) so a wave's MFMA
+// operand read is two rows of 32 consecutive floats.  Columns are XOR-swizzled
+// per k row (swz) so that (a) the two rows an MFMA operand read touches fall
+// in different bank halves and (b) the transposing store of a k-contiguous
+// operand (16 rows x 4 k-quads per wave instruction) is bank-conflict free.
+// Pipeline: LDS double buffer; at the top of iteration kt the registers of
+// tile kt+1 go to LDS and the global loads of tile kt+2 are issued, so both
+// overlap the MFMAs of tile kt; one barrier per K step.  Tiles wholly inside
+// the matrices (a uniform test) take an unguarded dwordx4 path; edge tiles
+// load element by element with bounds checks.
 // Workgroups are renumbered so that each XCD (the hardware deals workgroups
 // round-robin over 8 XCDs, each with its own L2) receives a contiguous run of
 // tiles, ordered in groups of 8 tile-rows so neighbouring tiles share A rows
@@ -27,77 +33,92 @@ namespace tship {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, BK = 16;
+constexpr int kBK = 16;
 constexpr int kGroupM = 8;
 constexpr int kXcds = 8;
 
-__device__ inline int swz(int k) { return (k & 1) << 5; }
+// Column swizzle of LDS row k: bit 4 from the k-quad, bit 5 from k's parity.
+__device__ __forceinline__ int swz(int k) { return (((k >> 2) & 3) << 4) ^ ((k & 1) << 5); }
 
 struct GemmArgs {
     const float *A;
     const float *B;
     float *C;
-    long M, N, K, lda, ldb, ldc;
+    int M, N, K, lda, ldb, ldc;
     int tiles_m, tiles_n;
-    bool a_vec, b_vec;  // 16-byte aligned base and leading dimension
+    int vec;  // both operands 16-byte aligned with leading dimensions % 4 == 0
 };
 
-// Stage one operand tile (logical [BK][128] slice, k-major) into registers.
-// KCONTIG: the operand's k index is contiguous in memory (row-major A, or
-// B^T); otherwise the 128-wide index (m of A, n of B) is contiguous.
-template <bool KCONTIG>
-__device__ inline void load_tile(const float *__restrict__ P, long ld, long rows, long K,
-                                 long r0, long k0, bool vec_ok, float4 (&reg)[2]) {
-    const int t = threadIdx.x;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
+// Staging of one operand tile: logical [BK][R] (k-major), R = 128 or 256
+// rows of the operand's non-k index.  KCONTIG: k is the contiguous index in
+// memory (row-major A, or B^T); otherwise the R index is contiguous.
+template <int R, int NT, bool KCONTIG>
+struct Stage {
+    static constexpr int NF = R * kBK / 4 / NT;  // float4 per thread
+    static_assert(NF >= 1 && R % 16 == 0, "tile does not divide over the workgroup");
+
+    // float4 number f -> (row, first k) of that float4 in the tile
+    static __device__ __forceinline__ void coords(int f, int &row, int &kk) {
         if (KCONTIG) {
-            const int row = (t >> 2) + 64 * s, kq = t & 3;
-            const long gr = r0 + row, gk = k0 + 4 * kq;
-            if (vec_ok && gr < rows && gk + 3 < K) {
-                reg[s] = *reinterpret_cast<const float4 *>(P + gr * ld + gk);
-            } else {
-                float v[4];
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    v[c] = (gr < rows && gk + c < K) ? P[gr * ld + gk + c] : 0.0f;
-                reg[s] = make_float4(v[0], v[1], v[2], v[3]);
-            }
+            // a wave instruction covers 16 rows x 4 k-quads: 16 lanes per k-quad
+            const int grp = f >> 6, l = f & 63;
+            const int rb = grp % (R / 16), kb = grp / (R / 16);
+            row = rb * 16 + (l & 15);
+            kk = 4 * (kb * 4 + (l >> 4));
         } else {
-            const int kk = (t >> 5) + 8 * s, q = t & 31;
-            const long gk = k0 + kk, gr = r0 + 4 * q;
-            if (vec_ok && gk < K && gr + 3 < rows) {
-                reg[s] = *reinterpret_cast<const float4 *>(P + gk * ld + gr);
-            } else {
-                float v[4];
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    v[c] = (gk < K && gr + c < rows) ? P[gk * ld + gr + c] : 0.0f;
-                reg[s] = make_float4(v[0], v[1], v[2], v[3]);
-            }
+            kk = f / (R / 4);
+            row = 4 * (f % (R / 4));
         }
     }
-}
 
-template <bool KCONTIG>
-__device__ inline void store_tile(float (*S)[128], const float4 (&reg)[2]) {
-    const int t = threadIdx.x;
+    // interior tile, 16-byte aligned: one dwordx4 per float4
+    static __device__ __forceinline__ void load_fast(const float *__restrict__ P, int ld, int r0,
+                                                     int k0, float4 (&reg)[NF]) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-        if (KCONTIG) {
-            const int row = (t >> 2) + 64 * s, kq = t & 3;
-            const float *v = reinterpret_cast<const float *>(&reg[s]);
+        for (int s = 0; s < NF; ++s) {
+            int row, kk;
+            coords(s * NT + threadIdx.x, row, kk);
+            reg[s] = KCONTIG
+                ? *reinterpret_cast<const float4 *>(P + (size_t)(r0 + row) * ld + (k0 + kk))
+                : *reinterpret_cast<const float4 *>(P + (size_t)(k0 + kk) * ld + (r0 + row));
+        }
+    }
+
+    // edge tile: element loads with bounds checks, zeros outside
+    static __device__ __forceinline__ void load_guarded(const float *__restrict__ P, int ld, int rows,
+                                                        int K, int r0, int k0, float4 (&reg)[NF]) {
+#pragma unroll
+        for (int s = 0; s < NF; ++s) {
+            int row, kk;
+            coords(s * NT + threadIdx.x, row, kk);
+            float v[4];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const int k = 4 * kq + c;
-                S[k][row ^ swz(k)] = v[c];
+                const int gr = KCONTIG ? r0 + row : r0 + row + c;
+                const int gk = KCONTIG ? k0 + kk + c : k0 + kk;
+                v[c] = (gr < rows && gk < K)
+                           ? (KCONTIG ? P[(size_t)gr * ld + gk] : P[(size_t)gk * ld + gr])
+                           : 0.0f;
             }
-        } else {
-            const int kk = (t >> 5) + 8 * s, q = t & 31;
-            *reinterpret_cast<float4 *>(&S[kk][(4 * q) ^ swz(kk)]) = reg[s];
+            reg[s] = make_float4(v[0], v[1], v[2], v[3]);
         }
     }
-}
+
+    static __device__ __forceinline__ void store(float *S, const float4 (&reg)[NF]) {
+#pragma unroll
+        for (int s = 0; s < NF; ++s) {
+            int row, kk;
+            coords(s * NT + threadIdx.x, row, kk);
+            if (KCONTIG) {
+                const float *v = reinterpret_cast<const float *>(&reg[s]);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) S[(kk + c) * R + (row ^ swz(kk + c))] = v[c];
+            } else {
+                *reinterpret_cast<float4 *>(&S[kk * R + (row ^ swz(kk))]) = reg[s];
+            }
+        }
+    }
+};
 
 // Tile coordinates of this workgroup (see the file comment).
 __device__ inline void tile_coords(int tiles_m, int tiles_n, int &tm, int &tn) {
@@ -117,60 +138,74 @@ __device__ inline void tile_coords(int tiles_m, int tiles_n, int &tm, int &tn) {
     tn = in_group / gsz;
 }
 
-template <bool TA, bool TB>
-__global__ __launch_bounds__(256) void gemm_f32_mfma(GemmArgs g) {
-    __shared__ float As[2][BK][BM];
-    __shared__ float Bs[2][BK][BN];
+template <bool TA, bool TB, int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
+    constexpr int NT = 64 * WM * WN;
+    constexpr int TMW = BM / WM, TNW = BN / WN;  // wave tile
+    constexpr int FM = TMW / 32, FN = TNW / 32;  // 32x32 accumulators per wave
+    using SA = Stage<BM, NT, !TA>;                // A is k-contiguous unless transposed
+    using SB = Stage<BN, NT, TB>;                 // B is k-contiguous only when transposed
+    __shared__ float As[2][kBK * BM];
+    __shared__ float Bs[2][kBK * BN];
 
     int tm, tn;
     tile_coords(g.tiles_m, g.tiles_n, tm, tn);
-    const long i0 = static_cast<long>(tm) * BM, j0 = static_cast<long>(tn) * BN;
-
+    const int i0 = tm * BM, j0 = tn * BN;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
     const int lrow = lane & 31, lhalf = lane >> 5;
 
-    floatx16 acc[2][2];
+    floatx16 acc[FM][FN];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < FM; ++a)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < FN; ++b)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
 
-    const long nk = (g.K + BK - 1) / BK;
-    float4 ra[2], rb[2];
-    // A is "k-contiguous" unless transposed; B is k-contiguous only when transposed.
-    load_tile<!TA>(g.A, g.lda, g.M, g.K, i0, 0, g.a_vec, ra);
-    load_tile<TB>(g.B, g.ldb, g.N, g.K, j0, 0, g.b_vec, rb);
-    store_tile<!TA>(As[0], ra);
-    store_tile<TB>(Bs[0], rb);
+    const int nk = (g.K + kBK - 1) / kBK;
+    const bool mn_inside = g.vec && (i0 + BM <= g.M) && (j0 + BN <= g.N);
+    float4 ra[SA::NF], rb[SB::NF];
+    auto load = [&](int k0) {
+        if (mn_inside && k0 + kBK <= g.K) {  // uniform across the workgroup
+            SA::load_fast(g.A, g.lda, i0, k0, ra);
+            SB::load_fast(g.B, g.ldb, j0, k0, rb);
+        } else {
+            SA::load_guarded(g.A, g.lda, g.M, g.K, i0, k0, ra);
+            SB::load_guarded(g.B, g.ldb, g.N, g.K, j0, k0, rb);
+        }
+    };
+
+    load(0);
+    SA::store(As[0], ra);
+    SB::store(Bs[0], rb);
+    if (nk > 1) load(kBK);
     __syncthreads();
 
-    for (long kt = 0; kt < nk; ++kt) {
+    for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
-        const bool more = kt + 1 < nk;
-        if (more) {
-            load_tile<!TA>(g.A, g.lda, g.M, g.K, i0, (kt + 1) * BK, g.a_vec, ra);
-            load_tile<TB>(g.B, g.ldb, g.N, g.K, j0, (kt + 1) * BK, g.b_vec, rb);
+        // LDS[cur] holds tile kt; registers hold tile kt+1.  Buffer cur^1 was
+        // last read before the previous barrier, so it can take tile kt+1 now.
+        if (kt + 1 < nk) {
+            SA::store(As[cur ^ 1], ra);
+            SB::store(Bs[cur ^ 1], rb);
+            if (kt + 2 < nk) load((kt + 2) * kBK);
         }
+        const float *Ac = As[cur];
+        const float *Bc = Bs[cur];
 #pragma unroll
-        for (int s = 0; s < BK / 2; ++s) {
+        for (int s = 0; s < kBK / 2; ++s) {
             const int k = 2 * s + lhalf;
-            float af[2], bf[2];
+            float af[FM], bf[FN];
 #pragma unroll
-            for (int a = 0; a < 2; ++a) af[a] = As[cur][k][(wm * 64 + a * 32 + lrow) ^ swz(k)];
+            for (int a = 0; a < FM; ++a) af[a] = Ac[k * BM + ((wm * TMW + a * 32 + lrow) ^ swz(k))];
 #pragma unroll
-            for (int b = 0; b < 2; ++b) bf[b] = Bs[cur][k][(wn * 64 + b * 32 + lrow) ^ swz(k)];
+            for (int b = 0; b < FN; ++b) bf[b] = Bc[k * BN + ((wn * TNW + b * 32 + lrow) ^ swz(k))];
 #pragma unroll
-            for (int a = 0; a < 2; ++a)
+            for (int a = 0; a < FM; ++a)
 #pragma unroll
-                for (int b = 0; b < 2; ++b)
+                for (int b = 0; b < FN; ++b)
                     acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a], bf[b], acc[a][b], 0, 0, 0);
-        }
-        if (more) {
-            store_tile<!TA>(As[cur ^ 1], ra);
-            store_tile<TB>(Bs[cur ^ 1], rb);
         }
         __syncthreads();
     }
@@ -178,17 +213,29 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma(GemmArgs g) {
     // Accumulator layout of v_mfma_f32_32x32x2_f32: lane l, register r holds
     // C[8*(r/4) + 4*(l/32) + r%4][l%32] of the 32x32 block.
 #pragma unroll
-    for (int a = 0; a < 2; ++a) {
+    for (int a = 0; a < FM; ++a) {
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            const long j = j0 + wn * 64 + b * 32 + lrow;
+        for (int b = 0; b < FN; ++b) {
+            const int j = j0 + wn * TNW + b * 32 + lrow;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const long i = i0 + wm * 64 + a * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-                if (i < g.M && j < g.N) g.C[i * g.ldc + j] = acc[a][b][r];
+                const int i = i0 + wm * TMW + a * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+                if (i < g.M && j < g.N) g.C[(size_t)i * g.ldc + j] = acc[a][b][r];
             }
         }
     }
+}
+
+template <int BM, int BN, int WM, int WN>
+static void launch_tiles(int ta, int tb, GemmArgs g, hipStream_t s) {
+    g.tiles_m = (g.M + BM - 1) / BM;
+    g.tiles_n = (g.N + BN - 1) / BN;
+    dim3 grid(static_cast<unsigned>(g.tiles_m) * static_cast<unsigned>(g.tiles_n));
+    dim3 block(64 * WM * WN);
+    if (!ta && !tb) hipLaunchKernelGGL((gemm_f32_mfma<false, false, BM, BN, WM, WN>), grid, block, 0, s, g);
+    else if (!ta && tb) hipLaunchKernelGGL((gemm_f32_mfma<false, true, BM, BN, WM, WN>), grid, block, 0, s, g);
+    else if (ta && !tb) hipLaunchKernelGGL((gemm_f32_mfma<true, false, BM, BN, WM, WN>), grid, block, 0, s, g);
+    else hipLaunchKernelGGL((gemm_f32_mfma<true, true, BM, BN, WM, WN>), grid, block, 0, s, g);
 }
 
 }  // namespace tship
@@ -206,22 +253,22 @@ extern "C" int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t 
     }
     if (!A || !B) return TS_HIP_EINVAL;
     if (lda < (trans_a ? M : K) || ldb < (trans_b ? K : N)) return TS_HIP_EINVAL;
-    const size_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    if (tiles_m * tiles_n > 0x7fffffffULL || M > 0x3fffffffffffULL) return TS_HIP_EINVAL;
+    // dimensions and leading dimensions are 32-bit inside the kernel (element
+    // offsets are formed in 64 bits), and the tile count must fit one grid
+    const size_t lim = 0x7ffffe00ULL;  // room for i0 + BM within int
+    if (M > lim || N > lim || K > lim || lda > lim || ldb > lim || ldc > lim) return TS_HIP_EINVAL;
+    if (((M + 127) / 128) * ((N + 127) / 128) > 0x7fffffffULL) return TS_HIP_EINVAL;
     GemmArgs g;
     g.A = A; g.B = B; g.C = C;
-    g.M = static_cast<long>(M); g.N = static_cast<long>(N); g.K = static_cast<long>(K);
-    g.lda = static_cast<long>(lda); g.ldb = static_cast<long>(ldb); g.ldc = static_cast<long>(ldc);
-    g.tiles_m = static_cast<int>(tiles_m);
-    g.tiles_n = static_cast<int>(tiles_n);
-    g.a_vec = aligned16(A) && (lda % 4 == 0);
-    g.b_vec = aligned16(B) && (ldb % 4 == 0);
-    dim3 grid(static_cast<unsigned>(tiles_m * tiles_n)), block(256);
+    g.M = static_cast<int>(M); g.N = static_cast<int>(N); g.K = static_cast<int>(K);
+    g.lda = static_cast<int>(lda); g.ldb = static_cast<int>(ldb); g.ldc = static_cast<int>(ldc);
+    g.tiles_m = g.tiles_n = 0;
+    g.vec = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0);
     hipStream_t s = as_stream(stream);
-    if (!trans_a && !trans_b) hipLaunchKernelGGL((gemm_f32_mfma<false, false>), grid, block, 0, s, g);
-    else if (!trans_a && trans_b) hipLaunchKernelGGL((gemm_f32_mfma<false, true>), grid, block, 0, s, g);
-    else if (trans_a && !trans_b) hipLaunchKernelGGL((gemm_f32_mfma<true, false>), grid, block, 0, s, g);
-    else hipLaunchKernelGGL((gemm_f32_mfma<true, true>), grid, block, 0, s, g);
+    // 256x256 tiles once they alone fill every CU; 128x128 below that.
+    const size_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256);
+    if (big_tiles >= static_cast<size_t>(device_cu_count())) launch_tiles<256, 256, 2, 4>(trans_a, trans_b, g, s);
+    else launch_tiles<128, 128, 2, 2>(trans_a, trans_b, g, s);
     return launch_status();
 }
 
