@@ -199,6 +199,28 @@ int ts_hip_adam_step(float *p, const float *g, float *m, float *v, float *v_hat_
                      float lr, float beta1, float beta2, float eps, float weight_decay,
                      uint64_t step_count, size_t tail_start, int amsgrad_first, void *stream);
 
+/* One parameter of a multi-tensor Adam launch (fields as in ts_hip_adam_step;
+ * the tail rule is the reference's, tail_start = 8*floor(n/8)). */
+typedef struct ts_hip_adam_param {
+    float *p;
+    const float *g;
+    float *m;
+    float *v;
+    float *v_hat_max; /* NULL unless AMSGrad */
+    size_t n;
+    int amsgrad_first;
+} ts_hip_adam_param;
+
+#define TS_HIP_ADAM_MAX_PARAMS 16
+
+/* Optimizer::step over up to TS_HIP_ADAM_MAX_PARAMS parameters in one launch
+ * (adam/mod.rs:1036-1044 steps them one after another; they are independent,
+ * so one launch gives the same bits).  Larger counts: call once per group of
+ * 16 with the same step_count. */
+int ts_hip_adam_step_multi(const ts_hip_adam_param *params, size_t count, float lr, float beta1,
+                           float beta2, float eps, float weight_decay, uint64_t step_count,
+                           void *stream);
+
 #ifdef __cplusplus
 }
 #endif

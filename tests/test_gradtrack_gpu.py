@@ -230,6 +230,23 @@ def test_division_by_zero_is_reported(TS):
 
 # ---- config 3: Adam alone -----------------------------------------------------------------------
 
+def test_adam_step_with_a_parameter_listed_twice(TS, G):
+    # adam/mod.rs:1036-1044 updates each listed parameter in turn, so a
+    # parameter listed twice is stepped twice with the same step_count
+    p0, g = normal(100, 6), normal(100, 7, 0.1)
+    p = TS.Tensor.from_slice(p0, [100]).with_requires_grad()
+    p.set_grad(TS.Tensor.from_slice(g, [100]))
+    opt = TS.Adam.new()
+    opt.add_parameter(p)
+    po = G.OTensor(p0.copy()).with_requires_grad()
+    po.grad = g.copy()
+    oopt = G.OAdam()
+    oopt.add_parameter(po)
+    opt.step([p, p])
+    oopt.step([po, po])
+    assert_bits_equal(p.data(), po.data, "parameter stepped twice")
+
+
 def test_config3_adam_100_steps_via_api(TS, G):
     # p ~ N(0,1), g ~ N(0, 1e-2) set once with set_grad (utils.rs:766-770), m = v = 0
     n = 1 << 22

@@ -282,3 +282,38 @@ def test_adam_100_steps_bit_exact(oracle):
     sync()
     assert_bits_equal(dp.get(), p, "p after 100 steps")
     assert_bits_equal(dv.get(), v, "v after 100 steps")
+
+
+def test_adam_multi_matches_per_parameter(oracle):
+    # one launch over several parameters (different sizes, tails, AMSGrad
+    # first/later steps, weight decay) gives the per-parameter bits
+    from train_station_amd._ffi import AdamParam
+    import ctypes
+    sizes = [1, 7, 9, 4096, 1000, (1 << 18) + 3]
+    for wd, ams in ((0.0, False), (0.01, True)):
+        host = []
+        for i, n in enumerate(sizes):
+            p = normal(n, 200 + i)
+            m = np.zeros(n, np.float32)
+            v = np.zeros(n, np.float32)
+            vm = np.zeros(n, np.float32) if ams else None
+            host.append([p, m, v, vm])
+        dev = [[Dev.of(h[0]), Dev.of(h[1]), Dev.of(h[2]), Dev.of(h[3]) if ams else None] for h in host]
+        for step in range(1, 4):
+            grads = [normal(n, 300 + 10 * step + i, 0.1) for i, n in enumerate(sizes)]
+            dg = [Dev.of(g) for g in grads]
+            arr = (AdamParam * len(sizes))()
+            for i, n in enumerate(sizes):
+                d = dev[i]
+                arr[i] = AdamParam(d[0].ptr, dg[i].ptr, d[1].ptr, d[2].ptr, d[3].ptr if ams else None, n,
+                                   int(step == 1))
+            _run("ts_hip_adam_step_multi", ctypes.cast(arr, ctypes.c_void_p), len(sizes), 1e-3, 0.9, 0.999,
+                 1e-8, wd, step, None)
+            for i, n in enumerate(sizes):
+                h = host[i]
+                oracle.adam_step(h[0], grads[i], h[1], h[2], step, weight_decay=wd, vmax=h[3],
+                                 amsgrad_first=(step == 1))
+        for i in range(len(sizes)):
+            assert_bits_equal(dev[i][0].get(), host[i][0], f"p[{i}] wd={wd} ams={ams}")
+            assert_bits_equal(dev[i][2].get(), host[i][2], f"v[{i}] wd={wd} ams={ams}")
+    assert hip.ts_hip_adam_step_multi(None, 17, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, None) == 100001

@@ -88,7 +88,15 @@ HIP_SIGNATURES = {
     "ts_hip_gemm": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, SZ, VP]),
     "ts_hip_adam_step": (_c.c_int, [VP, VP, VP, VP, VP, SZ, _c.c_float, _c.c_float, _c.c_float,
                                     _c.c_float, _c.c_float, _c.c_uint64, SZ, _c.c_int, VP]),
+    "ts_hip_adam_step_multi": (_c.c_int, [VP, SZ, _c.c_float, _c.c_float, _c.c_float, _c.c_float,
+                                          _c.c_float, _c.c_uint64, VP]),
 }
+
+
+class AdamParam(ctypes.Structure):
+    """struct ts_hip_adam_param of include/ts_hip.h"""
+    _fields_ = [("p", VP), ("g", VP), ("m", VP), ("v", VP), ("v_hat_max", VP), ("n", SZ),
+                ("amsgrad_first", _c.c_int)]
 
 TP = VP  # opaque ts_tensor* / ts_adam*
 

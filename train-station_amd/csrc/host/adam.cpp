@@ -43,6 +43,20 @@ void Adam::add_parameters(const std::vector<const Tensor *> &ps) {
 
 void Adam::step(const std::vector<Tensor *> &params) {
     step_count_ += 1;  // adam/mod.rs:1037
+    std::vector<ts_hip_adam_param> batch;
+    double bytes = 0.0;
+    auto flush = [&]() {
+        if (batch.empty()) return;
+        Profiler &P = Profiler::get();
+        P.begin();
+        check(ts_hip_adam_step_multi(batch.data(), batch.size(), config_.learning_rate, config_.beta1,
+                                     config_.beta2, config_.eps, config_.weight_decay, step_count_,
+                                     Runtime::get().stream()),
+              "ts_hip_adam_step_multi");
+        P.end(KernelClass::Adam, bytes);
+        batch.clear();
+        bytes = 0.0;
+    };
     for (Tensor *p : params) {
         auto it = states_.find(p->id());
         if (it == states_.end())  // adam/mod.rs:489-492
@@ -64,16 +78,19 @@ void Adam::step(const std::vector<Tensor *> &params) {
             first = 1;
         }
         if (!s.n) continue;
-        Profiler &P = Profiler::get();
-        P.begin();
-        check(ts_hip_adam_step(p->dev_mut(), g->dev(), s.m->ptr, s.v->ptr,
-                               config_.amsgrad ? s.v_hat_max->ptr : nullptr, s.n,
-                               config_.learning_rate, config_.beta1, config_.beta2, config_.eps,
-                               config_.weight_decay, step_count_, (s.n / 8) * 8, first,
-                               Runtime::get().stream()),
-              "ts_hip_adam_step");
-        P.end(KernelClass::Adam, 28.0 * s.n + (config_.amsgrad ? 8.0 * s.n : 0.0));
+        // parameters are independent: one launch steps up to 16 of them; a
+        // parameter listed twice is stepped twice in order, so it starts a new launch
+        for (const ts_hip_adam_param &q : batch)
+            if (q.p == p->dev_mut()) {
+                flush();
+                break;
+            }
+        batch.push_back(ts_hip_adam_param{p->dev_mut(), g->dev(), s.m->ptr, s.v->ptr,
+                                          config_.amsgrad ? s.v_hat_max->ptr : nullptr, s.n, first});
+        bytes += 28.0 * s.n + (config_.amsgrad ? 8.0 * s.n : 0.0);
+        if (batch.size() == TS_HIP_ADAM_MAX_PARAMS) flush();
     }
+    flush();
 }
 
 void Adam::zero_grad(const std::vector<Tensor *> &params) {

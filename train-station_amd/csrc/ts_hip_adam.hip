@@ -77,6 +77,52 @@ static float correction_factor(float beta, uint64_t step_count) {
 
 using namespace tship;
 
+struct MultiArgs {
+    ts_hip_adam_param prm[TS_HIP_ADAM_MAX_PARAMS];
+    int vec[TS_HIP_ADAM_MAX_PARAMS];
+    float b1, c1, b2, c2, cf1, cf2, lr, eps, wd;
+};
+
+// blockIdx.y selects the parameter; its workgroups stride over its float4
+// groups.  Same per-element arithmetic as adam_kernel.
+__global__ __launch_bounds__(kBlock) void adam_multi_kernel(MultiArgs A) {
+    const ts_hip_adam_param &q = A.prm[blockIdx.y];
+    AdamArgs a{};
+    a.p = q.p; a.g = q.g; a.m = q.m; a.v = q.v; a.vmax = q.v_hat_max;
+    a.n = q.n;
+    a.n4 = A.vec[blockIdx.y] ? q.n / 4 : 0;
+    a.tail_start = (q.n / 8) * 8;
+    a.amsgrad_first = q.amsgrad_first;
+    a.b1 = A.b1; a.c1 = A.c1; a.b2 = A.b2; a.c2 = A.c2;
+    a.cf1 = A.cf1; a.cf2 = A.cf2; a.lr = A.lr; a.eps = A.eps; a.wd = A.wd;
+    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    float4 *p4 = reinterpret_cast<float4 *>(a.p);
+    const float4 *g4 = reinterpret_cast<const float4 *>(a.g);
+    float4 *m4 = reinterpret_cast<float4 *>(a.m);
+    float4 *v4 = reinterpret_cast<float4 *>(a.v);
+    for (size_t i = t; i < a.n4; i += stride) {
+        float4 p = p4[i], g = g4[i], m = m4[i], v = v4[i];
+        float4 vm = a.vmax ? reinterpret_cast<const float4 *>(a.vmax)[i] : make_float4(0, 0, 0, 0);
+        float *vmp = a.vmax ? reinterpret_cast<float *>(&vm) : nullptr;
+        adam_elem(a, 4 * i + 0, p.x, g.x, m.x, v.x, vmp ? vmp + 0 : nullptr);
+        adam_elem(a, 4 * i + 1, p.y, g.y, m.y, v.y, vmp ? vmp + 1 : nullptr);
+        adam_elem(a, 4 * i + 2, p.z, g.z, m.z, v.z, vmp ? vmp + 2 : nullptr);
+        adam_elem(a, 4 * i + 3, p.w, g.w, m.w, v.w, vmp ? vmp + 3 : nullptr);
+        p4[i] = p;
+        m4[i] = m;
+        v4[i] = v;
+        if (a.vmax) reinterpret_cast<float4 *>(a.vmax)[i] = vm;
+    }
+    for (size_t i = 4 * a.n4 + t; i < a.n; i += stride) {
+        float p = a.p[i], m = a.m[i], v = a.v[i];
+        adam_elem(a, i, p, a.g[i], m, v, a.vmax ? a.vmax + i : nullptr);
+        a.p[i] = p;
+        a.m[i] = m;
+        a.v[i] = v;
+    }
+}
+
 extern "C" int ts_hip_adam_step(float *p, const float *g, float *m, float *v, float *v_hat_max,
                                 size_t n, float lr, float beta1, float beta2, float eps,
                                 float weight_decay, uint64_t step_count, size_t tail_start,
@@ -98,5 +144,35 @@ extern "C" int ts_hip_adam_step(float *p, const float *g, float *m, float *v, fl
     a.lr = lr; a.eps = eps; a.wd = weight_decay;
     unsigned grid = grid_for(a.n4 ? a.n4 : n);
     hipLaunchKernelGGL(adam_kernel, dim3(grid), dim3(kBlock), 0, as_stream(stream), a);
+    return launch_status();
+}
+
+extern "C" int ts_hip_adam_step_multi(const ts_hip_adam_param *params, size_t count, float lr,
+                                      float beta1, float beta2, float eps, float weight_decay,
+                                      uint64_t step_count, void *stream) {
+    if (count == 0) return TS_HIP_OK;
+    if (!params || count > TS_HIP_ADAM_MAX_PARAMS || step_count == 0) return TS_HIP_EINVAL;
+    MultiArgs A{};
+    size_t max_units = 0;
+    for (size_t i = 0; i < count; ++i) {
+        const ts_hip_adam_param &q = params[i];
+        if (q.n && (!q.p || !q.g || !q.m || !q.v)) return TS_HIP_EINVAL;
+        A.prm[i] = q;
+        A.vec[i] = aligned16(q.p) && aligned16(q.g) && aligned16(q.m) && aligned16(q.v) &&
+                   (!q.v_hat_max || aligned16(q.v_hat_max));
+        const size_t units = A.vec[i] ? q.n / 4 + q.n % 4 : q.n;
+        if (units > max_units) max_units = units;
+    }
+    if (max_units == 0) return TS_HIP_OK;
+    A.b1 = beta1; A.c1 = 1.0f - beta1;
+    A.b2 = beta2; A.c2 = 1.0f - beta2;
+    A.cf1 = correction_factor(beta1, step_count);
+    A.cf2 = correction_factor(beta2, step_count);
+    A.lr = lr; A.eps = eps; A.wd = weight_decay;
+    size_t gx = (max_units + kBlock - 1) / kBlock;
+    const size_t cap = static_cast<size_t>(device_cu_count()) * 8;
+    if (gx > cap) gx = cap;
+    hipLaunchKernelGGL(adam_multi_kernel, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(count)),
+                       dim3(kBlock), 0, as_stream(stream), A);
     return launch_status();
 }

@@ -93,42 +93,80 @@ static int launch_sum(const float *x, size_t n, float *out, float *workspace, si
 
 // ---- column reduction [rows, cols] -> [cols] --------------------------------
 
-// Row chunks of the first pass: enough workgroups to cover the device, at
-// least 8 rows per chunk, at most 256 chunks.
+// Pass 1: a thread owns 4 adjacent columns (one float4; 1 column when cols is
+// not a multiple of 4) over a contiguous chunk of rows; a workgroup covers
+// 256 such column groups, so each row step of a wave reads 1 KiB contiguously.
+// Row chunks are sized so the grid fills the device.
+constexpr size_t kDim0MaxChunks = 128;
+
 static size_t dim0_chunks(size_t rows, size_t cols) {
-    size_t col_blocks = (cols + kBlock - 1) / kBlock;
-    size_t want = 2048 / (col_blocks ? col_blocks : 1);
-    size_t by_rows = (rows + 7) / 8;
+    const size_t groups = (cols % 4 == 0) ? cols / 4 : cols;
+    const size_t col_blocks = (groups + kBlock - 1) / kBlock;
+    size_t want = 1024 / (col_blocks ? col_blocks : 1);   // ~4 workgroups per CU
+    size_t by_rows = (rows + 15) / 16;                    // at least 16 rows per chunk
     size_t c = want < by_rows ? want : by_rows;
-    if (c > 256) c = 256;
+    if (c > kDim0MaxChunks) c = kDim0MaxChunks;
     return c < 1 ? 1 : c;
 }
 
-// Pass 1: thread = one column, workgroup (x) = 256 columns, blockIdx.y = a
-// contiguous chunk of rows.  Coalesced: a wave reads 64 adjacent floats of
-// one row per step.
+template <bool VEC>
 __global__ __launch_bounds__(kBlock) void dim0_partial(const float *__restrict__ x, size_t rows,
                                                        size_t cols, size_t rows_per_chunk,
                                                        double *__restrict__ partial) {
-    const size_t c = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (c >= cols) return;
+    const size_t groups = VEC ? cols / 4 : cols;
+    const size_t gcol = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (gcol >= groups) return;
     const size_t r0 = static_cast<size_t>(blockIdx.y) * rows_per_chunk;
     size_t r1 = r0 + rows_per_chunk;
     if (r1 > rows) r1 = rows;
-    double acc = 0.0;
-    for (size_t r = r0; r < r1; ++r) acc += (double)x[r * cols + c];
-    partial[static_cast<size_t>(blockIdx.y) * cols + c] = acc;
+    double* out = partial + static_cast<size_t>(blockIdx.y) * cols;
+    if (VEC) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+        size_t r = r0;
+        for (; r + 4 <= r1; r += 4) {   // four independent loads in flight per thread
+            const float4 q0 = x4[(r + 0) * groups + gcol], q1 = x4[(r + 1) * groups + gcol];
+            const float4 q2 = x4[(r + 2) * groups + gcol], q3 = x4[(r + 3) * groups + gcol];
+            a0 += (double)q0.x; a1 += (double)q0.y; a2 += (double)q0.z; a3 += (double)q0.w;
+            a0 += (double)q1.x; a1 += (double)q1.y; a2 += (double)q1.z; a3 += (double)q1.w;
+            a0 += (double)q2.x; a1 += (double)q2.y; a2 += (double)q2.z; a3 += (double)q2.w;
+            a0 += (double)q3.x; a1 += (double)q3.y; a2 += (double)q3.z; a3 += (double)q3.w;
+        }
+        for (; r < r1; ++r) {
+            const float4 q = x4[r * groups + gcol];
+            a0 += (double)q.x; a1 += (double)q.y; a2 += (double)q.z; a3 += (double)q.w;
+        }
+        out[4 * gcol + 0] = a0;
+        out[4 * gcol + 1] = a1;
+        out[4 * gcol + 2] = a2;
+        out[4 * gcol + 3] = a3;
+    } else {
+        double acc = 0.0;
+        for (size_t r = r0; r < r1; ++r) acc += (double)x[r * cols + gcol];
+        out[gcol] = acc;
+    }
 }
 
-// Pass 2: thread = one column, adds the chunk partials in chunk order.
+// Pass 2: a workgroup owns 64 columns; its four waves each add a quarter of
+// the chunk partials (lane = column), then wave 0 adds the four wave sums in
+// order.
 __global__ __launch_bounds__(kBlock) void dim0_final(const double *__restrict__ partial,
                                                      size_t chunks, size_t cols,
                                                      float *__restrict__ out) {
-    const size_t c = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (c >= cols) return;
+    __shared__ double lds[kBlock / 64][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t c = static_cast<size_t>(blockIdx.x) * 64 + lane;
     double acc = 0.0;
-    for (size_t k = 0; k < chunks; ++k) acc += partial[k * cols + c];
-    out[c] = static_cast<float>(acc);
+    if (c < cols)
+        for (size_t k = wave; k < chunks; k += kBlock / 64) acc += partial[k * cols + c];
+    lds[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && c < cols) {
+        double s = 0.0;
+#pragma unroll
+        for (int w = 0; w < kBlock / 64; ++w) s += lds[w][lane];
+        out[c] = static_cast<float>(s);
+    }
 }
 
 }  // namespace tship
@@ -165,12 +203,15 @@ int ts_hip_sum_dim0(const float *x, size_t rows, size_t cols, float *out, float 
     const size_t rows_per_chunk = (rows + chunks - 1) / chunks;
     double *partial = reinterpret_cast<double *>(workspace);
     hipStream_t s = as_stream(stream);
-    unsigned gx = static_cast<unsigned>((cols + kBlock - 1) / kBlock);
-    hipLaunchKernelGGL(dim0_partial, dim3(gx, static_cast<unsigned>(chunks)), dim3(kBlock), 0, s,
-                       x, rows, cols, rows_per_chunk, partial);
+    const bool vec = (cols % 4 == 0) && aligned16(x);
+    const size_t groups = vec ? cols / 4 : cols;
+    dim3 grid1(static_cast<unsigned>((groups + kBlock - 1) / kBlock), static_cast<unsigned>(chunks));
+    if (vec) hipLaunchKernelGGL(dim0_partial<true>, grid1, dim3(kBlock), 0, s, x, rows, cols, rows_per_chunk, partial);
+    else hipLaunchKernelGGL(dim0_partial<false>, grid1, dim3(kBlock), 0, s, x, rows, cols, rows_per_chunk, partial);
     int st = launch_status();
     if (st) return st;
-    hipLaunchKernelGGL(dim0_final, dim3(gx), dim3(kBlock), 0, s, partial, chunks, cols, out);
+    hipLaunchKernelGGL(dim0_final, dim3(static_cast<unsigned>((cols + 63) / 64)), dim3(kBlock), 0, s,
+                       partial, chunks, cols, out);
     return launch_status();
 }
 
