@@ -207,6 +207,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
                 for (int b = 0; b < FN; ++b)
                     acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a], bf[b], acc[a][b], 0, 0, 0);
         }
+        // Scheduling hint: alternate one MFMA and one LDS read across the
+        // whole k-tile, so operand reads of later k-steps issue under the
+        // MFMAs of earlier ones instead of clustering ahead of them.
+#pragma unroll
+        for (int i = 0; i < kBK / 2 * FM * FN; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+        }
         __syncthreads();
     }
 
