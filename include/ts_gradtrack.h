@@ -32,6 +32,12 @@ ts_tensor *ts_tensor_zeros(const size_t *dims, size_t rank);
 ts_tensor *ts_tensor_ones(const size_t *dims, size_t rank);
 /* Tensor::from_slice (init/data.rs:227-247) */
 ts_tensor *ts_tensor_from_slice(const float *data, size_t len, const size_t *dims, size_t rank);
+/* Tensor::randn(dims, seed) / fill_randn (init/random.rs:231-299): values of
+ * the reference's XorShiftRng + Box-Muller, generated on the device.  With
+ * has_seed == 0 the seed comes from the clock, as XorShiftRng::new_from_time
+ * (random.rs:492-497) does. */
+ts_tensor *ts_tensor_randn(const size_t *dims, size_t rank, uint64_t seed, int has_seed);
+int ts_tensor_fill_randn(ts_tensor *t, uint64_t seed, int has_seed);
 /* Tensor::clone (core/mod.rs:344-378): new buffer, new id, no grad */
 ts_tensor *ts_tensor_clone(const ts_tensor *t);
 void ts_tensor_free(ts_tensor *t);

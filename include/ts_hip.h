@@ -114,6 +114,12 @@ int ts_hip_row_broadcast(int op, const float *x, const float *v, float *out, siz
                          unsigned long long *zero_index, void *stream);
 /* init/basic.rs:136-326 zeros/ones/fill: out[i] = value */
 int ts_hip_fill(float *out, float value, size_t n, void *stream);
+/* Tensor::randn / fill_randn with Some(seed) (init/random.rs:231-299,
+ * XorShiftRng :453-615): out[i] = Box-Muller of draws 2i+1 and 2i+2 of
+ * xorshift64(13,7,17) from `seed`, generated on the device.  ln and cos are
+ * correctly rounded (the reference takes them from the host libm's logf /
+ * cosf).  n == 0 is a no-op; n must not exceed 2^62. */
+int ts_hip_randn(float *out, size_t n, uint64_t seed, void *stream);
 /* Fill from a device scalar without a host round trip (the upstream gradient
  * of a scalar loss): out[i] = src[0] (grad_fn/reductions/sum.rs:4-16), or
  * multiplier * src[0] when use_multiplier (grad_fn/reductions/mean.rs:4-30). */

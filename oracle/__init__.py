@@ -62,6 +62,15 @@ def lib() -> ctypes.CDLL:
         L.o_adam_step.argtypes = [_F, _F, _F, _F, _F, _SZ, ctypes.c_float, ctypes.c_float,
                                   ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_uint64,
                                   ctypes.c_int]
+        L.o_randn.argtypes = [_F, _SZ, ctypes.c_uint64, ctypes.c_int]
+        L.o_xorshift_next.argtypes = [ctypes.c_uint64]
+        L.o_xorshift_next.restype = ctypes.c_uint64
+        L.o_xorshift_advance.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+        L.o_xorshift_advance.restype = ctypes.c_uint64
+        L.o_libm_cr_check.argtypes = [ctypes.c_int]
+        L.o_libm_cr_check.restype = ctypes.c_long
+        L.o_libm_glibc_diff.argtypes = [ctypes.c_int]
+        L.o_libm_glibc_diff.restype = ctypes.c_long
         _LIB = L
     return _LIB
 
@@ -261,3 +270,30 @@ def build() -> None:
     import subprocess
     subprocess.run(["make", "-B", "-C", str(_HERE)], check=True,
                    stdout=subprocess.DEVNULL if not os.environ.get("TS_VERBOSE") else None)
+
+
+def randn(n: int, seed: int, correctly_rounded: bool = False) -> np.ndarray:
+    """Tensor::randn(n, Some(seed)) values.  ``correctly_rounded`` evaluates ln
+    and cos in f64 and rounds once; otherwise the host libm's logf / cosf."""
+    out = np.empty(n, dtype=np.float32)
+    lib().o_randn(_p(out), n, ctypes.c_uint64(seed), int(correctly_rounded))
+    return out
+
+
+def xorshift_next(s: int) -> int:
+    return int(lib().o_xorshift_next(ctypes.c_uint64(s)))
+
+
+def xorshift_advance(s: int, k: int) -> int:
+    return int(lib().o_xorshift_advance(ctypes.c_uint64(s), ctypes.c_uint64(k)))
+
+
+def libm_cr_check(which: int) -> int:
+    """Inputs (of 2^23) where f64-rounded ln (0) / cos (1) disagrees with long double."""
+    return int(lib().o_libm_cr_check(which))
+
+
+def libm_glibc_diff(which: int) -> int:
+    """Inputs (of 2^23) where the host's logf (0) / cosf (1) differ from the
+    correctly rounded value."""
+    return int(lib().o_libm_glibc_diff(which))

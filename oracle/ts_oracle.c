@@ -26,8 +26,15 @@
  *   adam_step: torch.optim.Adam (float64) on the reference's own LibTorch
  *       validation cases incl. weight decay and AMSGrad (ltv/src/validation/optimizers/adam.rs:65-160) and
  *       on 100 random steps; closed form for constant gradients.
+ *   randn: xorshift64 against Marsaglia's published test vector (seed
+ *       88172645463325252 -> 8748534153485358512) and step-by-step advance;
+ *       seed 0 gives the closed-form constant sqrt(2 ln 2) * cos(pi) for
+ *       every element; mode 1 (f64 log / cos rounded once) is checked
+ *       correctly rounded on all 2^23 inputs against long double.
  *   parity unpinned: the exact bits of the bias-correction scalars depend on
- *       the host libm's f64 pow, as in the reference (adam/mod.rs:526-531).
+ *       the host libm's f64 pow, as in the reference (adam/mod.rs:526-531);
+ *       randn's mode 0 takes logf / cosf from the host libm as the reference
+ *       does, and glibc's are not correctly rounded on every input.
  */
 #include <math.h>
 #include <stddef.h>
@@ -289,4 +296,104 @@ EXPORT void o_adam_step(float *p, const float *g, float *m, float *v, float *vma
         float den = sqrtf(vh) + eps;
         p[i] = p[i] - (lr * mh) / den;
     }
+}
+
+/* ---- random initialisation -------------------------------------------------- */
+
+/* XorShiftRng::next_u64 (tensor/init/random.rs:524-529): Marsaglia's
+ * xorshift64 with the shift triple (13, 7, 17). */
+static uint64_t xs_next(uint64_t *s) {
+    uint64_t x = *s;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *s = x;
+    return x;
+}
+
+EXPORT uint64_t o_xorshift_next(uint64_t s) { return xs_next(&s); }
+
+/* State after k steps from s, one step at a time (the brute-force check of
+ * the device's jump-ahead). */
+EXPORT uint64_t o_xorshift_advance(uint64_t s, uint64_t k) {
+    while (k--) xs_next(&s);
+    return s;
+}
+
+/* next_f32 (random.rs:557-564): the low 23 bits of the draw become the
+ * mantissa of a float with biased exponent 126, a value in [0.5, 1). */
+static float xs_unit(uint64_t *s) {
+    uint32_t bits = (uint32_t)(xs_next(s) & 0x7FFFFFu) | (126u << 23);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* f32 natural log and cosine.  mode 0 calls the host libm's logf / cosf, as
+ * Rust's f32::ln / f32::cos do; mode 1 evaluates in f64 and rounds once,
+ * which is correctly rounded on every input next_normal can produce
+ * (checked against long double by o_libm_cr_check). */
+static float ln_f32(float x, int mode) { return mode ? (float)log((double)x) : logf(x); }
+static float cos_f32(float x, int mode) { return mode ? (float)cos((double)x) : cosf(x); }
+
+/* 2*PI in fp32: std::f32::consts::PI (0x40490FDB) doubled exactly. */
+static const float kTwoPiF = 6.28318548202514648438f;
+
+/* next_normal (random.rs:592-615): Box-Muller on two consecutive draws,
+ *   u1 = next_f32, u2 = next_f32, u1 clamped into (0, 1),
+ *   z  = sqrt(-2 * ln(u1)) * cos((2*PI) * u2)    all in fp32,
+ *   z  = 0 if NaN or infinite. */
+static float xs_normal(uint64_t *s, int mode) {
+    float u1 = xs_unit(s);
+    float u2 = xs_unit(s);
+    if (u1 <= 0.0f) u1 = 1e-7f;
+    else if (u1 >= 1.0f) u1 = 1.0f - 1e-7f;
+    float r = sqrtf(-2.0f * ln_f32(u1, mode));
+    float z = r * cos_f32(kTwoPiF * u2, mode);
+    return (isnan(z) || isinf(z)) ? 0.0f : z;
+}
+
+/* Tensor::randn / fill_randn (random.rs:231-299, XorShiftRng::new :473-475): element i takes draws
+ * 2i+1 and 2i+2 of XorShiftRng::new(seed), in order; both fill paths
+ * (fill_randn_simd_avx2 :340-362, fill_randn_scalar :401-419) draw
+ * sequentially, so the layout does not depend on the path taken. */
+EXPORT void o_randn(float *out, size_t n, uint64_t seed, int mode) {
+    uint64_t s = seed;
+    for (size_t i = 0; i < n; ++i) out[i] = xs_normal(&s, mode);
+}
+
+/* Exhaustive checks over the 2^23 values next_f32 can return.
+ * which = 0: ln(u); which = 1: cos((2*PI) * u).
+ * o_libm_cr_check counts inputs where the f64 evaluation rounded to f32
+ * disagrees with the long-double evaluation rounded to f32 (0 means mode 1
+ * is correctly rounded on the whole domain).  o_libm_glibc_diff counts
+ * inputs where the host's logf / cosf differ from mode 1. */
+static float unit_of(uint32_t m) {
+    uint32_t bits = m | (126u << 23);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+EXPORT long o_libm_cr_check(int which) {
+    long bad = 0;
+    for (uint32_t m = 0; m < (1u << 23); ++m) {
+        float u = unit_of(m);
+        float x = which ? kTwoPiF * u : u;
+        float a = which ? (float)cos((double)x) : (float)log((double)x);
+        float b = which ? (float)cosl((long double)x) : (float)logl((long double)x);
+        if (memcmp(&a, &b, 4) != 0) ++bad;
+    }
+    return bad;
+}
+
+EXPORT long o_libm_glibc_diff(int which) {
+    long diff = 0;
+    for (uint32_t m = 0; m < (1u << 23); ++m) {
+        float u = unit_of(m);
+        float a = which ? cos_f32(kTwoPiF * u, 0) : ln_f32(u, 0);
+        float b = which ? cos_f32(kTwoPiF * u, 1) : ln_f32(u, 1);
+        if (memcmp(&a, &b, 4) != 0) ++diff;
+    }
+    return diff;
 }

@@ -73,6 +73,7 @@ HIP_SIGNATURES = {
     "ts_hip_bias_add": (_c.c_int, [VP, VP, VP, SZ, SZ, _c.c_int, VP]),
     "ts_hip_row_broadcast": (_c.c_int, [_c.c_int, VP, VP, VP, SZ, SZ, _c.c_int, SZ, VP, VP]),
     "ts_hip_fill": (_c.c_int, [VP, _c.c_float, SZ, VP]),
+    "ts_hip_randn": (_c.c_int, [VP, SZ, _c.c_uint64, VP]),
     "ts_hip_fill_from_device": (_c.c_int, [VP, VP, _c.c_float, _c.c_int, SZ, VP]),
     "ts_hip_copy": (_c.c_int, [VP, VP, SZ, VP]),
     "ts_hip_relu_backward": (_c.c_int, [VP, VP, VP, SZ, VP]),
@@ -107,6 +108,8 @@ GRADTRACK_SIGNATURES = {
     "ts_tensor_zeros": (TP, [_c.POINTER(SZ), SZ]),
     "ts_tensor_ones": (TP, [_c.POINTER(SZ), SZ]),
     "ts_tensor_from_slice": (TP, [F, SZ, _c.POINTER(SZ), SZ]),
+    "ts_tensor_randn": (TP, [_c.POINTER(SZ), SZ, _c.c_uint64, _c.c_int]),
+    "ts_tensor_fill_randn": (_c.c_int, [TP, _c.c_uint64, _c.c_int]),
     "ts_tensor_clone": (TP, [TP]),
     "ts_tensor_free": (None, [TP]),
     "ts_tensor_id": (_c.c_uint64, [TP]),

@@ -89,6 +89,15 @@ ts_tensor *ts_tensor_from_slice(const float *data, size_t len, const size_t *dim
         return wrap(ts::Tensor::from_slice(data, len, dims_of(dims, rank)));
     });
 }
+ts_tensor *ts_tensor_randn(const size_t *dims, size_t rank, uint64_t seed, int has_seed) {
+    return guard_ptr([&] { return wrap(ts::Tensor::randn(dims_of(dims, rank), has_seed ? &seed : nullptr)); });
+}
+int ts_tensor_fill_randn(ts_tensor *t, uint64_t seed, int has_seed) {
+    return guard_int([&] {
+        if (!t) throw ts::Error("tensor handle is NULL");
+        t->t.fill_randn(has_seed ? &seed : nullptr);
+    });
+}
 ts_tensor *ts_tensor_clone(const ts_tensor *t) {
     return guard_ptr([&] { return wrap(T(t).clone()); });
 }

@@ -2,6 +2,7 @@
 // Each op launches one or two kernels of ts_hip.h on the library stream; no
 // op synchronises except data()/value().
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <sstream>
@@ -156,6 +157,32 @@ Tensor Tensor::filled(std::vector<size_t> dims, float v) {
 
 Tensor Tensor::zeros(std::vector<size_t> dims) { return filled(std::move(dims), 0.0f); }
 Tensor Tensor::ones(std::vector<size_t> dims) { return filled(std::move(dims), 1.0f); }
+
+// XorShiftRng::new_from_time (random.rs:492-497) hashes the system time; any
+// well-mixed 64-bit value of the clock serves (a splitmix64 finaliser of the
+// nanosecond count plus a per-process counter, so two calls in the same tick
+// still differ).
+static uint64_t seed_from_time() {
+    static std::atomic<uint64_t> calls{0};
+    uint64_t z = static_cast<uint64_t>(std::chrono::system_clock::now().time_since_epoch().count()) +
+                 0x9E3779B97F4A7C15ULL * (calls.fetch_add(1, std::memory_order_relaxed) + 1);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+void Tensor::fill_randn(const uint64_t *seed) {
+    if (!size_) return;  // random.rs:271-273
+    const uint64_t s = seed ? *seed : seed_from_time();
+    launch(KernelClass::Elementwise, 4.0 * size_, "ts_hip_randn",
+           [&] { return ts_hip_randn(dev_mut(), size_, s, S()); });
+}
+
+Tensor Tensor::randn(std::vector<size_t> dims, const uint64_t *seed) {
+    Tensor t = new_uninit(std::move(dims));
+    t.fill_randn(seed);
+    return t;
+}
 
 Tensor Tensor::from_slice(const float *data, size_t len, std::vector<size_t> dims) {
     const size_t n = product(dims);

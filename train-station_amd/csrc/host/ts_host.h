@@ -164,6 +164,11 @@ class Tensor {
     static Tensor ones(std::vector<size_t> dims);
     static Tensor filled(std::vector<size_t> dims, float v);
     static Tensor from_slice(const float *data, size_t len, std::vector<size_t> dims);
+    // Tensor::randn (init/random.rs:231-235): XorShiftRng values generated on
+    // the device; without a seed, one derived from the clock (random.rs:492-497)
+    static Tensor randn(std::vector<size_t> dims, const uint64_t *seed);
+    // fill_randn (random.rs:270-299), in place
+    void fill_randn(const uint64_t *seed);
 
     // Tensor::clone: new buffer with the same values, new id, no grad
     Tensor clone() const;

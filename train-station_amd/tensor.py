@@ -69,6 +69,16 @@ class Tensor:
         d, r = _dims(shape)
         return _wrap(_G.ts_tensor_from_slice(a.ctypes.data_as(F), a.size, d, r))
 
+    @staticmethod
+    def randn(shape: Sequence[int], seed: Optional[int] = None) -> "Tensor":
+        """Tensor::randn (init/random.rs:231-235), generated on the device."""
+        d, r = _dims(shape)
+        return _wrap(_G.ts_tensor_randn(d, r, 0 if seed is None else int(seed), seed is not None))
+
+    def fill_randn(self, seed: Optional[int] = None) -> None:
+        """fill_randn (random.rs:270-299), in place."""
+        _ok(_G.ts_tensor_fill_randn(self._h, 0 if seed is None else int(seed), seed is not None))
+
     def clone(self) -> "Tensor":
         return _wrap(_G.ts_tensor_clone(self._h))
 
