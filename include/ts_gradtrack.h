@@ -102,6 +102,50 @@ uint64_t ts_adam_step_count(const ts_adam *opt);
 /* copy a linked parameter's m or v (which 0 / 1) to the host */
 int ts_adam_state(const ts_adam *opt, const ts_tensor *param, int which, float *out, size_t len);
 
+/* ---- checkpoint / resume ------------------------------------------------------
+ * The reference's formats (serialization/binary "TS_B" v1 and JSON) through
+ * StructSerializable (serialization/core/traits.rs): to_binary / from_binary,
+ * to_json / from_json, save_* / load_* on a path.  Buffers returned through
+ * `data` are owned by the caller and released with ts_buffer_free; JSON text
+ * is NUL-terminated and *len excludes the NUL. */
+void ts_buffer_free(void *data);
+/* Tensor (tensor/core/serialization.rs:179-288): data, shape, device,
+ * requires_grad.  Loaded tensors are placed on the device. */
+int ts_tensor_to_binary(const ts_tensor *t, uint8_t **data, size_t *len);
+ts_tensor *ts_tensor_from_binary(const uint8_t *data, size_t len);
+int ts_tensor_to_json(const ts_tensor *t, char **json, size_t *len);
+ts_tensor *ts_tensor_from_json(const char *json, size_t len);
+int ts_tensor_save_binary(const ts_tensor *t, const char *path);
+int ts_tensor_save_json(const ts_tensor *t, const char *path);
+ts_tensor *ts_tensor_load_binary(const char *path);
+ts_tensor *ts_tensor_load_json(const char *path);
+/* Adam (optimizers/adam/serialization.rs:140-235): config, per-parameter
+ * m / v / v_hat_max / step, step_count, insertion_order.  A loaded optimizer
+ * keeps the saved states under the saved parameter ids; relink them onto the
+ * live parameters, in insertion order, with ts_adam_relink_parameters
+ * (adam/mod.rs:396-454) before stepping. */
+int ts_adam_to_binary(const ts_adam *opt, uint8_t **data, size_t *len);
+ts_adam *ts_adam_from_binary(const uint8_t *data, size_t len);
+int ts_adam_to_json(const ts_adam *opt, char **json, size_t *len);
+ts_adam *ts_adam_from_json(const char *json, size_t len);
+int ts_adam_save_binary(const ts_adam *opt, const char *path);
+int ts_adam_save_json(const ts_adam *opt, const char *path);
+ts_adam *ts_adam_load_binary(const char *path);
+ts_adam *ts_adam_load_json(const char *path);
+int ts_adam_relink_parameters(ts_adam *opt, const ts_tensor *const *params, size_t count);
+/* Adam::saved_parameter_count (adam/serialization.rs:226-228) */
+size_t ts_adam_saved_parameter_count(const ts_adam *opt);
+/* ParameterState::step of a linked parameter (0 if not linked) */
+uint64_t ts_adam_parameter_step(const ts_adam *opt, const ts_tensor *param);
+/* the optimizer's AdamConfig (learning_rate, beta1, beta2, eps, weight_decay)
+ * and amsgrad flag */
+int ts_adam_config(const ts_adam *opt, float *values5, int *amsgrad);
+/* AdamConfig on its own (adam/serialization.rs:40-62) */
+int ts_adam_config_to_binary(const float *values5, int amsgrad, uint8_t **data, size_t *len);
+int ts_adam_config_from_binary(const uint8_t *data, size_t len, float *values5, int *amsgrad);
+int ts_adam_config_to_json(const float *values5, int amsgrad, char **json, size_t *len);
+int ts_adam_config_from_json(const char *json, size_t len, float *values5, int *amsgrad);
+
 /* runtime: wait for queued work (reports a recorded division by zero) */
 int ts_synchronize(void);
 /* library stream (for timing events on the stream the kernels run on) */

@@ -54,6 +54,8 @@ int ts_hip_memcpy(float *dst, const float *src, size_t n_floats, int kind);
 /* hipMemcpyAsync wrapper (no counterpart in the stub; required by the
  * device Allocation of tensor/core/allocation.rs:43-187) */
 int ts_hip_memcpy_async(float *dst, const float *src, size_t n_floats, int kind, void *stream);
+/* the same for a byte count (checkpoint records are 5 bytes per element) */
+int ts_hip_memcpy_bytes(void *dst, const void *src, size_t bytes, int kind, void *stream);
 /* pinned host memory for asynchronous device->host copies */
 int ts_hip_host_malloc(void **ptr, size_t bytes);
 int ts_hip_host_free(void *ptr);
@@ -120,6 +122,19 @@ int ts_hip_fill(float *out, float value, size_t n, void *stream);
  * correctly rounded (the reference takes them from the host libm's logf /
  * cosf).  n == 0 is a no-op; n must not exceed 2^62. */
 int ts_hip_randn(float *out, size_t n, uint64_t seed, void *stream);
+
+/* Checkpoint encoding of a Tensor's data as the reference's binary format
+ * stores a Vec<f32> (serialization/core/impls.rs:278-288 makes it an Array
+ * of F32 values; binary/structs.rs:193-196 writes each as the type tag 10 and
+ * the f32 bits little-endian): dst receives 5*n bytes, record i =
+ * [10][bits of src[i], LE].  src 16-byte aligned, dst 4-byte aligned. */
+int ts_hip_encode_f32_records(const float *src, size_t n, void *dst, void *stream);
+/* The inverse (binary/structs.rs:395-398 reads tag 10 + f32).  When
+ * bad_index is not NULL, the index of the first record whose tag is not 10 is
+ * folded into *bad_index with a minimum (the caller sets it to ~0 first).
+ * src 4-byte aligned, dst 16-byte aligned. */
+int ts_hip_decode_f32_records(const void *src, size_t n, float *dst, unsigned long long *bad_index,
+                              void *stream);
 /* Fill from a device scalar without a host round trip (the upstream gradient
  * of a scalar loss): out[i] = src[0] (grad_fn/reductions/sum.rs:4-16), or
  * multiplier * src[0] when use_multiplier (grad_fn/reductions/mean.rs:4-30). */

@@ -46,6 +46,7 @@ HIP_SIGNATURES = {
     "ts_hip_free": (_c.c_int, [F]),
     "ts_hip_memcpy": (_c.c_int, [VP, VP, SZ, _c.c_int]),
     "ts_hip_memcpy_async": (_c.c_int, [VP, VP, SZ, _c.c_int, VP]),
+    "ts_hip_memcpy_bytes": (_c.c_int, [VP, VP, SZ, _c.c_int, VP]),
     "ts_hip_host_malloc": (_c.c_int, [_c.POINTER(VP), SZ]),
     "ts_hip_host_free": (_c.c_int, [VP]),
     "ts_hip_stream_create": (_c.c_int, [_c.POINTER(VP)]),
@@ -74,6 +75,8 @@ HIP_SIGNATURES = {
     "ts_hip_row_broadcast": (_c.c_int, [_c.c_int, VP, VP, VP, SZ, SZ, _c.c_int, SZ, VP, VP]),
     "ts_hip_fill": (_c.c_int, [VP, _c.c_float, SZ, VP]),
     "ts_hip_randn": (_c.c_int, [VP, SZ, _c.c_uint64, VP]),
+    "ts_hip_encode_f32_records": (_c.c_int, [VP, SZ, VP, VP]),
+    "ts_hip_decode_f32_records": (_c.c_int, [VP, SZ, VP, VP, VP]),
     "ts_hip_fill_from_device": (_c.c_int, [VP, VP, _c.c_float, _c.c_int, SZ, VP]),
     "ts_hip_copy": (_c.c_int, [VP, VP, SZ, VP]),
     "ts_hip_relu_backward": (_c.c_int, [VP, VP, VP, SZ, VP]),
@@ -154,6 +157,31 @@ GRADTRACK_SIGNATURES = {
     "ts_adam_set_learning_rate": (None, [TP, _c.c_float]),
     "ts_adam_step_count": (_c.c_uint64, [TP]),
     "ts_adam_state": (_c.c_int, [TP, TP, _c.c_int, F, SZ]),
+    "ts_buffer_free": (None, [VP]),
+    "ts_tensor_to_binary": (_c.c_int, [TP, _c.POINTER(VP), _c.POINTER(SZ)]),
+    "ts_tensor_from_binary": (TP, [VP, SZ]),
+    "ts_tensor_to_json": (_c.c_int, [TP, _c.POINTER(VP), _c.POINTER(SZ)]),
+    "ts_tensor_from_json": (TP, [_c.c_char_p, SZ]),
+    "ts_tensor_save_binary": (_c.c_int, [TP, _c.c_char_p]),
+    "ts_tensor_save_json": (_c.c_int, [TP, _c.c_char_p]),
+    "ts_tensor_load_binary": (TP, [_c.c_char_p]),
+    "ts_tensor_load_json": (TP, [_c.c_char_p]),
+    "ts_adam_to_binary": (_c.c_int, [TP, _c.POINTER(VP), _c.POINTER(SZ)]),
+    "ts_adam_from_binary": (TP, [VP, SZ]),
+    "ts_adam_to_json": (_c.c_int, [TP, _c.POINTER(VP), _c.POINTER(SZ)]),
+    "ts_adam_from_json": (TP, [_c.c_char_p, SZ]),
+    "ts_adam_save_binary": (_c.c_int, [TP, _c.c_char_p]),
+    "ts_adam_save_json": (_c.c_int, [TP, _c.c_char_p]),
+    "ts_adam_load_binary": (TP, [_c.c_char_p]),
+    "ts_adam_load_json": (TP, [_c.c_char_p]),
+    "ts_adam_relink_parameters": (_c.c_int, [TP, _c.POINTER(TP), SZ]),
+    "ts_adam_saved_parameter_count": (SZ, [TP]),
+    "ts_adam_parameter_step": (_c.c_uint64, [TP, TP]),
+    "ts_adam_config": (_c.c_int, [TP, F, _c.POINTER(_c.c_int)]),
+    "ts_adam_config_to_binary": (_c.c_int, [F, _c.c_int, _c.POINTER(VP), _c.POINTER(SZ)]),
+    "ts_adam_config_from_binary": (_c.c_int, [VP, SZ, F, _c.POINTER(_c.c_int)]),
+    "ts_adam_config_to_json": (_c.c_int, [F, _c.c_int, _c.POINTER(VP), _c.POINTER(SZ)]),
+    "ts_adam_config_from_json": (_c.c_int, [_c.c_char_p, SZ, F, _c.POINTER(_c.c_int)]),
     "ts_synchronize": (_c.c_int, []),
     "ts_stream": (VP, []),
     "ts_pool_live_bytes": (SZ, []),

@@ -26,6 +26,7 @@ void Adam::add_parameter(const Tensor &p) {
     if (states_.count(p.id())) return;
     State s;
     s.n = p.size();
+    s.dims = p.dims();
     if (s.n) {
         s.m = std::make_shared<Allocation>(s.n);
         s.v = std::make_shared<Allocation>(s.n);
@@ -96,6 +97,11 @@ void Adam::step(const std::vector<Tensor *> &params) {
 void Adam::zero_grad(const std::vector<Tensor *> &params) {
     for (Tensor *p : params) p->zero_grad();
     clear_gradients();
+}
+
+uint64_t Adam::parameter_step(size_t id) const {
+    auto it = states_.find(id);
+    return it == states_.end() ? 0 : it->second.step;
 }
 
 const float *Adam::state_m(size_t id) const {

@@ -1,4 +1,5 @@
 // C handle API (include/ts_gradtrack.h) over the C++ host classes.
+#include <cstdlib>
 #include <cstring>
 #include <exception>
 #include <string>
@@ -261,6 +262,165 @@ int ts_adam_state(const ts_adam *opt, const ts_tensor *param, int which, float *
                   "ts_hip_memcpy_async");
         ts::Runtime::get().sync();
     });
+}
+
+// ---- checkpoint / resume ------------------------------------------------------------
+
+void ts_buffer_free(void *data) { std::free(data); }
+
+}  // extern "C"
+
+namespace {
+
+template <class Bytes>
+void give_bytes(const Bytes &b, uint8_t **data, size_t *len) {
+    if (!data || !len) throw ts::Error("output pointer is NULL");
+    void *p = std::malloc(b.size() ? b.size() : 1);
+    if (!p) throw ts::Error("out of host memory");
+    if (b.size()) std::memcpy(p, b.data(), b.size());
+    *data = static_cast<uint8_t *>(p);
+    *len = b.size();
+}
+
+void give_text(const std::string &s, char **out, size_t *len) {
+    if (!out || !len) throw ts::Error("output pointer is NULL");
+    char *p = static_cast<char *>(std::malloc(s.size() + 1));
+    if (!p) throw ts::Error("out of host memory");
+    std::memcpy(p, s.data(), s.size());
+    p[s.size()] = '\0';
+    *out = p;
+    *len = s.size();
+}
+
+std::string text_of(const char *json, size_t len) {
+    if (len && !json) throw ts::Error("JSON pointer is NULL");
+    return std::string(json ? json : "", len);
+}
+
+const char *path_of(const char *path) {
+    if (!path) throw ts::Error("path is NULL");
+    return path;
+}
+
+ts::Adam &A(ts_adam *h) {
+    if (!h) throw ts::Error("optimizer handle is NULL");
+    return h->a;
+}
+const ts::Adam &A(const ts_adam *h) {
+    if (!h) throw ts::Error("optimizer handle is NULL");
+    return h->a;
+}
+
+ts::AdamConfig config_of(const float *v, int amsgrad) {
+    if (!v) throw ts::Error("config values pointer is NULL");
+    ts::AdamConfig c;
+    c.learning_rate = v[0];
+    c.beta1 = v[1];
+    c.beta2 = v[2];
+    c.eps = v[3];
+    c.weight_decay = v[4];
+    c.amsgrad = amsgrad != 0;
+    return c;
+}
+
+void put_config(const ts::AdamConfig &c, float *v, int *amsgrad) {
+    if (!v || !amsgrad) throw ts::Error("output pointer is NULL");
+    v[0] = c.learning_rate;
+    v[1] = c.beta1;
+    v[2] = c.beta2;
+    v[3] = c.eps;
+    v[4] = c.weight_decay;
+    *amsgrad = c.amsgrad ? 1 : 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ts_tensor_to_binary(const ts_tensor *t, uint8_t **data, size_t *len) {
+    return guard_int([&] { give_bytes(T(t).to_binary(), data, len); });
+}
+ts_tensor *ts_tensor_from_binary(const uint8_t *data, size_t len) {
+    return guard_ptr([&] {
+        if (len && !data) throw ts::Error("data pointer is NULL");
+        return wrap(ts::Tensor::from_binary(data, len));
+    });
+}
+int ts_tensor_to_json(const ts_tensor *t, char **json, size_t *len) {
+    return guard_int([&] { give_text(T(t).to_json(), json, len); });
+}
+ts_tensor *ts_tensor_from_json(const char *json, size_t len) {
+    return guard_ptr([&] { return wrap(ts::Tensor::from_json(text_of(json, len))); });
+}
+int ts_tensor_save_binary(const ts_tensor *t, const char *path) {
+    return guard_int([&] { T(t).save_binary(path_of(path)); });
+}
+int ts_tensor_save_json(const ts_tensor *t, const char *path) {
+    return guard_int([&] { T(t).save_json(path_of(path)); });
+}
+ts_tensor *ts_tensor_load_binary(const char *path) {
+    return guard_ptr([&] { return wrap(ts::Tensor::load_binary(path_of(path))); });
+}
+ts_tensor *ts_tensor_load_json(const char *path) {
+    return guard_ptr([&] { return wrap(ts::Tensor::load_json(path_of(path))); });
+}
+
+int ts_adam_to_binary(const ts_adam *opt, uint8_t **data, size_t *len) {
+    return guard_int([&] { give_bytes(A(opt).to_binary(), data, len); });
+}
+ts_adam *ts_adam_from_binary(const uint8_t *data, size_t len) {
+    return guard_ptr([&] {
+        if (len && !data) throw ts::Error("data pointer is NULL");
+        return new ts_adam{ts::Adam::from_binary(data, len)};
+    });
+}
+int ts_adam_to_json(const ts_adam *opt, char **json, size_t *len) {
+    return guard_int([&] { give_text(A(opt).to_json(), json, len); });
+}
+ts_adam *ts_adam_from_json(const char *json, size_t len) {
+    return guard_ptr([&] { return new ts_adam{ts::Adam::from_json(text_of(json, len))}; });
+}
+int ts_adam_save_binary(const ts_adam *opt, const char *path) {
+    return guard_int([&] { A(opt).save_binary(path_of(path)); });
+}
+int ts_adam_save_json(const ts_adam *opt, const char *path) {
+    return guard_int([&] { A(opt).save_json(path_of(path)); });
+}
+ts_adam *ts_adam_load_binary(const char *path) {
+    return guard_ptr([&] { return new ts_adam{ts::Adam::load_binary(path_of(path))}; });
+}
+ts_adam *ts_adam_load_json(const char *path) {
+    return guard_ptr([&] { return new ts_adam{ts::Adam::load_json(path_of(path))}; });
+}
+int ts_adam_relink_parameters(ts_adam *opt, const ts_tensor *const *params, size_t count) {
+    return guard_int([&] {
+        if (count && !params) throw ts::Error("parameter list is NULL");
+        std::vector<const ts::Tensor *> ps;
+        for (size_t i = 0; i < count; ++i) ps.push_back(&T(params[i]));
+        A(opt).relink_parameters(ps);
+    });
+}
+size_t ts_adam_saved_parameter_count(const ts_adam *opt) { return opt ? opt->a.saved_parameter_count() : 0; }
+uint64_t ts_adam_parameter_step(const ts_adam *opt, const ts_tensor *param) {
+    return (opt && param) ? opt->a.parameter_step(param->t.id()) : 0;
+}
+int ts_adam_config(const ts_adam *opt, float *values5, int *amsgrad) {
+    return guard_int([&] { put_config(A(opt).config(), values5, amsgrad); });
+}
+int ts_adam_config_to_binary(const float *values5, int amsgrad, uint8_t **data, size_t *len) {
+    return guard_int([&] { give_bytes(ts::adam_config_to_binary(config_of(values5, amsgrad)), data, len); });
+}
+int ts_adam_config_from_binary(const uint8_t *data, size_t len, float *values5, int *amsgrad) {
+    return guard_int([&] {
+        if (len && !data) throw ts::Error("data pointer is NULL");
+        put_config(ts::adam_config_from_binary(data, len), values5, amsgrad);
+    });
+}
+int ts_adam_config_to_json(const float *values5, int amsgrad, char **json, size_t *len) {
+    return guard_int([&] { give_text(ts::adam_config_to_json(config_of(values5, amsgrad)), json, len); });
+}
+int ts_adam_config_from_json(const char *json, size_t len, float *values5, int *amsgrad) {
+    return guard_int([&] { put_config(ts::adam_config_from_json(text_of(json, len)), values5, amsgrad); });
 }
 
 int ts_synchronize(void) {

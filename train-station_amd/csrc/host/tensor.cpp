@@ -12,10 +12,6 @@
 
 namespace ts {
 
-namespace {
-
-void *S() { return Runtime::get().stream(); }
-
 std::string dims_str(const std::vector<size_t> &d) {
     std::ostringstream os;
     os << "[";
@@ -23,6 +19,10 @@ std::string dims_str(const std::vector<size_t> &d) {
     os << "]";
     return os.str();
 }
+
+namespace {
+
+void *S() { return Runtime::get().stream(); }
 
 size_t product(const std::vector<size_t> &d) {
     size_t n = 1;

@@ -25,6 +25,8 @@
 #include <unordered_map>
 #include <vector>
 
+#include "ts_serial.h"
+
 namespace ts {
 
 struct Error : std::runtime_error {
@@ -170,6 +172,17 @@ class Tensor {
     // fill_randn (random.rs:270-299), in place
     void fill_randn(const uint64_t *seed);
 
+    // Checkpoint in the reference's formats (StructSerializable for Tensor,
+    // tensor/core/serialization.rs:179-288; serialization/core/traits.rs)
+    std::vector<uint8_t> to_binary() const;
+    static Tensor from_binary(const uint8_t *data, size_t len);
+    std::string to_json() const;
+    static Tensor from_json(const std::string &json);
+    void save_binary(const std::string &path) const;
+    void save_json(const std::string &path) const;
+    static Tensor load_binary(const std::string &path);
+    static Tensor load_json(const std::string &path);
+
     // Tensor::clone: new buffer with the same values, new id, no grad
     Tensor clone() const;
     // Handle on the same buffer with a new id (graph-internal sharing).
@@ -179,6 +192,7 @@ class Tensor {
     const std::vector<size_t> &dims() const { return dims_; }
     size_t size() const { return size_; }
     const float *dev() const { return alloc_ ? alloc_->ptr : nullptr; }
+    const std::shared_ptr<Allocation> &allocation() const { return alloc_; }
     float *dev_mut() { return alloc_ ? alloc_->ptr : nullptr; }
     SavedTensor saved() const { return SavedTensor{alloc_, dims_}; }
     static Tensor from_saved(const SavedTensor &s);
@@ -252,6 +266,15 @@ struct AdamConfig {
     bool amsgrad = false;
 };
 
+// AdamConfig on its own (StructSerializable, adam/serialization.rs:40-62)
+std::vector<uint8_t> adam_config_to_binary(const struct AdamConfig &c);
+std::string adam_config_to_json(const struct AdamConfig &c);
+struct AdamConfig adam_config_from_binary(const uint8_t *data, size_t len);
+struct AdamConfig adam_config_from_json(const std::string &json);
+
+// Rust's Debug form of a shape, "[2, 3]"
+std::string dims_str(const std::vector<size_t> &d);
+
 class Adam {
   public:
     Adam() = default;
@@ -272,12 +295,32 @@ class Adam {
     const float *state_m(size_t param_id) const;
     const float *state_v(size_t param_id) const;
 
+    // Checkpoint (optimizers/adam/serialization.rs:140-235).  A loaded
+    // optimizer holds the saved states under the saved parameter ids until
+    // relink_parameters maps them, by insertion position, onto live tensors
+    // (adam/mod.rs:396-454).
+    std::vector<uint8_t> to_binary() const;
+    static Adam from_binary(const uint8_t *data, size_t len);
+    std::string to_json() const;
+    static Adam from_json(const std::string &json);
+    void save_binary(const std::string &path) const;
+    void save_json(const std::string &path) const;
+    static Adam load_binary(const std::string &path);
+    static Adam load_json(const std::string &path);
+    void relink_parameters(const std::vector<const Tensor *> &params);
+    size_t saved_parameter_count() const { return states_.size(); }
+    // per-parameter step counter (ParameterState::step), 0 if not linked
+    uint64_t parameter_step(size_t param_id) const;
+
   private:
     struct State {
         std::shared_ptr<Allocation> m, v, v_hat_max;
+        std::vector<size_t> dims;
         size_t n = 0;
         uint64_t step = 0;
     };
+    ser::Fields to_fields(bool binary) const;
+    static Adam from_fields(const ser::Fields &f);
     AdamConfig config_;
     std::unordered_map<size_t, State> states_;
     std::vector<size_t> insertion_order_;

@@ -105,6 +105,14 @@ int ts_hip_memcpy_async(float *dst, const float *src, size_t n_floats, int kind,
         hipMemcpyAsync(dst, src, n_floats * sizeof(float), k, as_stream(stream)));
 }
 
+int ts_hip_memcpy_bytes(void *dst, const void *src, size_t bytes, int kind, void *stream) {
+    bool ok;
+    hipMemcpyKind k = copy_kind(kind, &ok);
+    if (!ok || (bytes && (!dst || !src))) return TS_HIP_EINVAL;
+    if (bytes == 0) return TS_HIP_OK;
+    return static_cast<int>(hipMemcpyAsync(dst, src, bytes, k, as_stream(stream)));
+}
+
 int ts_hip_host_malloc(void **ptr, size_t bytes) {
     if (!ptr) return TS_HIP_EINVAL;
     *ptr = nullptr;

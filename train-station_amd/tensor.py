@@ -33,6 +33,20 @@ def _ok(status: int) -> None:
         raise TsError(last_error())
 
 
+def _take_bytes(call) -> bytes:
+    """Run a native call that returns a malloc'd buffer through (data, len)."""
+    data, n = ctypes.c_void_p(), ctypes.c_size_t()
+    _ok(call(ctypes.byref(data), ctypes.byref(n)))
+    try:
+        return ctypes.string_at(data, n.value)
+    finally:
+        _G.ts_buffer_free(data)
+
+
+def _path(path) -> bytes:
+    return str(path).encode()
+
+
 class Tensor:
     """Handle on a device tensor owned by the native host library."""
 
@@ -183,6 +197,37 @@ class Tensor:
     def __repr__(self) -> str:
         return f"Tensor(id={self.id()}, shape={list(self.shape)}, requires_grad={self.requires_grad()})"
 
+    # -- checkpoint (tensor/core/serialization.rs, serialization/core/traits.rs) ----
+    def to_binary(self) -> bytes:
+        return _take_bytes(lambda d, n: _G.ts_tensor_to_binary(self._h, d, n))
+
+    @staticmethod
+    def from_binary(data: bytes) -> "Tensor":
+        buf = ctypes.create_string_buffer(bytes(data), len(data))
+        return _wrap(_G.ts_tensor_from_binary(buf, len(data)))
+
+    def to_json(self) -> str:
+        return _take_bytes(lambda d, n: _G.ts_tensor_to_json(self._h, d, n)).decode()
+
+    @staticmethod
+    def from_json(text: str) -> "Tensor":
+        b = text.encode()
+        return _wrap(_G.ts_tensor_from_json(b, len(b)))
+
+    def save_binary(self, path) -> None:
+        _ok(_G.ts_tensor_save_binary(self._h, _path(path)))
+
+    def save_json(self, path) -> None:
+        _ok(_G.ts_tensor_save_json(self._h, _path(path)))
+
+    @staticmethod
+    def load_binary(path) -> "Tensor":
+        return _wrap(_G.ts_tensor_load_binary(_path(path)))
+
+    @staticmethod
+    def load_json(path) -> "Tensor":
+        return _wrap(_G.ts_tensor_load_json(_path(path)))
+
 
 def _handles(params: Iterable[Tensor]):
     ps = list(params)
@@ -250,6 +295,95 @@ class Adam:
         out = np.empty(p.size(), dtype=np.float32)
         _ok(_G.ts_adam_state(self._h, p._h, {"m": 0, "v": 1}[which], out.ctypes.data_as(F), out.size))
         return out
+
+    def config(self) -> dict:
+        v = (ctypes.c_float * 5)()
+        a = ctypes.c_int()
+        _ok(_G.ts_adam_config(self._h, v, ctypes.byref(a)))
+        return dict(learning_rate=v[0], beta1=v[1], beta2=v[2], eps=v[3], weight_decay=v[4],
+                    amsgrad=bool(a.value))
+
+    def parameter_step(self, p: Tensor) -> int:
+        return int(_G.ts_adam_parameter_step(self._h, p._h))
+
+    # -- checkpoint (optimizers/adam/serialization.rs) --------------------------------
+    def to_binary(self) -> bytes:
+        return _take_bytes(lambda d, n: _G.ts_adam_to_binary(self._h, d, n))
+
+    @staticmethod
+    def from_binary(data: bytes) -> "Adam":
+        buf = ctypes.create_string_buffer(bytes(data), len(data))
+        h = _G.ts_adam_from_binary(buf, len(data))
+        if not h:
+            raise TsError(last_error())
+        return Adam(h)
+
+    def to_json(self) -> str:
+        return _take_bytes(lambda d, n: _G.ts_adam_to_json(self._h, d, n)).decode()
+
+    @staticmethod
+    def from_json(text: str) -> "Adam":
+        b = text.encode()
+        h = _G.ts_adam_from_json(b, len(b))
+        if not h:
+            raise TsError(last_error())
+        return Adam(h)
+
+    def save_binary(self, path) -> None:
+        _ok(_G.ts_adam_save_binary(self._h, _path(path)))
+
+    def save_json(self, path) -> None:
+        _ok(_G.ts_adam_save_json(self._h, _path(path)))
+
+    @staticmethod
+    def load_binary(path) -> "Adam":
+        h = _G.ts_adam_load_binary(_path(path))
+        if not h:
+            raise TsError(last_error())
+        return Adam(h)
+
+    @staticmethod
+    def load_json(path) -> "Adam":
+        h = _G.ts_adam_load_json(_path(path))
+        if not h:
+            raise TsError(last_error())
+        return Adam(h)
+
+    def relink_parameters(self, params: Iterable[Tensor]) -> None:
+        """adam/mod.rs:396-454: map saved states onto live parameters by position."""
+        arr, n = _handles(params)
+        _ok(_G.ts_adam_relink_parameters(self._h, arr, n))
+
+    def saved_parameter_count(self) -> int:
+        return int(_G.ts_adam_saved_parameter_count(self._h))
+
+
+def adam_config_to_binary(config: dict) -> bytes:
+    """AdamConfig::to_binary (adam/serialization.rs:40-62)."""
+    v = (ctypes.c_float * 5)(*[config[k] for k in _CONFIG_KEYS])
+    return _take_bytes(lambda d, n: _G.ts_adam_config_to_binary(v, int(bool(config["amsgrad"])), d, n))
+
+
+def adam_config_to_json(config: dict) -> str:
+    v = (ctypes.c_float * 5)(*[config[k] for k in _CONFIG_KEYS])
+    return _take_bytes(lambda d, n: _G.ts_adam_config_to_json(v, int(bool(config["amsgrad"])), d, n)).decode()
+
+
+def adam_config_from_binary(data: bytes) -> dict:
+    v, a = (ctypes.c_float * 5)(), ctypes.c_int()
+    buf = ctypes.create_string_buffer(bytes(data), len(data))
+    _ok(_G.ts_adam_config_from_binary(buf, len(data), v, ctypes.byref(a)))
+    return dict(zip(_CONFIG_KEYS, list(v)), amsgrad=bool(a.value))
+
+
+def adam_config_from_json(text: str) -> dict:
+    v, a = (ctypes.c_float * 5)(), ctypes.c_int()
+    b = text.encode()
+    _ok(_G.ts_adam_config_from_json(b, len(b), v, ctypes.byref(a)))
+    return dict(zip(_CONFIG_KEYS, list(v)), amsgrad=bool(a.value))
+
+
+_CONFIG_KEYS = ("learning_rate", "beta1", "beta2", "eps", "weight_decay")
 
 
 class NoGradTrack:
