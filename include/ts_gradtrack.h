@@ -54,7 +54,8 @@ int ts_tensor_set_requires_grad(ts_tensor *t, int requires_grad);
 int ts_tensor_requires_grad(const ts_tensor *t);
 
 /* recorded ops (tensor/ops/{add,sub,mul,div,relu,pow}.rs, ops/matmul/mod.rs,
- * tensor/reductions/{sum,mean}.rs) */
+ * tensor/reductions/{sum,mean}.rs).  The binary ops broadcast NumPy-style
+ * (ops/broadcasting.rs:299-478), up to rank 8. */
 ts_tensor *ts_tensor_add_tensor(const ts_tensor *a, const ts_tensor *b);
 ts_tensor *ts_tensor_sub_tensor(const ts_tensor *a, const ts_tensor *b);
 ts_tensor *ts_tensor_mul_tensor(const ts_tensor *a, const ts_tensor *b);
@@ -68,6 +69,19 @@ ts_tensor *ts_tensor_pow_scalar(const ts_tensor *a, float exponent);
 ts_tensor *ts_tensor_matmul(const ts_tensor *a, const ts_tensor *b);
 ts_tensor *ts_tensor_sum(const ts_tensor *a);
 ts_tensor *ts_tensor_mean(const ts_tensor *a);
+/* tensor/ops/{exp,log,sqrt,tanh,sigmoid,leaky_relu,softmax}.rs; exp / log /
+ * tanh (and sigmoid's exp) are correctly rounded where the reference uses the
+ * host libm */
+ts_tensor *ts_tensor_exp(const ts_tensor *a);
+ts_tensor *ts_tensor_log(const ts_tensor *a);
+ts_tensor *ts_tensor_sqrt(const ts_tensor *a);
+ts_tensor *ts_tensor_tanh(const ts_tensor *a);
+ts_tensor *ts_tensor_sigmoid(const ts_tensor *a);
+ts_tensor *ts_tensor_leaky_relu(const ts_tensor *a, float negative_slope);
+ts_tensor *ts_tensor_softmax(const ts_tensor *a, size_t dim);
+/* sum_dims / mean_dims (reductions/sum.rs:225-306, mean.rs:186-230) */
+ts_tensor *ts_tensor_sum_dims(const ts_tensor *a, const size_t *dims, size_t ndims, int keepdim);
+ts_tensor *ts_tensor_mean_dims(const ts_tensor *a, const size_t *dims, size_t ndims, int keepdim);
 
 /* Tensor::backward(Option<Tensor>) (utils.rs:634-636); grad_output may be NULL */
 int ts_tensor_backward(ts_tensor *t, const ts_tensor *grad_output);

@@ -143,6 +143,42 @@ int ts_hip_fill_from_device(float *out, const float *src, float multiplier, int 
 /* Tensor::clone for contiguous data (core/mod.rs:344-355) */
 int ts_hip_copy(const float *src, float *dst, size_t n, void *stream);
 
+/* ---- other recorded ops (tensor/ops/{exp,log,sqrt,tanh,sigmoid,leaky_relu,
+ * softmax}.rs) ------------------------------------------------------------- */
+
+/* out = exp(x), ln(x), tanh(x): correctly rounded (the reference calls the
+ * host libm's expf / logf / tanhf, which agree except in the last place on a
+ * small share of inputs) */
+int ts_hip_exp(const float *x, float *out, size_t n, void *stream);
+int ts_hip_log(const float *x, float *out, size_t n, void *stream);
+int ts_hip_tanh(const float *x, float *out, size_t n, void *stream);
+/* out = sqrt(x), correctly rounded as in the reference (bit-exact) */
+int ts_hip_sqrt(const float *x, float *out, size_t n, void *stream);
+/* sigmoid.rs:9-21: x >= 0 ? 1 / (1 + exp(-x)) : exp(x) / (1 + exp(x)) */
+int ts_hip_sigmoid(const float *x, float *out, size_t n, void *stream);
+/* leaky_relu.rs: x > 0 ? x : negative_slope * x (bit-exact) */
+int ts_hip_leaky_relu(const float *x, float negative_slope, float *out, size_t n, void *stream);
+/* softmax along an axis of a tensor viewed as [outer, reduce, inner]
+ * (softmax.rs:4-60): per slice max, exp(x - max), sequential fp32 sum,
+ * times 1/sum.  reduce must be > 0 when outer*inner > 0. */
+int ts_hip_softmax(const float *x, float *y, size_t outer, size_t reduce, size_t inner, void *stream);
+
+/* ---- broadcasting and axis sums (ops/broadcasting.rs:299-478,
+ * reductions/{sum,mean}.rs sum_dims / mean_dims, grad_fn/utils.rs:23-60) ---- */
+
+#define TS_HIP_MAX_RANK 8
+/* out (out_dims) = src (src_dims) broadcast NumPy-style: source axes align to
+ * the right, axes of size 1 (or missing) repeat; times scale when use_scale.
+ * Dims arrays are host memory; ranks up to TS_HIP_MAX_RANK. */
+int ts_hip_broadcast_copy(const float *src, const size_t *src_dims, size_t src_rank, float *out,
+                          const size_t *out_dims, size_t out_rank, float scale, int use_scale,
+                          void *stream);
+/* Sum of x (dims, rank) over the axes whose bit is set in reduce_mask, into
+ * out laid out with those axes of size 1 (keepdim); f64 accumulation in a
+ * fixed order, rounded once, then times scale (fp32) when use_scale. */
+int ts_hip_reduce_sum(const float *x, const size_t *dims, size_t rank, unsigned reduce_mask, float *out,
+                      float scale, int use_scale, void *stream);
+
 /* ---- elementwise backward -------------------------------------------------- */
 
 /* grad_fn/ops/relu.rs:4-17: gi = x > 0 ? go : 0.  A saved relu OUTPUT may be
@@ -162,6 +198,22 @@ int ts_hip_mul_backward(const float *go, const float *a, const float *b, float *
 int ts_hip_div_backward(const float *go, const float *a, const float *b, float *ga, float *gb,
                         size_t n, size_t tail_start, size_t zero_check_start,
                         unsigned long long *zero_index, void *stream);
+
+/* grad_fn/ops/log.rs: go * (1 / x), from the saved input x */
+int ts_hip_log_backward(const float *x, const float *go, float *gi, size_t n, void *stream);
+/* grad_fn/ops/sqrt.rs: go * ((1 / y) * 0.5), from the saved output y */
+int ts_hip_sqrt_backward(const float *y, const float *go, float *gi, size_t n, void *stream);
+/* grad_fn/ops/tanh.rs: go * (1 - y*y), from the saved output y */
+int ts_hip_tanh_backward(const float *y, const float *go, float *gi, size_t n, void *stream);
+/* grad_fn/ops/sigmoid.rs: go * y * (1 - y), from the saved output y */
+int ts_hip_sigmoid_backward(const float *y, const float *go, float *gi, size_t n, void *stream);
+/* grad_fn/ops/leaky_relu.rs: x > 0 ? go : negative_slope * go */
+int ts_hip_leaky_relu_backward(const float *x, const float *go, float *gi, size_t n, float negative_slope,
+                               void *stream);
+/* grad_fn/ops/softmax.rs:4-38: per slice dot = sequential sum of go*y, then
+ * gi = y * (go - dot).  (exp's backward is ts_hip_mul(go, y).) */
+int ts_hip_softmax_backward(const float *y, const float *go, float *gi, size_t outer, size_t reduce,
+                            size_t inner, void *stream);
 
 /* ---- reductions ------------------------------------------------------------- */
 

@@ -63,6 +63,14 @@ def lib() -> ctypes.CDLL:
                                   ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_uint64,
                                   ctypes.c_int]
         L.o_randn.argtypes = [_F, _SZ, ctypes.c_uint64, ctypes.c_int]
+        L.o_unary.argtypes = [ctypes.c_int, _F, _F, _SZ, ctypes.c_float, ctypes.c_int]
+        L.o_unary_bwd.argtypes = [ctypes.c_int, _F, _F, _F, _SZ, ctypes.c_float]
+        L.o_softmax.argtypes = [_F, _F, _SZ, _SZ, _SZ, ctypes.c_int]
+        L.o_softmax_bwd.argtypes = [_F, _F, _F, _SZ, _SZ, _SZ]
+        L.o_sum_dims.argtypes = [_F, ctypes.POINTER(_SZ), _SZ, ctypes.c_uint, _F, _D]
+        for name in ("o_unary_cr_check", "o_unary_glibc_diff"):
+            getattr(L, name).argtypes = [ctypes.c_int, ctypes.c_uint]
+            getattr(L, name).restype = ctypes.c_long
         L.o_xorshift_next.argtypes = [ctypes.c_uint64]
         L.o_xorshift_next.restype = ctypes.c_uint64
         L.o_xorshift_advance.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
@@ -297,3 +305,83 @@ def libm_glibc_diff(which: int) -> int:
     """Inputs (of 2^23) where the host's logf (0) / cosf (1) differ from the
     correctly rounded value."""
     return int(lib().o_libm_glibc_diff(which))
+
+
+UNARY = {"exp": 0, "log": 1, "sqrt": 2, "tanh": 3, "sigmoid": 4, "leaky_relu": 5}
+
+
+def unary(op: str, x, slope: float = 0.0, correctly_rounded: bool = False) -> np.ndarray:
+    """tensor/ops/{exp,log,sqrt,tanh,sigmoid,leaky_relu}.rs forward.  exp / ln /
+    tanh come from the host libm unless ``correctly_rounded``."""
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().o_unary(UNARY[op], _p(x), _p(out), x.size, ctypes.c_float(slope), int(correctly_rounded))
+    return out
+
+
+def unary_bwd(op: str, saved, go, slope: float = 0.0) -> np.ndarray:
+    """grad_fn/ops/{exp,log,sqrt,tanh,sigmoid,leaky_relu}.rs; saved = output for
+    exp / sqrt / tanh / sigmoid, input for log / leaky_relu."""
+    saved, go = _f32(saved), _f32(go)
+    gi = np.empty_like(go)
+    lib().o_unary_bwd(UNARY[op], _p(saved), _p(go), _p(gi), go.size, ctypes.c_float(slope))
+    return gi
+
+
+def _axis_view(shape, dim):
+    outer = int(np.prod(shape[:dim], dtype=np.int64))
+    inner = int(np.prod(shape[dim + 1:], dtype=np.int64))
+    return outer, int(shape[dim]), inner
+
+
+def softmax(x, dim: int, correctly_rounded: bool = False) -> np.ndarray:
+    x = _f32(x)
+    y = np.empty_like(x)
+    outer, red, inner = _axis_view(x.shape, dim)
+    lib().o_softmax(_p(x), _p(y), outer, red, inner, int(correctly_rounded))
+    return y
+
+
+def softmax_bwd(y, go, dim: int) -> np.ndarray:
+    y, go = _f32(y), _f32(go)
+    gi = np.empty_like(go)
+    outer, red, inner = _axis_view(y.shape, dim)
+    lib().o_softmax_bwd(_p(y), _p(go), _p(gi), outer, red, inner)
+    return gi
+
+
+def sum_dims_shape(shape, dims, keepdim: bool) -> list:
+    """reductions/sum.rs:237-252 (every zero-size axis is dropped when not keepdim)"""
+    out = list(shape)
+    for d in sorted(set(dims)):
+        out[d] = 1 if keepdim else 0
+    if not keepdim:
+        out = [v for v in out if v != 0]
+    return out or [1]
+
+
+def sum_dims(x, dims, keepdim: bool = False, f64: bool = False) -> np.ndarray:
+    """sum_dims (reductions/sum.rs:225-306): fp32 accumulation in input order
+    (or the same sums in f64)."""
+    x = _f32(x)
+    reduced = sorted(set(dims))
+    out_shape = sum_dims_shape(x.shape, dims, keepdim)
+    if x.size == 0:
+        return np.zeros(out_shape, np.float64 if f64 else np.float32)
+    mask = 0
+    for d in reduced:
+        mask |= 1 << d
+    kd = [1 if k in reduced else v for k, v in enumerate(x.shape)]
+    out = np.empty(int(np.prod(kd, dtype=np.int64)), np.float32)
+    out64 = np.empty(out.size, np.float64)
+    dims_arr = (_SZ * max(x.ndim, 1))(*x.shape)
+    lib().o_sum_dims(_p(x), dims_arr, x.ndim, mask, _p(out), out64.ctypes.data_as(_D))
+    return (out64 if f64 else out).reshape(out_shape)
+
+
+def unary_cr_check(op: str, stride: int) -> int:
+    return int(lib().o_unary_cr_check(UNARY[op], stride))
+
+
+def unary_glibc_diff(op: str, stride: int) -> int:
+    return int(lib().o_unary_glibc_diff(UNARY[op], stride))

@@ -38,6 +38,10 @@ import oracle as O
 
 _ids = itertools.count(1)
 
+# exp / ln / tanh in the recorded ops: False = the host libm (what the
+# reference computes), True = correctly rounded (what the device computes)
+CORRECTLY_ROUNDED = False
+
 # thread-local GradGraph of the reference (engine.rs:697-699); one per process here
 _operations: dict[int, tuple[list[int], "GradFn"]] = {}
 _gradients: dict[int, np.ndarray] = {}
@@ -72,6 +76,9 @@ class GradFn:
     scalar: Optional[float] = None
     requires: tuple = (True, True)                  # MatMul requires_grad pair
     numel: int = 0
+    dims: tuple = ()                                # sum_dims / mean_dims axes (sorted, unique)
+    keepdim: bool = False
+    axis: int = 0                                   # softmax
 
 
 class OTensor:
@@ -190,6 +197,58 @@ class OTensor:
         return out
 
     # -- autograd ------------------------------------------------------------
+    # -- tensor/ops/{exp,log,sqrt,tanh,sigmoid,leaky_relu,softmax}.rs -----------
+    def _unary(self, kind: str, slope: float = 0.0) -> "OTensor":
+        out = OTensor(O.unary(kind, self.data, slope, CORRECTLY_ROUNDED))
+        if self.requires_grad and is_grad_enabled():
+            keep_input = kind in ("log", "leaky_relu")
+            self._record(out, [self.id], GradFn(kind, saved=[self.data if keep_input else out.data],
+                                                scalar=slope))
+        return out
+
+    def exp(self):
+        return self._unary("exp")
+
+    def log(self):
+        return self._unary("log")
+
+    def sqrt(self):
+        return self._unary("sqrt")
+
+    def tanh(self):
+        return self._unary("tanh")
+
+    def sigmoid(self):
+        return self._unary("sigmoid")
+
+    def leaky_relu(self, negative_slope: float):
+        return self._unary("leaky_relu", negative_slope)
+
+    def softmax(self, dim: int):
+        assert dim < self.data.ndim, f"softmax dim {dim} out of bounds for rank {self.data.ndim}"
+        out = OTensor(O.softmax(self.data, dim, CORRECTLY_ROUNDED))
+        if self.requires_grad and is_grad_enabled():
+            self._record(out, [self.id], GradFn("softmax", saved=[out.data], axis=dim))
+        return out
+
+    def sum_dims(self, dims, keepdim: bool = False):
+        """reductions/sum.rs:225-306 (records whenever the input requires grad)"""
+        out = OTensor(O.sum_dims(self.data, dims, keepdim))
+        if self.requires_grad:
+            self._record(out, [self.id], GradFn("sum_dims", shapes=(self.shape,), dims=tuple(sorted(set(dims))),
+                                                keepdim=keepdim))
+        return out
+
+    def mean_dims(self, dims, keepdim: bool = False):
+        """reductions/mean.rs:186-230: sum times 1/factor, factor over the axes as listed"""
+        factor = int(np.prod([self.shape[d] for d in dims], dtype=np.int64))
+        scale = np.float32(1.0) / np.float32(factor) if factor > 0 else np.float32(0.0)
+        out = OTensor(O.mul_scalar(O.sum_dims(self.data, dims, keepdim), float(scale)))
+        if self.requires_grad:
+            self._record(out, [self.id], GradFn("mean_dims", shapes=(self.shape,),
+                                                dims=tuple(sorted(set(dims))), keepdim=keepdim))
+        return out
+
     def backward(self, grad_output: Optional[np.ndarray] = None) -> None:
         backward(self, grad_output)
 
@@ -208,25 +267,37 @@ class OTensor:
 
 
 def _broadcast(fn):
-    """[B,N] op [N] (or [N] op [B,N]) after materialising the 1-D operand
-    (ops/broadcasting.rs:299-478); only the row-broadcast case is restated."""
+    """Materialise both operands to the broadcast shape, then the same-shape
+    op (ops/broadcasting.rs:299-478: NumPy's rules, axes aligned right)."""
 
     def apply(a, b):
-        if a.ndim == 2 and b.ndim == 1 and b.shape[0] == a.shape[1]:
-            return fn(a, np.broadcast_to(b, a.shape).copy())
-        if a.ndim == 1 and b.ndim == 2 and a.shape[0] == b.shape[1]:
-            return fn(np.broadcast_to(a, b.shape).copy(), b)
-        raise ValueError(f"Cannot broadcast tensor shapes {a.shape} and {b.shape}")
+        shape = np.broadcast_shapes(a.shape, b.shape)
+        return fn(np.ascontiguousarray(np.broadcast_to(a, shape)), np.ascontiguousarray(np.broadcast_to(b, shape)))
 
     return apply
 
 
 def _reduce_to(g: np.ndarray, shape) -> np.ndarray:
-    """grad_fn/utils.rs:23-60 for the row-broadcast case: sum_dims(&[0])."""
-    if g.shape == tuple(shape):
+    """reduce_gradient_to_shape (grad_fn/utils.rs:23-60): sum_dims([0]) once
+    per leading axis, then sum_dims([i], keepdim) over each axis broadcast
+    from size 1, then a reshape -- with the reference's fp32 sums."""
+    shape = tuple(shape)
+    if g.shape == shape:
         return g
-    assert g.ndim == 2 and len(shape) == 1, (g.shape, shape)
-    return O.sum_dim0(g)
+    r = g
+    for _ in range(g.ndim - len(shape)):
+        r = O.sum_dims(r, [0], False)
+    for i, (cur, tgt) in enumerate(zip(list(r.shape), shape)):
+        if tgt == 1 and cur > 1:
+            r = O.sum_dims(r, [i], True)
+    return np.ascontiguousarray(r.reshape(shape))
+
+
+def _expand(go: np.ndarray, input_shape, dims, keepdim: bool) -> np.ndarray:
+    """apply_reduce_sum_dims (grad_fn/reductions/sum.rs:18-52): each input
+    element takes the gradient at its kept coordinates."""
+    kd = [1 if k in dims else v for k, v in enumerate(input_shape)]
+    return np.ascontiguousarray(np.broadcast_to(go.reshape(kd), input_shape))
 
 
 def _apply(fn: GradFn, go: np.ndarray) -> list[Optional[np.ndarray]]:
@@ -283,6 +354,16 @@ def _apply(fn: GradFn, go: np.ndarray) -> list[Optional[np.ndarray]]:
         if go.size == 1:
             return [O.fill(shape, float(base * np.float32(go.reshape(-1)[0])))]
         return [O.fill(shape, float(base))]
+    if k in ("exp", "log", "sqrt", "tanh", "sigmoid", "leaky_relu"):
+        return [O.unary_bwd(k, fn.saved[0], go, fn.scalar or 0.0)]
+    if k == "softmax":                               # grad_fn/ops/softmax.rs:4-38
+        return [O.softmax_bwd(fn.saved[0], go, fn.axis)]
+    if k == "sum_dims":                              # grad_fn/reductions/sum.rs:18-52
+        return [_expand(go, fn.shapes[0], fn.dims, fn.keepdim)]
+    if k == "mean_dims":                             # grad_fn/reductions/mean.rs:32-52
+        factor = int(np.prod([fn.shapes[0][d] for d in fn.dims], dtype=np.int64))
+        scale = np.float32(1.0) / np.float32(factor) if factor > 0 else np.float32(0.0)
+        return [O.mul_scalar(_expand(go, fn.shapes[0], fn.dims, fn.keepdim), float(scale))]
     raise NotImplementedError(k)
 
 

@@ -397,3 +397,168 @@ EXPORT long o_libm_glibc_diff(int which) {
     }
     return diff;
 }
+
+/* ---- other recorded ops (tensor/ops/{exp,log,sqrt,tanh,sigmoid,leaky_relu,softmax}.rs) ---- */
+
+/* f32 exp / ln / tanh: mode 0 is the host libm (expf, logf, tanhf), which
+ * Rust's f32::exp / ln / tanh call; mode 1 evaluates in f64 and rounds once. */
+static float f_exp(float x, int mode) { return mode ? (float)exp((double)x) : expf(x); }
+static float f_log(float x, int mode) { return mode ? (float)log((double)x) : logf(x); }
+static float f_tanh(float x, int mode) { return mode ? (float)tanh((double)x) : tanhf(x); }
+
+/* op: 0 exp (exp.rs scalar loop), 1 log (log.rs), 2 sqrt (sqrt.rs; AVX2
+ * sqrt_ps and f32::sqrt are both correctly rounded), 3 tanh (tanh.rs),
+ * 4 sigmoid (sigmoid.rs:9-21: x >= 0 ? 1/(1+exp(-x)) : z/(1+z), z = exp(x)),
+ * 5 leaky_relu (leaky_relu.rs: x > 0 ? x : slope*x) */
+EXPORT void o_unary(int op, const float *x, float *y, size_t n, float slope, int mode) {
+    for (size_t i = 0; i < n; ++i) {
+        const float v = x[i];
+        switch (op) {
+            case 0: y[i] = f_exp(v, mode); break;
+            case 1: y[i] = f_log(v, mode); break;
+            case 2: y[i] = sqrtf(v); break;
+            case 3: y[i] = f_tanh(v, mode); break;
+            case 4:
+                if (v >= 0.0f) {
+                    const float z = f_exp(-v, mode);
+                    y[i] = 1.0f / (1.0f + z);
+                } else {
+                    const float z = f_exp(v, mode);
+                    y[i] = z / (1.0f + z);
+                }
+                break;
+            default: y[i] = v > 0.0f ? v : slope * v; break;
+        }
+    }
+}
+
+/* Backward formulas (grad_fn/ops/{exp,log,sqrt,tanh,sigmoid,leaky_relu}.rs);
+ * `saved` is the output y for exp / sqrt / tanh / sigmoid and the input x for
+ * log / leaky_relu:
+ *   exp: go*y; log: inv = 1/x, go*inv; sqrt: inv = 1/y, s = inv*0.5, go*s;
+ *   tanh: go*(1 - y*y); sigmoid: go*y*(1 - y) (left to right);
+ *   leaky_relu: x > 0 ? go : slope*go */
+EXPORT void o_unary_bwd(int op, const float *saved, const float *go, float *gi, size_t n, float slope) {
+    for (size_t i = 0; i < n; ++i) {
+        const float s = saved[i], g = go[i];
+        switch (op) {
+            case 0: gi[i] = g * s; break;
+            case 1: {
+                const float inv = 1.0f / s;
+                gi[i] = g * inv;
+                break;
+            }
+            case 2: {
+                const float inv = 1.0f / s;
+                const float sc = inv * 0.5f;
+                gi[i] = g * sc;
+                break;
+            }
+            case 3: gi[i] = g * (1.0f - s * s); break;
+            case 4: gi[i] = g * s * (1.0f - s); break;
+            default: gi[i] = s > 0.0f ? g : slope * g; break;
+        }
+    }
+}
+
+/* softmax.rs:4-60 on [outer, reduce, inner]: per slice max, then exp(x - max)
+ * with a sequential fp32 sum, then y *= 1/sum */
+EXPORT void o_softmax(const float *x, float *y, size_t outer, size_t reduce, size_t inner, int mode) {
+    for (size_t o = 0; o < outer; ++o)
+        for (size_t i = 0; i < inner; ++i) {
+            const size_t base = o * reduce * inner + i;
+            float maxv = -INFINITY;
+            for (size_t j = 0; j < reduce; ++j) {
+                const float v = x[base + j * inner];
+                if (v > maxv) maxv = v;
+            }
+            float sum = 0.0f;
+            for (size_t j = 0; j < reduce; ++j) {
+                const float e = f_exp(x[base + j * inner] - maxv, mode);
+                y[base + j * inner] = e;
+                sum += e;
+            }
+            const float inv = 1.0f / sum;
+            for (size_t j = 0; j < reduce; ++j) y[base + j * inner] *= inv;
+        }
+}
+
+/* grad_fn/ops/softmax.rs:4-38: dot = sequential fp32 sum of go*y over the
+ * slice, gi = y * (go - dot) */
+EXPORT void o_softmax_bwd(const float *y, const float *go, float *gi, size_t outer, size_t reduce,
+                          size_t inner) {
+    for (size_t o = 0; o < outer; ++o)
+        for (size_t i = 0; i < inner; ++i) {
+            const size_t base = o * reduce * inner + i;
+            float dot = 0.0f;
+            for (size_t j = 0; j < reduce; ++j) dot += go[base + j * inner] * y[base + j * inner];
+            for (size_t j = 0; j < reduce; ++j)
+                gi[base + j * inner] = y[base + j * inner] * (go[base + j * inner] - dot);
+        }
+}
+
+/* sum_dims (reductions/sum.rs:254-287): every input element, in order, is
+ * added in fp32 to the output element its kept coordinates select.  out is
+ * in the keepdim layout (reduced axes of size 1) and starts at zero; out64
+ * (optional) receives the same sums in f64. */
+EXPORT void o_sum_dims(const float *x, const size_t *dims, size_t rank, unsigned mask, float *out,
+                       double *out64) {
+    size_t n = 1, n_out = 1;
+    for (size_t k = 0; k < rank; ++k) {
+        n *= dims[k];
+        if (!((mask >> k) & 1u)) n_out *= dims[k];
+    }
+    for (size_t o = 0; o < n_out; ++o) {
+        out[o] = 0.0f;
+        if (out64) out64[o] = 0.0;
+    }
+    for (size_t lin = 0; lin < n; ++lin) {
+        size_t rem = lin, o = 0, ostride = 1;
+        for (size_t k = rank; k-- > 0;) {
+            const size_t c = rem % dims[k];
+            rem /= dims[k];
+            if (!((mask >> k) & 1u)) {
+                o += c * ostride;
+                ostride *= dims[k];
+            }
+        }
+        out[o] += x[lin];
+        if (out64) out64[o] += (double)x[lin];
+    }
+}
+
+/* Inputs (of the 2^32 bit patterns, every `stride`-th) where the f64 value
+ * rounded once disagrees with the long-double value rounded once (op 0 exp,
+ * 1 log, 3 tanh); o_unary_glibc_diff counts where the host libm's expf /
+ * logf / tanhf differ from the f64 value rounded once. */
+EXPORT long o_unary_cr_check(int op, unsigned stride) {
+    long bad = 0;
+    for (uint64_t b = 0; b < (1ull << 32); b += stride) {
+        uint32_t bits = (uint32_t)b;
+        float x;
+        memcpy(&x, &bits, 4);
+        if (isnan(x)) continue;
+        float a, c;
+        if (op == 0) { a = (float)exp((double)x); c = (float)expl((long double)x); }
+        else if (op == 1) { a = (float)log((double)x); c = (float)logl((long double)x); }
+        else { a = (float)tanh((double)x); c = (float)tanhl((long double)x); }
+        if (memcmp(&a, &c, 4) != 0 && !(isnan(a) && isnan(c))) ++bad;
+    }
+    return bad;
+}
+
+EXPORT long o_unary_glibc_diff(int op, unsigned stride) {
+    long diff = 0;
+    for (uint64_t b = 0; b < (1ull << 32); b += stride) {
+        uint32_t bits = (uint32_t)b;
+        float x;
+        memcpy(&x, &bits, 4);
+        if (isnan(x)) continue;
+        float a, c;
+        if (op == 0) { a = expf(x); c = (float)exp((double)x); }
+        else if (op == 1) { a = logf(x); c = (float)log((double)x); }
+        else { a = tanhf(x); c = (float)tanh((double)x); }
+        if (memcmp(&a, &c, 4) != 0 && !(isnan(a) && isnan(c))) ++diff;
+    }
+    return diff;
+}

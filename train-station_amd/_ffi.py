@@ -83,6 +83,22 @@ HIP_SIGNATURES = {
     "ts_hip_pow_backward": (_c.c_int, [VP, VP, VP, SZ, _c.c_float, VP]),
     "ts_hip_mul_backward": (_c.c_int, [VP, VP, VP, VP, VP, SZ, VP]),
     "ts_hip_div_backward": (_c.c_int, [VP, VP, VP, VP, VP, SZ, SZ, SZ, VP, VP]),
+    "ts_hip_exp": (_c.c_int, [VP, VP, SZ, VP]),
+    "ts_hip_log": (_c.c_int, [VP, VP, SZ, VP]),
+    "ts_hip_tanh": (_c.c_int, [VP, VP, SZ, VP]),
+    "ts_hip_sqrt": (_c.c_int, [VP, VP, SZ, VP]),
+    "ts_hip_sigmoid": (_c.c_int, [VP, VP, SZ, VP]),
+    "ts_hip_leaky_relu": (_c.c_int, [VP, _c.c_float, VP, SZ, VP]),
+    "ts_hip_softmax": (_c.c_int, [VP, VP, SZ, SZ, SZ, VP]),
+    "ts_hip_broadcast_copy": (_c.c_int, [VP, _c.POINTER(SZ), SZ, VP, _c.POINTER(SZ), SZ, _c.c_float,
+                                         _c.c_int, VP]),
+    "ts_hip_reduce_sum": (_c.c_int, [VP, _c.POINTER(SZ), SZ, _c.c_uint, VP, _c.c_float, _c.c_int, VP]),
+    "ts_hip_log_backward": (_c.c_int, [VP, VP, VP, SZ, VP]),
+    "ts_hip_sqrt_backward": (_c.c_int, [VP, VP, VP, SZ, VP]),
+    "ts_hip_tanh_backward": (_c.c_int, [VP, VP, VP, SZ, VP]),
+    "ts_hip_sigmoid_backward": (_c.c_int, [VP, VP, VP, SZ, VP]),
+    "ts_hip_leaky_relu_backward": (_c.c_int, [VP, VP, VP, SZ, _c.c_float, VP]),
+    "ts_hip_softmax_backward": (_c.c_int, [VP, VP, VP, SZ, SZ, SZ, VP]),
     "ts_hip_sum_workspace_floats": (SZ, [SZ]),
     "ts_hip_sum": (_c.c_int, [VP, SZ, VP, VP, SZ, VP]),
     "ts_hip_mean": (_c.c_int, [VP, SZ, VP, VP, SZ, VP]),
@@ -134,6 +150,15 @@ GRADTRACK_SIGNATURES = {
     "ts_tensor_relu": (TP, [TP]),
     "ts_tensor_pow_scalar": (TP, [TP, _c.c_float]),
     "ts_tensor_matmul": (TP, [TP, TP]),
+    "ts_tensor_exp": (TP, [TP]),
+    "ts_tensor_log": (TP, [TP]),
+    "ts_tensor_sqrt": (TP, [TP]),
+    "ts_tensor_tanh": (TP, [TP]),
+    "ts_tensor_sigmoid": (TP, [TP]),
+    "ts_tensor_leaky_relu": (TP, [TP, _c.c_float]),
+    "ts_tensor_softmax": (TP, [TP, SZ]),
+    "ts_tensor_sum_dims": (TP, [TP, _c.POINTER(SZ), SZ, _c.c_int]),
+    "ts_tensor_mean_dims": (TP, [TP, _c.POINTER(SZ), SZ, _c.c_int]),
     "ts_tensor_sum": (TP, [TP]),
     "ts_tensor_mean": (TP, [TP]),
     "ts_tensor_backward": (_c.c_int, [TP, TP]),

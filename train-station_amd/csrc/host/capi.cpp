@@ -154,6 +154,23 @@ TS_SCALAR(ts_tensor_pow_scalar, pow_scalar)
 ts_tensor *ts_tensor_relu(const ts_tensor *a) {
     return guard_ptr([&] { return wrap(T(a).relu()); });
 }
+ts_tensor *ts_tensor_exp(const ts_tensor *a) { return guard_ptr([&] { return wrap(T(a).exp()); }); }
+ts_tensor *ts_tensor_log(const ts_tensor *a) { return guard_ptr([&] { return wrap(T(a).log()); }); }
+ts_tensor *ts_tensor_sqrt(const ts_tensor *a) { return guard_ptr([&] { return wrap(T(a).sqrt()); }); }
+ts_tensor *ts_tensor_tanh(const ts_tensor *a) { return guard_ptr([&] { return wrap(T(a).tanh()); }); }
+ts_tensor *ts_tensor_sigmoid(const ts_tensor *a) { return guard_ptr([&] { return wrap(T(a).sigmoid()); }); }
+ts_tensor *ts_tensor_leaky_relu(const ts_tensor *a, float negative_slope) {
+    return guard_ptr([&] { return wrap(T(a).leaky_relu(negative_slope)); });
+}
+ts_tensor *ts_tensor_softmax(const ts_tensor *a, size_t dim) {
+    return guard_ptr([&] { return wrap(T(a).softmax(dim)); });
+}
+ts_tensor *ts_tensor_sum_dims(const ts_tensor *a, const size_t *dims, size_t ndims, int keepdim) {
+    return guard_ptr([&] { return wrap(T(a).sum_dims(dims_of(dims, ndims), keepdim != 0)); });
+}
+ts_tensor *ts_tensor_mean_dims(const ts_tensor *a, const size_t *dims, size_t ndims, int keepdim) {
+    return guard_ptr([&] { return wrap(T(a).mean_dims(dims_of(dims, ndims), keepdim != 0)); });
+}
 ts_tensor *ts_tensor_sum(const ts_tensor *a) {
     return guard_ptr([&] { return wrap(T(a).sum()); });
 }

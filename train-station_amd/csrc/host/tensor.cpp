@@ -1,6 +1,7 @@
 // Tensor construction, recorded forward ops and their backward formulas.
 // Each op launches one or two kernels of ts_hip.h on the library stream; no
 // op synchronises except data()/value().
+#include <algorithm>
 #include <atomic>
 #include <chrono>
 #include <cmath>
@@ -90,13 +91,61 @@ Tensor neg_of(const Tensor &x) {
     return out;
 }
 
-// grad_fn/utils.rs:23-60 for the shapes the device path records: identical
-// shapes (shared, the reference clones) or the row broadcast, reduced with
-// sum_dims(&[0]).
+// compute_broadcast_shape (ops/broadcasting.rs:320-357): NumPy rules, axes
+// aligned to the right; panics with the reference's message otherwise.
+std::vector<size_t> broadcast_dims(const std::vector<size_t> &a, const std::vector<size_t> &b) {
+    const size_t ra = a.size(), rb = b.size(), r = ra > rb ? ra : rb;
+    std::vector<size_t> out(r);
+    for (size_t i = 0; i < r; ++i) {
+        const size_t da = i < ra ? a[ra - 1 - i] : 1, db = i < rb ? b[rb - 1 - i] : 1;
+        if (da == db || db == 1) out[r - 1 - i] = da;
+        else if (da == 1) out[r - 1 - i] = db;
+        else
+            throw Error("Cannot broadcast tensor shapes " + dims_str(a) + " and " + dims_str(b) +
+                        ": Cannot broadcast shapes " + dims_str(a) + " and " + dims_str(b) +
+                        ": incompatible dimensions at axis " + std::to_string(r - 1 - i));
+    }
+    if (r > TS_HIP_MAX_RANK) throw Error("broadcasting supports tensors of rank up to 8");
+    return out;
+}
+
+// The broadcast operand materialised on the device (create_broadcast_tensor,
+// broadcasting.rs:409-433), optionally scaled.
+Tensor bcast_to(const float *src, const std::vector<size_t> &src_dims, const std::vector<size_t> &dims,
+                float scale = 1.0f, bool use_scale = false) {
+    Tensor out = Tensor::new_uninit(dims);
+    if (out.size())
+        launch(KernelClass::Elementwise, 8.0 * out.size(), "ts_hip_broadcast_copy", [&] {
+            return ts_hip_broadcast_copy(src, src_dims.data(), src_dims.size(), out.dev_mut(), dims.data(),
+                                         dims.size(), scale, use_scale ? 1 : 0, S());
+        });
+    return out;
+}
+
+// Sum of x over the axes in `mask` into a tensor of `out_dims` (the keepdim
+// layout, possibly with the size-1 axes removed: the same element order).
+Tensor reduce_axes(const float *x, const std::vector<size_t> &dims, unsigned mask, std::vector<size_t> out_dims,
+                   float scale = 1.0f, bool use_scale = false) {
+    if (dims.size() > TS_HIP_MAX_RANK) throw Error("reductions support tensors of rank up to 8");
+    Tensor out = Tensor::new_uninit(std::move(out_dims));
+    const size_t n_in = product(dims);
+    if (out.size())
+        launch(KernelClass::Reduction, 4.0 * n_in + 4.0 * out.size(), "ts_hip_reduce_sum", [&] {
+            return ts_hip_reduce_sum(x, dims.data(), dims.size(), mask, out.dev_mut(), scale, use_scale ? 1 : 0,
+                                     S());
+        });
+    return out;
+}
+
+// reduce_gradient_to_shape (grad_fn/utils.rs:23-60): sum over the leading axes
+// broadcasting added and over the axes broadcast from size 1, as one
+// reduction (the reference chains sum_dims calls; the sums agree to
+// rounding).  [B, N] -> [N] uses the column-sum kernel.
 Tensor reduce_to(const Tensor &g, const std::vector<size_t> &target) {
     if (g.dims() == target) return g.alias();
-    if (g.dims().size() == 2 && target.size() == 1 && target[0] == g.dims()[1]) {
-        const size_t rows = g.dims()[0], cols = g.dims()[1];
+    const std::vector<size_t> &gd = g.dims();
+    if (gd.size() == 2 && target.size() == 1 && target[0] == gd[1]) {
+        const size_t rows = gd[0], cols = gd[1];
         Tensor out = Tensor::new_uninit({cols});
         const size_t ws = ts_hip_sum_dim0_workspace_floats(rows, cols);
         Allocation work(ws);
@@ -105,27 +154,39 @@ Tensor reduce_to(const Tensor &g, const std::vector<size_t> &target) {
         });
         return out;
     }
-    throw Error("reduce_gradient_to_shape: " + dims_str(g.dims()) + " -> " + dims_str(target) +
-                " is not a row broadcast");
+    if (target.size() > gd.size()) throw Error("reduce_gradient_to_shape: target has more axes than the gradient");
+    const size_t lead = gd.size() - target.size();
+    unsigned mask = 0;
+    for (size_t k = 0; k < gd.size(); ++k) {
+        if (k < lead) mask |= 1u << k;
+        else if (target[k - lead] == 1 && gd[k] > 1) mask |= 1u << k;
+        else if (target[k - lead] != gd[k])
+            throw Error("reduce_gradient_to_shape: " + dims_str(gd) + " -> " + dims_str(target));
+    }
+    return reduce_axes(g.dev(), gd, mask, target);
 }
 
-struct RowBroadcast {
-    bool matrix_first;  // the [rows,cols] operand is the left one
-    size_t rows, cols;
-};
-
-RowBroadcast row_broadcast_shape(const std::vector<size_t> &a, const std::vector<size_t> &b) {
-    if (a.size() == 2 && b.size() == 1 && b[0] == a[1]) return {true, a[0], a[1]};
-    if (a.size() == 1 && b.size() == 2 && a[0] == b[1]) return {false, b[0], b[1]};
-    throw Error("Cannot broadcast tensor shapes " + dims_str(a) + " and " + dims_str(b) +
-                ": the device path broadcasts a [N] operand over the rows of a [B, N] operand");
+bool is_row_broadcast(const std::vector<size_t> &full, const std::vector<size_t> &v) {
+    return full.size() == 2 && v.size() == 1 && v[0] == full[1];
 }
 
-// go (full shape) op broadcast(x) where x has shape xs: x itself when xs is
-// the full shape, else x broadcast over rows.
+// go (full shape) op broadcast(x): x itself when it has the full shape, the
+// row-broadcast kernel for a [N] vector over [B, N], else x materialised.
 Tensor with_bcast(const Tensor &go, const SavedTensor &x, int op) {
     if (x.dims == go.dims()) return same_shape(go.dev(), x.ptr(), go.dims(), op);
-    return row_bcast(go.dev(), x.ptr(), go.dims()[0], go.dims()[1], op, false);
+    if (is_row_broadcast(go.dims(), x.dims))
+        return row_bcast(go.dev(), x.ptr(), go.dims()[0], go.dims()[1], op, false);
+    Tensor xb = bcast_to(x.ptr(), x.dims, go.dims());
+    return same_shape(go.dev(), xb.dev(), go.dims(), op);
+}
+
+// softmax's [outer, reduce, inner] view of an axis
+void axis_view(const std::vector<size_t> &dims, size_t dim, size_t &outer, size_t &reduce, size_t &inner) {
+    outer = 1;
+    inner = 1;
+    for (size_t k = 0; k < dim; ++k) outer *= dims[k];
+    reduce = dims[dim];
+    for (size_t k = dim + 1; k < dims.size(); ++k) inner *= dims[k];
 }
 
 }  // namespace
@@ -270,11 +331,25 @@ Tensor Tensor::binary(const Tensor &o, GradFn::Kind kind) const {
     Tensor out;
     if (same) {
         out = same_shape(dev(), o.dev(), dims_, op);
+    } else if (is_row_broadcast(dims_, o.dims_)) {
+        out = row_bcast(dev(), o.dev(), dims_[0], dims_[1], op, false);
+    } else if (is_row_broadcast(o.dims_, dims_)) {
+        out = row_bcast(o.dev(), dev(), o.dims_[0], o.dims_[1], op, true);
     } else {
-        RowBroadcast rb = row_broadcast_shape(dims_, o.dims_);
-        const Tensor &mat = rb.matrix_first ? *this : o;
-        const Tensor &vec = rb.matrix_first ? o : *this;
-        out = row_bcast(mat.dev(), vec.dev(), rb.rows, rb.cols, op, !rb.matrix_first);
+        // broadcast_shapes (broadcasting.rs:362-407): materialise the operands
+        // that need it, then the same-shape kernel
+        const std::vector<size_t> full = broadcast_dims(dims_, o.dims_);
+        Tensor ab, bb;
+        const float *pa = dev(), *pb = o.dev();
+        if (dims_ != full) {
+            ab = bcast_to(dev(), dims_, full);
+            pa = ab.dev();
+        }
+        if (o.dims_ != full) {
+            bb = bcast_to(o.dev(), o.dims_, full);
+            pb = bb.dev();
+        }
+        out = same_shape(pa, pb, full, op);
     }
     if ((requires_grad_ || o.requires_grad_) && is_grad_enabled()) {
         GradFn fn{kind};
@@ -396,6 +471,141 @@ Tensor Tensor::mean() const {
         GradFn fn{GradFn::Kind::ReduceMean};
         fn.input_shape = dims_;
         fn.numel = size_;
+        record(out, {id_}, std::move(fn));
+    }
+    return out;
+}
+
+// ---- other recorded ops ---------------------------------------------------------------
+
+// tensor/ops/{exp,log,sqrt,tanh,sigmoid,leaky_relu}.rs: out = f(self); recorded
+// when self requires grad and grad is enabled, saving the output (exp, sqrt,
+// tanh, sigmoid) or the input (log, leaky_relu).
+template <class F>
+Tensor Tensor::unary(GradFn::Kind kind, const char *what, bool save_output, float slope, F &&launcher) const {
+    Tensor out = new_uninit(dims_);
+    if (size_) launch(KernelClass::Elementwise, 8.0 * size_, what, [&] { return launcher(out.dev_mut()); });
+    if (requires_grad_ && is_grad_enabled()) {
+        GradFn fn{kind};
+        fn.scalar = slope;
+        fn.saved = {save_output ? out.saved() : saved()};
+        record(out, {id_}, std::move(fn));
+    }
+    return out;
+}
+
+Tensor Tensor::exp() const {
+    return unary(GradFn::Kind::Exp, "ts_hip_exp", true, 0.0f,
+                 [&](float *o) { return ts_hip_exp(dev(), o, size_, S()); });
+}
+Tensor Tensor::log() const {
+    return unary(GradFn::Kind::Log, "ts_hip_log", false, 0.0f,
+                 [&](float *o) { return ts_hip_log(dev(), o, size_, S()); });
+}
+Tensor Tensor::sqrt() const {
+    return unary(GradFn::Kind::Sqrt, "ts_hip_sqrt", true, 0.0f,
+                 [&](float *o) { return ts_hip_sqrt(dev(), o, size_, S()); });
+}
+Tensor Tensor::tanh() const {
+    return unary(GradFn::Kind::Tanh, "ts_hip_tanh", true, 0.0f,
+                 [&](float *o) { return ts_hip_tanh(dev(), o, size_, S()); });
+}
+Tensor Tensor::sigmoid() const {
+    return unary(GradFn::Kind::Sigmoid, "ts_hip_sigmoid", true, 0.0f,
+                 [&](float *o) { return ts_hip_sigmoid(dev(), o, size_, S()); });
+}
+Tensor Tensor::leaky_relu(float slope) const {
+    return unary(GradFn::Kind::LeakyRelu, "ts_hip_leaky_relu", false, slope,
+                 [&](float *o) { return ts_hip_leaky_relu(dev(), slope, o, size_, S()); });
+}
+
+// softmax.rs:4-60
+Tensor Tensor::softmax(size_t dim) const {
+    if (dim >= dims_.size())
+        throw Error("softmax dim " + std::to_string(dim) + " out of bounds for rank " + std::to_string(dims_.size()));
+    size_t outer, reduce, inner;
+    axis_view(dims_, dim, outer, reduce, inner);
+    if (reduce == 0) throw Error("cannot softmax over empty dimension");
+    Tensor out = new_uninit(dims_);
+    if (size_)
+        launch(KernelClass::Reduction, 8.0 * size_, "ts_hip_softmax",
+               [&] { return ts_hip_softmax(dev(), out.dev_mut(), outer, reduce, inner, S()); });
+    if (requires_grad_ && is_grad_enabled()) {
+        GradFn fn{GradFn::Kind::Softmax};
+        fn.axis = dim;
+        fn.saved = {out.saved()};
+        record(out, {id_}, std::move(fn));
+    }
+    return out;
+}
+
+namespace {
+
+// sum_dims' output shape (reductions/sum.rs:237-252): reduced axes become 1
+// (keepdim) or are dropped -- the reference drops every zero-size axis at this
+// point -- and an empty shape becomes [1].
+std::vector<size_t> sum_dims_shape(const std::vector<size_t> &in, const std::vector<size_t> &reduced, bool keepdim) {
+    std::vector<size_t> out = in;
+    for (size_t d : reduced) out[d] = keepdim ? 1 : 0;
+    if (!keepdim) {
+        std::vector<size_t> kept;
+        for (size_t v : out)
+            if (v != 0) kept.push_back(v);
+        out = kept;
+    }
+    if (out.empty()) out.push_back(1);
+    return out;
+}
+
+std::vector<size_t> checked_axes(const std::vector<size_t> &dims, size_t rank, const char *what) {
+    if (dims.empty()) throw Error(std::string(what) + " requires at least one dimension");
+    for (size_t d : dims)
+        if (d >= rank)
+            throw Error(std::string(what) + " dim " + std::to_string(d) + " out of bounds for rank " +
+                        std::to_string(rank));
+    std::vector<size_t> r = dims;
+    std::sort(r.begin(), r.end());
+    r.erase(std::unique(r.begin(), r.end()), r.end());
+    return r;
+}
+
+unsigned axis_mask(const std::vector<size_t> &reduced) {
+    unsigned m = 0;
+    for (size_t d : reduced) m |= 1u << d;
+    return m;
+}
+
+}  // namespace
+
+Tensor Tensor::sum_dims(const std::vector<size_t> &dims, bool keepdim) const {
+    const std::vector<size_t> reduced = checked_axes(dims, dims_.size(), "sum_dims");
+    std::vector<size_t> out_dims = sum_dims_shape(dims_, reduced, keepdim);
+    Tensor out = size_ ? reduce_axes(dev(), dims_, axis_mask(reduced), out_dims) : Tensor::zeros(out_dims);
+    if (requires_grad_) {  // sum.rs:290-300 (no is_grad_enabled check)
+        GradFn fn{GradFn::Kind::ReduceSumDims};
+        fn.reduce_dims = reduced;
+        fn.input_shape = dims_;
+        fn.keepdim = keepdim;
+        record(out, {id_}, std::move(fn));
+    }
+    return out;
+}
+
+// mean.rs:186-230: the sum times 1/factor, factor = product of the listed
+// axes' sizes as given (a repeated axis counts twice, as there)
+Tensor Tensor::mean_dims(const std::vector<size_t> &dims, bool keepdim) const {
+    const std::vector<size_t> reduced = checked_axes(dims, dims_.size(), "mean_dims");
+    size_t factor = 1;
+    for (size_t d : dims) factor *= dims_[d];
+    const float scale = factor > 0 ? 1.0f / static_cast<float>(factor) : 0.0f;
+    std::vector<size_t> out_dims = sum_dims_shape(dims_, reduced, keepdim);
+    Tensor out = size_ ? reduce_axes(dev(), dims_, axis_mask(reduced), out_dims, scale, true)
+                       : Tensor::zeros(out_dims);
+    if (requires_grad_) {
+        GradFn fn{GradFn::Kind::ReduceMeanDims};
+        fn.reduce_dims = reduced;
+        fn.input_shape = dims_;
+        fn.keepdim = keepdim;
         record(out, {id_}, std::move(fn));
     }
     return out;
@@ -535,6 +745,61 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
             } else {
                 r.emplace_back(std::nullopt);
             }
+            break;
+        }
+        case K::Exp: {  // grad_fn/ops/exp.rs: go * y
+            Tensor g = Tensor::new_uninit(go.dims());
+            launch(KernelClass::Elementwise, 12.0 * n, "exp grad",
+                   [&] { return ts_hip_mul(go.dev(), saved[0].ptr(), g.dev_mut(), n, S()); });
+            r.emplace_back(std::move(g));
+            break;
+        }
+        case K::Log:
+        case K::Sqrt:
+        case K::Tanh:
+        case K::Sigmoid:
+        case K::LeakyRelu: {  // grad_fn/ops/{log,sqrt,tanh,sigmoid,leaky_relu}.rs
+            Tensor g = Tensor::new_uninit(go.dims());
+            launch(KernelClass::Elementwise, 12.0 * n, "activation grad", [&] {
+                const float *sv = saved[0].ptr();
+                switch (kind) {
+                    case K::Log: return ts_hip_log_backward(sv, go.dev(), g.dev_mut(), n, S());
+                    case K::Sqrt: return ts_hip_sqrt_backward(sv, go.dev(), g.dev_mut(), n, S());
+                    case K::Tanh: return ts_hip_tanh_backward(sv, go.dev(), g.dev_mut(), n, S());
+                    case K::Sigmoid: return ts_hip_sigmoid_backward(sv, go.dev(), g.dev_mut(), n, S());
+                    default: return ts_hip_leaky_relu_backward(sv, go.dev(), g.dev_mut(), n, scalar, S());
+                }
+            });
+            r.emplace_back(std::move(g));
+            break;
+        }
+        case K::Softmax: {  // grad_fn/ops/softmax.rs:4-38
+            size_t outer, red, inner;
+            axis_view(saved[0].dims, axis, outer, red, inner);
+            Tensor g = Tensor::new_uninit(go.dims());
+            launch(KernelClass::Reduction, 12.0 * n, "ts_hip_softmax_backward", [&] {
+                return ts_hip_softmax_backward(saved[0].ptr(), go.dev(), g.dev_mut(), outer, red, inner, S());
+            });
+            r.emplace_back(std::move(g));
+            break;
+        }
+        case K::ReduceSumDims:
+        case K::ReduceMeanDims: {  // grad_fn/reductions/sum.rs:18-52, mean.rs:32-52
+            // go holds the keepdim layout's values: broadcast them back over the
+            // reduced axes (times 1/factor for the mean, factor over the
+            // deduplicated axes as the backward computes it)
+            std::vector<size_t> kd = input_shape;
+            size_t factor = 1;
+            for (size_t d : reduce_dims) {
+                kd[d] = 1;
+                factor *= input_shape[d];
+            }
+            const bool mean = kind == K::ReduceMeanDims;
+            const float scale = factor > 0 ? 1.0f / static_cast<float>(factor) : 0.0f;
+            if (product(input_shape) && go.size() != product(kd))
+                throw Error("reduce_dims backward: gradient of " + std::to_string(go.size()) +
+                            " elements for an output of " + std::to_string(product(kd)));
+            r.emplace_back(bcast_to(go.dev(), kd, input_shape, scale, mean));
             break;
         }
         case K::ReduceSum: {  // grad_fn/reductions/sum.rs:4-16

@@ -136,7 +136,8 @@ struct SavedTensor {
 struct GradFn {
     enum class Kind {
         Add, Sub, Mul, Div, AddScalar, SubScalar, MulScalar, DivScalar,
-        Relu, PowScalar, MatMul, ReduceSum, ReduceMean
+        Relu, PowScalar, MatMul, ReduceSum, ReduceMean,
+        Exp, Log, Sqrt, Tanh, Sigmoid, LeakyRelu, Softmax, ReduceSumDims, ReduceMeanDims
     };
     explicit GradFn(Kind k) : kind(k) {}
     Kind kind;
@@ -147,6 +148,9 @@ struct GradFn {
     bool req_left = false, req_right = false;
     std::vector<size_t> input_shape;   // reductions
     size_t numel = 0;
+    std::vector<size_t> reduce_dims;   // sum_dims / mean_dims: sorted, deduplicated
+    bool keepdim = false;
+    size_t axis = 0;                   // softmax
 
     // GradFn::apply (grad_fn/mod.rs:490-789): gradients by operand position.
     std::vector<std::optional<Tensor>> apply(const Tensor &grad_output) const;
@@ -223,6 +227,17 @@ class Tensor {
     Tensor matmul(const Tensor &o) const;
     Tensor sum() const;
     Tensor mean() const;
+    // tensor/ops/{exp,log,sqrt,tanh,sigmoid,leaky_relu,softmax}.rs
+    Tensor exp() const;
+    Tensor log() const;
+    Tensor sqrt() const;
+    Tensor tanh() const;
+    Tensor sigmoid() const;
+    Tensor leaky_relu(float negative_slope) const;
+    Tensor softmax(size_t dim) const;
+    // reductions/sum.rs:225-306, reductions/mean.rs:186-230
+    Tensor sum_dims(const std::vector<size_t> &dims, bool keepdim) const;
+    Tensor mean_dims(const std::vector<size_t> &dims, bool keepdim) const;
 
     // host access (synchronises)
     std::vector<float> data() const;
@@ -233,6 +248,8 @@ class Tensor {
     friend struct GradFn;
     Tensor binary(const Tensor &o, GradFn::Kind kind) const;
     Tensor scalar_op(float s, GradFn::Kind kind) const;
+    template <class F>
+    Tensor unary(GradFn::Kind kind, const char *what, bool save_output, float slope, F &&launcher) const;
     void record(Tensor &out, std::vector<size_t> input_ids, GradFn fn) const;
 
     std::shared_ptr<Allocation> alloc_;

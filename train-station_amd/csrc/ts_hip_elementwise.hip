@@ -70,6 +70,67 @@ struct FillFromOp {
     }
 };
 
+// ---- activations (tensor/ops/{exp,log,sqrt,tanh,sigmoid,leaky_relu}.rs) ----
+// The reference calls f32::exp / ln / tanh, i.e. the host libm's expf / logf /
+// tanhf.  Here each is evaluated in f64 and rounded once: the correctly
+// rounded value, which those libm functions return on all but a small share
+// of inputs (where the two differ in the last place).
+__device__ inline float exp_cr(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
+__device__ inline float log_cr(float x) { return static_cast<float>(log(static_cast<double>(x))); }
+__device__ inline float tanh_cr(float x) { return static_cast<float>(tanh(static_cast<double>(x))); }
+
+struct ExpOp { static constexpr int NIN = 1, NOUT = 1;
+    __device__ void operator()(size_t, const float *x, float *y) const { y[0] = exp_cr(x[0]); } };
+struct LogOp { static constexpr int NIN = 1, NOUT = 1;
+    __device__ void operator()(size_t, const float *x, float *y) const { y[0] = log_cr(x[0]); } };
+// sqrt.rs: _mm256_sqrt_ps / f32::sqrt, both correctly rounded, as sqrtf is here
+struct SqrtOp { static constexpr int NIN = 1, NOUT = 1;
+    __device__ void operator()(size_t, const float *x, float *y) const { y[0] = sqrtf(x[0]); } };
+struct TanhOp { static constexpr int NIN = 1, NOUT = 1;
+    __device__ void operator()(size_t, const float *x, float *y) const { y[0] = tanh_cr(x[0]); } };
+// sigmoid.rs:9-21, the two-branch stable form
+struct SigmoidOp { static constexpr int NIN = 1, NOUT = 1;
+    __device__ void operator()(size_t, const float *x, float *y) const {
+        const float v = x[0];
+        if (v >= 0.0f) {
+            const float z = exp_cr(-v);
+            y[0] = 1.0f / (1.0f + z);
+        } else {
+            const float z = exp_cr(v);
+            y[0] = z / (1.0f + z);
+        }
+    } };
+// leaky_relu.rs: x > 0 ? x : slope * x (the AVX2 blend and the scalar tail agree)
+struct LeakyReluOp { static constexpr int NIN = 1, NOUT = 1; float slope;
+    __device__ void operator()(size_t, const float *x, float *y) const {
+        y[0] = x[0] > 0.0f ? x[0] : slope * x[0]; } };
+
+// grad_fn/ops/log.rs: inv = 1 / x, then go * inv.  Inputs (x, go).
+struct LogBwdOp { static constexpr int NIN = 2, NOUT = 1;
+    __device__ void operator()(size_t, const float *x, float *y) const {
+        const float inv = 1.0f / x[0];
+        y[0] = x[1] * inv; } };
+// grad_fn/ops/sqrt.rs: inv = 1 / s, scaled = inv * 0.5, go * scaled.  Inputs (s, go).
+struct SqrtBwdOp { static constexpr int NIN = 2, NOUT = 1;
+    __device__ void operator()(size_t, const float *x, float *y) const {
+        const float inv = 1.0f / x[0];
+        const float scaled = inv * 0.5f;
+        y[0] = x[1] * scaled; } };
+// grad_fn/ops/tanh.rs: go * (1 - t*t).  Inputs (t, go).
+struct TanhBwdOp { static constexpr int NIN = 2, NOUT = 1;
+    __device__ void operator()(size_t, const float *x, float *y) const {
+        const float t = x[0];
+        y[0] = x[1] * (1.0f - t * t); } };
+// grad_fn/ops/sigmoid.rs: (go * s) * (1 - s).  Inputs (s, go).
+struct SigmoidBwdOp { static constexpr int NIN = 2, NOUT = 1;
+    __device__ void operator()(size_t, const float *x, float *y) const {
+        const float s = x[0];
+        y[0] = x[1] * s * (1.0f - s); } };
+// grad_fn/ops/leaky_relu.rs: x > 0 ? go : slope * go.  Inputs (x, go).
+struct LeakyReluBwdOp { static constexpr int NIN = 2, NOUT = 1; float slope;
+    __device__ void operator()(size_t, const float *x, float *y) const {
+        y[0] = x[0] > 0.0f ? x[1] : slope * x[1]; } };
+
 // grad_fn/ops/relu.rs:4-17
 struct ReluBwdOp { static constexpr int NIN = 2, NOUT = 1;
     __device__ void operator()(size_t, const float *x, float *y) const {
@@ -333,6 +394,33 @@ int ts_hip_fill_from_device(float *out, const float *src, float multiplier, int 
     float *o[1] = {out};
     return launch_map<FillFromOp>(nullptr, o, n, FillFromOp{src, multiplier, use_multiplier},
                                   stream);
+}
+
+int ts_hip_exp(const float *x, float *out, size_t n, void *stream) { return map1(x, out, n, ExpOp{}, stream); }
+int ts_hip_log(const float *x, float *out, size_t n, void *stream) { return map1(x, out, n, LogOp{}, stream); }
+int ts_hip_sqrt(const float *x, float *out, size_t n, void *stream) { return map1(x, out, n, SqrtOp{}, stream); }
+int ts_hip_tanh(const float *x, float *out, size_t n, void *stream) { return map1(x, out, n, TanhOp{}, stream); }
+int ts_hip_sigmoid(const float *x, float *out, size_t n, void *stream) {
+    return map1(x, out, n, SigmoidOp{}, stream);
+}
+int ts_hip_leaky_relu(const float *x, float negative_slope, float *out, size_t n, void *stream) {
+    return map1(x, out, n, LeakyReluOp{negative_slope}, stream);
+}
+int ts_hip_log_backward(const float *x, const float *go, float *gi, size_t n, void *stream) {
+    return map2(x, go, gi, n, LogBwdOp{}, stream);
+}
+int ts_hip_sqrt_backward(const float *y, const float *go, float *gi, size_t n, void *stream) {
+    return map2(y, go, gi, n, SqrtBwdOp{}, stream);
+}
+int ts_hip_tanh_backward(const float *y, const float *go, float *gi, size_t n, void *stream) {
+    return map2(y, go, gi, n, TanhBwdOp{}, stream);
+}
+int ts_hip_sigmoid_backward(const float *y, const float *go, float *gi, size_t n, void *stream) {
+    return map2(y, go, gi, n, SigmoidBwdOp{}, stream);
+}
+int ts_hip_leaky_relu_backward(const float *x, const float *go, float *gi, size_t n, float negative_slope,
+                               void *stream) {
+    return map2(x, go, gi, n, LeakyReluBwdOp{negative_slope}, stream);
 }
 
 int ts_hip_relu_backward(const float *x, const float *go, float *gi, size_t n, void *stream) {

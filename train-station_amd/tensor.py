@@ -158,6 +158,36 @@ class Tensor:
     def matmul(self, other: "Tensor") -> "Tensor":
         return _wrap(_G.ts_tensor_matmul(self._h, other._h))
 
+    # -- tensor/ops/{exp,log,sqrt,tanh,sigmoid,leaky_relu,softmax}.rs -------------
+    def exp(self) -> "Tensor":
+        return _wrap(_G.ts_tensor_exp(self._h))
+
+    def log(self) -> "Tensor":
+        return _wrap(_G.ts_tensor_log(self._h))
+
+    def sqrt(self) -> "Tensor":
+        return _wrap(_G.ts_tensor_sqrt(self._h))
+
+    def tanh(self) -> "Tensor":
+        return _wrap(_G.ts_tensor_tanh(self._h))
+
+    def sigmoid(self) -> "Tensor":
+        return _wrap(_G.ts_tensor_sigmoid(self._h))
+
+    def leaky_relu(self, negative_slope: float) -> "Tensor":
+        return _wrap(_G.ts_tensor_leaky_relu(self._h, negative_slope))
+
+    def softmax(self, dim: int) -> "Tensor":
+        return _wrap(_G.ts_tensor_softmax(self._h, dim))
+
+    def sum_dims(self, dims: Sequence[int], keepdim: bool = False) -> "Tensor":
+        d, r = _dims(dims)
+        return _wrap(_G.ts_tensor_sum_dims(self._h, d, r, int(bool(keepdim))))
+
+    def mean_dims(self, dims: Sequence[int], keepdim: bool = False) -> "Tensor":
+        d, r = _dims(dims)
+        return _wrap(_G.ts_tensor_mean_dims(self._h, d, r, int(bool(keepdim))))
+
     def sum(self) -> "Tensor":
         return _wrap(_G.ts_tensor_sum(self._h))
 
