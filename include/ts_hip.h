@@ -252,6 +252,31 @@ int ts_hip_matmul(const float *a, const float *b, float *c, size_t m, size_t n, 
 int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
                 size_t lda, const float *B, size_t ldb, float *C, size_t ldc, void *stream);
 
+/* Batched C[b] = op(A[b]) . op(B[b]) (matmul/mod.rs:634-760 batched_matmul and
+ * the batched backward of grad_fn/ops/matmul.rs:150-219) on the same MFMA
+ * tiles: a batch grid of batch_rank axes (<= 6) with sizes batch_dims; the A /
+ * B matrices of batch coordinate c start at sum_k c_k * a_batch_strides[k]
+ * (resp. b_...) elements -- 0 on an axis the operand broadcasts -- and the C
+ * matrices are c_batch_stride elements apart, in row-major batch order. */
+int ts_hip_gemm_batched(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A, size_t lda,
+                        const float *B, size_t ldb, float *C, size_t ldc, size_t batch_rank,
+                        const size_t *batch_dims, const size_t *a_batch_strides, const size_t *b_batch_strides,
+                        size_t c_batch_stride, void *stream);
+/* Vector cases (matmul/mod.rs:332-632): trans 0: y[r] = sum_c A[r][c] x[c]
+ * (matrix . vector); trans 1: y[c] = sum_r x[r] A[r][c] (vector . matrix, and
+ * the backward of matrix . vector).  A is [rows, cols] row-major (lda == cols
+ * for trans 1); f64 accumulation.  trans 1 needs the workspace of
+ * ts_hip_gemv_workspace_floats (8-byte aligned). */
+size_t ts_hip_gemv_workspace_floats(int trans, size_t rows, size_t cols);
+int ts_hip_gemv(int trans, size_t rows, size_t cols, const float *A, size_t lda, const float *x, float *y,
+                float *workspace, size_t workspace_floats, void *stream);
+/* 1-D . 1-D (matmul/mod.rs:310-350 dot_product_1d): out[0] = sum a[i]*b[i],
+ * f64 accumulation; workspace as ts_hip_sum_workspace_floats(n) */
+int ts_hip_dot(const float *a, const float *b, size_t n, float *out, float *workspace, size_t workspace_floats,
+               void *stream);
+/* out[i][j] = a[i] * b[j] (grad_fn/ops/matmul.rs compute_outer_product, fp32) */
+int ts_hip_outer(const float *a, size_t m, const float *b, size_t n, float *out, void *stream);
+
 /* ---- optimizer ------------------------------------------------------------------ */
 
 /* optimizers/adam/mod.rs:485-1007, one parameter, fused into one pass that

@@ -83,7 +83,8 @@ class GradFn:
 
 class OTensor:
     def __init__(self, data: np.ndarray, requires_grad: bool = False):
-        self.data = np.ascontiguousarray(data, dtype=np.float32)
+        a = np.asarray(data, dtype=np.float32)  # keeps rank 0 (ascontiguousarray would not)
+        self.data = a if a.flags.c_contiguous else a.copy(order="C")
         self.id = next(_ids)
         self.requires_grad = requires_grad
         self.grad: Optional[np.ndarray] = None
@@ -176,8 +177,9 @@ class OTensor:
         return out
 
     def matmul(self, other):
-        assert self.data.ndim == 2 and other.data.ndim == 2
-        out = OTensor(O.gemm_f64(self.data, other.data).astype(np.float32))
+        """ops/matmul/mod.rs:263-310: 1D.1D dot (shape []), 1D.2D, 2D.1D, 2D.2D,
+        else batched with broadcast batch axes (both operands at least 2D)."""
+        out = OTensor(_matmul_f64(self.data, other.data))
         if (self.requires_grad or other.requires_grad) and is_grad_enabled():
             self._record(out, [self.id, other.id],
                          GradFn("matmul", saved=[self.data, other.data],
@@ -293,6 +295,24 @@ def _reduce_to(g: np.ndarray, shape) -> np.ndarray:
     return np.ascontiguousarray(r.reshape(shape))
 
 
+def _matmul_f64(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """The product in f64 rounded once to fp32, with the reference's shape rules
+    and messages (numpy's matmul broadcasts batch axes the same way)."""
+    if a.ndim == 1 and b.ndim == 1:
+        if a.shape[0] != b.shape[0]:
+            raise ValueError("Tensors must have same length for dot product")
+        return np.array(np.dot(a.astype(np.float64), b.astype(np.float64)), np.float32).reshape(())
+    if a.ndim == 1 and b.ndim == 2 and a.shape[0] != b.shape[0]:
+        raise ValueError("Vector length must match matrix rows")
+    if a.ndim == 2 and b.ndim == 1 and a.shape[1] != b.shape[0]:
+        raise ValueError("Matrix columns must match vector length")
+    if (a.ndim > 2 or b.ndim > 2) and (a.ndim < 2 or b.ndim < 2):
+        raise ValueError("Batched matmul requires at least 2D tensors")
+    if a.ndim == 2 and b.ndim == 2:
+        return O.gemm_f64(a, b).astype(np.float32)
+    return np.ascontiguousarray(np.matmul(a.astype(np.float64), b.astype(np.float64)).astype(np.float32))
+
+
 def _expand(go: np.ndarray, input_shape, dims, keepdim: bool) -> np.ndarray:
     """apply_reduce_sum_dims (grad_fn/reductions/sum.rs:18-52): each input
     element takes the gradient at its kept coordinates."""
@@ -338,10 +358,26 @@ def _apply(fn: GradFn, go: np.ndarray) -> list[Optional[np.ndarray]]:
         return [O.relu_bwd(fn.saved[0], go)]
     if k == "pow":                                   # grad_fn/ops/pow.rs:5-27
         return [O.pow_bwd(fn.saved[0], go, fn.scalar)]
-    if k == "matmul":                                # grad_fn/ops/matmul.rs:68-80
+    if k == "matmul":                                # grad_fn/ops/matmul.rs:4-219
         a, b = fn.saved
-        gl = O.gemm_f64(go, b, tb=True).astype(np.float32) if fn.requires[0] else None
-        gr = O.gemm_f64(a, go, ta=True).astype(np.float32) if fn.requires[1] else None
+        if a.ndim == 2 and b.ndim == 2:
+            gl = O.gemm_f64(go, b, tb=True).astype(np.float32) if fn.requires[0] else None
+            gr = O.gemm_f64(a, go, ta=True).astype(np.float32) if fn.requires[1] else None
+            return [gl, gr]
+        if a.ndim == 1 and b.ndim == 1:              # go * b, go * a (go has shape [])
+            g = np.broadcast_to(go.reshape(()), a.shape)
+            return [O.mul(np.ascontiguousarray(g), b) if fn.requires[0] else None,
+                    O.mul(np.ascontiguousarray(g), a) if fn.requires[1] else None]
+        g64, a64, b64 = (v.astype(np.float64) for v in (go, a, b))
+        if a.ndim == 1 and b.ndim == 2:              # go . M^T, outer(v, go)
+            return [(b64 @ g64).astype(np.float32) if fn.requires[0] else None,
+                    O.mul(*np.broadcast_arrays(a[:, None], go[None, :])) if fn.requires[1] else None]
+        if a.ndim == 2 and b.ndim == 1:              # outer(go, v), M^T . go
+            return [O.mul(*np.broadcast_arrays(go[:, None], b[None, :])) if fn.requires[0] else None,
+                    (a64.T @ g64).astype(np.float32) if fn.requires[1] else None]
+        # batched: go . B^T and A^T . go, then reduce_gradient_to_original_shape
+        gl = _reduce_to(np.matmul(g64, np.swapaxes(b64, -1, -2)).astype(np.float32), a.shape) if fn.requires[0] else None
+        gr = _reduce_to(np.matmul(np.swapaxes(a64, -1, -2), g64).astype(np.float32), b.shape) if fn.requires[1] else None
         return [gl, gr]
     if k == "sum":                                   # grad_fn/reductions/sum.rs:4-16
         shape = fn.shapes[0]

@@ -154,3 +154,34 @@ def test_graph_with_broadcasting_and_new_ops_against_torch_autograd():
     finally:
         G.CORRECTLY_ROUNDED = False
         G.clear_gradients()
+
+
+MATMUL_CASES = [((7,), (7,)), ((7,), (7, 5)), ((6, 7), (7,)), ((6, 7), (7, 5)), ((3, 6, 7), (3, 7, 5)),
+                ((2, 1, 6, 7), (4, 7, 5)), ((6, 7), (4, 7, 5)), ((2, 3, 6, 7), (7, 5)), ((1, 6, 7), (7, 5)),
+                ((6, 7), (1, 7, 5))]
+
+
+@pytest.mark.parametrize("sa,sb", MATMUL_CASES, ids=lambda s: "x".join(map(str, s)))
+def test_matmul_ranks_against_torch_autograd(sa, sb):
+    a, b = normal(sa, 1), normal(sb, 2)
+    A, B = G.OTensor(a.copy(), True), G.OTensor(b.copy(), True)
+    ta, tb = (torch.from_numpy(v.astype(np.float64)).requires_grad_(True) for v in (a, b))
+    y = A.matmul(B)
+    ty = torch.matmul(ta, tb)
+    assert y.shape == tuple(ty.shape)
+    assert np.max(np.abs(y.data - ty.detach().numpy())) <= 1e-6 * max(1.0, float(ty.abs().max()))
+    go = np.array(normal(y.shape, 3), np.float32).reshape(y.shape)
+    G.backward(y, go)
+    ty.backward(torch.from_numpy(go.astype(np.float64)))
+    for mine, theirs in ((A, ta), (B, tb)):
+        g = mine.grad_by_value()
+        assert g.shape == tuple(theirs.shape)  # operand-shaped gradients in every case
+        assert np.max(np.abs(g - theirs.grad.numpy())) <= 1e-5 * max(1.0, float(theirs.grad.abs().max()))
+    G.clear_gradients()
+
+
+@pytest.mark.parametrize("sa,sb,msg", [((3,), (4,), "same length"), ((3,), (4, 2), "Vector length"),
+                                       ((2, 3), (4,), "Matrix columns"), ((3,), (2, 3, 4), "at least 2D")])
+def test_matmul_shape_errors(sa, sb, msg):
+    with pytest.raises(ValueError, match=msg):
+        G.OTensor(normal(sa, 1)).matmul(G.OTensor(normal(sb, 2)))

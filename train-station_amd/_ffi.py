@@ -106,6 +106,12 @@ HIP_SIGNATURES = {
     "ts_hip_sum_dim0": (_c.c_int, [VP, SZ, SZ, VP, VP, SZ, VP]),
     "ts_hip_matmul": (_c.c_int, [VP, VP, VP, SZ, SZ, SZ, VP]),
     "ts_hip_gemm": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, SZ, VP]),
+    "ts_hip_gemm_batched": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, SZ, SZ,
+                                       _c.POINTER(SZ), _c.POINTER(SZ), _c.POINTER(SZ), SZ, VP]),
+    "ts_hip_gemv_workspace_floats": (SZ, [_c.c_int, SZ, SZ]),
+    "ts_hip_gemv": (_c.c_int, [_c.c_int, SZ, SZ, VP, SZ, VP, VP, VP, SZ, VP]),
+    "ts_hip_dot": (_c.c_int, [VP, VP, SZ, VP, VP, SZ, VP]),
+    "ts_hip_outer": (_c.c_int, [VP, SZ, VP, SZ, VP, VP]),
     "ts_hip_adam_step": (_c.c_int, [VP, VP, VP, VP, VP, SZ, _c.c_float, _c.c_float, _c.c_float,
                                     _c.c_float, _c.c_float, _c.c_uint64, SZ, _c.c_int, VP]),
     "ts_hip_adam_step_multi": (_c.c_int, [VP, SZ, _c.c_float, _c.c_float, _c.c_float, _c.c_float,

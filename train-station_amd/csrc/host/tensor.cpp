@@ -425,18 +425,112 @@ Tensor Tensor::pow_scalar(float e) const {
     return out;
 }
 
+namespace {
+
+// Output batch axes of batched_matmul (matmul/mod.rs:660-690): the batch
+// axes (all but the last two) broadcast right-aligned.
+std::vector<size_t> matmul_batch_dims(const std::vector<size_t> &a, const std::vector<size_t> &b) {
+    const size_t ra = a.size() - 2, rb = b.size() - 2, r = ra > rb ? ra : rb;
+    std::vector<size_t> out(r);
+    for (size_t i = 0; i < r; ++i) {
+        const size_t da = i < ra ? a[ra - 1 - i] : 1, db = i < rb ? b[rb - 1 - i] : 1;
+        if (da == 1) out[r - 1 - i] = db;
+        else if (db == 1 || da == db) out[r - 1 - i] = da;
+        else throw Error("Cannot broadcast dimensions " + std::to_string(da) + " and " + std::to_string(db));
+    }
+    return out;
+}
+
+// Element strides of an operand's matrices along the output batch axes
+// (calculate_batch_offset_with_broadcast, matmul/mod.rs:764-820): 0 where the
+// operand has size 1 or lacks the axis.
+std::vector<size_t> batch_strides(const std::vector<size_t> &dims, const std::vector<size_t> &out_batch) {
+    const size_t nb = dims.size() - 2, q = out_batch.size();
+    std::vector<size_t> st(q, 0);
+    size_t stride = dims[nb] * dims[nb + 1];
+    for (size_t j = nb; j-- > 0;) {
+        st[j + (q - nb)] = dims[j] == 1 ? 0 : stride;
+        stride *= dims[j];
+    }
+    return st;
+}
+
+// C[out_batch..., Mo, No] = op(A) . op(B) batch by batch; A and B carry their
+// own (possibly broadcast) batch axes.
+Tensor batched_gemm(int ta, int tb, const float *A, const std::vector<size_t> &adims, const float *B,
+                    const std::vector<size_t> &bdims, const std::vector<size_t> &out_batch, size_t Mo, size_t No,
+                    size_t Kc) {
+    if (out_batch.size() > 6) throw Error("batched matmul supports up to 6 batch axes");
+    std::vector<size_t> odims = out_batch;
+    odims.push_back(Mo);
+    odims.push_back(No);
+    Tensor out = Tensor::new_uninit(odims);
+    const std::vector<size_t> sa = batch_strides(adims, out_batch), sb = batch_strides(bdims, out_batch);
+    const size_t lda = adims.back(), ldb = bdims.back();
+    size_t batches = 1;
+    for (size_t d : out_batch) batches *= d;
+    if (out.size())
+        launch(KernelClass::Gemm, 2.0 * Mo * No * Kc * batches, "ts_hip_gemm_batched", [&] {
+            return ts_hip_gemm_batched(ta, tb, Mo, No, Kc, A, lda, B, ldb, out.dev_mut(), No, out_batch.size(),
+                                       out_batch.data(), sa.data(), sb.data(), Mo * No, S());
+        });
+    return out;
+}
+
+Tensor gemv(int trans, const float *A, size_t rows, size_t cols, const float *x) {
+    Tensor y = Tensor::new_uninit({trans ? cols : rows});
+    const size_t ws = ts_hip_gemv_workspace_floats(trans, rows, cols);
+    std::unique_ptr<Allocation> work = ws ? std::make_unique<Allocation>(ws) : nullptr;
+    launch(trans ? KernelClass::Reduction : KernelClass::Elementwise, 4.0 * rows * cols + 4.0 * (rows + cols),
+           "ts_hip_gemv", [&] {
+               return ts_hip_gemv(trans, rows, cols, A, cols, x, y.dev_mut(), work ? work->ptr : nullptr, ws, S());
+           });
+    return y;
+}
+
+Tensor outer(const float *a, size_t m, const float *b, size_t n) {
+    Tensor out = Tensor::new_uninit({m, n});
+    launch(KernelClass::Elementwise, 4.0 * (m * n + m + n), "ts_hip_outer",
+           [&] { return ts_hip_outer(a, m, b, n, out.dev_mut(), S()); });
+    return out;
+}
+
+}  // namespace
+
+// ops/matmul/mod.rs:263-310: dispatch on the ranks -- 1D.1D dot, 1D.2D and
+// 2D.1D vector products, 2D.2D, and batched N-D with broadcast batch axes.
 Tensor Tensor::matmul(const Tensor &o) const {
-    if (dims_.size() != 2 || o.dims_.size() != 2)
-        throw Error("matmul: the device path implements 2D @ 2D; got " + dims_str(dims_) + " @ " +
-                    dims_str(o.dims_));
-    const size_t m = dims_[0], k = dims_[1], n = o.dims_[1];
-    if (k != o.dims_[0])  // ops/matmul/mod.rs:577-583
-        throw Error("Inner dimensions must match: " + std::to_string(k) + " vs " +
-                    std::to_string(o.dims_[0]));
-    Tensor out = new_uninit({m, n});
-    launch(KernelClass::Gemm, 2.0 * m * n * k, "ts_hip_gemm", [&] {
-        return ts_hip_gemm(0, 0, m, n, k, dev(), k, o.dev(), n, out.dev_mut(), n, S());
-    });
+    const size_t ra = dims_.size(), rb = o.dims_.size();
+    Tensor out;
+    if (ra == 1 && rb == 1) {  // dot_product_1d (:310-350): a scalar of shape []
+        if (dims_[0] != o.dims_[0]) throw Error("Tensors must have same length for dot product");
+        out = new_uninit({});
+        const size_t ws = ts_hip_sum_workspace_floats(size_);
+        Allocation work(ws);
+        launch(KernelClass::Reduction, 8.0 * size_ + 4.0, "ts_hip_dot",
+               [&] { return ts_hip_dot(dev(), o.dev(), size_, out.dev_mut(), work.ptr, ws, S()); });
+    } else if (ra == 1 && rb == 2) {  // vector_matrix_mult (:352-420)
+        if (dims_[0] != o.dims_[0]) throw Error("Vector length must match matrix rows");
+        out = gemv(1, o.dev(), o.dims_[0], o.dims_[1], dev());
+    } else if (ra == 2 && rb == 1) {  // matrix_vector_mult (:488-560)
+        if (dims_[1] != o.dims_[0]) throw Error("Matrix columns must match vector length");
+        out = gemv(0, dev(), dims_[0], dims_[1], o.dev());
+    } else if (ra == 2 && rb == 2) {  // matrix_matrix_mult (:572-611)
+        const size_t m = dims_[0], k = dims_[1], n = o.dims_[1];
+        if (k != o.dims_[0])
+            throw Error("Inner dimensions must match: " + std::to_string(k) + " vs " + std::to_string(o.dims_[0]));
+        out = new_uninit({m, n});
+        launch(KernelClass::Gemm, 2.0 * m * n * k, "ts_hip_gemm", [&] {
+            return ts_hip_gemm(0, 0, m, n, k, dev(), k, o.dev(), n, out.dev_mut(), n, S());
+        });
+    } else {  // batched_matmul (:634-760)
+        if (ra < 2 || rb < 2) throw Error("Batched matmul requires at least 2D tensors");
+        const size_t m = dims_[ra - 2], k = dims_[ra - 1], k2 = o.dims_[rb - 2], n = o.dims_[rb - 1];
+        if (k != k2)
+            throw Error("Inner dimensions must match for batched matmul: " + std::to_string(k) + " vs " +
+                        std::to_string(k2));
+        out = batched_gemm(0, 0, dev(), dims_, o.dev(), o.dims_, matmul_batch_dims(dims_, o.dims_), m, n, k);
+    }
     if ((requires_grad_ || o.requires_grad_) && is_grad_enabled()) {
         GradFn fn{GradFn::Kind::MatMul};
         fn.saved = {saved(), o.saved()};
@@ -724,27 +818,47 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
             r.emplace_back(std::move(g));
             break;
         }
-        case K::MatMul: {  // grad_fn/ops/matmul.rs:68-80, transposes folded into the loads
+        case K::MatMul: {  // grad_fn/ops/matmul.rs:4-219, transposes folded into the loads
             const SavedTensor &a = saved[0], &b = saved[1];
-            const size_t M = a.dims[0], Kd = a.dims[1], N = b.dims[1];
-            if (req_left) {  // go[M,N] . b[Kd,N]^T -> [M,Kd]
-                Tensor gl = Tensor::new_uninit({M, Kd});
-                launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm(dX)", [&] {
-                    return ts_hip_gemm(0, 1, M, Kd, N, go.dev(), N, b.ptr(), N, gl.dev_mut(), Kd, S());
-                });
-                r.emplace_back(std::move(gl));
-            } else {
-                r.emplace_back(std::nullopt);
+            const size_t ra = a.dims.size(), rb = b.dims.size();
+            std::optional<Tensor> gl, gr;
+            if (ra == 1 && rb == 1) {  // (1,1): go * b, go * a with the scalar go broadcast
+                const size_t len = a.dims[0];
+                Tensor gob = bcast_to(go.dev(), go.dims(), {len});
+                if (req_left) gl = same_shape(gob.dev(), b.ptr(), {len}, 2);
+                if (req_right) gr = same_shape(gob.dev(), a.ptr(), {len}, 2);
+            } else if (ra == 1 && rb == 2) {  // (1,2): go . M^T, outer(v, go)
+                if (req_left) gl = gemv(0, b.ptr(), b.dims[0], b.dims[1], go.dev());
+                if (req_right) gr = outer(a.ptr(), a.dims[0], go.dev(), go.size());
+            } else if (ra == 2 && rb == 1) {  // (2,1): outer(go, v), M^T . go
+                if (req_left) gl = outer(go.dev(), go.size(), b.ptr(), b.dims[0]);
+                if (req_right) gr = gemv(1, a.ptr(), a.dims[0], a.dims[1], go.dev());
+            } else if (ra == 2 && rb == 2) {
+                const size_t M = a.dims[0], Kd = a.dims[1], N = b.dims[1];
+                if (req_left) {  // go[M,N] . b[Kd,N]^T -> [M,Kd]
+                    Tensor t = Tensor::new_uninit({M, Kd});
+                    launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm(dX)", [&] {
+                        return ts_hip_gemm(0, 1, M, Kd, N, go.dev(), N, b.ptr(), N, t.dev_mut(), Kd, S());
+                    });
+                    gl = std::move(t);
+                }
+                if (req_right) {  // a[M,Kd]^T . go[M,N] -> [Kd,N]
+                    Tensor t = Tensor::new_uninit({Kd, N});
+                    launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm(dW)", [&] {
+                        return ts_hip_gemm(1, 0, Kd, N, M, a.ptr(), Kd, go.dev(), N, t.dev_mut(), N, S());
+                    });
+                    gr = std::move(t);
+                }
+            } else {  // batched (:150-219): go . B^T and A^T . go per batch, reduced to the operand shapes
+                const size_t M = a.dims[ra - 2], Kd = a.dims[ra - 1], N = b.dims[rb - 1];
+                const std::vector<size_t> ob = matmul_batch_dims(a.dims, b.dims);
+                if (req_left)
+                    gl = reduce_to(batched_gemm(0, 1, go.dev(), go.dims(), b.ptr(), b.dims, ob, M, Kd, N), a.dims);
+                if (req_right)
+                    gr = reduce_to(batched_gemm(1, 0, a.ptr(), a.dims, go.dev(), go.dims(), ob, Kd, N, M), b.dims);
             }
-            if (req_right) {  // a[M,Kd]^T . go[M,N] -> [Kd,N]
-                Tensor gr = Tensor::new_uninit({Kd, N});
-                launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm(dW)", [&] {
-                    return ts_hip_gemm(1, 0, Kd, N, M, a.ptr(), Kd, go.dev(), N, gr.dev_mut(), N, S());
-                });
-                r.emplace_back(std::move(gr));
-            } else {
-                r.emplace_back(std::nullopt);
-            }
+            r.emplace_back(std::move(gl));
+            r.emplace_back(std::move(gr));
             break;
         }
         case K::Exp: {  // grad_fn/ops/exp.rs: go * y

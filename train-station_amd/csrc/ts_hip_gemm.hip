@@ -40,6 +40,8 @@ constexpr int kXcds = 8;
 // Column swizzle of LDS row k: bit 4 from the k-quad, bit 5 from k's parity.
 __device__ __forceinline__ int swz(int k) { return (((k >> 2) & 3) << 4) ^ ((k & 1) << 5); }
 
+constexpr int kMaxBatchRank = 6;
+
 struct GemmArgs {
     const float *A;
     const float *B;
@@ -47,6 +49,15 @@ struct GemmArgs {
     int M, N, K, lda, ldb, ldc;
     int tiles_m, tiles_n;
     int vec;  // both operands 16-byte aligned with leading dimensions % 4 == 0
+    // Batched form (batch_rank > 0): workgroup b computes tile b % tiles of
+    // batch b / tiles; a batch's coordinates (row-major over bdims) select
+    // A + sum(c_k * sa[k]) and B + sum(c_k * sb[k]) (0 strides on broadcast
+    // axes), and C + batch * sc.
+    int batch_rank;
+    int tiles;  // tiles_m * tiles_n
+    int bdims[kMaxBatchRank];
+    long long sa[kMaxBatchRank], sb[kMaxBatchRank];
+    long long sc;
 };
 
 // Staging of one operand tile: logical [BK][R] (k-major), R = 128 or 256
@@ -120,10 +131,9 @@ struct Stage {
     }
 };
 
-// Tile coordinates of this workgroup (see the file comment).
-__device__ inline void tile_coords(int tiles_m, int tiles_n, int &tm, int &tn) {
+// Tile coordinates of workgroup b of a G-tile grid (see the file comment).
+__device__ inline void tile_coords(int tiles_m, int tiles_n, int b, int &tm, int &tn) {
     const int G = tiles_m * tiles_n;
-    const int b = blockIdx.x;
     const int xcd = b % kXcds;
     int prefix = 0;
     for (int y = 0; y < xcd; ++y) prefix += (G - y + kXcds - 1) / kXcds;
@@ -148,8 +158,31 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
     __shared__ float As[2][kBK * BM];
     __shared__ float Bs[2][kBK * BN];
 
+    // Batched form: select this workgroup's batch (uniform).  The loop is
+    // unrolled with constant indices so the argument arrays stay in SGPRs.
+    const float *Ap = g.A, *Bp = g.B;
+    float *Cp = g.C;
+    int bid = blockIdx.x;
+    if (g.batch_rank > 0) {
+        const int batch = bid / g.tiles;
+        bid -= batch * g.tiles;
+        int rem = batch;
+        long long oa = 0, ob = 0;
+#pragma unroll
+        for (int k = kMaxBatchRank - 1; k >= 0; --k) {
+            if (k < g.batch_rank) {
+                const int c = rem % g.bdims[k];
+                rem /= g.bdims[k];
+                oa += c * g.sa[k];
+                ob += c * g.sb[k];
+            }
+        }
+        Ap += oa;
+        Bp += ob;
+        Cp += static_cast<long long>(batch) * g.sc;
+    }
     int tm, tn;
-    tile_coords(g.tiles_m, g.tiles_n, tm, tn);
+    tile_coords(g.tiles_m, g.tiles_n, bid, tm, tn);
     const int i0 = tm * BM, j0 = tn * BN;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / WN, wn = wave % WN;
@@ -168,11 +201,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
     float4 ra[SA::NF], rb[SB::NF];
     auto load = [&](int k0) {
         if (mn_inside && k0 + kBK <= g.K) {  // uniform across the workgroup
-            SA::load_fast(g.A, g.lda, i0, k0, ra);
-            SB::load_fast(g.B, g.ldb, j0, k0, rb);
+            SA::load_fast(Ap, g.lda, i0, k0, ra);
+            SB::load_fast(Bp, g.ldb, j0, k0, rb);
         } else {
-            SA::load_guarded(g.A, g.lda, g.M, g.K, i0, k0, ra);
-            SB::load_guarded(g.B, g.ldb, g.N, g.K, j0, k0, rb);
+            SA::load_guarded(Ap, g.lda, g.M, g.K, i0, k0, ra);
+            SB::load_guarded(Bp, g.ldb, g.N, g.K, j0, k0, rb);
         }
     };
 
@@ -228,17 +261,18 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int i = i0 + wm * TMW + a * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-                if (i < g.M && j < g.N) g.C[(size_t)i * g.ldc + j] = acc[a][b][r];
+                if (i < g.M && j < g.N) Cp[(size_t)i * g.ldc + j] = acc[a][b][r];
             }
         }
     }
 }
 
 template <int BM, int BN, int WM, int WN>
-static void launch_tiles(int ta, int tb, GemmArgs g, hipStream_t s) {
+static void launch_tiles(int ta, int tb, GemmArgs g, hipStream_t s, unsigned batches = 1) {
     g.tiles_m = (g.M + BM - 1) / BM;
     g.tiles_n = (g.N + BN - 1) / BN;
-    dim3 grid(static_cast<unsigned>(g.tiles_m) * static_cast<unsigned>(g.tiles_n));
+    g.tiles = g.tiles_m * g.tiles_n;
+    dim3 grid(static_cast<unsigned>(g.tiles) * batches);
     dim3 block(64 * WM * WN);
     if (!ta && !tb) hipLaunchKernelGGL((gemm_f32_mfma<false, false, BM, BN, WM, WN>), grid, block, 0, s, g);
     else if (!ta && tb) hipLaunchKernelGGL((gemm_f32_mfma<false, true, BM, BN, WM, WN>), grid, block, 0, s, g);
@@ -250,6 +284,33 @@ static void launch_tiles(int ta, int tb, GemmArgs g, hipStream_t s) {
 
 using namespace tship;
 
+// Argument checks and kernel selection shared by the plain and batched forms.
+static int gemm_launch(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A, size_t lda,
+                       const float *B, size_t ldb, float *C, size_t ldc, GemmArgs g, size_t batches,
+                       void *stream) {
+    if (!A || !B) return TS_HIP_EINVAL;
+    if (lda < (trans_a ? M : K) || ldb < (trans_b ? K : N)) return TS_HIP_EINVAL;
+    // dimensions and leading dimensions are 32-bit inside the kernel (element
+    // offsets are formed in 64 bits), and the workgroup count must fit one grid
+    const size_t lim = 0x7ffffe00ULL;  // room for i0 + BM within int
+    if (M > lim || N > lim || K > lim || lda > lim || ldb > lim || ldc > lim) return TS_HIP_EINVAL;
+    if (((M + 127) / 128) * ((N + 127) / 128) * batches > 0x7fffffffULL) return TS_HIP_EINVAL;
+    g.A = A; g.B = B; g.C = C;
+    g.M = static_cast<int>(M); g.N = static_cast<int>(N); g.K = static_cast<int>(K);
+    g.lda = static_cast<int>(lda); g.ldb = static_cast<int>(ldb); g.ldc = static_cast<int>(ldc);
+    g.tiles_m = g.tiles_n = 0;
+    bool strides4 = true;
+    for (int k = 0; k < g.batch_rank; ++k) strides4 = strides4 && g.sa[k] % 4 == 0 && g.sb[k] % 4 == 0;
+    g.vec = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) && strides4;
+    hipStream_t s = as_stream(stream);
+    // 256x256 tiles once they alone fill every CU; 128x128 below that.
+    const size_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batches;
+    const unsigned nb = static_cast<unsigned>(batches);
+    if (big_tiles >= static_cast<size_t>(device_cu_count())) launch_tiles<256, 256, 2, 4>(trans_a, trans_b, g, s, nb);
+    else launch_tiles<128, 128, 2, 2>(trans_a, trans_b, g, s, nb);
+    return launch_status();
+}
+
 extern "C" int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
                            size_t lda, const float *B, size_t ldb, float *C, size_t ldc,
                            void *stream) {
@@ -259,25 +320,35 @@ extern "C" int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t 
         if (ldc != N) return TS_HIP_EINVAL;
         return ts_hip_fill(C, 0.0f, M * N, stream);
     }
-    if (!A || !B) return TS_HIP_EINVAL;
-    if (lda < (trans_a ? M : K) || ldb < (trans_b ? K : N)) return TS_HIP_EINVAL;
-    // dimensions and leading dimensions are 32-bit inside the kernel (element
-    // offsets are formed in 64 bits), and the tile count must fit one grid
-    const size_t lim = 0x7ffffe00ULL;  // room for i0 + BM within int
-    if (M > lim || N > lim || K > lim || lda > lim || ldb > lim || ldc > lim) return TS_HIP_EINVAL;
-    if (((M + 127) / 128) * ((N + 127) / 128) > 0x7fffffffULL) return TS_HIP_EINVAL;
-    GemmArgs g;
-    g.A = A; g.B = B; g.C = C;
-    g.M = static_cast<int>(M); g.N = static_cast<int>(N); g.K = static_cast<int>(K);
-    g.lda = static_cast<int>(lda); g.ldb = static_cast<int>(ldb); g.ldc = static_cast<int>(ldc);
-    g.tiles_m = g.tiles_n = 0;
-    g.vec = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0);
-    hipStream_t s = as_stream(stream);
-    // 256x256 tiles once they alone fill every CU; 128x128 below that.
-    const size_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256);
-    if (big_tiles >= static_cast<size_t>(device_cu_count())) launch_tiles<256, 256, 2, 4>(trans_a, trans_b, g, s);
-    else launch_tiles<128, 128, 2, 2>(trans_a, trans_b, g, s);
-    return launch_status();
+    GemmArgs g{};
+    return gemm_launch(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, g, 1, stream);
+}
+
+extern "C" int ts_hip_gemm_batched(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
+                                   size_t lda, const float *B, size_t ldb, float *C, size_t ldc,
+                                   size_t batch_rank, const size_t *batch_dims, const size_t *a_batch_strides,
+                                   const size_t *b_batch_strides, size_t c_batch_stride, void *stream) {
+    if (batch_rank > static_cast<size_t>(kMaxBatchRank)) return TS_HIP_EINVAL;
+    if (batch_rank && (!batch_dims || !a_batch_strides || !b_batch_strides)) return TS_HIP_EINVAL;
+    size_t batches = 1;
+    for (size_t k = 0; k < batch_rank; ++k) batches *= batch_dims[k];
+    if (M == 0 || N == 0 || batches == 0) return TS_HIP_OK;
+    if (!C || ldc < N || c_batch_stride < (M - 1) * ldc + N) return TS_HIP_EINVAL;
+    if (K == 0) {  // empty contraction: every C batch = 0
+        if (ldc != N || c_batch_stride != M * N) return TS_HIP_EINVAL;
+        return ts_hip_fill(C, 0.0f, batches * M * N, stream);
+    }
+    if (batches > 0x7fffffffULL) return TS_HIP_EINVAL;
+    GemmArgs g{};
+    g.batch_rank = static_cast<int>(batch_rank);
+    for (size_t k = 0; k < batch_rank; ++k) {
+        if (batch_dims[k] > 0x7fffffffULL) return TS_HIP_EINVAL;
+        g.bdims[k] = static_cast<int>(batch_dims[k]);
+        g.sa[k] = static_cast<long long>(a_batch_strides[k]);
+        g.sb[k] = static_cast<long long>(b_batch_strides[k]);
+    }
+    g.sc = static_cast<long long>(c_batch_stride);
+    return gemm_launch(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, g, batches, stream);
 }
 
 extern "C" int ts_hip_matmul(const float *a, const float *b, float *c, size_t m, size_t n, size_t k,

@@ -35,4 +35,9 @@ inline unsigned grid_for(size_t units, size_t per_thread = 1) {
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Weighted column sums out[c] = sum_r w[r] * x[r][c] (w == nullptr: plain
+// column sums), f64 partials; workspace as ts_hip_sum_dim0_workspace_floats.
+int launch_colsum(const float *x, const float *w, size_t rows, size_t cols, size_t ld, float *out,
+                  float *workspace, size_t workspace_floats, void *stream);
+
 }  // namespace tship

@@ -39,18 +39,27 @@ __device__ inline double block_sum(double v) {
 }
 
 // Pass 1: workgroup b sums the float4 groups b, b+G, b+2G, ... (all threads
-// of the grid stride together) and writes one f64 partial.
-__global__ __launch_bounds__(kBlock) void sum_partial(const float *__restrict__ x, size_t n,
-                                                      size_t n4, double *__restrict__ partial) {
+// of the grid stride together) and writes one f64 partial.  PROD: the terms
+// are x[i] * y[i] formed in f64 (a dot product).
+template <bool PROD>
+__global__ __launch_bounds__(kBlock) void sum_partial(const float *__restrict__ x, const float *__restrict__ y,
+                                                      size_t n, size_t n4, double *__restrict__ partial) {
     const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
     const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
     double acc = 0.0;
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    const float4 *y4 = reinterpret_cast<const float4 *>(y);
     for (size_t v = t; v < n4; v += stride) {
-        float4 q = x4[v];
-        acc += (double)q.x + (double)q.y + (double)q.z + (double)q.w;
+        const float4 q = x4[v];
+        if (PROD) {
+            const float4 r = y4[v];
+            acc += (double)q.x * (double)r.x + (double)q.y * (double)r.y + (double)q.z * (double)r.z +
+                   (double)q.w * (double)r.w;
+        } else {
+            acc += (double)q.x + (double)q.y + (double)q.z + (double)q.w;
+        }
     }
-    for (size_t i = 4 * n4 + t; i < n; i += stride) acc += (double)x[i];
+    for (size_t i = 4 * n4 + t; i < n; i += stride) acc += PROD ? (double)x[i] * (double)y[i] : (double)x[i];
     double r = block_sum(acc);
     if (threadIdx.x == 0) partial[blockIdx.x] = r;
 }
@@ -70,7 +79,7 @@ __global__ __launch_bounds__(kBlock) void sum_final(const double *__restrict__ p
 }
 
 template <bool MEAN>
-static int launch_sum(const float *x, size_t n, float *out, float *workspace, size_t ws,
+static int launch_sum(const float *x, const float *y, size_t n, float *out, float *workspace, size_t ws,
                       void *stream) {
     if (!out) return TS_HIP_EINVAL;
     hipStream_t s = as_stream(stream);
@@ -82,9 +91,13 @@ static int launch_sum(const float *x, size_t n, float *out, float *workspace, si
     if (!workspace || ws < 2 * blocks) return TS_HIP_EWORKSPACE;
     if ((reinterpret_cast<uintptr_t>(workspace) & 7u) != 0) return TS_HIP_EINVAL;
     double *partial = reinterpret_cast<double *>(workspace);
-    size_t n4 = aligned16(x) ? n / 4 : 0;
-    hipLaunchKernelGGL(sum_partial, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, n,
-                       n4, partial);
+    size_t n4 = (aligned16(x) && (!y || aligned16(y))) ? n / 4 : 0;
+    if (y)
+        hipLaunchKernelGGL(sum_partial<true>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, y, n,
+                           n4, partial);
+    else
+        hipLaunchKernelGGL(sum_partial<false>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, y, n,
+                           n4, partial);
     int st = launch_status();
     if (st) return st;
     hipLaunchKernelGGL(sum_final<MEAN>, dim3(1), dim3(kBlock), 0, s, partial, blocks, n, out);
@@ -109,9 +122,10 @@ static size_t dim0_chunks(size_t rows, size_t cols) {
     return c < 1 ? 1 : c;
 }
 
-template <bool VEC>
-__global__ __launch_bounds__(kBlock) void dim0_partial(const float *__restrict__ x, size_t rows,
-                                                       size_t cols, size_t rows_per_chunk,
+// W: row r is weighted by w[r] (in f64) -- a transposed matrix-vector product.
+template <bool VEC, bool W>
+__global__ __launch_bounds__(kBlock) void dim0_partial(const float *__restrict__ x, const float *__restrict__ w,
+                                                       size_t rows, size_t cols, size_t rows_per_chunk,
                                                        double *__restrict__ partial) {
     const size_t groups = VEC ? cols / 4 : cols;
     const size_t gcol = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
@@ -127,14 +141,17 @@ __global__ __launch_bounds__(kBlock) void dim0_partial(const float *__restrict__
         for (; r + 4 <= r1; r += 4) {   // four independent loads in flight per thread
             const float4 q0 = x4[(r + 0) * groups + gcol], q1 = x4[(r + 1) * groups + gcol];
             const float4 q2 = x4[(r + 2) * groups + gcol], q3 = x4[(r + 3) * groups + gcol];
-            a0 += (double)q0.x; a1 += (double)q0.y; a2 += (double)q0.z; a3 += (double)q0.w;
-            a0 += (double)q1.x; a1 += (double)q1.y; a2 += (double)q1.z; a3 += (double)q1.w;
-            a0 += (double)q2.x; a1 += (double)q2.y; a2 += (double)q2.z; a3 += (double)q2.w;
-            a0 += (double)q3.x; a1 += (double)q3.y; a2 += (double)q3.z; a3 += (double)q3.w;
+            const double w0 = W ? (double)w[r] : 1.0, w1 = W ? (double)w[r + 1] : 1.0;
+            const double w2 = W ? (double)w[r + 2] : 1.0, w3 = W ? (double)w[r + 3] : 1.0;
+            a0 += w0 * q0.x; a1 += w0 * q0.y; a2 += w0 * q0.z; a3 += w0 * q0.w;
+            a0 += w1 * q1.x; a1 += w1 * q1.y; a2 += w1 * q1.z; a3 += w1 * q1.w;
+            a0 += w2 * q2.x; a1 += w2 * q2.y; a2 += w2 * q2.z; a3 += w2 * q2.w;
+            a0 += w3 * q3.x; a1 += w3 * q3.y; a2 += w3 * q3.z; a3 += w3 * q3.w;
         }
         for (; r < r1; ++r) {
             const float4 q = x4[r * groups + gcol];
-            a0 += (double)q.x; a1 += (double)q.y; a2 += (double)q.z; a3 += (double)q.w;
+            const double wr = W ? (double)w[r] : 1.0;
+            a0 += wr * q.x; a1 += wr * q.y; a2 += wr * q.z; a3 += wr * q.w;
         }
         out[4 * gcol + 0] = a0;
         out[4 * gcol + 1] = a1;
@@ -142,7 +159,7 @@ __global__ __launch_bounds__(kBlock) void dim0_partial(const float *__restrict__
         out[4 * gcol + 3] = a3;
     } else {
         double acc = 0.0;
-        for (size_t r = r0; r < r1; ++r) acc += (double)x[r * cols + gcol];
+        for (size_t r = r0; r < r1; ++r) acc += (W ? (double)w[r] : 1.0) * (double)x[r * cols + gcol];
         out[gcol] = acc;
     }
 }
@@ -169,6 +186,34 @@ __global__ __launch_bounds__(kBlock) void dim0_final(const double *__restrict__ 
     }
 }
 
+// out[c] = sum_r w[r] * x[r][c] (w == nullptr: plain column sums) for a
+// row-major [rows, cols] matrix with leading dimension ld.
+int launch_colsum(const float *x, const float *w, size_t rows, size_t cols, size_t ld, float *out,
+                  float *workspace, size_t workspace_floats, void *stream) {
+    if (cols == 0) return TS_HIP_OK;
+    if (!out) return TS_HIP_EINVAL;
+    if (rows == 0) return ts_hip_fill(out, 0.0f, cols, stream);
+    if (!x || ld != cols) return TS_HIP_EINVAL;
+    const size_t chunks = dim0_chunks(rows, cols);
+    if (!workspace || workspace_floats < 2 * chunks * cols) return TS_HIP_EWORKSPACE;
+    if ((reinterpret_cast<uintptr_t>(workspace) & 7u) != 0) return TS_HIP_EINVAL;
+    const size_t rows_per_chunk = (rows + chunks - 1) / chunks;
+    double *partial = reinterpret_cast<double *>(workspace);
+    hipStream_t s = as_stream(stream);
+    const bool vec = (cols % 4 == 0) && aligned16(x);
+    const size_t groups = vec ? cols / 4 : cols;
+    dim3 grid1(static_cast<unsigned>((groups + kBlock - 1) / kBlock), static_cast<unsigned>(chunks));
+    if (vec && w) hipLaunchKernelGGL((dim0_partial<true, true>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
+    else if (vec) hipLaunchKernelGGL((dim0_partial<true, false>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
+    else if (w) hipLaunchKernelGGL((dim0_partial<false, true>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
+    else hipLaunchKernelGGL((dim0_partial<false, false>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
+    int st = launch_status();
+    if (st) return st;
+    hipLaunchKernelGGL(dim0_final, dim3(static_cast<unsigned>((cols + 63) / 64)), dim3(kBlock), 0, s,
+                       partial, chunks, cols, out);
+    return launch_status();
+}
+
 }  // namespace tship
 
 using namespace tship;
@@ -179,12 +224,12 @@ size_t ts_hip_sum_workspace_floats(size_t n) { return 2 * sum_blocks(n); }
 
 int ts_hip_sum(const float *x, size_t n, float *out, float *workspace, size_t workspace_floats,
                void *stream) {
-    return launch_sum<false>(x, n, out, workspace, workspace_floats, stream);
+    return launch_sum<false>(x, nullptr, n, out, workspace, workspace_floats, stream);
 }
 
 int ts_hip_mean(const float *x, size_t n, float *out, float *workspace, size_t workspace_floats,
                 void *stream) {
-    return launch_sum<true>(x, n, out, workspace, workspace_floats, stream);
+    return launch_sum<true>(x, nullptr, n, out, workspace, workspace_floats, stream);
 }
 
 size_t ts_hip_sum_dim0_workspace_floats(size_t rows, size_t cols) {
@@ -193,26 +238,13 @@ size_t ts_hip_sum_dim0_workspace_floats(size_t rows, size_t cols) {
 
 int ts_hip_sum_dim0(const float *x, size_t rows, size_t cols, float *out, float *workspace,
                     size_t workspace_floats, void *stream) {
-    if (cols == 0) return TS_HIP_OK;
-    if (!out) return TS_HIP_EINVAL;
-    if (rows == 0) return ts_hip_fill(out, 0.0f, cols, stream);
-    if (!x) return TS_HIP_EINVAL;
-    const size_t chunks = dim0_chunks(rows, cols);
-    if (!workspace || workspace_floats < 2 * chunks * cols) return TS_HIP_EWORKSPACE;
-    if ((reinterpret_cast<uintptr_t>(workspace) & 7u) != 0) return TS_HIP_EINVAL;
-    const size_t rows_per_chunk = (rows + chunks - 1) / chunks;
-    double *partial = reinterpret_cast<double *>(workspace);
-    hipStream_t s = as_stream(stream);
-    const bool vec = (cols % 4 == 0) && aligned16(x);
-    const size_t groups = vec ? cols / 4 : cols;
-    dim3 grid1(static_cast<unsigned>((groups + kBlock - 1) / kBlock), static_cast<unsigned>(chunks));
-    if (vec) hipLaunchKernelGGL(dim0_partial<true>, grid1, dim3(kBlock), 0, s, x, rows, cols, rows_per_chunk, partial);
-    else hipLaunchKernelGGL(dim0_partial<false>, grid1, dim3(kBlock), 0, s, x, rows, cols, rows_per_chunk, partial);
-    int st = launch_status();
-    if (st) return st;
-    hipLaunchKernelGGL(dim0_final, dim3(static_cast<unsigned>((cols + 63) / 64)), dim3(kBlock), 0, s,
-                       partial, chunks, cols, out);
-    return launch_status();
+    return launch_colsum(x, nullptr, rows, cols, cols, out, workspace, workspace_floats, stream);
+}
+
+int ts_hip_dot(const float *a, const float *b, size_t n, float *out, float *workspace, size_t workspace_floats,
+               void *stream) {
+    if (n && !b) return TS_HIP_EINVAL;
+    return launch_sum<false>(a, b, n, out, workspace, workspace_floats, stream);
 }
 
 }  // extern "C"
