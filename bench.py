@@ -268,7 +268,7 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
-                     "kernel": "gemm_f32_mfma (all 3 layouts, every launch of the timed region)",
+                     "kernel": "gemm_f32_lds_dma (all 3 layouts, every launch of the timed region)",
                      "flop_per_launch": per_launch_flops,
                      "avg_launch_ms": round(g["ms"] / g["launches"], 4) if g["launches"] else None},
         "kernels": kernels,

@@ -237,6 +237,18 @@ def test_gemm_full_size_sampled_rows(oracle, ta, tb, M, N, K):
     assert max_rel(got, want) <= 1e-4
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(4100, 4100, 100), (4100, 4097, 103), (4096, 4096, 9), (100, 65536, 64),
+                                   (65536, 100, 40)])
+def test_gemm_large_grid_edges(oracle, ta, tb, M, N, K):
+    # enough 256x256 tiles to fill the chip: aligned layouts take the LDS-DMA
+    # kernel (clamped edge rows, a partial last k tile, K < 16), the others the
+    # register-staged one; f64 check on sampled rows, always including the last
+    print(f"[gemm grid] ta={ta} tb={tb} M={M} N={N} K={K}", flush=True)
+    got, want = _gemm_case(oracle, bool(ta), bool(tb), M, N, K, seed=11, check_rows=16)
+    assert max_rel(got, want) <= 1e-4
+
+
 def test_gemm_rejects_bad_leading_dimension():
     d = Dev(64)
     assert hip.ts_hip_gemm(0, 0, 8, 8, 8, d.ptr, 4, d.ptr, 8, d.ptr, 8, None) == 100001

@@ -36,7 +36,7 @@ def _T():
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
 @pytest.mark.parametrize("bshape_a,bshape_b,M,N,K", [
     ((3,), (3,), 64, 48, 40), ((2, 1), (1, 5), 33, 17, 9), ((4,), (1,), 130, 257, 129),
-    ((2, 3), (2, 3), 256, 256, 64), ((1,), (6,), 7, 300, 513)])
+    ((2, 3), (2, 3), 256, 256, 64), ((1,), (6,), 7, 300, 513), ((4, 1), (1, 4), 1024, 1000, 72)])
 def test_gemm_batched_against_f64(ta, tb, bshape_a, bshape_b, M, N, K):
     from gpu_util import Dev, sync
     hip, check, SZ = _hip()

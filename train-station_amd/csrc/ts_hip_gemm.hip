@@ -27,6 +27,15 @@
 // round-robin over 8 XCDs, each with its own L2) receives a contiguous run of
 // tiles, ordered in groups of 8 tile-rows so neighbouring tiles share A rows
 // and B columns in that L2.
+//
+// Large aligned problems (both operands 16-byte aligned, leading dimensions
+// % 4 == 0, enough 256x256 tiles to fill the chip) take gemm_f32_lds_dma
+// instead: operand tiles go from global memory straight into LDS with
+// global_load_lds_dwordx4 (no VGPR staging, no ds_write), and the MFMA
+// operands of the next two k-steps are read from LDS while the MFMAs of the
+// current two run, across tile boundaries too.  Its k order per MFMA differs
+// (k of step s, lane half h = 4*(s/2) + 2h + s%2) so that a k-contiguous
+// operand gives two steps' values in one 8-byte LDS read.
 #include "ts_hip_internal.h"
 
 namespace tship {
@@ -280,6 +289,253 @@ static void launch_tiles(int ta, int tb, GemmArgs g, hipStream_t s, unsigned bat
     else hipLaunchKernelGGL((gemm_f32_mfma<true, true, BM, BN, WM, WN>), grid, block, 0, s, g);
 }
 
+
+// ---------------------------------------------------------------------------
+// LDS-DMA path.  A 256 x 16 operand tile is 1024 16-byte chunks; DMA
+// instruction i of wave w carries chunks (NI*w + i)*64 + lane (one 1 KB LDS
+// run per instruction: the LDS address is M0 + 16 * lane).
+//   KCONTIG: chunk rb*64 + kq*16 + r16 holds row 16*rb + r16, k 4kq .. 4kq+3
+//   else:    chunk k*64 + c holds k row k, columns 4*(c ^ dswz(k)) .. +3
+// The XOR puts the two k rows one MFMA operand read touches (k and k+2, lane
+// halves 0 and 1) in different halves of the bank space.
+typedef __attribute__((address_space(3))) void lds_void;
+typedef float f2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ int dswz(int k) { return ((k >> 1) & 1) << 3; }
+
+template <bool KCONTIG, int NW>
+struct DmaStage {
+    static constexpr int NI = kBK / NW;  // DMA instructions per wave and operand tile
+    static_assert(NI * NW == kBK, "waves must divide the 16 DMA instructions of a tile");
+
+    // Interior k tile.  Rows (columns) past the matrix edge are clamped to the
+    // last one: they only feed outputs that are never stored.
+    static __device__ __forceinline__ void dma(const float *__restrict__ P, int ld, int rows, int r0, int k0,
+                                               float *S, int wave, int lane) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int q = NI * wave + i;
+            const float *src;
+            if (KCONTIG) {
+                int row = r0 + q * 16 + (lane & 15);
+                row = row < rows ? row : rows - 1;
+                src = P + (size_t)row * ld + k0 + (lane >> 4) * 4;
+            } else {
+                const int last = (rows - 1) & ~3;  // ld % 4 == 0, so the chunk stays inside the row
+                int col = r0 + 4 * (lane ^ dswz(q));
+                col = col <= last ? col : last;
+                src = P + (size_t)(k0 + q) * ld + col;
+            }
+            // Issued as inline assembly: through the builtin the compiler makes
+            // every later LDS read wait for this load.  Completion is awaited
+            // explicitly (vmcnt) before the barrier that publishes the tile.
+            // M0 is listed as clobbered although the compiler treats it as
+            // reserved (and warns); nothing else in these kernels uses M0.
+            const unsigned lds = static_cast<unsigned>(reinterpret_cast<size_t>((lds_void *)(S + q * 256)));
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+            asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+                         : "memory", "m0");
+#pragma clang diagnostic pop
+        }
+    }
+
+    // Partial last k tile: element loads with bounds checks, zeros outside.
+    static __device__ __forceinline__ void guarded(const float *__restrict__ P, int ld, int rows, int K, int r0,
+                                                   int k0, float *S, int wave, int lane) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int q = NI * wave + i;
+            float v[4];
+            if (KCONTIG) {
+                const int row = r0 + q * 16 + (lane & 15), kk = k0 + (lane >> 4) * 4;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) v[c] = (row < rows && kk + c < K) ? P[(size_t)row * ld + kk + c] : 0.0f;
+            } else {
+                const int kr = k0 + q, col = r0 + 4 * (lane ^ dswz(q));
+#pragma unroll
+                for (int c = 0; c < 4; ++c) v[c] = (kr < K && col + c < rows) ? P[(size_t)kr * ld + col + c] : 0.0f;
+            }
+            *reinterpret_cast<float4 *>(S + q * 256 + lane * 4) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    }
+
+    // MFMA operand of steps 2j and 2j+1 for tile-local row (column) rho, lane
+    // half h.  An ext_vector pair, not HIP's float2 struct: reads through the
+    // struct type make the compiler wait for pending LDS DMA.
+    static __device__ __forceinline__ f2v frag(const float *S, int j, int h, int rho) {
+        if (KCONTIG) {
+            return *reinterpret_cast<const f2v *>(S + (((rho >> 4) * 64 + j * 16 + (rho & 15)) << 2) + 2 * h);
+        } else {
+            const int k = 4 * j + 2 * h;
+            const int o = (((rho >> 2) ^ dswz(k)) << 2) + (rho & 3);
+            f2v v;
+            v.x = S[k * 256 + o];
+            v.y = S[(k + 1) * 256 + o];
+            return v;
+        }
+    }
+};
+
+// 256x256 tiles, WM x WN waves.  SCHED 1 spreads the next step pair's LDS
+// reads over the current pair's MFMAs; SCHED 0 issues them as one group
+// ahead of the MFMAs (measured per layout, see the launcher).
+template <bool TA, bool TB, int WM, int WN, int SCHED>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_f32_lds_dma(GemmArgs g) {
+    constexpr int BM = 256, BN = 256, NW = WM * WN;
+    constexpr int TMW = BM / WM, TNW = BN / WN, FM = TMW / 32, FN = TNW / 32, PAIRS = kBK / 4;
+    using SA = DmaStage<!TA, NW>;
+    using SB = DmaStage<TB, NW>;
+    __shared__ __attribute__((aligned(16))) float As[2][kBK * BM];
+    __shared__ __attribute__((aligned(16))) float Bs[2][kBK * BN];
+
+    const float *Ap = g.A, *Bp = g.B;
+    float *Cp = g.C;
+    int bid = blockIdx.x;
+    if (g.batch_rank > 0) {
+        const int batch = bid / g.tiles;
+        bid -= batch * g.tiles;
+        int rem = batch;
+        long long oa = 0, ob = 0;
+#pragma unroll
+        for (int k = kMaxBatchRank - 1; k >= 0; --k) {
+            if (k < g.batch_rank) {
+                const int c = rem % g.bdims[k];
+                rem /= g.bdims[k];
+                oa += c * g.sa[k];
+                ob += c * g.sb[k];
+            }
+        }
+        Ap += oa;
+        Bp += ob;
+        Cp += static_cast<long long>(batch) * g.sc;
+    }
+    int tm, tn;
+    tile_coords(g.tiles_m, g.tiles_n, bid, tm, tn);
+    const int i0 = tm * BM, j0 = tn * BN;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    const int lrow = lane & 31, lhalf = lane >> 5;
+
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int a = 0; a < FM; ++a)
+#pragma unroll
+        for (int b = 0; b < FN; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+    const int nfull = g.K / kBK;  // whole k tiles; a partial one is done after the loop
+    auto dma = [&](int kt, int buf) {
+        SA::dma(Ap, g.lda, g.M, i0, kt * kBK, As[buf], wave, lane);
+        SB::dma(Bp, g.ldb, g.N, j0, kt * kBK, Bs[buf], wave, lane);
+    };
+    f2v F[2][FM + FN];
+    auto rd = [&](int buf, int j, f2v (&f)[FM + FN]) {
+#pragma unroll
+        for (int a = 0; a < FM; ++a) f[a] = SA::frag(As[buf], j, lhalf, wm * TMW + a * 32 + lrow);
+#pragma unroll
+        for (int b = 0; b < FN; ++b) f[FM + b] = SB::frag(Bs[buf], j, lhalf, wn * TNW + b * 32 + lrow);
+    };
+    auto mm = [&](const f2v (&f)[FM + FN]) {
+#pragma unroll
+        for (int a = 0; a < FM; ++a)
+#pragma unroll
+            for (int b = 0; b < FN; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(f[a].x, f[FM + b].x, acc[a][b], 0, 0, 0);
+#pragma unroll
+        for (int a = 0; a < FM; ++a)
+#pragma unroll
+            for (int b = 0; b < FN; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(f[a].y, f[FM + b].y, acc[a][b], 0, 0, 0);
+    };
+    auto order = [&]() {
+        if (SCHED == 1) {
+#pragma unroll
+            for (int i = 0; i < FM + FN; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 2 * FM * FN - (FM + FN), 0);
+        }
+    };
+
+    // Pipeline: LDS buffer kt&1 holds tile kt; tile kt+1 is in flight into the
+    // other buffer; the registers F[j&1] hold step pair j.  Each wave waits for
+    // its own DMA (vmcnt) before the barrier that publishes the tile.
+    if (nfull > 0) {
+        dma(0, 0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (nfull > 1) dma(1, 1);
+        rd(0, 0, F[0]);
+    }
+    for (int kt = 0; kt < nfull; ++kt) {
+        const int cur = kt & 1;
+#pragma unroll
+        for (int j = 0; j < PAIRS - 1; ++j) {
+            rd(cur, j + 1, F[(j + 1) & 1]);
+            if (SCHED == 0) __builtin_amdgcn_sched_barrier(0);
+            mm(F[j & 1]);
+            order();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        // Tile kt+1 is published and every read of buffer cur is done: read
+        // the next tile's first pair and start tile kt+2 into buffer cur, then
+        // run this tile's last pair.  On the last tiles the DMA repeats tile
+        // nfull-1 and the read takes an idle buffer: both stay in bounds.
+        rd(cur ^ 1, 0, F[0]);
+        dma(kt + 2 < nfull ? kt + 2 : nfull - 1, cur);
+        if (SCHED == 0) __builtin_amdgcn_sched_barrier(0);
+        mm(F[(PAIRS - 1) & 1]);
+        order();
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (nfull * kBK < g.K) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const int buf = nfull & 1;
+        SA::guarded(Ap, g.lda, g.M, g.K, i0, nfull * kBK, As[buf], wave, lane);
+        SB::guarded(Bp, g.ldb, g.N, g.K, j0, nfull * kBK, Bs[buf], wave, lane);
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < PAIRS; ++j) {
+            rd(buf, j, F[0]);
+            mm(F[0]);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA outstanding at exit
+
+#pragma unroll
+    for (int a = 0; a < FM; ++a) {
+#pragma unroll
+        for (int b = 0; b < FN; ++b) {
+            const int j = j0 + wn * TNW + b * 32 + lrow;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int i = i0 + wm * TMW + a * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+                if (i < g.M && j < g.N) Cp[(size_t)i * g.ldc + j] = acc[a][b][r];
+            }
+        }
+    }
+}
+
+template <int WM, int WN, int SCHED>
+static void launch_dma(int ta, int tb, GemmArgs g, hipStream_t s, unsigned batches) {
+    g.tiles_m = (g.M + 255) / 256;
+    g.tiles_n = (g.N + 255) / 256;
+    g.tiles = g.tiles_m * g.tiles_n;
+    dim3 grid(static_cast<unsigned>(g.tiles) * batches);
+    dim3 block(64 * WM * WN);
+    if (!ta && !tb) hipLaunchKernelGGL((gemm_f32_lds_dma<false, false, WM, WN, SCHED>), grid, block, 0, s, g);
+    else if (!ta && tb) hipLaunchKernelGGL((gemm_f32_lds_dma<false, true, WM, WN, SCHED>), grid, block, 0, s, g);
+    else if (ta && !tb) hipLaunchKernelGGL((gemm_f32_lds_dma<true, false, WM, WN, SCHED>), grid, block, 0, s, g);
+    else hipLaunchKernelGGL((gemm_f32_lds_dma<true, true, WM, WN, SCHED>), grid, block, 0, s, g);
+}
+
 }  // namespace tship
 
 using namespace tship;
@@ -306,8 +562,15 @@ static int gemm_launch(int trans_a, int trans_b, size_t M, size_t N, size_t K, c
     // 256x256 tiles once they alone fill every CU; 128x128 below that.
     const size_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batches;
     const unsigned nb = static_cast<unsigned>(batches);
-    if (big_tiles >= static_cast<size_t>(device_cu_count())) launch_tiles<256, 256, 2, 4>(trans_a, trans_b, g, s, nb);
-    else launch_tiles<128, 128, 2, 2>(trans_a, trans_b, g, s, nb);
+    if (big_tiles >= static_cast<size_t>(device_cu_count())) {
+        if (!g.vec) launch_tiles<256, 256, 2, 4>(trans_a, trans_b, g, s, nb);
+        // wave grid and read order per layout: the fastest measured at 8192x4096x4096
+        else if (!trans_a && !trans_b) launch_dma<2, 2, 1>(trans_a, trans_b, g, s, nb);
+        else if (!trans_a && trans_b) launch_dma<2, 4, 0>(trans_a, trans_b, g, s, nb);
+        else launch_dma<2, 4, 1>(trans_a, trans_b, g, s, nb);
+    } else {
+        launch_tiles<128, 128, 2, 2>(trans_a, trans_b, g, s, nb);
+    }
     return launch_status();
 }
 
