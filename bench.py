@@ -2,15 +2,18 @@
 on one MI355X, on BASELINE config 5: batch 8192, six Linear(4096, 4096) layers
 with bias, ReLU after layers 1-5, MSE loss, fp32, Adam(lr 1e-3).
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c5|c4|c1]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c5|c4|c1|c2|c3]
                     [--no-cpu-baseline] [--cpu-sample-rows R]
 
 Prints one JSON line.  `value` is steps/s measured over exactly K steps with
-all inputs resident in HBM.  `roofline` is the fp32-MFMA roofline of the
-dominant kernel class (the GEMMs): algorithmic FLOPs of every GEMM launch in
-the timed region over their summed device-event durations, on the library
-stream.  `cpu_baseline` times the CPU restatement of the reference (oracle/,
-one core) on a bounded sample of the same step and extrapolates to steps/s.
+all inputs resident in HBM.  `roofline` is the roofline of the dominant kernel
+class: for the MLP configs (c1, c4, c5) the fp32-MFMA roofline of the GEMMs
+(algorithmic FLOPs of every GEMM launch in the timed region over their summed
+device-event durations, on the library stream); for the elementwise chain
+(c2) and Adam alone (c3) the HBM roofline of the bandwidth-bound kernels
+(algorithmic bytes over event time).  `cpu_baseline` times the CPU
+restatement of the reference (oracle/, one core) on a bounded sample of the
+same step and extrapolates to steps/s.
 """
 from __future__ import annotations
 
@@ -31,11 +34,15 @@ PEAK_FP32_MFMA_TFLOPS = 157.3   # MI355X dense fp32 matrix peak (published)
 PEAK_HBM_GBS = 8000.0           # MI355X HBM3E (published)
 
 CONFIGS = {
-    # name: (batch, layer widths, init, relu on the last layer)
+    # name: (batch, layer widths, init)
     "c5": (8192, [4096] * 7, "normal"),
     "c4": (1024, [784, 1024, 10], "kaiming"),
     "c1": (32, [784, 128], "readme"),
 }
+CHAIN_N = 1 << 26        # config 2: elementwise autograd chain length
+ADAM_P = 1 << 28         # config 3: Adam alone, parameter count
+CHAIN_BYTES_PER_ELEM = 148   # forward 60 + backward 88 B per element (algorithmic, one step)
+ADAM_BYTES_PER_PARAM = 28    # read p, g, m, v; write p, m, v
 
 
 def log(msg: str) -> None:
@@ -154,12 +161,139 @@ def cpu_baseline(cfg_name: str, sample_rows: int):
             "sample": sample, "breakdown_s": {k: round(v, 3) for k, v in timings.items()}}
 
 
+def cpu_baseline_chain(sample: int):
+    """Config 2 on the CPU restatement of the engine (oracle/gradtrack.py): the
+    forward chain and its backward on `sample` elements, scaled to 2^26."""
+    from oracle import gradtrack as G
+
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal(sample, dtype=np.float32)
+    b = rng.standard_normal(sample, dtype=np.float32)
+    c = rng.uniform(0.5, 2.0, sample).astype(np.float32)
+    A, Bt, C = (G.OTensor(v.copy(), True) for v in (a, b, c))
+    t0 = time.perf_counter()
+    loss = A.add_tensor(Bt).mul_tensor(C).sub_tensor(A.div_tensor(C)).relu().sum()
+    loss.backward()
+    dt = (time.perf_counter() - t0) * (CHAIN_N / sample)
+    G.clear_gradients()
+    return {"value": 1.0 / dt, "unit": "steps/s", "cores": 1, "kind": "port",
+            "sample": f"forward chain + backward through the restated engine on {sample} of {CHAIN_N} "
+                      f"elements, scaled to one full step ({dt:.2f} s)"}
+
+
+def cpu_baseline_adam(sample: int):
+    """Config 3 on the CPU restatement of Adam::step (oracle/): one step on
+    `sample` parameters, scaled to 2^28."""
+    import oracle as O
+
+    rng = np.random.default_rng(7)
+    p = rng.standard_normal(sample, dtype=np.float32)
+    g = rng.standard_normal(sample, dtype=np.float32) * np.float32(0.1)
+    m = np.zeros(sample, np.float32)
+    v = np.zeros(sample, np.float32)
+    t0 = time.perf_counter()
+    O.adam_step(p, g, m, v, 1)
+    dt = (time.perf_counter() - t0) * (ADAM_P / sample)
+    return {"value": 1.0 / dt, "unit": "steps/s", "cores": 1, "kind": "port",
+            "sample": f"one Adam step on {sample} of {ADAM_P} parameters, scaled ({dt:.2f} s)"}
+
+
+def bandwidth_main(args, TS, hip, hip_check) -> int:
+    """Configs 2 and 3: the HBM-bound paths, each step timed like the MLP step."""
+    rng = np.random.default_rng(0)
+    if args.config == "c2":
+        n = CHAIN_N
+        log(f"config c2: chain over {n} elements; uploading inputs")
+        a = TS.Tensor.from_slice(rng.standard_normal(n, dtype=np.float32), [n]).with_requires_grad()
+        b = TS.Tensor.from_slice(rng.standard_normal(n, dtype=np.float32), [n]).with_requires_grad()
+        c = TS.Tensor.from_slice(rng.uniform(0.5, 2.0, n).astype(np.float32), [n]).with_requires_grad()
+
+        def step():
+            loss = a.add_tensor(b).mul_tensor(c).sub_tensor(a.div_tensor(c)).relu().sum()
+            loss.backward()
+            TS.clear_gradients()      # leaves start every step without a gradient
+            return loss
+        work = float(CHAIN_BYTES_PER_ELEM) * n
+        classes = ("elementwise", "reduction")
+        workload = ("BASELINE config 2: elementwise autograd chain over 2^26 fp32, a,b ~N(0,1), c ~U(0.5,2), "
+                    "y=relu((a+b)*c - a/c), loss=sum(y), backward to a,b,c")
+        data = "synthetic (numpy default_rng(0))"
+    else:
+        n = ADAM_P
+        log(f"config c3: Adam on {n} parameters; generating on the device")
+        p = TS.Tensor.randn([n], seed=1).with_requires_grad()
+        g = TS.Tensor.randn([n], seed=2).mul_scalar(0.1)
+        p.set_grad(g)
+        opt = TS.Adam.with_learning_rate(1e-3)
+        opt.add_parameter(p)
+
+        def step():
+            opt.step([p])
+            return None
+        work = float(ADAM_BYTES_PER_PARAM) * n
+        classes = ("adam",)
+        workload = ("BASELINE config 3: Adam::step alone on 2^28 fp32 params, grads ~N(0, 1e-2) set once, "
+                    "m=v=0 initially, lr=1e-3, betas (0.9, 0.999), eps 1e-8")
+        data = "synthetic (device XorShiftRng randn: p seed 1, g = 0.1 * randn seed 2)"
+
+    for i in range(args.warmup):
+        step()
+    TS.synchronize()
+    TS.Profile.reset()
+    TS.Profile.enable(True)
+    TS.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    TS.synchronize()
+    t1 = time.perf_counter()
+    TS.Profile.enable(False)
+    wall_ms = (t1 - t0) * 1000.0 / args.steps
+    names = {"elementwise": TS.Profile.ELEMENTWISE, "reduction": TS.Profile.REDUCTION, "adam": TS.Profile.ADAM}
+    prof = {k: TS.Profile.read(names[k]) for k in classes}
+    kern_ms = sum(v["ms"] for v in prof.values())
+    kern_work = sum(v["work"] for v in prof.values())
+    achieved = kern_work / (kern_ms * 1e-3) / 1e9 if kern_ms > 0 else 0.0
+    kernels = {k: {"ms_per_step": round(v["ms"] / args.steps, 3), "launches_per_step": v["launches"] // args.steps,
+                   "GB/s": round(v["work"] / (v["ms"] * 1e-3) / 1e9, 1) if v["ms"] > 0 else 0.0}
+               for k, v in prof.items()}
+    result = {
+        "metric": {"c2": "fwd+bwd steps/sec of the elementwise chain (1 GPU); % HBM GB/s roofline",
+                   "c3": "Adam::step steps/sec (1 GPU); % HBM GB/s roofline"}[args.config],
+        "value": round(1000.0 / wall_ms, 4),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": data,
+        "config": {"workload": workload, "elements": n, "algorithmic_bytes_per_step": work},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": " + ".join(classes) + " kernels of the step (every launch of the timed region)",
+                     "step_bytes_per_wall_time_GBs": round(work / (wall_ms * 1e-3) / 1e9, 1)},
+        "kernels": kernels,
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline (oracle port, one core, bounded sample)")
+        result["cpu_baseline"] = (cpu_baseline_chain(CHAIN_N) if args.config == "c2"
+                                  else cpu_baseline_adam(1 << 26))
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c5", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="c5", choices=sorted(list(CONFIGS) + ["c2", "c3"]))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-rows", type=int, default=512)
     ap.add_argument("--copy-probe", type=int, default=0,
@@ -185,6 +319,9 @@ def main() -> int:
         TS.synchronize()
         log(f"copy probe: 3 launches over {n} floats ({8 * n} bytes each)")
         del src, dst
+
+    if args.config in ("c2", "c3"):
+        return bandwidth_main(args, TS, hip, hip_check)
 
     batch, widths, init = CONFIGS[args.config]
     readme = init == "readme"

@@ -19,50 +19,65 @@ struct AdamArgs {
     float b1, c1, b2, c2, cf1, cf2, lr, eps, wd;
 };
 
+// vmax: the AMSGrad running max of v_hat for this element (read and updated
+// only when a.vmax is set).
 __device__ inline void adam_elem(const AdamArgs &a, size_t i, float &p, float g, float &m,
-                                 float &v, float *vmax) {
+                                 float &v, float &vmax) {
     if (a.wd > 0.0f) g = g + a.wd * p;                        // adam/mod.rs:567-620
     m = a.b1 * m + a.c1 * g;                                  // :634-696
     v = (i < a.tail_start) ? a.b2 * v + a.c2 * (g * g)        // :709-774 AVX2 body
                            : a.b2 * v + (a.c2 * g) * g;       //          scalar tail
     const float mh = m * a.cf1;                               // :790-833 bias_correct
     float vh = v * a.cf2;
-    if (vmax) {                                               // :534-541 AMSGrad
-        const float old = a.amsgrad_first ? vh : *vmax;
+    if (a.vmax) {                                             // :534-541 AMSGrad
+        const float old = a.amsgrad_first ? vh : vmax;
         vh = old > vh ? old : vh;
-        *vmax = vh;
+        vmax = vh;
     }
     const float den = sqrtf(vh) + a.eps;                      // :913-1007
     p = p - (a.lr * mh) / den;
 }
 
-__global__ __launch_bounds__(kBlock) void adam_kernel(AdamArgs a) {
-    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
-    const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-    float4 *p4 = reinterpret_cast<float4 *>(a.p);
-    const float4 *g4 = reinterpret_cast<const float4 *>(a.g);
-    float4 *m4 = reinterpret_cast<float4 *>(a.m);
-    float4 *v4 = reinterpret_cast<float4 *>(a.v);
-    for (size_t q = t; q < a.n4; q += stride) {
-        float4 p = p4[q], g = g4[q], m = m4[q], v = v4[q];
-        float4 vm = a.vmax ? reinterpret_cast<const float4 *>(a.vmax)[q] : make_float4(0, 0, 0, 0);
-        float *vmp = a.vmax ? reinterpret_cast<float *>(&vm) : nullptr;
-        adam_elem(a, 4 * q + 0, p.x, g.x, m.x, v.x, vmp ? vmp + 0 : nullptr);
-        adam_elem(a, 4 * q + 1, p.y, g.y, m.y, v.y, vmp ? vmp + 1 : nullptr);
-        adam_elem(a, 4 * q + 2, p.z, g.z, m.z, v.z, vmp ? vmp + 2 : nullptr);
-        adam_elem(a, 4 * q + 3, p.w, g.w, m.w, v.w, vmp ? vmp + 3 : nullptr);
-        p4[q] = p;
-        m4[q] = m;
-        v4[q] = v;
-        if (a.vmax) reinterpret_cast<float4 *>(a.vmax)[q] = vm;
+// Thread t updates float4 group t (elements 4t .. 4t+3) when t < n4, and
+// element 4*n4 + t of the scalar remainder.  The gradient is read once per
+// step, so it is loaded with the non-temporal policy (measured +7% on the
+// whole kernel); p, m and v are read and written back.
+__device__ inline void adam_unit(const AdamArgs &a, size_t t) {
+    if (t < a.n4) {
+        float4 *p4 = reinterpret_cast<float4 *>(a.p);
+        float4 *m4 = reinterpret_cast<float4 *>(a.m);
+        float4 *v4 = reinterpret_cast<float4 *>(a.v);
+        float4 p = p4[t], m = m4[t], v = v4[t];
+        const float4 g = load_nt(reinterpret_cast<const float4 *>(a.g) + t);
+        float4 vm = a.vmax ? reinterpret_cast<const float4 *>(a.vmax)[t] : make_float4(0, 0, 0, 0);
+        adam_elem(a, 4 * t + 0, p.x, g.x, m.x, v.x, vm.x);
+        adam_elem(a, 4 * t + 1, p.y, g.y, m.y, v.y, vm.y);
+        adam_elem(a, 4 * t + 2, p.z, g.z, m.z, v.z, vm.z);
+        adam_elem(a, 4 * t + 3, p.w, g.w, m.w, v.w, vm.w);
+        p4[t] = p;
+        m4[t] = m;
+        v4[t] = v;
+        if (a.vmax) reinterpret_cast<float4 *>(a.vmax)[t] = vm;
     }
-    for (size_t i = 4 * a.n4 + t; i < a.n; i += stride) {
-        float p = a.p[i], m = a.m[i], v = a.v[i];
-        adam_elem(a, i, p, a.g[i], m, v, a.vmax ? a.vmax + i : nullptr);
+    const size_t i = 4 * a.n4 + t;
+    if (i < a.n) {
+        float p = a.p[i], m = a.m[i], v = a.v[i], vm = a.vmax ? a.vmax[i] : 0.0f;
+        adam_elem(a, i, p, a.g[i], m, v, vm);
         a.p[i] = p;
         a.m[i] = m;
         a.v[i] = v;
+        if (a.vmax) a.vmax[i] = vm;
     }
+}
+
+// Threads needed by one tensor: its float4 groups or its scalar remainder.
+inline size_t adam_threads(size_t n, size_t n4) {
+    const size_t rest = n - 4 * n4;
+    return n4 > rest ? n4 : rest;
+}
+
+__global__ __launch_bounds__(kBlock) void adam_kernel(AdamArgs a) {
+    adam_unit(a, static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x);
 }
 
 // adam/mod.rs:524-531: (1 - (beta as f64).powf(step as f32 as f64)) as f32,
@@ -80,47 +95,26 @@ using namespace tship;
 struct MultiArgs {
     ts_hip_adam_param prm[TS_HIP_ADAM_MAX_PARAMS];
     int vec[TS_HIP_ADAM_MAX_PARAMS];
+    unsigned first_block[TS_HIP_ADAM_MAX_PARAMS + 1];  // workgroups of tensor j: [first_block[j], first_block[j+1])
+    int count;
     float b1, c1, b2, c2, cf1, cf2, lr, eps, wd;
 };
 
-// blockIdx.y selects the parameter; its workgroups stride over its float4
-// groups.  Same per-element arithmetic as adam_kernel.
+// One flat grid over all tensors: workgroup b finds its tensor in the
+// (uniform) prefix table, then works as adam_kernel does on that tensor.
 __global__ __launch_bounds__(kBlock) void adam_multi_kernel(MultiArgs A) {
-    const ts_hip_adam_param &q = A.prm[blockIdx.y];
+    int j = 0;
+    while (j + 1 < A.count && blockIdx.x >= A.first_block[j + 1]) ++j;
+    const ts_hip_adam_param &q = A.prm[j];
     AdamArgs a{};
     a.p = q.p; a.g = q.g; a.m = q.m; a.v = q.v; a.vmax = q.v_hat_max;
     a.n = q.n;
-    a.n4 = A.vec[blockIdx.y] ? q.n / 4 : 0;
+    a.n4 = A.vec[j] ? q.n / 4 : 0;
     a.tail_start = (q.n / 8) * 8;
     a.amsgrad_first = q.amsgrad_first;
     a.b1 = A.b1; a.c1 = A.c1; a.b2 = A.b2; a.c2 = A.c2;
     a.cf1 = A.cf1; a.cf2 = A.cf2; a.lr = A.lr; a.eps = A.eps; a.wd = A.wd;
-    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
-    const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-    float4 *p4 = reinterpret_cast<float4 *>(a.p);
-    const float4 *g4 = reinterpret_cast<const float4 *>(a.g);
-    float4 *m4 = reinterpret_cast<float4 *>(a.m);
-    float4 *v4 = reinterpret_cast<float4 *>(a.v);
-    for (size_t i = t; i < a.n4; i += stride) {
-        float4 p = p4[i], g = g4[i], m = m4[i], v = v4[i];
-        float4 vm = a.vmax ? reinterpret_cast<const float4 *>(a.vmax)[i] : make_float4(0, 0, 0, 0);
-        float *vmp = a.vmax ? reinterpret_cast<float *>(&vm) : nullptr;
-        adam_elem(a, 4 * i + 0, p.x, g.x, m.x, v.x, vmp ? vmp + 0 : nullptr);
-        adam_elem(a, 4 * i + 1, p.y, g.y, m.y, v.y, vmp ? vmp + 1 : nullptr);
-        adam_elem(a, 4 * i + 2, p.z, g.z, m.z, v.z, vmp ? vmp + 2 : nullptr);
-        adam_elem(a, 4 * i + 3, p.w, g.w, m.w, v.w, vmp ? vmp + 3 : nullptr);
-        p4[i] = p;
-        m4[i] = m;
-        v4[i] = v;
-        if (a.vmax) reinterpret_cast<float4 *>(a.vmax)[i] = vm;
-    }
-    for (size_t i = 4 * a.n4 + t; i < a.n; i += stride) {
-        float p = a.p[i], m = a.m[i], v = a.v[i];
-        adam_elem(a, i, p, a.g[i], m, v, a.vmax ? a.vmax + i : nullptr);
-        a.p[i] = p;
-        a.m[i] = m;
-        a.v[i] = v;
-    }
+    adam_unit(a, static_cast<size_t>(blockIdx.x - A.first_block[j]) * kBlock + threadIdx.x);
 }
 
 extern "C" int ts_hip_adam_step(float *p, const float *g, float *m, float *v, float *v_hat_max,
@@ -142,8 +136,9 @@ extern "C" int ts_hip_adam_step(float *p, const float *g, float *m, float *v, fl
     a.cf1 = correction_factor(beta1, step_count);
     a.cf2 = correction_factor(beta2, step_count);
     a.lr = lr; a.eps = eps; a.wd = weight_decay;
-    unsigned grid = grid_for(a.n4 ? a.n4 : n);
-    hipLaunchKernelGGL(adam_kernel, dim3(grid), dim3(kBlock), 0, as_stream(stream), a);
+    const size_t blocks = (adam_threads(n, a.n4) + kBlock - 1) / kBlock;
+    if (blocks > 0x7fffffffULL) return TS_HIP_EINVAL;
+    hipLaunchKernelGGL(adam_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, as_stream(stream), a);
     return launch_status();
 }
 
@@ -153,26 +148,26 @@ extern "C" int ts_hip_adam_step_multi(const ts_hip_adam_param *params, size_t co
     if (count == 0) return TS_HIP_OK;
     if (!params || count > TS_HIP_ADAM_MAX_PARAMS || step_count == 0) return TS_HIP_EINVAL;
     MultiArgs A{};
-    size_t max_units = 0;
+    size_t blocks = 0;
     for (size_t i = 0; i < count; ++i) {
         const ts_hip_adam_param &q = params[i];
         if (q.n && (!q.p || !q.g || !q.m || !q.v)) return TS_HIP_EINVAL;
         A.prm[i] = q;
         A.vec[i] = aligned16(q.p) && aligned16(q.g) && aligned16(q.m) && aligned16(q.v) &&
                    (!q.v_hat_max || aligned16(q.v_hat_max));
-        const size_t units = A.vec[i] ? q.n / 4 + q.n % 4 : q.n;
-        if (units > max_units) max_units = units;
+        A.first_block[i] = static_cast<unsigned>(blocks);
+        blocks += (adam_threads(q.n, A.vec[i] ? q.n / 4 : 0) + kBlock - 1) / kBlock;
+        if (blocks > 0x7fffffffULL) return TS_HIP_EINVAL;
     }
-    if (max_units == 0) return TS_HIP_OK;
+    A.first_block[count] = static_cast<unsigned>(blocks);
+    A.count = static_cast<int>(count);
+    if (blocks == 0) return TS_HIP_OK;
     A.b1 = beta1; A.c1 = 1.0f - beta1;
     A.b2 = beta2; A.c2 = 1.0f - beta2;
     A.cf1 = correction_factor(beta1, step_count);
     A.cf2 = correction_factor(beta2, step_count);
     A.lr = lr; A.eps = eps; A.wd = weight_decay;
-    size_t gx = (max_units + kBlock - 1) / kBlock;
-    const size_t cap = static_cast<size_t>(device_cu_count()) * 8;
-    if (gx > cap) gx = cap;
-    hipLaunchKernelGGL(adam_multi_kernel, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(count)),
-                       dim3(kBlock), 0, as_stream(stream), A);
+    hipLaunchKernelGGL(adam_multi_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
+                       as_stream(stream), A);
     return launch_status();
 }

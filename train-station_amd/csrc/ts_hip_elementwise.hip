@@ -177,31 +177,35 @@ struct MapArgs {
     float *out[2];
 };
 
-// Vector part: float4 groups [0, n4); scalar tail [4*n4, n) by the first
-// threads of the grid.  n4 is 0 when any pointer is not 16-byte aligned.
+// One float4 group per thread (thread t < n4 takes elements 4t .. 4t+3) and
+// the scalar remainder [4*n4, n) by the first threads; n4 is 0 when any
+// pointer is not 16-byte aligned, and then every element is scalar.  Vector
+// results are written with non-temporal stores: the output streams to HBM
+// instead of displacing the inputs in L2 / MALL (measured +4% on data that
+// is not cached, +30% on data that is).
 template <class Op>
 __global__ __launch_bounds__(kBlock) void map_kernel(MapArgs args, size_t n, size_t n4, Op op) {
-    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
-    size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-    for (size_t v = t; v < n4; v += stride) {
+    const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (t < n4) {
         float4 xin[Op::NIN > 0 ? Op::NIN : 1];
 #pragma unroll
-        for (int k = 0; k < Op::NIN; ++k) xin[k] = reinterpret_cast<const float4 *>(args.in[k])[v];
+        for (int k = 0; k < Op::NIN; ++k) xin[k] = reinterpret_cast<const float4 *>(args.in[k])[t];
         float4 yout[Op::NOUT];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             float xs[Op::NIN > 0 ? Op::NIN : 1], ys[Op::NOUT];
 #pragma unroll
             for (int k = 0; k < Op::NIN; ++k) xs[k] = reinterpret_cast<const float *>(&xin[k])[c];
-            op(4 * v + c, xs, ys);
+            op(4 * t + c, xs, ys);
 #pragma unroll
             for (int k = 0; k < Op::NOUT; ++k) reinterpret_cast<float *>(&yout[k])[c] = ys[k];
         }
 #pragma unroll
         for (int k = 0; k < Op::NOUT; ++k)
-            if (args.out[k]) reinterpret_cast<float4 *>(args.out[k])[v] = yout[k];
+            if (args.out[k]) store_nt(reinterpret_cast<float4 *>(args.out[k]) + t, yout[k]);
     }
-    for (size_t i = 4 * n4 + t; i < n; i += stride) {
+    const size_t i = 4 * n4 + t;
+    if (i < n) {
         float xs[Op::NIN > 0 ? Op::NIN : 1], ys[Op::NOUT];
 #pragma unroll
         for (int k = 0; k < Op::NIN; ++k) xs[k] = args.in[k][i];
@@ -227,10 +231,13 @@ static int launch_map(const float *const *in, float *const *out, size_t n, Op op
         if (out[k]) { any_out = true; vec = vec && aligned16(out[k]); }
     }
     if (!any_out) return TS_HIP_EINVAL;
-    size_t n4 = vec ? n / 4 : 0;
-    unsigned grid = grid_for(n4 ? n4 : n);
-    hipLaunchKernelGGL(map_kernel<Op>, dim3(grid), dim3(kBlock), 0, as_stream(stream), args, n, n4,
-                       op);
+    const size_t n4 = vec ? n / 4 : 0;
+    const size_t rest = n - 4 * n4;
+    const size_t threads = n4 > rest ? n4 : rest;
+    const size_t blocks = (threads + kBlock - 1) / kBlock;
+    if (blocks > 0x7fffffffULL) return TS_HIP_EINVAL;
+    hipLaunchKernelGGL(map_kernel<Op>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, as_stream(stream),
+                       args, n, n4, op);
     return launch_status();
 }
 
@@ -288,7 +295,7 @@ __global__ __launch_bounds__(kBlock) void row_broadcast_vec4(const float4 *__res
         o.y = row_op(a, 4 * q + 1, xv.y, b.y);
         o.z = row_op(a, 4 * q + 2, xv.z, b.z);
         o.w = row_op(a, 4 * q + 3, xv.w, b.w);
-        out[q] = o;
+        store_nt(out + q, o);
     }
 }
 

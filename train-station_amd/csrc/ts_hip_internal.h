@@ -35,6 +35,19 @@ inline unsigned grid_for(size_t units, size_t per_thread = 1) {
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+typedef float f4v_t __attribute__((ext_vector_type(4)));
+
+// Non-temporal 16-byte store / load (the nt cache policy): for streams that
+// are written, or read, once per kernel.
+__device__ __forceinline__ void store_nt(float4 *p, float4 v) {
+    const f4v_t r = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(r, reinterpret_cast<f4v_t *>(p));
+}
+__device__ __forceinline__ float4 load_nt(const float4 *p) {
+    const f4v_t r = __builtin_nontemporal_load(reinterpret_cast<const f4v_t *>(p));
+    return make_float4(r.x, r.y, r.z, r.w);
+}
+
 // Weighted column sums out[c] = sum_r w[r] * x[r][c] (w == nullptr: plain
 // column sums), f64 partials; workspace as ts_hip_sum_dim0_workspace_floats.
 int launch_colsum(const float *x, const float *w, size_t rows, size_t cols, size_t ld, float *out,

@@ -70,7 +70,15 @@ template <bool MEAN>
 __global__ __launch_bounds__(kBlock) void sum_final(const double *__restrict__ partial,
                                                     size_t nparts, size_t n, float *out) {
     double acc = 0.0;
-    for (size_t i = threadIdx.x; i < nparts; i += kBlock) acc += partial[i];
+    size_t i = threadIdx.x;
+    for (; i + kBlock * 7 < nparts; i += kBlock * 8) {  // eight loads in flight
+        double v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = partial[i + kBlock * j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc += v[j];
+    }
+    for (; i < nparts; i += kBlock) acc += partial[i];
     double r = block_sum(acc);
     if (threadIdx.x == 0) {
         float s = static_cast<float>(r);
@@ -106,16 +114,21 @@ static int launch_sum(const float *x, const float *y, size_t n, float *out, floa
 
 // ---- column reduction [rows, cols] -> [cols] --------------------------------
 
-// Pass 1: a thread owns 4 adjacent columns (one float4; 1 column when cols is
-// not a multiple of 4) over a contiguous chunk of rows; a workgroup covers
-// 256 such column groups, so each row step of a wave reads 1 KiB contiguously.
-// Row chunks are sized so the grid fills the device.
+// Pass 1: a workgroup owns 64 column units (float4 groups of 4 adjacent
+// columns when cols % 4 == 0, single columns otherwise) and one chunk of
+// rows; its four waves take every fourth row of the chunk, each wave reading
+// 1 KiB contiguously per row with eight rows in flight per thread.  The four
+// row lanes are combined in LDS in a fixed order and one f64 partial per
+// column and chunk is written.  Chunks are sized so that the grid has about
+// 2048 workgroups.
 constexpr size_t kDim0MaxChunks = 128;
+constexpr int kDim0Cols = 64;  // column units per workgroup
+constexpr int kDim0Unroll = 8;
 
 static size_t dim0_chunks(size_t rows, size_t cols) {
-    const size_t groups = (cols % 4 == 0) ? cols / 4 : cols;
-    const size_t col_blocks = (groups + kBlock - 1) / kBlock;
-    size_t want = 1024 / (col_blocks ? col_blocks : 1);   // ~4 workgroups per CU
+    const size_t units = (cols % 4 == 0) ? cols / 4 : cols;
+    const size_t col_blocks = (units + kDim0Cols - 1) / kDim0Cols;
+    size_t want = 2048 / (col_blocks ? col_blocks : 1);
     size_t by_rows = (rows + 15) / 16;                    // at least 16 rows per chunk
     size_t c = want < by_rows ? want : by_rows;
     if (c > kDim0MaxChunks) c = kDim0MaxChunks;
@@ -127,62 +140,90 @@ template <bool VEC, bool W>
 __global__ __launch_bounds__(kBlock) void dim0_partial(const float *__restrict__ x, const float *__restrict__ w,
                                                        size_t rows, size_t cols, size_t rows_per_chunk,
                                                        double *__restrict__ partial) {
-    const size_t groups = VEC ? cols / 4 : cols;
-    const size_t gcol = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (gcol >= groups) return;
+    constexpr int L = VEC ? 4 : 1;  // columns per unit
+    __shared__ double lds[kBlock / kDim0Cols][kDim0Cols][L];
+    const size_t units = VEC ? cols / 4 : cols;
+    const int cl = threadIdx.x % kDim0Cols, rl = threadIdx.x / kDim0Cols;
+    constexpr int RL = kBlock / kDim0Cols;  // row lanes
+    const size_t u = static_cast<size_t>(blockIdx.x) * kDim0Cols + cl;
     const size_t r0 = static_cast<size_t>(blockIdx.y) * rows_per_chunk;
     size_t r1 = r0 + rows_per_chunk;
     if (r1 > rows) r1 = rows;
-    double* out = partial + static_cast<size_t>(blockIdx.y) * cols;
-    if (VEC) {
-        const float4 *x4 = reinterpret_cast<const float4 *>(x);
-        double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
-        size_t r = r0;
-        for (; r + 4 <= r1; r += 4) {   // four independent loads in flight per thread
-            const float4 q0 = x4[(r + 0) * groups + gcol], q1 = x4[(r + 1) * groups + gcol];
-            const float4 q2 = x4[(r + 2) * groups + gcol], q3 = x4[(r + 3) * groups + gcol];
-            const double w0 = W ? (double)w[r] : 1.0, w1 = W ? (double)w[r + 1] : 1.0;
-            const double w2 = W ? (double)w[r + 2] : 1.0, w3 = W ? (double)w[r + 3] : 1.0;
-            a0 += w0 * q0.x; a1 += w0 * q0.y; a2 += w0 * q0.z; a3 += w0 * q0.w;
-            a0 += w1 * q1.x; a1 += w1 * q1.y; a2 += w1 * q1.z; a3 += w1 * q1.w;
-            a0 += w2 * q2.x; a1 += w2 * q2.y; a2 += w2 * q2.z; a3 += w2 * q2.w;
-            a0 += w3 * q3.x; a1 += w3 * q3.y; a2 += w3 * q3.z; a3 += w3 * q3.w;
+    double acc[L];
+#pragma unroll
+    for (int c = 0; c < L; ++c) acc[c] = 0.0;
+    auto load = [&](size_t r, float (&q)[L]) {
+        if (VEC) {
+            const float4 v = reinterpret_cast<const float4 *>(x)[r * units + u];
+            q[0] = v.x; q[L > 1 ? 1 : 0] = v.y; q[L > 2 ? 2 : 0] = v.z; q[L > 3 ? 3 : 0] = v.w;
+        } else {
+            q[0] = x[r * cols + u];
         }
-        for (; r < r1; ++r) {
-            const float4 q = x4[r * groups + gcol];
+    };
+    if (u < units) {
+        size_t r = r0 + rl;
+        for (; r + RL * (kDim0Unroll - 1) < r1; r += RL * kDim0Unroll) {
+            float q[kDim0Unroll][L];
+#pragma unroll
+            for (int k = 0; k < kDim0Unroll; ++k) load(r + RL * k, q[k]);
+#pragma unroll
+            for (int k = 0; k < kDim0Unroll; ++k) {
+                const double wr = W ? (double)w[r + RL * k] : 1.0;
+#pragma unroll
+                for (int c = 0; c < L; ++c) acc[c] += wr * q[k][c];
+            }
+        }
+        for (; r < r1; r += RL) {
+            float q[L];
+            load(r, q);
             const double wr = W ? (double)w[r] : 1.0;
-            a0 += wr * q.x; a1 += wr * q.y; a2 += wr * q.z; a3 += wr * q.w;
+#pragma unroll
+            for (int c = 0; c < L; ++c) acc[c] += wr * q[c];
         }
-        out[4 * gcol + 0] = a0;
-        out[4 * gcol + 1] = a1;
-        out[4 * gcol + 2] = a2;
-        out[4 * gcol + 3] = a3;
-    } else {
-        double acc = 0.0;
-        for (size_t r = r0; r < r1; ++r) acc += (W ? (double)w[r] : 1.0) * (double)x[r * cols + gcol];
-        out[gcol] = acc;
+    }
+#pragma unroll
+    for (int c = 0; c < L; ++c) lds[rl][cl][c] = acc[c];
+    __syncthreads();
+    // thread t writes column (unit t / L, component t % L) of this workgroup
+    for (int t = threadIdx.x; t < kDim0Cols * L; t += kBlock) {
+        const int g = t / L, c = t % L;
+        const size_t col = (static_cast<size_t>(blockIdx.x) * kDim0Cols + g) * L + c;
+        if (col < cols) {
+            double sum = lds[0][g][c];
+#pragma unroll
+            for (int k = 1; k < RL; ++k) sum += lds[k][g][c];
+            partial[static_cast<size_t>(blockIdx.y) * cols + col] = sum;
+        }
     }
 }
 
-// Pass 2: a workgroup owns 64 columns; its four waves each add a quarter of
-// the chunk partials (lane = column), then wave 0 adds the four wave sums in
-// order.
+// Pass 2: a workgroup owns 16 columns; 16 chunk lanes each add every 16th
+// chunk partial, then the 16 lane sums are added in order.
 __global__ __launch_bounds__(kBlock) void dim0_final(const double *__restrict__ partial,
                                                      size_t chunks, size_t cols,
                                                      float *__restrict__ out) {
-    __shared__ double lds[kBlock / 64][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const size_t c = static_cast<size_t>(blockIdx.x) * 64 + lane;
+    __shared__ double lds[16][17];
+    const int cl = threadIdx.x & 15, kl = threadIdx.x >> 4;
+    const size_t c = static_cast<size_t>(blockIdx.x) * 16 + cl;
     double acc = 0.0;
-    if (c < cols)
-        for (size_t k = wave; k < chunks; k += kBlock / 64) acc += partial[k * cols + c];
-    lds[wave][lane] = acc;
-    __syncthreads();
-    if (wave == 0 && c < cols) {
-        double s = 0.0;
+    if (c < cols) {
+        size_t k = kl;
+        for (; k + 16 * 7 < chunks; k += 16 * 8) {  // eight loads in flight
+            double v[8];
 #pragma unroll
-        for (int w = 0; w < kBlock / 64; ++w) s += lds[w][lane];
-        out[c] = static_cast<float>(s);
+            for (int j = 0; j < 8; ++j) v[j] = partial[(k + 16 * j) * cols + c];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc += v[j];
+        }
+        for (; k < chunks; k += 16) acc += partial[k * cols + c];
+    }
+    lds[kl][cl] = acc;
+    __syncthreads();
+    if (threadIdx.x < 16 && c < cols) {
+        double sum = 0.0;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) sum += lds[k][cl];
+        out[c] = static_cast<float>(sum);
     }
 }
 
@@ -201,15 +242,17 @@ int launch_colsum(const float *x, const float *w, size_t rows, size_t cols, size
     double *partial = reinterpret_cast<double *>(workspace);
     hipStream_t s = as_stream(stream);
     const bool vec = (cols % 4 == 0) && aligned16(x);
-    const size_t groups = vec ? cols / 4 : cols;
-    dim3 grid1(static_cast<unsigned>((groups + kBlock - 1) / kBlock), static_cast<unsigned>(chunks));
+    const size_t units = vec ? cols / 4 : cols;
+    const size_t col_blocks = (units + kDim0Cols - 1) / kDim0Cols;
+    if (col_blocks > 0x7fffffffULL) return TS_HIP_EINVAL;
+    dim3 grid1(static_cast<unsigned>(col_blocks), static_cast<unsigned>(chunks));
     if (vec && w) hipLaunchKernelGGL((dim0_partial<true, true>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
     else if (vec) hipLaunchKernelGGL((dim0_partial<true, false>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
     else if (w) hipLaunchKernelGGL((dim0_partial<false, true>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
     else hipLaunchKernelGGL((dim0_partial<false, false>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
     int st = launch_status();
     if (st) return st;
-    hipLaunchKernelGGL(dim0_final, dim3(static_cast<unsigned>((cols + 63) / 64)), dim3(kBlock), 0, s,
+    hipLaunchKernelGGL(dim0_final, dim3(static_cast<unsigned>((cols + 15) / 16)), dim3(kBlock), 0, s,
                        partial, chunks, cols, out);
     return launch_status();
 }
