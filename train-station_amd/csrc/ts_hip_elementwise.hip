@@ -179,11 +179,14 @@ struct MapArgs {
 
 // One float4 group per thread (thread t < n4 takes elements 4t .. 4t+3) and
 // the scalar remainder [4*n4, n) by the first threads; n4 is 0 when any
-// pointer is not 16-byte aligned, and then every element is scalar.  Vector
-// results are written with non-temporal stores: the output streams to HBM
-// instead of displacing the inputs in L2 / MALL (measured +4% on data that
-// is not cached, +30% on data that is).
-template <class Op>
+// pointer is not 16-byte aligned, and then every element is scalar.  NT:
+// vector results are written with non-temporal stores, so the output streams
+// to HBM instead of displacing the inputs in L2 / MALL (measured +4% on data
+// that is not cached, +30% on data that is).  The gradients that a column
+// sum reads right after (ReLU and pow backward, whose outputs feed the bias
+// gradient) keep ordinary stores: the sum then finds them in MALL, which
+// saves more (-16% on that sum) than the store policy costs.
+template <class Op, bool NT>
 __global__ __launch_bounds__(kBlock) void map_kernel(MapArgs args, size_t n, size_t n4, Op op) {
     const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (t < n4) {
@@ -201,8 +204,12 @@ __global__ __launch_bounds__(kBlock) void map_kernel(MapArgs args, size_t n, siz
             for (int k = 0; k < Op::NOUT; ++k) reinterpret_cast<float *>(&yout[k])[c] = ys[k];
         }
 #pragma unroll
-        for (int k = 0; k < Op::NOUT; ++k)
-            if (args.out[k]) store_nt(reinterpret_cast<float4 *>(args.out[k]) + t, yout[k]);
+        for (int k = 0; k < Op::NOUT; ++k) {
+            if (!args.out[k]) continue;
+            float4 *o = reinterpret_cast<float4 *>(args.out[k]) + t;
+            if (NT) store_nt(o, yout[k]);
+            else *o = yout[k];
+        }
     }
     const size_t i = 4 * n4 + t;
     if (i < n) {
@@ -216,7 +223,7 @@ __global__ __launch_bounds__(kBlock) void map_kernel(MapArgs args, size_t n, siz
     }
 }
 
-template <class Op>
+template <class Op, bool NT = true>
 static int launch_map(const float *const *in, float *const *out, size_t n, Op op, void *stream) {
     if (n == 0) return TS_HIP_OK;
     MapArgs args{};
@@ -236,8 +243,8 @@ static int launch_map(const float *const *in, float *const *out, size_t n, Op op
     const size_t threads = n4 > rest ? n4 : rest;
     const size_t blocks = (threads + kBlock - 1) / kBlock;
     if (blocks > 0x7fffffffULL) return TS_HIP_EINVAL;
-    hipLaunchKernelGGL(map_kernel<Op>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, as_stream(stream),
-                       args, n, n4, op);
+    hipLaunchKernelGGL((map_kernel<Op, NT>), dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
+                       as_stream(stream), args, n, n4, op);
     return launch_status();
 }
 
@@ -248,11 +255,11 @@ static int map1(const float *x, float *out, size_t n, Op op, void *stream) {
     return launch_map(in, o, n, op, stream);
 }
 
-template <class Op>
+template <class Op, bool NT = true>
 static int map2(const float *a, const float *b, float *out, size_t n, Op op, void *stream) {
     const float *in[2] = {a, b};
     float *o[1] = {out};
-    return launch_map(in, o, n, op, stream);
+    return launch_map<Op, NT>(in, o, n, op, stream);
 }
 
 // Row broadcast [rows,cols] op [cols]: blockIdx.x walks column groups,
@@ -431,11 +438,11 @@ int ts_hip_leaky_relu_backward(const float *x, const float *go, float *gi, size_
 }
 
 int ts_hip_relu_backward(const float *x, const float *go, float *gi, size_t n, void *stream) {
-    return map2(x, go, gi, n, ReluBwdOp{}, stream);
+    return map2<ReluBwdOp, false>(x, go, gi, n, ReluBwdOp{}, stream);
 }
 int ts_hip_pow_backward(const float *x, const float *go, float *gi, size_t n, float e,
                         void *stream) {
-    return map2(x, go, gi, n, PowBwdOp{e}, stream);
+    return map2<PowBwdOp, false>(x, go, gi, n, PowBwdOp{e}, stream);
 }
 int ts_hip_mul_backward(const float *go, const float *a, const float *b, float *ga, float *gb,
                         size_t n, void *stream) {
