@@ -176,7 +176,7 @@ def test_sum_known_answers():
 
 
 @pytest.mark.parametrize("rows,cols", [(1, 1), (2, 4), (32, 128), (1024, 10), (33, 7), (1024, 1024),
-                                       (8192, 4096)])
+                                       (8192, 4096), (5000, 1001), (300, 4100), (8193, 260), (17, 70000)])
 def test_sum_dim0(oracle, rows, cols):
     print(f"[sum_dim0] {rows}x{cols}", flush=True)
     x = normal((rows, cols), 11)
@@ -301,7 +301,10 @@ def test_adam_multi_matches_per_parameter(oracle):
     # first/later steps, weight decay) gives the per-parameter bits
     from train_station_amd._ffi import AdamParam
     import ctypes
-    sizes = [1, 7, 9, 4096, 1000, (1 << 18) + 3]
+    # an empty tensor in the middle and one with unaligned buffers (scalar path)
+    # check the flat grid's tensor lookup
+    sizes = [1, 7, 9, 4096, 0, 1000, (1 << 18) + 3, 4099]
+    offs = [0, 0, 0, 0, 0, 0, 0, 1]
     for wd, ams in ((0.0, False), (0.01, True)):
         host = []
         for i, n in enumerate(sizes):
@@ -310,10 +313,11 @@ def test_adam_multi_matches_per_parameter(oracle):
             v = np.zeros(n, np.float32)
             vm = np.zeros(n, np.float32) if ams else None
             host.append([p, m, v, vm])
-        dev = [[Dev.of(h[0]), Dev.of(h[1]), Dev.of(h[2]), Dev.of(h[3]) if ams else None] for h in host]
+        dev = [[Dev.of(h[0], offs[i]), Dev.of(h[1], offs[i]), Dev.of(h[2], offs[i]),
+                Dev.of(h[3], offs[i]) if ams else None] for i, h in enumerate(host)]
         for step in range(1, 4):
             grads = [normal(n, 300 + 10 * step + i, 0.1) for i, n in enumerate(sizes)]
-            dg = [Dev.of(g) for g in grads]
+            dg = [Dev.of(g, offs[i]) for i, g in enumerate(grads)]
             arr = (AdamParam * len(sizes))()
             for i, n in enumerate(sizes):
                 d = dev[i]
