@@ -12,7 +12,12 @@
 // Its waves form a WM x WN grid; each wave owns (BM/WM) x (BN/WN) of C as a
 // grid of 32x32 v_mfma_f32_32x32x2_f32 accumulators.  Two shapes:
 //   large problems: 256x256 tiles, 8 waves (2 per SIMD), 128x64 per wave;
-//   small problems: 128x128 tiles, 4 waves, 64x64 per wave.
+//   smaller problems: 128x128 tiles, 4 waves, 64x64 per wave;
+//   small problems (fewer 128x128 tiles than half the CUs): 64x64 tiles,
+//   4 waves of one 32x32 accumulator each; when even those are fewer than a
+//   quarter of the CUs and K >= 512 (the README and config-4 shapes with
+//   M = 32 or N = 10), K is split into up to 16 slices computed as a batch
+//   into a stream-ordered temporary and added in slice order afterwards.
 // LDS holds each operand tile k-major (As[k][m], Bs[k][n]) so a wave's MFMA
 // operand read is two rows of 32 consecutive floats.  Columns are XOR-swizzled
 // per k row (swz) so that (a) the two rows an MFMA operand read touches fall
@@ -523,6 +528,18 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_lds_dma(GemmArgs g) {
     }
 }
 
+// Split-K: C[i][j] = sum over s of the slice products P_s[i][j] (P_s at
+// P + s*M*N, row-major M x N), added in slice order.
+__global__ __launch_bounds__(kBlock) void splitk_sum(const float *__restrict__ P, int slices, size_t M, size_t N,
+                                                     float *__restrict__ C, size_t ldc) {
+    const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const size_t mn = M * N;
+    if (t >= mn) return;
+    float acc = P[t];
+    for (int k = 1; k < slices; ++k) acc += P[static_cast<size_t>(k) * mn + t];
+    C[(t / N) * ldc + t % N] = acc;
+}
+
 template <int WM, int WN, int SCHED>
 static void launch_dma(int ta, int tb, GemmArgs g, hipStream_t s, unsigned batches) {
     g.tiles_m = (g.M + 255) / 256;
@@ -559,8 +576,10 @@ static int gemm_launch(int trans_a, int trans_b, size_t M, size_t N, size_t K, c
     for (int k = 0; k < g.batch_rank; ++k) strides4 = strides4 && g.sa[k] % 4 == 0 && g.sb[k] % 4 == 0;
     g.vec = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) && strides4;
     hipStream_t s = as_stream(stream);
-    // 256x256 tiles once they alone fill every CU; 128x128 below that.
+    // 256x256 tiles once they alone fill every CU; 128x128 while those give at
+    // least half as many workgroups as CUs; 64x64 (4 waves of 32x32) below.
     const size_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batches;
+    const size_t mid_tiles = ((M + 127) / 128) * ((N + 127) / 128) * batches;
     const unsigned nb = static_cast<unsigned>(batches);
     if (big_tiles >= static_cast<size_t>(device_cu_count())) {
         if (!g.vec) launch_tiles<256, 256, 2, 4>(trans_a, trans_b, g, s, nb);
@@ -568,8 +587,10 @@ static int gemm_launch(int trans_a, int trans_b, size_t M, size_t N, size_t K, c
         else if (!trans_a && !trans_b) launch_dma<2, 2, 1>(trans_a, trans_b, g, s, nb);
         else if (!trans_a && trans_b) launch_dma<2, 4, 0>(trans_a, trans_b, g, s, nb);
         else launch_dma<2, 4, 1>(trans_a, trans_b, g, s, nb);
-    } else {
+    } else if (2 * mid_tiles >= static_cast<size_t>(device_cu_count())) {
         launch_tiles<128, 128, 2, 2>(trans_a, trans_b, g, s, nb);
+    } else {
+        launch_tiles<64, 64, 2, 2>(trans_a, trans_b, g, s, nb);
     }
     return launch_status();
 }
@@ -582,6 +603,43 @@ extern "C" int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t 
     if (K == 0) {  // empty contraction: C = 0
         if (ldc != N) return TS_HIP_EINVAL;
         return ts_hip_fill(C, 0.0f, M * N, stream);
+    }
+    // Few output tiles and a long K: split K into S slices computed as a
+    // batch (slice s reads A and B from k = s*K/S on) into a stream-ordered
+    // temporary, then add the slices in order.
+    const size_t cus = static_cast<size_t>(device_cu_count());
+    const size_t tiles64 = ((M + 63) / 64) * ((N + 63) / 64);
+    int slices = 1;
+    if (4 * tiles64 < cus && K >= 512) {
+        for (int sl : {16, 8, 4, 2}) {
+            if (K % sl == 0 && K / sl >= 32 && tiles64 * sl <= 2 * cus) {
+                slices = sl;
+                break;
+            }
+        }
+    }
+    if (slices > 1 && A && B && lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N)) {
+        hipStream_t st = as_stream(stream);
+        float *P = nullptr;
+        if (hipMallocAsync(reinterpret_cast<void **>(&P), slices * M * N * sizeof(float), st) == hipSuccess) {
+            const size_t kc = K / slices;
+            GemmArgs g{};
+            g.batch_rank = 1;
+            g.bdims[0] = slices;
+            g.sa[0] = static_cast<long long>(trans_a ? kc * lda : kc);
+            g.sb[0] = static_cast<long long>(trans_b ? kc : kc * ldb);
+            g.sc = static_cast<long long>(M * N);
+            int status = gemm_launch(trans_a, trans_b, M, N, kc, A, lda, B, ldb, P, N, g, slices, stream);
+            if (status == TS_HIP_OK) {
+                const size_t blocks = (M * N + kBlock - 1) / kBlock;
+                hipLaunchKernelGGL(splitk_sum, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, st, P, slices, M,
+                                   N, C, ldc);
+                status = launch_status();
+            }
+            const hipError_t fe = hipFreeAsync(P, st);
+            return status != TS_HIP_OK ? status : static_cast<int>(fe);
+        }
+        (void)hipGetLastError();  // no stream-ordered allocation: run unsplit
     }
     GemmArgs g{};
     return gemm_launch(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, g, 1, stream);
