@@ -248,7 +248,11 @@ int ts_hip_matmul(const float *a, const float *b, float *c, size_t m, size_t n, 
  *   trans_b == 1: B(k,j) = B[j*ldb + k]   (B stored [N][ldb], i.e. B^T view)
  *   C(i,j) = C[i*ldc + j]
  * fp32 inputs, fp32 MFMA accumulation (v_mfma_f32_32x32x2_f32).  M, N, K and
- * the leading dimensions must be below 2^31 (TS_HIP_EINVAL otherwise). */
+ * the leading dimensions must be below 2^31 (TS_HIP_EINVAL otherwise).  For
+ * few output tiles with a long K (e.g. M = 32, K = 784) the call splits K and
+ * takes a temporary of up to 16*M*N floats from the stream-ordered allocator
+ * (hipMallocAsync / hipFreeAsync on `stream`); where that allocator is
+ * unavailable it runs unsplit. */
 int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
                 size_t lda, const float *B, size_t ldb, float *C, size_t ldc, void *stream);
 
