@@ -295,7 +295,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c5", choices=sorted(list(CONFIGS) + ["c2", "c3"]))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-rows", type=int, default=512)
+    ap.add_argument("--cpu-sample-rows", type=int, default=2048)
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="first launch a plain copy kernel (x * 1.0 -> out, 8 bytes per float) over "
                          "this many floats three times, as the calibration point of HBM byte counters")

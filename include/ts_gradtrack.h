@@ -162,6 +162,18 @@ int ts_adam_config_from_json(const char *json, size_t len, float *values5, int *
 
 /* runtime: wait for queued work (reports a recorded division by zero) */
 int ts_synchronize(void);
+
+/* Fusion of recorded ops into the producing product (no counterpart in the
+ * reference): with it on (the default), a 2-D matmul's product is deferred
+ * until its result is first read, a following add_tensor of a row vector and
+ * a relu are applied in that product's store, and in backward relu's gradient
+ * of the dX product is applied in its store (ts_hip_gemm_fused).  Results are
+ * bit-identical either way; off, every op launches its own kernels.  Products
+ * that read a tensor written in place (Adam::step, fill_randn) run before the
+ * write; a caller writing through ts_tensor_device_ptr should read the
+ * tensors that depend on it first, or switch fusion off. */
+void ts_fusion_enable(int on);
+int ts_fusion_enabled(void);
 /* library stream (for timing events on the stream the kernels run on) */
 void *ts_stream(void);
 /* device pool statistics and cache release */

@@ -256,6 +256,22 @@ int ts_hip_matmul(const float *a, const float *b, float *c, size_t m, size_t n, 
 int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
                 size_t lda, const float *B, size_t ldb, float *C, size_t ldc, void *stream);
 
+/* The same product with the elementwise ops that follow it fused into the
+ * store (no counterpart in the reference, which runs them as separate passes:
+ * matmul then add_tensor with a broadcast row bias, ops/add.rs:276-379, then
+ * relu, ops/relu.rs:77-273; or the product then relu's backward,
+ * grad_fn/ops/relu.rs:4-17).  Per output element, in this order:
+ *   v = op(A) . op(B) as ts_hip_gemm computes it;
+ *   bias != NULL:  v = v + bias[j]              (bias: N floats)
+ *   relu != 0:     v = v > 0 ? v : +0
+ *   mask != NULL:  v = mask[i*ldc + j] > 0 ? v : +0   (mask laid out as C)
+ *   C[i*ldc + j] = v
+ * Bit-identical to ts_hip_gemm followed by ts_hip_bias_add, ts_hip_relu and
+ * ts_hip_relu_backward(mask, C, C). */
+int ts_hip_gemm_fused(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A, size_t lda,
+                      const float *B, size_t ldb, const float *bias, int relu, const float *mask, float *C,
+                      size_t ldc, void *stream);
+
 /* Batched C[b] = op(A[b]) . op(B[b]) (matmul/mod.rs:634-760 batched_matmul and
  * the batched backward of grad_fn/ops/matmul.rs:150-219) on the same MFMA
  * tiles: a batch grid of batch_rank axes (<= 6) with sizes batch_dims; the A /

@@ -106,6 +106,8 @@ HIP_SIGNATURES = {
     "ts_hip_sum_dim0": (_c.c_int, [VP, SZ, SZ, VP, VP, SZ, VP]),
     "ts_hip_matmul": (_c.c_int, [VP, VP, VP, SZ, SZ, SZ, VP]),
     "ts_hip_gemm": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, SZ, VP]),
+    "ts_hip_gemm_fused": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, _c.c_int, VP, VP, SZ,
+                                     VP]),
     "ts_hip_gemm_batched": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, SZ, SZ,
                                        _c.POINTER(SZ), _c.POINTER(SZ), _c.POINTER(SZ), SZ, VP]),
     "ts_hip_gemv_workspace_floats": (SZ, [_c.c_int, SZ, SZ]),
@@ -214,6 +216,8 @@ GRADTRACK_SIGNATURES = {
     "ts_adam_config_to_json": (_c.c_int, [F, _c.c_int, _c.POINTER(VP), _c.POINTER(SZ)]),
     "ts_adam_config_from_json": (_c.c_int, [_c.c_char_p, SZ, F, _c.POINTER(_c.c_int)]),
     "ts_synchronize": (_c.c_int, []),
+    "ts_fusion_enable": (None, [_c.c_int]),
+    "ts_fusion_enabled": (_c.c_int, []),
     "ts_stream": (VP, []),
     "ts_pool_live_bytes": (SZ, []),
     "ts_pool_cached_bytes": (SZ, []),

@@ -31,8 +31,8 @@ void Adam::add_parameter(const Tensor &p) {
         s.m = std::make_shared<Allocation>(s.n);
         s.v = std::make_shared<Allocation>(s.n);
         void *st = Runtime::get().stream();
-        check(ts_hip_fill(s.m->ptr, 0.0f, s.n, st), "ts_hip_fill");
-        check(ts_hip_fill(s.v->ptr, 0.0f, s.n, st), "ts_hip_fill");
+        check(ts_hip_fill(s.m->get(), 0.0f, s.n, st), "ts_hip_fill");
+        check(ts_hip_fill(s.v->get(), 0.0f, s.n, st), "ts_hip_fill");
     }
     states_.emplace(p.id(), std::move(s));
     insertion_order_.push_back(p.id());
@@ -79,6 +79,8 @@ void Adam::step(const std::vector<Tensor *> &params) {
             first = 1;
         }
         if (!s.n) continue;
+        // p is updated in place: deferred products reading it run first
+        if (p->allocation()) p->allocation()->before_write();
         // parameters are independent: one launch steps up to 16 of them; a
         // parameter listed twice is stepped twice in order, so it starts a new launch
         for (const ts_hip_adam_param &q : batch)
@@ -86,8 +88,8 @@ void Adam::step(const std::vector<Tensor *> &params) {
                 flush();
                 break;
             }
-        batch.push_back(ts_hip_adam_param{p->dev_mut(), g->dev(), s.m->ptr, s.v->ptr,
-                                          config_.amsgrad ? s.v_hat_max->ptr : nullptr, s.n, first});
+        batch.push_back(ts_hip_adam_param{p->dev_mut(), g->dev(), s.m->get(), s.v->get(),
+                                          config_.amsgrad ? s.v_hat_max->get() : nullptr, s.n, first});
         bytes += 28.0 * s.n + (config_.amsgrad ? 8.0 * s.n : 0.0);
         if (batch.size() == TS_HIP_ADAM_MAX_PARAMS) flush();
     }
@@ -106,12 +108,12 @@ uint64_t Adam::parameter_step(size_t id) const {
 
 const float *Adam::state_m(size_t id) const {
     auto it = states_.find(id);
-    return (it == states_.end() || !it->second.m) ? nullptr : it->second.m->ptr;
+    return (it == states_.end() || !it->second.m) ? nullptr : it->second.m->get();
 }
 
 const float *Adam::state_v(size_t id) const {
     auto it = states_.find(id);
-    return (it == states_.end() || !it->second.v) ? nullptr : it->second.v->ptr;
+    return (it == states_.end() || !it->second.v) ? nullptr : it->second.v->get();
 }
 
 }  // namespace ts

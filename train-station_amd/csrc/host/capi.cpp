@@ -113,7 +113,9 @@ size_t ts_tensor_dims(const ts_tensor *t, size_t *out, size_t cap) {
     return d.size();
 }
 size_t ts_tensor_size(const ts_tensor *t) { return t ? t->t.size() : 0; }
-const float *ts_tensor_device_ptr(const ts_tensor *t) { return t ? t->t.dev() : nullptr; }
+const float *ts_tensor_device_ptr(const ts_tensor *t) {
+    return guard_ptr([&]() -> const float * { return t ? t->t.dev() : nullptr; });
+}
 
 int ts_tensor_with_requires_grad(ts_tensor *t) {
     return guard_int([&] {
@@ -439,6 +441,9 @@ int ts_adam_config_to_json(const float *values5, int amsgrad, char **json, size_
 int ts_adam_config_from_json(const char *json, size_t len, float *values5, int *amsgrad) {
     return guard_int([&] { put_config(ts::adam_config_from_json(text_of(json, len)), values5, amsgrad); });
 }
+
+void ts_fusion_enable(int on) { ts::set_fusion(on != 0); }
+int ts_fusion_enabled(void) { return ts::fusion_enabled() ? 1 : 0; }
 
 int ts_synchronize(void) {
     return guard_int([&] { ts::Runtime::get().sync(); });

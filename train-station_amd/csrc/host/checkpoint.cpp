@@ -110,12 +110,12 @@ std::vector<uint8_t> device_to_binary(const float *dev, const std::vector<size_t
         const float *src = dev;
         if (reinterpret_cast<uintptr_t>(src) & 15u) {
             aligned = std::make_unique<Allocation>(n);
-            check(ts_hip_copy(dev, aligned->ptr, n, stream()), "ts_hip_copy");
-            src = aligned->ptr;
+            check(ts_hip_copy(dev, aligned->get(), n, stream()), "ts_hip_copy");
+            src = aligned->get();
         }
         Allocation records((5 * n + 3) / 4);
-        check(ts_hip_encode_f32_records(src, n, records.ptr, stream()), "ts_hip_encode_f32_records");
-        check(ts_hip_memcpy_bytes(out.data() + kDataRecordsAt, records.ptr, 5 * n, 1, stream()),
+        check(ts_hip_encode_f32_records(src, n, records.get(), stream()), "ts_hip_encode_f32_records");
+        check(ts_hip_memcpy_bytes(out.data() + kDataRecordsAt, records.get(), 5 * n, 1, stream()),
               "ts_hip_memcpy_bytes");
         Runtime::get().sync();
     }
@@ -145,9 +145,9 @@ void upload_array(const Value &data, size_t n, float *dev) {
     if (!n) return;
     if (data.form == ser::ArrayForm::Records) {
         Allocation records((5 * n + 3) / 4);
-        check(ts_hip_memcpy_bytes(records.ptr, data.buf->data() + data.offset, 5 * n, 0, stream()),
+        check(ts_hip_memcpy_bytes(records.get(), data.buf->data() + data.offset, 5 * n, 0, stream()),
               "ts_hip_memcpy_bytes");
-        check(ts_hip_decode_f32_records(records.ptr, n, dev, nullptr, stream()),
+        check(ts_hip_decode_f32_records(records.get(), n, dev, nullptr, stream()),
               "ts_hip_decode_f32_records");
         Runtime::get().sync();
         return;
@@ -326,9 +326,9 @@ Fields Adam::to_fields(bool binary) const {
     for (size_t id : insertion_order_) {
         const State &s = states_.at(id);
         Fields st;
-        st.emplace_back("m", nested(s.m ? s.m->ptr : nullptr, s.dims));
-        st.emplace_back("v", nested(s.v ? s.v->ptr : nullptr, s.dims));
-        st.emplace_back("v_hat_max", s.v_hat_max ? Value::some(nested(s.v_hat_max->ptr, s.dims)) : Value::none());
+        st.emplace_back("m", nested(s.m ? s.m->get() : nullptr, s.dims));
+        st.emplace_back("v", nested(s.v ? s.v->get() : nullptr, s.dims));
+        st.emplace_back("v_hat_max", s.v_hat_max ? Value::some(nested(s.v_hat_max->get(), s.dims)) : Value::none());
         st.emplace_back("step", Value::usize(s.step));
         states.emplace_back(std::to_string(id), Value::object(std::move(st)));
     }
@@ -440,7 +440,7 @@ void Adam::relink_parameters(const std::vector<const Tensor *> &params) {
             auto dup = [&](const std::shared_ptr<Allocation> &a) -> std::shared_ptr<Allocation> {
                 if (!a) return a;
                 auto b = std::make_shared<Allocation>(s.n);
-                check(ts_hip_copy(a->ptr, b->ptr, s.n, stream()), "ts_hip_copy");
+                check(ts_hip_copy(a->get(), b->get(), s.n, stream()), "ts_hip_copy");
                 return b;
             };
             s.m = dup(s.m);

@@ -107,10 +107,23 @@ void DevicePool::empty_cache() {
 }
 
 Allocation::Allocation(size_t n_floats) : n(n_floats) {
-    ptr = DevicePool::get().acquire(n_floats, &rounded);
+    ptr_ = DevicePool::get().acquire(n_floats, &rounded);
 }
 
-Allocation::~Allocation() { DevicePool::get().release(ptr, rounded); }
+Allocation::~Allocation() { DevicePool::get().release(ptr_, rounded); }
+
+float *Allocation::get() {
+    if (pending) materialize(*this);
+    return ptr_;
+}
+
+void Allocation::before_write() {
+    std::vector<std::weak_ptr<Allocation>> rs;
+    rs.swap(readers);
+    for (auto &w : rs)
+        if (auto r = w.lock())
+            if (r->pending) materialize(*r);
+}
 
 // ---- profiler -----------------------------------------------------------------
 
@@ -121,40 +134,61 @@ Profiler &Profiler::get() {
 
 void Profiler::enable(bool on) {
     if (!on && enabled_) collect();
+    while (!open_.empty()) abort();
     enabled_ = on;
+}
+
+// Launches can nest: a deferred product runs when a later launch first reads
+// its result, inside that launch's window.  The outer window is then split
+// around the inner one, so each launch is charged only its own time.
+void *Profiler::event() {
+    void *ev = nullptr;
+    if (!spare_.empty()) { ev = spare_.back(); spare_.pop_back(); }
+    else check(ts_hip_event_create(&ev), "ts_hip_event_create");
+    check(ts_hip_event_record(ev, Runtime::get().stream()), "ts_hip_event_record");
+    return ev;
 }
 
 void Profiler::begin() {
     if (!enabled_) return;
-    void *ev = nullptr;
-    if (!spare_.empty()) { ev = spare_.back(); spare_.pop_back(); }
-    else check(ts_hip_event_create(&ev), "ts_hip_event_create");
-    check(ts_hip_event_record(ev, Runtime::get().stream()), "ts_hip_event_record");
-    open_ = ev;
+    if (!open_.empty()) open_.back().back().second = event();  // pause the enclosing launch
+    open_.push_back({{event(), nullptr}});
+}
+
+void Profiler::abort() {
+    if (!enabled_ || open_.empty()) return;
+    for (auto &seg : open_.back()) {
+        if (seg.first) spare_.push_back(seg.first);
+        if (seg.second) spare_.push_back(seg.second);
+    }
+    open_.pop_back();
+    if (!open_.empty()) open_.back().push_back({event(), nullptr});
 }
 
 void Profiler::end(KernelClass k, double work) {
-    if (!enabled_ || !open_) return;
-    void *ev = nullptr;
-    if (!spare_.empty()) { ev = spare_.back(); spare_.pop_back(); }
-    else check(ts_hip_event_create(&ev), "ts_hip_event_create");
-    check(ts_hip_event_record(ev, Runtime::get().stream()), "ts_hip_event_record");
-    pending_.push_back(Pending{open_, ev, k, work});
-    open_ = nullptr;
+    if (!enabled_ || open_.empty()) return;
+    open_.back().back().second = event();
+    pending_.push_back(Pending{std::move(open_.back()), k, work});
+    open_.pop_back();
+    if (!open_.empty()) open_.back().push_back({event(), nullptr});  // resume the enclosing one
 }
 
 void Profiler::collect() {
     if (pending_.empty()) return;
     check(ts_hip_stream_synchronize(Runtime::get().stream()), "ts_hip_stream_synchronize");
     for (auto &p : pending_) {
-        float ms = 0.0f;
-        check(ts_hip_event_elapsed_ms(&ms, p.start, p.stop), "ts_hip_event_elapsed_ms");
+        double ms = 0.0;
+        for (auto &seg : p.segments) {
+            float part = 0.0f;
+            check(ts_hip_event_elapsed_ms(&part, seg.first, seg.second), "ts_hip_event_elapsed_ms");
+            ms += part;
+            spare_.push_back(seg.first);
+            spare_.push_back(seg.second);
+        }
         auto &t = totals_[static_cast<int>(p.k)];
         t.ms += ms;
         t.work += p.work;
         t.launches += 1;
-        spare_.push_back(p.start);
-        spare_.push_back(p.stop);
     }
     pending_.clear();
 }

@@ -36,7 +36,12 @@ template <class F>
 void launch(KernelClass k, double work, const char *what, F &&f) {
     Profiler &P = Profiler::get();
     P.begin();
-    check(f(), what);
+    try {
+        check(f(), what);
+    } catch (...) {
+        P.abort();
+        throw;
+    }
     P.end(k, work);
 }
 
@@ -150,7 +155,7 @@ Tensor reduce_to(const Tensor &g, const std::vector<size_t> &target) {
         const size_t ws = ts_hip_sum_dim0_workspace_floats(rows, cols);
         Allocation work(ws);
         launch(KernelClass::Reduction, 4.0 * rows * cols + 4.0 * cols, "ts_hip_sum_dim0", [&] {
-            return ts_hip_sum_dim0(g.dev(), rows, cols, out.dev_mut(), work.ptr, ws, S());
+            return ts_hip_sum_dim0(g.dev(), rows, cols, out.dev_mut(), work.get(), ws, S());
         });
         return out;
     }
@@ -190,6 +195,49 @@ void axis_view(const std::vector<size_t> &dims, size_t dim, size_t &outer, size_
 }
 
 }  // namespace
+
+// ---- deferred products ------------------------------------------------------
+
+namespace {
+bool g_fusion = true;
+
+void add_reader(const std::shared_ptr<Allocation> &input, const std::shared_ptr<Allocation> &reader) {
+    if (!input) return;
+    auto &rs = input->readers;
+    size_t live = 0;  // drop readers that are gone or already produced
+    for (auto &w : rs) {
+        auto r = w.lock();
+        if (r && r->pending) rs[live++] = w;
+    }
+    rs.resize(live);
+    rs.push_back(reader);
+}
+}  // namespace
+
+void set_fusion(bool on) { g_fusion = on; }
+bool fusion_enabled() { return g_fusion; }
+
+void set_pending(const std::shared_ptr<Allocation> &out, std::shared_ptr<PendingGemm> p) {
+    add_reader(p->A, out);
+    add_reader(p->B, out);
+    add_reader(p->bias, out);
+    add_reader(p->mask, out);
+    out->pending = std::move(p);
+}
+
+void materialize(Allocation &a) {
+    std::shared_ptr<PendingGemm> p = std::move(a.pending);
+    a.pending.reset();
+    // inputs first (they may be deferred themselves), outside this launch's window
+    const float *A = p->A->get(), *B = p->B->get();
+    const float *bias = p->bias ? p->bias->get() : nullptr;
+    const float *mask = p->mask ? p->mask->get() : nullptr;
+    float *C = a.raw();
+    launch(KernelClass::Gemm, 2.0 * p->M * p->N * p->K, "ts_hip_gemm_fused", [&] {
+        return ts_hip_gemm_fused(p->ta, p->tb, p->M, p->N, p->K, A, p->lda, B, p->ldb, bias, p->relu ? 1 : 0,
+                                 mask, C, p->N, S());
+    });
+}
 
 size_t next_tensor_id() {
     // tensor/core/mod.rs:131: one process-wide atomic counter
@@ -235,6 +283,7 @@ static uint64_t seed_from_time() {
 void Tensor::fill_randn(const uint64_t *seed) {
     if (!size_) return;  // random.rs:271-273
     const uint64_t s = seed ? *seed : seed_from_time();
+    alloc_->before_write();
     launch(KernelClass::Elementwise, 4.0 * size_, "ts_hip_randn",
            [&] { return ts_hip_randn(dev_mut(), size_, s, S()); });
 }
@@ -325,11 +374,27 @@ void Tensor::record(Tensor &out, std::vector<size_t> input_ids, GradFn fn) const
     register_operation(out.id_, std::move(input_ids), std::move(fn));
 }
 
+// A deferred product [M, N] plus a row vector [N] (either order: fp32
+// addition is commutative) becomes the product with a bias epilogue.
+static bool fuse_bias(const Tensor &mat, const Tensor &vec) {
+    const auto &a = mat.allocation();
+    return fusion_enabled() && a && a->pending && a->pending->bare() && vec.allocation() &&
+           is_row_broadcast(mat.dims(), vec.dims());
+}
+
 Tensor Tensor::binary(const Tensor &o, GradFn::Kind kind) const {
     const bool same = dims_ == o.dims_;
     const int op = opcode(kind);
     Tensor out;
-    if (same) {
+    const bool fuse_self = kind == GradFn::Kind::Add && fuse_bias(*this, o);
+    const bool fuse_other = !fuse_self && kind == GradFn::Kind::Add && fuse_bias(o, *this);
+    if (fuse_self || fuse_other) {
+        const Tensor &mat = fuse_self ? *this : o, &vec = fuse_self ? o : *this;
+        out = new_uninit(mat.dims_);
+        auto p = std::make_shared<PendingGemm>(*mat.alloc_->pending);
+        p->bias = vec.alloc_;
+        set_pending(out.alloc_, std::move(p));
+    } else if (same) {
         out = same_shape(dev(), o.dev(), dims_, op);
     } else if (is_row_broadcast(dims_, o.dims_)) {
         out = row_bcast(dev(), o.dev(), dims_[0], dims_[1], op, false);
@@ -399,8 +464,14 @@ Tensor Tensor::div_scalar(float s) const { return scalar_op(s, GradFn::Kind::Div
 
 Tensor Tensor::relu() const {
     Tensor out = new_uninit(dims_);
-    launch(KernelClass::Elementwise, 8.0 * size_, "ts_hip_relu",
-           [&] { return ts_hip_relu(dev(), out.dev_mut(), size_, S()); });
+    if (fusion_enabled() && alloc_ && alloc_->pending && !alloc_->pending->relu && !alloc_->pending->mask) {
+        auto p = std::make_shared<PendingGemm>(*alloc_->pending);  // relu joins the deferred product
+        p->relu = true;
+        set_pending(out.alloc_, std::move(p));
+    } else {
+        launch(KernelClass::Elementwise, 8.0 * size_, "ts_hip_relu",
+               [&] { return ts_hip_relu(dev(), out.dev_mut(), size_, S()); });
+    }
     if (requires_grad_ && is_grad_enabled()) {
         GradFn fn{GradFn::Kind::Relu};
         // The reference saves its input (ops/relu.rs:80-87); the output has
@@ -483,7 +554,7 @@ Tensor gemv(int trans, const float *A, size_t rows, size_t cols, const float *x)
     std::unique_ptr<Allocation> work = ws ? std::make_unique<Allocation>(ws) : nullptr;
     launch(trans ? KernelClass::Reduction : KernelClass::Elementwise, 4.0 * rows * cols + 4.0 * (rows + cols),
            "ts_hip_gemv", [&] {
-               return ts_hip_gemv(trans, rows, cols, A, cols, x, y.dev_mut(), work ? work->ptr : nullptr, ws, S());
+               return ts_hip_gemv(trans, rows, cols, A, cols, x, y.dev_mut(), work ? work->get() : nullptr, ws, S());
            });
     return y;
 }
@@ -508,7 +579,7 @@ Tensor Tensor::matmul(const Tensor &o) const {
         const size_t ws = ts_hip_sum_workspace_floats(size_);
         Allocation work(ws);
         launch(KernelClass::Reduction, 8.0 * size_ + 4.0, "ts_hip_dot",
-               [&] { return ts_hip_dot(dev(), o.dev(), size_, out.dev_mut(), work.ptr, ws, S()); });
+               [&] { return ts_hip_dot(dev(), o.dev(), size_, out.dev_mut(), work.get(), ws, S()); });
     } else if (ra == 1 && rb == 2) {  // vector_matrix_mult (:352-420)
         if (dims_[0] != o.dims_[0]) throw Error("Vector length must match matrix rows");
         out = gemv(1, o.dev(), o.dims_[0], o.dims_[1], dev());
@@ -520,9 +591,17 @@ Tensor Tensor::matmul(const Tensor &o) const {
         if (k != o.dims_[0])
             throw Error("Inner dimensions must match: " + std::to_string(k) + " vs " + std::to_string(o.dims_[0]));
         out = new_uninit({m, n});
-        launch(KernelClass::Gemm, 2.0 * m * n * k, "ts_hip_gemm", [&] {
-            return ts_hip_gemm(0, 0, m, n, k, dev(), k, o.dev(), n, out.dev_mut(), n, S());
-        });
+        if (fusion_enabled() && out.size_ && k) {  // deferred: a following bias add / relu joins it
+            auto p = std::make_shared<PendingGemm>();
+            p->M = m; p->N = n; p->K = k; p->lda = k; p->ldb = n;
+            p->A = alloc_;
+            p->B = o.alloc_;
+            set_pending(out.alloc_, std::move(p));
+        } else {
+            launch(KernelClass::Gemm, 2.0 * m * n * k, "ts_hip_gemm", [&] {
+                return ts_hip_gemm(0, 0, m, n, k, dev(), k, o.dev(), n, out.dev_mut(), n, S());
+            });
+        }
     } else {  // batched_matmul (:634-760)
         if (ra < 2 || rb < 2) throw Error("Batched matmul requires at least 2D tensors");
         const size_t m = dims_[ra - 2], k = dims_[ra - 1], k2 = o.dims_[rb - 2], n = o.dims_[rb - 1];
@@ -546,7 +625,7 @@ Tensor Tensor::sum() const {
     const size_t ws = ts_hip_sum_workspace_floats(size_);
     Allocation work(ws);
     launch(KernelClass::Reduction, 4.0 * size_ + 4.0, "ts_hip_sum",
-           [&] { return ts_hip_sum(dev(), size_, out.dev_mut(), work.ptr, ws, S()); });
+           [&] { return ts_hip_sum(dev(), size_, out.dev_mut(), work.get(), ws, S()); });
     if (requires_grad_) {  // reductions/sum.rs:131-138 (no is_grad_enabled check)
         GradFn fn{GradFn::Kind::ReduceSum};
         fn.input_shape = dims_;
@@ -560,7 +639,7 @@ Tensor Tensor::mean() const {
     const size_t ws = ts_hip_sum_workspace_floats(size_);
     Allocation work(ws);
     launch(KernelClass::Reduction, 4.0 * size_ + 4.0, "ts_hip_mean",
-           [&] { return ts_hip_mean(dev(), size_, out.dev_mut(), work.ptr, ws, S()); });
+           [&] { return ts_hip_mean(dev(), size_, out.dev_mut(), work.get(), ws, S()); });
     if (requires_grad_) {  // reductions/mean.rs:97-106
         GradFn fn{GradFn::Kind::ReduceMean};
         fn.input_shape = dims_;
@@ -804,9 +883,17 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
         }
         case K::Relu: {  // grad_fn/ops/relu.rs:4-17 (saved[0] is the relu output)
             Tensor g = Tensor::new_uninit(go.dims());
-            launch(KernelClass::Elementwise, 12.0 * n, "ts_hip_relu_backward", [&] {
-                return ts_hip_relu_backward(saved[0].ptr(), go.dev(), g.dev_mut(), n, S());
-            });
+            const auto &ga = go.allocation();
+            if (fusion_enabled() && ga && ga->pending && ga->pending->bare() && saved[0].alloc) {
+                // the incoming gradient is a deferred dX product: mask it in its store
+                auto p = std::make_shared<PendingGemm>(*ga->pending);
+                p->mask = saved[0].alloc;
+                set_pending(g.allocation(), std::move(p));
+            } else {
+                launch(KernelClass::Elementwise, 12.0 * n, "ts_hip_relu_backward", [&] {
+                    return ts_hip_relu_backward(saved[0].ptr(), go.dev(), g.dev_mut(), n, S());
+                });
+            }
             r.emplace_back(std::move(g));
             break;
         }
@@ -837,9 +924,19 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
                 const size_t M = a.dims[0], Kd = a.dims[1], N = b.dims[1];
                 if (req_left) {  // go[M,N] . b[Kd,N]^T -> [M,Kd]
                     Tensor t = Tensor::new_uninit({M, Kd});
-                    launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm(dX)", [&] {
-                        return ts_hip_gemm(0, 1, M, Kd, N, go.dev(), N, b.ptr(), N, t.dev_mut(), Kd, S());
-                    });
+                    if (fusion_enabled() && t.size() && N && go.allocation() && b.alloc) {
+                        // deferred: relu's backward, usually next, joins it as a mask
+                        auto p = std::make_shared<PendingGemm>();
+                        p->ta = 0; p->tb = 1;
+                        p->M = M; p->N = Kd; p->K = N; p->lda = N; p->ldb = N;
+                        p->A = go.allocation();
+                        p->B = b.alloc;
+                        set_pending(t.allocation(), std::move(p));
+                    } else {
+                        launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm(dX)", [&] {
+                            return ts_hip_gemm(0, 1, M, Kd, N, go.dev(), N, b.ptr(), N, t.dev_mut(), Kd, S());
+                        });
+                    }
                     gl = std::move(t);
                 }
                 if (req_right) {  // a[M,Kd]^T . go[M,N] -> [Kd,N]

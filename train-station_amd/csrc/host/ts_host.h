@@ -23,6 +23,7 @@
 #include <stdexcept>
 #include <string>
 #include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "ts_serial.h"
@@ -73,6 +74,23 @@ class DevicePool {
     size_t live_ = 0, cached_ = 0;
 };
 
+struct Allocation;
+
+// A deferred producer of an allocation's contents: C = op(A) . op(B) with the
+// epilogue of ts_hip_gemm_fused (row bias, relu, relu-backward mask), run when
+// the contents are first needed.  matmul returns its product deferred; a
+// following broadcast bias add, relu, or (in backward) relu's gradient of the
+// dX product extends the producer instead of launching a pass of its own, so
+// the chain runs as one kernel and intermediates nobody reads are never
+// written.  Results are the bits of the unfused ops.
+struct PendingGemm {
+    int ta = 0, tb = 0;
+    size_t M = 0, N = 0, K = 0, lda = 0, ldb = 0;
+    std::shared_ptr<Allocation> A, B, bias, mask;
+    bool relu = false;
+    bool bare() const { return !bias && !mask && !relu; }
+};
+
 // Device variant of tensor/core/allocation.rs:43-187: owns one pooled device
 // buffer; shared (Arc-like) by tensors, saved graph operands and gradients.
 struct Allocation {
@@ -80,9 +98,28 @@ struct Allocation {
     ~Allocation();
     Allocation(const Allocation &) = delete;
     Allocation &operator=(const Allocation &) = delete;
-    float *ptr = nullptr;
+    // The device buffer, after running a pending producer.
+    float *get();
+    // The device buffer as it is (for the producer itself and the pool).
+    float *raw() const { return ptr_; }
+    // Before this buffer is written in place: runs every still-pending
+    // producer that reads it, so they see the old contents.
+    void before_write();
+    std::shared_ptr<PendingGemm> pending;
+    std::vector<std::weak_ptr<Allocation>> readers;  // pending allocations reading this one
     size_t n = 0, rounded = 0;
+
+  private:
+    float *ptr_ = nullptr;
 };
+
+// Runs a's pending producer (tensor.cpp).
+void materialize(Allocation &a);
+// Makes `out` pending on p and records it as a reader of p's inputs.
+void set_pending(const std::shared_ptr<Allocation> &out, std::shared_ptr<PendingGemm> p);
+// Fusion switch (on by default): off, every op launches its own kernels.
+void set_fusion(bool on);
+bool fusion_enabled();
 
 // ---- profiling ----------------------------------------------------------------
 
@@ -104,19 +141,22 @@ class Profiler {
     bool enabled() const { return enabled_; }
     void begin();
     void end(KernelClass k, double work);
+    void abort();  // the launch failed: drop its window
     // Synchronises and folds every recorded launch into the totals.
     void collect();
     ClassStats stats(KernelClass k) const { return totals_[static_cast<int>(k)]; }
     void reset();
 
   private:
+    using Segments = std::vector<std::pair<void *, void *>>;  // (start, stop) event pairs
     struct Pending {
-        void *start, *stop;
+        Segments segments;
         KernelClass k;
         double work;
     };
+    void *event();
     bool enabled_ = false;
-    void *open_ = nullptr;
+    std::vector<Segments> open_;  // launches in progress, innermost last
     std::vector<Pending> pending_;
     std::vector<void *> spare_;
     ClassStats totals_[static_cast<int>(KernelClass::kCount)];
@@ -129,7 +169,7 @@ class Tensor;
 struct SavedTensor {
     std::shared_ptr<Allocation> alloc;
     std::vector<size_t> dims;
-    const float *ptr() const { return alloc ? alloc->ptr : nullptr; }
+    const float *ptr() const { return alloc ? alloc->get() : nullptr; }
 };
 
 // GradFn variants on the training-step path (gradtrack/grad_fn/mod.rs:127-450).
@@ -195,9 +235,9 @@ class Tensor {
     size_t id() const { return id_; }
     const std::vector<size_t> &dims() const { return dims_; }
     size_t size() const { return size_; }
-    const float *dev() const { return alloc_ ? alloc_->ptr : nullptr; }
+    const float *dev() const { return alloc_ ? alloc_->get() : nullptr; }
     const std::shared_ptr<Allocation> &allocation() const { return alloc_; }
-    float *dev_mut() { return alloc_ ? alloc_->ptr : nullptr; }
+    float *dev_mut() { return alloc_ ? alloc_->get() : nullptr; }
     SavedTensor saved() const { return SavedTensor{alloc_, dims_}; }
     static Tensor from_saved(const SavedTensor &s);
 

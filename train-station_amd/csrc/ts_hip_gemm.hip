@@ -72,7 +72,75 @@ struct GemmArgs {
     int bdims[kMaxBatchRank];
     long long sa[kMaxBatchRank], sb[kMaxBatchRank];
     long long sc;
+    // Epilogue (plain form only; all null / 0 for a bare product): the stored
+    // value is the product, plus bias[j] when bias is set, then max(., +0) as
+    // relu does when relu is set, then kept only where mask[i*ldc + j] > 0
+    // (relu's backward with its saved output) when mask is set.
+    const float *bias;
+    const float *mask;
+    int relu;
 };
+
+// Store of a wave's FM x FN accumulator blocks, the wave tile's corner at
+// (i0, j0).  Accumulator layout of v_mfma_f32_32x32x2_f32: lane l, register
+// r holds C[8*(r/4) + 4*(l/32) + r%4][l%32] of the 32x32 block.  With EPI the
+// stored value is the product, plus bias[j], then max(., +0) (relu), then
+// kept only where mask[i*ldc + j] > 0: the unfused ops in their order.  A row
+// of blocks at a time: its mask is loaded before its first store, so those
+// loads overlap each other (every block's at once would need a register per
+// output element).  EPI is one of the kinds below; kEpiBiasRelu ignores
+// the mask, so a kernel that never sees one keeps no registers for it.
+enum : int { kEpiNone = 0, kEpiBiasRelu = 1, kEpiAll = 2 };
+
+template <int EPI, int FM, int FN>
+__device__ __forceinline__ void store_tile(const GemmArgs &g, const floatx16 (&acc)[FM][FN], float *Cp, int i0,
+                                           int j0, int lrow, int lhalf) {
+    float bj[FN];  // bias of the lane's column in each block column
+#pragma unroll
+    for (int b = 0; b < FN; ++b) {
+        const int j = j0 + b * 32 + lrow;
+        bj[b] = (EPI != kEpiNone && g.bias && j < g.N) ? g.bias[j] : 0.0f;
+    }
+#pragma unroll
+    for (int a = 0; a < FM; ++a) {
+        float mk[FN][16];
+        if (EPI == kEpiAll && g.mask) {
+#pragma unroll
+            for (int b = 0; b < FN; ++b) {
+                const int j = j0 + b * 32 + lrow;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int i = i0 + a * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+                    mk[b][r] = (i < g.M && j < g.N) ? g.mask[(size_t)i * g.ldc + j] : 0.0f;
+                }
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < FN; ++b) {
+            const int j = j0 + b * 32 + lrow;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int i = i0 + a * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+                float v = acc[a][b][r];
+                if (EPI != kEpiNone) {
+                    if (g.bias) v = v + bj[b];
+                    if (g.relu) v = v > 0.0f ? v : 0.0f;
+                    if (EPI == kEpiAll && g.mask) v = mk[b][r] > 0.0f ? v : 0.0f;
+                }
+                if (i < g.M && j < g.N) Cp[(size_t)i * g.ldc + j] = v;
+            }
+        }
+        if (EPI == kEpiAll) __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// The epilogue of one element of the split-K sum (store_tile's, elementwise).
+__device__ __forceinline__ float epilogue(const GemmArgs &g, float v, int i, int j) {
+    if (g.bias) v = v + g.bias[j];
+    if (g.relu) v = v > 0.0f ? v : 0.0f;
+    if (g.mask) v = g.mask[(size_t)i * g.ldc + j] > 0.0f ? v : 0.0f;
+    return v;
+}
 
 // Staging of one operand tile: logical [BK][R] (k-major), R = 128 or 256
 // rows of the operand's non-k index.  KCONTIG: k is the contiguous index in
@@ -162,7 +230,9 @@ __device__ inline void tile_coords(int tiles_m, int tiles_n, int b, int &tm, int
     tn = in_group / gsz;
 }
 
-template <bool TA, bool TB, int BM, int BN, int WM, int WN>
+// EPI: the epilogue kind applied at the store (a separate instantiation per
+// kind, so the bare product keeps its register allocation).
+template <bool TA, bool TB, int BM, int BN, int WM, int WN, int EPI>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
     constexpr int NT = 64 * WM * WN;
     constexpr int TMW = BM / WM, TNW = BN / WN;  // wave tile
@@ -265,20 +335,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
         __syncthreads();
     }
 
-    // Accumulator layout of v_mfma_f32_32x32x2_f32: lane l, register r holds
-    // C[8*(r/4) + 4*(l/32) + r%4][l%32] of the 32x32 block.
-#pragma unroll
-    for (int a = 0; a < FM; ++a) {
-#pragma unroll
-        for (int b = 0; b < FN; ++b) {
-            const int j = j0 + wn * TNW + b * 32 + lrow;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int i = i0 + wm * TMW + a * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-                if (i < g.M && j < g.N) Cp[(size_t)i * g.ldc + j] = acc[a][b][r];
-            }
-        }
-    }
+    store_tile<EPI, FM, FN>(g, acc, Cp, i0 + wm * TMW, j0 + wn * TNW, lrow, lhalf);
+}
+
+template <int BM, int BN, int WM, int WN, int EPI>
+static void launch_tiles_as(int ta, int tb, const GemmArgs &g, dim3 grid, dim3 block, hipStream_t s) {
+    if (!ta && !tb) hipLaunchKernelGGL((gemm_f32_mfma<false, false, BM, BN, WM, WN, EPI>), grid, block, 0, s, g);
+    else if (!ta && tb) hipLaunchKernelGGL((gemm_f32_mfma<false, true, BM, BN, WM, WN, EPI>), grid, block, 0, s, g);
+    else if (ta && !tb) hipLaunchKernelGGL((gemm_f32_mfma<true, false, BM, BN, WM, WN, EPI>), grid, block, 0, s, g);
+    else hipLaunchKernelGGL((gemm_f32_mfma<true, true, BM, BN, WM, WN, EPI>), grid, block, 0, s, g);
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -288,10 +353,8 @@ static void launch_tiles(int ta, int tb, GemmArgs g, hipStream_t s, unsigned bat
     g.tiles = g.tiles_m * g.tiles_n;
     dim3 grid(static_cast<unsigned>(g.tiles) * batches);
     dim3 block(64 * WM * WN);
-    if (!ta && !tb) hipLaunchKernelGGL((gemm_f32_mfma<false, false, BM, BN, WM, WN>), grid, block, 0, s, g);
-    else if (!ta && tb) hipLaunchKernelGGL((gemm_f32_mfma<false, true, BM, BN, WM, WN>), grid, block, 0, s, g);
-    else if (ta && !tb) hipLaunchKernelGGL((gemm_f32_mfma<true, false, BM, BN, WM, WN>), grid, block, 0, s, g);
-    else hipLaunchKernelGGL((gemm_f32_mfma<true, true, BM, BN, WM, WN>), grid, block, 0, s, g);
+    if (g.bias || g.mask || g.relu) launch_tiles_as<BM, BN, WM, WN, kEpiAll>(ta, tb, g, grid, block, s);
+    else launch_tiles_as<BM, BN, WM, WN, kEpiNone>(ta, tb, g, grid, block, s);
 }
 
 
@@ -385,7 +448,7 @@ struct DmaStage {
 // 256x256 tiles, WM x WN waves.  SCHED 1 spreads the next step pair's LDS
 // reads over the current pair's MFMAs; SCHED 0 issues them as one group
 // ahead of the MFMAs (measured per layout, see the launcher).
-template <bool TA, bool TB, int WM, int WN, int SCHED>
+template <bool TA, bool TB, int WM, int WN, int SCHED, int EPI>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_lds_dma(GemmArgs g) {
     constexpr int BM = 256, BN = 256, NW = WM * WN;
     constexpr int TMW = BM / WM, TNW = BN / WN, FM = TMW / 32, FN = TNW / 32, PAIRS = kBK / 4;
@@ -514,43 +577,33 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_lds_dma(GemmArgs g) {
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA outstanding at exit
 
-#pragma unroll
-    for (int a = 0; a < FM; ++a) {
-#pragma unroll
-        for (int b = 0; b < FN; ++b) {
-            const int j = j0 + wn * TNW + b * 32 + lrow;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int i = i0 + wm * TMW + a * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-                if (i < g.M && j < g.N) Cp[(size_t)i * g.ldc + j] = acc[a][b][r];
-            }
-        }
-    }
+    store_tile<EPI, FM, FN>(g, acc, Cp, i0 + wm * TMW, j0 + wn * TNW, lrow, lhalf);
 }
 
 // Split-K: C[i][j] = sum over s of the slice products P_s[i][j] (P_s at
 // P + s*M*N, row-major M x N), added in slice order.
 __global__ __launch_bounds__(kBlock) void splitk_sum(const float *__restrict__ P, int slices, size_t M, size_t N,
-                                                     float *__restrict__ C, size_t ldc) {
+                                                     float *__restrict__ C, size_t ldc, GemmArgs e) {
     const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
     const size_t mn = M * N;
     if (t >= mn) return;
     float acc = P[t];
     for (int k = 1; k < slices; ++k) acc += P[static_cast<size_t>(k) * mn + t];
-    C[(t / N) * ldc + t % N] = acc;
+    const size_t i = t / N, j = t % N;
+    C[i * ldc + j] = epilogue(e, acc, static_cast<int>(i), static_cast<int>(j));
 }
 
-template <int WM, int WN, int SCHED>
+template <int WM, int WN, int SCHED, int EPI>
 static void launch_dma(int ta, int tb, GemmArgs g, hipStream_t s, unsigned batches) {
     g.tiles_m = (g.M + 255) / 256;
     g.tiles_n = (g.N + 255) / 256;
     g.tiles = g.tiles_m * g.tiles_n;
     dim3 grid(static_cast<unsigned>(g.tiles) * batches);
     dim3 block(64 * WM * WN);
-    if (!ta && !tb) hipLaunchKernelGGL((gemm_f32_lds_dma<false, false, WM, WN, SCHED>), grid, block, 0, s, g);
-    else if (!ta && tb) hipLaunchKernelGGL((gemm_f32_lds_dma<false, true, WM, WN, SCHED>), grid, block, 0, s, g);
-    else if (ta && !tb) hipLaunchKernelGGL((gemm_f32_lds_dma<true, false, WM, WN, SCHED>), grid, block, 0, s, g);
-    else hipLaunchKernelGGL((gemm_f32_lds_dma<true, true, WM, WN, SCHED>), grid, block, 0, s, g);
+    if (!ta && !tb) hipLaunchKernelGGL((gemm_f32_lds_dma<false, false, WM, WN, SCHED, EPI>), grid, block, 0, s, g);
+    else if (!ta && tb) hipLaunchKernelGGL((gemm_f32_lds_dma<false, true, WM, WN, SCHED, EPI>), grid, block, 0, s, g);
+    else if (ta && !tb) hipLaunchKernelGGL((gemm_f32_lds_dma<true, false, WM, WN, SCHED, EPI>), grid, block, 0, s, g);
+    else hipLaunchKernelGGL((gemm_f32_lds_dma<true, true, WM, WN, SCHED, EPI>), grid, block, 0, s, g);
 }
 
 }  // namespace tship
@@ -582,11 +635,23 @@ static int gemm_launch(int trans_a, int trans_b, size_t M, size_t N, size_t K, c
     const size_t mid_tiles = ((M + 127) / 128) * ((N + 127) / 128) * batches;
     const unsigned nb = static_cast<unsigned>(batches);
     if (big_tiles >= static_cast<size_t>(device_cu_count())) {
+        const bool epi = g.bias || g.mask || g.relu;
         if (!g.vec) launch_tiles<256, 256, 2, 4>(trans_a, trans_b, g, s, nb);
-        // wave grid and read order per layout: the fastest measured at 8192x4096x4096
-        else if (!trans_a && !trans_b) launch_dma<2, 2, 1>(trans_a, trans_b, g, s, nb);
-        else if (!trans_a && trans_b) launch_dma<2, 4, 0>(trans_a, trans_b, g, s, nb);
-        else launch_dma<2, 4, 1>(trans_a, trans_b, g, s, nb);
+        // wave grid and read order per layout: the fastest measured at 8192x4096x4096.
+        // A mask epilogue on NN takes the 8-wave grid: the 4-wave one holds
+        // its accumulators in AGPRs and has no registers left for a row of
+        // mask values (it spills); bias and relu alone fit.
+        else if (!trans_a && !trans_b) {
+            if (g.mask) launch_dma<2, 4, 1, kEpiAll>(trans_a, trans_b, g, s, nb);
+            else if (epi) launch_dma<2, 2, 1, kEpiBiasRelu>(trans_a, trans_b, g, s, nb);
+            else launch_dma<2, 2, 1, kEpiNone>(trans_a, trans_b, g, s, nb);
+        } else if (!trans_a && trans_b) {
+            if (epi) launch_dma<2, 4, 0, kEpiAll>(trans_a, trans_b, g, s, nb);
+            else launch_dma<2, 4, 0, kEpiNone>(trans_a, trans_b, g, s, nb);
+        } else {
+            if (epi) launch_dma<2, 4, 1, kEpiAll>(trans_a, trans_b, g, s, nb);
+            else launch_dma<2, 4, 1, kEpiNone>(trans_a, trans_b, g, s, nb);
+        }
     } else if (2 * mid_tiles >= static_cast<size_t>(device_cu_count())) {
         launch_tiles<128, 128, 2, 2>(trans_a, trans_b, g, s, nb);
     } else {
@@ -595,14 +660,19 @@ static int gemm_launch(int trans_a, int trans_b, size_t M, size_t N, size_t K, c
     return launch_status();
 }
 
-extern "C" int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
-                           size_t lda, const float *B, size_t ldb, float *C, size_t ldc,
-                           void *stream) {
+// One 2-D product with an optional epilogue (GemmArgs::bias / mask / relu).
+static int gemm_plain(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A, size_t lda,
+                      const float *B, size_t ldb, float *C, size_t ldc, const float *bias, const float *mask,
+                      int relu, void *stream) {
     if (M == 0 || N == 0) return TS_HIP_OK;
     if (!C || ldc < N) return TS_HIP_EINVAL;
-    if (K == 0) {  // empty contraction: C = 0
+    if (K == 0) {  // empty contraction: C = 0, then the epilogue
         if (ldc != N) return TS_HIP_EINVAL;
-        return ts_hip_fill(C, 0.0f, M * N, stream);
+        int st = ts_hip_fill(C, 0.0f, M * N, stream);
+        if (st == TS_HIP_OK && bias) st = ts_hip_row_broadcast(0, C, bias, C, M, N, 0, 0, nullptr, stream);
+        if (st == TS_HIP_OK && relu) st = ts_hip_relu(C, C, M * N, stream);
+        if (st == TS_HIP_OK && mask) st = ts_hip_relu_backward(mask, C, C, M * N, stream);
+        return st;
     }
     // Few output tiles and a long K: split K into S slices computed as a
     // batch (slice s reads A and B from k = s*K/S on) into a stream-ordered
@@ -623,6 +693,11 @@ extern "C" int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t 
         float *P = nullptr;
         if (hipMallocAsync(reinterpret_cast<void **>(&P), slices * M * N * sizeof(float), st) == hipSuccess) {
             const size_t kc = K / slices;
+            GemmArgs e{};  // epilogue after the slice sum
+            e.bias = bias;
+            e.mask = mask;
+            e.relu = relu;
+            e.ldc = static_cast<int>(ldc);
             GemmArgs g{};
             g.batch_rank = 1;
             g.bdims[0] = slices;
@@ -633,7 +708,7 @@ extern "C" int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t 
             if (status == TS_HIP_OK) {
                 const size_t blocks = (M * N + kBlock - 1) / kBlock;
                 hipLaunchKernelGGL(splitk_sum, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, st, P, slices, M,
-                                   N, C, ldc);
+                                   N, C, ldc, e);
                 status = launch_status();
             }
             const hipError_t fe = hipFreeAsync(P, st);
@@ -642,7 +717,22 @@ extern "C" int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t 
         (void)hipGetLastError();  // no stream-ordered allocation: run unsplit
     }
     GemmArgs g{};
+    g.bias = bias;
+    g.mask = mask;
+    g.relu = relu;
     return gemm_launch(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, g, 1, stream);
+}
+
+extern "C" int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
+                           size_t lda, const float *B, size_t ldb, float *C, size_t ldc,
+                           void *stream) {
+    return gemm_plain(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, nullptr, nullptr, 0, stream);
+}
+
+extern "C" int ts_hip_gemm_fused(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
+                                 size_t lda, const float *B, size_t ldb, const float *bias, int relu,
+                                 const float *mask, float *C, size_t ldc, void *stream) {
+    return gemm_plain(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, bias, mask, relu != 0, stream);
 }
 
 extern "C" int ts_hip_gemm_batched(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,

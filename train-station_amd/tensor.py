@@ -436,6 +436,17 @@ def clear_gradients() -> None:
     _G.ts_clear_gradients()
 
 
+def set_fusion(on: bool) -> None:
+    """Fuse a 2-D matmul with a following row-bias add and relu (and, in
+    backward, the dX product with relu's gradient) into one kernel; results
+    are bit-identical either way.  On by default."""
+    _G.ts_fusion_enable(1 if on else 0)
+
+
+def fusion_enabled() -> bool:
+    return bool(_G.ts_fusion_enabled())
+
+
 def synchronize() -> None:
     _ok(_G.ts_synchronize())
 
