@@ -91,6 +91,9 @@ struct GemmArgs {
 // output element).  EPI is one of the kinds below; kEpiBiasRelu ignores
 // the mask, so a kernel that never sees one keeps no registers for it.
 enum : int { kEpiNone = 0, kEpiBiasRelu = 1, kEpiAll = 2 };
+// s_waitcnt immediate for vmcnt(0) with expcnt and lgkmcnt left at their
+// maxima (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8]).
+constexpr int kWaitVm0 = 0x0F70;
 
 template <int EPI, int FM, int FN>
 __device__ __forceinline__ void store_tile(const GemmArgs &g, const floatx16 (&acc)[FM][FN], float *Cp, int i0,
@@ -101,6 +104,19 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const floatx16 (&a
         const int j = j0 + b * 32 + lrow;
         bj[b] = (EPI != kEpiNone && g.bias && j < g.N) ? g.bias[j] : 0.0f;
     }
+    // Wait for the bias here, once.  Left to the compiler, the wait lands in
+    // every guarded store's branch, and as a full vmcnt(0) (the load may be
+    // pending on the path that skipped the previous store), so each store
+    // would wait for all earlier ones to complete.
+    if (EPI != kEpiNone) __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    auto value = [&](float v, int b, float m) {
+        if (EPI != kEpiNone) {
+            if (g.bias) v = v + bj[b];
+            if (g.relu) v = v > 0.0f ? v : 0.0f;
+            if (EPI == kEpiAll && g.mask) v = m > 0.0f ? v : 0.0f;
+        }
+        return v;
+    };
 #pragma unroll
     for (int a = 0; a < FM; ++a) {
         float mk[FN][16];
@@ -114,6 +130,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const floatx16 (&a
                     mk[b][r] = (i < g.M && j < g.N) ? g.mask[(size_t)i * g.ldc + j] : 0.0f;
                 }
             }
+            __builtin_amdgcn_s_waitcnt(kWaitVm0);  // as for the bias
         }
 #pragma unroll
         for (int b = 0; b < FN; ++b) {
@@ -121,13 +138,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs &g, const floatx16 (&a
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int i = i0 + a * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-                float v = acc[a][b][r];
-                if (EPI != kEpiNone) {
-                    if (g.bias) v = v + bj[b];
-                    if (g.relu) v = v > 0.0f ? v : 0.0f;
-                    if (EPI == kEpiAll && g.mask) v = mk[b][r] > 0.0f ? v : 0.0f;
-                }
-                if (i < g.M && j < g.N) Cp[(size_t)i * g.ldc + j] = v;
+                if (i < g.M && j < g.N) Cp[(size_t)i * g.ldc + j] = value(acc[a][b][r], b, mk[b][r]);
             }
         }
         if (EPI == kEpiAll) __builtin_amdgcn_sched_barrier(0);
@@ -268,7 +279,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
     int tm, tn;
     tile_coords(g.tiles_m, g.tiles_n, bid, tm, tn);
     const int i0 = tm * BM, j0 = tn * BN;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WN, wn = wave % WN;
     const int lrow = lane & 31, lhalf = lane >> 5;
 
