@@ -100,6 +100,21 @@ def pmc_traffic(cfg_name: str):
     return (float(m.group(1)), str(path.relative_to(ROOT))) if m else (None, None)
 
 
+def host_info():
+    """The host the CPU baseline ran on: CPU model, logical cores present and
+    cores this process may use (the baseline itself uses one)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "host_cores": os.cpu_count(), "usable_cores": len(os.sched_getaffinity(0))}
+
+
 def cpu_baseline(cfg_name: str, sample_rows: int):
     """Single-core CPU restatement (oracle/) of one config-5 step, timed on a
     bounded sample and scaled: the three GEMM layouts on `sample_rows` output
@@ -158,7 +173,7 @@ def cpu_baseline(cfg_name: str, sample_rows: int):
               f"elementwise/reduction passes on 1/64 of the activations, Adam on 1/16 of "
               f"{P} params; scaled to one full step ({total:.1f} s)")
     return {"value": 1.0 / total, "unit": "steps/s", "cores": 1, "kind": "port",
-            "sample": sample, "breakdown_s": {k: round(v, 3) for k, v in timings.items()}}
+            "sample": sample, "breakdown_s": {k: round(v, 3) for k, v in timings.items()}, "host": host_info()}
 
 
 def cpu_baseline_chain(sample: int):
@@ -178,7 +193,7 @@ def cpu_baseline_chain(sample: int):
     G.clear_gradients()
     return {"value": 1.0 / dt, "unit": "steps/s", "cores": 1, "kind": "port",
             "sample": f"forward chain + backward through the restated engine on {sample} of {CHAIN_N} "
-                      f"elements, scaled to one full step ({dt:.2f} s)"}
+                      f"elements, scaled to one full step ({dt:.2f} s)", "host": host_info()}
 
 
 def cpu_baseline_adam(sample: int):
@@ -195,7 +210,7 @@ def cpu_baseline_adam(sample: int):
     O.adam_step(p, g, m, v, 1)
     dt = (time.perf_counter() - t0) * (ADAM_P / sample)
     return {"value": 1.0 / dt, "unit": "steps/s", "cores": 1, "kind": "port",
-            "sample": f"one Adam step on {sample} of {ADAM_P} parameters, scaled ({dt:.2f} s)"}
+            "sample": f"one Adam step on {sample} of {ADAM_P} parameters, scaled ({dt:.2f} s)", "host": host_info()}
 
 
 def bandwidth_main(args, TS, hip, hip_check) -> int:
