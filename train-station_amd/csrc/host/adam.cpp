@@ -48,13 +48,11 @@ void Adam::step(const std::vector<Tensor *> &params) {
     double bytes = 0.0;
     auto flush = [&]() {
         if (batch.empty()) return;
-        Profiler &P = Profiler::get();
-        P.begin();
-        check(ts_hip_adam_step_multi(batch.data(), batch.size(), config_.learning_rate, config_.beta1,
-                                     config_.beta2, config_.eps, config_.weight_decay, step_count_,
-                                     Runtime::get().stream()),
-              "ts_hip_adam_step_multi");
-        P.end(KernelClass::Adam, bytes);
+        launch(KernelClass::Adam, bytes, "ts_hip_adam_step_multi", [&] {
+            return ts_hip_adam_step_multi(batch.data(), batch.size(), config_.learning_rate, config_.beta1,
+                                          config_.beta2, config_.eps, config_.weight_decay, step_count_,
+                                          Runtime::get().stream());
+        });
         batch.clear();
         bytes = 0.0;
     };

@@ -40,11 +40,10 @@ void accumulate_gradient(size_t id, Tensor g) {
     Tensor &existing = it->second;
     Tensor sum = Tensor::new_uninit(existing.dims());
     const size_t n = sum.size();
-    Profiler &P = Profiler::get();
-    P.begin();
-    check(ts_hip_add(existing.dev(), g.dev(), sum.dev_mut(), n, Runtime::get().stream()),
-          "ts_hip_add(accumulate)");
-    P.end(KernelClass::Elementwise, 12.0 * n);
+    const float *a = existing.dev(), *b = g.dev();  // runs deferred producers first
+    float *out = sum.dev_mut();
+    launch(KernelClass::Elementwise, 12.0 * n, "ts_hip_add(accumulate)",
+           [&] { return ts_hip_add(a, b, out, n, Runtime::get().stream()); });
     existing = std::move(sum);
 }
 

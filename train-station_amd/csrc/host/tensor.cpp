@@ -31,20 +31,6 @@ size_t product(const std::vector<size_t> &d) {
     return n;
 }
 
-// Run one launcher, timed by the profiler when it is enabled.
-template <class F>
-void launch(KernelClass k, double work, const char *what, F &&f) {
-    Profiler &P = Profiler::get();
-    P.begin();
-    try {
-        check(f(), what);
-    } catch (...) {
-        P.abort();
-        throw;
-    }
-    P.end(k, work);
-}
-
 // Reference AVX2 body/tail split: 8-wide for negate and Adam
 // (core/utils.rs:856-865, adam/mod.rs:727-773), 32-wide unrolled body for the
 // division zero check (ops/div.rs:356-417).
@@ -226,8 +212,10 @@ void set_pending(const std::shared_ptr<Allocation> &out, std::shared_ptr<Pending
 }
 
 void materialize(Allocation &a) {
-    std::shared_ptr<PendingGemm> p = std::move(a.pending);
-    a.pending.reset();
+    // The record stays until the launch has succeeded: after a failed launch
+    // the next read of the buffer tries again (and reports the error again)
+    // instead of returning contents that were never written.
+    const std::shared_ptr<PendingGemm> p = a.pending;
     // inputs first (they may be deferred themselves), outside this launch's window
     const float *A = p->A->get(), *B = p->B->get();
     const float *bias = p->bias ? p->bias->get() : nullptr;
@@ -237,6 +225,7 @@ void materialize(Allocation &a) {
         return ts_hip_gemm_fused(p->ta, p->tb, p->M, p->N, p->K, A, p->lda, B, p->ldb, bias, p->relu ? 1 : 0,
                                  mask, C, p->N, S());
     });
+    a.pending.reset();
 }
 
 size_t next_tensor_id() {

@@ -162,6 +162,23 @@ class Profiler {
     ClassStats totals_[static_cast<int>(KernelClass::kCount)];
 };
 
+// Runs one launcher (a call returning a ts_hip status), timed by the profiler
+// when it is enabled; a failed status throws with `what` in the message.
+// Operands should be fetched before the call (a deferred operand that runs
+// inside the window is charged to its own class all the same).
+template <class F>
+void launch(KernelClass k, double work, const char *what, F &&f) {
+    Profiler &P = Profiler::get();
+    P.begin();
+    try {
+        check(f(), what);
+    } catch (...) {
+        P.abort();
+        throw;
+    }
+    P.end(k, work);
+}
+
 // ---- tensors --------------------------------------------------------------------
 
 class Tensor;
