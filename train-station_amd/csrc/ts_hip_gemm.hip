@@ -604,17 +604,37 @@ __global__ __launch_bounds__(kBlock) void splitk_sum(const float *__restrict__ P
     C[i * ldc + j] = epilogue(e, acc, static_cast<int>(i), static_cast<int>(j));
 }
 
-template <int WM, int WN, int SCHED, int EPI>
-static void launch_dma(int ta, int tb, GemmArgs g, hipStream_t s, unsigned batches) {
+template <bool TA, bool TB, int WM, int WN, int SCHED, int EPI>
+static void launch_dma(GemmArgs g, hipStream_t s, unsigned batches) {
     g.tiles_m = (g.M + 255) / 256;
     g.tiles_n = (g.N + 255) / 256;
     g.tiles = g.tiles_m * g.tiles_n;
     dim3 grid(static_cast<unsigned>(g.tiles) * batches);
     dim3 block(64 * WM * WN);
-    if (!ta && !tb) hipLaunchKernelGGL((gemm_f32_lds_dma<false, false, WM, WN, SCHED, EPI>), grid, block, 0, s, g);
-    else if (!ta && tb) hipLaunchKernelGGL((gemm_f32_lds_dma<false, true, WM, WN, SCHED, EPI>), grid, block, 0, s, g);
-    else if (ta && !tb) hipLaunchKernelGGL((gemm_f32_lds_dma<true, false, WM, WN, SCHED, EPI>), grid, block, 0, s, g);
-    else hipLaunchKernelGGL((gemm_f32_lds_dma<true, true, WM, WN, SCHED, EPI>), grid, block, 0, s, g);
+    hipLaunchKernelGGL((gemm_f32_lds_dma<TA, TB, WM, WN, SCHED, EPI>), grid, block, 0, s, g);
+}
+
+// The DMA kernel of one layout: wave grid and LDS-read order per layout, the
+// fastest measured at 8192x4096x4096 (only these instantiations exist).  A
+// mask epilogue on NN takes the 8-wave grid: the 4-wave one holds its
+// accumulators in AGPRs and has no registers left for a row of mask values
+// (it spills); bias and relu alone fit.
+static void launch_dma_layout(int ta, int tb, const GemmArgs &g, hipStream_t s, unsigned nb) {
+    const bool epi = g.bias || g.mask || g.relu;
+    if (!ta && !tb) {
+        if (g.mask) launch_dma<false, false, 2, 4, 1, kEpiAll>(g, s, nb);
+        else if (epi) launch_dma<false, false, 2, 2, 1, kEpiBiasRelu>(g, s, nb);
+        else launch_dma<false, false, 2, 2, 1, kEpiNone>(g, s, nb);
+    } else if (!ta && tb) {
+        if (epi) launch_dma<false, true, 2, 4, 0, kEpiAll>(g, s, nb);
+        else launch_dma<false, true, 2, 4, 0, kEpiNone>(g, s, nb);
+    } else if (ta && !tb) {
+        if (epi) launch_dma<true, false, 2, 4, 1, kEpiAll>(g, s, nb);
+        else launch_dma<true, false, 2, 4, 1, kEpiNone>(g, s, nb);
+    } else {
+        if (epi) launch_dma<true, true, 2, 4, 1, kEpiAll>(g, s, nb);
+        else launch_dma<true, true, 2, 4, 1, kEpiNone>(g, s, nb);
+    }
 }
 
 }  // namespace tship
@@ -646,23 +666,8 @@ static int gemm_launch(int trans_a, int trans_b, size_t M, size_t N, size_t K, c
     const size_t mid_tiles = ((M + 127) / 128) * ((N + 127) / 128) * batches;
     const unsigned nb = static_cast<unsigned>(batches);
     if (big_tiles >= static_cast<size_t>(device_cu_count())) {
-        const bool epi = g.bias || g.mask || g.relu;
         if (!g.vec) launch_tiles<256, 256, 2, 4>(trans_a, trans_b, g, s, nb);
-        // wave grid and read order per layout: the fastest measured at 8192x4096x4096.
-        // A mask epilogue on NN takes the 8-wave grid: the 4-wave one holds
-        // its accumulators in AGPRs and has no registers left for a row of
-        // mask values (it spills); bias and relu alone fit.
-        else if (!trans_a && !trans_b) {
-            if (g.mask) launch_dma<2, 4, 1, kEpiAll>(trans_a, trans_b, g, s, nb);
-            else if (epi) launch_dma<2, 2, 1, kEpiBiasRelu>(trans_a, trans_b, g, s, nb);
-            else launch_dma<2, 2, 1, kEpiNone>(trans_a, trans_b, g, s, nb);
-        } else if (!trans_a && trans_b) {
-            if (epi) launch_dma<2, 4, 0, kEpiAll>(trans_a, trans_b, g, s, nb);
-            else launch_dma<2, 4, 0, kEpiNone>(trans_a, trans_b, g, s, nb);
-        } else {
-            if (epi) launch_dma<2, 4, 1, kEpiAll>(trans_a, trans_b, g, s, nb);
-            else launch_dma<2, 4, 1, kEpiNone>(trans_a, trans_b, g, s, nb);
-        }
+        else launch_dma_layout(trans_a, trans_b, g, s, nb);
     } else if (2 * mid_tiles >= static_cast<size_t>(device_cu_count())) {
         launch_tiles<128, 128, 2, 2>(trans_a, trans_b, g, s, nb);
     } else {
