@@ -318,7 +318,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU: the path is built and measured on "
-                          "a single MI355X (how it would shard is described in DESIGN.md); "
+                          "a single MI355X (multi-GPU sharding is a design, not built); "
                           "run with --gpus 1"}))
         return 2
 
