@@ -116,64 +116,82 @@ def host_info():
 
 
 def cpu_baseline(cfg_name: str, sample_rows: int):
-    """Single-core CPU restatement (oracle/) of one config-5 step, timed on a
-    bounded sample and scaled: the three GEMM layouts on `sample_rows` output
-    rows, the step's elementwise/reduction passes on 1/64 of the activations,
-    Adam on 1/16 of the parameters."""
+    """Single-core CPU restatement (oracle/) of one MLP step of `cfg_name`,
+    timed on a bounded sample and scaled, layer by layer: the forward product
+    and the dX product on `sample_rows` of the batch rows, the dW product on
+    `sample_rows` of its output rows; the elementwise and reduction passes on
+    1/64 of each activation's rows; Adam on 1/16 of the parameters."""
     import oracle as O
 
-    batch, widths, _ = CONFIGS[cfg_name]
+    batch, widths, init = CONFIGS[cfg_name]
+    readme = init == "readme"
     rng = np.random.default_rng(7)
-    D = widths[1]
     layers = len(widths) - 1
     R = min(sample_rows, batch)
-    timings = {}
+    rows = max(1, batch // 64)  # activation rows of the elementwise sample
+    timings = {"gemm_s": 0.0, "elementwise_s": 0.0}
 
-    X = rng.standard_normal((R, widths[0]), dtype=np.float32)
-    W = rng.standard_normal((widths[0], D), dtype=np.float32)
-    dY = rng.standard_normal((R, D), dtype=np.float32)
-    Xfull_T = rng.standard_normal((batch, R), dtype=np.float32)      # X for the dW slab: [K=batch, M=R]
-    dYfull = rng.standard_normal((batch, D), dtype=np.float32)
-    t0 = time.perf_counter(); O.gemm_f32(X, W); t_nn = time.perf_counter() - t0            # X.W
-    t0 = time.perf_counter(); O.gemm_f32(dY, W, tb=True); t_nt = time.perf_counter() - t0  # dY.W^T
-    t0 = time.perf_counter(); O.gemm_f32(Xfull_T, dYfull, ta=True); t_tn = time.perf_counter() - t0  # X^T.dY
-    scale = batch / R
-    gemm_s = layers * (t_nn * scale) + (layers - 1) * (t_nt * scale) + layers * (t_tn * D / R)
-    timings["gemm_s"] = gemm_s
+    product_s = {}  # each product timed once per shape: (kind, fan_in, fan_out) -> seconds per step
 
-    # elementwise + reductions of one step on 1/64 of each activation
-    n = batch * D // 64
-    a = rng.standard_normal(n, dtype=np.float32)
-    b = rng.standard_normal(n, dtype=np.float32)
-    bias = rng.standard_normal(D, dtype=np.float32)
-    t0 = time.perf_counter()
-    for _ in range(layers):
-        z = O.bias_add(a.reshape(-1, D), bias)        # forward bias add
-        r = O.relu(z)                                  # forward relu
-        O.relu_bwd(r, b)                               # relu mask gradient
-        O.sum_dim0(b.reshape(-1, D))                   # bias gradient
-        O.add(a, b)                                    # gradient accumulation
-    d = O.sub(a, b); p2 = O.pow2(d); O.mean(p2)        # MSE forward
-    O.pow_bwd(d, b, 2.0); O.fill(n, 1.0)               # MSE backward
-    elem_s = (time.perf_counter() - t0) * 64
-    timings["elementwise_s"] = elem_s
+    def product(kind, fi, fo):
+        key = (kind, fi, fo)
+        if key not in product_s:
+            W = rng.standard_normal((fi, fo), dtype=np.float32)
+            if kind == "dW":                                   # X^T.dY on up to sample_rows output rows
+                Rw = min(sample_rows, fi)
+                Xt = rng.standard_normal((batch, Rw), dtype=np.float32)
+                dY = rng.standard_normal((batch, fo), dtype=np.float32)
+                t0 = time.perf_counter(); O.gemm_f32(Xt, dY, ta=True)
+                product_s[key] = (time.perf_counter() - t0) * fi / Rw
+            elif kind == "dX":                                 # dY.W^T on R batch rows
+                dY = rng.standard_normal((R, fo), dtype=np.float32)
+                t0 = time.perf_counter(); O.gemm_f32(dY, W, tb=True)
+                product_s[key] = (time.perf_counter() - t0) * batch / R
+            else:                                              # X.W on R batch rows
+                X = rng.standard_normal((R, fi), dtype=np.float32)
+                t0 = time.perf_counter(); O.gemm_f32(X, W)
+                product_s[key] = (time.perf_counter() - t0) * batch / R
+        return product_s[key]
 
-    P = layers * (widths[0] * D + D)
-    ns = P // 16
+    for i in range(layers):
+        fi, fo = widths[i], widths[i + 1]
+        timings["gemm_s"] += product("fwd", fi, fo) + product("dW", fi, fo) + (product("dX", fi, fo) if i > 0 else 0.0)
+
+        n = rows * fo
+        a = rng.standard_normal(n, dtype=np.float32)
+        b = rng.standard_normal(n, dtype=np.float32)
+        bias = rng.standard_normal(fo, dtype=np.float32)
+        t0 = time.perf_counter()
+        z = O.bias_add(a.reshape(-1, fo), bias)            # forward bias add
+        if i < layers - 1 or readme:
+            r = O.relu(z)                                  # forward relu
+            O.relu_bwd(r, b)                               # relu mask gradient
+        O.sum_dim0(b.reshape(-1, fo))                      # bias gradient
+        if i > 0:
+            O.add(a, b)                                    # gradient accumulation
+        if i == layers - 1:
+            if readme:
+                O.mean(a); O.fill(n, 1.0)                  # sum forward, its backward fill
+            else:
+                d = O.sub(a, b); p2 = O.pow2(d); O.mean(p2)    # MSE forward
+                O.pow_bwd(d, b, 2.0); O.fill(n, 1.0)           # MSE backward
+        timings["elementwise_s"] += (time.perf_counter() - t0) * batch / rows
+
+    P = sum(widths[i] * widths[i + 1] + widths[i + 1] for i in range(layers))
+    ns = max(1, P // 16)
     p = rng.standard_normal(ns, dtype=np.float32)
     g = rng.standard_normal(ns, dtype=np.float32) * np.float32(0.1)
     m = np.zeros(ns, np.float32)
     v = np.zeros(ns, np.float32)
     t0 = time.perf_counter()
     O.adam_step(p, g, m, v, 1)
-    adam_s = (time.perf_counter() - t0) * 16
-    timings["adam_s"] = adam_s
-    total = gemm_s + elem_s + adam_s
-    sample = (f"GEMM layouts NN/NT/TN on {R} of {batch} output rows (TN: {R} of {D}), "
-              f"elementwise/reduction passes on 1/64 of the activations, Adam on 1/16 of "
-              f"{P} params; scaled to one full step ({total:.1f} s)")
+    timings["adam_s"] = (time.perf_counter() - t0) * P / ns
+    total = sum(timings.values())
+    sample = (f"per layer: forward and dX products on {R} of {batch} rows, dW on up to {sample_rows} of its "
+              f"output rows, elementwise/reduction passes on {rows} of {batch} rows, Adam on 1/16 of "
+              f"{P} params; scaled to one full step ({total:.2f} s)")
     return {"value": 1.0 / total, "unit": "steps/s", "cores": 1, "kind": "port",
-            "sample": sample, "breakdown_s": {k: round(v, 3) for k, v in timings.items()}, "host": host_info()}
+            "sample": sample, "breakdown_s": {k: round(v, 4) for k, v in timings.items()}, "host": host_info()}
 
 
 def cpu_baseline_chain(sample: int):
@@ -429,7 +447,7 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (oracle port, one core, bounded sample)")
-        result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_sample_rows) if args.config == "c5" else None
+        result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_sample_rows)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
