@@ -1,0 +1,59 @@
+"""bench.py on the CPU: the one-GPU refusal, the algorithmic work figures the
+roofline divides by, and the CPU-baseline record (nothing here touches a GPU).
+
+The work figures are closed forms of the configurations: 17 products of
+2*8192*4096*4096 FLOP for config 5 (6 forward, 6 dW, 5 dX: the input needs no
+gradient), 3.351 GFLOP for config 4 and 12.85 MFLOP for config 1 (forward and
+dW only), 148 bytes per element for the config-2 chain and 28 per parameter
+for Adam (read p, g, m, v; write p, m, v).
+"""
+from __future__ import annotations
+
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT))
+
+import bench  # noqa: E402
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120, cwd=ROOT)
+    assert r.returncode == 2
+    line = json.loads(r.stdout.strip().splitlines()[-1])
+    assert "one GPU" in line["error"]
+
+
+def test_gemm_flops_per_step_are_the_closed_forms():
+    batch, widths, init = bench.CONFIGS["c5"]
+    assert bench.step_flops(batch, widths, init == "readme") == 17 * 2.0 * 8192 * 4096 * 4096
+    batch, widths, init = bench.CONFIGS["c4"]
+    c4 = 2.0 * 1024 * 784 * 1024 * 2 + 2.0 * 1024 * 1024 * 10 * 3
+    assert bench.step_flops(batch, widths, init == "readme") == c4
+    assert abs(c4 - 3.351e9) < 1e6
+    batch, widths, init = bench.CONFIGS["c1"]
+    assert bench.step_flops(batch, widths, init == "readme") == 2 * 2.0 * 32 * 784 * 128  # 12.85 MFLOP
+
+
+def test_bandwidth_work_per_unit():
+    # forward add/mul/div/sub 12 B each, relu 8, sum 4; backward fill 4, relu mask 12,
+    # neg 8, div 20, mul 20, two accumulations 12 + 12
+    assert bench.CHAIN_BYTES_PER_ELEM == 4 * 12 + 8 + 4 + 4 + 12 + 8 + 20 + 20 + 12 + 12
+    assert bench.ADAM_BYTES_PER_PARAM == 4 * 4 + 3 * 4
+
+
+@pytest.mark.parametrize("cfg", ["c1", "c4"])
+def test_cpu_baseline_record(cfg):
+    r = bench.cpu_baseline(cfg, 64)
+    assert r["kind"] == "port" and r["cores"] == 1 and r["unit"] == "steps/s"
+    assert r["value"] > 0
+    assert set(r["breakdown_s"]) == {"gemm_s", "elementwise_s", "adam_s"}
+    assert abs(1.0 / r["value"] - sum(r["breakdown_s"].values())) < 1e-3 + 0.01 / r["value"]
+    host = r["host"]
+    assert host["host_cores"] >= host["usable_cores"] >= 1 and host["cpu_model"]
