@@ -3,7 +3,7 @@ on one MI355X, on BASELINE config 5: batch 8192, six Linear(4096, 4096) layers
 with bias, ReLU after layers 1-5, MSE loss, fp32, Adam(lr 1e-3).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c5|c4|c1|c2|c3]
-                    [--no-cpu-baseline] [--cpu-sample-rows R]
+                    [--no-cpu-baseline] [--cpu-sample-rows R] [--graph]
 
 Prints one JSON line.  `value` is steps/s measured over exactly K steps with
 all inputs resident in HBM.  `roofline` is the roofline of the dominant kernel
@@ -329,6 +329,9 @@ def main() -> int:
     ap.add_argument("--config", default="c5", choices=sorted(list(CONFIGS) + ["c2", "c3"]))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-rows", type=int, default=2048)
+    ap.add_argument("--graph", action="store_true",
+                    help="also time the same step recorded once as a HIP graph and replayed (StepGraph); "
+                         "reported beside the eager figure, which stays `value`")
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="first launch a plain copy kernel (x * 1.0 -> out, 8 bytes per float) over "
                          "this many floats three times, as the calibration point of HBM byte counters")
@@ -445,6 +448,21 @@ def main() -> int:
         "event_ms_per_step": round(ev_ms.value / args.steps, 3),
         "final_loss": final_loss,
     }
+    if args.graph:
+        # the same loop, one step recorded and then replayed: every replay
+        # runs the whole step (the first runs the recorded one); untimed
+        # replays warm the graph up
+        with TS.StepGraph.record() as g:
+            gloss = step()
+        g.replay(max(1, args.warmup))
+        TS.synchronize()
+        t0 = time.perf_counter()
+        g.replay(args.steps)
+        TS.synchronize()
+        g_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+        result["graph"] = {"value": round(1000.0 / g_ms, 4), "unit": "steps/s", "ms_per_step": round(g_ms, 4),
+                           "final_loss": gloss.value(), "note": "the same step replayed from a HIP graph"}
+        g.free()
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (oracle port, one core, bounded sample)")
         result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_sample_rows)

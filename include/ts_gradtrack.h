@@ -22,6 +22,7 @@ extern "C" {
 
 typedef struct ts_tensor ts_tensor;
 typedef struct ts_adam ts_adam;
+typedef struct ts_step_graph ts_step_graph;
 
 const char *ts_last_error(void);
 
@@ -174,6 +175,32 @@ int ts_synchronize(void);
  * tensors that depend on it first, or switch fusion off. */
 void ts_fusion_enable(int on);
 int ts_fusion_enabled(void);
+
+/* Step graphs (no counterpart in the reference, whose steps run eagerly on
+ * the CPU): the library stream's work between ts_step_graph_begin and
+ * ts_step_graph_end (typically a forward, ts_tensor_backward, ts_adam_step and
+ * ts_adam_zero_grad) is recorded as a HIP graph, not run; each replay runs all
+ * of it as one graph launch, the first replay running the recorded step
+ * itself.  A replayed ts_adam_step uses the bias corrections of the step count
+ * it would have in an eager loop, and the optimizer's counters advance with the
+ * replays, so N replays give the bits of N eager steps.  Rules:
+ *  - inside the recording nothing may wait for or read the device
+ *    (ts_tensor_value / data, ts_synchronize) or upload host data
+ *    (ts_tensor_from_slice): create inputs before, read results after a replay;
+ *  - every buffer the recorded work touches stays reserved until the graph is
+ *    freed (tensors dropped meanwhile are not reused), and a replay reads the
+ *    current contents of the inputs it recorded: refill them in place
+ *    (ts_tensor_device_ptr + copies) to feed new data;
+ *  - record an AMSGrad step only after the optimizer's first step; the
+ *    learning rate and other settings are the recorded ones;
+ *  - the profiler must be off while recording.
+ * On an error inside the recording, call ts_step_graph_abort. */
+int ts_step_graph_begin(void);
+ts_step_graph *ts_step_graph_end(void);
+void ts_step_graph_abort(void);
+int ts_step_graph_recording(void);
+int ts_step_graph_replay(ts_step_graph *g, size_t times);
+void ts_step_graph_free(ts_step_graph *g);
 /* library stream (for timing events on the stream the kernels run on) */
 void *ts_stream(void);
 /* device pool statistics and cache release */

@@ -71,6 +71,16 @@ int ts_hip_event_destroy(void *event);
 int ts_hip_event_record(void *event, void *stream);
 int ts_hip_event_synchronize(void *event);
 int ts_hip_event_elapsed_ms(float *ms, void *start, void *stop);
+/* HIP graphs (no counterpart in the reference): work issued on `stream`
+ * between begin and end is recorded, not run (relaxed capture mode: the
+ * caller's other HIP calls stay legal, stream synchronisation does not), then
+ * instantiated into *graph_exec; ts_hip_graph_launch runs it on a stream.  A
+ * recorded launch keeps the pointers and arguments it was given. */
+int ts_hip_stream_begin_capture(void *stream);
+int ts_hip_stream_end_capture(void *stream, void **graph_exec);
+int ts_hip_stream_is_capturing(void *stream, int *capturing);
+int ts_hip_graph_launch(void *graph_exec, void *stream);
+int ts_hip_graph_destroy(void *graph_exec);
 /* message for a status returned by any ts_hip_* call */
 const char *ts_hip_error_string(int status);
 /* free / total device memory in bytes */
@@ -256,6 +266,11 @@ int ts_hip_matmul(const float *a, const float *b, float *c, size_t m, size_t n, 
 int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
                 size_t lda, const float *B, size_t ldb, float *C, size_t ldc, void *stream);
 
+/* Floats of workspace a split product needs (the temporary ts_hip_gemm takes
+ * from the stream-ordered allocator for few output tiles with a long K):
+ * 0 when the product M x N x K is not split. */
+size_t ts_hip_gemm_workspace_floats(size_t M, size_t N, size_t K);
+
 /* The same product with the elementwise ops that follow it fused into the
  * store (no counterpart in the reference, which runs them as separate passes:
  * matmul then add_tensor with a broadcast row bias, ops/add.rs:276-379, then
@@ -267,10 +282,14 @@ int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t K, const fl
  *   mask != NULL:  v = mask[i*ldc + j] > 0 ? v : +0   (mask laid out as C)
  *   C[i*ldc + j] = v
  * Bit-identical to ts_hip_gemm followed by ts_hip_bias_add, ts_hip_relu and
- * ts_hip_relu_backward(mask, C, C). */
+ * ts_hip_relu_backward(mask, C, C).  A split product (see
+ * ts_hip_gemm_workspace_floats) uses `workspace` (device, at least that many
+ * floats; TS_HIP_EWORKSPACE if fewer) as its temporary, so the call allocates
+ * nothing and can be recorded into a HIP graph; with workspace == NULL it
+ * allocates as ts_hip_gemm does. */
 int ts_hip_gemm_fused(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A, size_t lda,
                       const float *B, size_t ldb, const float *bias, int relu, const float *mask, float *C,
-                      size_t ldc, void *stream);
+                      size_t ldc, float *workspace, size_t workspace_floats, void *stream);
 
 /* Batched C[b] = op(A[b]) . op(B[b]) (matmul/mod.rs:634-760 batched_matmul and
  * the batched backward of grad_fn/ops/matmul.rs:150-219) on the same MFMA
@@ -338,6 +357,21 @@ typedef struct ts_hip_adam_param {
 int ts_hip_adam_step_multi(const ts_hip_adam_param *params, size_t count, float lr, float beta1,
                            float beta2, float eps, float weight_decay, uint64_t step_count,
                            void *stream);
+
+/* The same step with its bias corrections read on the device: pair s = *slot
+ * of `bias_corrections` (device memory, [cf1, cf2] pairs as
+ * ts_hip_adam_bias_corrections computes them), so one recorded step replays at
+ * later step counts (no counterpart in the reference, which steps eagerly). */
+int ts_hip_adam_step_multi_table(const ts_hip_adam_param *params, size_t count, float lr, float beta1,
+                                 float beta2, float eps, float weight_decay, const float *bias_corrections,
+                                 const unsigned *slot, void *stream);
+/* Host: the bias corrections of steps first_step .. first_step + count - 1 as
+ * ts_hip_adam_step_multi computes them (adam/mod.rs:524-531, bias_correct
+ * :790-833): out[2i] = 1 / (1 - beta1^t), out[2i+1] = 1 / (1 - beta2^t), the
+ * power in f64, the rest in f32. */
+int ts_hip_adam_bias_corrections(float beta1, float beta2, uint64_t first_step, size_t count, float *out);
+/* *slot += 1, in stream order (the replay counter of a recorded step) */
+int ts_hip_slot_advance(unsigned *slot, void *stream);
 
 #ifdef __cplusplus
 }

@@ -58,8 +58,12 @@ def test_fused_entry_point_matches_separate_kernels(M, N, K, off, mode):
     use_relu = mode in ("relu", "bias_relu", "all")
     use_mask = mode in ("mask", "mask_nn", "all")
     fused, ref = Dev(M * N), Dev(M * N)
+    # a split product takes its temporary from the workspace (the host's way)
+    ws_floats = hip.ts_hip_gemm_workspace_floats(M, N, K)
+    dws = Dev(max(ws_floats, 1))
     check(hip.ts_hip_gemm_fused(0, tb, M, N, K, da.ptr, K, db.ptr, ldb, dbias.ptr if use_bias else None,
-                                int(use_relu), dmask.ptr if use_mask else None, fused.ptr, N, None))
+                                int(use_relu), dmask.ptr if use_mask else None, fused.ptr, N,
+                                dws.ptr if ws_floats else None, ws_floats, None))
     check(hip.ts_hip_gemm(0, tb, M, N, K, da.ptr, K, db.ptr, ldb, ref.ptr, N, None))
     if use_bias:
         check(hip.ts_hip_bias_add(ref.ptr, dbias.ptr, ref.ptr, M, N, 0, None))

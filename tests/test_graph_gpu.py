@@ -1,0 +1,213 @@
+"""Step graphs: one training step recorded as a HIP graph and replayed
+(ts_step_graph_*).  N replays must give the bits of N eager steps of the same
+loop: the same kernels in the same order, Adam's bias corrections following
+the step count (adam/mod.rs:524-531 via the device table), and the
+optimizer's counters advancing with the replays.  Also: the buffers a graph
+uses stay reserved while other work allocates, errors inside a recording
+leave the library usable, and AMSGrad's first step cannot be recorded.
+"""
+from __future__ import annotations
+
+import gc
+
+import numpy as np
+import pytest
+
+from conftest import assert_bits_equal
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture
+def T():
+    import train_station_amd as T
+    yield T
+    if T.recording():
+        T.native_gradtrack.ts_step_graph_abort()
+    T.set_fusion(True)
+    T.clear_gradients()
+
+
+def _model(T, widths, batch, seed, readme=False):
+    rng = np.random.default_rng(seed)
+    ps = []
+    for i in range(len(widths) - 1):
+        w = (rng.standard_normal((widths[i], widths[i + 1])) / np.sqrt(widths[i])).astype(np.float32)
+        b = (0.1 * rng.standard_normal(widths[i + 1])).astype(np.float32)
+        ps += [T.Tensor.from_slice(w, w.shape).with_requires_grad(),
+               T.Tensor.from_slice(b, b.shape).with_requires_grad()]
+    x = T.Tensor.from_slice(rng.standard_normal((batch, widths[0])).astype(np.float32), [batch, widths[0]])
+    t = T.Tensor.from_slice(rng.standard_normal((batch, widths[-1])).astype(np.float32), [batch, widths[-1]])
+    return ps, x, t
+
+
+def _step(ps, x, t, opt, readme):
+    h = x
+    n = len(ps) // 2
+    for i in range(n):
+        h = h.matmul(ps[2 * i]).add_tensor(ps[2 * i + 1])
+        if i < n - 1 or readme:
+            h = h.relu()
+    loss = h.sum() if readme else h.sub_tensor(t).pow_scalar(2.0).mean()
+    loss.backward()
+    opt.step(ps)
+    opt.zero_grad(ps)
+    return loss
+
+
+CASES = {  # name: widths, batch, readme
+    "mlp_c4": ([784, 1024, 10], 1024, False),     # the 1024x10 products split K
+    "readme_c1": ([784, 128], 32, True),          # forward and dW split K
+    "deep": ([256, 512, 512, 128], 512, False),
+}
+
+
+def _eager(T, case, steps, amsgrad=False):
+    widths, batch, readme = CASES[case]
+    ps, x, t = _model(T, widths, batch, 11)
+    opt = T.Adam.with_config(amsgrad=True) if amsgrad else T.Adam.with_learning_rate(1e-3)
+    opt.add_parameters(ps)
+    loss = None
+    for _ in range(steps):
+        loss = _step(ps, x, t, opt, readme)
+    return [p.data() for p in ps], loss.value(), opt
+
+
+@pytest.mark.parametrize("case", sorted(CASES))
+@pytest.mark.parametrize("fusion", [True, False])
+def test_replays_give_the_bits_of_eager_steps(T, case, fusion):
+    T.set_fusion(fusion)
+    widths, batch, readme = CASES[case]
+    want, want_loss, _ = _eager(T, case, 7)
+    print(f"[graph] {case} fusion={fusion}", flush=True)
+
+    ps, x, t = _model(T, widths, batch, 11)
+    opt = T.Adam.with_learning_rate(1e-3)
+    opt.add_parameters(ps)
+    _step(ps, x, t, opt, readme)                       # step 1 eagerly
+    before = [p.data() for p in ps]
+    with T.StepGraph.record() as g:                   # step 2, recorded, not run
+        loss = _step(ps, x, t, opt, readme)
+    for a, b in zip(before, [p.data() for p in ps]):  # nothing ran yet
+        assert_bits_equal(a, b)
+    g.replay(2)                                       # steps 2 and 3
+    g.replay(4)                                       # steps 4 .. 7
+    got = [p.data() for p in ps]
+    for i, (a, b) in enumerate(zip(got, want)):
+        assert_bits_equal(a, b, f"param {i} after 7 steps")
+    assert loss.value() == want_loss                  # the loss of step 7
+    assert opt.step_count() == 7
+    for p in ps:
+        assert opt.parameter_step(p) == 7
+    g.free()
+
+
+def test_counters_follow_the_replays(T):
+    widths, batch, readme = CASES["deep"]
+    ps, x, t = _model(T, widths, batch, 3)
+    opt = T.Adam.with_learning_rate(1e-3)
+    opt.add_parameters(ps)
+    with T.StepGraph.record() as g:                   # the very first step, recorded
+        _step(ps, x, t, opt, readme)
+    assert opt.step_count() == 1                      # counted when recorded
+    g.replay(1)
+    assert opt.step_count() == 1
+    g.replay(3)
+    assert opt.step_count() == 4
+    # an eager step after the replays continues the count
+    _step(ps, x, t, opt, readme)
+    assert opt.step_count() == 5
+    g.free()
+
+
+def test_first_recorded_step_matches_eager(T):
+    widths, batch, readme = CASES["deep"]
+    want, want_loss, _ = _eager(T, "deep", 3)
+    ps, x, t = _model(T, widths, batch, 11)
+    opt = T.Adam.with_learning_rate(1e-3)
+    opt.add_parameters(ps)
+    with T.StepGraph.record() as g:
+        loss = _step(ps, x, t, opt, readme)
+    g.replay(3)
+    for i, (a, b) in enumerate(zip([p.data() for p in ps], want)):
+        assert_bits_equal(a, b, f"param {i}")
+    assert loss.value() == want_loss
+    g.free()
+
+
+def test_graph_buffers_stay_reserved(T):
+    widths, batch, readme = CASES["deep"]
+    want, _, _ = _eager(T, "deep", 4)
+    ps, x, t = _model(T, widths, batch, 11)
+    opt = T.Adam.with_learning_rate(1e-3)
+    opt.add_parameters(ps)
+    _step(ps, x, t, opt, readme)
+    with T.StepGraph.record() as g:
+        _step(ps, x, t, opt, readme)
+    T.clear_gradients()
+    # eager work between replays allocates buffers of the recorded sizes
+    rng = np.random.default_rng(5)
+    keep = []
+    for shape in ([batch, 512], [512, 512], [batch, 128], [512], [256, 512]):
+        v = rng.standard_normal(shape).astype(np.float32)
+        keep.append((T.Tensor.from_slice(v, shape).add_scalar(1.0), v + np.float32(1.0)))
+    g.replay(1)
+    extra = [T.Tensor.from_slice(v, v.shape).mul_scalar(2.0) for _, v in keep]
+    g.replay(2)
+    for (tt, v), e in zip(keep, extra):
+        assert_bits_equal(tt.data(), v)
+        assert_bits_equal(e.data(), v * np.float32(2.0))
+    for i, (a, b) in enumerate(zip([p.data() for p in ps], want)):
+        assert_bits_equal(a, b, f"param {i}")
+    del keep, extra
+    gc.collect()
+    live = T.pool_stats()["live_bytes"]
+    g.free()                                          # the recorded step's dropped temporaries were parked
+    assert T.pool_stats()["live_bytes"] < live
+
+
+def test_reading_inside_a_recording_is_refused(T):
+    widths, batch, readme = CASES["deep"]
+    ps, x, t = _model(T, widths, batch, 2)
+    opt = T.Adam.with_learning_rate(1e-3)
+    opt.add_parameters(ps)
+    with pytest.raises(T.TsError, match="recorded"):
+        with T.StepGraph.record():
+            loss = _step(ps, x, t, opt, readme)
+            loss.value()
+    assert not T.recording()
+    assert opt.step_count() == 0                      # the aborted step never ran
+    # the library works on afterwards, eagerly and recorded
+    T.clear_gradients()
+    _step(ps, x, t, opt, readme)
+    with T.StepGraph.record() as g:
+        _step(ps, x, t, opt, readme)
+    g.replay(1)
+    g.free()
+
+
+def test_amsgrad_first_step_is_not_recorded(T):
+    widths, batch, readme = CASES["deep"]
+    ps, x, t = _model(T, widths, batch, 4)
+    opt = T.Adam.with_config(amsgrad=True)
+    opt.add_parameters(ps)
+    with pytest.raises(T.TsError, match="AMSGrad"):
+        with T.StepGraph.record():
+            _step(ps, x, t, opt, readme)
+    assert opt.step_count() == 0
+    T.clear_gradients()
+
+
+def test_amsgrad_replays_after_the_first_step(T):
+    widths, batch, readme = CASES["deep"]
+    want, _, _ = _eager(T, "deep", 4, amsgrad=True)
+    ps, x, t = _model(T, widths, batch, 11)
+    opt = T.Adam.with_config(amsgrad=True)
+    opt.add_parameters(ps)
+    _step(ps, x, t, opt, readme)
+    with T.StepGraph.record() as g:
+        _step(ps, x, t, opt, readme)
+    g.replay(3)
+    for i, (a, b) in enumerate(zip([p.data() for p in ps], want)):
+        assert_bits_equal(a, b, f"param {i}")
+    g.free()

@@ -14,15 +14,16 @@ Layers, bottom up:
 Importing the package loads both libraries; it raises if they are not built.
 """
 from ._ffi import TsError, gradtrack as native_gradtrack, hip as native_hip, hip_check
-from .tensor import (Adam, NoGradTrack, Profile, Tensor, adam_config_from_binary,
+from .tensor import (Adam, NoGradTrack, Profile, StepGraph, Tensor, adam_config_from_binary,
                      adam_config_from_json, adam_config_to_binary, adam_config_to_json,
-                     clear_gradients, empty_cache, fusion_enabled, is_grad_enabled, pool_stats, set_fusion,
-                     stream, synchronize)
+                     clear_gradients, empty_cache, fusion_enabled, is_grad_enabled, pool_stats, recording,
+                     set_fusion, stream, synchronize)
 
 __all__ = [
-    "Adam", "NoGradTrack", "Profile", "Tensor", "TsError", "adam_config_from_binary",
+    "Adam", "NoGradTrack", "Profile", "StepGraph", "Tensor", "TsError", "adam_config_from_binary",
     "adam_config_from_json", "adam_config_to_binary", "adam_config_to_json", "clear_gradients",
     "empty_cache", "fusion_enabled",
-    "hip_check", "is_grad_enabled", "native_gradtrack", "native_hip", "pool_stats", "set_fusion", "stream",
+    "hip_check", "is_grad_enabled", "native_gradtrack", "native_hip", "pool_stats", "recording", "set_fusion",
+    "stream",
     "synchronize",
 ]

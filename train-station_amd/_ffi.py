@@ -107,7 +107,8 @@ HIP_SIGNATURES = {
     "ts_hip_matmul": (_c.c_int, [VP, VP, VP, SZ, SZ, SZ, VP]),
     "ts_hip_gemm": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, SZ, VP]),
     "ts_hip_gemm_fused": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, _c.c_int, VP, VP, SZ,
-                                     VP]),
+                                     VP, SZ, VP]),
+    "ts_hip_gemm_workspace_floats": (SZ, [SZ, SZ, SZ]),
     "ts_hip_gemm_batched": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, SZ, SZ,
                                        _c.POINTER(SZ), _c.POINTER(SZ), _c.POINTER(SZ), SZ, VP]),
     "ts_hip_gemv_workspace_floats": (SZ, [_c.c_int, SZ, SZ]),
@@ -118,6 +119,15 @@ HIP_SIGNATURES = {
                                     _c.c_float, _c.c_float, _c.c_uint64, SZ, _c.c_int, VP]),
     "ts_hip_adam_step_multi": (_c.c_int, [VP, SZ, _c.c_float, _c.c_float, _c.c_float, _c.c_float,
                                           _c.c_float, _c.c_uint64, VP]),
+    "ts_hip_adam_step_multi_table": (_c.c_int, [VP, SZ, _c.c_float, _c.c_float, _c.c_float, _c.c_float,
+                                                _c.c_float, VP, VP, VP]),
+    "ts_hip_adam_bias_corrections": (_c.c_int, [_c.c_float, _c.c_float, _c.c_uint64, SZ, VP]),
+    "ts_hip_slot_advance": (_c.c_int, [VP, VP]),
+    "ts_hip_stream_begin_capture": (_c.c_int, [VP]),
+    "ts_hip_stream_end_capture": (_c.c_int, [VP, _c.POINTER(VP)]),
+    "ts_hip_stream_is_capturing": (_c.c_int, [VP, _c.POINTER(_c.c_int)]),
+    "ts_hip_graph_launch": (_c.c_int, [VP, VP]),
+    "ts_hip_graph_destroy": (_c.c_int, [VP]),
 }
 
 
@@ -218,6 +228,12 @@ GRADTRACK_SIGNATURES = {
     "ts_synchronize": (_c.c_int, []),
     "ts_fusion_enable": (None, [_c.c_int]),
     "ts_fusion_enabled": (_c.c_int, []),
+    "ts_step_graph_begin": (_c.c_int, []),
+    "ts_step_graph_end": (TP, []),
+    "ts_step_graph_abort": (None, []),
+    "ts_step_graph_recording": (_c.c_int, []),
+    "ts_step_graph_replay": (_c.c_int, [TP, SZ]),
+    "ts_step_graph_free": (None, [TP]),
     "ts_stream": (VP, []),
     "ts_pool_live_bytes": (SZ, []),
     "ts_pool_cached_bytes": (SZ, []),

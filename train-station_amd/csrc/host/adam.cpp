@@ -2,6 +2,7 @@
 // state m / v (and v_hat_max under AMSGrad) lives in pooled device buffers;
 // each step is one fused kernel per parameter.
 #include <cstdio>
+#include <optional>
 
 #include "ts_hip.h"
 #include "ts_host.h"
@@ -42,16 +43,49 @@ void Adam::add_parameters(const std::vector<const Tensor *> &ps) {
     for (const Tensor *p : ps) add_parameter(*p);
 }
 
+void Adam::settle() const {
+    for (const auto &r : replayed_) {
+        if (!r->pending) continue;
+        step_count_ += static_cast<uint64_t>(r->pending);  // wraps correctly for -1
+        for (size_t id : r->params) {
+            auto it = states_.find(id);
+            if (it != states_.end()) it->second.step += static_cast<uint64_t>(r->pending);
+        }
+        r->pending = 0;
+    }
+}
+
 void Adam::step(const std::vector<Tensor *> &params) {
+    settle();
+    // While a step is being recorded, the launches read their bias
+    // corrections from the recording's table (each replay is a later step).
+    StepRecorder &rec = StepRecorder::get();
+    const bool recording = rec.open();
+    if (recording && config_.amsgrad)  // a replay would restart the running maximum every step
+        for (Tensor *p : params) {
+            auto it = states_.find(p->id());
+            if (it != states_.end() && p->grad_ref() && it->second.n && !it->second.v_hat_max)
+                throw Error("record an AMSGrad step only after the optimizer's first step");
+        }
     step_count_ += 1;  // adam/mod.rs:1037
+    std::optional<StepRecorder::AdamSlot> slot;
+    std::vector<size_t> stepped;
     std::vector<ts_hip_adam_param> batch;
     double bytes = 0.0;
     auto flush = [&]() {
         if (batch.empty()) return;
+        if (recording && !slot) {
+            slot = rec.adam_step(config_.beta1, config_.beta2, step_count_, {});
+            replayed_.push_back(slot->steps);  // linked at once: an abort takes the count back
+        }
         launch(KernelClass::Adam, bytes, "ts_hip_adam_step_multi", [&] {
+            void *st = Runtime::get().stream();
+            if (slot)
+                return ts_hip_adam_step_multi_table(batch.data(), batch.size(), config_.learning_rate,
+                                                    config_.beta1, config_.beta2, config_.eps,
+                                                    config_.weight_decay, slot->table, slot->slot, st);
             return ts_hip_adam_step_multi(batch.data(), batch.size(), config_.learning_rate, config_.beta1,
-                                          config_.beta2, config_.eps, config_.weight_decay, step_count_,
-                                          Runtime::get().stream());
+                                          config_.beta2, config_.eps, config_.weight_decay, step_count_, st);
         });
         batch.clear();
         bytes = 0.0;
@@ -76,6 +110,7 @@ void Adam::step(const std::vector<Tensor *> &params) {
             s.v_hat_max = std::make_shared<Allocation>(s.n);
             first = 1;
         }
+        stepped.push_back(p->id());
         if (!s.n) continue;
         // p is updated in place: deferred products reading it run first
         if (p->allocation()) p->allocation()->before_write();
@@ -92,6 +127,7 @@ void Adam::step(const std::vector<Tensor *> &params) {
         if (batch.size() == TS_HIP_ADAM_MAX_PARAMS) flush();
     }
     flush();
+    if (slot) slot->steps->params = std::move(stepped);
 }
 
 void Adam::zero_grad(const std::vector<Tensor *> &params) {
@@ -100,6 +136,7 @@ void Adam::zero_grad(const std::vector<Tensor *> &params) {
 }
 
 uint64_t Adam::parameter_step(size_t id) const {
+    settle();
     auto it = states_.find(id);
     return it == states_.end() ? 0 : it->second.step;
 }

@@ -15,6 +15,10 @@ struct ts_adam {
     ts::Adam a;
 };
 
+struct ts_step_graph {
+    std::unique_ptr<ts::StepGraph> g;
+};
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -444,6 +448,27 @@ int ts_adam_config_from_json(const char *json, size_t len, float *values5, int *
 
 void ts_fusion_enable(int on) { ts::set_fusion(on != 0); }
 int ts_fusion_enabled(void) { return ts::fusion_enabled() ? 1 : 0; }
+
+int ts_step_graph_begin(void) {
+    return guard_int([&] { ts::StepRecorder::get().begin(); });
+}
+ts_step_graph *ts_step_graph_end(void) {
+    return guard_ptr([&] { return new ts_step_graph{std::unique_ptr<ts::StepGraph>(ts::StepRecorder::get().end())}; });
+}
+void ts_step_graph_abort(void) {
+    try {
+        ts::StepRecorder::get().abort();
+    } catch (...) {
+    }
+}
+int ts_step_graph_recording(void) { return ts::StepRecorder::get().open() ? 1 : 0; }
+int ts_step_graph_replay(ts_step_graph *g, size_t times) {
+    return guard_int([&] {
+        if (!g) throw ts::Error("null step graph");
+        g->g->replay(times);
+    });
+}
+void ts_step_graph_free(ts_step_graph *g) { delete g; }
 
 int ts_synchronize(void) {
     return guard_int([&] { ts::Runtime::get().sync(); });

@@ -313,6 +313,7 @@ AdamConfig adam_config_from_json(const std::string &json) { return config_from_f
 // over 1,000,000 bytes (binary/reader.rs:79-94), which JSON text of more than
 // about 10^5 values exceeds, while a binary object may hold 10^8 bytes.
 Fields Adam::to_fields(bool binary) const {
+    settle();
     Fields states;
     auto nested = [&](const float *dev, const std::vector<size_t> &dims) {
         return binary ? Value::binary_object(device_to_binary(dev, dims, false))

@@ -33,6 +33,8 @@ Runtime &Runtime::get() {
 }
 
 void Runtime::sync() {
+    if (StepRecorder::get().open())
+        throw Error("a step being recorded cannot wait for or read device results: end the recording first");
     check(ts_hip_stream_synchronize(stream_), "ts_hip_stream_synchronize");
     unsigned long long idx = kNoZero;
     check(ts_hip_memcpy(reinterpret_cast<float *>(&idx),
@@ -74,6 +76,7 @@ float *DevicePool::acquire(size_t n_floats, size_t *rounded) {
             it->second.pop_back();
             cached_ -= r * sizeof(float);
             live_ += r * sizeof(float);
+            if (sink_) pin(p);
             return p;
         }
     }
@@ -87,15 +90,53 @@ float *DevicePool::acquire(size_t n_floats, size_t *rounded) {
     check(st, "ts_hip_malloc");
     std::lock_guard<std::mutex> lock(g_pool_mutex);
     live_ += r * sizeof(float);
+    if (sink_) pin(p);
     return p;
 }
 
 void DevicePool::release(float *p, size_t rounded) {
     if (!p) return;
     std::lock_guard<std::mutex> lock(g_pool_mutex);
+    if (pins_.count(p)) {  // a recorded step still uses it: park until unpinned
+        parked_[p] = rounded;
+        return;
+    }
     free_[rounded].push_back(p);
     live_ -= rounded * sizeof(float);
     cached_ += rounded * sizeof(float);
+}
+
+void DevicePool::pin_begin(std::vector<float *> *sink) {
+    std::lock_guard<std::mutex> lock(g_pool_mutex);
+    sink_ = sink;
+    sink_set_.clear();
+}
+
+void DevicePool::pin_end() {
+    std::lock_guard<std::mutex> lock(g_pool_mutex);
+    sink_ = nullptr;
+    sink_set_.clear();
+}
+
+void DevicePool::pin(float *p) {
+    if (!p || !sink_set_.insert(p).second) return;  // once per recording
+    ++pins_[p];
+    sink_->push_back(p);
+}
+
+void DevicePool::unpin(const std::vector<float *> &blocks) {
+    std::lock_guard<std::mutex> lock(g_pool_mutex);
+    for (float *p : blocks) {
+        auto it = pins_.find(p);
+        if (it == pins_.end() || --it->second > 0) continue;
+        pins_.erase(it);
+        auto pk = parked_.find(p);
+        if (pk == parked_.end()) continue;  // still owned: released normally later
+        free_[pk->second].push_back(p);
+        live_ -= pk->second * sizeof(float);
+        cached_ += pk->second * sizeof(float);
+        parked_.erase(pk);
+    }
 }
 
 void DevicePool::empty_cache() {
@@ -114,6 +155,7 @@ Allocation::~Allocation() { DevicePool::get().release(ptr_, rounded); }
 
 float *Allocation::get() {
     if (pending) materialize(*this);
+    DevicePool::get().note_use(ptr_);
     return ptr_;
 }
 
@@ -133,6 +175,7 @@ Profiler &Profiler::get() {
 }
 
 void Profiler::enable(bool on) {
+    if (on && StepRecorder::get().open()) throw Error("the profiler cannot time a step being recorded");
     if (!on && enabled_) collect();
     while (!open_.empty()) abort();
     enabled_ = on;

@@ -6,6 +6,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <memory>
 #include <sstream>
 
 #include "ts_hip.h"
@@ -24,6 +25,18 @@ std::string dims_str(const std::vector<size_t> &d) {
 namespace {
 
 void *S() { return Runtime::get().stream(); }
+
+// One 2-D product (with its optional epilogue) through ts_hip_gemm_fused; a
+// split product's temporary comes from the pool, so no op allocates on the
+// library stream (which keeps every step recordable as a HIP graph).
+int gemm2d(int ta, int tb, size_t M, size_t N, size_t K, const float *A, size_t lda, const float *B, size_t ldb,
+           const float *bias, bool relu, const float *mask, float *C, size_t ldc) {
+    const size_t ws = ts_hip_gemm_workspace_floats(M, N, K);
+    std::unique_ptr<Allocation> work;  // back to the pool on return: later work is stream-ordered after it
+    if (ws) work = std::make_unique<Allocation>(ws);
+    return ts_hip_gemm_fused(ta, tb, M, N, K, A, lda, B, ldb, bias, relu ? 1 : 0, mask, C, ldc,
+                             work ? work->get() : nullptr, ws, S());
+}
 
 size_t product(const std::vector<size_t> &d) {
     size_t n = 1;
@@ -222,8 +235,7 @@ void materialize(Allocation &a) {
     const float *mask = p->mask ? p->mask->get() : nullptr;
     float *C = a.raw();
     launch(KernelClass::Gemm, 2.0 * p->M * p->N * p->K, "ts_hip_gemm_fused", [&] {
-        return ts_hip_gemm_fused(p->ta, p->tb, p->M, p->N, p->K, A, p->lda, B, p->ldb, bias, p->relu ? 1 : 0,
-                                 mask, C, p->N, S());
+        return gemm2d(p->ta, p->tb, p->M, p->N, p->K, A, p->lda, B, p->ldb, bias, p->relu, mask, C, p->N);
     });
     a.pending.reset();
 }
@@ -588,7 +600,7 @@ Tensor Tensor::matmul(const Tensor &o) const {
             set_pending(out.alloc_, std::move(p));
         } else {
             launch(KernelClass::Gemm, 2.0 * m * n * k, "ts_hip_gemm", [&] {
-                return ts_hip_gemm(0, 0, m, n, k, dev(), k, o.dev(), n, out.dev_mut(), n, S());
+                return gemm2d(0, 0, m, n, k, dev(), k, o.dev(), n, nullptr, false, nullptr, out.dev_mut(), n);
             });
         }
     } else {  // batched_matmul (:634-760)
@@ -923,7 +935,8 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
                         set_pending(t.allocation(), std::move(p));
                     } else {
                         launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm(dX)", [&] {
-                            return ts_hip_gemm(0, 1, M, Kd, N, go.dev(), N, b.ptr(), N, t.dev_mut(), Kd, S());
+                            return gemm2d(0, 1, M, Kd, N, go.dev(), N, b.ptr(), N, nullptr, false, nullptr,
+                                          t.dev_mut(), Kd);
                         });
                     }
                     gl = std::move(t);
@@ -931,7 +944,8 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
                 if (req_right) {  // a[M,Kd]^T . go[M,N] -> [Kd,N]
                     Tensor t = Tensor::new_uninit({Kd, N});
                     launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm(dW)", [&] {
-                        return ts_hip_gemm(1, 0, Kd, N, M, a.ptr(), Kd, go.dev(), N, t.dev_mut(), N, S());
+                        return gemm2d(1, 0, Kd, N, M, a.ptr(), Kd, go.dev(), N, nullptr, false, nullptr,
+                                      t.dev_mut(), N);
                     });
                     gr = std::move(t);
                 }

@@ -23,6 +23,7 @@
 #include <stdexcept>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
 #include <utility>
 #include <vector>
 
@@ -69,9 +70,26 @@ class DevicePool {
     size_t live_bytes() const { return live_; }
     size_t cached_bytes() const { return cached_; }
 
+    // Step recording (StepRecorder): while a recording is open, every block
+    // acquired or used (note_use) is pinned to it; a pinned block released by
+    // its owner is parked instead of reused, until every recording that
+    // pinned it has been freed (unpin), so a replay never finds its buffers
+    // handed to other work.
+    void pin_begin(std::vector<float *> *sink);
+    void pin_end();
+    void note_use(float *p) {
+        if (sink_) pin(p);
+    }
+    void unpin(const std::vector<float *> &blocks);
+
   private:
+    void pin(float *p);
     std::unordered_map<size_t, std::vector<float *>> free_;
     size_t live_ = 0, cached_ = 0;
+    std::unordered_map<float *, int> pins_;       // block -> recordings pinning it
+    std::unordered_map<float *, size_t> parked_;  // released while pinned -> rounded size
+    std::vector<float *> *sink_ = nullptr;        // the open recording's pin list
+    std::unordered_set<float *> sink_set_;
 };
 
 struct Allocation;
@@ -349,6 +367,8 @@ struct AdamConfig adam_config_from_json(const std::string &json);
 // Rust's Debug form of a shape, "[2, 3]"
 std::string dims_str(const std::vector<size_t> &d);
 
+struct ReplaySteps;
+
 class Adam {
   public:
     Adam() = default;
@@ -363,7 +383,10 @@ class Adam {
     float learning_rate() const { return config_.learning_rate; }
     void set_learning_rate(float lr) { config_.learning_rate = lr; }
     const AdamConfig &config() const { return config_; }
-    uint64_t step_count() const { return step_count_; }
+    uint64_t step_count() const {
+        settle();
+        return step_count_;
+    }
     size_t parameter_count() const { return states_.size(); }
     // m / v of a linked parameter (device), for checkpoint and tests.
     const float *state_m(size_t param_id) const;
@@ -393,12 +416,68 @@ class Adam {
         size_t n = 0;
         uint64_t step = 0;
     };
+    // Adds the steps that replays of recorded steps ran to the counters.
+    void settle() const;
     ser::Fields to_fields(bool binary) const;
     static Adam from_fields(const ser::Fields &f);
     AdamConfig config_;
-    std::unordered_map<size_t, State> states_;
+    mutable std::unordered_map<size_t, State> states_;
     std::vector<size_t> insertion_order_;
-    uint64_t step_count_ = 0;
+    mutable uint64_t step_count_ = 0;
+    std::vector<std::shared_ptr<ReplaySteps>> replayed_;  // one per recorded step call
+};
+
+// ---- step recording ----------------------------------------------------------------
+
+// Steps run by replays of one recorded Adam::step beyond the recorded one
+// (which the optimizer counted when it was recorded; an aborted recording
+// takes that count back with -1); the optimizer adds them to its counters
+// when it next reads them.
+struct ReplaySteps {
+    int64_t pending = 0;
+    std::vector<size_t> params;  // the parameters that step updated
+};
+
+// One recorded step: a HIP graph of the library stream's work between
+// StepRecorder::begin and end, the blocks it pinned, and per recorded
+// Adam::step a table of bias corrections indexed by a device replay counter.
+struct StepGraph {
+    ~StepGraph();
+    // Runs the recorded work `times` times in stream order; the first replay
+    // ever runs the recorded step itself.
+    void replay(size_t times);
+    void *exec = nullptr;
+    std::vector<float *> pins;
+    std::shared_ptr<Allocation> slot;  // replay counter (one unsigned)
+    struct AdamUse {
+        std::shared_ptr<Allocation> table;  // kReplayChunk [cf1, cf2] pairs
+        float beta1 = 0, beta2 = 0;
+        uint64_t first_step = 0;
+        std::shared_ptr<ReplaySteps> steps;
+    };
+    std::vector<AdamUse> adams;
+    uint64_t executed = 0;  // replays run so far
+};
+
+class StepRecorder {
+  public:
+    static constexpr size_t kReplayChunk = 1024;  // replays per bias-correction table fill
+    static StepRecorder &get();
+    bool open() const { return graph_ != nullptr; }
+    void begin();
+    StepGraph *end();
+    void abort();
+    // Called by Adam::step while recording: the table and counter its launch
+    // reads, and the link through which replays credit the optimizer.
+    struct AdamSlot {
+        const float *table;
+        const unsigned *slot;
+        std::shared_ptr<ReplaySteps> steps;
+    };
+    AdamSlot adam_step(float beta1, float beta2, uint64_t step, std::vector<size_t> params);
+
+  private:
+    std::unique_ptr<StepGraph> graph_;
 };
 
 }  // namespace ts

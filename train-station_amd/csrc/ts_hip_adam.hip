@@ -98,6 +98,10 @@ struct MultiArgs {
     unsigned first_block[TS_HIP_ADAM_MAX_PARAMS + 1];  // workgroups of tensor j: [first_block[j], first_block[j+1])
     int count;
     float b1, c1, b2, c2, cf1, cf2, lr, eps, wd;
+    // When set, the bias corrections are cf_table[2*s], cf_table[2*s+1] with
+    // s = *cf_slot instead of cf1 / cf2 (a step recorded once and replayed).
+    const float *cf_table;
+    const unsigned *cf_slot;
 };
 
 // One flat grid over all tensors: workgroup b finds its tensor in the
@@ -114,7 +118,20 @@ __global__ __launch_bounds__(kBlock) void adam_multi_kernel(MultiArgs A) {
     a.amsgrad_first = q.amsgrad_first;
     a.b1 = A.b1; a.c1 = A.c1; a.b2 = A.b2; a.c2 = A.c2;
     a.cf1 = A.cf1; a.cf2 = A.cf2; a.lr = A.lr; a.eps = A.eps; a.wd = A.wd;
+    if (A.cf_table) {  // vector loads at device scope: the slot changes between launches
+        const unsigned sl = __hip_atomic_load(A.cf_slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        a.cf1 = __hip_atomic_load(A.cf_table + 2 * sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        a.cf2 = __hip_atomic_load(A.cf_table + 2 * sl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     adam_unit(a, static_cast<size_t>(blockIdx.x - A.first_block[j]) * kBlock + threadIdx.x);
+}
+
+// *slot += 1 by one lane, with vector memory operations.
+__global__ void slot_advance_kernel(unsigned *slot) {
+    if (threadIdx.x == 0) {
+        const unsigned v = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(slot, v + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 extern "C" int ts_hip_adam_step(float *p, const float *g, float *m, float *v, float *v_hat_max,
@@ -142,11 +159,11 @@ extern "C" int ts_hip_adam_step(float *p, const float *g, float *m, float *v, fl
     return launch_status();
 }
 
-extern "C" int ts_hip_adam_step_multi(const ts_hip_adam_param *params, size_t count, float lr,
-                                      float beta1, float beta2, float eps, float weight_decay,
-                                      uint64_t step_count, void *stream) {
+static int adam_multi(const ts_hip_adam_param *params, size_t count, float lr, float beta1, float beta2,
+                      float eps, float weight_decay, float cf1, float cf2, const float *cf_table,
+                      const unsigned *cf_slot, void *stream) {
     if (count == 0) return TS_HIP_OK;
-    if (!params || count > TS_HIP_ADAM_MAX_PARAMS || step_count == 0) return TS_HIP_EINVAL;
+    if (!params || count > TS_HIP_ADAM_MAX_PARAMS) return TS_HIP_EINVAL;
     MultiArgs A{};
     size_t blocks = 0;
     for (size_t i = 0; i < count; ++i) {
@@ -164,10 +181,44 @@ extern "C" int ts_hip_adam_step_multi(const ts_hip_adam_param *params, size_t co
     if (blocks == 0) return TS_HIP_OK;
     A.b1 = beta1; A.c1 = 1.0f - beta1;
     A.b2 = beta2; A.c2 = 1.0f - beta2;
-    A.cf1 = correction_factor(beta1, step_count);
-    A.cf2 = correction_factor(beta2, step_count);
+    A.cf1 = cf1;
+    A.cf2 = cf2;
+    A.cf_table = cf_table;
+    A.cf_slot = cf_slot;
     A.lr = lr; A.eps = eps; A.wd = weight_decay;
     hipLaunchKernelGGL(adam_multi_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
                        as_stream(stream), A);
+    return launch_status();
+}
+
+extern "C" int ts_hip_adam_step_multi(const ts_hip_adam_param *params, size_t count, float lr,
+                                      float beta1, float beta2, float eps, float weight_decay,
+                                      uint64_t step_count, void *stream) {
+    if (step_count == 0) return TS_HIP_EINVAL;
+    return adam_multi(params, count, lr, beta1, beta2, eps, weight_decay, correction_factor(beta1, step_count),
+                      correction_factor(beta2, step_count), nullptr, nullptr, stream);
+}
+
+extern "C" int ts_hip_adam_step_multi_table(const ts_hip_adam_param *params, size_t count, float lr,
+                                            float beta1, float beta2, float eps, float weight_decay,
+                                            const float *bias_corrections, const unsigned *slot, void *stream) {
+    if (!bias_corrections || !slot) return TS_HIP_EINVAL;
+    return adam_multi(params, count, lr, beta1, beta2, eps, weight_decay, 0.0f, 0.0f, bias_corrections, slot,
+                      stream);
+}
+
+extern "C" int ts_hip_adam_bias_corrections(float beta1, float beta2, uint64_t first_step, size_t count,
+                                            float *out) {
+    if (!out || first_step == 0) return TS_HIP_EINVAL;
+    for (size_t i = 0; i < count; ++i) {
+        out[2 * i] = correction_factor(beta1, first_step + i);
+        out[2 * i + 1] = correction_factor(beta2, first_step + i);
+    }
+    return TS_HIP_OK;
+}
+
+extern "C" int ts_hip_slot_advance(unsigned *slot, void *stream) {
+    if (!slot) return TS_HIP_EINVAL;
+    hipLaunchKernelGGL(slot_advance_kernel, dim3(1), dim3(64), 0, as_stream(stream), slot);
     return launch_status();
 }

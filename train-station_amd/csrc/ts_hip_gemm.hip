@@ -676,10 +676,26 @@ static int gemm_launch(int trans_a, int trans_b, size_t M, size_t N, size_t K, c
     return launch_status();
 }
 
+// Few output tiles and a long K: K is split into this many slices (1: not
+// split), computed as a batch into a temporary of slices*M*N floats and then
+// added in slice order.
+static int split_slices(size_t M, size_t N, size_t K) {
+    const size_t cus = static_cast<size_t>(device_cu_count());
+    const size_t tiles64 = ((M + 63) / 64) * ((N + 63) / 64);
+    if (4 * tiles64 < cus && K >= 512) {
+        for (int sl : {16, 8, 4, 2}) {
+            if (K % sl == 0 && K / sl >= 32 && tiles64 * sl <= 2 * cus) return sl;
+        }
+    }
+    return 1;
+}
+
 // One 2-D product with an optional epilogue (GemmArgs::bias / mask / relu).
+// A split product's temporary is `ws` when given (at least slices*M*N
+// floats), else it comes from the stream-ordered allocator.
 static int gemm_plain(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A, size_t lda,
                       const float *B, size_t ldb, float *C, size_t ldc, const float *bias, const float *mask,
-                      int relu, void *stream) {
+                      int relu, float *ws, size_t ws_floats, void *stream) {
     if (M == 0 || N == 0) return TS_HIP_OK;
     if (!C || ldc < N) return TS_HIP_EINVAL;
     if (K == 0) {  // empty contraction: C = 0, then the epilogue
@@ -690,24 +706,13 @@ static int gemm_plain(int trans_a, int trans_b, size_t M, size_t N, size_t K, co
         if (st == TS_HIP_OK && mask) st = ts_hip_relu_backward(mask, C, C, M * N, stream);
         return st;
     }
-    // Few output tiles and a long K: split K into S slices computed as a
-    // batch (slice s reads A and B from k = s*K/S on) into a stream-ordered
-    // temporary, then add the slices in order.
-    const size_t cus = static_cast<size_t>(device_cu_count());
-    const size_t tiles64 = ((M + 63) / 64) * ((N + 63) / 64);
-    int slices = 1;
-    if (4 * tiles64 < cus && K >= 512) {
-        for (int sl : {16, 8, 4, 2}) {
-            if (K % sl == 0 && K / sl >= 32 && tiles64 * sl <= 2 * cus) {
-                slices = sl;
-                break;
-            }
-        }
-    }
+    const int slices = split_slices(M, N, K);
     if (slices > 1 && A && B && lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N)) {
         hipStream_t st = as_stream(stream);
-        float *P = nullptr;
-        if (hipMallocAsync(reinterpret_cast<void **>(&P), slices * M * N * sizeof(float), st) == hipSuccess) {
+        const size_t need = slices * M * N;
+        float *P = ws;
+        if (ws && ws_floats < need) return TS_HIP_EWORKSPACE;
+        if (P || hipMallocAsync(reinterpret_cast<void **>(&P), need * sizeof(float), st) == hipSuccess) {
             const size_t kc = K / slices;
             GemmArgs e{};  // epilogue after the slice sum
             e.bias = bias;
@@ -727,6 +732,7 @@ static int gemm_plain(int trans_a, int trans_b, size_t M, size_t N, size_t K, co
                                    N, C, ldc, e);
                 status = launch_status();
             }
+            if (ws) return status;
             const hipError_t fe = hipFreeAsync(P, st);
             return status != TS_HIP_OK ? status : static_cast<int>(fe);
         }
@@ -742,13 +748,21 @@ static int gemm_plain(int trans_a, int trans_b, size_t M, size_t N, size_t K, co
 extern "C" int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
                            size_t lda, const float *B, size_t ldb, float *C, size_t ldc,
                            void *stream) {
-    return gemm_plain(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, nullptr, nullptr, 0, stream);
+    return gemm_plain(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, nullptr, nullptr, 0, nullptr, 0, stream);
+}
+
+extern "C" size_t ts_hip_gemm_workspace_floats(size_t M, size_t N, size_t K) {
+    if (M == 0 || N == 0 || K == 0) return 0;
+    const int slices = split_slices(M, N, K);
+    return slices > 1 ? static_cast<size_t>(slices) * M * N : 0;
 }
 
 extern "C" int ts_hip_gemm_fused(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
                                  size_t lda, const float *B, size_t ldb, const float *bias, int relu,
-                                 const float *mask, float *C, size_t ldc, void *stream) {
-    return gemm_plain(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, bias, mask, relu != 0, stream);
+                                 const float *mask, float *C, size_t ldc, float *workspace,
+                                 size_t workspace_floats, void *stream) {
+    return gemm_plain(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, bias, mask, relu != 0, workspace,
+                      workspace_floats, stream);
 }
 
 extern "C" int ts_hip_gemm_batched(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,

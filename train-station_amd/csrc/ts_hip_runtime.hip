@@ -173,6 +173,43 @@ int ts_hip_event_elapsed_ms(float *ms, void *start, void *stop) {
                                                 reinterpret_cast<hipEvent_t>(stop)));
 }
 
+int ts_hip_stream_begin_capture(void *stream) {
+    if (!stream) return TS_HIP_EINVAL;  // the null stream cannot be recorded
+    return static_cast<int>(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeRelaxed));
+}
+
+int ts_hip_stream_end_capture(void *stream, void **graph_exec) {
+    if (!stream || !graph_exec) return TS_HIP_EINVAL;
+    *graph_exec = nullptr;
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(as_stream(stream), &graph);
+    if (e != hipSuccess) return static_cast<int>(e);
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);  // the executable graph keeps its own copy
+    if (e != hipSuccess) return static_cast<int>(e);
+    *graph_exec = exec;
+    return TS_HIP_OK;
+}
+
+int ts_hip_stream_is_capturing(void *stream, int *capturing) {
+    if (!capturing) return TS_HIP_EINVAL;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(as_stream(stream), &st);
+    *capturing = st == hipStreamCaptureStatusActive ? 1 : 0;
+    return static_cast<int>(e);
+}
+
+int ts_hip_graph_launch(void *graph_exec, void *stream) {
+    if (!graph_exec) return TS_HIP_EINVAL;
+    return static_cast<int>(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph_exec), as_stream(stream)));
+}
+
+int ts_hip_graph_destroy(void *graph_exec) {
+    if (!graph_exec) return TS_HIP_OK;
+    return static_cast<int>(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph_exec)));
+}
+
 const char *ts_hip_error_string(int status) {
     switch (status) {
         case TS_HIP_OK: return "success";

@@ -8,6 +8,7 @@ panics surface as ``TsError``.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 from typing import Iterable, Optional, Sequence
 
@@ -445,6 +446,53 @@ def set_fusion(on: bool) -> None:
 
 def fusion_enabled() -> bool:
     return bool(_G.ts_fusion_enabled())
+
+
+class StepGraph:
+    """One recorded training step (include/ts_gradtrack.h, ts_step_graph_*):
+    the work issued inside ``with StepGraph.record() as g:`` is recorded as a
+    HIP graph, not run; ``g.replay(n)`` runs it n times (the first replay runs
+    the recorded step itself) with Adam's step counts advancing as in an eager
+    loop.  Inside the recording nothing may read the device or upload host
+    data; results are read after a replay."""
+
+    def __init__(self) -> None:
+        self._h = None
+
+    @staticmethod
+    @contextlib.contextmanager
+    def record():
+        g = StepGraph()
+        _ok(_G.ts_step_graph_begin())
+        try:
+            yield g
+        except BaseException:
+            _G.ts_step_graph_abort()
+            raise
+        h = _G.ts_step_graph_end()
+        if not h:
+            raise TsError(last_error() or "recording the step failed")
+        g._h = h
+
+    def replay(self, times: int = 1) -> None:
+        if not self._h:
+            raise TsError("the step graph holds no recording")
+        _ok(_G.ts_step_graph_replay(self._h, int(times)))
+
+    def free(self) -> None:
+        if self._h:
+            _G.ts_step_graph_free(self._h)
+            self._h = None
+
+    def __del__(self) -> None:
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def recording() -> bool:
+    return bool(_G.ts_step_graph_recording())
 
 
 def synchronize() -> None:
