@@ -186,6 +186,22 @@ def test_reading_inside_a_recording_is_refused(T):
     g.free()
 
 
+def test_uploads_inside_a_recording_are_refused(T):
+    widths, batch, readme = CASES["deep"]
+    ps, x, t = _model(T, widths, batch, 6)
+    opt = T.Adam.with_learning_rate(1e-3)
+    opt.add_parameters(ps)
+    with pytest.raises(T.TsError, match="cannot upload"):
+        with T.StepGraph.record():
+            T.Tensor.from_slice(np.ones(8, np.float32), [8])
+    assert not T.recording()
+    with pytest.raises(T.TsError, match="cannot upload"):
+        with T.StepGraph.record():
+            _step(ps, x, t, opt, readme).data()
+    assert opt.step_count() == 0
+    T.clear_gradients()
+
+
 def test_amsgrad_first_step_is_not_recorded(T):
     widths, batch, readme = CASES["deep"]
     ps, x, t = _model(T, widths, batch, 4)

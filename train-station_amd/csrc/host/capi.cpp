@@ -281,6 +281,7 @@ int ts_adam_state(const ts_adam *opt, const ts_tensor *param, int which, float *
         const float *src = which == 0 ? opt->a.state_m(p.id()) : opt->a.state_v(p.id());
         if (!src) throw ts::Error("parameter is not linked to this optimizer");
         if (len != p.size()) throw ts::Error("state buffer length mismatch");
+        ts::refuse_while_recording("adam state");
         ts::check(ts_hip_memcpy_async(out, src, len, 1, ts::Runtime::get().stream()),
                   "ts_hip_memcpy_async");
         ts::Runtime::get().sync();

@@ -94,6 +94,7 @@ constexpr size_t kDataRecordsAt = 24 + 8 + 4 + 4 + 1 + 8;
 
 // The binary form of a device buffer as a Tensor of `dims`.
 std::vector<uint8_t> device_to_binary(const float *dev, const std::vector<size_t> &dims, bool requires_grad) {
+    refuse_while_recording("checkpoint");
     const size_t n = product(dims);
     Value data;
     data.kind = Kind::Array;
@@ -123,6 +124,7 @@ std::vector<uint8_t> device_to_binary(const float *dev, const std::vector<size_t
 }
 
 std::vector<float> device_to_host(const float *dev, size_t n) {
+    refuse_while_recording("checkpoint");
     std::vector<float> h(n);
     if (n) {
         check(ts_hip_memcpy_async(h.data(), dev, n, 1, stream()), "ts_hip_memcpy_async");
@@ -142,6 +144,7 @@ std::string device_to_json(const float *dev, const std::vector<size_t> &dims, bo
 
 // Writes the values of a data Array into device memory (n floats).
 void upload_array(const Value &data, size_t n, float *dev) {
+    refuse_while_recording("checkpoint");
     if (!n) return;
     if (data.form == ser::ArrayForm::Records) {
         Allocation records((5 * n + 3) / 4);

@@ -300,6 +300,7 @@ Tensor Tensor::from_slice(const float *data, size_t len, std::vector<size_t> dim
     if (len != n)  // init/data.rs:227-247 returns Err on a length mismatch
         throw Error("Data length " + std::to_string(len) + " doesn't match shape " +
                     dims_str(dims) + " (size " + std::to_string(n) + ")");
+    refuse_while_recording("from_slice");
     Tensor t = new_uninit(std::move(dims));
     if (n) {
         check(ts_hip_memcpy_async(t.dev_mut(), data, n, 0, S()), "ts_hip_memcpy_async");
@@ -791,6 +792,7 @@ void Tensor::copy_to_host(float *out, size_t len) const {
     if (len != size_)
         throw Error("copy_to_host: buffer of " + std::to_string(len) + " floats for a tensor of " +
                     std::to_string(size_));
+    refuse_while_recording("copy_to_host");
     if (size_) check(ts_hip_memcpy_async(out, dev(), size_, 1, S()), "ts_hip_memcpy_async");
     Runtime::get().sync();
 }

@@ -480,4 +480,12 @@ class StepRecorder {
     std::unique_ptr<StepGraph> graph_;
 };
 
+// Host <-> device copies cannot be recorded (a replay would copy from or to
+// host memory that no longer holds the data): refused while recording.
+inline void refuse_while_recording(const char *what) {
+    if (StepRecorder::get().open())
+        throw Error(std::string(what) + ": a step being recorded cannot upload or read device data; "
+                                        "create inputs before the recording and read results after a replay");
+}
+
 }  // namespace ts
