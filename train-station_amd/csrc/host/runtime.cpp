@@ -110,12 +110,19 @@ void DevicePool::pin_begin(std::vector<float *> *sink) {
     std::lock_guard<std::mutex> lock(g_pool_mutex);
     sink_ = sink;
     sink_set_.clear();
+    pinning_.store(true, std::memory_order_relaxed);
 }
 
 void DevicePool::pin_end() {
     std::lock_guard<std::mutex> lock(g_pool_mutex);
     sink_ = nullptr;
     sink_set_.clear();
+    pinning_.store(false, std::memory_order_relaxed);
+}
+
+void DevicePool::pin_locked(float *p) {
+    std::lock_guard<std::mutex> lock(g_pool_mutex);
+    if (sink_) pin(p);
 }
 
 void DevicePool::pin(float *p) {

@@ -16,6 +16,7 @@
 // Reference panics become ts::Error exceptions.
 #pragma once
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 #include <memory>
@@ -78,12 +79,14 @@ class DevicePool {
     void pin_begin(std::vector<float *> *sink);
     void pin_end();
     void note_use(float *p) {
-        if (sink_) pin(p);
+        if (pinning_.load(std::memory_order_relaxed)) pin_locked(p);
     }
     void unpin(const std::vector<float *> &blocks);
 
   private:
-    void pin(float *p);
+    void pin(float *p);         // pool mutex held
+    void pin_locked(float *p);  // takes the pool mutex
+    std::atomic<bool> pinning_{false};
     std::unordered_map<size_t, std::vector<float *>> free_;
     size_t live_ = 0, cached_ = 0;
     std::unordered_map<float *, int> pins_;       // block -> recordings pinning it
