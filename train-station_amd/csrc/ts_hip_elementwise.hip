@@ -248,11 +248,11 @@ static int launch_map(const float *const *in, float *const *out, size_t n, Op op
     return launch_status();
 }
 
-template <class Op>
+template <class Op, bool NT = true>
 static int map1(const float *x, float *out, size_t n, Op op, void *stream) {
     const float *in[1] = {x};
     float *o[1] = {out};
-    return launch_map(in, o, n, op, stream);
+    return launch_map<Op, NT>(in, o, n, op, stream);
 }
 
 template <class Op, bool NT = true>
@@ -357,7 +357,9 @@ int ts_hip_relu(const float *x, float *out, size_t n, void *stream) {
     return map1(x, out, n, ReluOp{}, stream);
 }
 int ts_hip_pow_scalar(const float *x, float e, float *out, size_t n, void *stream) {
-    if (e == 2.0f) return map1(x, out, n, Pow2Op{}, stream);
+    // ordinary stores for the square: in the MSE loss the mean reads it right
+    // after and then finds it in MALL
+    if (e == 2.0f) return map1<Pow2Op, false>(x, out, n, Pow2Op{}, stream);
     if (e == 0.5f) return map1(x, out, n, PowHalfOp{}, stream);
     return map1(x, out, n, PowOp{e}, stream);
 }
