@@ -102,6 +102,50 @@ def test_replays_give_the_bits_of_eager_steps(T, case, fusion):
     g.free()
 
 
+def _other_ops_step(T, leaves, opt):
+    # the C2 chain (with division), 3-D broadcasting, a batched product, the
+    # activations and axis reductions, all recorded
+    a, b, c, w3, s = leaves
+    chain = a.add_tensor(b).mul_tensor(c).sub_tensor(a.div_tensor(c)).relu().sum()
+    y = w3.matmul(s).sigmoid().tanh()                       # [2,16,24] . [24,8] -> [2,16,8]
+    z = y.add_tensor(y.mean_dims([2], True)).softmax(2).log().mean()
+    loss = chain.mul_scalar(1e-6).add_tensor(z)
+    loss.backward()
+    opt.step(leaves)
+    opt.zero_grad(leaves)
+    return loss
+
+
+def test_replays_of_other_ops(T):
+    def make():
+        rng = np.random.default_rng(8)
+        n = 4099  # ragged: scalar tails
+        vals = [rng.standard_normal(n).astype(np.float32), rng.standard_normal(n).astype(np.float32),
+                rng.uniform(0.5, 2.0, n).astype(np.float32),
+                (0.2 * rng.standard_normal((2, 16, 24))).astype(np.float32),
+                (0.2 * rng.standard_normal((24, 8))).astype(np.float32)]
+        leaves = [T.Tensor.from_slice(v, list(v.shape)).with_requires_grad() for v in vals]
+        opt = T.Adam.with_learning_rate(1e-2)
+        opt.add_parameters(leaves)
+        return leaves, opt
+
+    leaves, opt = make()
+    for _ in range(5):
+        want_loss = _other_ops_step(T, leaves, opt).value()
+    want = [v.data() for v in leaves]
+
+    leaves, opt = make()
+    _other_ops_step(T, leaves, opt)
+    with T.StepGraph.record() as g:
+        loss = _other_ops_step(T, leaves, opt)
+    g.replay(4)
+    for i, (v, w) in enumerate(zip(leaves, want)):
+        assert_bits_equal(v.data(), w, f"leaf {i}")
+    assert loss.value() == want_loss
+    assert opt.step_count() == 5
+    g.free()
+
+
 def test_counters_follow_the_replays(T):
     widths, batch, readme = CASES["deep"]
     ps, x, t = _model(T, widths, batch, 3)
