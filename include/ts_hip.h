@@ -56,6 +56,18 @@ int ts_hip_memcpy(float *dst, const float *src, size_t n_floats, int kind);
 int ts_hip_memcpy_async(float *dst, const float *src, size_t n_floats, int kind, void *stream);
 /* the same for a byte count (checkpoint records are 5 bytes per element) */
 int ts_hip_memcpy_bytes(void *dst, const void *src, size_t bytes, int kind, void *stream);
+/* Code objects: load a caller's gfx950 code object (hipModuleLoadData),
+ * look a kernel up by name and launch it (hipModuleLaunchKernel; kernel_params
+ * is an array of pointers to the arguments, as there).  This library's own
+ * kernels are linked into it and need none of this; the entries complete the
+ * runtime surface a host binding needs for kernels of its own (no
+ * counterpart in the reference's CUDA stub, cuda/mod.rs:139-208). */
+int ts_hip_module_load_data(const void *image, void **module);
+int ts_hip_module_unload(void *module);
+int ts_hip_module_get_function(void *module, const char *name, void **function);
+int ts_hip_module_launch(void *function, unsigned grid_x, unsigned grid_y, unsigned grid_z, unsigned block_x,
+                         unsigned block_y, unsigned block_z, unsigned lds_bytes, void *stream,
+                         void **kernel_params);
 /* pinned host memory for asynchronous device->host copies */
 int ts_hip_host_malloc(void **ptr, size_t bytes);
 int ts_hip_host_free(void *ptr);

@@ -123,6 +123,11 @@ HIP_SIGNATURES = {
                                                 _c.c_float, VP, VP, VP]),
     "ts_hip_adam_bias_corrections": (_c.c_int, [_c.c_float, _c.c_float, _c.c_uint64, SZ, VP]),
     "ts_hip_slot_advance": (_c.c_int, [VP, VP]),
+    "ts_hip_module_load_data": (_c.c_int, [VP, _c.POINTER(VP)]),
+    "ts_hip_module_unload": (_c.c_int, [VP]),
+    "ts_hip_module_get_function": (_c.c_int, [VP, _c.c_char_p, _c.POINTER(VP)]),
+    "ts_hip_module_launch": (_c.c_int, [VP, _c.c_uint, _c.c_uint, _c.c_uint, _c.c_uint, _c.c_uint, _c.c_uint,
+                                        _c.c_uint, VP, _c.POINTER(VP)]),
     "ts_hip_stream_begin_capture": (_c.c_int, [VP]),
     "ts_hip_stream_end_capture": (_c.c_int, [VP, _c.POINTER(VP)]),
     "ts_hip_stream_is_capturing": (_c.c_int, [VP, _c.POINTER(_c.c_int)]),

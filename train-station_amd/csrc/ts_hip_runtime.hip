@@ -28,6 +28,14 @@ int device_cu_count() {
     return g_cu_count[dev];
 }
 
+// A HIP status returned to the caller is also consumed from HIP's per-thread
+// last error, so that a failure reported here is not reported again by the
+// next kernel launch's status check.
+static int status_of(hipError_t e) {
+    if (e != hipSuccess) (void)hipGetLastError();
+    return static_cast<int>(e);
+}
+
 static hipMemcpyKind copy_kind(int kind, bool *ok) {
     *ok = true;
     switch (kind) {
@@ -47,14 +55,14 @@ extern "C" {
 int ts_hip_initialize(void) {
     int count = 0;
     hipError_t e = hipGetDeviceCount(&count);
-    if (e != hipSuccess) return static_cast<int>(e);
+    if (e != hipSuccess) return tship::status_of(e);
     if (count <= 0) return TS_HIP_ENODEVICE;
     hipDeviceProp_t prop;
     e = hipGetDeviceProperties(&prop, 0);
-    if (e != hipSuccess) return static_cast<int>(e);
+    if (e != hipSuccess) return tship::status_of(e);
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return TS_HIP_ENODEVICE;
     e = hipSetDevice(0);
-    if (e != hipSuccess) return static_cast<int>(e);
+    if (e != hipSuccess) return tship::status_of(e);
     device_cu_count();
     return TS_HIP_OK;
 }
@@ -66,26 +74,26 @@ int ts_hip_get_device_count(int *count) {
     *count = 0;
     hipError_t e = hipGetDeviceCount(count);
     if (e == hipErrorNoDevice) { *count = 0; return TS_HIP_OK; }
-    return static_cast<int>(e);
+    return tship::status_of(e);
 }
 
-int ts_hip_set_device(int device_id) { return static_cast<int>(hipSetDevice(device_id)); }
+int ts_hip_set_device(int device_id) { return tship::status_of(hipSetDevice(device_id)); }
 
 int ts_hip_get_device(int *device_id) {
     if (!device_id) return TS_HIP_EINVAL;
-    return static_cast<int>(hipGetDevice(device_id));
+    return tship::status_of(hipGetDevice(device_id));
 }
 
 int ts_hip_malloc(float **ptr, size_t n_floats) {
     if (!ptr) return TS_HIP_EINVAL;
     *ptr = nullptr;
     if (n_floats == 0) return TS_HIP_OK;
-    return static_cast<int>(hipMalloc(reinterpret_cast<void **>(ptr), n_floats * sizeof(float)));
+    return tship::status_of(hipMalloc(reinterpret_cast<void **>(ptr), n_floats * sizeof(float)));
 }
 
 int ts_hip_free(float *ptr) {
     if (!ptr) return TS_HIP_OK;
-    return static_cast<int>(hipFree(ptr));
+    return tship::status_of(hipFree(ptr));
 }
 
 int ts_hip_memcpy(float *dst, const float *src, size_t n_floats, int kind) {
@@ -93,7 +101,7 @@ int ts_hip_memcpy(float *dst, const float *src, size_t n_floats, int kind) {
     hipMemcpyKind k = copy_kind(kind, &ok);
     if (!ok || (n_floats && (!dst || !src))) return TS_HIP_EINVAL;
     if (n_floats == 0) return TS_HIP_OK;
-    return static_cast<int>(hipMemcpy(dst, src, n_floats * sizeof(float), k));
+    return tship::status_of(hipMemcpy(dst, src, n_floats * sizeof(float), k));
 }
 
 int ts_hip_memcpy_async(float *dst, const float *src, size_t n_floats, int kind, void *stream) {
@@ -101,7 +109,7 @@ int ts_hip_memcpy_async(float *dst, const float *src, size_t n_floats, int kind,
     hipMemcpyKind k = copy_kind(kind, &ok);
     if (!ok || (n_floats && (!dst || !src))) return TS_HIP_EINVAL;
     if (n_floats == 0) return TS_HIP_OK;
-    return static_cast<int>(
+    return tship::status_of(
         hipMemcpyAsync(dst, src, n_floats * sizeof(float), k, as_stream(stream)));
 }
 
@@ -110,19 +118,19 @@ int ts_hip_memcpy_bytes(void *dst, const void *src, size_t bytes, int kind, void
     hipMemcpyKind k = copy_kind(kind, &ok);
     if (!ok || (bytes && (!dst || !src))) return TS_HIP_EINVAL;
     if (bytes == 0) return TS_HIP_OK;
-    return static_cast<int>(hipMemcpyAsync(dst, src, bytes, k, as_stream(stream)));
+    return tship::status_of(hipMemcpyAsync(dst, src, bytes, k, as_stream(stream)));
 }
 
 int ts_hip_host_malloc(void **ptr, size_t bytes) {
     if (!ptr) return TS_HIP_EINVAL;
     *ptr = nullptr;
     if (bytes == 0) return TS_HIP_OK;
-    return static_cast<int>(hipHostMalloc(ptr, bytes, hipHostMallocDefault));
+    return tship::status_of(hipHostMalloc(ptr, bytes, hipHostMallocDefault));
 }
 
 int ts_hip_host_free(void *ptr) {
     if (!ptr) return TS_HIP_OK;
-    return static_cast<int>(hipHostFree(ptr));
+    return tship::status_of(hipHostFree(ptr));
 }
 
 int ts_hip_stream_create(void **stream) {
@@ -130,52 +138,83 @@ int ts_hip_stream_create(void **stream) {
     hipStream_t s = nullptr;
     hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
     *stream = s;
-    return static_cast<int>(e);
+    return tship::status_of(e);
 }
 
 int ts_hip_stream_destroy(void *stream) {
     if (!stream) return TS_HIP_OK;
-    return static_cast<int>(hipStreamDestroy(as_stream(stream)));
+    return tship::status_of(hipStreamDestroy(as_stream(stream)));
 }
 
 int ts_hip_stream_synchronize(void *stream) {
-    return static_cast<int>(hipStreamSynchronize(as_stream(stream)));
+    return tship::status_of(hipStreamSynchronize(as_stream(stream)));
 }
 
-int ts_hip_device_synchronize(void) { return static_cast<int>(hipDeviceSynchronize()); }
+int ts_hip_device_synchronize(void) { return tship::status_of(hipDeviceSynchronize()); }
 
 int ts_hip_event_create(void **event) {
     if (!event) return TS_HIP_EINVAL;
     hipEvent_t ev = nullptr;
     hipError_t e = hipEventCreate(&ev);
     *event = ev;
-    return static_cast<int>(e);
+    return tship::status_of(e);
 }
 
 int ts_hip_event_destroy(void *event) {
     if (!event) return TS_HIP_OK;
-    return static_cast<int>(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)));
+    return tship::status_of(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)));
 }
 
 int ts_hip_event_record(void *event, void *stream) {
     if (!event) return TS_HIP_EINVAL;
-    return static_cast<int>(hipEventRecord(reinterpret_cast<hipEvent_t>(event), as_stream(stream)));
+    return tship::status_of(hipEventRecord(reinterpret_cast<hipEvent_t>(event), as_stream(stream)));
 }
 
 int ts_hip_event_synchronize(void *event) {
     if (!event) return TS_HIP_EINVAL;
-    return static_cast<int>(hipEventSynchronize(reinterpret_cast<hipEvent_t>(event)));
+    return tship::status_of(hipEventSynchronize(reinterpret_cast<hipEvent_t>(event)));
 }
 
 int ts_hip_event_elapsed_ms(float *ms, void *start, void *stop) {
     if (!ms || !start || !stop) return TS_HIP_EINVAL;
-    return static_cast<int>(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start),
+    return tship::status_of(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start),
                                                 reinterpret_cast<hipEvent_t>(stop)));
+}
+
+int ts_hip_module_load_data(const void *image, void **module) {
+    if (!image || !module) return TS_HIP_EINVAL;
+    hipModule_t m = nullptr;
+    const hipError_t e = hipModuleLoadData(&m, image);
+    *module = e == hipSuccess ? m : nullptr;
+    return tship::status_of(e);
+}
+
+int ts_hip_module_unload(void *module) {
+    if (!module) return TS_HIP_OK;
+    return tship::status_of(hipModuleUnload(reinterpret_cast<hipModule_t>(module)));
+}
+
+int ts_hip_module_get_function(void *module, const char *name, void **function) {
+    if (!module || !name || !function) return TS_HIP_EINVAL;
+    hipFunction_t f = nullptr;
+    const hipError_t e = hipModuleGetFunction(&f, reinterpret_cast<hipModule_t>(module), name);
+    *function = e == hipSuccess ? f : nullptr;
+    return tship::status_of(e);
+}
+
+int ts_hip_module_launch(void *function, unsigned grid_x, unsigned grid_y, unsigned grid_z, unsigned block_x,
+                         unsigned block_y, unsigned block_z, unsigned lds_bytes, void *stream,
+                         void **kernel_params) {
+    if (!function || !grid_x || !grid_y || !grid_z || !block_x || !block_y || !block_z) return TS_HIP_EINVAL;
+    if (static_cast<unsigned long long>(block_x) * block_y * block_z > 1024) return TS_HIP_EINVAL;
+    return tship::status_of(hipModuleLaunchKernel(reinterpret_cast<hipFunction_t>(function), grid_x, grid_y,
+                                                  grid_z, block_x, block_y, block_z, lds_bytes,
+                                                  as_stream(stream), kernel_params, nullptr));
 }
 
 int ts_hip_stream_begin_capture(void *stream) {
     if (!stream) return TS_HIP_EINVAL;  // the null stream cannot be recorded
-    return static_cast<int>(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeRelaxed));
+    return tship::status_of(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeRelaxed));
 }
 
 int ts_hip_stream_end_capture(void *stream, void **graph_exec) {
@@ -183,11 +222,11 @@ int ts_hip_stream_end_capture(void *stream, void **graph_exec) {
     *graph_exec = nullptr;
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(as_stream(stream), &graph);
-    if (e != hipSuccess) return static_cast<int>(e);
+    if (e != hipSuccess) return tship::status_of(e);
     hipGraphExec_t exec = nullptr;
     e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);  // the executable graph keeps its own copy
-    if (e != hipSuccess) return static_cast<int>(e);
+    if (e != hipSuccess) return tship::status_of(e);
     *graph_exec = exec;
     return TS_HIP_OK;
 }
@@ -197,17 +236,17 @@ int ts_hip_stream_is_capturing(void *stream, int *capturing) {
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     const hipError_t e = hipStreamIsCapturing(as_stream(stream), &st);
     *capturing = st == hipStreamCaptureStatusActive ? 1 : 0;
-    return static_cast<int>(e);
+    return tship::status_of(e);
 }
 
 int ts_hip_graph_launch(void *graph_exec, void *stream) {
     if (!graph_exec) return TS_HIP_EINVAL;
-    return static_cast<int>(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph_exec), as_stream(stream)));
+    return tship::status_of(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph_exec), as_stream(stream)));
 }
 
 int ts_hip_graph_destroy(void *graph_exec) {
     if (!graph_exec) return TS_HIP_OK;
-    return static_cast<int>(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph_exec)));
+    return tship::status_of(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph_exec)));
 }
 
 const char *ts_hip_error_string(int status) {
@@ -222,7 +261,7 @@ const char *ts_hip_error_string(int status) {
 
 int ts_hip_mem_info(size_t *free_bytes, size_t *total_bytes) {
     if (!free_bytes || !total_bytes) return TS_HIP_EINVAL;
-    return static_cast<int>(hipMemGetInfo(free_bytes, total_bytes));
+    return tship::status_of(hipMemGetInfo(free_bytes, total_bytes));
 }
 
 }  // extern "C"
