@@ -73,7 +73,7 @@ struct GemmArgs {
     long long sa[kMaxBatchRank], sb[kMaxBatchRank];
     long long sc;
     // Epilogue (plain form only; all null / 0 for a bare product): the stored
-    // value is the product, plus bias[j] when bias is set, then max(., +0) as
+    // value is the product, plus bias[j] when bias is set, then v > 0 ? v : +0 as
     // relu does when relu is set, then kept only where mask[i*ldc + j] > 0
     // (relu's backward with its saved output) when mask is set.
     const float *bias;
@@ -84,7 +84,7 @@ struct GemmArgs {
 // Store of a wave's FM x FN accumulator blocks, the wave tile's corner at
 // (i0, j0).  Accumulator layout of v_mfma_f32_32x32x2_f32: lane l, register
 // r holds C[8*(r/4) + 4*(l/32) + r%4][l%32] of the 32x32 block.  With EPI the
-// stored value is the product, plus bias[j], then max(., +0) (relu), then
+// stored value is the product, plus bias[j], then v > 0 ? v : +0 (relu), then
 // kept only where mask[i*ldc + j] > 0: the unfused ops in their order.  A row
 // of blocks at a time: its mask is loaded before its first store, so those
 // loads overlap each other (every block's at once would need a register per
