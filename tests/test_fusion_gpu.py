@@ -195,3 +195,32 @@ def test_profiler_charges_fused_products_to_the_gemm_class(fusion):
     assert g["launches"] == 8
     flops = 2.0 * 1024 * (256 * 512 + 512 * 512 + 512 * 128)
     assert abs(g["work"] - flops * (1 + 1) - 2.0 * 1024 * (512 * 512 + 512 * 128)) < 1.0
+
+
+def test_product_with_several_consumers(fusion):
+    # a deferred product read by the fused bias + relu chain and, separately,
+    # by other ops (a scalar multiply, a second bias add): every branch and
+    # every gradient equals the unfused graph's
+    T = fusion
+    out = {}
+    for on in (True, False):
+        T.set_fusion(on)
+        x = T.Tensor.from_slice(normal((300, 260), 1), [300, 260])
+        w = T.Tensor.from_slice((normal((260, 130), 2) / 16).astype(np.float32), [260, 130]).with_requires_grad()
+        b = T.Tensor.from_slice(normal(130, 3), [130]).with_requires_grad()
+        b2 = T.Tensor.from_slice(normal(130, 4), [130]).with_requires_grad()
+        h = x.matmul(w)
+        a = h.add_tensor(b).relu()          # fused into the product's store
+        c = h.mul_scalar(2.0)               # reads the bare product
+        d = b2.add_tensor(h).relu()         # a second fused chain on the same product
+        loss = a.add_tensor(c).mul_tensor(d).sum()
+        loss.backward()
+        out[on] = (loss.value(), a.data(), c.data(), d.data(),
+                   [p.grad_by_value().data() for p in (w, b, b2)])
+        T.clear_gradients()
+    (l1, a1, c1, d1, g1), (l0, a0, c0, d0, g0) = out[True], out[False]
+    assert l1 == l0
+    for name, u, v in (("a", a1, a0), ("c", c1, c0), ("d", d1, d0)):
+        assert_bits_equal(u, v, name)
+    for i, (u, v) in enumerate(zip(g1, g0)):
+        assert_bits_equal(u, v, f"grad {i}")
