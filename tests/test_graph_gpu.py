@@ -210,6 +210,30 @@ def test_graph_buffers_stay_reserved(T):
     assert T.pool_stats()["live_bytes"] < live
 
 
+def test_product_deferred_before_the_recording_stays_reserved(T):
+    # a product deferred before the recording and run inside it because
+    # Adam::step overwrites its operand (before_write) writes its output on
+    # every replay: that block must not be handed to other work when its
+    # tensor is dropped
+    x = T.Tensor.from_slice(np.ones((256, 192), np.float32), [256, 192])
+    w = T.Tensor.from_slice(np.full((192, 256), 0.5, np.float32), [192, 256]).with_requires_grad()
+    gw = T.Tensor.from_slice(np.full((192, 256), 0.01, np.float32), [192, 256])
+    opt = T.Adam.with_learning_rate(1e-3)
+    opt.add_parameter(w)
+    h = x.matmul(w)                                    # deferred, not run
+    with T.StepGraph.record() as g:
+        w.set_grad(gw)
+        opt.step([w])                                  # runs h's product first, inside the recording
+    del h
+    gc.collect()
+    other = [T.Tensor.from_slice(np.full((256, 256), 7.0, np.float32), [256, 256]) for _ in range(4)]
+    g.replay(3)
+    for o in other:
+        assert_bits_equal(o.data(), np.full((256, 256), 7.0, np.float32))
+    g.free()
+    T.clear_gradients()
+
+
 def test_reading_inside_a_recording_is_refused(T):
     widths, batch, readme = CASES["deep"]
     ps, x, t = _model(T, widths, batch, 2)

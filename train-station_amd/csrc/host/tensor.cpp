@@ -234,6 +234,7 @@ void materialize(Allocation &a) {
     const float *bias = p->bias ? p->bias->get() : nullptr;
     const float *mask = p->mask ? p->mask->get() : nullptr;
     float *C = a.raw();
+    DevicePool::get().note_use(C);  // a step being recorded writes it on every replay
     launch(KernelClass::Gemm, 2.0 * p->M * p->N * p->K, "ts_hip_gemm_fused", [&] {
         return gemm2d(p->ta, p->tb, p->M, p->N, p->K, A, p->lda, B, p->ldb, bias, p->relu, mask, C, p->N);
     });
