@@ -211,6 +211,10 @@ void ts_pool_empty_cache(void);
 /* kernel timing with device events: class 0 GEMM (work = FLOP), 1 elementwise,
  * 2 reduction, 3 Adam (work = algorithmic bytes) */
 void ts_profile_enable(int on);
+/* Classes timed while profiling: bit k for class k (0 GEMM, 1 elementwise,
+ * 2 reduction, 3 Adam); all by default.  Launches of the other classes record
+ * no events and perturb the stream less. */
+void ts_profile_classes(unsigned mask);
 void ts_profile_reset(void);
 int ts_profile_read(int kernel_class, double *ms, double *work, uint64_t *launches);
 

@@ -243,6 +243,7 @@ GRADTRACK_SIGNATURES = {
     "ts_pool_live_bytes": (SZ, []),
     "ts_pool_cached_bytes": (SZ, []),
     "ts_pool_empty_cache": (None, []),
+    "ts_profile_classes": (None, [_c.c_uint]),
     "ts_profile_enable": (None, [_c.c_int]),
     "ts_profile_reset": (None, []),
     "ts_profile_read": (_c.c_int, [_c.c_int, _c.POINTER(_c.c_double), _c.POINTER(_c.c_double),

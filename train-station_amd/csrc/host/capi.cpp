@@ -491,6 +491,8 @@ void ts_pool_empty_cache(void) {
     ts::DevicePool::get().empty_cache();
 }
 
+void ts_profile_classes(unsigned mask) { ts::Profiler::get().set_classes(mask); }
+
 void ts_profile_enable(int on) {
     try {
         ts::Profiler::get().enable(on != 0);

@@ -188,9 +188,6 @@ void Profiler::enable(bool on) {
     enabled_ = on;
 }
 
-// Launches can nest: a deferred product runs when a later launch first reads
-// its result, inside that launch's window.  The outer window is then split
-// around the inner one, so each launch is charged only its own time.
 void *Profiler::event() {
     void *ev = nullptr;
     if (!spare_.empty()) { ev = spare_.back(); spare_.pop_back(); }
@@ -199,28 +196,56 @@ void *Profiler::event() {
     return ev;
 }
 
-void Profiler::begin() {
+// Launches can nest: a deferred product runs when a later launch first reads
+// its result, inside that launch's window.  The innermost timed window that
+// encloses a timed launch is paused for its duration and resumed after it, so
+// each timed launch is charged its own time only.  (An untimed launch inside a
+// timed window would be charged to it; nested launches are deferred products,
+// GEMMs, so that happens only when the GEMM class is not timed.)
+void Profiler::pause_enclosing() {
+    for (size_t i = open_.size(); i-- > 0;)
+        if (open_[i].timed) {
+            open_[i].segments.back().second = event();
+            return;
+        }
+}
+
+void Profiler::resume_enclosing() {
+    for (size_t i = open_.size(); i-- > 0;)
+        if (open_[i].timed) {
+            open_[i].segments.push_back({event(), nullptr});
+            return;
+        }
+}
+
+void Profiler::begin(KernelClass k) {
     if (!enabled_) return;
-    if (!open_.empty()) open_.back().back().second = event();  // pause the enclosing launch
-    open_.push_back({{event(), nullptr}});
+    const bool timed = (classes_ >> static_cast<int>(k)) & 1u;
+    if (timed) pause_enclosing();
+    Frame f{timed, {}};
+    if (timed) f.segments.push_back({event(), nullptr});
+    open_.push_back(std::move(f));
 }
 
 void Profiler::abort() {
     if (!enabled_ || open_.empty()) return;
-    for (auto &seg : open_.back()) {
+    Frame f = std::move(open_.back());
+    open_.pop_back();
+    for (auto &seg : f.segments) {
         if (seg.first) spare_.push_back(seg.first);
         if (seg.second) spare_.push_back(seg.second);
     }
-    open_.pop_back();
-    if (!open_.empty()) open_.back().push_back({event(), nullptr});
+    if (f.timed) resume_enclosing();
 }
 
 void Profiler::end(KernelClass k, double work) {
     if (!enabled_ || open_.empty()) return;
-    open_.back().back().second = event();
-    pending_.push_back(Pending{std::move(open_.back()), k, work});
+    Frame f = std::move(open_.back());
     open_.pop_back();
-    if (!open_.empty()) open_.back().push_back({event(), nullptr});  // resume the enclosing one
+    if (!f.timed) return;
+    f.segments.back().second = event();
+    pending_.push_back(Pending{std::move(f.segments), k, work});
+    resume_enclosing();
 }
 
 void Profiler::collect() {

@@ -160,7 +160,11 @@ class Profiler {
     static Profiler &get();
     void enable(bool on);
     bool enabled() const { return enabled_; }
-    void begin();
+    // Classes timed (bit k for KernelClass k; all by default).  Launches of
+    // other classes record no events, so timing one class perturbs the rest
+    // of the stream least.
+    void set_classes(unsigned mask) { classes_ = mask; }
+    void begin(KernelClass k);
     void end(KernelClass k, double work);
     void abort();  // the launch failed: drop its window
     // Synchronises and folds every recorded launch into the totals.
@@ -175,9 +179,16 @@ class Profiler {
         KernelClass k;
         double work;
     };
+    struct Frame {
+        bool timed;         // its class is selected: its segments are recorded
+        Segments segments;  // while timed
+    };
     void *event();
+    void pause_enclosing();
+    void resume_enclosing();
     bool enabled_ = false;
-    std::vector<Segments> open_;  // launches in progress, innermost last
+    unsigned classes_ = ~0u;
+    std::vector<Frame> open_;  // launches in progress, innermost last
     std::vector<Pending> pending_;
     std::vector<void *> spare_;
     ClassStats totals_[static_cast<int>(KernelClass::kCount)];
@@ -190,7 +201,7 @@ class Profiler {
 template <class F>
 void launch(KernelClass k, double work, const char *what, F &&f) {
     Profiler &P = Profiler::get();
-    P.begin();
+    P.begin(k);
     try {
         check(f(), what);
     } catch (...) {

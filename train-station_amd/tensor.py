@@ -509,7 +509,10 @@ class Profile:
     GEMM, ELEMENTWISE, REDUCTION, ADAM = 0, 1, 2, 3
 
     @staticmethod
-    def enable(on: bool = True) -> None:
+    def enable(on: bool = True, classes: Optional[Sequence[int]] = None) -> None:
+        """Time launches of `classes` (default: all); the others record no events."""
+        mask = 0xFFFFFFFF if classes is None else sum(1 << int(k) for k in classes)
+        _G.ts_profile_classes(mask)
         _G.ts_profile_enable(int(bool(on)))
 
     @staticmethod
