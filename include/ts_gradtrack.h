@@ -183,7 +183,9 @@ int ts_fusion_enabled(void);
  * of it as one graph launch, the first replay running the recorded step
  * itself.  A replayed ts_adam_step uses the bias corrections of the step count
  * it would have in an eager loop, and the optimizer's counters advance with the
- * replays, so N replays give the bits of N eager steps.  Rules:
+ * replays, so N replays give the bits of N eager steps (a graph freed before
+ * its first replay leaves the counters as they were before the recording).
+ * Rules:
  *  - inside the recording nothing may wait for or read the device
  *    (ts_tensor_value / data, ts_synchronize) or upload host data
  *    (ts_tensor_from_slice): create inputs before, read results after a replay;
@@ -191,6 +193,8 @@ int ts_fusion_enabled(void);
  *    freed (tensors dropped meanwhile are not reused), and a replay reads the
  *    current contents of the inputs it recorded: refill them in place
  *    (ts_tensor_device_ptr + copies) to feed new data;
+ *  - link parameters to the optimizer (ts_adam_add_parameter) before the
+ *    recording;
  *  - record an AMSGrad step only after the optimizer's first step; the
  *    learning rate and other settings are the recorded ones;
  *  - the profiler must be off while recording.

@@ -254,6 +254,48 @@ def test_reading_inside_a_recording_is_refused(T):
     g.free()
 
 
+def test_a_graph_freed_unreplayed_leaves_the_counters(T):
+    # the recorded step never runs: the optimizer's count returns to its value
+    # before the recording, and eager steps after it match an eager-only loop
+    widths, batch, readme = CASES["deep"]
+    ps, x, t = _model(T, widths, batch, 3)
+    ps2, x2, t2 = _model(T, widths, batch, 3)
+    opt = T.Adam.with_learning_rate(1e-3)
+    opt.add_parameters(ps)
+    opt2 = T.Adam.with_learning_rate(1e-3)
+    opt2.add_parameters(ps2)
+    _step(ps, x, t, opt, readme)
+    _step(ps2, x2, t2, opt2, readme)
+    with T.StepGraph.record() as g:
+        _step(ps, x, t, opt, readme)
+    assert opt.step_count() == 2                      # counted at recording
+    g.free()
+    assert opt.step_count() == 1
+    for _ in range(2):
+        _step(ps, x, t, opt, readme)
+        _step(ps2, x2, t2, opt2, readme)
+    assert opt.step_count() == opt2.step_count() == 3
+    for p, q in zip(ps, ps2):
+        assert_bits_equal(p.data(), q.data())
+    T.clear_gradients()
+
+
+def test_linking_a_parameter_inside_a_recording_is_refused(T):
+    # its state's zero fill would rerun on every replay
+    widths, batch, readme = CASES["deep"]
+    ps, x, t = _model(T, widths, batch, 4)
+    opt = T.Adam.with_learning_rate(1e-3)
+    opt.add_parameters(ps[:-1])
+    with pytest.raises(T.TsError, match="before recording"):
+        with T.StepGraph.record():
+            opt.add_parameters(ps[-1:])
+    assert not T.recording()
+    opt.add_parameters(ps[-1:])                       # eagerly, it links
+    _step(ps, x, t, opt, readme)
+    assert opt.step_count() == 1
+    T.clear_gradients()
+
+
 def test_uploads_inside_a_recording_are_refused(T):
     widths, batch, readme = CASES["deep"]
     ps, x, t = _model(T, widths, batch, 6)

@@ -25,6 +25,9 @@ Adam Adam::with_learning_rate(float lr) {
 void Adam::add_parameter(const Tensor &p) {
     if (!p.requires_grad()) throw Error("Parameter must require gradients");
     if (states_.count(p.id())) return;
+    // the state's zero fill would be recorded and so rerun by every replay
+    if (StepRecorder::get().open())
+        throw Error("add_parameter: link parameters to the optimizer before recording a step");
     State s;
     s.n = p.size();
     s.dims = p.dims();

@@ -73,14 +73,17 @@ StepGraph *StepRecorder::end() {
 void StepRecorder::abort() {
     if (!graph_) return;
     std::unique_ptr<StepGraph> g = std::move(graph_);
-    for (StepGraph::AdamUse &u : g->adams) u.steps->pending -= 1;  // the recorded step never runs
     void *exec = nullptr;
     (void)ts_hip_stream_end_capture(Runtime::get().stream(), &exec);
     DevicePool::get().pin_end();
-    g->exec = exec;  // destroyed with g
+    g->exec = exec;  // destroyed with g, which takes back the recorded step's count
 }
 
 StepGraph::~StepGraph() {
+    // the optimizer counted the recorded step when it was recorded; a graph
+    // that never ran (aborted, failed or freed unreplayed) takes that back
+    if (!executed)
+        for (AdamUse &u : adams) u.steps->pending -= 1;
     if (exec) {
         // replays may still be running
         (void)ts_hip_stream_synchronize(Runtime::get().stream());
