@@ -296,6 +296,46 @@ def test_adam_100_steps_bit_exact(oracle):
     assert_bits_equal(dv.get(), v, "v after 100 steps")
 
 
+def test_adam_large_tensors_bit_exact(oracle):
+    # tensors of 2^26 parameters and more take the non-temporal load / store
+    # path (one tensor alone, then in one launch beside a small tensor, which
+    # keeps the ordinary path); AMSGrad and weight decay on, odd size for the tail
+    from train_station_amd._ffi import AdamParam
+    import ctypes
+    n = (1 << 26) + 5
+    print(f"[adam] large n={n}", flush=True)
+    p = normal(n, 16)
+    m = np.zeros(n, np.float32)
+    v = np.zeros(n, np.float32)
+    vm = np.zeros(n, np.float32)
+    small = [normal(1000, 17), np.zeros(1000, np.float32), np.zeros(1000, np.float32)]
+    dp, dm, dv, dvm = Dev.of(p), Dev.of(m), Dev.of(v), Dev.of(vm)
+    ds = [Dev.of(a) for a in small]
+    for step in range(1, 4):
+        g = normal(n, 400 + step, 0.1)
+        dg = Dev.of(g)
+        if step < 3:
+            _run("ts_hip_adam_step", dp.ptr, dg.ptr, dm.ptr, dv.ptr, dvm.ptr, n, 1e-3, 0.9, 0.999, 1e-8, 0.01,
+                 step, (n // 8) * 8, int(step == 1), None)
+        else:
+            gs = normal(1000, 500, 0.1)
+            dgs = Dev.of(gs)
+            arr = (AdamParam * 2)()
+            arr[0] = AdamParam(dp.ptr, dg.ptr, dm.ptr, dv.ptr, dvm.ptr, n, 0)
+            arr[1] = AdamParam(ds[0].ptr, dgs.ptr, ds[1].ptr, ds[2].ptr, None, 1000, 0)
+            _run("ts_hip_adam_step_multi", ctypes.cast(arr, ctypes.c_void_p), 2, 1e-3, 0.9, 0.999, 1e-8, 0.01,
+                 step, None)
+        oracle.adam_step(p, g, m, v, step, weight_decay=0.01, vmax=vm, amsgrad_first=(step == 1))
+    # the small tensor stepped once (its first step, without AMSGrad)
+    oracle.adam_step(small[0], gs, small[1], small[2], 3, weight_decay=0.01)
+    assert_bits_equal(dp.get(), p, "p")
+    assert_bits_equal(dm.get(), m, "m")
+    assert_bits_equal(dv.get(), v, "v")
+    assert_bits_equal(dvm.get(), vm, "v_hat_max")
+    assert_bits_equal(ds[0].get(), small[0], "small p")
+    assert_bits_equal(ds[2].get(), small[2], "small v")
+
+
 def test_adam_multi_matches_per_parameter(oracle):
     # one launch over several parameters (different sizes, tails, AMSGrad
     # first/later steps, weight decay) gives the per-parameter bits
