@@ -88,12 +88,14 @@ def step_flops(batch, widths, readme):
 
 
 def pmc_traffic(cfg_name: str):
-    """HBM bytes per GEMM launch from the committed rocprofv3 --pmc summary of
-    this workload (FETCH_SIZE and WRITE_SIZE runs, each scaled by the copy-kernel
-    calibration recorded in the same file), or None."""
+    """HBM bytes per launch of the roofline's kernel (the GEMMs; Adam for config
+    3) from the committed rocprofv3 --pmc summary of this workload (FETCH_SIZE and
+    WRITE_SIZE runs, each scaled by the copy-kernel calibration recorded in the
+    same file), or None."""
     import re
 
-    path = ROOT / "profiles" / f"{cfg_name}_gemm_pmc.md"
+    kernel = {"c3": "adam"}.get(cfg_name, "gemm")
+    path = ROOT / "profiles" / f"{cfg_name}_{kernel}_pmc.md"
     if not path.exists():
         return None, None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+-]+)", path.read_text())
@@ -290,6 +292,9 @@ def bandwidth_main(args, TS, hip, hip_check) -> int:
     kernels = {k: {"ms_per_step": round(v["ms"] / args.steps, 3), "launches_per_step": v["launches"] // args.steps,
                    "GB/s": round(v["work"] / (v["ms"] * 1e-3) / 1e9, 1) if v["ms"] > 0 else 0.0}
                for k, v in prof.items()}
+    # HBM bytes per launch from the committed counters: config 3 only (one Adam
+    # launch per step; config 2 runs several kernels of different byte counts)
+    traffic, traffic_src = pmc_traffic(args.config) if args.config == "c3" else (None, None)
     result = {
         "metric": {"c2": "fwd+bwd steps/sec of the elementwise chain (1 GPU); % HBM GB/s roofline",
                    "c3": "Adam::step steps/sec (1 GPU); % HBM GB/s roofline"}[args.config],
@@ -306,7 +311,7 @@ def bandwidth_main(args, TS, hip, hip_check) -> int:
         "data": data,
         "config": {"workload": workload, "elements": n, "algorithmic_bytes_per_step": work},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
                      "kernel": " + ".join(classes) + " kernels of the step (every launch of the timed region)",
                      "step_bytes_per_wall_time_GBs": round(work / (wall_ms * 1e-3) / 1e9, 1)},
         "kernels": kernels,

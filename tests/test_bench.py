@@ -57,3 +57,14 @@ def test_cpu_baseline_record(cfg):
     assert abs(1.0 / r["value"] - sum(r["breakdown_s"].values())) < 1e-3 + 0.01 / r["value"]
     host = r["host"]
     assert host["host_cores"] >= host["usable_cores"] >= 1 and host["cpu_model"]
+
+
+def test_traffic_from_the_committed_counters():
+    # config 3: one Adam launch per step reads and writes each operand once, so
+    # the counted HBM bytes match 28 B per parameter of 2^28 parameters
+    traffic, src = bench.pmc_traffic("c3")
+    assert src == "profiles/c3_adam_pmc.md"
+    assert abs(traffic / (28 * 2 ** 28) - 1.0) < 0.01
+    traffic, src = bench.pmc_traffic("c5")
+    assert src == "profiles/c5_gemm_pmc.md" and traffic > 0
+    assert bench.pmc_traffic("c2") == (None, None)
