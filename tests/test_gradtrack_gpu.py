@@ -354,3 +354,34 @@ def test_config5_full_size_step(TS, oracle):
     expected = 1e-3 * np.abs(g1) / (np.abs(g1) + 1e-8)
     assert float(np.max(np.abs(moved - expected))) <= 2e-8
     opt.zero_grad(ps)
+
+
+@pytest.mark.gpu
+def test_sub_backward_skips_the_unconsumed_negation(TS):
+    # gradients go to the recorded inputs by position; with constant targets only
+    # the first is consumed, so y - t runs no negation pass, and the gradients
+    # match the case where both inputs require them
+    n = 4099
+    yv, tv = normal(n, 31), normal(n, 32)
+
+    def run(t_grad):
+        y = TS.Tensor.from_slice(yv, [n]).with_requires_grad()
+        t = TS.Tensor.from_slice(tv, [n])
+        if t_grad:
+            t = t.with_requires_grad()
+        TS.Profile.reset()
+        TS.Profile.enable(True)
+        y.sub_tensor(t).pow_scalar(2.0).mean().backward()
+        TS.Profile.enable(False)
+        launches = TS.Profile.read(TS.Profile.ELEMENTWISE)["launches"]
+        gy = y.grad_by_value().data()
+        gt = t.grad_by_value().data() if t_grad else None
+        TS.clear_gradients()
+        return launches, gy, gt
+
+    l1, gy1, _ = run(False)
+    l2, gy2, gt2 = run(True)
+    assert l2 == l1 + 1
+    assert_bits_equal(gy1, gy2)
+    assert_bits_equal(gt2, -gy2)
+    np.testing.assert_allclose(gy1, 2.0 * (yv - tv) / n, rtol=1e-5, atol=1e-9)

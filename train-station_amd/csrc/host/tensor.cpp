@@ -427,6 +427,8 @@ Tensor Tensor::binary(const Tensor &o, GradFn::Kind kind) const {
             fn.shape_b = o.dims_;
         }
         if (kind == GradFn::Kind::Mul || kind == GradFn::Kind::Div) fn.saved = {saved(), o.saved()};
+        fn.req_left = requires_grad_;
+        fn.req_right = o.requires_grad_;
         std::vector<size_t> ids;
         if (requires_grad_) ids.push_back(id_);
         if (o.requires_grad_) ids.push_back(o.id_);
@@ -826,10 +828,17 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
             break;
         }
         case K::Sub: {  // grad_fn/ops/sub.rs:4-33
-            if (!has_shapes) { r.emplace_back(go.alias()); r.emplace_back(neg_of(go)); }
-            else {
+            // Gradients go to the recorded inputs by position, and only the
+            // inputs that require gradients are recorded: the second gradient
+            // has a consumer only when both do (a loss y - t with constant
+            // targets t skips the negation pass).
+            const bool second = req_left && req_right;
+            if (!has_shapes) {
+                r.emplace_back(go.alias());
+                if (second) r.emplace_back(neg_of(go));
+            } else {
                 r.emplace_back(reduce_to(go, shape_a));
-                r.emplace_back(neg_of(reduce_to(go, shape_b)));
+                if (second) r.emplace_back(neg_of(reduce_to(go, shape_b)));
             }
             break;
         }
