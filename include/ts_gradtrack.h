@@ -86,6 +86,12 @@ ts_tensor *ts_tensor_mean_dims(const ts_tensor *a, const size_t *dims, size_t nd
 
 /* Tensor::backward(Option<Tensor>) (utils.rs:634-636); grad_output may be NULL */
 int ts_tensor_backward(ts_tensor *t, const ts_tensor *grad_output);
+/* Tensor::grad (utils.rs:491-506): the gradient stored on the tensor itself
+ * (set_grad, or the backward root's own accumulation), as a handle on the
+ * same buffer and id (no copy; free the handle, the gradient stays); NULL
+ * with ts_last_error() "" when there is none -- also when only the graph's
+ * gradient map holds one, as in the reference. */
+ts_tensor *ts_tensor_grad(const ts_tensor *t);
 /* grad_by_value (utils.rs:525-534): a copy, or NULL with ts_last_error() ""
  * when there is no gradient */
 ts_tensor *ts_tensor_grad_by_value(const ts_tensor *t);
@@ -101,6 +107,8 @@ void ts_clear_gradients(void);
 void ts_no_grad_push(void);
 void ts_no_grad_pop(void);
 int ts_is_grad_enabled(void);
+/* set_grad_enabled (no_grad_track.rs:188-199): replaces the innermost state */
+void ts_set_grad_enabled(int enabled);
 
 /* Adam (optimizers/adam/mod.rs:227-320, :1036-1068) */
 ts_adam *ts_adam_new(void);
@@ -179,13 +187,18 @@ int ts_fusion_enabled(void);
 /* Step graphs (no counterpart in the reference, whose steps run eagerly on
  * the CPU): the library stream's work between ts_step_graph_begin and
  * ts_step_graph_end (typically a forward, ts_tensor_backward, ts_adam_step and
- * ts_adam_zero_grad) is recorded as a HIP graph, not run; each replay runs all
- * of it as one graph launch, the first replay running the recorded step
- * itself.  A replayed ts_adam_step uses the bias corrections of the step count
- * it would have in an eager loop, and the optimizer's counters advance with the
- * replays, so N replays give the bits of N eager steps (a graph freed before
- * its first replay leaves the counters as they were before the recording).
+ * ts_adam_zero_grad) is recorded as a HIP graph, not run -- and not counted:
+ * the optimizer's counters are the same after the recording as before it.
+ * Each replay runs all of it as one graph launch, and each recorded
+ * ts_adam_step in it takes the bias corrections of the step count that
+ * follows the optimizer's count at that moment (eager steps, other graphs and
+ * earlier replays included), so any interleaving of replays and eager steps
+ * gives the bits of the same steps run eagerly, and the counters advance with
+ * the replays.
  * Rules:
+ *  - begin refuses while the gradient map holds gradients (a recorded
+ *    accumulation would add that fixed buffer again on every replay): start
+ *    the recording after zero_grad and end the recorded step with zero_grad;
  *  - inside the recording nothing may wait for or read the device
  *    (ts_tensor_value / data, ts_synchronize) or upload host data
  *    (ts_tensor_from_slice): create inputs before, read results after a replay;

@@ -230,14 +230,27 @@ def sum_dim0_f64(x):
     return out
 
 
-def gemm_f64(a, b, ta=False, tb=False) -> np.ndarray:
-    """op(a) @ op(b) with f64 accumulation; op transposes a [K,M] / b [N,K] view."""
+# Products of at least this many multiply-adds take numpy's float64 matmul
+# (multi-threaded BLAS) instead of the C triple loop: both accumulate exactly
+# representable f32 products in f64, differing only in f64 summation order
+# (pinned against each other in tests/test_oracle.py).  Many-step training
+# comparisons at the configuration shapes need the speed.
+GEMM_F64_BLAS_MIN_MACS = 1 << 22
+
+
+def gemm_f64(a, b, ta=False, tb=False, path: str = "auto") -> np.ndarray:
+    """op(a) @ op(b) with f64 accumulation; op transposes a [K,M] / b [N,K] view.
+    ``path``: "loop" (C), "blas" (numpy float64 matmul) or "auto" (by size)."""
     a, b = _f32(a), _f32(b)
     M = a.shape[1] if ta else a.shape[0]
     K = a.shape[0] if ta else a.shape[1]
     N = b.shape[0] if tb else b.shape[1]
     Kb = b.shape[1] if tb else b.shape[0]
     assert K == Kb, (a.shape, b.shape, ta, tb)
+    if path == "blas" or (path == "auto" and M * N * K >= GEMM_F64_BLAS_MIN_MACS):
+        a64 = a.astype(np.float64)
+        b64 = b.astype(np.float64)
+        return np.ascontiguousarray((a64.T if ta else a64) @ (b64.T if tb else b64))
     out = np.empty((M, N), dtype=np.float64)
     lib().o_gemm_f64(int(ta), int(tb), M, N, K, _p(a), a.shape[1], _p(b), b.shape[1],
                      out.ctypes.data_as(_D))

@@ -403,6 +403,32 @@ def _apply(fn: GradFn, go: np.ndarray) -> list[Optional[np.ndarray]]:
     raise NotImplementedError(k)
 
 
+# Test hook: when set, called as hook(input_id, scale, terms) for every
+# gradient a 2-D matmul backward or a row-broadcast add backward produces,
+# where scale[i] = sum of |terms| of the sum that produced element i (for
+# a^T.go: (|a|^T.|go|)[i, j]; for go.b^T: (|go|.|b|^T)[i, j]; for a bias
+# column sum: sum_r |go[r, j]|) and terms is that sum's length.  Any fp32
+# evaluation of the sum, in any order, lies within terms * 2^-23 * scale of
+# the exact value; a gradient smaller than that has no fp32-determined sign.
+GRAD_SCALE_HOOK = None
+
+
+def _report_scales(fn: GradFn, current: np.ndarray, input_ids, grads) -> None:
+    if fn.kind == "matmul" and fn.saved[0].ndim == 2 and fn.saved[1].ndim == 2:
+        # matmul records both operands (input_ids = [a, b]); f32 products of
+        # the absolute values are ample for a bound
+        a, b = (np.abs(v).astype(np.float32) for v in fn.saved)
+        g = np.abs(current).astype(np.float32)
+        if grads[0] is not None:
+            GRAD_SCALE_HOOK(input_ids[0], (g @ b.T).astype(np.float64), b.shape[1])
+        if grads[1] is not None:
+            GRAD_SCALE_HOOK(input_ids[1], (a.T @ g).astype(np.float64), a.shape[0])
+    elif fn.kind == "add" and fn.shapes is not None:  # gradients go to input_ids by position
+        for idx, shape in enumerate(fn.shapes):
+            if idx < len(input_ids) and len(shape) == 1 and current.ndim == 2 and shape[0] == current.shape[1]:
+                GRAD_SCALE_HOOK(input_ids[idx], np.abs(current.astype(np.float64)).sum(axis=0), current.shape[0])
+
+
 def backward(t: OTensor, grad_output: Optional[np.ndarray] = None) -> None:
     """GradEngine::backward (engine.rs:962-1047)."""
     init = O.fill(t.shape, 1.0) if grad_output is None else np.ascontiguousarray(grad_output, np.float32)
@@ -420,6 +446,8 @@ def backward(t: OTensor, grad_output: Optional[np.ndarray] = None) -> None:
             continue
         input_ids, fn = op
         grads = _apply(fn, current)
+        if GRAD_SCALE_HOOK is not None:
+            _report_scales(fn, current, input_ids, grads)
         for idx, iid in enumerate(input_ids):
             if idx < len(grads) and grads[idx] is not None:
                 g = grads[idx]

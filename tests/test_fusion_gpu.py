@@ -200,7 +200,8 @@ def test_profiler_charges_fused_products_to_the_gemm_class(fusion):
 def test_product_with_several_consumers(fusion):
     # a deferred product read by the fused bias + relu chain and, separately,
     # by other ops (a scalar multiply, a second bias add): every branch and
-    # every gradient equals the unfused graph's
+    # every gradient equals the unfused graph's, and the product runs once
+    # (the chain already deferred on it becomes its epilogue alone)
     T = fusion
     out = {}
     for on in (True, False):
@@ -209,12 +210,24 @@ def test_product_with_several_consumers(fusion):
         w = T.Tensor.from_slice((normal((260, 130), 2) / 16).astype(np.float32), [260, 130]).with_requires_grad()
         b = T.Tensor.from_slice(normal(130, 3), [130]).with_requires_grad()
         b2 = T.Tensor.from_slice(normal(130, 4), [130]).with_requires_grad()
+        T.Profile.reset()
+        T.Profile.enable(True)
         h = x.matmul(w)
         a = h.add_tensor(b).relu()          # fused into the product's store
         c = h.mul_scalar(2.0)               # reads the bare product
         d = b2.add_tensor(h).relu()         # a second fused chain on the same product
         loss = a.add_tensor(c).mul_tensor(d).sum()
+        T.synchronize()
+        T.Profile.enable(False)
+        assert T.Profile.read(T.Profile.GEMM)["launches"] == 1, on   # the forward product, once
+        T.Profile.reset()
+        T.Profile.enable(True)
         loss.backward()
+        T.synchronize()
+        T.Profile.enable(False)
+        # the LIFO engine applies the product's node once per gradient path
+        # that reaches it (engine.rs:962-1047): three dW products, x needs none
+        assert T.Profile.read(T.Profile.GEMM)["launches"] == 3, on
         out[on] = (loss.value(), a.data(), c.data(), d.data(),
                    [p.grad_by_value().data() for p in (w, b, b2)])
         T.clear_gradients()
@@ -224,3 +237,30 @@ def test_product_with_several_consumers(fusion):
         assert_bits_equal(u, v, name)
     for i, (u, v) in enumerate(zip(g1, g0)):
         assert_bits_equal(u, v, f"grad {i}")
+
+
+def test_two_fused_chains_on_one_product_run_it_once(fusion):
+    # both consumers extend the deferred product before anything reads it:
+    # the second one runs the product (bare) and turns the first chain into
+    # its epilogue alone; a chain forked from a chain follows
+    T = fusion
+    out = {}
+    for on in (True, False):
+        T.set_fusion(on)
+        x = T.Tensor.from_slice(normal((512, 384), 5), [512, 384])
+        w = T.Tensor.from_slice((normal((384, 256), 6) / 20).astype(np.float32), [384, 256])
+        b1 = T.Tensor.from_slice(normal(256, 7), [256])
+        b2 = T.Tensor.from_slice(normal(256, 8), [256])
+        T.Profile.reset()
+        T.Profile.enable(True)
+        h = x.matmul(w)
+        z1 = h.add_tensor(b1)               # fork of the product
+        r1 = z1.relu()                      # fork of the fork
+        r2 = h.add_tensor(b2).relu()        # second consumer: the product runs here, once
+        z1_read = z1.data()                 # the first fork, as its epilogue alone
+        vals = (r1.data(), r2.data(), z1_read, h.data())
+        T.Profile.enable(False)
+        assert T.Profile.read(T.Profile.GEMM)["launches"] == 1, on
+        out[on] = vals
+    for name, u, v in zip(("relu(h+b1)", "relu(h+b2)", "h+b1", "h"), out[True], out[False]):
+        assert_bits_equal(u, v, name)

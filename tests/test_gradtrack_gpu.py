@@ -4,11 +4,12 @@ libts_hip.so) against the oracle's restatement of the reference
 
 Bars: elementwise ops, ReLU masks and Adam arithmetic bit-exact; matmul-derived
 gradients and reductions <= 1e-4 normwise relative error (max|d| / max|ref|);
-parameters after many Adam steps <= 1e-4 normwise L2 relative error (see
-_train_both), with ReLU masks teacher-forced where a pre-activation is within
-rounding of zero (see _relu_both).  Loss values are
-compared with the f64 value (the reference's own sequential fp32 sum drifts,
-see tests/test_oracle.py)."""
+parameters after 100 Adam steps <= 1e-4 relative per element (against the
+tensor's RMS for elements smaller than it), with a counted, bounded set of
+exceptions whose gradients had no fp32-determined sign (see _train_both), and
+ReLU masks teacher-forced where a pre-activation is within rounding of zero
+(see _relu_both).  Loss values are compared with the f64 value (the
+reference's own sequential fp32 sum drifts, see tests/test_oracle.py)."""
 from __future__ import annotations
 
 import numpy as np
@@ -145,7 +146,28 @@ def _mlp_both(xd, td, pd, xo, to, po, stats, readme=False):
     return h.sub_tensor(td).pow_scalar(2.0).mean(), ho.sub_tensor(to).pow_scalar(2.0).mean()
 
 
-def _train_both(TS, G, ws, x, t, steps, readme=False, lr=1e-3):
+EPS32 = 2.0 ** -23
+
+
+def _train_both(TS, G, ws, x, t, steps, readme=False, lr=1e-3, max_excluded=0.01):
+    """`steps` training steps on the device and in the oracle from the same
+    weights, then the north star's bar on every parameter element:
+
+        |p_dev - p_ref| <= 1e-4 * max(|p_ref|, rms(p_ref))
+
+    i.e. 1e-4 relative, against the tensor's RMS for elements smaller than it
+    (fp32 rounding of a weight that crossed zero leaves an absolute trace of
+    that scale; a relative measure at |p| -> 0 would be ill-posed).
+
+    Counted exceptions: an element whose Adam denominator -- the RMS of its
+    gradient history, sqrt(v_hat) up to the first steps' weighting -- was at
+    some step below the worst-case rounding bound of that step's gradient,
+    terms * 2^-23 * sum|terms| (the oracle reports sum|terms| for every
+    product and bias sum, GRAD_SCALE_HOOK).  Such a gradient has no
+    fp32-determined sign, so two correct implementations move the element by
+    up to ~lr in opposite directions.  The set is computed from the oracle
+    alone; its size must stay below `max_excluded` of the elements and each
+    excluded element within steps * lr of the oracle.  Returns the report."""
     pd = [TS.Tensor.from_slice(v, v.shape).with_requires_grad() for v in ws]
     po = [G.OTensor(v.copy()).with_requires_grad() for v in ws]
     opt, oopt = TS.Adam.with_learning_rate(lr), G.OAdam(lr)
@@ -154,31 +176,61 @@ def _train_both(TS, G, ws, x, t, steps, readme=False, lr=1e-3):
     xd, xo = TS.Tensor.from_slice(x, x.shape), G.OTensor(x)
     td = TS.Tensor.from_slice(t, t.shape) if t is not None else None
     to = G.OTensor(t) if t is not None else None
+    index = {p.id: k for k, p in enumerate(po)}
+    bound = {}
+
+    def hook(iid, scale, terms):
+        if iid in index:
+            bound[index[iid]] = terms * EPS32 * scale.reshape(-1)
+
+    sumsq = [np.zeros(v.size) for v in ws]
+    excluded = [np.zeros(v.size, bool) for v in ws]
     stats = {}
-    for step in range(steps):
-        loss, lo = _mlp_both(xd, td, pd, xo, to, po, stats, readme)
-        loss.backward()
-        lo.backward()
-        if step == 0:
-            for d, o in zip(pd, po):
-                assert max_rel(d.grad_by_value().data(), o.grad_by_value()) <= 1e-4
-        exact = lo.value()
-        assert abs(loss.value() - exact) <= 1e-4 * abs(exact), (step, loss.value(), exact)
-        opt.step(pd)
-        opt.zero_grad(pd)
-        oopt.step(po)
-        oopt.zero_grad(po)
-    # Parameters after several steps: normwise L2.  Adam's first steps move
-    # each element by about lr * sign(g); an element whose gradient cancels to
-    # the GEMM's rounding level has no fp32-determined sign, so a single
-    # element may differ by up to ~lr per step between two correct GEMMs.
-    worst = 0.0
-    for d, o in zip(pd, po):
-        got = d.data()
-        print(f"[train {steps} steps] max_rel {max_rel(got, o.data):.2e} rel_l2 {rel_l2(got, o.data):.2e}")
-        worst = max(worst, rel_l2(got, o.data))
-    print(f"[train] mask flips conditioned on: {stats.get('flips', 0)}")
-    return worst
+    G.GRAD_SCALE_HOOK = hook
+    try:
+        for step in range(steps):
+            bound.clear()
+            loss, lo = _mlp_both(xd, td, pd, xo, to, po, stats, readme)
+            loss.backward()
+            lo.backward()
+            if step == 0:
+                for d, o in zip(pd, po):
+                    assert max_rel(d.grad_by_value().data(), o.grad_by_value()) <= 1e-4
+            exact = lo.value()
+            assert abs(loss.value() - exact) <= 1e-4 * abs(exact), (step, loss.value(), exact)
+            for k, o in enumerate(po):
+                g = o.grad_by_value().reshape(-1).astype(np.float64)
+                sumsq[k] += g * g
+                assert k in bound, f"no rounding scale reported for parameter {k}"
+                excluded[k] |= np.sqrt(sumsq[k] / (step + 1)) < bound[k]
+            opt.step(pd)
+            opt.zero_grad(pd)
+            oopt.step(po)
+            oopt.zero_grad(po)
+            if step % 10 == 9:
+                print(f"[train] step {step + 1} of {steps}: loss {exact:.6g}", flush=True)
+    finally:
+        G.GRAD_SCALE_HOOK = None
+    report = {"steps": steps, "mask_flips_conditioned_on": stats.get("flips", 0), "params": []}
+    for k, (d, o) in enumerate(zip(pd, po)):
+        got = d.data().reshape(-1).astype(np.float64)
+        ref = o.data.reshape(-1).astype(np.float64)
+        diff = np.abs(got - ref)
+        tol = 1e-4 * np.maximum(np.abs(ref), np.sqrt(np.mean(ref * ref)))
+        ex = excluded[k]
+        fail = (diff > tol) & ~ex
+        entry = {"shape": list(o.data.shape), "max_err_over_tol": float(np.max(diff[~ex] / tol[~ex])) if (~ex).any() else 0.0,
+                 "max_rel_elementwise": float(np.max(diff / np.maximum(np.abs(ref), 1e-30))),
+                 "rel_l2": rel_l2(got, ref), "excluded": int(ex.sum()), "excluded_frac": float(ex.mean()),
+                 "excluded_over_tol": int(np.count_nonzero(ex & (diff > tol))),
+                 "excluded_max_abs": float(diff[ex].max()) if ex.any() else 0.0}
+        report["params"].append(entry)
+        print(f"[train {steps} steps] param {k} {entry}", flush=True)
+        assert not fail.any(), (k, int(fail.sum()), np.flatnonzero(fail)[:5], diff[fail][:5], tol[fail][:5])
+        assert ex.mean() <= max_excluded, (k, float(ex.mean()))
+        assert entry["excluded_max_abs"] <= steps * lr, (k, entry["excluded_max_abs"])
+    print(f"[train] mask flips conditioned on: {report['mask_flips_conditioned_on']}", flush=True)
+    return report
 
 
 # ---- config 1: README quick-start step ---------------------------------------------------------
@@ -187,7 +239,7 @@ def test_config1_readme_step(TS, G):
     # x[32,784] ~ N(0,1), W[784,128] ~ N(0,1), b = 0; y = relu(x.W + b); loss = sum(y); 100 Adam steps
     x = normal((32, 784), 0)
     ws = [normal((784, 128), 1), np.zeros(128, np.float32)]
-    assert _train_both(TS, G, ws, x, None, 100, readme=True) <= 1e-4
+    _train_both(TS, G, ws, x, None, 100, readme=True)
 
 
 # ---- config 2: elementwise autograd chain ------------------------------------------------------
@@ -281,20 +333,23 @@ def _mlp_weights(dims, seed, init):
     return ws, rng
 
 
-def test_config4_mlp(TS, G):
-    # batch 1024, 784 -> 1024 -> 10, Kaiming-uniform, MSE; 10 steps against the oracle
+@pytest.mark.timeout(300)
+def test_config4_mlp_100_steps(TS, G):
+    # batch 1024, 784 -> 1024 -> 10, Kaiming-uniform, MSE; 100 steps at full size
     ws, rng = _mlp_weights([784, 1024, 10], 0, "kaiming")
     x = rng.standard_normal((1024, 784)).astype(np.float32)
     t = rng.standard_normal((1024, 10)).astype(np.float32)
-    assert _train_both(TS, G, ws, x, t, 10) <= 1e-4
+    _train_both(TS, G, ws, x, t, 100)
 
 
-def test_config5_scaled_mlp(TS, G):
-    # config 5 structure (6 layers, N(0, 1/fan_in) weights, ReLU on layers 1-5, MSE) at width 256
-    ws, rng = _mlp_weights([256] * 7, 1, "normal")
-    x = rng.standard_normal((512, 256)).astype(np.float32)
-    t = rng.standard_normal((512, 256)).astype(np.float32)
-    assert _train_both(TS, G, ws, x, t, 5) <= 1e-4
+@pytest.mark.timeout(600)
+def test_config5_scaled_mlp_100_steps(TS, G):
+    # config 5's structure (6 layers, N(0, 1/fan_in) weights, ReLU on layers
+    # 1-5, MSE) at width 1024 and batch 2048, 100 steps
+    ws, rng = _mlp_weights([1024] * 7, 1, "normal")
+    x = rng.standard_normal((2048, 1024)).astype(np.float32)
+    t = rng.standard_normal((2048, 1024)).astype(np.float32)
+    _train_both(TS, G, ws, x, t, 100, max_excluded=0.02)
 
 
 def _mlp(lib_tensor, x, t, params, relu_last=False):
@@ -385,3 +440,163 @@ def test_sub_backward_skips_the_unconsumed_negation(TS):
     assert_bits_equal(gy1, gy2)
     assert_bits_equal(gt2, -gy2)
     np.testing.assert_allclose(gy1, 2.0 * (yv - tv) / n, rtol=1e-5, atol=1e-9)
+
+
+# ---- NoGradTrack, Tensor::grad, set_learning_rate ------------------------------------------------
+
+def test_no_grad_track_matches_the_oracle(TS, G):
+    # gradtrack/no_grad_track.rs:80-235: inside the guard the elementwise ops,
+    # relu, pow and matmul record nothing (ops/add.rs:127, :178, ...), while
+    # sum and mean still record whenever their input requires grad
+    # (reductions/sum.rs:131-138, mean.rs:97-106); guards nest and restore
+    rng = np.random.default_rng(41)
+    xv = rng.standard_normal((16, 12)).astype(np.float32)
+    wv = rng.standard_normal((12, 8)).astype(np.float32)
+    bv = rng.standard_normal(8).astype(np.float32)
+    cv = rng.uniform(0.5, 2.0, (16, 8)).astype(np.float32)
+
+    def run(L, make, guard):
+        x = make(xv).with_requires_grad()
+        w = make(wv).with_requires_grad()
+        b = make(bv).with_requires_grad()
+        c = make(cv).with_requires_grad()
+        with guard():
+            inner = [x.matmul(w), x.matmul(w).add_tensor(b), x.matmul(w).sub_tensor(c), x.matmul(w).mul_tensor(c),
+                     x.matmul(w).div_tensor(c), x.matmul(w).relu(), x.matmul(w).pow_scalar(2.0),
+                     x.mul_scalar(3.0)]
+            with guard():
+                nested = x.add_tensor(x)
+            after_nested = x.add_tensor(x)          # still inside the outer guard
+            s_in = x.sum()                          # records: the input requires grad
+            m_in = c.mean()
+        outside = x.matmul(w).add_tensor(b).relu()  # recording again
+        flags = [bool(t.requires_grad() if callable(t.requires_grad) else t.requires_grad)
+                 for t in inner + [nested, after_nested, s_in, m_in, outside]]
+        outside.sum().add_tensor(s_in).add_tensor(m_in).backward()
+        gx = x.grad_by_value()
+        gw = w.grad_by_value()
+        gc = c.grad_by_value()
+        return flags, gx, gw, gc
+
+    def dev(v):
+        return TS.Tensor.from_slice(v, list(v.shape))
+
+    def host(v):
+        return G.OTensor(v.copy())
+
+    f_d, gx_d, gw_d, gc_d = run(TS, dev, TS.NoGradTrack)
+    f_o, gx_o, gw_o, gc_o = run(G, host, G.NoGradTrack)
+    assert f_d == f_o == [False] * 10 + [True, True, True]
+    assert TS.is_grad_enabled()
+    assert max_rel(gx_d.data(), gx_o) <= 1e-5       # relu(x.w + b) path plus the recorded sum (ones)
+    assert max_rel(gw_d.data(), gw_o) <= 1e-5
+    assert_bits_equal(gc_d.data(), gc_o, "mean gradient recorded inside the guard")
+
+
+def test_tensor_grad_is_the_tensors_own_gradient(TS):
+    # Tensor::grad (tensor/core/utils.rs:491-506): Some(&self.grad) when the
+    # tensor holds its own gradient, None when only the graph's map does
+    x = TS.Tensor.from_slice(np.arange(6, dtype=np.float32), [2, 3]).with_requires_grad()
+    assert x.grad() is None
+    y = x.mul_scalar(2.0).sum()
+    y.backward()
+    assert x.grad() is None                          # a leaf's gradient lives in the map
+    assert x.grad_by_value().data().tolist() == [[2.0] * 3] * 2
+    TS.clear_gradients()
+    g = TS.Tensor.from_slice(np.full(6, 0.5, np.float32), [2, 3])
+    x.set_grad(g)
+    own = x.grad()
+    assert own is not None and own.shape == (2, 3)
+    assert_bits_equal(own.data(), np.full((2, 3), 0.5, np.float32))
+    again = x.grad()                                 # the stored gradient itself, not a copy
+    assert (again.id(), again.device_ptr()) == (own.id(), own.device_ptr())
+    assert x.grad_by_value().device_ptr() != own.device_ptr()
+    del own, again                                   # freeing the handles keeps the gradient
+    assert_bits_equal(x.grad().data(), np.full((2, 3), 0.5, np.float32))
+    # the backward root accumulates into its own grad (utils.rs:735)
+    r = TS.Tensor.from_slice(np.ones(4, np.float32), [4]).with_requires_grad()
+    r.backward()
+    assert r.grad().data().tolist() == [1.0] * 4
+    x.zero_grad()
+    assert x.grad() is None
+
+
+def test_set_learning_rate_changes_the_next_step(TS, G):
+    # Optimizer::set_learning_rate (adam/mod.rs:1077-1092) takes effect at the
+    # next step, bit-exactly as the oracle's Adam with the same schedule
+    n = 4099
+    p0, gv = normal(n, 51), normal(n, 52, 0.1)
+    p = TS.Tensor.from_slice(p0, [n]).with_requires_grad()
+    p.set_grad(TS.Tensor.from_slice(gv, [n]))
+    opt = TS.Adam.with_learning_rate(1e-3)
+    opt.add_parameter(p)
+    po = G.OTensor(p0.copy()).with_requires_grad()
+    po.grad = gv.copy()
+    oopt = G.OAdam(1e-3)
+    oopt.add_parameter(po)
+    for lr in (1e-3, 1e-3, 5e-2, 2.5e-4, 0.0, 1e-3):
+        opt.set_learning_rate(lr)
+        oopt.lr = lr
+        assert opt.learning_rate() == np.float32(lr)
+        before = p.data()
+        opt.step([p])
+        oopt.step([po])
+        assert_bits_equal(p.data(), po.data, f"after a step at lr {lr}")
+        if lr == 0.0:
+            assert_bits_equal(p.data(), before, "lr 0 leaves the parameter")
+
+
+# ---- positional gradients of single-operand records ----------------------------------------------
+
+@pytest.mark.parametrize("op", ["mul", "div", "sub"])
+@pytest.mark.parametrize("recorded", ["left", "right"])
+def test_only_the_consumed_gradient_is_computed(TS, G, op, recorded):
+    # With one operand requiring grad, input_ids lists only it and the
+    # backward's first gradient goes to it by position (ops/{mul,div,sub}.rs,
+    # engine.rs:1023-1035): the second formula has no consumer and no pass
+    # runs for it.  The gradient equals the oracle's positional result.
+    n = 4099
+    av, bv = normal(n, 61), uniform(n, 0.5, 2.0, 62)
+
+    def build(make, req):
+        a, b = make(av), make(bv)
+        (a if req == "left" else b).with_requires_grad()
+        y = getattr(a, f"{op}_tensor")(b)
+        return a, b, y.mul_tensor(y).sum()
+
+    a, b, loss = build(lambda v: TS.Tensor.from_slice(v, [n]), recorded)
+    TS.Profile.reset()
+    TS.Profile.enable(True)
+    loss.backward()
+    TS.Profile.enable(False)
+    ew = TS.Profile.read(TS.Profile.ELEMENTWISE)
+    got = (a if recorded == "left" else b).grad_by_value().data()
+    ao, bo, lo = build(lambda v: G.OTensor(v.copy()), recorded)
+    lo.backward()
+    want = (ao if recorded == "left" else bo).grad_by_value()
+    assert_bits_equal(got, want, f"{op} gradient to the {recorded} operand")
+    # the scalar seed (ones), the sum's fill, y*y's backward (both operands
+    # are y: one launch writing two gradients, then their accumulation) and
+    # the op's one-gradient pass
+    bytes_op = {"mul": 12.0, "div": 16.0, "sub": 0.0}[op] * n
+    launches_op = 0 if op == "sub" else 1
+    assert ew["launches"] == 4 + launches_op
+    assert abs(ew["work"] - (4.0 + 4.0 * n + 20.0 * n + 12.0 * n + bytes_op)) < 1.0
+
+
+@pytest.mark.parametrize("shape", ["same", "row"])
+def test_constant_minus_recorded_operand(TS, G, shape):
+    # c - y with constant c: input_ids = [y] and y receives the FIRST
+    # gradient, go (or go reduced to c's shape when c broadcasts), by
+    # position -- the reference's mapping (ops/sub.rs:149-156), not -go
+    B, N = 64, 33
+    yv = normal((B, N), 71)
+    cv = normal((B, N) if shape == "same" else (N,), 72)
+    y = TS.Tensor.from_slice(yv, [B, N]).with_requires_grad()
+    c = TS.Tensor.from_slice(cv, list(cv.shape))
+    c.sub_tensor(y).mul_scalar(3.0).sum().backward()
+    yo = G.OTensor(yv.copy()).with_requires_grad()
+    G.OTensor(cv.copy()).sub_tensor(yo).mul_scalar(3.0).sum().backward()
+    got, want = y.grad_by_value(), yo.grad_by_value()
+    assert got.shape == want.shape
+    assert_bits_equal(got.data(), want, "positional gradient of c - y")

@@ -153,7 +153,7 @@ def test_counters_follow_the_replays(T):
     opt.add_parameters(ps)
     with T.StepGraph.record() as g:                   # the very first step, recorded
         _step(ps, x, t, opt, readme)
-    assert opt.step_count() == 1                      # counted when recorded
+    assert opt.step_count() == 0                      # a recording runs nothing
     g.replay(1)
     assert opt.step_count() == 1
     g.replay(3)
@@ -161,6 +161,152 @@ def test_counters_follow_the_replays(T):
     # an eager step after the replays continues the count
     _step(ps, x, t, opt, readme)
     assert opt.step_count() == 5
+    for p in ps:
+        assert opt.parameter_step(p) == 5
+    g.free()
+
+
+def test_replays_count_from_the_optimizer_at_replay_time(T):
+    # record, 2 replays, 1 eager step, 2 replays: the bits of 5 eager steps
+    # (each replay takes its bias corrections from the count the optimizer
+    # has when it runs, eager steps in between included)
+    widths, batch, readme = CASES["deep"]
+    want, want_loss, _ = _eager(T, "deep", 6)
+    ps, x, t = _model(T, widths, batch, 11)
+    opt = T.Adam.with_learning_rate(1e-3)
+    opt.add_parameters(ps)
+    _step(ps, x, t, opt, readme)                      # step 1
+    with T.StepGraph.record() as g:
+        loss = _step(ps, x, t, opt, readme)
+    assert opt.step_count() == 1
+    g.replay(2)                                       # steps 2, 3
+    _step(ps, x, t, opt, readme)                      # step 4, eager
+    assert opt.step_count() == 4
+    g.replay(2)                                       # steps 5, 6
+    assert opt.step_count() == 6
+    for p in ps:
+        assert opt.parameter_step(p) == 6
+    for i, (a, b) in enumerate(zip([p.data() for p in ps], want)):
+        assert_bits_equal(a, b, f"param {i} after 6 steps")
+    assert loss.value() == want_loss
+    g.free()
+
+
+def test_two_optimizer_steps_in_one_recording(T):
+    # each replay runs both recorded steps, as steps 2k+1 and 2k+2
+    widths, batch, readme = CASES["deep"]
+    want, want_loss, _ = _eager(T, "deep", 6)
+    ps, x, t = _model(T, widths, batch, 11)
+    opt = T.Adam.with_learning_rate(1e-3)
+    opt.add_parameters(ps)
+    with T.StepGraph.record() as g:
+        _step(ps, x, t, opt, readme)
+        loss = _step(ps, x, t, opt, readme)
+    assert opt.step_count() == 0
+    g.replay(1)
+    assert opt.step_count() == 2
+    g.replay(2)
+    assert opt.step_count() == 6
+    for i, (a, b) in enumerate(zip([p.data() for p in ps], want)):
+        assert_bits_equal(a, b, f"param {i} after 6 steps")
+    assert loss.value() == want_loss
+    g.free()
+
+
+def test_two_graphs_on_one_optimizer(T):
+    # a graph for the full batch and one for a short last batch, interleaved
+    # with an eager step: the bits of the same steps run eagerly
+    widths, batch, readme = CASES["deep"]
+    rng = np.random.default_rng(21)
+    xs = rng.standard_normal((batch, widths[0])).astype(np.float32)
+    ts = rng.standard_normal((batch, widths[-1])).astype(np.float32)
+    short = batch // 4
+    order = ["full", "full", "short", "eager", "full", "short"]
+
+    def run(recorded):
+        ps, _, _ = _model(T, widths, batch, 11)
+        x = T.Tensor.from_slice(xs, list(xs.shape))
+        t = T.Tensor.from_slice(ts, list(ts.shape))
+        xsh = T.Tensor.from_slice(xs[:short].copy(), [short, widths[0]])
+        tsh = T.Tensor.from_slice(ts[:short].copy(), [short, widths[-1]])
+        opt = T.Adam.with_learning_rate(1e-3)
+        opt.add_parameters(ps)
+        graphs = {}
+        if recorded:
+            with T.StepGraph.record() as gf:
+                _step(ps, x, t, opt, readme)
+            with T.StepGraph.record() as gs:
+                _step(ps, xsh, tsh, opt, readme)
+            graphs = {"full": gf, "short": gs}
+        for kind in order:
+            if recorded and kind in graphs:
+                graphs[kind].replay(1)
+            elif kind == "short":
+                _step(ps, xsh, tsh, opt, readme)
+            else:
+                _step(ps, x, t, opt, readme)
+        out = [p.data() for p in ps]
+        assert opt.step_count() == len(order)
+        for g in graphs.values():
+            g.free()
+        return out
+
+    want = run(False)
+    got = run(True)
+    for i, (a, b) in enumerate(zip(got, want)):
+        assert_bits_equal(a, b, f"param {i}")
+
+
+def test_recording_with_gradients_held_is_refused(T):
+    # a recorded accumulation would add the same stale gradient on every replay
+    widths, batch, readme = CASES["deep"]
+    ps, x, t = _model(T, widths, batch, 3)
+    h = x
+    for i in range(len(ps) // 2):
+        h = h.matmul(ps[2 * i]).add_tensor(ps[2 * i + 1])
+    h.sub_tensor(t).pow_scalar(2.0).mean().backward()
+    with pytest.raises(T.TsError, match="no gradients are held"):
+        T.StepGraph.record().__enter__()
+    assert not T.recording()
+    T.clear_gradients()
+    opt = T.Adam.with_learning_rate(1e-3)
+    opt.add_parameters(ps)
+    with T.StepGraph.record() as g:
+        _step(ps, x, t, opt, readme)
+    g.replay(1)
+    assert opt.step_count() == 1
+    g.free()
+
+
+def test_an_optimizer_step_that_fails_while_recording_takes_its_counts_back(T):
+    # the step counts each parameter as it goes; an unlinked parameter late in
+    # the list raises, the recording aborts, and every count is as before
+    widths, batch, readme = CASES["deep"]
+    ps, x, t = _model(T, widths, batch, 5)
+    stray = T.Tensor.from_slice(np.ones(4, np.float32), [4]).with_requires_grad()
+    opt = T.Adam.with_learning_rate(1e-3)
+    opt.add_parameters(ps)
+    _step(ps, x, t, opt, readme)
+    with pytest.raises(T.TsError, match="linked to optimizer"):
+        with T.StepGraph.record():
+            h = x
+            for i in range(len(ps) // 2):
+                h = h.matmul(ps[2 * i]).add_tensor(ps[2 * i + 1])
+            h.sub_tensor(t).pow_scalar(2.0).mean().backward()
+            opt.step(ps + [stray])
+    assert not T.recording()
+    assert opt.step_count() == 1
+    for p in ps:
+        assert opt.parameter_step(p) == 1
+    T.clear_gradients()
+    # a recorded step whose parameters hold no gradient still counts once per replay
+    with T.StepGraph.record() as g:
+        opt.step(ps)
+    assert opt.step_count() == 1
+    g.replay(2)
+    assert opt.step_count() == 3
+    for p in ps:
+        assert opt.parameter_step(p) == 1
     g.free()
 
 
@@ -268,7 +414,7 @@ def test_a_graph_freed_unreplayed_leaves_the_counters(T):
     _step(ps2, x2, t2, opt2, readme)
     with T.StepGraph.record() as g:
         _step(ps, x, t, opt, readme)
-    assert opt.step_count() == 2                      # counted at recording
+    assert opt.step_count() == 1                      # a recording runs nothing
     g.free()
     assert opt.step_count() == 1
     for _ in range(2):

@@ -169,6 +169,32 @@ def test_gemm_layouts_against_torch_and_brute_force(oracle, ta, tb):
     assert max_rel(got32, want.numpy()) < 1e-5
 
 
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_gemm_f64_blas_path_matches_the_loop(oracle, ta, tb):
+    # Large products take numpy's float64 matmul; both paths sum exact f32
+    # products in f64, so they agree to f64 rounding and, rounded to f32, in
+    # all but a last-place tie or two.
+    M, N, K = 96, 80, 777
+    a = normal((K, M) if ta else (M, K), 40)
+    b = normal((N, K) if tb else (K, N), 41)
+    loop = oracle.gemm_f64(a, b, ta=ta, tb=tb, path="loop")
+    blas = oracle.gemm_f64(a, b, ta=ta, tb=tb, path="blas")
+    assert blas.dtype == np.float64 and blas.shape == (M, N)
+    scale = np.abs(a).max() * np.abs(b).max() * K
+    assert np.max(np.abs(loop - blas)) <= 1e-13 * scale
+    differ = np.count_nonzero(loop.astype(np.float32) != blas.astype(np.float32))
+    assert differ <= 2, differ
+    # a transposed operand is read through the view, not copied wrongly:
+    # brute force on a few elements
+    Am = a.T if ta else a
+    Bm = b.T if tb else b
+    for i, j in ((0, 0), (M - 1, N - 1), (17, 61)):
+        s = sum(float(Am[i, k]) * float(Bm[k, j]) for k in range(K))
+        assert abs(blas[i, j] - s) <= 1e-12 * scale
+    # the automatic choice switches at the documented size
+    assert oracle.GEMM_F64_BLAS_MIN_MACS == 1 << 22
+
+
 def test_gemm_known_answer(oracle):
     ka = golden("known_answers.json")["matmul_2x2"]   # matmul/mod.rs:1145-1195
     a = np.array(ka["a"], np.float32).reshape(2, 2)

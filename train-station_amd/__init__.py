@@ -17,13 +17,12 @@ from ._ffi import TsError, gradtrack as native_gradtrack, hip as native_hip, hip
 from .tensor import (Adam, NoGradTrack, Profile, StepGraph, Tensor, adam_config_from_binary,
                      adam_config_from_json, adam_config_to_binary, adam_config_to_json,
                      clear_gradients, empty_cache, fusion_enabled, is_grad_enabled, pool_stats, recording,
-                     set_fusion, stream, synchronize)
+                     set_fusion, set_grad_enabled, stream, synchronize, with_no_grad)
 
 __all__ = [
     "Adam", "NoGradTrack", "Profile", "StepGraph", "Tensor", "TsError", "adam_config_from_binary",
     "adam_config_from_json", "adam_config_to_binary", "adam_config_to_json", "clear_gradients",
     "empty_cache", "fusion_enabled",
     "hip_check", "is_grad_enabled", "native_gradtrack", "native_hip", "pool_stats", "recording", "set_fusion",
-    "stream",
-    "synchronize",
+    "set_grad_enabled", "stream", "synchronize", "with_no_grad",
 ]

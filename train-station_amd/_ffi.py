@@ -185,6 +185,7 @@ GRADTRACK_SIGNATURES = {
     "ts_tensor_sum": (TP, [TP]),
     "ts_tensor_mean": (TP, [TP]),
     "ts_tensor_backward": (_c.c_int, [TP, TP]),
+    "ts_tensor_grad": (TP, [TP]),
     "ts_tensor_grad_by_value": (TP, [TP]),
     "ts_tensor_set_grad": (_c.c_int, [TP, TP]),
     "ts_tensor_zero_grad": (_c.c_int, [TP]),
@@ -194,6 +195,7 @@ GRADTRACK_SIGNATURES = {
     "ts_no_grad_push": (None, []),
     "ts_no_grad_pop": (None, []),
     "ts_is_grad_enabled": (_c.c_int, []),
+    "ts_set_grad_enabled": (None, [_c.c_int]),
     "ts_adam_new": (TP, []),
     "ts_adam_with_config": (TP, [_c.c_float, _c.c_float, _c.c_float, _c.c_float, _c.c_float, _c.c_int]),
     "ts_adam_with_learning_rate": (TP, [_c.c_float]),

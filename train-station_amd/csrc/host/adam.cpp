@@ -47,15 +47,12 @@ void Adam::add_parameters(const std::vector<const Tensor *> &ps) {
 }
 
 void Adam::settle() const {
-    for (const auto &r : replayed_) {
-        if (!r->pending) continue;
-        step_count_ += static_cast<uint64_t>(r->pending);  // wraps correctly for -1
-        for (size_t id : r->params) {
-            auto it = states_.find(id);
-            if (it != states_.end()) it->second.step += static_cast<uint64_t>(r->pending);
-        }
-        r->pending = 0;
+    if (ledger_->param_delta.empty()) return;
+    for (const auto &d : ledger_->param_delta) {
+        auto it = states_.find(d.first);
+        if (it != states_.end()) it->second.step += static_cast<uint64_t>(d.second);  // wraps correctly for < 0
     }
+    ledger_->param_delta.clear();
 }
 
 void Adam::step(const std::vector<Tensor *> &params) {
@@ -70,17 +67,16 @@ void Adam::step(const std::vector<Tensor *> &params) {
             if (it != states_.end() && p->grad_ref() && it->second.n && !it->second.v_hat_max)
                 throw Error("record an AMSGrad step only after the optimizer's first step");
         }
-    step_count_ += 1;  // adam/mod.rs:1037
+    // registered before anything is counted, so the end or abort of the
+    // recording takes back exactly what this call counted
     std::optional<StepRecorder::AdamSlot> slot;
-    std::vector<size_t> stepped;
+    if (recording) slot = rec.adam_step(config_.beta1, config_.beta2, ledger_);
+    ledger_->step_count += 1;  // adam/mod.rs:1037
+    const uint64_t step_count = ledger_->step_count;
     std::vector<ts_hip_adam_param> batch;
     double bytes = 0.0;
     auto flush = [&]() {
         if (batch.empty()) return;
-        if (recording && !slot) {
-            slot = rec.adam_step(config_.beta1, config_.beta2, step_count_, {});
-            replayed_.push_back(slot->steps);  // linked at once: an abort takes the count back
-        }
         launch(KernelClass::Adam, bytes, "ts_hip_adam_step_multi", [&] {
             void *st = Runtime::get().stream();
             if (slot)
@@ -88,7 +84,7 @@ void Adam::step(const std::vector<Tensor *> &params) {
                                                     config_.beta1, config_.beta2, config_.eps,
                                                     config_.weight_decay, slot->table, slot->slot, st);
             return ts_hip_adam_step_multi(batch.data(), batch.size(), config_.learning_rate, config_.beta1,
-                                          config_.beta2, config_.eps, config_.weight_decay, step_count_, st);
+                                          config_.beta2, config_.eps, config_.weight_decay, step_count, st);
         });
         batch.clear();
         bytes = 0.0;
@@ -108,12 +104,12 @@ void Adam::step(const std::vector<Tensor *> &params) {
         if (g->size() != p->size() || s.n != p->size())
             throw Error("Momentum and gradient size mismatch");
         s.step += 1;
+        if (slot) rec.adam_param(slot->use, p->id());
         int first = 0;
         if (config_.amsgrad && !s.v_hat_max && s.n) {
             s.v_hat_max = std::make_shared<Allocation>(s.n);
             first = 1;
         }
-        stepped.push_back(p->id());
         if (!s.n) continue;
         // p is updated in place: deferred products reading it run first
         if (p->allocation()) p->allocation()->before_write();
@@ -130,7 +126,6 @@ void Adam::step(const std::vector<Tensor *> &params) {
         if (batch.size() == TS_HIP_ADAM_MAX_PARAMS) flush();
     }
     flush();
-    if (slot) slot->steps->params = std::move(stepped);
 }
 
 void Adam::zero_grad(const std::vector<Tensor *> &params) {

@@ -191,6 +191,14 @@ int ts_tensor_backward(ts_tensor *t, const ts_tensor *grad_output) {
     });
 }
 
+ts_tensor *ts_tensor_grad(const ts_tensor *t) {
+    return guard_ptr([&]() -> ts_tensor * {
+        const ts::Tensor *g = T(t).grad_direct();
+        if (!g) return nullptr;
+        return wrap(g->view());
+    });
+}
+
 ts_tensor *ts_tensor_grad_by_value(const ts_tensor *t) {
     return guard_ptr([&]() -> ts_tensor * {
         auto g = T(t).grad_by_value();
@@ -229,6 +237,7 @@ void ts_clear_gradients(void) { ts::clear_gradients(); }
 void ts_no_grad_push(void) { ts::push_grad_enabled(false); }
 void ts_no_grad_pop(void) { ts::pop_grad_enabled(); }
 int ts_is_grad_enabled(void) { return ts::is_grad_enabled() ? 1 : 0; }
+void ts_set_grad_enabled(int enabled) { ts::set_grad_enabled(enabled != 0); }
 
 ts_adam *ts_adam_new(void) {
     return guard_ptr([&] { return new ts_adam{ts::Adam()}; });

@@ -341,7 +341,7 @@ Fields Adam::to_fields(bool binary) const {
     Fields f;
     f.emplace_back("config", Value::object(config_fields(config_)));
     f.emplace_back("states", Value::object(std::move(states)));
-    f.emplace_back("step_count", Value::usize(step_count_));
+    f.emplace_back("step_count", Value::usize(ledger_->step_count));
     f.emplace_back("insertion_order", Value::array(std::move(order)));
     return f;
 }
@@ -386,7 +386,7 @@ Adam Adam::from_fields(const ser::Fields &f) {
         s.v = v.allocation();
         a.states_[id] = std::move(s);
     }
-    a.step_count_ = ser::as_usize(need(f, "step_count"), "step_count");
+    a.ledger_->step_count = ser::as_usize(need(f, "step_count"), "step_count");
     const auto order = ser::array_to_usize(need(f, "insertion_order"), "insertion_order");
     a.insertion_order_.assign(order.begin(), order.end());
     return a;
@@ -422,6 +422,7 @@ Adam Adam::load_json(const std::string &path) {
 
 // adam/mod.rs:396-454
 void Adam::relink_parameters(const std::vector<const Tensor *> &params) {
+    settle();  // replayed steps land on the states under their old ids first
     for (size_t i = 0; i < params.size(); ++i)
         if (!params[i]->requires_grad())
             throw Error("Parameter at index " + std::to_string(i) + " must require gradients");

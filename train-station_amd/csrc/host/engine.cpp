@@ -52,8 +52,12 @@ void accumulate_gradient(size_t id, Tensor g) {
 bool is_grad_enabled() { return grad_stack().back(); }
 void push_grad_enabled(bool on) { grad_stack().push_back(on); }
 void pop_grad_enabled() {
-    if (grad_stack().size() > 1) grad_stack().pop_back();
+    std::vector<bool> &s = grad_stack();
+    if (s.size() > 1) s.pop_back();
+    else s.assign(1, true);  // an unbalanced pop restores the default state
 }
+void set_grad_enabled(bool on) { grad_stack().back() = on; }
+bool gradients_pending() { return !graph().gradients.empty(); }
 
 void clear_gradients() {
     graph().operations.clear();

@@ -10,8 +10,8 @@
 // parks, instead of reusing, any of them released meanwhile.  Adam's bias
 // corrections depend on the step count, so a recorded Adam::step reads them
 // from a device table indexed by a replay counter that the graph's last node
-// advances; the host fills the table before each run of replays with the
-// values an eager step would use.
+// advances; before each run of replays the host fills the table with the
+// values eager steps would use from the optimizer's count at that moment.
 #include <algorithm>
 
 #include "ts_hip.h"
@@ -27,6 +27,9 @@ StepRecorder &StepRecorder::get() {
 void StepRecorder::begin() {
     if (graph_) throw Error("a step recording is already open");
     if (Profiler::get().enabled()) throw Error("disable the profiler before recording a step");
+    if (gradients_pending())
+        throw Error("a step can be recorded only while no gradients are held: call zero_grad (or "
+                    "clear_gradients) first, and end the recorded step with zero_grad");
     Runtime &rt = Runtime::get();
     rt.sync();  // work queued before the recording runs eagerly, first
     auto g = std::make_unique<StepGraph>();
@@ -37,24 +40,42 @@ void StepRecorder::begin() {
     graph_ = std::move(g);
 }
 
-StepRecorder::AdamSlot StepRecorder::adam_step(float beta1, float beta2, uint64_t step,
-                                               std::vector<size_t> params) {
+StepRecorder::AdamSlot StepRecorder::adam_step(float beta1, float beta2, const std::shared_ptr<AdamLedger> &ledger) {
     if (!graph_) throw Error("no step recording is open");
     if (!graph_->slot) graph_->slot = std::make_shared<Allocation>(1);  // pinned: acquired while recording
     StepGraph::AdamUse u;
     u.table = std::make_shared<Allocation>(2 * kReplayChunk);
     u.beta1 = beta1;
     u.beta2 = beta2;
-    u.first_step = step;
-    u.steps = std::make_shared<ReplaySteps>();
-    u.steps->params = std::move(params);
-    graph_->adams.push_back(u);
-    return {u.table->get(), reinterpret_cast<const unsigned *>(graph_->slot->get()), u.steps};
+    u.ledger = ledger;
+    for (const StepGraph::AdamUse &o : graph_->adams)
+        if (o.ledger == ledger) ++u.order;
+    graph_->adams.push_back(std::move(u));
+    const StepGraph::AdamUse &b = graph_->adams.back();
+    return {b.table->get(), reinterpret_cast<const unsigned *>(graph_->slot->get()), graph_->adams.size() - 1};
+}
+
+void StepRecorder::adam_param(size_t use, size_t param_id) {
+    if (!graph_ || use >= graph_->adams.size()) throw Error("no recorded optimizer step to add a parameter to");
+    graph_->adams[use].params.push_back(param_id);
+}
+
+void StepRecorder::take_back(StepGraph &g) {
+    for (StepGraph::AdamUse &u : g.adams) {
+        u.ledger->step_count -= 1;
+        for (size_t id : u.params) u.ledger->param_delta[id] -= 1;
+    }
+    for (StepGraph::AdamUse &u : g.adams) {
+        u.per_replay = 0;
+        for (const StepGraph::AdamUse &o : g.adams)
+            if (o.ledger == u.ledger) ++u.per_replay;
+    }
 }
 
 StepGraph *StepRecorder::end() {
     if (!graph_) throw Error("no step recording is open");
     std::unique_ptr<StepGraph> g = std::move(graph_);
+    take_back(*g);
     void *stream = Runtime::get().stream();
     // the last node moves the replay counter on to the next table entry
     const int adv = g->slot ? ts_hip_slot_advance(reinterpret_cast<unsigned *>(g->slot->get()), stream)
@@ -73,17 +94,14 @@ StepGraph *StepRecorder::end() {
 void StepRecorder::abort() {
     if (!graph_) return;
     std::unique_ptr<StepGraph> g = std::move(graph_);
+    take_back(*g);
     void *exec = nullptr;
     (void)ts_hip_stream_end_capture(Runtime::get().stream(), &exec);
     DevicePool::get().pin_end();
-    g->exec = exec;  // destroyed with g, which takes back the recorded step's count
+    g->exec = exec;
 }
 
 StepGraph::~StepGraph() {
-    // the optimizer counted the recorded step when it was recorded; a graph
-    // that never ran (aborted, failed or freed unreplayed) takes that back
-    if (!executed)
-        for (AdamUse &u : adams) u.steps->pending -= 1;
     if (exec) {
         // replays may still be running
         (void)ts_hip_stream_synchronize(Runtime::get().stream());
@@ -103,19 +121,31 @@ void StepGraph::replay(size_t times) {
             rt.sync();  // earlier replays have read their tables
             cf.resize(2 * chunk);
             for (AdamUse &u : adams) {
-                check(ts_hip_adam_bias_corrections(u.beta1, u.beta2, u.first_step + executed, chunk, cf.data()),
-                      "ts_hip_adam_bias_corrections");
+                // replay i runs this optimizer's recorded steps as its steps
+                // count + i*per_replay + 1 .. + per_replay, in recorded order,
+                // from the count it has now (eager steps and other graphs
+                // included)
+                const uint64_t base = u.ledger->step_count + u.order + 1;
+                if (u.per_replay == 1) {
+                    check(ts_hip_adam_bias_corrections(u.beta1, u.beta2, base, chunk, cf.data()),
+                          "ts_hip_adam_bias_corrections");
+                } else {
+                    for (size_t i = 0; i < chunk; ++i)
+                        check(ts_hip_adam_bias_corrections(u.beta1, u.beta2, base + i * u.per_replay, 1,
+                                                           cf.data() + 2 * i),
+                              "ts_hip_adam_bias_corrections");
+                }
                 check(ts_hip_memcpy(u.table->get(), cf.data(), 2 * chunk, 0), "ts_hip_memcpy");
             }
             const unsigned zero = 0;
             check(ts_hip_memcpy(slot->get(), reinterpret_cast<const float *>(&zero), 1, 0), "ts_hip_memcpy");
         }
         for (size_t i = 0; i < chunk; ++i) check(ts_hip_graph_launch(exec, rt.stream()), "ts_hip_graph_launch");
-        // the optimizer counted the recorded step when it was recorded; every
-        // further replay is one more step
-        const uint64_t extra_before = executed ? executed - 1 : 0;
         executed += chunk;
-        for (AdamUse &u : adams) u.steps->pending += static_cast<int64_t>((executed - 1) - extra_before);
+        for (AdamUse &u : adams) {
+            u.ledger->step_count += chunk;
+            for (size_t id : u.params) u.ledger->param_delta[id] += static_cast<int64_t>(chunk);
+        }
         done += chunk;
     }
 }

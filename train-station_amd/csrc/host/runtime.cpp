@@ -82,12 +82,17 @@ float *DevicePool::acquire(size_t n_floats, size_t *rounded) {
     }
     float *p = nullptr;
     int st = ts_hip_malloc(&p, r);
-    if (st != TS_HIP_OK) {  // return cached blocks to the device and retry once
+    // Return cached blocks to the device and retry once.  That needs a wait
+    // for queued work, which a step being recorded cannot do: there the
+    // allocation failure itself is reported.
+    if (st != TS_HIP_OK && !pinning_.load(std::memory_order_relaxed)) {
         Runtime::get().sync();
         empty_cache();
         st = ts_hip_malloc(&p, r);
     }
-    check(st, "ts_hip_malloc");
+    if (st != TS_HIP_OK)
+        throw Error("ts_hip_malloc of " + std::to_string(r * sizeof(float)) + " bytes failed (" +
+                    ts_hip_error_string(st) + ")");
     std::lock_guard<std::mutex> lock(g_pool_mutex);
     live_ += r * sizeof(float);
     if (sink_) pin(p);

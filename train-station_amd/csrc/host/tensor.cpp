@@ -219,26 +219,116 @@ bool fusion_enabled() { return g_fusion; }
 void set_pending(const std::shared_ptr<Allocation> &out, std::shared_ptr<PendingGemm> p) {
     add_reader(p->A, out);
     add_reader(p->B, out);
+    add_reader(p->src, out);
     add_reader(p->bias, out);
     add_reader(p->mask, out);
     out->pending = std::move(p);
 }
+
+std::shared_ptr<PendingGemm> new_product(const std::shared_ptr<Allocation> &out) {
+    auto p = std::make_shared<PendingGemm>();
+    p->group = std::make_shared<ProductGroup>();
+    p->group->bare = out;
+    p->group->members.push_back(out);
+    return p;
+}
+
+std::shared_ptr<PendingGemm> fork_pending(const std::shared_ptr<Allocation> &src, const std::shared_ptr<Allocation> &out) {
+    if (!src || !src->pending) return nullptr;
+    auto p = std::make_shared<PendingGemm>(*src->pending);
+    if (p->group) p->group->members.push_back(out);
+    return p;
+}
+
+namespace {
+
+// The group's other members whose records still run its product.
+std::vector<std::shared_ptr<Allocation>> pending_members(const Allocation &a, const PendingGemm &p) {
+    std::vector<std::shared_ptr<Allocation>> out;
+    if (!p.group) return out;
+    auto &ms = p.group->members;
+    size_t live = 0;
+    for (auto &w : ms) {
+        auto m = w.lock();
+        if (!m || !m->pending || m->pending->src || m->pending->group != p.group) continue;
+        ms[live++] = w;
+        if (m.get() != &a) out.push_back(std::move(m));
+    }
+    ms.resize(live);
+    return out;
+}
+
+void launch_product(const PendingGemm &p, float *C, bool with_epilogue) {
+    // inputs first (they may be deferred themselves), outside this launch's window
+    const float *A = p.A->get(), *B = p.B->get();
+    const float *bias = with_epilogue && p.bias ? p.bias->get() : nullptr;
+    const float *mask = with_epilogue && p.mask ? p.mask->get() : nullptr;
+    const bool relu = with_epilogue && p.relu;
+    DevicePool::get().note_use(C);  // a step being recorded writes it on every replay
+    launch(KernelClass::Gemm, 2.0 * p.M * p.N * p.K, "ts_hip_gemm_fused", [&] {
+        return gemm2d(p.ta, p.tb, p.M, p.N, p.K, A, p.lda, B, p.ldb, bias, relu, mask, C, p.N);
+    });
+}
+
+}  // namespace
 
 void materialize(Allocation &a) {
     // The record stays until the launch has succeeded: after a failed launch
     // the next read of the buffer tries again (and reports the error again)
     // instead of returning contents that were never written.
     const std::shared_ptr<PendingGemm> p = a.pending;
-    // inputs first (they may be deferred themselves), outside this launch's window
-    const float *A = p->A->get(), *B = p->B->get();
-    const float *bias = p->bias ? p->bias->get() : nullptr;
-    const float *mask = p->mask ? p->mask->get() : nullptr;
     float *C = a.raw();
-    DevicePool::get().note_use(C);  // a step being recorded writes it on every replay
-    launch(KernelClass::Gemm, 2.0 * p->M * p->N * p->K, "ts_hip_gemm_fused", [&] {
-        return gemm2d(p->ta, p->tb, p->M, p->N, p->K, A, p->lda, B, p->ldb, bias, p->relu, mask, C, p->N);
-    });
-    a.pending.reset();
+    if (p->src) {  // epilogue only: the separate kernels, in the fused epilogue's order
+        const float *x = p->src->get();
+        const float *bias = p->bias ? p->bias->get() : nullptr;
+        const float *mask = p->mask ? p->mask->get() : nullptr;
+        DevicePool::get().note_use(C);
+        const size_t n = p->M * p->N;
+        if (bias) {
+            launch(KernelClass::Elementwise, 8.0 * n + 4.0 * p->N, "ts_hip_bias_add",
+                   [&] { return ts_hip_bias_add(x, bias, C, p->M, p->N, 0, S()); });
+            x = C;
+        }
+        if (p->relu) {
+            launch(KernelClass::Elementwise, 8.0 * n, "ts_hip_relu", [&] { return ts_hip_relu(x, C, n, S()); });
+            x = C;
+        }
+        if (mask || x != C)
+            launch(KernelClass::Elementwise, 12.0 * n, "ts_hip_relu_backward", [&] {
+                return mask ? ts_hip_relu_backward(mask, x, C, n, S()) : ts_hip_copy(x, C, n, S());
+            });
+        a.pending.reset();
+        return;
+    }
+    const std::vector<std::shared_ptr<Allocation>> others = pending_members(a, *p);
+    if (others.empty()) {  // the only consumer: the product with its epilogue, in one launch
+        launch_product(*p, C, true);
+        a.pending.reset();
+        return;
+    }
+    // Several consumers: the product once, bare, into its own buffer (or a
+    // temporary when that was dropped); then every member keeps only its
+    // epilogue, reading it.
+    std::shared_ptr<Allocation> prod = p->group->bare.lock();
+    if (!prod || !prod->pending || !prod->pending->bare() || prod->pending->group != p->group)
+        prod = std::make_shared<Allocation>(p->M * p->N);
+    launch_product(*p, prod->raw(), false);
+    if (prod->pending) prod->pending.reset();
+    std::vector<std::shared_ptr<Allocation>> all = others;
+    all.push_back(a.shared_from_this());
+    for (auto &m : all) {
+        if (m == prod || !m->pending || m->pending->src) continue;
+        const std::shared_ptr<PendingGemm> old = m->pending;
+        auto e = std::make_shared<PendingGemm>();
+        e->M = old->M;
+        e->N = old->N;
+        e->src = prod;
+        e->bias = old->bias;
+        e->relu = old->relu;
+        e->mask = old->mask;
+        set_pending(m, e);
+    }
+    if (a.pending) materialize(a);
 }
 
 size_t next_tensor_id() {
@@ -327,6 +417,16 @@ Tensor Tensor::alias() const {
     return t;
 }
 
+Tensor Tensor::view() const {
+    Tensor t;
+    t.alloc_ = alloc_;
+    t.dims_ = dims_;
+    t.size_ = size_;
+    t.id_ = id_;
+    t.requires_grad_ = requires_grad_;
+    return t;
+}
+
 Tensor Tensor::from_saved(const SavedTensor &s) {
     Tensor t;
     t.alloc_ = s.alloc;
@@ -391,12 +491,17 @@ Tensor Tensor::binary(const Tensor &o, GradFn::Kind kind) const {
     Tensor out;
     const bool fuse_self = kind == GradFn::Kind::Add && fuse_bias(*this, o);
     const bool fuse_other = !fuse_self && kind == GradFn::Kind::Add && fuse_bias(o, *this);
+    std::shared_ptr<PendingGemm> fused;
     if (fuse_self || fuse_other) {
         const Tensor &mat = fuse_self ? *this : o, &vec = fuse_self ? o : *this;
         out = new_uninit(mat.dims_);
-        auto p = std::make_shared<PendingGemm>(*mat.alloc_->pending);
-        p->bias = vec.alloc_;
-        set_pending(out.alloc_, std::move(p));
+        fused = fork_pending(mat.alloc_, out.alloc_);
+        if (fused) {
+            fused->bias = vec.alloc_;
+            set_pending(out.alloc_, std::move(fused));
+        } else {  // the product had a consumer already and has now run: the kernel reads it
+            out = row_bcast(mat.dev(), vec.dev(), mat.dims_[0], mat.dims_[1], 0, fuse_other);
+        }
     } else if (same) {
         out = same_shape(dev(), o.dev(), dims_, op);
     } else if (is_row_broadcast(dims_, o.dims_)) {
@@ -469,10 +574,12 @@ Tensor Tensor::div_scalar(float s) const { return scalar_op(s, GradFn::Kind::Div
 
 Tensor Tensor::relu() const {
     Tensor out = new_uninit(dims_);
-    if (fusion_enabled() && alloc_ && alloc_->pending && !alloc_->pending->relu && !alloc_->pending->mask) {
-        auto p = std::make_shared<PendingGemm>(*alloc_->pending);  // relu joins the deferred product
-        p->relu = true;
-        set_pending(out.alloc_, std::move(p));
+    std::shared_ptr<PendingGemm> fused;
+    if (fusion_enabled() && alloc_ && alloc_->pending && !alloc_->pending->relu && !alloc_->pending->mask)
+        fused = fork_pending(alloc_, out.alloc_);  // relu joins the deferred product
+    if (fused) {
+        fused->relu = true;
+        set_pending(out.alloc_, std::move(fused));
     } else {
         launch(KernelClass::Elementwise, 8.0 * size_, "ts_hip_relu",
                [&] { return ts_hip_relu(dev(), out.dev_mut(), size_, S()); });
@@ -597,7 +704,7 @@ Tensor Tensor::matmul(const Tensor &o) const {
             throw Error("Inner dimensions must match: " + std::to_string(k) + " vs " + std::to_string(o.dims_[0]));
         out = new_uninit({m, n});
         if (fusion_enabled() && out.size_ && k) {  // deferred: a following bias add / relu joins it
-            auto p = std::make_shared<PendingGemm>();
+            auto p = new_product(out.alloc_);
             p->M = m; p->N = n; p->K = k; p->lda = k; p->ldb = n;
             p->A = alloc_;
             p->B = o.alloc_;
@@ -843,32 +950,46 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
             break;
         }
         case K::Mul: {  // grad_fn/ops/mul.rs:4-49
+            // As for Sub: gradients go to the recorded inputs by position, so
+            // the second one has a consumer only when both inputs are recorded.
             const SavedTensor &a = saved[0], &b = saved[1];
+            const bool second = req_left && req_right;
             if (!has_shapes) {
-                Tensor ga = Tensor::new_uninit(go.dims()), gb = Tensor::new_uninit(go.dims());
-                launch(KernelClass::Elementwise, 20.0 * n, "ts_hip_mul_backward", [&] {
-                    return ts_hip_mul_backward(go.dev(), a.ptr(), b.ptr(), ga.dev_mut(),
-                                               gb.dev_mut(), n, S());
-                });
-                r.emplace_back(std::move(ga));
-                r.emplace_back(std::move(gb));
+                Tensor ga = Tensor::new_uninit(go.dims());
+                if (second) {
+                    Tensor gb = Tensor::new_uninit(go.dims());
+                    launch(KernelClass::Elementwise, 20.0 * n, "ts_hip_mul_backward", [&] {
+                        return ts_hip_mul_backward(go.dev(), a.ptr(), b.ptr(), ga.dev_mut(), gb.dev_mut(), n, S());
+                    });
+                    r.emplace_back(std::move(ga));
+                    r.emplace_back(std::move(gb));
+                } else {
+                    launch(KernelClass::Elementwise, 12.0 * n, "ts_hip_mul(grad)",
+                           [&] { return ts_hip_mul(go.dev(), b.ptr(), ga.dev_mut(), n, S()); });
+                    r.emplace_back(std::move(ga));
+                }
             } else {
                 r.emplace_back(reduce_to(with_bcast(go, b, 2), shape_a));
-                r.emplace_back(reduce_to(with_bcast(go, a, 2), shape_b));
+                if (second) r.emplace_back(reduce_to(with_bcast(go, a, 2), shape_b));
             }
             break;
         }
         case K::Div: {  // grad_fn/ops/div.rs:4-49
             const SavedTensor &a = saved[0], &b = saved[1];
             if (!has_shapes) {
-                Tensor ga = Tensor::new_uninit(go.dims()), gb = Tensor::new_uninit(go.dims());
-                launch(KernelClass::Elementwise, 20.0 * n, "ts_hip_div_backward", [&] {
+                // the second gradient only when both inputs are recorded (see
+                // Mul); the kernel still checks both divisors (b, then b*b)
+                // for the reference's zero-divisor panic
+                const bool second = req_left && req_right;
+                Tensor ga = Tensor::new_uninit(go.dims());
+                Tensor gb = second ? Tensor::new_uninit(go.dims()) : Tensor();
+                launch(KernelClass::Elementwise, (second ? 20.0 : 16.0) * n, "ts_hip_div_backward", [&] {
                     return ts_hip_div_backward(go.dev(), a.ptr(), b.ptr(), ga.dev_mut(),
-                                               gb.dev_mut(), n, tail8(n), tail32(n),
+                                               second ? gb.dev_mut() : nullptr, n, tail8(n), tail32(n),
                                                Runtime::get().zero_index(), S());
                 });
                 r.emplace_back(std::move(ga));
-                r.emplace_back(std::move(gb));
+                if (second) r.emplace_back(std::move(gb));
             } else {
                 Tensor ga_full = with_bcast(go, b, 3);                  // go / b
                 Tensor neg_grad = with_bcast(go, a, 2);                 // go * a
@@ -897,11 +1018,12 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
         case K::Relu: {  // grad_fn/ops/relu.rs:4-17 (saved[0] is the relu output)
             Tensor g = Tensor::new_uninit(go.dims());
             const auto &ga = go.allocation();
-            if (fusion_enabled() && ga && ga->pending && ga->pending->bare() && saved[0].alloc) {
-                // the incoming gradient is a deferred dX product: mask it in its store
-                auto p = std::make_shared<PendingGemm>(*ga->pending);
-                p->mask = saved[0].alloc;
-                set_pending(g.allocation(), std::move(p));
+            std::shared_ptr<PendingGemm> fused;
+            if (fusion_enabled() && ga && ga->pending && ga->pending->bare() && saved[0].alloc)
+                fused = fork_pending(ga, g.allocation());  // the incoming gradient is a deferred dX product
+            if (fused) {  // mask it in its store
+                fused->mask = saved[0].alloc;
+                set_pending(g.allocation(), std::move(fused));
             } else {
                 launch(KernelClass::Elementwise, 12.0 * n, "ts_hip_relu_backward", [&] {
                     return ts_hip_relu_backward(saved[0].ptr(), go.dev(), g.dev_mut(), n, S());
@@ -939,7 +1061,7 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
                     Tensor t = Tensor::new_uninit({M, Kd});
                     if (fusion_enabled() && t.size() && N && go.allocation() && b.alloc) {
                         // deferred: relu's backward, usually next, joins it as a mask
-                        auto p = std::make_shared<PendingGemm>();
+                        auto p = new_product(t.allocation());
                         p->ta = 0; p->tb = 1;
                         p->M = M; p->N = Kd; p->K = N; p->lda = N; p->ldb = N;
                         p->A = go.allocation();

@@ -104,17 +104,34 @@ struct Allocation;
 // dX product extends the producer instead of launching a pass of its own, so
 // the chain runs as one kernel and intermediates nobody reads are never
 // written.  Results are the bits of the unfused ops.
+//
+// Each product runs once.  A consumer extends a record by forking a copy of
+// it; the product's own buffer and every fork belong to one ProductGroup.
+// When a member is first needed and it is the group's only member still
+// pending, the product runs fused into it (the usual chain: the bare product
+// and the bias add's result are dropped, the relu output is read).  With
+// other members pending, the product runs once, bare, into its own buffer (or
+// a temporary when that was dropped), and every pending member becomes an
+// epilogue-only record reading it (`src`): its bias / relu / mask run as the
+// separate elementwise kernels, whose bits are the fused epilogue's.
+struct ProductGroup {
+    std::weak_ptr<Allocation> bare;                  // the product's own buffer
+    std::vector<std::weak_ptr<Allocation>> members;  // it and every fork
+};
+
 struct PendingGemm {
     int ta = 0, tb = 0;
     size_t M = 0, N = 0, K = 0, lda = 0, ldb = 0;
     std::shared_ptr<Allocation> A, B, bias, mask;
+    std::shared_ptr<Allocation> src;  // epilogue-only: the produced [M, N] buffer the epilogue reads
     bool relu = false;
-    bool bare() const { return !bias && !mask && !relu; }
+    std::shared_ptr<ProductGroup> group;
+    bool bare() const { return !src && !bias && !mask && !relu; }
 };
 
 // Device variant of tensor/core/allocation.rs:43-187: owns one pooled device
 // buffer; shared (Arc-like) by tensors, saved graph operands and gradients.
-struct Allocation {
+struct Allocation : std::enable_shared_from_this<Allocation> {
     explicit Allocation(size_t n_floats);
     ~Allocation();
     Allocation(const Allocation &) = delete;
@@ -138,6 +155,12 @@ struct Allocation {
 void materialize(Allocation &a);
 // Makes `out` pending on p and records it as a reader of p's inputs.
 void set_pending(const std::shared_ptr<Allocation> &out, std::shared_ptr<PendingGemm> p);
+// A new deferred product C = op(A) . op(B) for `out`, the first member of
+// its group.
+std::shared_ptr<PendingGemm> new_product(const std::shared_ptr<Allocation> &out);
+// A copy of src's pending record for `out` to extend with an epilogue, joined
+// to src's product group; nullptr when src has no pending record.
+std::shared_ptr<PendingGemm> fork_pending(const std::shared_ptr<Allocation> &src, const std::shared_ptr<Allocation> &out);
 // Fusion switch (on by default): off, every op launches its own kernels.
 void set_fusion(bool on);
 bool fusion_enabled();
@@ -280,6 +303,9 @@ class Tensor {
     Tensor clone() const;
     // Handle on the same buffer with a new id (graph-internal sharing).
     Tensor alias() const;
+    // Handle on the same buffer with the same id: this tensor itself, as a
+    // reference to it (&Tensor) would see it; carries no gradient.
+    Tensor view() const;
 
     size_t id() const { return id_; }
     const std::vector<size_t> &dims() const { return dims_; }
@@ -296,6 +322,9 @@ class Tensor {
     void set_requires_grad(bool r);
     void backward(const Tensor *grad_output = nullptr);
     std::optional<Tensor> grad_by_value() const;
+    // Tensor::grad (utils.rs:491-506): the gradient stored on the tensor
+    // itself, or nullptr -- also when only the graph's map holds one, as there.
+    const Tensor *grad_direct() const { return grad_.get(); }
     // The gradient Adam reads: self.grad, else the graph's map entry; no copy.
     const Tensor *grad_ref() const;
     void set_grad(Tensor g);
@@ -353,10 +382,12 @@ size_t next_tensor_id();
 
 // ---- gradtrack -------------------------------------------------------------------
 
-bool is_grad_enabled();
-void push_grad_enabled(bool on);   // NoGradTrack::new / with_no_grad (no_grad_track.rs)
-void pop_grad_enabled();
-void clear_gradients();            // engine.rs:812-816
+bool is_grad_enabled();             // no_grad_track.rs:155-160
+void push_grad_enabled(bool on);    // NoGradTrack::new / with_no_grad (no_grad_track.rs:96-104, :229-235)
+void pop_grad_enabled();            // NoGradTrack's Drop (no_grad_track.rs:117-127)
+void set_grad_enabled(bool on);     // no_grad_track.rs:188-199: replaces the innermost state
+void clear_gradients();             // engine.rs:812-816
+bool gradients_pending();           // the gradient map holds at least one gradient
 void register_operation(size_t output_id, std::vector<size_t> input_ids, GradFn fn);
 const Tensor *accumulated_gradient(size_t id);
 void engine_backward(Tensor &root, const Tensor *grad_output);
@@ -381,11 +412,23 @@ struct AdamConfig adam_config_from_json(const std::string &json);
 // Rust's Debug form of a shape, "[2, 3]"
 std::string dims_str(const std::vector<size_t> &d);
 
-struct ReplaySteps;
+// Step counters of one optimizer: its global step count and, per parameter,
+// the steps that replays of recorded steps ran (or a recording took back)
+// that the parameter's state has not absorbed yet.  Shared by the optimizer
+// and every step graph that recorded one of its steps, so a replay reads the
+// count the optimizer has at that moment, whatever ran in between.
+struct AdamLedger {
+    uint64_t step_count = 0;                          // adam/mod.rs:1037, replays included
+    std::unordered_map<size_t, int64_t> param_delta;  // parameter id -> steps to add to its State
+};
 
 class Adam {
   public:
     Adam() = default;
+    Adam(Adam &&) = default;
+    Adam &operator=(Adam &&) = default;
+    Adam(const Adam &) = delete;
+    Adam &operator=(const Adam &) = delete;
     static Adam with_config(AdamConfig c);
     static Adam with_learning_rate(float lr);
     void add_parameter(const Tensor &p);
@@ -397,10 +440,7 @@ class Adam {
     float learning_rate() const { return config_.learning_rate; }
     void set_learning_rate(float lr) { config_.learning_rate = lr; }
     const AdamConfig &config() const { return config_; }
-    uint64_t step_count() const {
-        settle();
-        return step_count_;
-    }
+    uint64_t step_count() const { return ledger_->step_count; }
     size_t parameter_count() const { return states_.size(); }
     // m / v of a linked parameter (device), for checkpoint and tests.
     const float *state_m(size_t param_id) const;
@@ -430,35 +470,26 @@ class Adam {
         size_t n = 0;
         uint64_t step = 0;
     };
-    // Adds the steps that replays of recorded steps ran to the counters.
+    // Adds the ledger's per-parameter deltas to the states.
     void settle() const;
     ser::Fields to_fields(bool binary) const;
     static Adam from_fields(const ser::Fields &f);
     AdamConfig config_;
     mutable std::unordered_map<size_t, State> states_;
     std::vector<size_t> insertion_order_;
-    mutable uint64_t step_count_ = 0;
-    std::vector<std::shared_ptr<ReplaySteps>> replayed_;  // one per recorded step call
+    std::shared_ptr<AdamLedger> ledger_ = std::make_shared<AdamLedger>();
 };
 
 // ---- step recording ----------------------------------------------------------------
 
-// Steps run by replays of one recorded Adam::step beyond the recorded one
-// (which the optimizer counted when it was recorded; an aborted recording
-// takes that count back with -1); the optimizer adds them to its counters
-// when it next reads them.
-struct ReplaySteps {
-    int64_t pending = 0;
-    std::vector<size_t> params;  // the parameters that step updated
-};
-
 // One recorded step: a HIP graph of the library stream's work between
 // StepRecorder::begin and end, the blocks it pinned, and per recorded
 // Adam::step a table of bias corrections indexed by a device replay counter.
+// A recording itself runs nothing, so it leaves every step counter as it was;
+// each replay then counts as many steps as it ran.
 struct StepGraph {
     ~StepGraph();
-    // Runs the recorded work `times` times in stream order; the first replay
-    // ever runs the recorded step itself.
+    // Runs the recorded work `times` times in stream order.
     void replay(size_t times);
     void *exec = nullptr;
     std::vector<float *> pins;
@@ -466,8 +497,10 @@ struct StepGraph {
     struct AdamUse {
         std::shared_ptr<Allocation> table;  // kReplayChunk [cf1, cf2] pairs
         float beta1 = 0, beta2 = 0;
-        uint64_t first_step = 0;
-        std::shared_ptr<ReplaySteps> steps;
+        std::shared_ptr<AdamLedger> ledger;
+        size_t order = 0;       // recorded steps of the same optimizer before this one
+        size_t per_replay = 0;  // recorded steps of that optimizer in this graph
+        std::vector<size_t> params;  // the parameters this step updated
     };
     std::vector<AdamUse> adams;
     uint64_t executed = 0;  // replays run so far
@@ -478,19 +511,25 @@ class StepRecorder {
     static constexpr size_t kReplayChunk = 1024;  // replays per bias-correction table fill
     static StepRecorder &get();
     bool open() const { return graph_ != nullptr; }
+    // Refuses to start while the gradient map holds gradients: a recorded
+    // accumulation would add that fixed buffer again on every replay.
     void begin();
     StepGraph *end();
     void abort();
-    // Called by Adam::step while recording: the table and counter its launch
-    // reads, and the link through which replays credit the optimizer.
+    // Called by Adam::step while recording, before it counts the step: the
+    // table and counter its launch reads; `use` names the step for
+    // adam_param, which records each parameter as soon as it is stepped.
     struct AdamSlot {
         const float *table;
         const unsigned *slot;
-        std::shared_ptr<ReplaySteps> steps;
+        size_t use;
     };
-    AdamSlot adam_step(float beta1, float beta2, uint64_t step, std::vector<size_t> params);
+    AdamSlot adam_step(float beta1, float beta2, const std::shared_ptr<AdamLedger> &ledger);
+    void adam_param(size_t use, size_t param_id);
 
   private:
+    // The counts the recorded Adam steps added while recording, taken back.
+    static void take_back(StepGraph &g);
     std::unique_ptr<StepGraph> graph_;
 };
 

@@ -199,6 +199,18 @@ class Tensor:
     def backward(self, grad_output: Optional["Tensor"] = None) -> None:
         _ok(_G.ts_tensor_backward(self._h, grad_output._h if grad_output is not None else None))
 
+    def grad(self) -> Optional["Tensor"]:
+        """Tensor::grad (utils.rs:491-506): the gradient stored on the tensor
+        itself, sharing its buffer; None when there is none, also when only
+        the graph's gradient map holds one (use grad_by_value for that)."""
+        h = _G.ts_tensor_grad(self._h)
+        if not h:
+            err = last_error()
+            if err:
+                raise TsError(err)
+            return None
+        return Tensor(h)
+
     def grad_by_value(self) -> Optional["Tensor"]:
         h = _G.ts_tensor_grad_by_value(self._h)
         if not h:
@@ -433,6 +445,17 @@ def is_grad_enabled() -> bool:
     return bool(_G.ts_is_grad_enabled())
 
 
+def set_grad_enabled(enabled: bool) -> None:
+    """no_grad_track.rs:188-199: replaces the innermost gradient state."""
+    _G.ts_set_grad_enabled(int(bool(enabled)))
+
+
+def with_no_grad(f):
+    """no_grad_track.rs:229-235: runs f() with gradient tracking disabled."""
+    with NoGradTrack():
+        return f()
+
+
 def clear_gradients() -> None:
     _G.ts_clear_gradients()
 
@@ -451,10 +474,12 @@ def fusion_enabled() -> bool:
 class StepGraph:
     """One recorded training step (include/ts_gradtrack.h, ts_step_graph_*):
     the work issued inside ``with StepGraph.record() as g:`` is recorded as a
-    HIP graph, not run; ``g.replay(n)`` runs it n times (the first replay runs
-    the recorded step itself) with Adam's step counts advancing as in an eager
-    loop.  Inside the recording nothing may read the device or upload host
-    data; results are read after a replay."""
+    HIP graph, not run (and not counted); ``g.replay(n)`` runs it n times,
+    each replay's Adam steps taking the step counts that follow the
+    optimizer's count at that moment, as eager steps would.  The recording
+    starts with no gradients held and should end with ``zero_grad``.  Inside
+    the recording nothing may read the device or upload host data; results are
+    read after a replay."""
 
     def __init__(self) -> None:
         self._h = None
