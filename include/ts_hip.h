@@ -15,7 +15,11 @@
  * caller can panic with a message from ts_hip_error_string().
  *
  * All tensor pointers are device pointers to contiguous row-major f32 data.
- * Launchers are asynchronous on `stream` and never allocate.
+ * Launchers are asynchronous on `stream`.  They allocate nothing, with one
+ * exception: ts_hip_gemm (and ts_hip_matmul, which calls it) takes a split-K
+ * temporary from the stream-ordered allocator for few output tiles with a
+ * long K.  ts_hip_gemm_fused (caller's workspace) and ts_hip_gemm_noalloc
+ * (fixed device array) compute the same products without allocating.
  * No torch or HIP types appear in these signatures.
  */
 #ifndef TS_HIP_H
@@ -32,6 +36,7 @@ extern "C" {
 #define TS_HIP_EINVAL 100001      /* bad argument (shape, NULL pointer, kind) */
 #define TS_HIP_ENODEVICE 100002   /* no gfx950 device visible */
 #define TS_HIP_EWORKSPACE 100003  /* workspace smaller than *_workspace_floats() */
+#define TS_HIP_ESCRATCH 100004    /* problem needs more scratch than ts_hip_gemm_noalloc holds */
 
 /* ---- runtime -------------------------------------------------------------- */
 
@@ -277,6 +282,18 @@ int ts_hip_matmul(const float *a, const float *b, float *c, size_t m, size_t n, 
  * unavailable it runs unsplit. */
 int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
                 size_t lda, const float *B, size_t ldb, float *C, size_t ldc, void *stream);
+
+/* ts_hip_gemm without any allocation.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * kernels and results (bit for bit) as ts_hip_gemm; a split product's
+ * temporary comes from a fixed device array of 2^21 floats (8 MiB) that each
+ * device holds for the life of the process, which every split this device
+ * can choose fits (a product needing more returns TS_HIP_ESCRATCH).  The
+ * array is shared by all calls on a device: calls that overlap on one device
+ * (on several streams) race and must be serialised by the caller. */
+int ts_hip_gemm_noalloc(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
+                        size_t lda, const float *B, size_t ldb, float *C, size_t ldc, void *stream);
 
 /* Floats of workspace a split product needs (the temporary ts_hip_gemm takes
  * from the stream-ordered allocator for few output tiles with a long K):

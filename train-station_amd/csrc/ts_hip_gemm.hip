@@ -41,6 +41,9 @@
 // current two run, across tile boundaries too.  Its k order per MFMA differs
 // (k of step s, lane half h = 4*(s/2) + 2h + s%2) so that a k-contiguous
 // operand gives two steps' values in one 8-byte LDS read.
+#include <mutex>
+#include <vector>
+
 #include "ts_hip_internal.h"
 
 namespace tship {
@@ -749,6 +752,57 @@ extern "C" int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t 
                            size_t lda, const float *B, size_t ldb, float *C, size_t ldc,
                            void *stream) {
     return gemm_plain(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, nullptr, nullptr, 0, nullptr, 0, stream);
+}
+
+// ---- allocation-free form --------------------------------------------------
+//
+// ts_hip_gemm_noalloc takes the split-K temporary from this fixed device
+// array instead of the stream-ordered allocator.  A split runs only while
+// 4 * (64x64 tiles) < CUs with slices * tiles <= 2 * CUs, so it never needs
+// more than 2 * CUs * 64 * 64 floats: 2^21 (8 MiB) on the 256 CUs of an
+// MI355X.  Every device the library runs on holds its own copy for the life
+// of the process.  Calls that overlap on one device (several streams) share
+// it and race; the split slices are fully written before they are read, so
+// nothing needs clearing between calls.
+static constexpr size_t kScratchFloats = size_t(1) << 21;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+namespace tship {
+static std::mutex g_scratch_mutex;
+static std::vector<float *> g_scratch;  // device ordinal -> this device's copy of `scratch`
+
+// The device address of the current device's copy of `scratch`, looked up
+// once per device with that device current (host code must never pass the
+// symbol itself: on the host it names a host-side stand-in).
+static int scratch_address(float **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return static_cast<int>(e);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (static_cast<size_t>(dev) >= g_scratch.size()) g_scratch.resize(dev + 1, nullptr);
+    if (!g_scratch[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return e != hipSuccess ? static_cast<int>(e) : TS_HIP_EINVAL;
+        g_scratch[dev] = static_cast<float *>(p);
+    }
+    *out = g_scratch[dev];
+    return TS_HIP_OK;
+}
+}  // namespace tship
+
+extern "C" int ts_hip_gemm_noalloc(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
+                                   size_t lda, const float *B, size_t ldb, float *C, size_t ldc, void *stream) {
+    const size_t need = ts_hip_gemm_workspace_floats(M, N, K);
+    if (need > kScratchFloats) return TS_HIP_ESCRATCH;
+    float *ws = nullptr;
+    if (need) {
+        const int st = scratch_address(&ws);
+        if (st != TS_HIP_OK) return st;
+    }
+    // with a workspace given, a split product takes its temporary from it;
+    // unsplit products and empty contractions use none
+    return gemm_plain(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, nullptr, nullptr, 0, ws, need, stream);
 }
 
 extern "C" size_t ts_hip_gemm_workspace_floats(size_t M, size_t N, size_t K) {

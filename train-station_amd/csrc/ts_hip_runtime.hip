@@ -255,6 +255,7 @@ const char *ts_hip_error_string(int status) {
         case TS_HIP_EINVAL: return "invalid argument (shape, pointer, alignment or copy kind)";
         case TS_HIP_ENODEVICE: return "no gfx950 device visible";
         case TS_HIP_EWORKSPACE: return "workspace smaller than the size the kernel needs";
+        case TS_HIP_ESCRATCH: return "product needs more scratch than the allocation-free entry point holds";
         default: return hipGetErrorString(static_cast<hipError_t>(status));
     }
 }
