@@ -5,8 +5,10 @@ with bias, ReLU after layers 1-5, MSE loss, fp32, Adam(lr 1e-3).
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c5|c4|c1|c2|c3]
                     [--no-cpu-baseline] [--cpu-sample-rows R] [--graph]
 
-Prints one JSON line.  `value` is steps/s measured over exactly K steps with
-all inputs resident in HBM.  `roofline` is the roofline of the dominant kernel
+Prints one JSON line.  `value` is steps/s of config 5 measured over exactly K
+steps with all inputs resident in HBM; without --config the same line carries
+every other BASELINE config under "configs" (each with its own steps, roofline
+and CPU baseline), measured in the same run.  `roofline` is the roofline of the dominant kernel
 class: for the MLP configs (c1, c4, c5) the fp32-MFMA roofline of the GEMMs
 (algorithmic FLOPs of every GEMM launch in the timed region over their summed
 device-event durations, on the library stream); for the elementwise chain
@@ -42,6 +44,8 @@ CONFIGS = {
 CHAIN_N = 1 << 26        # config 2: elementwise autograd chain length
 ADAM_P = 1 << 28         # config 3: Adam alone, parameter count
 CHAIN_BYTES_PER_ELEM = 148   # forward 60 + backward 88 B per element (algorithmic, one step)
+# the configs measured after the headline in a default run: (name, timed steps, warm-up steps)
+OTHER_CONFIGS = (("c1", 200, 10), ("c4", 100, 5), ("c2", 20, 3), ("c3", 100, 3))
 ADAM_BYTES_PER_PARAM = 28    # read p, g, m, v; write p, m, v
 
 
@@ -233,10 +237,10 @@ def cpu_baseline_adam(sample: int):
             "sample": f"one Adam step on {sample} of {ADAM_P} parameters, scaled ({dt:.2f} s)", "host": host_info()}
 
 
-def bandwidth_main(args, TS, hip, hip_check) -> int:
+def run_bandwidth(TS, cfg: str, steps: int, warmup: int, cpu: bool) -> dict:
     """Configs 2 and 3: the HBM-bound paths, each step timed like the MLP step."""
     rng = np.random.default_rng(0)
-    if args.config == "c2":
+    if cfg == "c2":
         n = CHAIN_N
         log(f"config c2: chain over {n} elements; uploading inputs")
         a = TS.Tensor.from_slice(rng.standard_normal(n, dtype=np.float32), [n]).with_requires_grad()
@@ -271,38 +275,38 @@ def bandwidth_main(args, TS, hip, hip_check) -> int:
                     "m=v=0 initially, lr=1e-3, betas (0.9, 0.999), eps 1e-8")
         data = "synthetic (device XorShiftRng randn: p seed 1, g = 0.1 * randn seed 2)"
 
-    for i in range(args.warmup):
+    for i in range(warmup):
         step()
     TS.synchronize()
     TS.Profile.reset()
     TS.Profile.enable(True)
     TS.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     TS.synchronize()
     t1 = time.perf_counter()
     TS.Profile.enable(False)
-    wall_ms = (t1 - t0) * 1000.0 / args.steps
+    wall_ms = (t1 - t0) * 1000.0 / steps
     names = {"elementwise": TS.Profile.ELEMENTWISE, "reduction": TS.Profile.REDUCTION, "adam": TS.Profile.ADAM}
     prof = {k: TS.Profile.read(names[k]) for k in classes}
     kern_ms = sum(v["ms"] for v in prof.values())
     kern_work = sum(v["work"] for v in prof.values())
     achieved = kern_work / (kern_ms * 1e-3) / 1e9 if kern_ms > 0 else 0.0
-    kernels = {k: {"ms_per_step": round(v["ms"] / args.steps, 3), "launches_per_step": v["launches"] // args.steps,
+    kernels = {k: {"ms_per_step": round(v["ms"] / steps, 3), "launches_per_step": v["launches"] // steps,
                    "GB/s": round(v["work"] / (v["ms"] * 1e-3) / 1e9, 1) if v["ms"] > 0 else 0.0}
                for k, v in prof.items()}
     # HBM bytes per launch from the committed counters: config 3 only (one Adam
     # launch per step; config 2 runs several kernels of different byte counts)
-    traffic, traffic_src = pmc_traffic(args.config) if args.config == "c3" else (None, None)
+    traffic, traffic_src = pmc_traffic(cfg) if cfg == "c3" else (None, None)
     result = {
         "metric": {"c2": "fwd+bwd steps/sec of the elementwise chain (1 GPU); % HBM GB/s roofline",
-                   "c3": "Adam::step steps/sec (1 GPU); % HBM GB/s roofline"}[args.config],
+                   "c3": "Adam::step steps/sec (1 GPU); % HBM GB/s roofline"}[cfg],
         "value": round(1000.0 / wall_ms, 4),
         "unit": "steps/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(wall_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -316,14 +320,144 @@ def bandwidth_main(args, TS, hip, hip_check) -> int:
                      "step_bytes_per_wall_time_GBs": round(work / (wall_ms * 1e-3) / 1e9, 1)},
         "kernels": kernels,
     }
-    if not args.no_cpu_baseline:
+    if cpu:
         log("timing the CPU baseline (oracle port, one core, bounded sample)")
-        result["cpu_baseline"] = (cpu_baseline_chain(CHAIN_N) if args.config == "c2"
+        result["cpu_baseline"] = (cpu_baseline_chain(CHAIN_N) if cfg == "c2"
                                   else cpu_baseline_adam(1 << 26))
     else:
         result["cpu_baseline"] = None
-    print(json.dumps(result), flush=True)
-    return 0
+    return result
+
+
+def run_mlp(TS, hip, hip_check, cfg: str, steps: int, warmup: int, cpu: bool, cpu_rows: int, graph: bool) -> dict:
+    """An MLP config (c1, c4, c5): W untimed warm-up steps, then exactly K
+    steps between two device synchronisations, the GEMMs timed with events."""
+    batch, widths, init = CONFIGS[cfg]
+    readme = init == "readme"
+    rng = np.random.default_rng(0)
+    log(f"config {cfg}: batch {batch}, widths {widths}; uploading inputs")
+    ps = make_params(TS, widths, init, rng)
+    x = TS.Tensor.from_slice(rng.standard_normal((batch, widths[0]), dtype=np.float32), [batch, widths[0]])
+    t = TS.Tensor.from_slice(rng.standard_normal((batch, widths[-1]), dtype=np.float32), [batch, widths[-1]])
+    opt = TS.Adam.with_learning_rate(1e-3)
+    opt.add_parameters(ps)
+
+    def step():
+        loss = forward_loss(x, t, ps, readme)
+        loss.backward()
+        opt.step(ps)
+        opt.zero_grad(ps)
+        return loss
+
+    for i in range(warmup):
+        loss = step()
+        log(f"warmup step {i}: loss {loss.value():.6f}")
+    TS.synchronize()
+
+    stream = TS.stream()
+    ev0, ev1 = ctypes.c_void_p(), ctypes.c_void_p()
+    hip_check(hip.ts_hip_event_create(ctypes.byref(ev0)))
+    hip_check(hip.ts_hip_event_create(ctypes.byref(ev1)))
+    # The timed region times the roofline's class (the GEMMs) with device
+    # events around each launch; the other kernels run untimed, so the
+    # events perturb the step as little as possible.
+    TS.Profile.reset()
+    TS.Profile.enable(True, classes=[TS.Profile.GEMM])
+    TS.synchronize()
+    t0 = time.perf_counter()
+    hip_check(hip.ts_hip_event_record(ev0, stream))
+    for _ in range(steps):
+        loss = step()
+    hip_check(hip.ts_hip_event_record(ev1, stream))
+    TS.synchronize()
+    t1 = time.perf_counter()
+    TS.Profile.enable(False)
+    ev_ms = ctypes.c_float()
+    hip_check(hip.ts_hip_event_elapsed_ms(ctypes.byref(ev_ms), ev0, ev1))
+    final_loss = loss.value()
+    g = TS.Profile.read(TS.Profile.GEMM)
+
+    # Per-class breakdown: a separate pass after the timed one, every class timed.
+    breakdown_steps = max(1, min(steps, 5))
+    TS.Profile.reset()
+    TS.Profile.enable(True)
+    for _ in range(breakdown_steps):
+        step()
+    TS.synchronize()
+    TS.Profile.enable(False)
+    classes = {"gemm": TS.Profile.GEMM, "elementwise": TS.Profile.ELEMENTWISE,
+               "reduction": TS.Profile.REDUCTION, "adam": TS.Profile.ADAM}
+    prof = {k: TS.Profile.read(v) for k, v in classes.items()}
+
+    wall_ms = (t1 - t0) * 1000.0 / steps
+    gemm_tflops = g["work"] / (g["ms"] * 1e-3) / 1e12 if g["ms"] > 0 else 0.0
+    kernels = {"pass": f"a separate pass of {breakdown_steps} steps after the timed region, every class timed"}
+    for k, s in prof.items():
+        if s["launches"] == 0:
+            continue
+        rate = s["work"] / (s["ms"] * 1e-3) if s["ms"] > 0 else 0.0
+        per_step = {"ms_per_step": round(s["ms"] / breakdown_steps, 3),
+                    "launches_per_step": s["launches"] // breakdown_steps}
+        if k == "gemm":
+            kernels[k] = {**per_step, "TFLOP/s": round(rate / 1e12, 2),
+                          "frac_mfma_peak": round(rate / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)}
+        else:
+            kernels[k] = {**per_step, "GB/s": round(rate / 1e9, 1), "frac_hbm_peak": round(rate / 1e9 / PEAK_HBM_GBS, 4)}
+    per_launch_flops = g["work"] / g["launches"] if g["launches"] else 0.0
+    traffic, traffic_src = pmc_traffic(cfg)
+
+    result = {
+        "metric": "fwd+bwd+Adam steps/sec (1 GPU); % fp32 MFMA peak and % HBM GB/s roofline",
+        "value": round(1000.0 / wall_ms, 4),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(wall_ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": {"c5": "synthetic (numpy default_rng(0); N(0,1/fan_in) weights, N(0,1) inputs and targets)",
+                 "c4": "synthetic (numpy default_rng(0); Kaiming-uniform weights, N(0,1) inputs and targets)",
+                 "c1": "synthetic (numpy default_rng(0); N(0,1) weights and inputs, zero bias)"}[cfg],
+        "config": {"workload": {"c5": "BASELINE config 5: deep wide MLP, batch 8192, 6 x Linear(4096,4096)+bias, "
+                                      "ReLU on layers 1-5, MSE, fwd+bwd+Adam(lr 1e-3)",
+                                "c4": "BASELINE config 4: MLP batch 1024, 784->1024->10, MSE, fwd+bwd+Adam",
+                                "c1": "BASELINE config 1: README step x[32,784] W[784,128], relu, sum, Adam"}[cfg],
+                   "batch": batch, "widths": widths, "gemm_flop_per_step": step_flops(batch, widths, readme)},
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
+                     "kernel": ("gemm_f32_lds_dma (all 3 layouts, every launch of the timed region)" if cfg == "c5"
+                                else "every GEMM launch of the timed region (gemm_f32_mfma tiles, split-K where "
+                                     "the output has few tiles)"),
+                     "flop_per_launch": per_launch_flops,
+                     "avg_launch_ms": round(g["ms"] / g["launches"], 4) if g["launches"] else None},
+        "kernels": kernels,
+        "event_ms_per_step": round(ev_ms.value / steps, 3),
+        "final_loss": final_loss,
+    }
+    if graph:
+        # the same loop, one step recorded and then replayed: every replay
+        # runs the whole step; untimed replays warm the graph up
+        with TS.StepGraph.record() as g:
+            gloss = step()
+        g.replay(max(1, warmup))
+        TS.synchronize()
+        t0 = time.perf_counter()
+        g.replay(steps)
+        TS.synchronize()
+        g_ms = (time.perf_counter() - t0) * 1000.0 / steps
+        result["graph"] = {"value": round(1000.0 / g_ms, 4), "unit": "steps/s", "ms_per_step": round(g_ms, 4),
+                           "final_loss": gloss.value(), "note": "the same step replayed from a HIP graph"}
+        g.free()
+    if cpu:
+        log("timing the CPU baseline (oracle port, one core, bounded sample)")
+        result["cpu_baseline"] = cpu_baseline(cfg, cpu_rows)
+    else:
+        result["cpu_baseline"] = None
+    return result
 
 
 def main() -> int:
@@ -331,7 +465,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c5", choices=sorted(list(CONFIGS) + ["c2", "c3"]))
+    ap.add_argument("--config", default=None, choices=sorted(list(CONFIGS) + ["c2", "c3"]),
+                    help="measure this config alone (default: config 5 as the headline, then every other "
+                         "config under \"configs\")")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-rows", type=int, default=2048)
     ap.add_argument("--graph", action="store_true",
@@ -361,131 +497,32 @@ def main() -> int:
         log(f"copy probe: 3 launches over {n} floats ({8 * n} bytes each)")
         del src, dst
 
-    if args.config in ("c2", "c3"):
-        return bandwidth_main(args, TS, hip, hip_check)
+    if args.config:
+        result = (run_bandwidth(TS, args.config, args.steps, args.warmup, not args.no_cpu_baseline)
+                  if args.config in ("c2", "c3") else
+                  run_mlp(TS, hip, hip_check, args.config, args.steps, args.warmup, not args.no_cpu_baseline,
+                          args.cpu_sample_rows, args.graph))
+        print(json.dumps(result), flush=True)
+        return 0
 
-    batch, widths, init = CONFIGS[args.config]
-    readme = init == "readme"
-    rng = np.random.default_rng(0)
-    log(f"config {args.config}: batch {batch}, widths {widths}; uploading inputs")
-    ps = make_params(TS, widths, init, rng)
-    x = TS.Tensor.from_slice(rng.standard_normal((batch, widths[0]), dtype=np.float32), [batch, widths[0]])
-    t = TS.Tensor.from_slice(rng.standard_normal((batch, widths[-1]), dtype=np.float32), [batch, widths[-1]])
-    opt = TS.Adam.with_learning_rate(1e-3)
-    opt.add_parameters(ps)
-
-    def step():
-        loss = forward_loss(x, t, ps, readme)
-        loss.backward()
-        opt.step(ps)
-        opt.zero_grad(ps)
-        return loss
-
-    for i in range(args.warmup):
-        loss = step()
-        log(f"warmup step {i}: loss {loss.value():.6f}")
-    TS.synchronize()
-
-    stream = TS.stream()
-    ev0, ev1 = ctypes.c_void_p(), ctypes.c_void_p()
-    hip_check(hip.ts_hip_event_create(ctypes.byref(ev0)))
-    hip_check(hip.ts_hip_event_create(ctypes.byref(ev1)))
-    # The timed region times the roofline's class (the GEMMs) with device
-    # events around each launch; the other kernels run untimed, so the
-    # events perturb the step as little as possible.
-    TS.Profile.reset()
-    TS.Profile.enable(True, classes=[TS.Profile.GEMM])
-    TS.synchronize()
-    t0 = time.perf_counter()
-    hip_check(hip.ts_hip_event_record(ev0, stream))
-    for _ in range(args.steps):
-        loss = step()
-    hip_check(hip.ts_hip_event_record(ev1, stream))
-    TS.synchronize()
-    t1 = time.perf_counter()
-    TS.Profile.enable(False)
-    ev_ms = ctypes.c_float()
-    hip_check(hip.ts_hip_event_elapsed_ms(ctypes.byref(ev_ms), ev0, ev1))
-    final_loss = loss.value()
-    g = TS.Profile.read(TS.Profile.GEMM)
-
-    # Per-class breakdown: a separate pass after the timed one, every class timed.
-    breakdown_steps = max(1, min(args.steps, 5))
-    TS.Profile.reset()
-    TS.Profile.enable(True)
-    for _ in range(breakdown_steps):
-        step()
-    TS.synchronize()
-    TS.Profile.enable(False)
-    classes = {"gemm": TS.Profile.GEMM, "elementwise": TS.Profile.ELEMENTWISE,
-               "reduction": TS.Profile.REDUCTION, "adam": TS.Profile.ADAM}
-    prof = {k: TS.Profile.read(v) for k, v in classes.items()}
-
-    wall_ms = (t1 - t0) * 1000.0 / args.steps
-    gemm_tflops = g["work"] / (g["ms"] * 1e-3) / 1e12 if g["ms"] > 0 else 0.0
-    kernels = {"pass": f"a separate pass of {breakdown_steps} steps after the timed region, every class timed"}
-    for k, s in prof.items():
-        if s["launches"] == 0:
-            continue
-        rate = s["work"] / (s["ms"] * 1e-3) if s["ms"] > 0 else 0.0
-        per_step = {"ms_per_step": round(s["ms"] / breakdown_steps, 3),
-                    "launches_per_step": s["launches"] // breakdown_steps}
-        if k == "gemm":
-            kernels[k] = {**per_step, "TFLOP/s": round(rate / 1e12, 2),
-                          "frac_mfma_peak": round(rate / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)}
+    # Default: config 5 is the headline (value, steps, warmup and roofline of
+    # the line); every other BASELINE config is measured in the same run, with
+    # its own steps, roofline and CPU baseline, under "configs".
+    result = run_mlp(TS, hip, hip_check, "c5", args.steps, args.warmup, not args.no_cpu_baseline,
+                     args.cpu_sample_rows, args.graph)
+    others = {}
+    for cfg, steps, warmup in OTHER_CONFIGS:
+        TS.clear_gradients()
+        TS.empty_cache()
+        log(f"config {cfg}: {steps} timed steps after {warmup} warm-up steps")
+        if cfg in ("c2", "c3"):
+            r = run_bandwidth(TS, cfg, steps, warmup, not args.no_cpu_baseline)
         else:
-            kernels[k] = {**per_step, "GB/s": round(rate / 1e9, 1), "frac_hbm_peak": round(rate / 1e9 / PEAK_HBM_GBS, 4)}
-    per_launch_flops = g["work"] / g["launches"] if g["launches"] else 0.0
-    traffic, traffic_src = pmc_traffic(args.config)
-
-    result = {
-        "metric": "fwd+bwd+Adam steps/sec (1 GPU); % fp32 MFMA peak and % HBM GB/s roofline",
-        "value": round(1000.0 / wall_ms, 4),
-        "unit": "steps/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(wall_ms, 3),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (numpy default_rng(0); N(0,1/fan_in) weights, N(0,1) inputs and targets)",
-        "config": {"workload": {"c5": "BASELINE config 5: deep wide MLP, batch 8192, 6 x Linear(4096,4096)+bias, "
-                                      "ReLU on layers 1-5, MSE, fwd+bwd+Adam(lr 1e-3)",
-                                "c4": "BASELINE config 4: MLP batch 1024, 784->1024->10, MSE, fwd+bwd+Adam",
-                                "c1": "BASELINE config 1: README step x[32,784] W[784,128], relu, sum, Adam"}[args.config],
-                   "batch": batch, "widths": widths, "gemm_flop_per_step": step_flops(batch, widths, readme)},
-        "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": traffic,
-                     "traffic_source": traffic_src,
-                     "kernel": "gemm_f32_lds_dma (all 3 layouts, every launch of the timed region)",
-                     "flop_per_launch": per_launch_flops,
-                     "avg_launch_ms": round(g["ms"] / g["launches"], 4) if g["launches"] else None},
-        "kernels": kernels,
-        "event_ms_per_step": round(ev_ms.value / args.steps, 3),
-        "final_loss": final_loss,
-    }
-    if args.graph:
-        # the same loop, one step recorded and then replayed: every replay
-        # runs the whole step (the first runs the recorded one); untimed
-        # replays warm the graph up
-        with TS.StepGraph.record() as g:
-            gloss = step()
-        g.replay(max(1, args.warmup))
-        TS.synchronize()
-        t0 = time.perf_counter()
-        g.replay(args.steps)
-        TS.synchronize()
-        g_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
-        result["graph"] = {"value": round(1000.0 / g_ms, 4), "unit": "steps/s", "ms_per_step": round(g_ms, 4),
-                           "final_loss": gloss.value(), "note": "the same step replayed from a HIP graph"}
-        g.free()
-    if not args.no_cpu_baseline:
-        log("timing the CPU baseline (oracle port, one core, bounded sample)")
-        result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_sample_rows)
-    else:
-        result["cpu_baseline"] = None
+            r = run_mlp(TS, hip, hip_check, cfg, steps, warmup, not args.no_cpu_baseline, args.cpu_sample_rows,
+                        graph=True)
+        others[cfg] = {k: r[k] for k in ("metric", "value", "unit", "steps", "warmup", "ms_per_step", "config",
+                                         "roofline", "kernels", "cpu_baseline", "graph") if k in r}
+    result["configs"] = others
     print(json.dumps(result), flush=True)
     return 0
 

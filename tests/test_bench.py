@@ -68,3 +68,12 @@ def test_traffic_from_the_committed_counters():
     traffic, src = bench.pmc_traffic("c5")
     assert src == "profiles/c5_gemm_pmc.md" and traffic > 0
     assert bench.pmc_traffic("c2") == (None, None)
+
+
+def test_a_default_run_covers_every_baseline_config():
+    # config 5 is the headline; the others are measured in the same run with
+    # their own step counts (config 3 at the full 2^28 parameters)
+    names = [c for c, _, _ in bench.OTHER_CONFIGS]
+    assert sorted(names + ["c5"]) == ["c1", "c2", "c3", "c4", "c5"]
+    assert all(steps > 0 and warmup >= 0 for _, steps, warmup in bench.OTHER_CONFIGS)
+    assert bench.ADAM_P == 1 << 28 and bench.CHAIN_N == 1 << 26
