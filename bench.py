@@ -460,6 +460,72 @@ def run_mlp(TS, hip, hip_check, cfg: str, steps: int, warmup: int, cpu: bool, cp
     return result
 
 
+# (name, trans_a, trans_b, M, N, K): the products of configs 5 and 4
+GEMM_SHAPES = (
+    ("c5_fwd_NN", 0, 0, 8192, 4096, 4096),
+    ("c5_dX_NT", 0, 1, 8192, 4096, 4096),
+    ("c5_dW_TN", 1, 0, 4096, 4096, 8192),
+    ("c4_fwd1_NN", 0, 0, 1024, 1024, 784),
+    ("c4_dW1_TN", 1, 0, 784, 1024, 1024),
+    ("c4_fwd2_NN", 0, 0, 1024, 10, 1024),
+    ("c4_dX2_NT", 0, 1, 1024, 1024, 10),
+    ("c4_dW2_TN", 1, 0, 1024, 10, 1024),
+    ("c1_fwd_NN", 0, 0, 32, 128, 784),
+    ("c1_dW_TN", 1, 0, 784, 128, 32),
+)
+
+
+def gemm_compare(hip, hip_check, reps: int) -> dict:
+    """Each product of configs 5, 4 and 1 through this library's GEMM
+    (ts_hip_gemm_noalloc: ts_hip_gemm's kernels, the split-K temporary from its
+    fixed array, so no allocation is timed) and through torch's fp32 matmul
+    (rocBLAS / hipBLASLt, transposes passed as operand flags on views, no
+    copies), on the same stream, each timed over `reps` launches with events on
+    that stream; max relative difference of the two results."""
+    import torch
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    out = {}
+    for name, ta, tb, M, N, K in GEMM_SHAPES:
+        g = torch.Generator(device=dev).manual_seed(1)
+        a = torch.randn((K, M) if ta else (M, K), device=dev, generator=g)
+        b = torch.randn((N, K) if tb else (K, N), device=dev, generator=g)
+        c = torch.empty((M, N), device=dev)
+        lda, ldb = a.shape[1], b.shape[1]
+        av, bv = (a.t() if ta else a), (b.t() if tb else b)
+
+        def ours():
+            hip_check(hip.ts_hip_gemm_noalloc(ta, tb, M, N, K, a.data_ptr(), lda, b.data_ptr(), ldb, c.data_ptr(), N,
+                                              sp))
+
+        def theirs():
+            torch.matmul(av, bv, out=c_ref)
+
+        c_ref = torch.empty((M, N), device=dev)
+        rec = {}
+        for label, fn in (("ours", ours), ("torch_matmul", theirs)):
+            for _ in range(3):
+                fn()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                fn()
+            e1.record(stream)
+            e1.synchronize()
+            ms = e0.elapsed_time(e1) / reps
+            rec[label] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 2)}
+        diff = (c - c_ref).abs().max().item() / max(c_ref.abs().max().item(), 1e-30)
+        rec["max_rel_diff"] = diff
+        rec["ours_over_theirs"] = round(rec["torch_matmul"]["us"] / rec["ours"]["us"], 3)
+        out[name] = rec
+        log(f"{name}: {rec}")
+        del a, b, c, c_ref
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -473,6 +539,9 @@ def main() -> int:
     ap.add_argument("--graph", action="store_true",
                     help="also time the same step recorded once as a HIP graph and replayed (StepGraph); "
                          "reported beside the eager figure, which stays `value`")
+    ap.add_argument("--gemm-compare", type=int, default=0, metavar="REPS",
+                    help="instead of a training step: time every product of configs 5 and 4 through "
+                         "ts_hip_gemm and through torch's fp32 matmul (rocBLAS / hipBLASLt), REPS launches each")
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="first launch a plain copy kernel (x * 1.0 -> out, 8 bytes per float) over "
                          "this many floats three times, as the calibration point of HBM byte counters")
@@ -496,6 +565,11 @@ def main() -> int:
         TS.synchronize()
         log(f"copy probe: 3 launches over {n} floats ({8 * n} bytes each)")
         del src, dst
+
+    if args.gemm_compare:
+        print(json.dumps({"gemm_compare": gemm_compare(hip, hip_check, args.gemm_compare),
+                          "peak_TFLOPs": PEAK_FP32_MFMA_TFLOPS}), flush=True)
+        return 0
 
     if args.config:
         result = (run_bandwidth(TS, args.config, args.steps, args.warmup, not args.no_cpu_baseline)

@@ -191,7 +191,9 @@ def test_sum_dim0(oracle, rows, cols):
 
 
 GEMM_SHAPES = [(1, 1, 1), (2, 2, 2), (32, 128, 784), (784, 128, 32), (129, 127, 33), (1024, 10, 1024),
-               (1024, 1024, 10), (1024, 1024, 784), (784, 1024, 1024), (300, 200, 4096)]
+               (1024, 1024, 10), (1024, 1024, 784), (784, 1024, 1024), (300, 200, 4096),
+               # skinny (N <= 16): ragged rows, K not a multiple of 4, K longer than the chunk of every wave
+               (1000, 16, 777), (63, 1, 4096), (5000, 13, 65), (70, 9, 3)]
 
 
 def _gemm_case(oracle, ta, tb, M, N, K, seed, check_rows=None):

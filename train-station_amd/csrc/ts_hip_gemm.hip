@@ -191,6 +191,29 @@ struct Stage {
         }
     }
 
+    // edge tile along M / N with every k inside: the same dwordx4 loads with
+    // the row index kept inside the operand (rows past the edge feed outputs
+    // that are never stored, so any in-bounds values serve).  Needs the
+    // layout of g.vec (16-byte aligned, ld % 4 == 0): for a k-contiguous
+    // operand a row is clamped to rows - 1; otherwise a float4 of 4 rows
+    // starts at most at (rows - 1) & ~3, which ld >= rows rounded up to 4
+    // keeps inside the row.
+    static __device__ __forceinline__ void load_clamped(const float *__restrict__ P, int ld, int rows, int r0,
+                                                        int k0, float4 (&reg)[NF]) {
+#pragma unroll
+        for (int s = 0; s < NF; ++s) {
+            int row, kk;
+            coords(s * NT + threadIdx.x, row, kk);
+            if (KCONTIG) {
+                const int r = min(r0 + row, rows - 1);
+                reg[s] = *reinterpret_cast<const float4 *>(P + (size_t)r * ld + (k0 + kk));
+            } else {
+                const int r = min(r0 + row, (rows - 1) & ~3);
+                reg[s] = *reinterpret_cast<const float4 *>(P + (size_t)(k0 + kk) * ld + r);
+            }
+        }
+    }
+
     // edge tile: element loads with bounds checks, zeros outside
     static __device__ __forceinline__ void load_guarded(const float *__restrict__ P, int ld, int rows,
                                                         int K, int r0, int k0, float4 (&reg)[NF]) {
@@ -245,8 +268,10 @@ __device__ inline void tile_coords(int tiles_m, int tiles_n, int b, int &tm, int
 }
 
 // EPI: the epilogue kind applied at the store (a separate instantiation per
-// kind, so the bare product keeps its register allocation).
-template <bool TA, bool TB, int BM, int BN, int WM, int WN, int EPI>
+// kind, so the bare product keeps its register allocation).  PF: operand tiles
+// prefetched into registers ahead of the LDS stage (deeper for small tiles,
+// whose k-steps are too short to cover a global load).
+template <bool TA, bool TB, int BM, int BN, int WM, int WN, int EPI, int PF>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
     constexpr int NT = 64 * WM * WN;
     constexpr int TMW = BM / WM, TNW = BN / WN;  // wave tile
@@ -296,68 +321,89 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
 
     const int nk = (g.K + kBK - 1) / kBK;
     const bool mn_inside = g.vec && (i0 + BM <= g.M) && (j0 + BN <= g.N);
-    float4 ra[SA::NF], rb[SB::NF];
-    auto load = [&](int k0) {
+    // Register ring of PF operand tiles: tile t >= 1 is loaded into slot
+    // (t - 1) % PF and stored to LDS at step t - 1, so its global loads have
+    // PF k-steps to arrive (one step is short for a small wave tile).  The
+    // loop is unrolled PF times so the slots are static registers.
+    float4 ra[PF][SA::NF], rb[PF][SB::NF];
+    auto load = [&](int k0, float4(&a)[SA::NF], float4(&b)[SB::NF]) {
         if (mn_inside && k0 + kBK <= g.K) {  // uniform across the workgroup
-            SA::load_fast(Ap, g.lda, i0, k0, ra);
-            SB::load_fast(Bp, g.ldb, j0, k0, rb);
+            SA::load_fast(Ap, g.lda, i0, k0, a);
+            SB::load_fast(Bp, g.ldb, j0, k0, b);
+        } else if (g.vec && k0 + kBK <= g.K) {  // an M / N edge tile: clamped rows, still dwordx4
+            SA::load_clamped(Ap, g.lda, g.M, i0, k0, a);
+            SB::load_clamped(Bp, g.ldb, g.N, j0, k0, b);
         } else {
-            SA::load_guarded(Ap, g.lda, g.M, g.K, i0, k0, ra);
-            SB::load_guarded(Bp, g.ldb, g.N, g.K, j0, k0, rb);
+            SA::load_guarded(Ap, g.lda, g.M, g.K, i0, k0, a);
+            SB::load_guarded(Bp, g.ldb, g.N, g.K, j0, k0, b);
         }
     };
 
-    load(0);
-    SA::store(As[0], ra);
-    SB::store(Bs[0], rb);
-    if (nk > 1) load(kBK);
+    load(0, ra[0], rb[0]);
+    SA::store(As[0], ra[0]);
+    SB::store(Bs[0], rb[0]);
+#pragma unroll
+    for (int p = 0; p < PF; ++p)
+        if (1 + p < nk) load((1 + p) * kBK, ra[p], rb[p]);
     __syncthreads();
 
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        // LDS[cur] holds tile kt; registers hold tile kt+1.  Buffer cur^1 was
-        // last read before the previous barrier, so it can take tile kt+1 now.
-        if (kt + 1 < nk) {
-            SA::store(As[cur ^ 1], ra);
-            SB::store(Bs[cur ^ 1], rb);
-            if (kt + 2 < nk) load((kt + 2) * kBK);
+    for (int kt0 = 0; kt0 < nk; kt0 += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+            const int kt = kt0 + u;
+            if (kt >= nk) break;  // uniform
+            const int cur = kt & 1;
+            // LDS[cur] holds tile kt; slot u holds tile kt+1.  Buffer cur^1
+            // was last read before the previous barrier, so it can take tile
+            // kt+1 now, and slot u then takes tile kt+1+PF.
+            if (kt + 1 < nk) {
+                SA::store(As[cur ^ 1], ra[u]);
+                SB::store(Bs[cur ^ 1], rb[u]);
+                if (kt + 1 + PF < nk) load((kt + 1 + PF) * kBK, ra[u], rb[u]);
+            }
+            const float *Ac = As[cur];
+            const float *Bc = Bs[cur];
+#pragma unroll
+            for (int s = 0; s < kBK / 2; ++s) {
+                const int k = 2 * s + lhalf;
+                float af[FM], bf[FN];
+#pragma unroll
+                for (int a = 0; a < FM; ++a) af[a] = Ac[k * BM + ((wm * TMW + a * 32 + lrow) ^ swz(k))];
+#pragma unroll
+                for (int b = 0; b < FN; ++b) bf[b] = Bc[k * BN + ((wn * TNW + b * 32 + lrow) ^ swz(k))];
+#pragma unroll
+                for (int a = 0; a < FM; ++a)
+#pragma unroll
+                    for (int b = 0; b < FN; ++b)
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a], bf[b], acc[a][b], 0, 0, 0);
+            }
+            // Scheduling hint: alternate one MFMA and one LDS read across the
+            // whole k-tile, so operand reads of later k-steps issue under the
+            // MFMAs of earlier ones instead of clustering ahead of them.
+#pragma unroll
+            for (int i = 0; i < kBK / 2 * FM * FN; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+            }
+            __syncthreads();
         }
-        const float *Ac = As[cur];
-        const float *Bc = Bs[cur];
-#pragma unroll
-        for (int s = 0; s < kBK / 2; ++s) {
-            const int k = 2 * s + lhalf;
-            float af[FM], bf[FN];
-#pragma unroll
-            for (int a = 0; a < FM; ++a) af[a] = Ac[k * BM + ((wm * TMW + a * 32 + lrow) ^ swz(k))];
-#pragma unroll
-            for (int b = 0; b < FN; ++b) bf[b] = Bc[k * BN + ((wn * TNW + b * 32 + lrow) ^ swz(k))];
-#pragma unroll
-            for (int a = 0; a < FM; ++a)
-#pragma unroll
-                for (int b = 0; b < FN; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a], bf[b], acc[a][b], 0, 0, 0);
-        }
-        // Scheduling hint: alternate one MFMA and one LDS read across the
-        // whole k-tile, so operand reads of later k-steps issue under the
-        // MFMAs of earlier ones instead of clustering ahead of them.
-#pragma unroll
-        for (int i = 0; i < kBK / 2 * FM * FN; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
-        }
-        __syncthreads();
     }
 
     store_tile<EPI, FM, FN>(g, acc, Cp, i0 + wm * TMW, j0 + wn * TNW, lrow, lhalf);
 }
 
+// Register prefetch depth per tile size: one tile ahead for 256x256 tiles
+// (a k-step of 8 waves' 128x64 blocks is long), four for the smaller ones.
+template <int BM>
+constexpr int prefetch_tiles() { return BM >= 256 ? 1 : 4; }
+
 template <int BM, int BN, int WM, int WN, int EPI>
 static void launch_tiles_as(int ta, int tb, const GemmArgs &g, dim3 grid, dim3 block, hipStream_t s) {
-    if (!ta && !tb) hipLaunchKernelGGL((gemm_f32_mfma<false, false, BM, BN, WM, WN, EPI>), grid, block, 0, s, g);
-    else if (!ta && tb) hipLaunchKernelGGL((gemm_f32_mfma<false, true, BM, BN, WM, WN, EPI>), grid, block, 0, s, g);
-    else if (ta && !tb) hipLaunchKernelGGL((gemm_f32_mfma<true, false, BM, BN, WM, WN, EPI>), grid, block, 0, s, g);
-    else hipLaunchKernelGGL((gemm_f32_mfma<true, true, BM, BN, WM, WN, EPI>), grid, block, 0, s, g);
+    constexpr int PF = prefetch_tiles<BM>();
+    if (!ta && !tb) hipLaunchKernelGGL((gemm_f32_mfma<false, false, BM, BN, WM, WN, EPI, PF>), grid, block, 0, s, g);
+    else if (!ta && tb) hipLaunchKernelGGL((gemm_f32_mfma<false, true, BM, BN, WM, WN, EPI, PF>), grid, block, 0, s, g);
+    else if (ta && !tb) hipLaunchKernelGGL((gemm_f32_mfma<true, false, BM, BN, WM, WN, EPI, PF>), grid, block, 0, s, g);
+    else hipLaunchKernelGGL((gemm_f32_mfma<true, true, BM, BN, WM, WN, EPI, PF>), grid, block, 0, s, g);
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -370,7 +416,6 @@ static void launch_tiles(int ta, int tb, GemmArgs g, hipStream_t s, unsigned bat
     if (g.bias || g.mask || g.relu) launch_tiles_as<BM, BN, WM, WN, kEpiAll>(ta, tb, g, grid, block, s);
     else launch_tiles_as<BM, BN, WM, WN, kEpiNone>(ta, tb, g, grid, block, s);
 }
-
 
 // ---------------------------------------------------------------------------
 // LDS-DMA path.  A 256 x 16 operand tile is 1024 16-byte chunks; DMA
@@ -595,14 +640,21 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_lds_dma(GemmArgs g) {
 }
 
 // Split-K: C[i][j] = sum over s of the slice products P_s[i][j] (P_s at
-// P + s*M*N, row-major M x N), added in slice order.
+// P + s*M*N, row-major M x N), added in slice order; at most 16 slices (both
+// splitting paths stay within that).
 __global__ __launch_bounds__(kBlock) void splitk_sum(const float *__restrict__ P, int slices, size_t M, size_t N,
                                                      float *__restrict__ C, size_t ldc, GemmArgs e) {
     const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
     const size_t mn = M * N;
     if (t >= mn) return;
-    float acc = P[t];
-    for (int k = 1; k < slices; ++k) acc += P[static_cast<size_t>(k) * mn + t];
+    // every slice's value in flight at once (slices <= 16), then the sum in slice order
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = k < slices ? P[static_cast<size_t>(k) * mn + t] : 0.0f;
+    float acc = v[0];
+#pragma unroll
+    for (int k = 1; k < 16; ++k)
+        if (k < slices) acc += v[k];
     const size_t i = t / N, j = t % N;
     C[i * ldc + j] = epilogue(e, acc, static_cast<int>(i), static_cast<int>(j));
 }
@@ -679,10 +731,157 @@ static int gemm_launch(int trans_a, int trans_b, size_t M, size_t N, size_t K, c
     return launch_status();
 }
 
+// ---- skinny products (N <= 16) -----------------------------------------------
+//
+// A product with at most 16 output columns (a layer with few outputs: config
+// 4's 1024x10 products) is a stream over A with N multiply-adds per element:
+// MFMA tiles would pad N to 32 or more.  A workgroup of 4 waves takes 64 rows,
+// a lane per row, and one slice of K (grid.y slices, enough row groups x
+// slices for every CU); its waves split the slice into 4 contiguous ranges.
+// A wave walks its range in chunks of 64 k: the chunk's B rows go to the
+// wave's own LDS slab, zero-padded to 16 columns, its A values are loaded
+// all at once, and each k then reads its B row as four broadcast float4s and
+// does 16 fma on the lane's accumulators (k ascending).  The waves' sums are
+// added in wave order through LDS; with one slice the result is stored with
+// the epilogue, else slice s goes to P[s][M][N] and splitk_sum adds the slices
+// in order and applies the epilogue.  Deterministic; the accumulation order
+// differs from the MFMA kernels' (both within rounding of the exact product).
+constexpr int kSkinnyN = 16;
+constexpr int kSkinnyWaves = 4;
+constexpr int kSkinnyChunk = 64;
+constexpr int kSkinnyMaxSlices = 16;
+static_assert(kSkinnyMaxSlices <= 16, "splitk_sum adds at most 16 slices");
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny(GemmArgs g, float *P) {
+    __shared__ float part[kSkinnyWaves][kSkinnyN][64];
+    __shared__ float4 bs[kSkinnyWaves][kSkinnyChunk][kSkinnyN / 4];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int i = blockIdx.x * 64 + lane;
+    const int ir = i < g.M ? i : g.M - 1;  // rows past M: an in-bounds row, never stored
+    const float *__restrict__ A = g.A;
+    const float *__restrict__ B = g.B;
+    // k range of this wave within this workgroup's slice (lengths are
+    // multiples of 4, so a row-major A row is read as float4)
+    const int slices = gridDim.y, slice = blockIdx.y;
+    const int ks = ((g.K + slices - 1) / slices + 3) & ~3;
+    const int sb = min(g.K, slice * ks), se = min(g.K, sb + ks);
+    const int kc = ((ks + kSkinnyWaves - 1) / kSkinnyWaves + 3) & ~3;
+    const int kb = min(se, sb + wave * kc);
+    const int ke = min(se, kb + kc);
+    const int chunks = (kc + kSkinnyChunk - 1) / kSkinnyChunk;  // the same for every wave
+    float acc[kSkinnyN];
+#pragma unroll
+    for (int j = 0; j < kSkinnyN; ++j) acc[j] = 0.0f;
+    const float *arow = A + (size_t)ir * g.lda;
+    const bool a4 = !TA && g.vec;
+    for (int c = 0; c < chunks; ++c) {
+        const int k0 = kb + c * kSkinnyChunk;
+        const int len = max(0, min(kSkinnyChunk, ke - k0));  // uniform per wave
+        // the chunk's A values first (they do not wait for the B slab), every
+        // load of the chunk in flight at once, then the fma
+        float av[kSkinnyChunk];
+        if (len == kSkinnyChunk && a4) {  // row-major A: 4 k per dwordx4 load
+#pragma unroll
+            for (int q = 0; q < kSkinnyChunk / 4; ++q) {
+                const float4 v = *reinterpret_cast<const float4 *>(arow + k0 + 4 * q);
+                av[4 * q] = v.x;
+                av[4 * q + 1] = v.y;
+                av[4 * q + 2] = v.z;
+                av[4 * q + 3] = v.w;
+            }
+        } else {  // A stored [K][lda]: the lanes read 64 consecutive floats per k
+#pragma unroll
+            for (int kk = 0; kk < kSkinnyChunk; ++kk)
+                av[kk] = kk < len ? (TA ? A[(size_t)(k0 + kk) * g.lda + ir] : arow[k0 + kk]) : 0.0f;
+        }
+        // stage: lane l takes B row k0 + l, columns past N (and rows past the
+        // range) as zeros
+        {
+            const int k = k0 + lane;
+            float v[kSkinnyN];
+#pragma unroll
+            for (int j = 0; j < kSkinnyN; ++j)
+                v[j] = (lane < len && j < g.N) ? (TB ? B[(size_t)j * g.ldb + k] : B[(size_t)k * g.ldb + j]) : 0.0f;
+#pragma unroll
+            for (int q = 0; q < kSkinnyN / 4; ++q)
+                bs[wave][lane][q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kSkinnyChunk; ++kk) {
+            if (kk < len) {  // uniform per wave
+                const float4 b0 = bs[wave][kk][0], b1 = bs[wave][kk][1], b2 = bs[wave][kk][2], b3 = bs[wave][kk][3];
+                const float b[kSkinnyN] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w,
+                                           b2.x, b2.y, b2.z, b2.w, b3.x, b3.y, b3.z, b3.w};
+#pragma unroll
+                for (int j = 0; j < kSkinnyN; ++j) acc[j] = __builtin_fmaf(av[kk], b[j], acc[j]);
+            }
+        }
+        __syncthreads();  // the slab is restaged next chunk
+    }
+#pragma unroll
+    for (int j = 0; j < kSkinnyN; ++j) part[wave][j][lane] = acc[j];
+    __syncthreads();
+    if (i >= g.M) return;
+    for (int j = wave; j < g.N; j += kSkinnyWaves) {
+        float v = part[0][j][lane];
+#pragma unroll
+        for (int w = 1; w < kSkinnyWaves; ++w) v += part[w][j][lane];
+        if (slices == 1) g.C[(size_t)i * g.ldc + j] = epilogue(g, v, i, j);
+        else P[((size_t)slice * g.M + i) * g.N + j] = v;
+    }
+}
+
+static bool skinny(size_t N) { return N <= static_cast<size_t>(kSkinnyN); }
+
+// Slices of K for a skinny product: enough (row group x slice) workgroups for
+// every CU, each slice at least 64 k long; 1 when the row groups alone
+// fill the chip.
+static int skinny_slices(size_t M, size_t K) {
+    const size_t cus = static_cast<size_t>(device_cu_count());
+    const size_t groups = (M + 63) / 64;
+    if (groups >= cus) return 1;
+    size_t sl = (cus + groups - 1) / groups;
+    if (sl > static_cast<size_t>(kSkinnyMaxSlices)) sl = kSkinnyMaxSlices;
+    const size_t by_k = K / 64 > 0 ? K / 64 : 1;
+    if (sl > by_k) sl = by_k;
+    return static_cast<int>(sl);
+}
+
+// P: slices * M * N floats when skinny_slices(M, K) > 1 (else unused).
+static int launch_skinny(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A, size_t lda,
+                         const float *B, size_t ldb, float *C, size_t ldc, GemmArgs g, float *P, void *stream) {
+    if (!A || !B) return TS_HIP_EINVAL;
+    if (lda < (trans_a ? M : K) || ldb < (trans_b ? K : N)) return TS_HIP_EINVAL;
+    const size_t lim = 0x7ffffe00ULL;
+    if (M > lim || K > lim || lda > lim || ldb > lim || ldc > lim) return TS_HIP_EINVAL;
+    const int slices = skinny_slices(M, K);
+    if (slices > 1 && !P) return TS_HIP_EINVAL;
+    g.A = A; g.B = B; g.C = C;
+    g.M = static_cast<int>(M); g.N = static_cast<int>(N); g.K = static_cast<int>(K);
+    g.lda = static_cast<int>(lda); g.ldb = static_cast<int>(ldb); g.ldc = static_cast<int>(ldc);
+    g.vec = aligned16(A) && (lda % 4 == 0);
+    const dim3 grid(static_cast<unsigned>((M + 63) / 64), static_cast<unsigned>(slices)), block(64 * kSkinnyWaves);
+    hipStream_t s = as_stream(stream);
+    if (!trans_a && !trans_b) hipLaunchKernelGGL((gemm_skinny<false, false>), grid, block, 0, s, g, P);
+    else if (!trans_a) hipLaunchKernelGGL((gemm_skinny<false, true>), grid, block, 0, s, g, P);
+    else if (!trans_b) hipLaunchKernelGGL((gemm_skinny<true, false>), grid, block, 0, s, g, P);
+    else hipLaunchKernelGGL((gemm_skinny<true, true>), grid, block, 0, s, g, P);
+    int st = launch_status();
+    if (st != TS_HIP_OK || slices == 1) return st;
+    const size_t blocks = (M * N + kBlock - 1) / kBlock;
+    hipLaunchKernelGGL(splitk_sum, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, P, slices, M, N, C, ldc,
+                       g);
+    return launch_status();
+}
+
 // Few output tiles and a long K: K is split into this many slices (1: not
 // split), computed as a batch into a temporary of slices*M*N floats and then
 // added in slice order.
 static int split_slices(size_t M, size_t N, size_t K) {
+    if (skinny(N)) return skinny_slices(M, K);
     const size_t cus = static_cast<size_t>(device_cu_count());
     const size_t tiles64 = ((M + 63) / 64) * ((N + 63) / 64);
     if (4 * tiles64 < cus && K >= 512) {
@@ -708,6 +907,26 @@ static int gemm_plain(int trans_a, int trans_b, size_t M, size_t N, size_t K, co
         if (st == TS_HIP_OK && relu) st = ts_hip_relu(C, C, M * N, stream);
         if (st == TS_HIP_OK && mask) st = ts_hip_relu_backward(mask, C, C, M * N, stream);
         return st;
+    }
+    if (skinny(N)) {  // few output columns: the skinny kernel, K split over the CUs
+        GemmArgs g{};
+        g.bias = bias;
+        g.mask = mask;
+        g.relu = relu;
+        const int slices = skinny_slices(M, K);
+        if (slices == 1) return launch_skinny(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, g, nullptr, stream);
+        hipStream_t st = as_stream(stream);
+        const size_t need = static_cast<size_t>(slices) * M * N;
+        if (ws && ws_floats < need) return TS_HIP_EWORKSPACE;
+        float *P = ws;
+        if (!P && hipMallocAsync(reinterpret_cast<void **>(&P), need * sizeof(float), st) != hipSuccess) {
+            (void)hipGetLastError();
+            return TS_HIP_EINVAL;  // no stream-ordered allocator: the caller passes a workspace
+        }
+        const int status = launch_skinny(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, g, P, stream);
+        if (ws) return status;
+        const hipError_t fe = hipFreeAsync(P, st);
+        return status != TS_HIP_OK ? status : static_cast<int>(fe);
     }
     const int slices = split_slices(M, N, K);
     if (slices > 1 && A && B && lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N)) {
@@ -757,10 +976,11 @@ extern "C" int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t 
 // ---- allocation-free form --------------------------------------------------
 //
 // ts_hip_gemm_noalloc takes the split-K temporary from this fixed device
-// array instead of the stream-ordered allocator.  A split runs only while
-// 4 * (64x64 tiles) < CUs with slices * tiles <= 2 * CUs, so it never needs
-// more than 2 * CUs * 64 * 64 floats: 2^21 (8 MiB) on the 256 CUs of an
-// MI355X.  Every device the library runs on holds its own copy for the life
+// array instead of the stream-ordered allocator.  An MFMA split runs only
+// while 4 * (64x64 tiles) < CUs with slices * tiles <= 2 * CUs, so it never
+// needs more than 2 * CUs * 64 * 64 floats: 2^21 (8 MiB) on the 256 CUs of an
+// MI355X; a skinny split (N <= 16) has fewer 64-row groups than CUs and at
+// most CUs / groups + 1 slices, so slices * M * N <= 128 * CUs * 16 = 2^19.  Every device the library runs on holds its own copy for the life
 // of the process.  Calls that overlap on one device (several streams) share
 // it and race; the split slices are fully written before they are read, so
 // nothing needs clearing between calls.
