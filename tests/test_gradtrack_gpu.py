@@ -26,6 +26,7 @@ def TS():
 
     TS.clear_gradients()
     yield TS
+    TS.set_fusion(True)
     TS.clear_gradients()
 
 
@@ -419,7 +420,8 @@ def test_sub_backward_skips_the_unconsumed_negation(TS):
     n = 4099
     yv, tv = normal(n, 31), normal(n, 32)
 
-    def run(t_grad):
+    def run(t_grad, fusion=False):
+        TS.set_fusion(fusion)  # op-by-op launches; with fusion the chain is one pass either way
         y = TS.Tensor.from_slice(yv, [n]).with_requires_grad()
         t = TS.Tensor.from_slice(tv, [n])
         if t_grad:
@@ -432,6 +434,7 @@ def test_sub_backward_skips_the_unconsumed_negation(TS):
         gy = y.grad_by_value().data()
         gt = t.grad_by_value().data() if t_grad else None
         TS.clear_gradients()
+        TS.set_fusion(True)
         return launches, gy, gt
 
     l1, gy1, _ = run(False)
@@ -440,6 +443,9 @@ def test_sub_backward_skips_the_unconsumed_negation(TS):
     assert_bits_equal(gy1, gy2)
     assert_bits_equal(gt2, -gy2)
     np.testing.assert_allclose(gy1, 2.0 * (yv - tv) / n, rtol=1e-5, atol=1e-9)
+    _, gy3, gt3 = run(True, fusion=True)
+    assert_bits_equal(gy3, gy2)
+    assert_bits_equal(gt3, gt2)
 
 
 # ---- NoGradTrack, Tensor::grad, set_learning_rate ------------------------------------------------
@@ -564,16 +570,27 @@ def test_only_the_consumed_gradient_is_computed(TS, G, op, recorded):
         y = getattr(a, f"{op}_tensor")(b)
         return a, b, y.mul_tensor(y).sum()
 
-    a, b, loss = build(lambda v: TS.Tensor.from_slice(v, [n]), recorded)
-    TS.Profile.reset()
-    TS.Profile.enable(True)
-    loss.backward()
-    TS.Profile.enable(False)
-    ew = TS.Profile.read(TS.Profile.ELEMENTWISE)
-    got = (a if recorded == "left" else b).grad_by_value().data()
     ao, bo, lo = build(lambda v: G.OTensor(v.copy()), recorded)
     lo.backward()
     want = (ao if recorded == "left" else bo).grad_by_value()
+    # with fusion the unconsumed formula is never evaluated at all: bits only
+    TS.set_fusion(True)
+    a, b, loss = build(lambda v: TS.Tensor.from_slice(v, [n]), recorded)
+    loss.backward()
+    assert_bits_equal((a if recorded == "left" else b).grad_by_value().data(), want, f"{op} fused")
+    TS.clear_gradients()
+    # op by op: the kernels launched show that no pass ran for it
+    TS.set_fusion(False)
+    try:
+        a, b, loss = build(lambda v: TS.Tensor.from_slice(v, [n]), recorded)
+        TS.Profile.reset()
+        TS.Profile.enable(True)
+        loss.backward()
+        TS.Profile.enable(False)
+        ew = TS.Profile.read(TS.Profile.ELEMENTWISE)
+        got = (a if recorded == "left" else b).grad_by_value().data()
+    finally:
+        TS.set_fusion(True)
     assert_bits_equal(got, want, f"{op} gradient to the {recorded} operand")
     # the scalar seed (ones), the sum's fill, y*y's backward (both operands
     # are y: one launch writing two gradients, then their accumulation) and

@@ -1,0 +1,249 @@
+"""Fused elementwise programs (ts_hip_map) and the host's deferred chains built
+on them.  Every op of a program must give the bits of its separate kernel
+(the reference's fp32 formula and order: ops/{add,sub,mul,div,relu,pow}.rs,
+core/utils.rs:802-871, grad_fn/ops/relu.rs), a fused sum / mean the bits of
+ts_hip_sum / ts_hip_mean over the same values, and a recorded chain the bits
+of the op-by-op graph, with fusion on and off.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import assert_bits_equal, normal, uniform
+
+pytestmark = pytest.mark.gpu
+
+SIZES = [1, 7, 1003, (1 << 20) + 5]
+
+
+def _ffi():
+    from train_station_amd import _ffi
+    return _ffi
+
+
+def _program(inputs, ops, outputs, scalar=0, reduce_reg=-1):
+    """inputs: device pointers; ops: (code name, a, b, imm, flags) with
+    registers numbered as in include/ts_hip.h; outputs: (pointer, register)."""
+    F = _ffi()
+    p = F.MapProgram()
+    p.n_inputs = len(inputs)
+    for k, ptr in enumerate(inputs):
+        p.inputs[k] = ptr
+    p.scalar_inputs = scalar
+    p.n_ops = len(ops)
+    for k, (code, a, b, imm, flags) in enumerate(ops):
+        p.ops[k] = F.MapOp(F.MAP_CODES[code], a, b, flags, imm)
+    p.n_outputs = len(outputs)
+    for k, (ptr, reg) in enumerate(outputs):
+        p.outputs[k] = ptr
+        p.output_regs[k] = reg
+    p.reduce_reg = reduce_reg
+    return p
+
+
+R0 = 5  # register of op 0 (TS_HIP_MAP_MAX_INPUTS)
+
+
+def test_register_numbering_follows_the_header():
+    assert _ffi().MAP_MAX_INPUTS == R0
+
+
+@pytest.mark.parametrize("offset", [0, 1])
+@pytest.mark.parametrize("n", SIZES)
+def test_each_op_matches_its_kernel(n, offset):
+    from gpu_util import Dev, ZeroIndex, hip, hip_check, sync
+    print(f"[map ops] n={n} offset={offset}", flush=True)
+    a = normal(n, 1)
+    b = uniform(n, 0.5, 2.0, 2) * np.where(np.arange(n) % 3 == 0, -1, 1).astype(np.float32)
+    a[: min(n, 4)] = np.array([0.0, -0.0, np.inf, -np.inf], np.float32)[: min(n, 4)]
+    da, db = Dev.of(a, offset), Dev.of(b, offset)
+    tail8, tail32 = 8 * (n // 8), 32 * (n // 32)
+    zi = ZeroIndex()
+    cases = [  # (op, imm, reference launcher)
+        ("add", 0.0, lambda o: hip.ts_hip_add(da.ptr, db.ptr, o, n, None)),
+        ("sub", 0.0, lambda o: hip.ts_hip_sub(da.ptr, db.ptr, o, n, None)),
+        ("mul", 0.0, lambda o: hip.ts_hip_mul(da.ptr, db.ptr, o, n, None)),
+        ("div", 0.0, lambda o: hip.ts_hip_div(da.ptr, db.ptr, o, n, tail32, zi.ptr, None)),
+        ("neg", 0.0, lambda o: hip.ts_hip_neg(da.ptr, o, n, tail8, None)),
+        ("relu", 0.0, lambda o: hip.ts_hip_relu(da.ptr, o, n, None)),
+        ("relu_bwd", 0.0, lambda o: hip.ts_hip_relu_backward(da.ptr, db.ptr, o, n, None)),
+        ("add_s", 0.37, lambda o: hip.ts_hip_add_scalar(da.ptr, ctypes.c_float(0.37), o, n, None)),
+        ("sub_s", 0.37, lambda o: hip.ts_hip_sub_scalar(da.ptr, ctypes.c_float(0.37), o, n, None)),
+        ("mul_s", -3.1, lambda o: hip.ts_hip_mul_scalar(da.ptr, ctypes.c_float(-3.1), o, n, None)),
+        ("div_s", 7.0, lambda o: hip.ts_hip_div_scalar(da.ptr, ctypes.c_float(7.0), o, n, None)),
+        ("square", 0.0, lambda o: hip.ts_hip_pow_scalar(da.ptr, ctypes.c_float(2.0), o, n, None)),
+    ]
+    for code, imm, ref in cases:
+        got, want = Dev(n, offset), Dev(n, offset)
+        flags = _ffi().MAP_CHECKED if code == "div" else 0
+        prog = _program([da.ptr, db.ptr], [(code, 0, 1, imm, flags)], [(got.ptr, R0)])
+        hip_check(hip.ts_hip_map(ctypes.byref(prog), n, tail8, tail32, zi.ptr, None, 0, None, 0, None), code)
+        hip_check(ref(want.ptr), code)
+        sync()
+        assert_bits_equal(got.get(), want.get(), f"{code} n={n}")
+
+
+def test_chain_multi_output_and_scalar_input():
+    # the config-2 backward as one program over (y, go, c, a, t1), go one value
+    # for every element: the three gradients equal the separate kernels' chain
+    from gpu_util import Dev, hip, hip_check, sync
+    n = 4099
+    y, c, a, t1 = normal(n, 3), uniform(n, 0.5, 2.0, 4), normal(n, 5), normal(n, 6)
+    go = np.array([1.0], np.float32)
+    dy, dc, da, dt, dgo = (Dev.of(v) for v in (y, c, a, t1, go))
+    tail8, tail32 = 8 * (n // 8), 32 * (n // 32)
+    r = R0  # op k writes register r + k
+    ops = [("relu_bwd", 0, 1, 0.0, 0),              # r+0  g4 = y > 0 ? go : 0
+           ("neg", r, r, 0.0, 0),                   # r+1  g3
+           ("div", r + 1, 2, 0.0, 1),               # r+2  g3 / c
+           ("mul", r, 2, 0.0, 0),                   # r+3  g4 * c
+           ("add", r + 2, r + 3, 0.0, 0),           # r+4  ga
+           ("mul", r + 1, 3, 0.0, 0),               # r+5  g3 * a
+           ("mul", 2, 2, 0.0, 0),                   # r+6  c * c
+           ("div", r + 5, r + 6, 0.0, 1),           # r+7
+           ("neg", r + 7, r + 7, 0.0, 0),           # r+8  gc_1
+           ("mul", r, 4, 0.0, 0),                   # r+9  gc_2 = g4 * t1
+           ("add", r + 8, r + 9, 0.0, 0)]           # r+10 gc
+    ga, gb, gc = Dev(n), Dev(n), Dev(n)
+    prog = _program([dy.ptr, dgo.ptr, dc.ptr, da.ptr, dt.ptr], ops,
+                    [(ga.ptr, r + 4), (gb.ptr, r + 3), (gc.ptr, r + 10)], scalar=1 << 1)
+    hip_check(hip.ts_hip_map(ctypes.byref(prog), n, tail8, tail32, None, None, 0, None, 0, None), "map")
+    # the same through the separate kernels
+    ones = Dev.of(np.ones(n, np.float32))
+    g4, g3, q, qb, wa, wc = (Dev(n) for _ in range(6))
+    hip_check(hip.ts_hip_relu_backward(dy.ptr, ones.ptr, g4.ptr, n, None))
+    hip_check(hip.ts_hip_neg(g4.ptr, g3.ptr, n, tail8, None))
+    hip_check(hip.ts_hip_div_backward(g3.ptr, da.ptr, dc.ptr, q.ptr, qb.ptr, n, tail8, tail32, None, None))
+    hip_check(hip.ts_hip_mul_backward(g4.ptr, dt.ptr, dc.ptr, wa.ptr, wc.ptr, n, None))
+    want_a, want_c = Dev(n), Dev(n)
+    hip_check(hip.ts_hip_add(q.ptr, wa.ptr, want_a.ptr, n, None))
+    hip_check(hip.ts_hip_add(qb.ptr, wc.ptr, want_c.ptr, n, None))
+    sync()
+    assert_bits_equal(ga.get(), want_a.get(), "ga")
+    assert_bits_equal(gb.get(), wa.get(), "gb")
+    assert_bits_equal(gc.get(), want_c.get(), "gc")
+
+
+@pytest.mark.parametrize("n", [1, 5, 4096, 100003, 1 << 22])
+@pytest.mark.parametrize("mean", [0, 1])
+def test_fused_sum_has_the_bits_of_ts_hip_sum(n, mean):
+    from gpu_util import Dev, hip, hip_check, sync
+    y, t = normal(n, 7), normal(n, 8)
+    dy, dt = Dev.of(y), Dev.of(t)
+    d, out = Dev(n), Dev(1)
+    ws = hip.ts_hip_map_workspace_floats(n)
+    dws = Dev(ws + 2)
+    # d = y - t stored; sum / mean of d * d without storing it
+    prog = _program([dy.ptr, dt.ptr], [("sub", 0, 1, 0.0, 0), ("square", R0, R0, 0.0, 0)], [(d.ptr, R0)],
+                    reduce_reg=R0 + 1)
+    hip_check(hip.ts_hip_map(ctypes.byref(prog), n, 8 * (n // 8), 32 * (n // 32), None, out.ptr, mean, dws.ptr, ws,
+                             None), "map")
+    sq, want = Dev(n), Dev(1)
+    hip_check(hip.ts_hip_sub(dy.ptr, dt.ptr, sq.ptr, n, None))
+    hip_check(hip.ts_hip_pow_scalar(sq.ptr, ctypes.c_float(2.0), sq.ptr, n, None))
+    sw = hip.ts_hip_sum_workspace_floats(n)
+    dsw = Dev(sw + 2)
+    fn = hip.ts_hip_mean if mean else hip.ts_hip_sum
+    hip_check(fn(sq.ptr, n, want.ptr, dsw.ptr, sw, None))
+    sync()
+    assert_bits_equal(out.get(), want.get(), f"fused {'mean' if mean else 'sum'} n={n}")
+    assert_bits_equal(d.get(), (y - t).astype(np.float32), "stored difference")
+
+
+def test_division_by_zero_index_is_reported_as_by_ts_hip_div():
+    from gpu_util import Dev, ZeroIndex, hip, hip_check, sync
+    n = 100
+    a = np.ones(n, np.float32)
+    b = np.ones(n, np.float32)
+    b[5] = 0.0   # inside the unchecked body (< 96)
+    b[97] = 0.0  # checked tail
+    da, db, out = Dev.of(a), Dev.of(b), Dev(n)
+    zi = ZeroIndex()
+    prog = _program([da.ptr, db.ptr], [("div", 0, 1, 0.0, 1)], [(out.ptr, R0)])
+    hip_check(hip.ts_hip_map(ctypes.byref(prog), n, 96, 96, zi.ptr, None, 0, None, 0, None))
+    sync()
+    assert zi.value() == 97
+    zi.reset()
+    prog = _program([da.ptr, db.ptr], [("div", 0, 1, 0.0, 0)], [(out.ptr, R0)])  # unchecked
+    hip_check(hip.ts_hip_map(ctypes.byref(prog), n, 96, 96, zi.ptr, None, 0, None, 0, None))
+    sync()
+    assert zi.value() is None
+    assert np.isinf(out.get()[5]) and np.isinf(out.get()[97])
+
+
+def test_bad_programs_are_refused():
+    from gpu_util import Dev, hip
+    d = Dev(16)
+    bad = [
+        _program([d.ptr], [("add", 0, R0 + 1, 0.0, 0)], [(d.ptr, R0)]),    # reads a later register
+        _program([d.ptr], [("add", 0, 3, 0.0, 0)], [(d.ptr, R0)]),         # input register past n_inputs
+        _program([d.ptr], [("add", 0, 0, 0.0, 0)], [(d.ptr, R0 + 1)]),     # output of no op
+        _program([d.ptr], [("add", 0, 0, 0.0, 0)], []),                    # nothing stored, no sum
+    ]
+    for p in bad:
+        assert hip.ts_hip_map(ctypes.byref(p), 16, 16, 0, None, None, 0, None, 0, None) == 100001
+    p = _program([d.ptr], [("add", 0, 0, 0.0, 0)], [(d.ptr, R0)], reduce_reg=R0)
+    out = Dev(1)
+    assert hip.ts_hip_map(ctypes.byref(p), 16, 16, 0, None, out.ptr, 0, None, 0, None) == 100003  # no workspace
+
+
+# ---- deferred chains through the handle API ------------------------------------------------------
+
+@pytest.fixture
+def T():
+    import train_station_amd as T
+    yield T
+    T.set_fusion(True)
+    T.clear_gradients()
+
+
+def _chain(T, a, b, c, n):
+    ta, tb, tc = (T.Tensor.from_slice(v, [n]).with_requires_grad() for v in (a, b, c))
+    y = ta.add_tensor(tb).mul_tensor(tc).sub_tensor(ta.div_tensor(tc)).relu()
+    loss = y.sum()
+    loss.backward()
+    out = (loss.value(), y.data(), ta.grad_by_value().data(), tb.grad_by_value().data(),
+           tc.grad_by_value().data())
+    T.clear_gradients()
+    return out
+
+
+@pytest.mark.parametrize("n", [1003, (1 << 20) + 13])
+def test_chain_bits_with_fusion_on_and_off(T, oracle, n):
+    a, b = normal(n, 11), normal(n, 12)
+    c = uniform(n, 0.5, 2.0, 13)
+    T.set_fusion(True)
+    on = _chain(T, a, b, c, n)
+    T.set_fusion(False)
+    off = _chain(T, a, b, c, n)
+    assert on[0] == off[0], "loss"
+    for name, u, v in zip(("y", "ga", "gb", "gc"), on[1:], off[1:]):
+        assert_bits_equal(u, v, name)
+
+
+def test_chain_runs_as_few_fused_passes(T):
+    # forward: one pass computing y (stored: relu saves it) and a + b (stored:
+    # mul saves it) with the sum's first pass; backward: the scalar seed and
+    # one pass writing the three gradients.  Bytes per element: 12 read + 8
+    # written, then 16 read (y, c, a, a + b) + 12 written.
+    n = 1 << 20
+    a, b = normal(n, 21), normal(n, 22)
+    c = uniform(n, 0.5, 2.0, 23)
+    T.set_fusion(True)
+    ta, tb, tc = (T.Tensor.from_slice(v, [n]).with_requires_grad() for v in (a, b, c))
+    T.synchronize()
+    T.Profile.reset()
+    T.Profile.enable(True)
+    loss = ta.add_tensor(tb).mul_tensor(tc).sub_tensor(ta.div_tensor(tc)).relu().sum()
+    loss.backward()
+    T.synchronize()
+    T.Profile.enable(False)
+    ew = T.Profile.read(T.Profile.ELEMENTWISE)
+    red = T.Profile.read(T.Profile.REDUCTION)
+    assert red["launches"] == 0
+    assert ew["launches"] == 3, ew                      # forward pass, seed (ones), backward pass
+    per_elem = (ew["work"] - 4.0) / n
+    assert per_elem == 20.0 + 28.0, per_elem

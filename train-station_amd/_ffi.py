@@ -35,6 +35,27 @@ def _load(name: str) -> ctypes.CDLL:
 
 # --- include/ts_hip.h ------------------------------------------------------------
 
+MAP_MAX_INPUTS, MAP_MAX_OPS, MAP_MAX_OUTPUTS = 5, 11, 4
+# TS_HIP_MAP_* op codes and flags of include/ts_hip.h
+MAP_CODES = {"add": 0, "sub": 1, "mul": 2, "div": 3, "neg": 4, "relu": 5, "relu_bwd": 6, "add_s": 7, "sub_s": 8,
+             "mul_s": 9, "div_s": 10, "square": 11}
+MAP_CHECKED = 1
+
+
+class MapOp(ctypes.Structure):
+    """struct ts_hip_map_op of include/ts_hip.h"""
+    _fields_ = [("code", _c.c_uint8), ("a", _c.c_uint8), ("b", _c.c_uint8), ("flags", _c.c_uint8),
+                ("imm", _c.c_float)]
+
+
+class MapProgram(ctypes.Structure):
+    """struct ts_hip_map_program of include/ts_hip.h"""
+    _fields_ = [("inputs", VP * MAP_MAX_INPUTS), ("scalar_inputs", _c.c_uint32), ("n_inputs", _c.c_uint32),
+                ("n_ops", _c.c_uint32), ("n_outputs", _c.c_uint32), ("ops", MapOp * MAP_MAX_OPS),
+                ("outputs", VP * MAP_MAX_OUTPUTS), ("output_regs", _c.c_uint8 * MAP_MAX_OUTPUTS),
+                ("reduce_reg", _c.c_int32)]
+
+
 # name -> (restype, argtypes); every symbol declared in include/ts_hip.h
 HIP_SIGNATURES = {
     "ts_hip_initialize": (_c.c_int, []),
@@ -100,6 +121,8 @@ HIP_SIGNATURES = {
     "ts_hip_leaky_relu_backward": (_c.c_int, [VP, VP, VP, SZ, _c.c_float, VP]),
     "ts_hip_softmax_backward": (_c.c_int, [VP, VP, VP, SZ, SZ, SZ, VP]),
     "ts_hip_sum_workspace_floats": (SZ, [SZ]),
+    "ts_hip_map_workspace_floats": (SZ, [SZ]),
+    "ts_hip_map": (_c.c_int, [_c.POINTER(MapProgram), SZ, SZ, SZ, VP, VP, _c.c_int, VP, SZ, VP]),
     "ts_hip_sum": (_c.c_int, [VP, SZ, VP, VP, SZ, VP]),
     "ts_hip_mean": (_c.c_int, [VP, SZ, VP, VP, SZ, VP]),
     "ts_hip_sum_dim0_workspace_floats": (SZ, [SZ, SZ]),

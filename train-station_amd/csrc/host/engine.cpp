@@ -38,13 +38,7 @@ void accumulate_gradient(size_t id, Tensor g) {
         return;
     }
     Tensor &existing = it->second;
-    Tensor sum = Tensor::new_uninit(existing.dims());
-    const size_t n = sum.size();
-    const float *a = existing.dev(), *b = g.dev();  // runs deferred producers first
-    float *out = sum.dev_mut();
-    launch(KernelClass::Elementwise, 12.0 * n, "ts_hip_add(accumulate)",
-           [&] { return ts_hip_add(a, b, out, n, Runtime::get().stream()); });
-    existing = std::move(sum);
+    existing = add_gradients(existing, g);
 }
 
 }  // namespace
@@ -105,6 +99,15 @@ void engine_backward(Tensor &root, const Tensor *grad_output) {
             if (graph().operations.count(input_id)) worklist.push_back(input_id);
         }
     }
+    // The gradients left are the leaves'; those still deferred run now, in as
+    // few passes as they fit (they share their inputs): backward returns with
+    // every gradient computed, as the reference's does.
+    std::vector<std::shared_ptr<Allocation>> deferred;
+    for (auto &kv : graph().gradients)
+        if (kv.second.allocation() && kv.second.allocation()->map) deferred.push_back(kv.second.allocation());
+    if (root.grad_ref() && root.grad_ref()->allocation() && root.grad_ref()->allocation()->map)
+        deferred.push_back(root.grad_ref()->allocation());
+    materialize_maps(deferred);
 }
 
 }  // namespace ts

@@ -167,6 +167,7 @@ Allocation::~Allocation() { DevicePool::get().release(ptr_, rounded); }
 
 float *Allocation::get() {
     if (pending) materialize(*this);
+    else if (map) materialize_map(*this);
     DevicePool::get().note_use(ptr_);
     return ptr_;
 }
@@ -175,8 +176,10 @@ void Allocation::before_write() {
     std::vector<std::weak_ptr<Allocation>> rs;
     rs.swap(readers);
     for (auto &w : rs)
-        if (auto r = w.lock())
+        if (auto r = w.lock()) {
             if (r->pending) materialize(*r);
+            else if (r->map) materialize_map(*r);
+        }
 }
 
 // ---- profiler -----------------------------------------------------------------

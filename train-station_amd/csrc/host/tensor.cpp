@@ -6,7 +6,10 @@
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <cstring>
+#include <map>
 #include <memory>
+#include <tuple>
 #include <sstream>
 
 #include "ts_hip.h"
@@ -87,7 +90,11 @@ Tensor row_bcast(const float *m, const float *v, size_t rows, size_t cols, int o
     return out;
 }
 
+Tensor map_unary(uint8_t code, const Tensor &x, float imm);
+bool defer_ok(size_t n);
+
 Tensor neg_of(const Tensor &x) {
+    if (defer_ok(x.size())) return map_unary(TS_HIP_MAP_NEG, x, 0.0f);
     Tensor out = Tensor::new_uninit(x.dims());
     const size_t n = x.size();
     launch(KernelClass::Elementwise, 8.0 * n, "ts_hip_neg",
@@ -206,7 +213,7 @@ void add_reader(const std::shared_ptr<Allocation> &input, const std::shared_ptr<
     size_t live = 0;  // drop readers that are gone or already produced
     for (auto &w : rs) {
         auto r = w.lock();
-        if (r && r->pending) rs[live++] = w;
+        if (r && r->deferred()) rs[live++] = w;
     }
     rs.resize(live);
     rs.push_back(reader);
@@ -329,6 +336,227 @@ void materialize(Allocation &a) {
         set_pending(m, e);
     }
     if (a.pending) materialize(a);
+}
+
+// ---- deferred elementwise programs -------------------------------------------
+
+namespace {
+
+// One program under construction: its leaves and nodes, common
+// subexpressions shared (the same op on the same operands is one node).
+struct MapBuilder {
+    PendingMap p;
+    int ops = 0;
+    std::map<std::tuple<uint8_t, uint8_t, int, int, uint32_t>, int> cse;
+
+    int leaf(const std::shared_ptr<Allocation> &al, bool scalar) {
+        for (size_t k = 0; k < p.leaves.size(); ++k)
+            if (p.leaves[k] == al && (((p.scalar >> k) & 1u) != 0) == scalar)
+                for (size_t j = 0; j < p.nodes.size(); ++j)
+                    if (p.nodes[j].code == MapNode::kLeaf && p.nodes[j].a == static_cast<int>(k)) return static_cast<int>(j);
+        const int k = static_cast<int>(p.leaves.size());
+        p.leaves.push_back(al);
+        if (scalar) p.scalar |= 1u << k;
+        MapNode nd;
+        nd.a = static_cast<int16_t>(k);
+        p.nodes.push_back(nd);
+        return static_cast<int>(p.nodes.size()) - 1;
+    }
+    int op(uint8_t code, int a, int b, float imm = 0.0f, uint8_t flags = 0) {
+        if (b < 0) b = a;
+        uint32_t bits;
+        std::memcpy(&bits, &imm, 4);
+        const auto key = std::make_tuple(code, flags, a, b, bits);
+        auto it = cse.find(key);
+        if (it != cse.end()) return it->second;
+        MapNode nd;
+        nd.code = code;
+        nd.flags = flags;
+        nd.a = static_cast<int16_t>(a);
+        nd.b = static_cast<int16_t>(b);
+        nd.imm = imm;
+        p.nodes.push_back(nd);
+        ++ops;
+        const int id = static_cast<int>(p.nodes.size()) - 1;
+        cse.emplace(key, id);
+        return id;
+    }
+    // m's program merged in; returns the node of its value, which records
+    // `origin` (the allocation m was deferred for)
+    int import(const PendingMap &m, const std::shared_ptr<Allocation> &origin) {
+        std::vector<int> remap(m.nodes.size(), -1);
+        for (size_t j = 0; j < m.nodes.size(); ++j) {
+            const MapNode &nd = m.nodes[j];
+            if (nd.code == MapNode::kLeaf) {
+                remap[j] = leaf(m.leaves[nd.a], ((m.scalar >> nd.a) & 1u) != 0);
+            } else {
+                remap[j] = op(nd.code, remap[nd.a], remap[nd.b], nd.imm, nd.flags);
+                if (p.nodes[remap[j]].origin.expired() && !nd.origin.expired()) p.nodes[remap[j]].origin = nd.origin;
+            }
+        }
+        const int r = remap[m.root];
+        if (origin && p.nodes[r].code != MapNode::kLeaf) p.nodes[r].origin = origin;
+        return r;
+    }
+    // the value of `al` (n elements): its deferred program merged in, or a leaf
+    int value(const std::shared_ptr<Allocation> &al, size_t n) {
+        if (al->map && al->map->n == n) return import(*al->map, al);
+        return leaf(al, false);
+    }
+    bool fits() const {
+        return p.leaves.size() <= static_cast<size_t>(TS_HIP_MAP_MAX_INPUTS) && ops <= TS_HIP_MAP_MAX_OPS;
+    }
+};
+
+struct MapOutput {
+    std::shared_ptr<Allocation> alloc;
+    int node;
+};
+
+// Runs one program: stores `outs` (and any still-deferred origin the program
+// computes on the way that something else holds), and with sum_out set adds
+// node `reduce` up as ts_hip_sum / ts_hip_mean would.
+void launch_program(MapBuilder &b, std::vector<MapOutput> outs, int reduce = -1, float *sum_out = nullptr,
+                    bool mean = false) {
+    const size_t n = b.p.n;
+    for (size_t j = 0; j < b.p.nodes.size() && outs.size() < static_cast<size_t>(TS_HIP_MAP_MAX_OUTPUTS); ++j) {
+        auto o = b.p.nodes[j].origin.lock();
+        // still held (a saved operand, or its tensor): it may be read again,
+        // and this pass computes it anyway, so it stores it
+        if (!o || !o->map || o.use_count() <= 1) continue;
+        bool listed = false;
+        for (const MapOutput &m : outs) listed = listed || m.alloc == o;
+        if (!listed) outs.push_back({o, static_cast<int>(j)});
+    }
+    // leaves first: deferred ones run before, outside this launch's window
+    ts_hip_map_program prog{};
+    prog.n_inputs = static_cast<uint32_t>(b.p.leaves.size());
+    prog.scalar_inputs = b.p.scalar;
+    double bytes = 0.0;
+    for (size_t k = 0; k < b.p.leaves.size(); ++k) {
+        prog.inputs[k] = b.p.leaves[k]->get();
+        if (!((b.p.scalar >> k) & 1u)) bytes += 4.0 * n;
+    }
+    std::vector<int> reg(b.p.nodes.size(), -1);
+    for (size_t j = 0; j < b.p.nodes.size(); ++j) {
+        const MapNode &nd = b.p.nodes[j];
+        if (nd.code == MapNode::kLeaf) {
+            reg[j] = nd.a;
+            continue;
+        }
+        ts_hip_map_op &op = prog.ops[prog.n_ops];
+        op.code = nd.code;
+        op.a = static_cast<uint8_t>(reg[nd.a]);
+        op.b = static_cast<uint8_t>(reg[nd.b]);
+        op.flags = nd.flags;
+        op.imm = nd.imm;
+        reg[j] = TS_HIP_MAP_MAX_INPUTS + static_cast<int>(prog.n_ops);
+        ++prog.n_ops;
+    }
+    for (const MapOutput &m : outs) {
+        float *C = m.alloc->raw();
+        DevicePool::get().note_use(C);  // a step being recorded writes it on every replay
+        prog.outputs[prog.n_outputs] = C;
+        prog.output_regs[prog.n_outputs] = static_cast<uint8_t>(reg[m.node]);
+        ++prog.n_outputs;
+        bytes += 4.0 * n;
+    }
+    prog.reduce_reg = reduce >= 0 ? reg[reduce] : -1;
+    std::unique_ptr<Allocation> work;
+    size_t wsf = 0;
+    if (sum_out) {
+        wsf = ts_hip_map_workspace_floats(n);
+        work = std::make_unique<Allocation>(wsf);
+    }
+    Runtime &rt = Runtime::get();
+    launch(KernelClass::Elementwise, bytes, "ts_hip_map", [&] {
+        return ts_hip_map(&prog, n, tail8(n), tail32(n), rt.zero_index(), sum_out, mean ? 1 : 0,
+                          work ? work->get() : nullptr, wsf, S());
+    });
+    for (const MapOutput &m : outs) m.alloc->map.reset();
+}
+
+// The deferred value of `dims` computed by build(builder, operand nodes) from
+// `operands` (allocation, one-value-for-every-element); the operands' own
+// deferred programs are merged in, or, if the result would exceed the program
+// limits, run first and read as leaves.
+template <class F>
+std::shared_ptr<PendingMap> defer(size_t n, const std::vector<std::pair<std::shared_ptr<Allocation>, bool>> &operands,
+                                  F &&build) {
+    for (int attempt = 0; attempt < 2; ++attempt) {
+        MapBuilder b;
+        b.p.n = n;
+        std::vector<int> ids;
+        for (const auto &o : operands) ids.push_back(o.second ? b.leaf(o.first, true) : b.value(o.first, n));
+        b.p.root = build(b, ids);
+        if (b.fits()) return std::make_shared<PendingMap>(std::move(b.p));
+        for (const auto &o : operands) o.first->get();
+    }
+    throw Error("an elementwise program exceeds the fused pass's limits");
+}
+
+// A new tensor of `dims` holding the deferred value p.
+Tensor deferred_tensor(const std::vector<size_t> &dims, std::shared_ptr<PendingMap> p) {
+    Tensor out = Tensor::new_uninit(dims);
+    const auto &al = out.allocation();
+    for (const auto &l : p->leaves) add_reader(l, al);
+    al->map = std::move(p);
+    return out;
+}
+
+// Deferral applies to same-shape operands of at least one element with
+// fusion on.
+bool defer_ok(size_t n) { return fusion_enabled() && n > 0; }
+
+Tensor map_binary(uint8_t code, const Tensor &x, const Tensor &y, uint8_t flags = 0) {
+    auto p = defer(x.size(), {{x.allocation(), false}, {y.allocation(), false}},
+                   [&](MapBuilder &b, const std::vector<int> &v) { return b.op(code, v[0], v[1], 0.0f, flags); });
+    return deferred_tensor(x.dims(), std::move(p));
+}
+
+Tensor map_unary(uint8_t code, const Tensor &x, float imm = 0.0f) {
+    auto p = defer(x.size(), {{x.allocation(), false}},
+                   [&](MapBuilder &b, const std::vector<int> &v) { return b.op(code, v[0], -1, imm); });
+    return deferred_tensor(x.dims(), std::move(p));
+}
+
+}  // namespace
+
+void materialize_map(Allocation &a) { materialize_maps({a.shared_from_this()}); }
+
+Tensor add_gradients(const Tensor &existing, const Tensor &g) {
+    if (defer_ok(existing.size()) && existing.size() == g.size()) return map_binary(TS_HIP_MAP_ADD, existing, g);
+    return same_shape(existing.dev(), g.dev(), existing.dims(), 0);
+}
+
+void materialize_maps(const std::vector<std::shared_ptr<Allocation>> &allocs) {
+    MapBuilder group;
+    std::vector<MapOutput> outs;
+    auto flush = [&]() {
+        if (!outs.empty()) launch_program(group, outs);
+        group = MapBuilder();
+        outs.clear();
+    };
+    for (const auto &al : allocs) {
+        if (!al || !al->map) continue;
+        bool listed = false;
+        for (const MapOutput &m : outs) listed = listed || m.alloc == al;
+        if (listed) continue;
+        if (!outs.empty() && group.p.n == al->map->n && outs.size() < static_cast<size_t>(TS_HIP_MAP_MAX_OUTPUTS)) {
+            MapBuilder trial = group;
+            const int r = trial.import(*al->map, al);
+            if (trial.fits()) {
+                group = std::move(trial);
+                outs.push_back({al, r});
+                continue;
+            }
+        }
+        flush();
+        group.p.n = al->map->n;
+        const int r = group.import(*al->map, al);
+        outs.push_back({al, r});
+    }
+    flush();
 }
 
 size_t next_tensor_id() {
@@ -463,7 +691,8 @@ void Tensor::set_grad(Tensor g) {
 void Tensor::accumulate_grad(Tensor g) {
     if (!requires_grad_) return;
     if (grad_) {
-        Tensor acc = same_shape(grad_->dev(), g.dev(), grad_->dims(), 0);
+        Tensor acc = (defer_ok(size_) && grad_->size() == g.size()) ? map_binary(TS_HIP_MAP_ADD, *grad_, g)
+                                                                     : same_shape(grad_->dev(), g.dev(), grad_->dims(), 0);
         grad_ = std::make_shared<Tensor>(std::move(acc));
     } else {
         grad_ = std::make_shared<Tensor>(std::move(g));
@@ -502,6 +731,9 @@ Tensor Tensor::binary(const Tensor &o, GradFn::Kind kind) const {
         } else {  // the product had a consumer already and has now run: the kernel reads it
             out = row_bcast(mat.dev(), vec.dev(), mat.dims_[0], mat.dims_[1], 0, fuse_other);
         }
+    } else if (same && defer_ok(size_)) {  // deferred: the chain it belongs to runs as one pass
+        static const uint8_t codes[4] = {TS_HIP_MAP_ADD, TS_HIP_MAP_SUB, TS_HIP_MAP_MUL, TS_HIP_MAP_DIV};
+        out = map_binary(codes[op], *this, o, op == 3 ? TS_HIP_MAP_CHECKED : 0);
     } else if (same) {
         out = same_shape(dev(), o.dev(), dims_, op);
     } else if (is_row_broadcast(dims_, o.dims_)) {
@@ -550,8 +782,17 @@ Tensor Tensor::div_tensor(const Tensor &o) const { return binary(o, GradFn::Kind
 Tensor Tensor::scalar_op(float s, GradFn::Kind kind) const {
     if (kind == GradFn::Kind::DivScalar && s == 0.0f)  // ops/div.rs:511-514
         throw Error("Division by zero: cannot divide tensor by zero scalar");
-    Tensor out = new_uninit(dims_);
-    launch(KernelClass::Elementwise, 8.0 * size_, "scalar op", [&] {
+    Tensor out;
+    if (defer_ok(size_)) {
+        const uint8_t code = kind == GradFn::Kind::AddScalar   ? TS_HIP_MAP_ADD_S
+                             : kind == GradFn::Kind::SubScalar ? TS_HIP_MAP_SUB_S
+                             : kind == GradFn::Kind::MulScalar ? TS_HIP_MAP_MUL_S
+                                                               : TS_HIP_MAP_DIV_S;
+        out = map_unary(code, *this, s);
+    } else {
+        out = new_uninit(dims_);
+    }
+    if (!out.allocation() || !out.allocation()->map) launch(KernelClass::Elementwise, 8.0 * size_, "scalar op", [&] {
         switch (kind) {
             case GradFn::Kind::AddScalar: return ts_hip_add_scalar(dev(), s, out.dev_mut(), size_, S());
             case GradFn::Kind::SubScalar: return ts_hip_sub_scalar(dev(), s, out.dev_mut(), size_, S());
@@ -580,6 +821,8 @@ Tensor Tensor::relu() const {
     if (fused) {
         fused->relu = true;
         set_pending(out.alloc_, std::move(fused));
+    } else if (defer_ok(size_)) {
+        out = map_unary(TS_HIP_MAP_RELU, *this);
     } else {
         launch(KernelClass::Elementwise, 8.0 * size_, "ts_hip_relu",
                [&] { return ts_hip_relu(dev(), out.dev_mut(), size_, S()); });
@@ -596,9 +839,14 @@ Tensor Tensor::relu() const {
 }
 
 Tensor Tensor::pow_scalar(float e) const {
-    Tensor out = new_uninit(dims_);
-    launch(KernelClass::Elementwise, 8.0 * size_, "ts_hip_pow_scalar",
-           [&] { return ts_hip_pow_scalar(dev(), e, out.dev_mut(), size_, S()); });
+    Tensor out;
+    if (e == 2.0f && defer_ok(size_)) {  // pow.rs:124-162: x * x
+        out = map_unary(TS_HIP_MAP_SQUARE, *this);
+    } else {
+        out = new_uninit(dims_);
+        launch(KernelClass::Elementwise, 8.0 * size_, "ts_hip_pow_scalar",
+               [&] { return ts_hip_pow_scalar(dev(), e, out.dev_mut(), size_, S()); });
+    }
     if (requires_grad_ && is_grad_enabled()) {
         GradFn fn{GradFn::Kind::PowScalar};
         fn.scalar = e;
@@ -732,12 +980,32 @@ Tensor Tensor::matmul(const Tensor &o) const {
     return out;
 }
 
+namespace {
+// sum / mean of a deferred elementwise value in the pass that computes it
+// (the bits of ts_hip_sum / ts_hip_mean over the stored values); the value
+// itself is stored only when something besides its tensor holds it (a saved
+// operand), else it stays deferred.  x is the tensor's own reference.
+void fused_sum(const std::shared_ptr<Allocation> &x, float *out, bool mean) {
+    MapBuilder b;
+    b.p.n = x->map->n;
+    const int r = b.import(*x->map, x);
+    std::vector<MapOutput> outs;
+    if (x.use_count() > 1) outs.push_back({x, r});
+    else b.p.nodes[r].origin.reset();  // not stored: it stays deferred
+    launch_program(b, outs, r, out, mean);
+}
+}  // namespace
+
 Tensor Tensor::sum() const {
     Tensor out = new_uninit({1});
-    const size_t ws = ts_hip_sum_workspace_floats(size_);
-    Allocation work(ws);
-    launch(KernelClass::Reduction, 4.0 * size_ + 4.0, "ts_hip_sum",
-           [&] { return ts_hip_sum(dev(), size_, out.dev_mut(), work.get(), ws, S()); });
+    if (alloc_ && alloc_->map && fusion_enabled()) {
+        fused_sum(alloc_, out.dev_mut(), false);
+    } else {
+        const size_t ws = ts_hip_sum_workspace_floats(size_);
+        Allocation work(ws);
+        launch(KernelClass::Reduction, 4.0 * size_ + 4.0, "ts_hip_sum",
+               [&] { return ts_hip_sum(dev(), size_, out.dev_mut(), work.get(), ws, S()); });
+    }
     if (requires_grad_) {  // reductions/sum.rs:131-138 (no is_grad_enabled check)
         GradFn fn{GradFn::Kind::ReduceSum};
         fn.input_shape = dims_;
@@ -748,10 +1016,14 @@ Tensor Tensor::sum() const {
 
 Tensor Tensor::mean() const {
     Tensor out = new_uninit({1});
-    const size_t ws = ts_hip_sum_workspace_floats(size_);
-    Allocation work(ws);
-    launch(KernelClass::Reduction, 4.0 * size_ + 4.0, "ts_hip_mean",
-           [&] { return ts_hip_mean(dev(), size_, out.dev_mut(), work.get(), ws, S()); });
+    if (alloc_ && alloc_->map && fusion_enabled()) {
+        fused_sum(alloc_, out.dev_mut(), true);
+    } else {
+        const size_t ws = ts_hip_sum_workspace_floats(size_);
+        Allocation work(ws);
+        launch(KernelClass::Reduction, 4.0 * size_ + 4.0, "ts_hip_mean",
+               [&] { return ts_hip_mean(dev(), size_, out.dev_mut(), work.get(), ws, S()); });
+    }
     if (requires_grad_) {  // reductions/mean.rs:97-106
         GradFn fn{GradFn::Kind::ReduceMean};
         fn.input_shape = dims_;
@@ -954,7 +1226,10 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
             // the second one has a consumer only when both inputs are recorded.
             const SavedTensor &a = saved[0], &b = saved[1];
             const bool second = req_left && req_right;
-            if (!has_shapes) {
+            if (!has_shapes && defer_ok(n)) {  // deferred: joins the chain's pass
+                r.emplace_back(map_binary(TS_HIP_MAP_MUL, go, Tensor::from_saved(b)));
+                if (second) r.emplace_back(map_binary(TS_HIP_MAP_MUL, go, Tensor::from_saved(a)));
+            } else if (!has_shapes) {
                 Tensor ga = Tensor::new_uninit(go.dims());
                 if (second) {
                     Tensor gb = Tensor::new_uninit(go.dims());
@@ -976,7 +1251,18 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
         }
         case K::Div: {  // grad_fn/ops/div.rs:4-49
             const SavedTensor &a = saved[0], &b = saved[1];
-            if (!has_shapes) {
+            if (!has_shapes && req_left && req_right && defer_ok(n)) {  // deferred: joins the chain's pass
+                // ga = go / b; gb = neg((go * a) / (b * b)); both divisions checked
+                const Tensor ta = Tensor::from_saved(a), tb = Tensor::from_saved(b);
+                r.emplace_back(map_binary(TS_HIP_MAP_DIV, go, tb, TS_HIP_MAP_CHECKED));
+                auto p = defer(n, {{go.allocation(), false}, {ta.allocation(), false}, {tb.allocation(), false}},
+                               [](MapBuilder &m, const std::vector<int> &v) {
+                                   const int num = m.op(TS_HIP_MAP_MUL, v[0], v[1]);
+                                   const int den = m.op(TS_HIP_MAP_MUL, v[2], v[2]);
+                                   return m.op(TS_HIP_MAP_NEG, m.op(TS_HIP_MAP_DIV, num, den, 0.0f, TS_HIP_MAP_CHECKED), -1);
+                               });
+                r.emplace_back(deferred_tensor(go.dims(), std::move(p)));
+            } else if (!has_shapes) {
                 // the second gradient only when both inputs are recorded (see
                 // Mul); the kernel still checks both divisors (b, then b*b)
                 // for the reference's zero-divisor panic
@@ -1007,6 +1293,10 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
             break;
         case K::MulScalar:
         case K::DivScalar: {
+            if (defer_ok(n)) {
+                r.emplace_back(map_unary(kind == K::MulScalar ? TS_HIP_MAP_MUL_S : TS_HIP_MAP_DIV_S, go, scalar));
+                break;
+            }
             Tensor g = Tensor::new_uninit(go.dims());
             launch(KernelClass::Elementwise, 8.0 * n, "scalar grad", [&] {
                 return kind == K::MulScalar ? ts_hip_mul_scalar(go.dev(), scalar, g.dev_mut(), n, S())
@@ -1024,6 +1314,8 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
             if (fused) {  // mask it in its store
                 fused->mask = saved[0].alloc;
                 set_pending(g.allocation(), std::move(fused));
+            } else if (defer_ok(n) && saved[0].alloc) {
+                g = map_binary(TS_HIP_MAP_RELU_BWD, Tensor::from_saved(saved[0]), go);
             } else {
                 launch(KernelClass::Elementwise, 12.0 * n, "ts_hip_relu_backward", [&] {
                     return ts_hip_relu_backward(saved[0].ptr(), go.dev(), g.dev_mut(), n, S());
@@ -1033,6 +1325,14 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
             break;
         }
         case K::PowScalar: {  // grad_fn/ops/pow.rs:5-27
+            if (scalar == 2.0f && defer_ok(n)) {  // go * (2 * x): powf(x, 1) == x
+                auto p = defer(n, {{go.allocation(), false}, {saved[0].alloc, false}},
+                               [](MapBuilder &m, const std::vector<int> &v) {
+                                   return m.op(TS_HIP_MAP_MUL, v[0], m.op(TS_HIP_MAP_MUL_S, v[1], -1, 2.0f));
+                               });
+                r.emplace_back(deferred_tensor(go.dims(), std::move(p)));
+                break;
+            }
             Tensor g = Tensor::new_uninit(go.dims());
             launch(KernelClass::Elementwise, 12.0 * n, "ts_hip_pow_backward", [&] {
                 return ts_hip_pow_backward(saved[0].ptr(), go.dev(), g.dev_mut(), n, scalar, S());
@@ -1151,6 +1451,12 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
             break;
         }
         case K::ReduceSum: {  // grad_fn/reductions/sum.rs:4-16
+            if (go.size() == 1 && defer_ok(product(input_shape))) {  // every element takes go[0]
+                auto p = defer(product(input_shape), {{go.allocation(), true}},
+                               [](MapBuilder &, const std::vector<int> &v) { return v[0]; });
+                r.emplace_back(deferred_tensor(input_shape, std::move(p)));
+                break;
+            }
             Tensor g = Tensor::new_uninit(input_shape);
             launch(KernelClass::Elementwise, 4.0 * g.size(), "sum grad", [&] {
                 return go.size() == 1 ? ts_hip_fill_from_device(g.dev_mut(), go.dev(), 1.0f, 0, g.size(), S())
@@ -1161,6 +1467,14 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
         }
         case K::ReduceMean: {  // grad_fn/reductions/mean.rs:4-30
             const float base = numel > 0 ? 1.0f / static_cast<float>(numel) : 0.0f;
+            if (go.size() == 1 && defer_ok(product(input_shape))) {  // base * go[0] (one product, commutative)
+                auto p = defer(product(input_shape), {{go.allocation(), true}},
+                               [&](MapBuilder &m, const std::vector<int> &v) {
+                                   return m.op(TS_HIP_MAP_MUL_S, v[0], -1, base);
+                               });
+                r.emplace_back(deferred_tensor(input_shape, std::move(p)));
+                break;
+            }
             Tensor g = Tensor::new_uninit(input_shape);
             launch(KernelClass::Elementwise, 4.0 * g.size(), "mean grad", [&] {
                 return go.size() == 1 ? ts_hip_fill_from_device(g.dev_mut(), go.dev(), base, 1, g.size(), S())

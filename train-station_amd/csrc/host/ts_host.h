@@ -129,6 +129,33 @@ struct PendingGemm {
     bool bare() const { return !src && !bias && !mask && !relu; }
 };
 
+// A deferred elementwise value: a chain of same-shape elementwise ops (and
+// their backward formulas) recorded as a small program over leaf buffers and
+// run by ts_hip_map when the value is first needed.  An op whose operands are
+// such values extends their programs instead of launching, so a chain runs as
+// one pass that reads each leaf once and writes only what is read later.
+// Every node is one op of ts_hip.h's map set, in the reference's fp32 order,
+// so each value has the bits of the op-by-op sequence.
+struct MapNode {
+    static constexpr uint8_t kLeaf = 255;
+    uint8_t code = kLeaf;  // TS_HIP_MAP_* or kLeaf
+    uint8_t flags = 0;     // TS_HIP_MAP_CHECKED on a division checked for zero
+    int16_t a = -1, b = -1;  // operand nodes (earlier ones); a leaf: its index in leaves
+    float imm = 0.0f;
+    // the allocation this node's value was deferred for, if any: when a
+    // program computes it anyway and the allocation is still pending and held
+    // elsewhere, the same pass stores it
+    std::weak_ptr<Allocation> origin;
+};
+
+struct PendingMap {
+    size_t n = 0;  // elements
+    std::vector<std::shared_ptr<Allocation>> leaves;
+    uint32_t scalar = 0;  // bit k: leaf k is one value used for every element
+    std::vector<MapNode> nodes;  // in evaluation order
+    int root = -1;
+};
+
 // Device variant of tensor/core/allocation.rs:43-187: owns one pooled device
 // buffer; shared (Arc-like) by tensors, saved graph operands and gradients.
 struct Allocation : std::enable_shared_from_this<Allocation> {
@@ -144,6 +171,8 @@ struct Allocation : std::enable_shared_from_this<Allocation> {
     // producer that reads it, so they see the old contents.
     void before_write();
     std::shared_ptr<PendingGemm> pending;
+    std::shared_ptr<PendingMap> map;                 // deferred elementwise value
+    bool deferred() const { return pending || map; }
     std::vector<std::weak_ptr<Allocation>> readers;  // pending allocations reading this one
     size_t n = 0, rounded = 0;
 
@@ -153,6 +182,11 @@ struct Allocation : std::enable_shared_from_this<Allocation> {
 
 // Runs a's pending producer (tensor.cpp).
 void materialize(Allocation &a);
+// Runs a's deferred elementwise program (tensor.cpp).
+void materialize_map(Allocation &a);
+// Runs the deferred elementwise programs of several allocations, merged into
+// as few passes as the program limits allow (tensor.cpp).
+void materialize_maps(const std::vector<std::shared_ptr<Allocation>> &allocs);
 // Makes `out` pending on p and records it as a reader of p's inputs.
 void set_pending(const std::shared_ptr<Allocation> &out, std::shared_ptr<PendingGemm> p);
 // A new deferred product C = op(A) . op(B) for `out`, the first member of
@@ -387,6 +421,8 @@ void push_grad_enabled(bool on);    // NoGradTrack::new / with_no_grad (no_grad_
 void pop_grad_enabled();            // NoGradTrack's Drop (no_grad_track.rs:117-127)
 void set_grad_enabled(bool on);     // no_grad_track.rs:188-199: replaces the innermost state
 void clear_gradients();             // engine.rs:812-816
+// existing + g (engine.rs:514-524), deferred into the gradients' pass when fusion is on
+Tensor add_gradients(const Tensor &existing, const Tensor &g);
 bool gradients_pending();           // the gradient map holds at least one gradient
 void register_operation(size_t output_id, std::vector<size_t> input_ids, GradFn fn);
 const Tensor *accumulated_gradient(size_t id);

@@ -48,6 +48,43 @@ __device__ __forceinline__ float4 load_nt(const float4 *p) {
     return make_float4(r.x, r.y, r.z, r.w);
 }
 
+// ---- the scalar sum's partition (ts_hip_sum, and the fused sum of ts_hip_map,
+// which must give the same bits) ----------------------------------------------
+
+constexpr size_t kSumChunk = 8192;  // inputs per first-pass workgroup (minimum)
+constexpr size_t kSumMaxBlocks = 2048;
+
+inline size_t sum_blocks(size_t n) {
+    size_t b = (n + kSumChunk - 1) / kSumChunk;
+    if (b > kSumMaxBlocks) b = kSumMaxBlocks;
+    return b < 1 ? 1 : b;
+}
+
+__device__ inline double wave_sum(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Sum of a workgroup's per-thread values, returned to thread 0.
+__device__ inline double block_sum(double v) {
+    __shared__ double lds[kBlock / 64];
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) lds[wave] = v;
+    __syncthreads();
+    double r = 0.0;
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int w = 0; w < kBlock / 64; ++w) r += lds[w];
+    }
+    return r;
+}
+
+// The sum's second pass: one workgroup adds the nparts f64 partials in a fixed
+// order and writes the fp32 sum (divided by (float)n when mean) to out[0].
+int launch_sum_final(const double *partial, size_t nparts, size_t n, float *out, bool mean, hipStream_t s);
+
 // Weighted column sums out[c] = sum_r w[r] * x[r][c] (w == nullptr: plain
 // column sums), f64 partials; workspace as ts_hip_sum_dim0_workspace_floats.
 int launch_colsum(const float *x, const float *w, size_t rows, size_t cols, size_t ld, float *out,

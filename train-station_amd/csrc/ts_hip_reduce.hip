@@ -8,36 +8,6 @@
 
 namespace tship {
 
-constexpr size_t kSumChunk = 8192;  // inputs per first-pass workgroup (minimum)
-constexpr size_t kSumMaxBlocks = 2048;
-
-static size_t sum_blocks(size_t n) {
-    size_t b = (n + kSumChunk - 1) / kSumChunk;
-    if (b > kSumMaxBlocks) b = kSumMaxBlocks;
-    return b < 1 ? 1 : b;
-}
-
-__device__ inline double wave_sum(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-// Sum of a workgroup's per-thread values, returned to thread 0.
-__device__ inline double block_sum(double v) {
-    __shared__ double lds[kBlock / 64];
-    v = wave_sum(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) lds[wave] = v;
-    __syncthreads();
-    double r = 0.0;
-    if (threadIdx.x == 0) {
-#pragma unroll
-        for (int w = 0; w < kBlock / 64; ++w) r += lds[w];
-    }
-    return r;
-}
-
 // Pass 1: workgroup b sums the float4 groups b, b+G, b+2G, ... (all threads
 // of the grid stride together) and writes one f64 partial.  PROD: the terms
 // are x[i] * y[i] formed in f64 (a dot product).
@@ -86,6 +56,12 @@ __global__ __launch_bounds__(kBlock) void sum_final(const double *__restrict__ p
     }
 }
 
+int launch_sum_final(const double *partial, size_t nparts, size_t n, float *out, bool mean, hipStream_t s) {
+    if (mean) hipLaunchKernelGGL(sum_final<true>, dim3(1), dim3(kBlock), 0, s, partial, nparts, n, out);
+    else hipLaunchKernelGGL(sum_final<false>, dim3(1), dim3(kBlock), 0, s, partial, nparts, n, out);
+    return launch_status();
+}
+
 template <bool MEAN>
 static int launch_sum(const float *x, const float *y, size_t n, float *out, float *workspace, size_t ws,
                       void *stream) {
@@ -108,8 +84,7 @@ static int launch_sum(const float *x, const float *y, size_t n, float *out, floa
                            n4, partial);
     int st = launch_status();
     if (st) return st;
-    hipLaunchKernelGGL(sum_final<MEAN>, dim3(1), dim3(kBlock), 0, s, partial, blocks, n, out);
-    return launch_status();
+    return launch_sum_final(partial, blocks, n, out, MEAN, s);
 }
 
 // ---- column reduction [rows, cols] -> [cols] --------------------------------
