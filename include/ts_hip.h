@@ -88,6 +88,16 @@ int ts_hip_event_destroy(void *event);
 int ts_hip_event_record(void *event, void *stream);
 int ts_hip_event_synchronize(void *event);
 int ts_hip_event_elapsed_ms(float *ms, void *start, void *stop);
+/* Kernel-attached timing (no counterpart in the reference): between begin and
+ * end, every kernel this library launches from the calling thread carries the
+ * two events in its own dispatch -- `start` takes the first kernel's start
+ * time, `stop` each kernel's end time -- so ts_hip_event_elapsed_ms(start,
+ * stop) spans the kernels alone, without the queue time of a separately
+ * recorded event.  end stores how many kernels were stamped (0: the events
+ * were never recorded and must not be read).  One window per thread; begin
+ * while one is open replaces it. */
+int ts_hip_timing_begin(void *start, void *stop);
+int ts_hip_timing_end(int *kernels);
 /* HIP graphs (no counterpart in the reference): work issued on `stream`
  * between begin and end is recorded, not run (relaxed capture mode: the
  * caller's other HIP calls stay legal, stream synchronisation does not), then

@@ -79,6 +79,8 @@ HIP_SIGNATURES = {
     "ts_hip_event_record": (_c.c_int, [VP, VP]),
     "ts_hip_event_synchronize": (_c.c_int, [VP]),
     "ts_hip_event_elapsed_ms": (_c.c_int, [_c.POINTER(_c.c_float), VP, VP]),
+    "ts_hip_timing_begin": (_c.c_int, [VP, VP]),
+    "ts_hip_timing_end": (_c.c_int, [_c.POINTER(_c.c_int)]),
     "ts_hip_error_string": (_c.c_char_p, [_c.c_int]),
     "ts_hip_mem_info": (_c.c_int, [_c.POINTER(SZ), _c.POINTER(SZ)]),
     "ts_hip_add": (_c.c_int, [VP, VP, VP, SZ, VP]),

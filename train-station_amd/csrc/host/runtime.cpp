@@ -200,20 +200,39 @@ void *Profiler::event() {
     void *ev = nullptr;
     if (!spare_.empty()) { ev = spare_.back(); spare_.pop_back(); }
     else check(ts_hip_event_create(&ev), "ts_hip_event_create");
-    check(ts_hip_event_record(ev, Runtime::get().stream()), "ts_hip_event_record");
     return ev;
+}
+
+// A segment is a timing window of the HIP library: the kernels launched while
+// it is open carry its events in their own dispatches, so the elapsed time is
+// that of the kernels (first start to last end), not of separately queued
+// event records around them.
+void Profiler::open_segment(Segments &segs) {
+    Segment seg;
+    seg.start = event();
+    seg.stop = event();
+    segs.push_back(seg);
+    check(ts_hip_timing_begin(seg.start, seg.stop), "ts_hip_timing_begin");
+}
+
+void Profiler::close_segment(Segments &segs) {
+    if (segs.empty() || segs.back().kernels >= 0) return;
+    int n = 0;
+    check(ts_hip_timing_end(&n), "ts_hip_timing_end");
+    segs.back().kernels = n;
 }
 
 // Launches can nest: a deferred product runs when a later launch first reads
 // its result, inside that launch's window.  The innermost timed window that
-// encloses a timed launch is paused for its duration and resumed after it, so
-// each timed launch is charged its own time only.  (An untimed launch inside a
-// timed window would be charged to it; nested launches are deferred products,
-// GEMMs, so that happens only when the GEMM class is not timed.)
+// encloses a timed launch is closed for its duration and a new segment opened
+// after it, so each timed launch is charged its own kernels only.  (An
+// untimed launch inside a timed window is charged to it; nested launches are
+// deferred products, GEMMs, so that happens only when the GEMM class is not
+// timed.)
 void Profiler::pause_enclosing() {
     for (size_t i = open_.size(); i-- > 0;)
         if (open_[i].timed) {
-            open_[i].segments.back().second = event();
+            close_segment(open_[i].segments);
             return;
         }
 }
@@ -221,7 +240,7 @@ void Profiler::pause_enclosing() {
 void Profiler::resume_enclosing() {
     for (size_t i = open_.size(); i-- > 0;)
         if (open_[i].timed) {
-            open_[i].segments.push_back({event(), nullptr});
+            open_segment(open_[i].segments);
             return;
         }
 }
@@ -231,27 +250,28 @@ void Profiler::begin(KernelClass k) {
     const bool timed = (classes_ >> static_cast<int>(k)) & 1u;
     if (timed) pause_enclosing();
     Frame f{timed, {}};
-    if (timed) f.segments.push_back({event(), nullptr});
     open_.push_back(std::move(f));
+    if (timed) open_segment(open_.back().segments);
 }
 
 void Profiler::abort() {
     if (!enabled_ || open_.empty()) return;
+    close_segment(open_.back().segments);
     Frame f = std::move(open_.back());
     open_.pop_back();
     for (auto &seg : f.segments) {
-        if (seg.first) spare_.push_back(seg.first);
-        if (seg.second) spare_.push_back(seg.second);
+        spare_.push_back(seg.start);
+        spare_.push_back(seg.stop);
     }
     if (f.timed) resume_enclosing();
 }
 
 void Profiler::end(KernelClass k, double work) {
     if (!enabled_ || open_.empty()) return;
+    close_segment(open_.back().segments);
     Frame f = std::move(open_.back());
     open_.pop_back();
     if (!f.timed) return;
-    f.segments.back().second = event();
     pending_.push_back(Pending{std::move(f.segments), k, work});
     resume_enclosing();
 }
@@ -262,11 +282,13 @@ void Profiler::collect() {
     for (auto &p : pending_) {
         double ms = 0.0;
         for (auto &seg : p.segments) {
-            float part = 0.0f;
-            check(ts_hip_event_elapsed_ms(&part, seg.first, seg.second), "ts_hip_event_elapsed_ms");
-            ms += part;
-            spare_.push_back(seg.first);
-            spare_.push_back(seg.second);
+            if (seg.kernels > 0) {
+                float part = 0.0f;
+                check(ts_hip_event_elapsed_ms(&part, seg.start, seg.stop), "ts_hip_event_elapsed_ms");
+                ms += part;
+            }
+            spare_.push_back(seg.start);
+            spare_.push_back(seg.stop);
         }
         auto &t = totals_[static_cast<int>(p.k)];
         t.ms += ms;

@@ -230,7 +230,13 @@ class Profiler {
     void reset();
 
   private:
-    using Segments = std::vector<std::pair<void *, void *>>;  // (start, stop) event pairs
+    // A run of kernels timed by one pair of events carried in their dispatches
+    // (ts_hip_timing_begin/end); kernels == 0: the events were never recorded.
+    struct Segment {
+        void *start = nullptr, *stop = nullptr;
+        int kernels = -1;  // -1 while the window is open
+    };
+    using Segments = std::vector<Segment>;
     struct Pending {
         Segments segments;
         KernelClass k;
@@ -241,6 +247,8 @@ class Profiler {
         Segments segments;  // while timed
     };
     void *event();
+    void open_segment(Segments &segs);
+    void close_segment(Segments &segs);
     void pause_enclosing();
     void resume_enclosing();
     bool enabled_ = false;

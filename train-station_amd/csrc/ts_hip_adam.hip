@@ -179,10 +179,10 @@ extern "C" int ts_hip_adam_step(float *p, const float *g, float *m, float *v, fl
     const size_t blocks = (adam_threads(n, a.n4) + kBlock - 1) / kBlock;
     if (blocks > 0x7fffffffULL) return TS_HIP_EINVAL;
     if (n >= kAdamNtMin)
-        hipLaunchKernelGGL(adam_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
+        launch(adam_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
                            as_stream(stream), a);
     else
-        hipLaunchKernelGGL(adam_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
+        launch(adam_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
                            as_stream(stream), a);
     return launch_status();
 }
@@ -215,7 +215,7 @@ static int adam_multi(const ts_hip_adam_param *params, size_t count, float lr, f
     A.cf_table = cf_table;
     A.cf_slot = cf_slot;
     A.lr = lr; A.eps = eps; A.wd = weight_decay;
-    hipLaunchKernelGGL(adam_multi_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
+    launch(adam_multi_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
                        as_stream(stream), A);
     return launch_status();
 }
@@ -248,6 +248,6 @@ extern "C" int ts_hip_adam_bias_corrections(float beta1, float beta2, uint64_t f
 
 extern "C" int ts_hip_slot_advance(unsigned *slot, void *stream) {
     if (!slot) return TS_HIP_EINVAL;
-    hipLaunchKernelGGL(slot_advance_kernel, dim3(1), dim3(64), 0, as_stream(stream), slot);
+    launch(slot_advance_kernel, dim3(1), dim3(64), 0, as_stream(stream), slot);
     return launch_status();
 }

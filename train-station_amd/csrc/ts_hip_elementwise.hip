@@ -243,7 +243,7 @@ static int launch_map(const float *const *in, float *const *out, size_t n, Op op
     const size_t threads = n4 > rest ? n4 : rest;
     const size_t blocks = (threads + kBlock - 1) / kBlock;
     if (blocks > 0x7fffffffULL) return TS_HIP_EINVAL;
-    hipLaunchKernelGGL((map_kernel<Op, NT>), dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
+    launch((map_kernel<Op, NT>), dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
                        as_stream(stream), args, n, n4, op);
     return launch_status();
 }
@@ -391,11 +391,11 @@ int ts_hip_row_broadcast(int op, const float *x, const float *v, float *out, siz
     dim3 grid(gx, gy);
     hipStream_t s = as_stream(stream);
     if (vec)
-        hipLaunchKernelGGL(row_broadcast_vec4, grid, dim3(kBlock), 0, s,
+        launch(row_broadcast_vec4, grid, dim3(kBlock), 0, s,
                            reinterpret_cast<const float4 *>(x), reinterpret_cast<const float4 *>(v),
                            reinterpret_cast<float4 *>(out), a);
     else
-        hipLaunchKernelGGL(row_broadcast_scalar, grid, dim3(kBlock), 0, s, x, v, out, a);
+        launch(row_broadcast_scalar, grid, dim3(kBlock), 0, s, x, v, out, a);
     return launch_status();
 }
 

@@ -156,7 +156,7 @@ __device__ __forceinline__ float epilogue(const GemmArgs &g, float v, int i, int
     return v;
 }
 
-// Staging of one operand tile: logical [BK][R] (k-major), R = 128 or 256
+// Staging of one operand tile: logical [BK][R] (k-major), R = 64, 128 or 256
 // rows of the operand's non-k index.  KCONTIG: k is the contiguous index in
 // memory (row-major A, or B^T); otherwise the R index is contiguous.
 template <int R, int NT, bool KCONTIG>
@@ -178,49 +178,36 @@ struct Stage {
         }
     }
 
-    // interior tile, 16-byte aligned: one dwordx4 per float4
-    static __device__ __forceinline__ void load_fast(const float *__restrict__ P, int ld, int r0,
-                                                     int k0, float4 (&reg)[NF]) {
-#pragma unroll
-        for (int s = 0; s < NF; ++s) {
-            int row, kk;
-            coords(s * NT + threadIdx.x, row, kk);
-            reg[s] = KCONTIG
-                ? *reinterpret_cast<const float4 *>(P + (size_t)(r0 + row) * ld + (k0 + kk))
-                : *reinterpret_cast<const float4 *>(P + (size_t)(k0 + kk) * ld + (r0 + row));
-        }
-    }
-
-    // edge tile along M / N with every k inside: the same dwordx4 loads with
-    // the row index kept inside the operand (rows past the edge feed outputs
-    // that are never stored, so any in-bounds values serve).  Needs the
+    // a tile with every k inside: one dwordx4 per float4, the row index kept
+    // inside the operand (rows past an M / N edge feed outputs that are never
+    // stored, so any in-bounds values serve).  Needs the
     // layout of g.vec (16-byte aligned, ld % 4 == 0): for a k-contiguous
     // operand a row is clamped to rows - 1; otherwise a float4 of 4 rows
     // starts at most at (rows - 1) & ~3, which ld >= rows rounded up to 4
     // keeps inside the row.
     static __device__ __forceinline__ void load_clamped(const float *__restrict__ P, int ld, int rows, int r0,
-                                                        int k0, float4 (&reg)[NF]) {
+                                                        int k0, f4v_t (&reg)[NF]) {
 #pragma unroll
         for (int s = 0; s < NF; ++s) {
             int row, kk;
-            coords(s * NT + threadIdx.x, row, kk);
+            coords(s * NT + static_cast<int>(threadIdx.x), row, kk);
             if (KCONTIG) {
                 const int r = min(r0 + row, rows - 1);
-                reg[s] = *reinterpret_cast<const float4 *>(P + (size_t)r * ld + (k0 + kk));
+                reg[s] = *reinterpret_cast<const f4v_t *>(P + (size_t)r * ld + (k0 + kk));
             } else {
                 const int r = min(r0 + row, (rows - 1) & ~3);
-                reg[s] = *reinterpret_cast<const float4 *>(P + (size_t)(k0 + kk) * ld + r);
+                reg[s] = *reinterpret_cast<const f4v_t *>(P + (size_t)(k0 + kk) * ld + r);
             }
         }
     }
 
     // edge tile: element loads with bounds checks, zeros outside
     static __device__ __forceinline__ void load_guarded(const float *__restrict__ P, int ld, int rows,
-                                                        int K, int r0, int k0, float4 (&reg)[NF]) {
+                                                        int K, int r0, int k0, f4v_t (&reg)[NF]) {
 #pragma unroll
         for (int s = 0; s < NF; ++s) {
             int row, kk;
-            coords(s * NT + threadIdx.x, row, kk);
+            coords(s * NT + static_cast<int>(threadIdx.x), row, kk);
             float v[4];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
@@ -230,21 +217,20 @@ struct Stage {
                            ? (KCONTIG ? P[(size_t)gr * ld + gk] : P[(size_t)gk * ld + gr])
                            : 0.0f;
             }
-            reg[s] = make_float4(v[0], v[1], v[2], v[3]);
+            reg[s] = f4v_t{v[0], v[1], v[2], v[3]};
         }
     }
 
-    static __device__ __forceinline__ void store(float *S, const float4 (&reg)[NF]) {
+    static __device__ __forceinline__ void store(float *S, const f4v_t (&reg)[NF]) {
 #pragma unroll
         for (int s = 0; s < NF; ++s) {
             int row, kk;
-            coords(s * NT + threadIdx.x, row, kk);
+            coords(s * NT + static_cast<int>(threadIdx.x), row, kk);
             if (KCONTIG) {
-                const float *v = reinterpret_cast<const float *>(&reg[s]);
 #pragma unroll
-                for (int c = 0; c < 4; ++c) S[(kk + c) * R + (row ^ swz(kk + c))] = v[c];
+                for (int c = 0; c < 4; ++c) S[(kk + c) * R + (row ^ swz(kk + c))] = reg[s][c];
             } else {
-                *reinterpret_cast<float4 *>(&S[kk * R + (row ^ swz(kk))]) = reg[s];
+                *reinterpret_cast<f4v_t *>(&S[kk * R + (row ^ swz(kk))]) = reg[s];
             }
         }
     }
@@ -270,16 +256,21 @@ __device__ inline void tile_coords(int tiles_m, int tiles_n, int b, int &tm, int
 // EPI: the epilogue kind applied at the store (a separate instantiation per
 // kind, so the bare product keeps its register allocation).  PF: operand tiles
 // prefetched into registers ahead of the LDS stage (deeper for small tiles,
-// whose k-steps are too short to cover a global load).
-template <bool TA, bool TB, int BM, int BN, int WM, int WN, int EPI, int PF>
+// whose k-steps are too short to cover a global load).  VEC (operands 16-byte
+// aligned, leading dimensions % 4 == 0): the loop runs the whole k tiles with
+// dwordx4 loads whose rows are clamped into the operand (rows past an M / N
+// edge feed outputs that are never stored), and a partial last tile follows
+// it with element loads; otherwise every tile takes bounds-checked element
+// loads (zeros outside).
+template <bool TA, bool TB, int BM, int BN, int WM, int WN, int EPI, int PF, bool VEC>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
     constexpr int NT = 64 * WM * WN;
     constexpr int TMW = BM / WM, TNW = BN / WN;  // wave tile
     constexpr int FM = TMW / 32, FN = TNW / 32;  // 32x32 accumulators per wave
     using SA = Stage<BM, NT, !TA>;                // A is k-contiguous unless transposed
     using SB = Stage<BN, NT, TB>;                 // B is k-contiguous only when transposed
-    __shared__ float As[2][kBK * BM];
-    __shared__ float Bs[2][kBK * BN];
+    __shared__ __attribute__((aligned(16))) float As[2][kBK * BM];
+    __shared__ __attribute__((aligned(16))) float Bs[2][kBK * BN];
 
     // Batched form: select this workgroup's batch (uniform).  The loop is
     // unrolled with constant indices so the argument arrays stay in SGPRs.
@@ -319,18 +310,35 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
 
-    const int nk = (g.K + kBK - 1) / kBK;
-    const bool mn_inside = g.vec && (i0 + BM <= g.M) && (j0 + BN <= g.N);
-    // Register ring of PF operand tiles: tile t >= 1 is loaded into slot
-    // (t - 1) % PF and stored to LDS at step t - 1, so its global loads have
-    // PF k-steps to arrive (one step is short for a small wave tile).  The
-    // loop is unrolled PF times so the slots are static registers.
-    float4 ra[PF][SA::NF], rb[PF][SB::NF];
-    auto load = [&](int k0, float4(&a)[SA::NF], float4(&b)[SB::NF]) {
-        if (mn_inside && k0 + kBK <= g.K) {  // uniform across the workgroup
-            SA::load_fast(Ap, g.lda, i0, k0, a);
-            SB::load_fast(Bp, g.ldb, j0, k0, b);
-        } else if (g.vec && k0 + kBK <= g.K) {  // an M / N edge tile: clamped rows, still dwordx4
+    // One k tile from LDS: every operand read, then the MFMAs in k order
+    // (the reads complete in order, so each MFMA waits only for its own).
+    auto mma = [&](const float *Ac, const float *Bc) {
+        float af[kBK / 2][FM], bf[kBK / 2][FN];
+#pragma unroll
+        for (int s = 0; s < kBK / 2; ++s) {
+            const int k = 2 * s + lhalf;
+#pragma unroll
+            for (int a = 0; a < FM; ++a) af[s][a] = Ac[k * BM + ((wm * TMW + a * 32 + lrow) ^ swz(k))];
+#pragma unroll
+            for (int b = 0; b < FN; ++b) bf[s][b] = Bc[k * BN + ((wn * TNW + b * 32 + lrow) ^ swz(k))];
+        }
+#pragma unroll
+        for (int s = 0; s < kBK / 2; ++s)
+#pragma unroll
+            for (int a = 0; a < FM; ++a)
+#pragma unroll
+                for (int b = 0; b < FN; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s][a], bf[s][b], acc[a][b], 0, 0, 0);
+    };
+
+    // Every step issues the same loads (steps past the end re-load the last
+    // tile), so the compiler's load counters stay exact and the PF-deep
+    // register ring really has PF tiles of loads in flight.
+    const int nt = VEC ? g.K / kBK : (g.K + kBK - 1) / kBK;  // tiles of the loop
+    f4v_t ra[PF][SA::NF], rb[PF][SB::NF];
+    auto load = [&](int t, f4v_t(&a)[SA::NF], f4v_t(&b)[SB::NF]) {
+        const int k0 = min(t, nt - 1) * kBK;
+        if (VEC) {
             SA::load_clamped(Ap, g.lda, g.M, i0, k0, a);
             SB::load_clamped(Bp, g.ldb, g.N, j0, k0, b);
         } else {
@@ -339,56 +347,43 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
         }
     };
 
-    load(0, ra[0], rb[0]);
-    SA::store(As[0], ra[0]);
-    SB::store(Bs[0], rb[0]);
+    if (nt > 0) {
+        load(0, ra[0], rb[0]);
+        SA::store(As[0], ra[0]);
+        SB::store(Bs[0], rb[0]);
 #pragma unroll
-    for (int p = 0; p < PF; ++p)
-        if (1 + p < nk) load((1 + p) * kBK, ra[p], rb[p]);
-    __syncthreads();
+        for (int p = 0; p < PF; ++p) load(1 + p, ra[p], rb[p]);
+        __syncthreads();
 
-    for (int kt0 = 0; kt0 < nk; kt0 += PF) {
+        for (int kt0 = 0; kt0 < nt; kt0 += PF) {
 #pragma unroll
-        for (int u = 0; u < PF; ++u) {
-            const int kt = kt0 + u;
-            if (kt >= nk) break;  // uniform
-            const int cur = kt & 1;
-            // LDS[cur] holds tile kt; slot u holds tile kt+1.  Buffer cur^1
-            // was last read before the previous barrier, so it can take tile
-            // kt+1 now, and slot u then takes tile kt+1+PF.
-            if (kt + 1 < nk) {
+            for (int u = 0; u < PF; ++u) {
+                const int kt = kt0 + u;
+                if (kt >= nt) break;  // uniform
+                const int cur = kt & 1;
+                // LDS[cur] holds tile kt: its operands are read and its MFMAs
+                // issued; slot u (tile kt+1, past the end a re-load) goes to
+                // buffer cur^1, last read before the previous barrier, and
+                // slot u then takes tile kt+1+PF.  One basic block, so the
+                // scheduler can place the stores and loads in the MFMAs'
+                // shadow (a wave issues in order).
+                mma(As[cur], Bs[cur]);
                 SA::store(As[cur ^ 1], ra[u]);
                 SB::store(Bs[cur ^ 1], rb[u]);
-                if (kt + 1 + PF < nk) load((kt + 1 + PF) * kBK, ra[u], rb[u]);
+                load(kt + 1 + PF, ra[u], rb[u]);
+                __syncthreads();
             }
-            const float *Ac = As[cur];
-            const float *Bc = Bs[cur];
-#pragma unroll
-            for (int s = 0; s < kBK / 2; ++s) {
-                const int k = 2 * s + lhalf;
-                float af[FM], bf[FN];
-#pragma unroll
-                for (int a = 0; a < FM; ++a) af[a] = Ac[k * BM + ((wm * TMW + a * 32 + lrow) ^ swz(k))];
-#pragma unroll
-                for (int b = 0; b < FN; ++b) bf[b] = Bc[k * BN + ((wn * TNW + b * 32 + lrow) ^ swz(k))];
-#pragma unroll
-                for (int a = 0; a < FM; ++a)
-#pragma unroll
-                    for (int b = 0; b < FN; ++b)
-                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a], bf[b], acc[a][b], 0, 0, 0);
-            }
-            // Scheduling hint: alternate one MFMA and one LDS read across the
-            // whole k-tile, so operand reads of later k-steps issue under the
-            // MFMAs of earlier ones instead of clustering ahead of them.
-#pragma unroll
-            for (int i = 0; i < kBK / 2 * FM * FN; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
-            }
-            __syncthreads();
         }
     }
-
+    if (VEC && nt * kBK < g.K) {  // the partial last k tile (uniform)
+        f4v_t pa[SA::NF], pb[SB::NF];
+        SA::load_guarded(Ap, g.lda, g.M, g.K, i0, nt * kBK, pa);
+        SB::load_guarded(Bp, g.ldb, g.N, g.K, j0, nt * kBK, pb);
+        SA::store(As[0], pa);
+        SB::store(Bs[0], pb);
+        __syncthreads();
+        mma(As[0], Bs[0]);
+    }
     store_tile<EPI, FM, FN>(g, acc, Cp, i0 + wm * TMW, j0 + wn * TNW, lrow, lhalf);
 }
 
@@ -397,13 +392,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
 template <int BM>
 constexpr int prefetch_tiles() { return BM >= 256 ? 1 : 4; }
 
+template <int BM, int BN, int WM, int WN, int EPI, bool VEC>
+static void launch_tiles_vec(int ta, int tb, const GemmArgs &g, dim3 grid, dim3 block, hipStream_t s) {
+    constexpr int PF = prefetch_tiles<BM>();
+    if (!ta && !tb) launch((gemm_f32_mfma<false, false, BM, BN, WM, WN, EPI, PF, VEC>), grid, block, 0, s, g);
+    else if (!ta && tb) launch((gemm_f32_mfma<false, true, BM, BN, WM, WN, EPI, PF, VEC>), grid, block, 0, s, g);
+    else if (ta && !tb) launch((gemm_f32_mfma<true, false, BM, BN, WM, WN, EPI, PF, VEC>), grid, block, 0, s, g);
+    else launch((gemm_f32_mfma<true, true, BM, BN, WM, WN, EPI, PF, VEC>), grid, block, 0, s, g);
+}
+
 template <int BM, int BN, int WM, int WN, int EPI>
 static void launch_tiles_as(int ta, int tb, const GemmArgs &g, dim3 grid, dim3 block, hipStream_t s) {
-    constexpr int PF = prefetch_tiles<BM>();
-    if (!ta && !tb) hipLaunchKernelGGL((gemm_f32_mfma<false, false, BM, BN, WM, WN, EPI, PF>), grid, block, 0, s, g);
-    else if (!ta && tb) hipLaunchKernelGGL((gemm_f32_mfma<false, true, BM, BN, WM, WN, EPI, PF>), grid, block, 0, s, g);
-    else if (ta && !tb) hipLaunchKernelGGL((gemm_f32_mfma<true, false, BM, BN, WM, WN, EPI, PF>), grid, block, 0, s, g);
-    else hipLaunchKernelGGL((gemm_f32_mfma<true, true, BM, BN, WM, WN, EPI, PF>), grid, block, 0, s, g);
+    if (g.vec) launch_tiles_vec<BM, BN, WM, WN, EPI, true>(ta, tb, g, grid, block, s);
+    else launch_tiles_vec<BM, BN, WM, WN, EPI, false>(ta, tb, g, grid, block, s);
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -666,7 +667,7 @@ static void launch_dma(GemmArgs g, hipStream_t s, unsigned batches) {
     g.tiles = g.tiles_m * g.tiles_n;
     dim3 grid(static_cast<unsigned>(g.tiles) * batches);
     dim3 block(64 * WM * WN);
-    hipLaunchKernelGGL((gemm_f32_lds_dma<TA, TB, WM, WN, SCHED, EPI>), grid, block, 0, s, g);
+    launch((gemm_f32_lds_dma<TA, TB, WM, WN, SCHED, EPI>), grid, block, 0, s, g);
 }
 
 // The DMA kernel of one layout: wave grid and LDS-read order per layout, the
@@ -865,14 +866,14 @@ static int launch_skinny(int trans_a, int trans_b, size_t M, size_t N, size_t K,
     g.vec = aligned16(A) && (lda % 4 == 0);
     const dim3 grid(static_cast<unsigned>((M + 63) / 64), static_cast<unsigned>(slices)), block(64 * kSkinnyWaves);
     hipStream_t s = as_stream(stream);
-    if (!trans_a && !trans_b) hipLaunchKernelGGL((gemm_skinny<false, false>), grid, block, 0, s, g, P);
-    else if (!trans_a) hipLaunchKernelGGL((gemm_skinny<false, true>), grid, block, 0, s, g, P);
-    else if (!trans_b) hipLaunchKernelGGL((gemm_skinny<true, false>), grid, block, 0, s, g, P);
-    else hipLaunchKernelGGL((gemm_skinny<true, true>), grid, block, 0, s, g, P);
+    if (!trans_a && !trans_b) launch((gemm_skinny<false, false>), grid, block, 0, s, g, P);
+    else if (!trans_a) launch((gemm_skinny<false, true>), grid, block, 0, s, g, P);
+    else if (!trans_b) launch((gemm_skinny<true, false>), grid, block, 0, s, g, P);
+    else launch((gemm_skinny<true, true>), grid, block, 0, s, g, P);
     int st = launch_status();
     if (st != TS_HIP_OK || slices == 1) return st;
     const size_t blocks = (M * N + kBlock - 1) / kBlock;
-    hipLaunchKernelGGL(splitk_sum, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, P, slices, M, N, C, ldc,
+    launch(splitk_sum, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, P, slices, M, N, C, ldc,
                        g);
     return launch_status();
 }
@@ -950,7 +951,7 @@ static int gemm_plain(int trans_a, int trans_b, size_t M, size_t N, size_t K, co
             int status = gemm_launch(trans_a, trans_b, M, N, kc, A, lda, B, ldb, P, N, g, slices, stream);
             if (status == TS_HIP_OK) {
                 const size_t blocks = (M * N + kBlock - 1) / kBlock;
-                hipLaunchKernelGGL(splitk_sum, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, st, P, slices, M,
+                launch(splitk_sum, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, st, P, slices, M,
                                    N, C, ldc, e);
                 status = launch_status();
             }

@@ -69,7 +69,7 @@ int ts_hip_gemv(int trans, size_t rows, size_t cols, const float *A, size_t lda,
     const int vec = aligned16(A) && aligned16(x) && lda % 4 == 0;
     const size_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
     if (blocks > 0x7fffffffULL) return TS_HIP_EINVAL;
-    hipLaunchKernelGGL(gemv_rows, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, as_stream(stream), A,
+    launch(gemv_rows, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, as_stream(stream), A,
                        rows, cols, lda, x, y, vec);
     return launch_status();
 }
@@ -77,7 +77,7 @@ int ts_hip_gemv(int trans, size_t rows, size_t cols, const float *A, size_t lda,
 int ts_hip_outer(const float *a, size_t m, const float *b, size_t n, float *out, void *stream) {
     if (m == 0 || n == 0) return TS_HIP_OK;
     if (!a || !b || !out) return TS_HIP_EINVAL;
-    hipLaunchKernelGGL(outer_product, dim3(grid_for(m * n)), dim3(kBlock), 0, as_stream(stream), a, m, b, n, out);
+    launch(outer_product, dim3(grid_for(m * n)), dim3(kBlock), 0, as_stream(stream), a, m, b, n, out);
     return launch_status();
 }
 

@@ -144,7 +144,7 @@ extern "C" int ts_hip_randn(float *out, size_t n, uint64_t seed, void *stream) {
     const size_t threads = (n + (size_t(1) << log_run) - 1) >> log_run;
     const size_t blocks = (threads + kBlock - 1) / kBlock;
     if (blocks > 0x7fffffffULL) return TS_HIP_EINVAL;
-    hipLaunchKernelGGL(randn_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
+    launch(randn_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
                        as_stream(stream), out, n, seed, log_run, aligned16(out) ? 1 : 0);
     return launch_status();
 }

@@ -1,6 +1,7 @@
 // Shared helpers of the gfx950 backend (device code and launchers).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -18,6 +19,29 @@ inline int launch_status() {
 }
 
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// The calling thread's kernel timing window (ts_hip_timing_begin/end), or null.
+struct TimingWindow {
+    hipEvent_t start, stop;
+    int kernels;
+};
+TimingWindow *timing_window();
+
+// Every kernel of the library is launched through here: a plain launch, or,
+// inside a timing window, one that carries the window's events in its
+// dispatch (the first kernel the start event, each kernel the stop event).
+template <typename... KArgs, typename... Args>
+inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds, hipStream_t s,
+                   Args... args) {
+    TimingWindow *w = timing_window();
+    if (!w) {
+        kernel<<<grid, block, lds, s>>>(args...);
+        return;
+    }
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, s, w->kernels == 0 ? w->start : nullptr, w->stop, 0u,
+                          static_cast<KArgs>(args)...);
+    ++w->kernels;
+}
 
 // Number of compute units of the current device (cached per device).
 int device_cu_count();

@@ -241,14 +241,14 @@ extern "C" int ts_hip_map(const ts_hip_map_program *prog, size_t n, size_t tail_
         // several groups per thread (the prefetch overlaps them), enough
         // workgroups to fill every CU many times over
         const unsigned blocks = grid_for(threads, 4);
-        hipLaunchKernelGGL(map_program_kernel<false>, dim3(blocks), dim3(kBlock), 0, s, a);
+        launch(map_program_kernel<false>, dim3(blocks), dim3(kBlock), 0, s, a);
         return launch_status();
     }
     const size_t blocks = sum_blocks(n);
     if (!workspace || workspace_floats < 2 * blocks) return TS_HIP_EWORKSPACE;
     if ((reinterpret_cast<uintptr_t>(workspace) & 7u) != 0) return TS_HIP_EINVAL;
     a.partial = reinterpret_cast<double *>(workspace);
-    hipLaunchKernelGGL(map_program_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, a);
+    launch(map_program_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, a);
     const int st = launch_status();
     if (st != TS_HIP_OK) return st;
     return launch_sum_final(a.partial, blocks, n, sum_out, mean != 0, s);

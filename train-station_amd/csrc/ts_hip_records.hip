@@ -94,7 +94,7 @@ int ts_hip_encode_f32_records(const float *src, size_t n, void *dst, void *strea
     if (!src || !dst) return TS_HIP_EINVAL;
     // float4 loads and dword stores
     if (!aligned16(src) || (reinterpret_cast<uintptr_t>(dst) & 3u) != 0) return TS_HIP_EINVAL;
-    hipLaunchKernelGGL(encode_records, dim3(grid_for(n / 4 + 1)), dim3(kBlock), 0, as_stream(stream),
+    launch(encode_records, dim3(grid_for(n / 4 + 1)), dim3(kBlock), 0, as_stream(stream),
                        src, n, static_cast<uint32_t *>(dst));
     return launch_status();
 }
@@ -104,7 +104,7 @@ int ts_hip_decode_f32_records(const void *src, size_t n, float *dst, unsigned lo
     if (n == 0) return TS_HIP_OK;
     if (!src || !dst) return TS_HIP_EINVAL;
     if (!aligned16(dst) || (reinterpret_cast<uintptr_t>(src) & 3u) != 0) return TS_HIP_EINVAL;
-    hipLaunchKernelGGL(decode_records, dim3(grid_for(n / 4 + 1)), dim3(kBlock), 0, as_stream(stream),
+    launch(decode_records, dim3(grid_for(n / 4 + 1)), dim3(kBlock), 0, as_stream(stream),
                        static_cast<const uint32_t *>(src), n, dst, bad_index);
     return launch_status();
 }

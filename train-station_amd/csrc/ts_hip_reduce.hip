@@ -57,8 +57,8 @@ __global__ __launch_bounds__(kBlock) void sum_final(const double *__restrict__ p
 }
 
 int launch_sum_final(const double *partial, size_t nparts, size_t n, float *out, bool mean, hipStream_t s) {
-    if (mean) hipLaunchKernelGGL(sum_final<true>, dim3(1), dim3(kBlock), 0, s, partial, nparts, n, out);
-    else hipLaunchKernelGGL(sum_final<false>, dim3(1), dim3(kBlock), 0, s, partial, nparts, n, out);
+    if (mean) launch(sum_final<true>, dim3(1), dim3(kBlock), 0, s, partial, nparts, n, out);
+    else launch(sum_final<false>, dim3(1), dim3(kBlock), 0, s, partial, nparts, n, out);
     return launch_status();
 }
 
@@ -77,10 +77,10 @@ static int launch_sum(const float *x, const float *y, size_t n, float *out, floa
     double *partial = reinterpret_cast<double *>(workspace);
     size_t n4 = (aligned16(x) && (!y || aligned16(y))) ? n / 4 : 0;
     if (y)
-        hipLaunchKernelGGL(sum_partial<true>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, y, n,
+        launch(sum_partial<true>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, y, n,
                            n4, partial);
     else
-        hipLaunchKernelGGL(sum_partial<false>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, y, n,
+        launch(sum_partial<false>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, y, n,
                            n4, partial);
     int st = launch_status();
     if (st) return st;
@@ -221,13 +221,13 @@ int launch_colsum(const float *x, const float *w, size_t rows, size_t cols, size
     const size_t col_blocks = (units + kDim0Cols - 1) / kDim0Cols;
     if (col_blocks > 0x7fffffffULL) return TS_HIP_EINVAL;
     dim3 grid1(static_cast<unsigned>(col_blocks), static_cast<unsigned>(chunks));
-    if (vec && w) hipLaunchKernelGGL((dim0_partial<true, true>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
-    else if (vec) hipLaunchKernelGGL((dim0_partial<true, false>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
-    else if (w) hipLaunchKernelGGL((dim0_partial<false, true>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
-    else hipLaunchKernelGGL((dim0_partial<false, false>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
+    if (vec && w) launch((dim0_partial<true, true>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
+    else if (vec) launch((dim0_partial<true, false>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
+    else if (w) launch((dim0_partial<false, true>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
+    else launch((dim0_partial<false, false>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
     int st = launch_status();
     if (st) return st;
-    hipLaunchKernelGGL(dim0_final, dim3(static_cast<unsigned>((cols + 15) / 16)), dim3(kBlock), 0, s,
+    launch(dim0_final, dim3(static_cast<unsigned>((cols + 15) / 16)), dim3(kBlock), 0, s,
                        partial, chunks, cols, out);
     return launch_status();
 }

@@ -28,6 +28,11 @@ int device_cu_count() {
     return g_cu_count[dev];
 }
 
+static thread_local TimingWindow g_window;
+static thread_local bool g_window_open = false;
+
+TimingWindow *timing_window() { return g_window_open ? &g_window : nullptr; }
+
 // A HIP status returned to the caller is also consumed from HIP's per-thread
 // last error, so that a failure reported here is not reported again by the
 // next kernel launch's status check.
@@ -179,6 +184,20 @@ int ts_hip_event_elapsed_ms(float *ms, void *start, void *stop) {
     if (!ms || !start || !stop) return TS_HIP_EINVAL;
     return tship::status_of(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start),
                                                 reinterpret_cast<hipEvent_t>(stop)));
+}
+
+int ts_hip_timing_begin(void *start, void *stop) {
+    if (!start || !stop) return TS_HIP_EINVAL;
+    tship::g_window = {reinterpret_cast<hipEvent_t>(start), reinterpret_cast<hipEvent_t>(stop), 0};
+    tship::g_window_open = true;
+    return TS_HIP_OK;
+}
+
+int ts_hip_timing_end(int *kernels) {
+    if (!kernels) return TS_HIP_EINVAL;
+    *kernels = tship::g_window_open ? tship::g_window.kernels : 0;
+    tship::g_window_open = false;
+    return TS_HIP_OK;
 }
 
 int ts_hip_module_load_data(const void *image, void **module) {

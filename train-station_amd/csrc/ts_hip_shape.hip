@@ -129,7 +129,7 @@ int ts_hip_broadcast_copy(const float *src, const size_t *src_dims, size_t src_r
         L.dims[0] = 1;
         L.src_stride[0] = 0;
     }
-    hipLaunchKernelGGL(broadcast_gather, dim3(grid_for(n)), dim3(kBlock), 0, as_stream(stream), src, out, n, L,
+    launch(broadcast_gather, dim3(grid_for(n)), dim3(kBlock), 0, as_stream(stream), src, out, n, L,
                        scale, use_scale);
     return launch_status();
 }
@@ -178,14 +178,14 @@ int ts_hip_reduce_sum(const float *x, const size_t *dims, size_t rank, unsigned 
     if (R.n_out >= cus * 256 || R.n_red < 64) {
         const uint64_t blocks = (R.n_out + kBlock - 1) / kBlock;
         if (blocks > 0x7fffffffULL) return TS_HIP_EINVAL;
-        hipLaunchKernelGGL(reduce_axes<1>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, out, R,
+        launch(reduce_axes<1>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, out, R,
                            scale, use_scale);
     } else if (R.n_out >= cus * 4) {
         const uint64_t blocks = (R.n_out + 3) / 4;
-        hipLaunchKernelGGL(reduce_axes<64>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, out, R,
+        launch(reduce_axes<64>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, out, R,
                            scale, use_scale);
     } else {
-        hipLaunchKernelGGL(reduce_axes<256>, dim3(static_cast<unsigned>(R.n_out)), dim3(kBlock), 0, s, x, out,
+        launch(reduce_axes<256>, dim3(static_cast<unsigned>(R.n_out)), dim3(kBlock), 0, s, x, out,
                            R, scale, use_scale);
     }
     return launch_status();

@@ -63,7 +63,7 @@ int ts_hip_softmax(const float *x, float *y, size_t outer, size_t reduce, size_t
     const size_t slices = outer * inner;
     if (slices == 0 || reduce == 0) return reduce == 0 && slices ? TS_HIP_EINVAL : TS_HIP_OK;
     if (!x || !y) return TS_HIP_EINVAL;
-    hipLaunchKernelGGL(softmax_fwd, dim3(grid_for(slices)), dim3(kBlock), 0, as_stream(stream), x, y, outer,
+    launch(softmax_fwd, dim3(grid_for(slices)), dim3(kBlock), 0, as_stream(stream), x, y, outer,
                        reduce, inner);
     return launch_status();
 }
@@ -73,7 +73,7 @@ int ts_hip_softmax_backward(const float *y, const float *go, float *gi, size_t o
     const size_t slices = outer * inner;
     if (slices == 0 || reduce == 0) return TS_HIP_OK;
     if (!y || !go || !gi) return TS_HIP_EINVAL;
-    hipLaunchKernelGGL(softmax_bwd, dim3(grid_for(slices)), dim3(kBlock), 0, as_stream(stream), y, go, gi,
+    launch(softmax_bwd, dim3(grid_for(slices)), dim3(kBlock), 0, as_stream(stream), y, go, gi,
                        outer, reduce, inner);
     return launch_status();
 }
