@@ -311,7 +311,11 @@ int ts_hip_mean(const float *x, size_t n, float *out, float *workspace, size_t w
 /* Workspace (device floats) needed by ts_hip_sum_dim0 for [rows,cols]. */
 size_t ts_hip_sum_dim0_workspace_floats(size_t rows, size_t cols);
 /* reductions/sum.rs:225-306 sum_dims(&[0]) on [rows,cols] -> [cols]; the
- * bias-gradient column reduction of grad_fn/utils.rs:23-60. */
+ * bias-gradient column reduction of grad_fn/utils.rs:23-60.  Fixed order:
+ * chunks of 64 rows, each added row by row in f64 from +0, the chunk sums
+ * added in chunk order in f64 from +0, rounded to fp32 once (not the
+ * reference's fp32 row order; within 1e-4 of it, within f64 rounding of the
+ * exact sum). */
 int ts_hip_sum_dim0(const float *x, size_t rows, size_t cols, float *out, float *workspace,
                     size_t workspace_floats, void *stream);
 
@@ -374,6 +378,22 @@ size_t ts_hip_gemm_workspace_floats(size_t M, size_t N, size_t K);
 int ts_hip_gemm_fused(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A, size_t lda,
                       const float *B, size_t ldb, const float *bias, int relu, const float *mask, float *C,
                       size_t ldc, float *workspace, size_t workspace_floats, void *stream);
+
+/* The weight gradient of a linear layer together with its bias gradient (no
+ * counterpart in the reference, which reduces the bias gradient in a pass of
+ * its own: grad_fn/ops/add.rs:4-28 through reduce_gradient_to_shape,
+ * grad_fn/utils.rs:23-60, i.e. sum_dims(&[0]) of reductions/sum.rs:225-306):
+ *   C[M,N] = op(A)[M,K] . B[K,N]   as ts_hip_gemm(trans_a, 0, ...) computes it
+ *   colsum[n] = sum over k of B[k*ldb + n]   with the bits of ts_hip_sum_dim0
+ * With trans_a == 1 (dW = X^T . dY) the product's own workgroups add B's
+ * columns from the tiles they stage, so dY is read once; other shapes take a
+ * column-sum pass after the product.  M == 0 gives the column sums alone.
+ * Workspace as ts_hip_gemm_colsum_workspace_floats (8-byte aligned; NULL:
+ * taken from the stream-ordered allocator). */
+size_t ts_hip_gemm_colsum_workspace_floats(int trans_a, size_t M, size_t N, size_t K);
+int ts_hip_gemm_colsum(int trans_a, size_t M, size_t N, size_t K, const float *A, size_t lda, const float *B,
+                       size_t ldb, float *C, size_t ldc, float *colsum, float *workspace, size_t workspace_floats,
+                       void *stream);
 
 /* Batched C[b] = op(A[b]) . op(B[b]) (matmul/mod.rs:634-760 batched_matmul and
  * the batched backward of grad_fn/ops/matmul.rs:150-219) on the same MFMA

@@ -230,6 +230,39 @@ def sum_dim0_f64(x):
     return out
 
 
+# The device's column-sum order (ts_hip_sum_dim0, and the bias gradient the
+# weight-gradient product writes alongside it): chunks of 64 rows, each added
+# row by row; groups of 8 consecutive chunk sums added in chunk order; the
+# group sums added in group order -- every sum in f64 from +0 -- and one
+# rounding to fp32.  Its bits are the device's; the value is the reference's
+# sum_dims(&[0]) (reductions/sum.rs:225-306) to within the f64 rounding of the
+# partials, far inside the 1e-4 the reference's own fp32 row order allows.
+COLSUM_ROWS = 64
+COLSUM_GROUP = 8
+
+
+def sum_dim0_chunked(x, weights=None):
+    """Column sums (weights: row r scaled by weights[r] in f64, the transposed
+    matrix-vector product) in the device's fixed order; fp32 result."""
+    x = _f32(x)
+    rows, cols = x.shape
+    w = None if weights is None else np.asarray(weights, dtype=np.float32).astype(np.float64)
+    chunks = []
+    for c0 in range(0, rows, COLSUM_ROWS):
+        s = np.zeros(cols, dtype=np.float64)
+        for r in range(c0, min(c0 + COLSUM_ROWS, rows)):
+            row = x[r].astype(np.float64)
+            s = s + (row if w is None else w[r] * row)
+        chunks.append(s)
+    total = np.zeros(cols, dtype=np.float64)
+    for g0 in range(0, len(chunks), COLSUM_GROUP):
+        g = np.zeros(cols, dtype=np.float64)
+        for s in chunks[g0:g0 + COLSUM_GROUP]:
+            g = g + s
+        total = total + g
+    return total.astype(np.float32)
+
+
 # Products of at least this many multiply-adds take numpy's float64 matmul
 # (multi-threaded BLAS) instead of the C triple loop: both accumulate exactly
 # representable f32 products in f64, differing only in f64 summation order

@@ -266,3 +266,55 @@ def test_two_fused_chains_on_one_product_run_it_once(fusion):
         out[on] = vals
     for name, u, v in zip(("relu(h+b1)", "relu(h+b2)", "h+b1", "h"), out[True], out[False]):
         assert_bits_equal(u, v, name)
+
+
+@pytest.mark.parametrize("widths,batch", [([784, 1024, 10], 1024), ([256, 512, 512, 128], 1024), ([64, 96, 48], 33)])
+def test_bias_gradients_come_out_of_the_weight_products(fusion, widths, batch):
+    """With fusion on, each bias gradient (the column sum of the layer's
+    output gradient, grad_fn/utils.rs:23-60) is written by the dW product that
+    reads the same rows: no reduction launches in backward, the same GEMM
+    launches, and the bits of the separate column sum."""
+    T = fusion
+    grads, counts = {}, {}
+    for on in (True, False):
+        T.set_fusion(on)
+        ps, x, t = _mlp(T, widths, batch, 11)
+        h = x
+        n = len(ps) // 2
+        for i in range(n):
+            h = h.matmul(ps[2 * i]).add_tensor(ps[2 * i + 1])
+            if i < n - 1:
+                h = h.relu()
+        loss = h.sub_tensor(t).pow_scalar(2.0).mean()
+        loss.value()
+        T.synchronize()
+        T.Profile.reset()
+        T.Profile.enable(True)
+        loss.backward()
+        T.synchronize()
+        T.Profile.enable(False)
+        counts[on] = (T.Profile.read(T.Profile.GEMM)["launches"], T.Profile.read(T.Profile.REDUCTION)["launches"])
+        grads[on] = [p.grad_by_value().data() for p in ps]
+        T.clear_gradients()
+    for i, (a, b) in enumerate(zip(grads[True], grads[False])):
+        assert_bits_equal(a, b, f"grad {i}")
+    n = len(widths) - 1
+    assert counts[True] == (counts[False][0], 0), counts
+    assert counts[False][1] == n, counts
+
+
+def test_bias_gradient_without_a_weight_product_runs_on_its_own(fusion):
+    # W is constant: no dW product reads the rows, so the deferred column sum
+    # runs by itself at the end of backward, with the same bits
+    T = fusion
+    vals = {}
+    for on in (True, False):
+        T.set_fusion(on)
+        x = T.Tensor.from_slice(normal((300, 70), 12), [300, 70])
+        w = T.Tensor.from_slice(normal((70, 40), 13), [70, 40])
+        b = T.Tensor.from_slice(normal(40, 14), [40]).with_requires_grad()
+        loss = x.matmul(w).add_tensor(b).relu().sum()
+        loss.backward()
+        vals[on] = b.grad_by_value().data()
+        T.clear_gradients()
+    assert_bits_equal(vals[True], vals[False], "bias grad")

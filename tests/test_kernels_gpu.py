@@ -186,6 +186,7 @@ def test_sum_dim0(oracle, rows, cols):
     want = oracle.sum_dim0_f64(x)
     got = do.get()
     assert max_rel(got, want) <= 1e-6
+    assert_bits_equal(got, oracle.sum_dim0_chunked(x), f"sum_dim0 {rows}x{cols}")   # the fixed order
     if rows * cols <= 1 << 16:
         assert max_rel(got, oracle.sum_dim0(x)) <= 1e-4   # the reference's fp32 row order
 

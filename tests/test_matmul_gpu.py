@@ -78,6 +78,9 @@ def test_gemv_both_orientations(rows, cols):
         check(hip.ts_hip_gemv(trans, rows, cols, dA.ptr, cols, dx.ptr, dy.ptr, dw.ptr, ws, None))
         sync()
         assert max_rel(dy.get(), want) < 1e-6, (trans, rows, cols)
+        if trans:  # the weighted column sum: the fixed chunk order, bit for bit
+            import oracle
+            assert_bits_equal(dy.get(), oracle.sum_dim0_chunked(A, x), f"gemv^T {rows}x{cols}")
 
 
 def test_dot_and_outer():

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import assert_bits_equal, golden, max_rel, normal, uniform
+from conftest import assert_bits_equal, bits, golden, max_rel, normal, uniform
 
 SPECIAL = np.array([0.0, -0.0, 1.0, -1.0, 1e-45, -1e-45, 1e-38, 3.4e38, -3.4e38, np.inf, -np.inf,
                     0.5, 2.0, 1e30, -1e-30, 7.0], dtype=np.float32)
@@ -147,6 +147,59 @@ def test_sum_dim0_against_torch(oracle):
     assert max_rel(oracle.sum_dim0_f64(x), want) < 1e-12
     ints = np.arange(12, dtype=np.float32).reshape(4, 3)
     assert oracle.sum_dim0(ints).tolist() == [18.0, 22.0, 26.0]
+
+
+def test_sum_dim0_chunked_order(oracle):
+    """The device's column-sum order, pinned by what fixes it independently:
+    a brute-force pure-Python restatement on small inputs (chunk sums from
+    +0 in row order, groups of 8 chunk sums, then the groups), exact integer
+    sums, the f64 sum to within rounding, and the special values (all -0
+    gives +0; a row past a chunk boundary starts a new chunk, which changes
+    the bits of a cancelling sum)."""
+    def brute(x, w=None):
+        rows, cols = x.shape
+        out = []
+        for c in range(cols):
+            chunk_sums = []
+            for c0 in range(0, rows, oracle.COLSUM_ROWS):
+                s = 0.0
+                for r in range(c0, min(c0 + oracle.COLSUM_ROWS, rows)):
+                    s += (1.0 if w is None else float(w[r])) * float(x[r, c])
+                chunk_sums.append(s)
+            total = 0.0
+            for g0 in range(0, len(chunk_sums), oracle.COLSUM_GROUP):
+                grp = 0.0
+                for s in chunk_sums[g0:g0 + oracle.COLSUM_GROUP]:
+                    grp += s
+                total += grp
+            out.append(total)
+        return np.array(out, dtype=np.float64).astype(np.float32)
+
+    for rows, cols, seed in ((1, 3, 1), (63, 5, 2), (64, 4, 3), (65, 7, 4), (200, 9, 5), (1100, 3, 6)):
+        x = normal((rows, cols), seed)
+        w = normal(rows, seed + 50)
+        assert bits(oracle.sum_dim0_chunked(x)).tolist() == bits(brute(x)).tolist()
+        assert bits(oracle.sum_dim0_chunked(x, w)).tolist() == bits(brute(x, w)).tolist()
+        assert max_rel(oracle.sum_dim0_chunked(x), oracle.sum_dim0_f64(x)) < 1e-6
+    ints = np.arange(12, dtype=np.float32).reshape(4, 3)
+    assert oracle.sum_dim0_chunked(ints).tolist() == [18.0, 22.0, 26.0]
+    negz = np.full((130, 2), -0.0, np.float32)
+    assert bits(oracle.sum_dim0_chunked(negz)).tolist() == [0, 0]
+    # 1 + 2^-30 * 64 rows then -1: chunked, the small terms are kept in the
+    # first chunk's f64 sum; a flat fp32 sum would lose them
+    x = np.zeros((65, 1), np.float32)
+    x[0, 0] = 1.0
+    x[1:64, 0] = 2.0 ** -30
+    x[64, 0] = -1.0
+    assert float(oracle.sum_dim0_chunked(x)[0]) == np.float32(63 * 2.0 ** -30)
+    # 10 chunks: 1, seven zeros, then 2^60 and -2^60.  Groups of 8: the first
+    # group is 1, the second 2^60 - 2^60 = 0, total 1; chunk by chunk the 1
+    # would be lost in 1 + 2^60 (f64) and the total would be 0
+    x = np.zeros((10 * 64, 1), np.float32)
+    x[0, 0] = 1.0
+    x[64 * 8, 0] = 2.0 ** 60
+    x[64 * 9, 0] = -(2.0 ** 60)
+    assert float(oracle.sum_dim0_chunked(x)[0]) == 1.0
 
 
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])

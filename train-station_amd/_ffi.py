@@ -134,6 +134,8 @@ HIP_SIGNATURES = {
     "ts_hip_gemm_fused": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, _c.c_int, VP, VP, SZ,
                                      VP, SZ, VP]),
     "ts_hip_gemm_noalloc": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, SZ, VP]),
+    "ts_hip_gemm_colsum_workspace_floats": (SZ, [_c.c_int, SZ, SZ, SZ]),
+    "ts_hip_gemm_colsum": (_c.c_int, [_c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, SZ, VP, VP, SZ, VP]),
     "ts_hip_gemm_workspace_floats": (SZ, [SZ, SZ, SZ]),
     "ts_hip_gemm_batched": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, SZ, SZ,
                                        _c.POINTER(SZ), _c.POINTER(SZ), _c.POINTER(SZ), SZ, VP]),

@@ -108,6 +108,11 @@ void engine_backward(Tensor &root, const Tensor *grad_output) {
     if (root.grad_ref() && root.grad_ref()->allocation() && root.grad_ref()->allocation()->map)
         deferred.push_back(root.grad_ref()->allocation());
     materialize_maps(deferred);
+    // and the column sums (bias gradients) no weight-gradient product produced
+    for (auto &kv : graph().gradients)
+        if (kv.second.allocation() && kv.second.allocation()->colsum) kv.second.allocation()->get();
+    if (root.grad_ref() && root.grad_ref()->allocation() && root.grad_ref()->allocation()->colsum)
+        root.grad_ref()->allocation()->get();
 }
 
 }  // namespace ts

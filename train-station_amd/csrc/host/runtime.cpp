@@ -168,6 +168,7 @@ Allocation::~Allocation() { DevicePool::get().release(ptr_, rounded); }
 float *Allocation::get() {
     if (pending) materialize(*this);
     else if (map) materialize_map(*this);
+    else if (colsum) materialize_colsum(*this);
     DevicePool::get().note_use(ptr_);
     return ptr_;
 }
@@ -179,6 +180,7 @@ void Allocation::before_write() {
         if (auto r = w.lock()) {
             if (r->pending) materialize(*r);
             else if (r->map) materialize_map(*r);
+            else if (r->colsum) materialize_colsum(*r);
         }
 }
 

@@ -148,6 +148,8 @@ Tensor reduce_axes(const float *x, const std::vector<size_t> &dims, unsigned mas
     return out;
 }
 
+void add_reader(const std::shared_ptr<Allocation> &input, const std::shared_ptr<Allocation> &reader);
+
 // reduce_gradient_to_shape (grad_fn/utils.rs:23-60): sum over the leading axes
 // broadcasting added and over the axes broadcast from size 1, as one
 // reduction (the reference chains sum_dims calls; the sums agree to
@@ -158,6 +160,15 @@ Tensor reduce_to(const Tensor &g, const std::vector<size_t> &target) {
     if (gd.size() == 2 && target.size() == 1 && target[0] == gd[1]) {
         const size_t rows = gd[0], cols = gd[1];
         Tensor out = Tensor::new_uninit({cols});
+        if (fusion_enabled() && rows && cols && g.allocation()) {  // deferred: a bias gradient, see PendingColsum
+            auto p = std::make_shared<PendingColsum>();
+            p->src = g.allocation();
+            p->rows = rows;
+            p->cols = cols;
+            add_reader(p->src, out.allocation());
+            out.allocation()->colsum = std::move(p);
+            return out;
+        }
         const size_t ws = ts_hip_sum_dim0_workspace_floats(rows, cols);
         Allocation work(ws);
         launch(KernelClass::Reduction, 4.0 * rows * cols + 4.0 * cols, "ts_hip_sum_dim0", [&] {
@@ -230,6 +241,18 @@ void set_pending(const std::shared_ptr<Allocation> &out, std::shared_ptr<Pending
     add_reader(p->bias, out);
     add_reader(p->mask, out);
     out->pending = std::move(p);
+}
+
+void materialize_colsum(Allocation &a) {
+    const std::shared_ptr<PendingColsum> p = std::move(a.colsum);
+    a.colsum.reset();
+    const float *x = p->src->get();
+    const size_t rows = p->rows, cols = p->cols;
+    const size_t ws = ts_hip_sum_dim0_workspace_floats(rows, cols);
+    Allocation work(ws);
+    launch(KernelClass::Reduction, 4.0 * rows * cols + 4.0 * cols, "ts_hip_sum_dim0", [&] {
+        return ts_hip_sum_dim0(x, rows, cols, a.raw(), work.get(), ws, S());
+    });
 }
 
 std::shared_ptr<PendingGemm> new_product(const std::shared_ptr<Allocation> &out) {
@@ -1377,10 +1400,36 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
                 }
                 if (req_right) {  // a[M,Kd]^T . go[M,N] -> [Kd,N]
                     Tensor t = Tensor::new_uninit({Kd, N});
-                    launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm(dW)", [&] {
-                        return gemm2d(1, 0, Kd, N, M, a.ptr(), Kd, go.dev(), N, nullptr, false, nullptr,
-                                      t.dev_mut(), N);
-                    });
+                    // A bias gradient still waiting to sum go's rows (the
+                    // add before this product, grad_fn/ops/add.rs:4-28)
+                    // comes out of this product: go is read once for both.
+                    std::shared_ptr<Allocation> db;
+                    if (fusion_enabled() && go.allocation())
+                        for (auto &w : go.allocation()->readers) {
+                            auto r = w.lock();
+                            if (r && r->colsum && r->colsum->src == go.allocation() && r->colsum->rows == M &&
+                                r->colsum->cols == N) {
+                                db = r;
+                                break;
+                            }
+                        }
+                    if (db) {
+                        db->colsum.reset();
+                        const float *A = a.ptr(), *B = go.dev();
+                        float *C = t.dev_mut();
+                        const size_t ws = ts_hip_gemm_colsum_workspace_floats(1, Kd, N, M);
+                        std::unique_ptr<Allocation> work;  // from the pool: the launch allocates nothing
+                        if (ws) work = std::make_unique<Allocation>(ws);
+                        launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm_colsum(dW, db)", [&] {
+                            return ts_hip_gemm_colsum(1, Kd, N, M, A, Kd, B, N, C, N, db->raw(),
+                                                      work ? work->get() : nullptr, ws, S());
+                        });
+                    } else {
+                        launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm(dW)", [&] {
+                            return gemm2d(1, 0, Kd, N, M, a.ptr(), Kd, go.dev(), N, nullptr, false, nullptr,
+                                          t.dev_mut(), N);
+                        });
+                    }
                     gr = std::move(t);
                 }
             } else {  // batched (:150-219): go . B^T and A^T . go per batch, reduced to the operand shapes

@@ -156,6 +156,17 @@ struct PendingMap {
     int root = -1;
 };
 
+// A deferred column sum out[n] = sum over r of src[r][n] of a [rows, cols]
+// buffer: the bias gradient, reduce_to [rows, cols] -> [cols].  It runs as
+// ts_hip_sum_dim0 when first read, unless the weight-gradient product that
+// reads the same rows runs first: that product writes it too
+// (ts_hip_gemm_colsum), so the rows are read once for both.  Same bits either
+// way.
+struct PendingColsum {
+    std::shared_ptr<Allocation> src;
+    size_t rows = 0, cols = 0;
+};
+
 // Device variant of tensor/core/allocation.rs:43-187: owns one pooled device
 // buffer; shared (Arc-like) by tensors, saved graph operands and gradients.
 struct Allocation : std::enable_shared_from_this<Allocation> {
@@ -172,7 +183,8 @@ struct Allocation : std::enable_shared_from_this<Allocation> {
     void before_write();
     std::shared_ptr<PendingGemm> pending;
     std::shared_ptr<PendingMap> map;                 // deferred elementwise value
-    bool deferred() const { return pending || map; }
+    std::shared_ptr<PendingColsum> colsum;           // deferred column sum
+    bool deferred() const { return pending || map || colsum; }
     std::vector<std::weak_ptr<Allocation>> readers;  // pending allocations reading this one
     size_t n = 0, rounded = 0;
 
@@ -184,6 +196,8 @@ struct Allocation : std::enable_shared_from_this<Allocation> {
 void materialize(Allocation &a);
 // Runs a's deferred elementwise program (tensor.cpp).
 void materialize_map(Allocation &a);
+// Runs a's deferred column sum (tensor.cpp).
+void materialize_colsum(Allocation &a);
 // Runs the deferred elementwise programs of several allocations, merged into
 // as few passes as the program limits allow (tensor.cpp).
 void materialize_maps(const std::vector<std::shared_ptr<Allocation>> &allocs);

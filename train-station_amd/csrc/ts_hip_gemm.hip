@@ -82,6 +82,16 @@ struct GemmArgs {
     const float *bias;
     const float *mask;
     int relu;
+    // Column sums of B (trans_b == 0; the bias gradient beside a weight
+    // gradient) in the column sum's fixed order.  The MFMA kernels write the
+    // sum of each chunk of kColsumRows rows to colsum_part[chunk][n] (f64)
+    // from the B tiles they stage anyway -- chunk c by the workgroups of tile
+    // row c % tiles_m, so the work is spread over the grid -- and a pass after
+    // the product adds the chunks into colsum[n]; the skinny kernel's slice sum
+    // adds B's columns in a workgroup of its own.  Null: none.
+    float *colsum;
+    double *colsum_part;
+    int kslice;  // skinny: k rows per slice
 };
 
 // Store of a wave's FM x FN accumulator blocks, the wave tile's corner at
@@ -262,7 +272,7 @@ __device__ inline void tile_coords(int tiles_m, int tiles_n, int b, int &tm, int
 // edge feed outputs that are never stored), and a partial last tile follows
 // it with element loads; otherwise every tile takes bounds-checked element
 // loads (zeros outside).
-template <bool TA, bool TB, int BM, int BN, int WM, int WN, int EPI, int PF, bool VEC>
+template <bool TA, bool TB, int BM, int BN, int WM, int WN, int EPI, int PF, bool VEC, bool CS = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
     constexpr int NT = 64 * WM * WN;
     constexpr int TMW = BM / WM, TNW = BN / WN;  // wave tile
@@ -309,6 +319,24 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
         for (int b = 0; b < FN; ++b)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+    // CS: the chunk sums of B's columns (GemmArgs::colsum_part) by the first
+    // BN threads, one column each, from the B tiles in LDS; chunk c (four k
+    // tiles) by the workgroups of tile row c % tiles_m.
+    static_assert(!CS || !TB, "column sums of B need trans_b == 0");
+    const bool cs_thread = CS && static_cast<int>(threadIdx.x) < BN;
+    const int cs_c = static_cast<int>(threadIdx.x) % BN;
+    double cs_s = 0.0;
+    auto cs_mine = [&](int kt) { return ((kt >> 2) % g.tiles_m) == tm; };  // uniform
+    auto cs_flush = [&](int chunk) {
+        if (j0 + cs_c < g.N) g.colsum_part[(size_t)chunk * g.N + j0 + cs_c] = cs_s;
+        cs_s = 0.0;
+    };
+    auto cs_tile = [&](const float *Bc, int kt) {
+#pragma unroll
+        for (int k = 0; k < kBK; ++k) cs_s += (double)Bc[k * BN + (cs_c ^ swz(k))];
+        if ((kt & 3) == 3) cs_flush(kt >> 2);
+    };
 
     // One k tile from LDS: every operand read, then the MFMAs in k order
     // (the reads complete in order, so each MFMA waits only for its own).
@@ -368,6 +396,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
                 // scheduler can place the stores and loads in the MFMAs'
                 // shadow (a wave issues in order).
                 mma(As[cur], Bs[cur]);
+                if (cs_thread && cs_mine(kt)) cs_tile(Bs[cur], kt);
                 SA::store(As[cur ^ 1], ra[u]);
                 SB::store(Bs[cur ^ 1], rb[u]);
                 load(kt + 1 + PF, ra[u], rb[u]);
@@ -383,6 +412,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
         SB::store(Bs[0], pb);
         __syncthreads();
         mma(As[0], Bs[0]);
+        if (cs_thread && cs_mine(nt)) cs_tile(Bs[0], nt);  // zeros past K add nothing
+    }
+    if (CS) {  // the last chunk, unless a tile ended exactly on it
+        const int last = (g.K - 1) / kBK;
+        if (cs_thread && cs_mine(last) && (last & 3) != 3) cs_flush(last >> 2);
     }
     store_tile<EPI, FM, FN>(g, acc, Cp, i0 + wm * TMW, j0 + wn * TNW, lrow, lhalf);
 }
@@ -395,6 +429,10 @@ constexpr int prefetch_tiles() { return BM >= 256 ? 1 : 4; }
 template <int BM, int BN, int WM, int WN, int EPI, bool VEC>
 static void launch_tiles_vec(int ta, int tb, const GemmArgs &g, dim3 grid, dim3 block, hipStream_t s) {
     constexpr int PF = prefetch_tiles<BM>();
+    if (g.colsum && ta && !tb) {  // dW with db (no epilogue)
+        launch((gemm_f32_mfma<true, false, BM, BN, WM, WN, kEpiNone, PF, VEC, true>), grid, block, 0, s, g);
+        return;
+    }
     if (!ta && !tb) launch((gemm_f32_mfma<false, false, BM, BN, WM, WN, EPI, PF, VEC>), grid, block, 0, s, g);
     else if (!ta && tb) launch((gemm_f32_mfma<false, true, BM, BN, WM, WN, EPI, PF, VEC>), grid, block, 0, s, g);
     else if (ta && !tb) launch((gemm_f32_mfma<true, false, BM, BN, WM, WN, EPI, PF, VEC>), grid, block, 0, s, g);
@@ -508,7 +546,7 @@ struct DmaStage {
 // 256x256 tiles, WM x WN waves.  SCHED 1 spreads the next step pair's LDS
 // reads over the current pair's MFMAs; SCHED 0 issues them as one group
 // ahead of the MFMAs (measured per layout, see the launcher).
-template <bool TA, bool TB, int WM, int WN, int SCHED, int EPI>
+template <bool TA, bool TB, int WM, int WN, int SCHED, int EPI, bool CS>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_lds_dma(GemmArgs g) {
     constexpr int BM = 256, BN = 256, NW = WM * WN;
     constexpr int TMW = BM / WM, TNW = BN / WN, FM = TMW / 32, FN = TNW / 32, PAIRS = kBK / 4;
@@ -553,6 +591,23 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_lds_dma(GemmArgs g) {
         for (int b = 0; b < FN; ++b)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+    // CS: the chunk sums of B's columns (GemmArgs::colsum_part) by the first
+    // four waves, one column each, from the B tiles in LDS; chunk c (four k
+    // tiles) by the workgroups of tile row c % tiles_m.
+    static_assert(!CS || !TB, "column sums of B need trans_b == 0");
+    const bool cs_wave = CS && wave < 4;  // uniform per wave
+    const int cs_c = threadIdx.x & 255;
+    double cs_s = 0.0;
+    auto cs_mine = [&](int kt) { return ((kt >> 2) % g.tiles_m) == tm; };  // uniform
+    auto cs_rows = [&](const float *S, int k0, int k1) {
+#pragma unroll
+        for (int k = k0; k < k1; ++k) cs_s += (double)S[k * 256 + ((((cs_c >> 2) ^ dswz(k)) << 2) | (cs_c & 3))];
+    };
+    auto cs_flush = [&](int chunk) {
+        if (j0 + cs_c < g.N) g.colsum_part[(size_t)chunk * g.N + j0 + cs_c] = cs_s;
+        cs_s = 0.0;
+    };
 
     const int nfull = g.K / kBK;  // whole k tiles; a partial one is done after the loop
     auto dma = [&](int kt, int buf) {
@@ -608,6 +663,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_lds_dma(GemmArgs g) {
             mm(F[j & 1]);
             order();
             __builtin_amdgcn_sched_barrier(0);
+            if (cs_wave && cs_mine(kt)) {  // this tile's rows, before the barrier that frees its buffer
+                cs_rows(Bs[cur], 4 * j, 4 * j + 4);
+                if (j == PAIRS - 2) {
+                    cs_rows(Bs[cur], 4 * j + 4, kBK);
+                    if ((kt & 3) == 3) cs_flush(kt >> 2);
+                }
+            }
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
@@ -634,8 +696,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_lds_dma(GemmArgs g) {
             rd(buf, j, F[0]);
             mm(F[0]);
         }
+        if (cs_wave && cs_mine(nfull)) cs_rows(Bs[buf], 0, kBK);  // zeros past K add nothing
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA outstanding at exit
+    if (CS) {  // the last chunk, unless the loop ended exactly on it
+        const int last = (g.K - 1) / kBK;
+        if (cs_wave && cs_mine(last) && !(last < nfull && (last & 3) == 3)) cs_flush(last >> 2);
+    }
 
     store_tile<EPI, FM, FN>(g, acc, Cp, i0 + wm * TMW, j0 + wn * TNW, lrow, lhalf);
 }
@@ -647,6 +714,46 @@ __global__ __launch_bounds__(kBlock) void splitk_sum(const float *__restrict__ P
                                                      float *__restrict__ C, size_t ldc, GemmArgs e) {
     const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
     const size_t mn = M * N;
+    if (e.colsum && blockIdx.x == gridDim.x - 1) {
+        // The skinny product's column sums of B (N <= 16), in the column sum's
+        // order, by the workgroup past the product: in rounds of 16 chunks,
+        // thread (chunk lane q, column j) adds its chunk's rows (all loaded at
+        // once), then the first lane adds the round's two groups of chunk sums
+        // in order.
+        constexpr int R = static_cast<int>(kColsumRows), G = static_cast<int>(kColsumGroup);
+        __shared__ double cs[16][17];
+        const int j = threadIdx.x & 15, q = threadIdx.x >> 4;
+        const size_t chunks = colsum_chunk_count(static_cast<size_t>(e.K));
+        double total = 0.0;
+        for (size_t c0 = 0; c0 < chunks; c0 += 16) {  // uniform
+            const size_t c = c0 + q;
+            double sum = 0.0;
+            if (j < e.N && c < chunks) {
+                float v[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const size_t k = c * R + r;
+                    v[r] = k < static_cast<size_t>(e.K) ? e.B[k * e.ldb + j] : 0.0f;
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r) sum += (double)v[r];
+            }
+            cs[q][j] = sum;
+            __syncthreads();
+            if (q == 0) {
+#pragma unroll
+                for (int h = 0; h < 16 / G; ++h) {
+                    double grp = 0.0;
+#pragma unroll
+                    for (int i = 0; i < G; ++i) grp += cs[h * G + i][j];
+                    total += grp;
+                }
+            }
+            __syncthreads();
+        }
+        if (q == 0 && j < e.N) e.colsum[j] = static_cast<float>(total);
+        return;
+    }
     if (t >= mn) return;
     // every slice's value in flight at once (slices <= 16), then the sum in slice order
     float v[16];
@@ -660,14 +767,14 @@ __global__ __launch_bounds__(kBlock) void splitk_sum(const float *__restrict__ P
     C[i * ldc + j] = epilogue(e, acc, static_cast<int>(i), static_cast<int>(j));
 }
 
-template <bool TA, bool TB, int WM, int WN, int SCHED, int EPI>
+template <bool TA, bool TB, int WM, int WN, int SCHED, int EPI, bool CS = false>
 static void launch_dma(GemmArgs g, hipStream_t s, unsigned batches) {
     g.tiles_m = (g.M + 255) / 256;
     g.tiles_n = (g.N + 255) / 256;
     g.tiles = g.tiles_m * g.tiles_n;
     dim3 grid(static_cast<unsigned>(g.tiles) * batches);
     dim3 block(64 * WM * WN);
-    launch((gemm_f32_lds_dma<TA, TB, WM, WN, SCHED, EPI>), grid, block, 0, s, g);
+    launch((gemm_f32_lds_dma<TA, TB, WM, WN, SCHED, EPI, CS>), grid, block, 0, s, g);
 }
 
 // The DMA kernel of one layout: wave grid and LDS-read order per layout, the
@@ -685,7 +792,8 @@ static void launch_dma_layout(int ta, int tb, const GemmArgs &g, hipStream_t s, 
         if (epi) launch_dma<false, true, 2, 4, 0, kEpiAll>(g, s, nb);
         else launch_dma<false, true, 2, 4, 0, kEpiNone>(g, s, nb);
     } else if (ta && !tb) {
-        if (epi) launch_dma<true, false, 2, 4, 1, kEpiAll>(g, s, nb);
+        if (g.colsum) launch_dma<true, false, 2, 4, 1, kEpiNone, true>(g, s, nb);  // dW with db
+        else if (epi) launch_dma<true, false, 2, 4, 1, kEpiAll>(g, s, nb);
         else launch_dma<true, false, 2, 4, 1, kEpiNone>(g, s, nb);
     } else {
         if (epi) launch_dma<true, true, 2, 4, 1, kEpiAll>(g, s, nb);
@@ -763,10 +871,11 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny(GemmArgs g, flo
     const int ir = i < g.M ? i : g.M - 1;  // rows past M: an in-bounds row, never stored
     const float *__restrict__ A = g.A;
     const float *__restrict__ B = g.B;
-    // k range of this wave within this workgroup's slice (lengths are
+    // k range of this wave within this workgroup's slice (slices are
+    // g.kslice rows, a multiple of the column sum's chunk; wave ranges are
     // multiples of 4, so a row-major A row is read as float4)
     const int slices = gridDim.y, slice = blockIdx.y;
-    const int ks = ((g.K + slices - 1) / slices + 3) & ~3;
+    const int ks = g.kslice;
     const int sb = min(g.K, slice * ks), se = min(g.K, sb + ks);
     const int kc = ((ks + kSkinnyWaves - 1) / kSkinnyWaves + 3) & ~3;
     const int kb = min(se, sb + wave * kc);
@@ -840,18 +949,28 @@ static bool skinny(size_t N) { return N <= static_cast<size_t>(kSkinnyN); }
 // Slices of K for a skinny product: enough (row group x slice) workgroups for
 // every CU, each slice at least 64 k long; 1 when the row groups alone
 // fill the chip.
+// Rows per slice for a wanted slice count, a whole number of the column sum's
+// chunks.
+static size_t skinny_kslice(size_t K, size_t sl) {
+    const size_t per = (K + sl - 1) / sl;
+    return (per + kColsumRows - 1) / kColsumRows * kColsumRows;
+}
+
 static int skinny_slices(size_t M, size_t K) {
     const size_t cus = static_cast<size_t>(device_cu_count());
     const size_t groups = (M + 63) / 64;
-    if (groups >= cus) return 1;
+    if (groups >= cus || K == 0) return 1;
     size_t sl = (cus + groups - 1) / groups;
     if (sl > static_cast<size_t>(kSkinnyMaxSlices)) sl = kSkinnyMaxSlices;
     const size_t by_k = K / 64 > 0 ? K / 64 : 1;
     if (sl > by_k) sl = by_k;
-    return static_cast<int>(sl);
+    const size_t ks = skinny_kslice(K, sl);
+    return static_cast<int>((K + ks - 1) / ks);  // slices that hold rows
 }
 
 // P: slices * M * N floats when skinny_slices(M, K) > 1 (else unused).
+// With g.colsum set and one slice, g.colsum_part holds colsum_chunk_count(K) * N
+// doubles for the column-sum pass.
 static int launch_skinny(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A, size_t lda,
                          const float *B, size_t ldb, float *C, size_t ldc, GemmArgs g, float *P, void *stream) {
     if (!A || !B) return TS_HIP_EINVAL;
@@ -860,21 +979,29 @@ static int launch_skinny(int trans_a, int trans_b, size_t M, size_t N, size_t K,
     if (M > lim || K > lim || lda > lim || ldb > lim || ldc > lim) return TS_HIP_EINVAL;
     const int slices = skinny_slices(M, K);
     if (slices > 1 && !P) return TS_HIP_EINVAL;
+    if (g.colsum && !g.colsum_part) return TS_HIP_EINVAL;
     g.A = A; g.B = B; g.C = C;
     g.M = static_cast<int>(M); g.N = static_cast<int>(N); g.K = static_cast<int>(K);
     g.lda = static_cast<int>(lda); g.ldb = static_cast<int>(ldb); g.ldc = static_cast<int>(ldc);
     g.vec = aligned16(A) && (lda % 4 == 0);
+    g.kslice = static_cast<int>(skinny_kslice(K, static_cast<size_t>(slices)));
+    if (!g.colsum) g.colsum_part = nullptr;
     const dim3 grid(static_cast<unsigned>((M + 63) / 64), static_cast<unsigned>(slices)), block(64 * kSkinnyWaves);
     hipStream_t s = as_stream(stream);
+    if (g.colsum && trans_b) return TS_HIP_EINVAL;
     if (!trans_a && !trans_b) launch((gemm_skinny<false, false>), grid, block, 0, s, g, P);
     else if (!trans_a) launch((gemm_skinny<false, true>), grid, block, 0, s, g, P);
     else if (!trans_b) launch((gemm_skinny<true, false>), grid, block, 0, s, g, P);
     else launch((gemm_skinny<true, true>), grid, block, 0, s, g, P);
     int st = launch_status();
-    if (st != TS_HIP_OK || slices == 1) return st;
-    const size_t blocks = (M * N + kBlock - 1) / kBlock;
-    launch(splitk_sum, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, P, slices, M, N, C, ldc,
-                       g);
+    if (st != TS_HIP_OK) return st;
+    if (slices == 1)  // the column sums as a pass of their own
+        return g.colsum ? launch_colsum(B, nullptr, K, N, ldb, g.colsum, reinterpret_cast<float *>(g.colsum_part),
+                                        2 * colsum_chunk_count(K) * N, stream)
+                        : TS_HIP_OK;
+    // the slice sum; with column sums, one more workgroup adds B's columns
+    const size_t blocks = (M * N + kBlock - 1) / kBlock + (g.colsum ? 1 : 0);
+    launch(splitk_sum, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, P, slices, M, N, C, ldc, g);
     return launch_status();
 }
 
@@ -893,85 +1020,129 @@ static int split_slices(size_t M, size_t N, size_t K) {
     return 1;
 }
 
-// One 2-D product with an optional epilogue (GemmArgs::bias / mask / relu).
-// A split product's temporary is `ws` when given (at least slices*M*N
-// floats), else it comes from the stream-ordered allocator.
+// Workspace of one product: the split temporary (slices * M * N floats) and,
+// with column sums of B, colsum_chunk_count(K) * N doubles of chunk sums after
+// it (8-byte aligned) -- written by the product's kernels (trans_a == 1,
+// unsplit or skinny) or by a column-sum pass after the product.
+struct GemmPlan {
+    bool skinny = false;
+    int slices = 1;
+    size_t split_floats = 0;
+    size_t part_floats = 0;
+    bool cs_kernel = false;  // the product's kernels write the column sums
+    size_t part_offset() const { return (split_floats + 1) & ~size_t(1); }
+    size_t total() const { return part_floats ? part_offset() + part_floats : split_floats; }
+};
+
+static GemmPlan gemm_plan(int trans_a, int trans_b, size_t M, size_t N, size_t K, bool colsum) {
+    GemmPlan p;
+    if (M == 0 || N == 0 || K == 0) return p;
+    p.skinny = skinny(N);
+    p.slices = p.skinny ? skinny_slices(M, K) : split_slices(M, N, K);
+    p.split_floats = p.slices > 1 ? static_cast<size_t>(p.slices) * M * N : 0;
+    p.cs_kernel = colsum && !p.skinny && p.slices == 1 && trans_a && !trans_b;
+    p.part_floats = colsum ? 2 * colsum_chunk_count(K) * N : 0;
+    return p;
+}
+
+// One 2-D product with an optional epilogue (GemmArgs::bias / mask / relu)
+// and optional column sums of B (colsum, trans_b == 0, no epilogue).  The
+// workspace is `ws` when given (at least gemm_plan(...).total() floats),
+// else it comes from the stream-ordered allocator.
 static int gemm_plain(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A, size_t lda,
                       const float *B, size_t ldb, float *C, size_t ldc, const float *bias, const float *mask,
-                      int relu, float *ws, size_t ws_floats, void *stream) {
+                      int relu, float *colsum, float *ws, size_t ws_floats, void *stream) {
     if (M == 0 || N == 0) return TS_HIP_OK;
     if (!C || ldc < N) return TS_HIP_EINVAL;
+    if (colsum && (trans_b || bias || mask || relu)) return TS_HIP_EINVAL;
     if (K == 0) {  // empty contraction: C = 0, then the epilogue
         if (ldc != N) return TS_HIP_EINVAL;
         int st = ts_hip_fill(C, 0.0f, M * N, stream);
         if (st == TS_HIP_OK && bias) st = ts_hip_row_broadcast(0, C, bias, C, M, N, 0, 0, nullptr, stream);
         if (st == TS_HIP_OK && relu) st = ts_hip_relu(C, C, M * N, stream);
         if (st == TS_HIP_OK && mask) st = ts_hip_relu_backward(mask, C, C, M * N, stream);
+        if (st == TS_HIP_OK && colsum) st = ts_hip_fill(colsum, 0.0f, N, stream);
         return st;
     }
-    if (skinny(N)) {  // few output columns: the skinny kernel, K split over the CUs
+    if (!A || !B || lda < (trans_a ? M : K) || ldb < (trans_b ? K : N)) return TS_HIP_EINVAL;
+    const GemmPlan plan = gemm_plan(trans_a, trans_b, M, N, K, colsum != nullptr);
+    const size_t need = plan.total();
+    hipStream_t st = as_stream(stream);
+    float *W = ws;
+    bool owned = false;
+    if (need && ws && (ws_floats < need || (plan.part_floats && (reinterpret_cast<uintptr_t>(ws) & 7u))))
+        return TS_HIP_EWORKSPACE;
+    if (need && !W) {
+        if (hipMallocAsync(reinterpret_cast<void **>(&W), need * sizeof(float), st) == hipSuccess) {
+            owned = true;
+        } else {
+            (void)hipGetLastError();
+            W = nullptr;
+            // no stream-ordered allocator: an MFMA split runs unsplit; the
+            // rest needs the caller's workspace
+            if (plan.skinny && plan.slices > 1) return TS_HIP_EINVAL;
+            if (plan.part_floats) return TS_HIP_EINVAL;
+        }
+    }
+    double *part = plan.part_floats ? reinterpret_cast<double *>(W + plan.part_offset()) : nullptr;
+    int status;
+    if (plan.skinny) {  // few output columns: the skinny kernel, K split over the CUs
         GemmArgs g{};
         g.bias = bias;
         g.mask = mask;
         g.relu = relu;
-        const int slices = skinny_slices(M, K);
-        if (slices == 1) return launch_skinny(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, g, nullptr, stream);
-        hipStream_t st = as_stream(stream);
-        const size_t need = static_cast<size_t>(slices) * M * N;
-        if (ws && ws_floats < need) return TS_HIP_EWORKSPACE;
-        float *P = ws;
-        if (!P && hipMallocAsync(reinterpret_cast<void **>(&P), need * sizeof(float), st) != hipSuccess) {
-            (void)hipGetLastError();
-            return TS_HIP_EINVAL;  // no stream-ordered allocator: the caller passes a workspace
+        g.colsum = colsum;
+        g.colsum_part = part;
+        status = launch_skinny(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, g, W, stream);
+    } else if (plan.slices > 1 && W) {
+        const int slices = plan.slices;
+        const size_t kc = K / slices;
+        GemmArgs e{};  // epilogue after the slice sum
+        e.bias = bias;
+        e.mask = mask;
+        e.relu = relu;
+        e.ldc = static_cast<int>(ldc);
+        GemmArgs g{};
+        g.batch_rank = 1;
+        g.bdims[0] = slices;
+        g.sa[0] = static_cast<long long>(trans_a ? kc * lda : kc);
+        g.sb[0] = static_cast<long long>(trans_b ? kc : kc * ldb);
+        g.sc = static_cast<long long>(M * N);
+        status = gemm_launch(trans_a, trans_b, M, N, kc, A, lda, B, ldb, W, N, g, slices, stream);
+        if (status == TS_HIP_OK) {
+            const size_t blocks = (M * N + kBlock - 1) / kBlock;
+            launch(splitk_sum, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, st, W, slices, M, N, C, ldc, e);
+            status = launch_status();
         }
-        const int status = launch_skinny(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, g, P, stream);
-        if (ws) return status;
-        const hipError_t fe = hipFreeAsync(P, st);
-        return status != TS_HIP_OK ? status : static_cast<int>(fe);
-    }
-    const int slices = split_slices(M, N, K);
-    if (slices > 1 && A && B && lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N)) {
-        hipStream_t st = as_stream(stream);
-        const size_t need = slices * M * N;
-        float *P = ws;
-        if (ws && ws_floats < need) return TS_HIP_EWORKSPACE;
-        if (P || hipMallocAsync(reinterpret_cast<void **>(&P), need * sizeof(float), st) == hipSuccess) {
-            const size_t kc = K / slices;
-            GemmArgs e{};  // epilogue after the slice sum
-            e.bias = bias;
-            e.mask = mask;
-            e.relu = relu;
-            e.ldc = static_cast<int>(ldc);
-            GemmArgs g{};
-            g.batch_rank = 1;
-            g.bdims[0] = slices;
-            g.sa[0] = static_cast<long long>(trans_a ? kc * lda : kc);
-            g.sb[0] = static_cast<long long>(trans_b ? kc : kc * ldb);
-            g.sc = static_cast<long long>(M * N);
-            int status = gemm_launch(trans_a, trans_b, M, N, kc, A, lda, B, ldb, P, N, g, slices, stream);
-            if (status == TS_HIP_OK) {
-                const size_t blocks = (M * N + kBlock - 1) / kBlock;
-                launch(splitk_sum, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, st, P, slices, M,
-                                   N, C, ldc, e);
-                status = launch_status();
-            }
-            if (ws) return status;
-            const hipError_t fe = hipFreeAsync(P, st);
-            return status != TS_HIP_OK ? status : static_cast<int>(fe);
+        if (status == TS_HIP_OK && colsum)
+            status = launch_colsum(B, nullptr, K, N, ldb, colsum, reinterpret_cast<float *>(part), plan.part_floats,
+                                   stream);
+    } else {
+        GemmArgs g{};
+        g.bias = bias;
+        g.mask = mask;
+        g.relu = relu;
+        if (plan.cs_kernel) {
+            g.colsum = colsum;
+            g.colsum_part = part;
         }
-        (void)hipGetLastError();  // no stream-ordered allocation: run unsplit
+        status = gemm_launch(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, g, 1, stream);
+        if (status == TS_HIP_OK && plan.cs_kernel)
+            status = launch_colsum_final(part, colsum_chunk_count(K), N, colsum, st);
+        else if (status == TS_HIP_OK && colsum)
+            status = launch_colsum(B, nullptr, K, N, ldb, colsum, reinterpret_cast<float *>(part), plan.part_floats,
+                                   stream);
     }
-    GemmArgs g{};
-    g.bias = bias;
-    g.mask = mask;
-    g.relu = relu;
-    return gemm_launch(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, g, 1, stream);
+    if (!owned) return status;
+    const hipError_t fe = hipFreeAsync(W, st);
+    return status != TS_HIP_OK ? status : static_cast<int>(fe);
 }
 
 extern "C" int ts_hip_gemm(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
                            size_t lda, const float *B, size_t ldb, float *C, size_t ldc,
                            void *stream) {
-    return gemm_plain(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, nullptr, nullptr, 0, nullptr, 0, stream);
+    return gemm_plain(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, nullptr, nullptr, 0, nullptr, nullptr, 0,
+                      stream);
 }
 
 // ---- allocation-free form --------------------------------------------------
@@ -1023,20 +1194,52 @@ extern "C" int ts_hip_gemm_noalloc(int trans_a, int trans_b, size_t M, size_t N,
     }
     // with a workspace given, a split product takes its temporary from it;
     // unsplit products and empty contractions use none
-    return gemm_plain(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, nullptr, nullptr, 0, ws, need, stream);
+    return gemm_plain(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, nullptr, nullptr, 0, nullptr, ws, need,
+                      stream);
 }
 
 extern "C" size_t ts_hip_gemm_workspace_floats(size_t M, size_t N, size_t K) {
-    if (M == 0 || N == 0 || K == 0) return 0;
-    const int slices = split_slices(M, N, K);
-    return slices > 1 ? static_cast<size_t>(slices) * M * N : 0;
+    return gemm_plan(0, 0, M, N, K, false).total();
 }
 
 extern "C" int ts_hip_gemm_fused(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
                                  size_t lda, const float *B, size_t ldb, const float *bias, int relu,
                                  const float *mask, float *C, size_t ldc, float *workspace,
                                  size_t workspace_floats, void *stream) {
-    return gemm_plain(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, bias, mask, relu != 0, workspace,
+    return gemm_plain(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, bias, mask, relu != 0, nullptr, workspace,
+                      workspace_floats, stream);
+}
+
+extern "C" size_t ts_hip_gemm_colsum_workspace_floats(int trans_a, size_t M, size_t N, size_t K) {
+    if (N == 0 || K == 0) return 0;
+    if (M == 0) return 2 * colsum_chunk_count(K) * N;  // the column sums alone
+    return gemm_plan(trans_a, 0, M, N, K, true).total();
+}
+
+extern "C" int ts_hip_gemm_colsum(int trans_a, size_t M, size_t N, size_t K, const float *A, size_t lda,
+                                  const float *B, size_t ldb, float *C, size_t ldc, float *colsum, float *workspace,
+                                  size_t workspace_floats, void *stream) {
+    if (!colsum) return TS_HIP_EINVAL;
+    if (N == 0) return TS_HIP_OK;
+    if (M == 0) {  // no product, the column sums alone
+        if (K == 0) return ts_hip_fill(colsum, 0.0f, N, stream);
+        if (!B || ldb < N) return TS_HIP_EINVAL;
+        const size_t need = 2 * colsum_chunk_count(K) * N;
+        if (workspace) {
+            if (workspace_floats < need) return TS_HIP_EWORKSPACE;
+            return launch_colsum(B, nullptr, K, N, ldb, colsum, workspace, workspace_floats, stream);
+        }
+        hipStream_t st = as_stream(stream);
+        float *W = nullptr;
+        if (hipMallocAsync(reinterpret_cast<void **>(&W), need * sizeof(float), st) != hipSuccess) {
+            (void)hipGetLastError();
+            return TS_HIP_EINVAL;
+        }
+        const int status = launch_colsum(B, nullptr, K, N, ldb, colsum, W, need, stream);
+        const hipError_t fe = hipFreeAsync(W, st);
+        return status != TS_HIP_OK ? status : static_cast<int>(fe);
+    }
+    return gemm_plain(trans_a, 0, M, N, K, A, lda, B, ldb, C, ldc, nullptr, nullptr, 0, colsum, workspace,
                       workspace_floats, stream);
 }
 

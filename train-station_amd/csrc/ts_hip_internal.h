@@ -109,9 +109,27 @@ __device__ inline double block_sum(double v) {
 // order and writes the fp32 sum (divided by (float)n when mean) to out[0].
 int launch_sum_final(const double *partial, size_t nparts, size_t n, float *out, bool mean, hipStream_t s);
 
+// ---- the column sum's order (ts_hip_sum_dim0, and the bias gradient the
+// weight-gradient GEMM produces alongside its product, which must give the
+// same bits) ---------------------------------------------------------------------
+//
+// Rows are taken in chunks of kColsumRows: a chunk's rows are added in row
+// order, a group of kColsumGroup consecutive chunks' sums in chunk order, the
+// group sums in group order -- each sum in f64 starting from +0 -- and the
+// total is rounded to fp32 once.  (Starting from +0 no partial is ever -0, so
+// zero padding past the last row or chunk changes nothing.)
+constexpr size_t kColsumRows = 64;
+constexpr size_t kColsumGroup = 8;
+
+__host__ __device__ inline size_t colsum_chunk_count(size_t rows) { return (rows + kColsumRows - 1) / kColsumRows; }
+
 // Weighted column sums out[c] = sum_r w[r] * x[r][c] (w == nullptr: plain
-// column sums), f64 partials; workspace as ts_hip_sum_dim0_workspace_floats.
+// column sums) in that order; workspace as ts_hip_sum_dim0_workspace_floats.
 int launch_colsum(const float *x, const float *w, size_t rows, size_t cols, size_t ld, float *out,
                   float *workspace, size_t workspace_floats, void *stream);
+
+// The column sum's second pass: out[c] = the chunk sums partial[k * cols + c]
+// added by groups as above, rounded to fp32.
+int launch_colsum_final(const double *partial, size_t chunks, size_t cols, float *out, hipStream_t s);
 
 }  // namespace tship

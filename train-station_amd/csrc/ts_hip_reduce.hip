@@ -88,148 +88,126 @@ static int launch_sum(const float *x, const float *y, size_t n, float *out, floa
 }
 
 // ---- column reduction [rows, cols] -> [cols] --------------------------------
-
-// Pass 1: a workgroup owns 64 column units (float4 groups of 4 adjacent
-// columns when cols % 4 == 0, single columns otherwise) and one chunk of
-// rows; its four waves take every fourth row of the chunk, each wave reading
-// 1 KiB contiguously per row with eight rows in flight per thread.  The four
-// row lanes are combined in LDS in a fixed order and one f64 partial per
-// column and chunk is written.  Chunks are sized so that the grid has about
-// 2048 workgroups.
-constexpr size_t kDim0MaxChunks = 128;
-constexpr int kDim0Cols = 64;  // column units per workgroup
-constexpr int kDim0Unroll = 8;
-
-static size_t dim0_chunks(size_t rows, size_t cols) {
-    const size_t units = (cols % 4 == 0) ? cols / 4 : cols;
-    const size_t col_blocks = (units + kDim0Cols - 1) / kDim0Cols;
-    size_t want = 2048 / (col_blocks ? col_blocks : 1);
-    size_t by_rows = (rows + 15) / 16;                    // at least 16 rows per chunk
-    size_t c = want < by_rows ? want : by_rows;
-    if (c > kDim0MaxChunks) c = kDim0MaxChunks;
-    return c < 1 ? 1 : c;
-}
-
+//
+// The sum's order is fixed (see kColsumRows): each chunk of 64 rows is added
+// row by row, groups of 8 chunk sums in chunk order, the group sums in group
+// order, all in f64 from +0, then rounded to fp32.  The GEMM kernels that
+// produce a bias gradient alongside the weight gradient follow the same
+// order, so either path gives the same bits.
+//
+// Pass 1: thread (column unit u, chunk c) adds its chunk's rows in order (a
+// column unit is a float4 of 4 adjacent columns when cols % 4 == 0 and x is
+// 16-byte aligned, else one column), 16 rows in flight at a time, and writes
+// one f64 partial per column and chunk.
 // W: row r is weighted by w[r] (in f64) -- a transposed matrix-vector product.
+// Workgroup b takes column block b % col_blocks of chunk b / col_blocks.
 template <bool VEC, bool W>
-__global__ __launch_bounds__(kBlock) void dim0_partial(const float *__restrict__ x, const float *__restrict__ w,
-                                                       size_t rows, size_t cols, size_t rows_per_chunk,
-                                                       double *__restrict__ partial) {
+__global__ __launch_bounds__(kBlock) void colsum_chunks(const float *__restrict__ x, const float *__restrict__ w,
+                                                        size_t rows, size_t cols, size_t ld, size_t col_blocks,
+                                                        double *__restrict__ partial) {
     constexpr int L = VEC ? 4 : 1;  // columns per unit
-    __shared__ double lds[kBlock / kDim0Cols][kDim0Cols][L];
+    constexpr int kFly = 16;        // rows in flight
     const size_t units = VEC ? cols / 4 : cols;
-    const int cl = threadIdx.x % kDim0Cols, rl = threadIdx.x / kDim0Cols;
-    constexpr int RL = kBlock / kDim0Cols;  // row lanes
-    const size_t u = static_cast<size_t>(blockIdx.x) * kDim0Cols + cl;
-    const size_t r0 = static_cast<size_t>(blockIdx.y) * rows_per_chunk;
-    size_t r1 = r0 + rows_per_chunk;
-    if (r1 > rows) r1 = rows;
+    const size_t chunk = blockIdx.x / col_blocks;
+    const size_t u = (blockIdx.x % col_blocks) * kBlock + threadIdx.x;
+    if (u >= units) return;
+    const size_t r0 = chunk * kColsumRows;
+    const size_t r1 = r0 + kColsumRows < rows ? r0 + kColsumRows : rows;
     double acc[L];
 #pragma unroll
     for (int c = 0; c < L; ++c) acc[c] = 0.0;
     auto load = [&](size_t r, float (&q)[L]) {
         if (VEC) {
-            const float4 v = reinterpret_cast<const float4 *>(x)[r * units + u];
+            const float4 v = *reinterpret_cast<const float4 *>(x + r * ld + 4 * u);
             q[0] = v.x; q[L > 1 ? 1 : 0] = v.y; q[L > 2 ? 2 : 0] = v.z; q[L > 3 ? 3 : 0] = v.w;
         } else {
-            q[0] = x[r * cols + u];
+            q[0] = x[r * ld + u];
         }
     };
-    if (u < units) {
-        size_t r = r0 + rl;
-        for (; r + RL * (kDim0Unroll - 1) < r1; r += RL * kDim0Unroll) {
-            float q[kDim0Unroll][L];
+    size_t r = r0;
+    for (; r + kFly <= r1; r += kFly) {
+        float q[kFly][L];
 #pragma unroll
-            for (int k = 0; k < kDim0Unroll; ++k) load(r + RL * k, q[k]);
+        for (int k = 0; k < kFly; ++k) load(r + k, q[k]);
 #pragma unroll
-            for (int k = 0; k < kDim0Unroll; ++k) {
-                const double wr = W ? (double)w[r + RL * k] : 1.0;
+        for (int k = 0; k < kFly; ++k) {
+            const double wr = W ? (double)w[r + k] : 1.0;
 #pragma unroll
-                for (int c = 0; c < L; ++c) acc[c] += wr * q[k][c];
-            }
-        }
-        for (; r < r1; r += RL) {
-            float q[L];
-            load(r, q);
-            const double wr = W ? (double)w[r] : 1.0;
-#pragma unroll
-            for (int c = 0; c < L; ++c) acc[c] += wr * q[c];
+            for (int c = 0; c < L; ++c) acc[c] += W ? wr * q[k][c] : (double)q[k][c];
         }
     }
+    for (; r < r1; ++r) {
+        float q[L];
+        load(r, q);
+        const double wr = W ? (double)w[r] : 1.0;
 #pragma unroll
-    for (int c = 0; c < L; ++c) lds[rl][cl][c] = acc[c];
-    __syncthreads();
-    // thread t writes column (unit t / L, component t % L) of this workgroup
-    for (int t = threadIdx.x; t < kDim0Cols * L; t += kBlock) {
-        const int g = t / L, c = t % L;
-        const size_t col = (static_cast<size_t>(blockIdx.x) * kDim0Cols + g) * L + c;
-        if (col < cols) {
-            double sum = lds[0][g][c];
-#pragma unroll
-            for (int k = 1; k < RL; ++k) sum += lds[k][g][c];
-            partial[static_cast<size_t>(blockIdx.y) * cols + col] = sum;
-        }
+        for (int c = 0; c < L; ++c) acc[c] += W ? wr * q[c] : (double)q[c];
     }
+#pragma unroll
+    for (int c = 0; c < L; ++c) partial[chunk * cols + u * L + c] = acc[c];
 }
 
-// Pass 2: a workgroup owns 16 columns; 16 chunk lanes each add every 16th
-// chunk partial, then the 16 lane sums are added in order.
-__global__ __launch_bounds__(kBlock) void dim0_final(const double *__restrict__ partial,
-                                                     size_t chunks, size_t cols,
-                                                     float *__restrict__ out) {
-    __shared__ double lds[16][17];
-    const int cl = threadIdx.x & 15, kl = threadIdx.x >> 4;
+// Pass 2: a workgroup takes 16 columns; in rounds of 16 groups, thread
+// (group lane gl, column cl) adds its group's chunk sums (8 loads in flight),
+// and the group sums are added in group order by the first lane.
+__global__ __launch_bounds__(kBlock) void colsum_final(const double *__restrict__ partial, size_t chunks,
+                                                       size_t cols, float *__restrict__ out) {
+    constexpr int G = static_cast<int>(kColsumGroup);
+    __shared__ double gs[16][17];
+    const int cl = threadIdx.x & 15, gl = threadIdx.x >> 4;
     const size_t c = static_cast<size_t>(blockIdx.x) * 16 + cl;
-    double acc = 0.0;
-    if (c < cols) {
-        size_t k = kl;
-        for (; k + 16 * 7 < chunks; k += 16 * 8) {  // eight loads in flight
-            double v[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = partial[(k + 16 * j) * cols + c];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc += v[j];
-        }
-        for (; k < chunks; k += 16) acc += partial[k * cols + c];
-    }
-    lds[kl][cl] = acc;
-    __syncthreads();
-    if (threadIdx.x < 16 && c < cols) {
+    const size_t groups = (chunks + G - 1) / G;
+    double total = 0.0;
+    for (size_t g0 = 0; g0 < groups; g0 += 16) {  // uniform
+        const size_t g = g0 + gl;
         double sum = 0.0;
+        if (c < cols && g < groups) {
+            double v[G];
 #pragma unroll
-        for (int k = 0; k < 16; ++k) sum += lds[k][cl];
-        out[c] = static_cast<float>(sum);
+            for (int j = 0; j < G; ++j) v[j] = g * G + j < chunks ? partial[(g * G + j) * cols + c] : 0.0;
+#pragma unroll
+            for (int j = 0; j < G; ++j) sum += v[j];
+        }
+        gs[gl][cl] = sum;
+        __syncthreads();
+        if (gl == 0)
+            for (int j = 0; j < 16; ++j) total += gs[j][cl];  // groups past the end add +0
+        __syncthreads();
     }
+    if (gl == 0 && c < cols) out[c] = static_cast<float>(total);
+}
+
+int launch_colsum_final(const double *partial, size_t chunks, size_t cols, float *out, hipStream_t s) {
+    launch(colsum_final, dim3(static_cast<unsigned>((cols + 15) / 16)), dim3(kBlock), 0, s, partial, chunks, cols,
+           out);
+    return launch_status();
 }
 
 // out[c] = sum_r w[r] * x[r][c] (w == nullptr: plain column sums) for a
-// row-major [rows, cols] matrix with leading dimension ld.
+// row-major [rows, cols] matrix with leading dimension ld >= cols.
 int launch_colsum(const float *x, const float *w, size_t rows, size_t cols, size_t ld, float *out,
                   float *workspace, size_t workspace_floats, void *stream) {
     if (cols == 0) return TS_HIP_OK;
     if (!out) return TS_HIP_EINVAL;
     if (rows == 0) return ts_hip_fill(out, 0.0f, cols, stream);
-    if (!x || ld != cols) return TS_HIP_EINVAL;
-    const size_t chunks = dim0_chunks(rows, cols);
+    if (!x || ld < cols) return TS_HIP_EINVAL;
+    const size_t chunks = colsum_chunk_count(rows);
     if (!workspace || workspace_floats < 2 * chunks * cols) return TS_HIP_EWORKSPACE;
     if ((reinterpret_cast<uintptr_t>(workspace) & 7u) != 0) return TS_HIP_EINVAL;
-    const size_t rows_per_chunk = (rows + chunks - 1) / chunks;
     double *partial = reinterpret_cast<double *>(workspace);
     hipStream_t s = as_stream(stream);
-    const bool vec = (cols % 4 == 0) && aligned16(x);
+    const bool vec = (cols % 4 == 0) && (ld % 4 == 0) && aligned16(x);
     const size_t units = vec ? cols / 4 : cols;
-    const size_t col_blocks = (units + kDim0Cols - 1) / kDim0Cols;
-    if (col_blocks > 0x7fffffffULL) return TS_HIP_EINVAL;
-    dim3 grid1(static_cast<unsigned>(col_blocks), static_cast<unsigned>(chunks));
-    if (vec && w) launch((dim0_partial<true, true>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
-    else if (vec) launch((dim0_partial<true, false>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
-    else if (w) launch((dim0_partial<false, true>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
-    else launch((dim0_partial<false, false>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, rows_per_chunk, partial);
+    const size_t col_blocks = (units + kBlock - 1) / kBlock;
+    if (col_blocks * chunks > 0x7fffffffULL) return TS_HIP_EINVAL;
+    const dim3 grid1(static_cast<unsigned>(col_blocks * chunks));
+    if (vec && w) launch((colsum_chunks<true, true>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, ld, col_blocks, partial);
+    else if (vec) launch((colsum_chunks<true, false>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, ld, col_blocks, partial);
+    else if (w) launch((colsum_chunks<false, true>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, ld, col_blocks, partial);
+    else launch((colsum_chunks<false, false>), grid1, dim3(kBlock), 0, s, x, w, rows, cols, ld, col_blocks, partial);
     int st = launch_status();
     if (st) return st;
-    launch(dim0_final, dim3(static_cast<unsigned>((cols + 15) / 16)), dim3(kBlock), 0, s,
-                       partial, chunks, cols, out);
-    return launch_status();
+    return launch_colsum_final(partial, chunks, cols, out, s);
 }
 
 }  // namespace tship
@@ -251,7 +229,7 @@ int ts_hip_mean(const float *x, size_t n, float *out, float *workspace, size_t w
 }
 
 size_t ts_hip_sum_dim0_workspace_floats(size_t rows, size_t cols) {
-    return 2 * dim0_chunks(rows, cols) * cols;
+    return 2 * colsum_chunk_count(rows) * cols;
 }
 
 int ts_hip_sum_dim0(const float *x, size_t rows, size_t cols, float *out, float *workspace,
