@@ -31,6 +31,9 @@ struct MapArgsK {
     unsigned long long *zero_index;
     bool vec;  // every input and output is 16-byte aligned
     double *partial;  // reduce: one f64 partial per workgroup
+    // the inputs read per element (not scalar), compacted: pointer and register
+    const float *vin[kMapIn];
+    int vreg[kMapIn];
 };
 
 // The register file of W consecutive elements: one local array per element,
@@ -39,7 +42,8 @@ struct MapArgsK {
 // struct go to scratch; separate arrays with uniform indices stay in VGPRs,
 // read and written with indexed moves).  C... are the elements' offsets.
 template <size_t... C, class... R>
-__device__ __forceinline__ void run_program(const MapArgsK &a, size_t i0, std::index_sequence<C...>, R &...r) {
+__device__ __forceinline__ void run_program(const MapArgsK &a, size_t i0, unsigned long long &zmin,
+                                            std::index_sequence<C...>, R &...r) {
     constexpr int W = sizeof...(C);
     const ts_hip_map_program &p = a.p;
     // unrolled: every op's fields sit at a fixed kernel-argument offset (read
@@ -60,8 +64,9 @@ __device__ __forceinline__ void run_program(const MapArgsK &a, size_t i0, std::i
             case TS_HIP_MAP_MUL: ((v[C] = x[C] * y[C]), ...); break;
             case TS_HIP_MAP_DIV: {
                 if ((op.flags & TS_HIP_MAP_CHECKED) && a.zero_index) {
+                    // the first zero divisor this thread sees (reported once, after its loop)
                     auto check = [&](float d, size_t i) {
-                        if (i >= a.check_start && d == 0.0f) atomicMin(a.zero_index, (unsigned long long)i);
+                        if (i >= a.check_start && d == 0.0f && i < zmin) zmin = i;
                     };
                     (check(y[C], i0 + C), ...);
                 }
@@ -133,6 +138,79 @@ __device__ __forceinline__ void store_outputs(const MapArgsK &a, size_t i0, bool
 // sum has the bits of ts_hip_sum over the stored values), the next group's
 // inputs loaded before the current group is evaluated, so a wave keeps loads
 // in flight while it computes.
+//
+// map_program_vec: 16-byte aligned operands, NV inputs read per element and NO
+// stored values known at compile time.  Every iteration then issues exactly
+// NV loads and NO stores (the next group's index clamped into range, a
+// division's zero check kept in a register and reported after the loop), so
+// the compiler's load counters are exact: the loop waits only for the next
+// group's loads, never for its own stores to complete.
+template <bool REDUCE, int NV, int NO>
+__global__ __launch_bounds__(kBlock) void map_program_vec(MapArgsK a) {
+    const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    const int rq = a.p.reduce_reg;
+    const auto seq = std::make_index_sequence<4>{};
+    double acc = 0.0;
+    unsigned long long zmin = ~0ull;
+    float sv[kMapIn];  // scalar inputs, read once
+#pragma unroll
+    for (int k = 0; k < kMapIn; ++k)
+        sv[k] = (k < static_cast<int>(a.p.n_inputs) && (a.p.scalar_inputs & (1u << k))) ? a.p.inputs[k][0] : 0.0f;
+    f4v_t nx[NV > 0 ? NV : 1];  // the next group's per-element inputs
+    auto fetch = [&](size_t g) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) nx[j] = *reinterpret_cast<const f4v_t *>(a.vin[j] + 4 * g);
+    };
+    if (t < a.n4) fetch(t);
+    for (size_t g = t; g < a.n4; g += stride) {
+        float r0[kMapRegs], r1[kMapRegs], r2[kMapRegs], r3[kMapRegs];
+#pragma unroll
+        for (int k = 0; k < kMapIn; ++k) {
+            r0[k] = sv[k];
+            r1[k] = sv[k];
+            r2[k] = sv[k];
+            r3[k] = sv[k];
+        }
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int k = a.vreg[j];
+            r0[k] = nx[j][0];
+            r1[k] = nx[j][1];
+            r2[k] = nx[j][2];
+            r3[k] = nx[j][3];
+        }
+        const size_t gn = g + stride < a.n4 ? g + stride : a.n4 - 1;  // in range: the same loads every step
+        fetch(gn);
+        run_program(a, 4 * g, zmin, seq, r0, r1, r2, r3);
+#pragma unroll
+        for (int o = 0; o < NO; ++o) {
+            const int q = a.p.output_regs[o];
+            f4v_t v;
+            v[0] = r0[q];
+            v[1] = r1[q];
+            v[2] = r2[q];
+            v[3] = r3[q];
+            *reinterpret_cast<f4v_t *>(a.p.outputs[o] + 4 * g) = v;
+        }
+        if (REDUCE) acc += (double)r0[rq] + (double)r1[rq] + (double)r2[rq] + (double)r3[rq];
+    }
+    for (size_t i = 4 * a.n4 + t; i < a.n; i += stride) {
+        float r0[kMapRegs];
+        const auto one = std::make_index_sequence<1>{};
+        load_inputs(a, i, false, one, r0);
+        run_program(a, i, zmin, one, r0);
+        store_outputs(a, i, false, one, r0);
+        if (REDUCE) acc += (double)r0[rq];
+    }
+    if (zmin != ~0ull) atomicMin(a.zero_index, zmin);
+    if (REDUCE) {
+        const double s = block_sum(acc);
+        if (threadIdx.x == 0) a.partial[blockIdx.x] = s;
+    }
+}
+
+// Any alignment and counts: the same evaluation with element loads.
 template <bool REDUCE>
 __global__ __launch_bounds__(kBlock) void map_program_kernel(MapArgsK a) {
     const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
@@ -140,40 +218,11 @@ __global__ __launch_bounds__(kBlock) void map_program_kernel(MapArgsK a) {
     const int rq = a.p.reduce_reg;
     const auto seq = std::make_index_sequence<4>{};
     double acc = 0.0;
-    float n0[kMapIn], n1[kMapIn], n2[kMapIn], n3[kMapIn];  // the next group's inputs
-    auto fetch = [&](size_t g) {
-#pragma unroll
-        for (int k = 0; k < kMapIn; ++k) {
-            if (k >= static_cast<int>(a.p.n_inputs)) break;
-            const float *in = a.p.inputs[k];
-            if (a.p.scalar_inputs & (1u << k)) {
-                n0[k] = n1[k] = n2[k] = n3[k] = in[0];
-            } else if (a.vec) {
-                const float4 q = *reinterpret_cast<const float4 *>(in + 4 * g);
-                n0[k] = q.x;
-                n1[k] = q.y;
-                n2[k] = q.z;
-                n3[k] = q.w;
-            } else {
-                n0[k] = in[4 * g];
-                n1[k] = in[4 * g + 1];
-                n2[k] = in[4 * g + 2];
-                n3[k] = in[4 * g + 3];
-            }
-        }
-    };
-    if (t < a.n4) fetch(t);
+    unsigned long long zmin = ~0ull;
     for (size_t g = t; g < a.n4; g += stride) {
         float r0[kMapRegs], r1[kMapRegs], r2[kMapRegs], r3[kMapRegs];
-#pragma unroll
-        for (int k = 0; k < kMapIn; ++k) {
-            r0[k] = n0[k];
-            r1[k] = n1[k];
-            r2[k] = n2[k];
-            r3[k] = n3[k];
-        }
-        if (g + stride < a.n4) fetch(g + stride);
-        run_program(a, 4 * g, seq, r0, r1, r2, r3);
+        load_inputs(a, 4 * g, a.vec, seq, r0, r1, r2, r3);
+        run_program(a, 4 * g, zmin, seq, r0, r1, r2, r3);
         store_outputs(a, 4 * g, a.vec, seq, r0, r1, r2, r3);
         if (REDUCE) acc += (double)r0[rq] + (double)r1[rq] + (double)r2[rq] + (double)r3[rq];
     }
@@ -181,13 +230,48 @@ __global__ __launch_bounds__(kBlock) void map_program_kernel(MapArgsK a) {
         float r0[kMapRegs];
         const auto one = std::make_index_sequence<1>{};
         load_inputs(a, i, false, one, r0);
-        run_program(a, i, one, r0);
+        run_program(a, i, zmin, one, r0);
         store_outputs(a, i, false, one, r0);
         if (REDUCE) acc += (double)r0[rq];
     }
+    if (zmin != ~0ull) atomicMin(a.zero_index, zmin);
     if (REDUCE) {
         const double s = block_sum(acc);
         if (threadIdx.x == 0) a.partial[blockIdx.x] = s;
+    }
+}
+
+// The launch: the counted form for aligned operands, the general one else.
+template <bool REDUCE, int NV, int NO>
+static void launch_vec_as(const MapArgsK &a, dim3 grid, hipStream_t s) {
+    launch(map_program_vec<REDUCE, NV, NO>, grid, dim3(kBlock), 0, s, a);
+}
+
+template <bool REDUCE, int NV>
+static void launch_vec_no(const MapArgsK &a, int no, dim3 grid, hipStream_t s) {
+    switch (no) {
+        case 0: launch_vec_as<REDUCE, NV, 0>(a, grid, s); break;
+        case 1: launch_vec_as<REDUCE, NV, 1>(a, grid, s); break;
+        case 2: launch_vec_as<REDUCE, NV, 2>(a, grid, s); break;
+        case 3: launch_vec_as<REDUCE, NV, 3>(a, grid, s); break;
+        default: launch_vec_as<REDUCE, NV, 4>(a, grid, s); break;
+    }
+}
+
+template <bool REDUCE>
+static void launch_map(const MapArgsK &a, int nv, dim3 grid, hipStream_t s) {
+    if (!a.vec) {
+        launch(map_program_kernel<REDUCE>, grid, dim3(kBlock), 0, s, a);
+        return;
+    }
+    const int no = static_cast<int>(a.p.n_outputs);
+    switch (nv) {
+        case 0: launch_vec_no<REDUCE, 0>(a, no, grid, s); break;
+        case 1: launch_vec_no<REDUCE, 1>(a, no, grid, s); break;
+        case 2: launch_vec_no<REDUCE, 2>(a, no, grid, s); break;
+        case 3: launch_vec_no<REDUCE, 3>(a, no, grid, s); break;
+        case 4: launch_vec_no<REDUCE, 4>(a, no, grid, s); break;
+        default: launch_vec_no<REDUCE, 5>(a, no, grid, s); break;
     }
 }
 
@@ -235,20 +319,27 @@ extern "C" int ts_hip_map(const ts_hip_map_program *prog, size_t n, size_t tail_
     a.check_start = zero_check_start;
     a.zero_index = zero_index;
     a.vec = vec;
+    int nv = 0;
+    for (uint32_t k = 0; k < p.n_inputs; ++k)
+        if (!(p.scalar_inputs & (1u << k))) {
+            a.vin[nv] = p.inputs[k];
+            a.vreg[nv] = static_cast<int>(k);
+            ++nv;
+        }
     if (!reduce) {
         const size_t rest = n - 4 * a.n4;
         const size_t threads = a.n4 > rest ? a.n4 : rest;
         // several groups per thread (the prefetch overlaps them), enough
         // workgroups to fill every CU many times over
         const unsigned blocks = grid_for(threads, 4);
-        launch(map_program_kernel<false>, dim3(blocks), dim3(kBlock), 0, s, a);
+        launch_map<false>(a, nv, dim3(blocks), s);
         return launch_status();
     }
     const size_t blocks = sum_blocks(n);
     if (!workspace || workspace_floats < 2 * blocks) return TS_HIP_EWORKSPACE;
     if ((reinterpret_cast<uintptr_t>(workspace) & 7u) != 0) return TS_HIP_EINVAL;
     a.partial = reinterpret_cast<double *>(workspace);
-    launch(map_program_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, a);
+    launch_map<true>(a, nv, dim3(static_cast<unsigned>(blocks)), s);
     const int st = launch_status();
     if (st != TS_HIP_OK) return st;
     return launch_sum_final(a.partial, blocks, n, sum_out, mean != 0, s);
