@@ -75,7 +75,7 @@ __device__ __forceinline__ float4 load_nt(const float4 *p) {
 // ---- the scalar sum's partition (ts_hip_sum, and the fused sum of ts_hip_map,
 // which must give the same bits) ----------------------------------------------
 
-constexpr size_t kSumChunk = 8192;  // inputs per first-pass workgroup (minimum)
+constexpr size_t kSumChunk = 1024;  // inputs per first-pass workgroup (minimum): one group of 4 per thread
 constexpr size_t kSumMaxBlocks = 2048;
 
 inline size_t sum_blocks(size_t n) {

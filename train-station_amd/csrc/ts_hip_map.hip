@@ -329,9 +329,10 @@ extern "C" int ts_hip_map(const ts_hip_map_program *prog, size_t n, size_t tail_
     if (!reduce) {
         const size_t rest = n - 4 * a.n4;
         const size_t threads = a.n4 > rest ? a.n4 : rest;
-        // several groups per thread (the prefetch overlaps them), enough
-        // workgroups to fill every CU many times over
-        const unsigned blocks = grid_for(threads, 4);
+        // a group per thread up to 16 workgroups per CU, then several per
+        // thread (the prefetch overlaps them): a small program is one short
+        // round of loads, not a chain of them
+        const unsigned blocks = grid_for(threads, 1);
         launch_map<false>(a, nv, dim3(blocks), s);
         return launch_status();
     }
