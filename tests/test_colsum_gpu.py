@@ -1,8 +1,8 @@
 """ts_hip_gemm_colsum: a weight gradient C = op(A) . B with the bias gradient
 colsum[n] = sum_k B[k][n] beside it.  Every kernel path is covered (the
 256x256 LDS-DMA tiles, the register-staged 64/128/256 tiles with aligned and
-unaligned operands, the skinny kernel split and unsplit, an MFMA split-K
-product, trans_a == 0, ragged K); on each, C has the bits of ts_hip_gemm
+unaligned operands, the narrow one-pass kernel and the sliced skinny kernel
+for N <= 16, an MFMA split-K product, trans_a == 0, ragged K); on each, C has the bits of ts_hip_gemm
 and colsum the bits of ts_hip_sum_dim0, both restated by the oracle (the
 column sum's fixed chunk order, oracle.sum_dim0_chunked, bit for bit; the
 product within the matmul tolerance of the f64 product)."""
@@ -22,8 +22,11 @@ CASES = [
     (1, 2048, 2048, 1000, 2048, 0),   # 128x128 tiles, K not a multiple of 16 or 64
     (1, 4096, 4096, 520, 4097, 1),    # unaligned B: 256x256 register tiles, element loads
     (1, 700, 300, 77, 300, 0),        # 64x64 tiles, a partial last k tile
-    (1, 1024, 10, 1024, 10, 0),       # skinny, split over K (config 4's dW2)
-    (1, 20000, 7, 300, 7, 0),         # skinny, unsplit (the chunk sums added by a pass of their own)
+    (1, 1024, 10, 1024, 10, 0),       # narrow (N <= 16, config 4's dW2): workgroup 0 adds the chunks
+    (1, 20000, 7, 300, 7, 0),         # narrow, many row blocks, ragged wave ranges
+    (1, 512, 12, 5000, 12, 0),        # narrow, 79 chunks: a partial last chunk and a partial last group
+    (1, 64, 10, 16384, 10, 0),        # sliced skinny kernel (long K, few rows): the slice sum's extra workgroup
+    (1, 16400, 3, 8256, 3, 0),        # narrow, K past its chunk table: the product, then a column-sum pass
     (1, 32, 128, 784, 128, 0),        # MFMA split-K: the column sum runs as its own pass
     (0, 512, 256, 640, 256, 0),       # trans_a == 0: product, then the column sum pass
     (1, 64, 64, 5, 64, 0),            # K shorter than one tile
@@ -126,8 +129,8 @@ def test_column_sum_order_on_special_values(oracle):
     sync()
     assert_bits_equal(out.get(), want, "ts_hip_sum_dim0")
     # 64 output rows: a split-K product, then the column-sum pass; 4096: 64x64
-    # tiles with the chunks spread over 64 tile rows; 4 columns: the skinny
-    # kernel's slice sum
+    # tiles with the chunks spread over 64 tile rows; 4 columns: the narrow
+    # kernel's workgroup 0
     for M, N in ((64, cols), (4096, cols), (4096, 4)):
         a = normal((rows, M), 22)
         xs = np.ascontiguousarray(x[:, :N])

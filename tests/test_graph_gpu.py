@@ -56,7 +56,7 @@ def _step(ps, x, t, opt, readme):
 
 
 CASES = {  # name: widths, batch, readme
-    "mlp_c4": ([784, 1024, 10], 1024, False),     # the 1024x10 products split K
+    "mlp_c4": ([784, 1024, 10], 1024, False),     # the 1024x10 products: the narrow kernel
     "readme_c1": ([784, 128], 32, True),          # forward and dW split K
     "deep": ([256, 512, 512, 128], 512, False),
 }

@@ -193,8 +193,12 @@ def test_sum_dim0(oracle, rows, cols):
 
 GEMM_SHAPES = [(1, 1, 1), (2, 2, 2), (32, 128, 784), (784, 128, 32), (129, 127, 33), (1024, 10, 1024),
                (1024, 1024, 10), (1024, 1024, 784), (784, 1024, 1024), (300, 200, 4096),
-               # skinny (N <= 16): ragged rows, K not a multiple of 4, K longer than the chunk of every wave
-               (1000, 16, 777), (63, 1, 4096), (5000, 13, 65), (70, 9, 3)]
+               # N <= 16 (the narrow kernel): ragged rows, K not a multiple of 4, ragged wave ranges
+               (1000, 16, 777), (63, 1, 4096), (5000, 13, 65), (70, 9, 3),
+               # N <= 16 over few rows with a long K: the sliced skinny kernel and its slice sum
+               (64, 10, 16384),
+               # K <= 16 (one k tile, operands straight to registers): ragged edges, K = 16 and 1
+               (129, 127, 16), (100, 33, 1)]
 
 
 def _gemm_case(oracle, ta, tb, M, N, K, seed, check_rows=None):
@@ -245,8 +249,9 @@ def test_gemm_full_size_sampled_rows(oracle, ta, tb, M, N, K):
                                    (65536, 100, 40)])
 def test_gemm_large_grid_edges(oracle, ta, tb, M, N, K):
     # enough 256x256 tiles to fill the chip: aligned layouts take the LDS-DMA
-    # kernel (clamped edge rows, a partial last k tile, K < 16), the others the
-    # register-staged one; f64 check on sampled rows, always including the last
+    # kernel (clamped edge rows, a partial last k tile), the others the
+    # register-staged one, K <= 16 the one-tile kernel; f64 check on sampled
+    # rows, always including the last
     print(f"[gemm grid] ta={ta} tb={tb} M={M} N={N} K={K}", flush=True)
     got, want = _gemm_case(oracle, bool(ta), bool(tb), M, N, K, seed=11, check_rows=16)
     assert max_rel(got, want) <= 1e-4

@@ -87,8 +87,9 @@ struct GemmArgs {
     // sum of each chunk of kColsumRows rows to colsum_part[chunk][n] (f64)
     // from the B tiles they stage anyway -- chunk c by the workgroups of tile
     // row c % tiles_m, so the work is spread over the grid -- and a pass after
-    // the product adds the chunks into colsum[n]; the skinny kernel's slice sum
-    // adds B's columns in a workgroup of its own.  Null: none.
+    // the product adds the chunks into colsum[n]; the narrow kernel and the
+    // skinny kernel's slice sum add B's columns in a workgroup of their own.
+    // Null: none.
     float *colsum;
     double *colsum_part;
     int kslice;  // skinny: k rows per slice
@@ -801,6 +802,92 @@ static void launch_dma_layout(int ta, int tb, const GemmArgs &g, hipStream_t s, 
     }
 }
 
+// ---- short contractions (K <= 16) --------------------------------------------
+//
+// One k tile: a wave's 32x32 block takes at most 8 MFMAs, so its operands go
+// from global memory straight to registers (no LDS, no barrier), and the
+// epilogue's mask and bias are loaded beside them rather than after the
+// MFMAs: one round of loads, the MFMAs, the stores.  64x64 workgroup tiles
+// of four 32x32 waves, numbered as the tiled kernels number theirs; MFMA s
+// takes k = 2s + (lane half), as a tiled kernel's k tile does, and stops at
+// the last MFMA that holds a k < K (the tiled kernels add the zero products
+// of the rest), so the stored values are the same.
+template <bool TA, bool TB, int EPI>
+__global__ __launch_bounds__(256) void gemm_short_k(GemmArgs g) {
+    int tm, tn;
+    tile_coords(g.tiles_m, g.tiles_n, blockIdx.x, tm, tn);
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    const int i0 = tm * 64 + (wave >> 1) * 32, j = tn * 64 + (wave & 1) * 32 + lrow;
+    const float *__restrict__ A = g.A;
+    const float *__restrict__ B = g.B;
+    // Every load is unconditional, at an in-bounds address (rows and columns
+    // past the edge read the last one and feed outputs that are never
+    // stored; k past K reads k = K-1 and is replaced by zero), so all of
+    // them are in flight together: a load under a condition makes the
+    // compiler wait for it before the next.
+    // The operands are issued first: the mask values are consumed early (as
+    // compare results), which waits for every load issued before them.
+    const int ia = min(i0 + lrow, g.M - 1), jb = min(j, g.N - 1);
+    float af[kBK / 2], bf[kBK / 2];
+#pragma unroll
+    for (int s = 0; s < kBK / 2; ++s) {
+        const int k = min(2 * s + lhalf, g.K - 1);
+        const float a = TA ? A[(size_t)k * g.lda + ia] : A[(size_t)ia * g.lda + k];
+        const float b = TB ? B[(size_t)jb * g.ldb + k] : B[(size_t)k * g.ldb + jb];
+        const bool in = 2 * s + lhalf < g.K;
+        af[s] = in ? a : 0.0f;
+        bf[s] = in ? b : 0.0f;
+    }
+    float mk[16], bj = 0.0f;
+    if (EPI != kEpiNone) {
+        if (g.bias) bj = g.bias[jb];  // uniform
+        if (EPI == kEpiAll && g.mask) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int i = min(i0 + 8 * (r >> 2) + 4 * lhalf + (r & 3), g.M - 1);
+                mk[r] = g.mask[(size_t)i * g.ldc + jb];
+            }
+        }
+    }
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    const int steps = (g.K + 1) / 2;  // uniform
+#pragma unroll
+    for (int s = 0; s < kBK / 2; ++s)
+        if (s < steps) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s], bf[s], acc, 0, 0, 0);
+    if (j >= g.N) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int i = i0 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+        float v = acc[r];
+        if (EPI != kEpiNone) {  // store_tile's order: bias, relu, mask
+            if (g.bias) v = v + bj;
+            if (g.relu) v = v > 0.0f ? v : 0.0f;
+            if (EPI == kEpiAll && g.mask) v = mk[r] > 0.0f ? v : 0.0f;
+        }
+        if (i < g.M) g.C[(size_t)i * g.ldc + j] = v;
+    }
+}
+
+template <int EPI>
+static void launch_short_k_as(int ta, int tb, const GemmArgs &g, dim3 grid, hipStream_t s) {
+    if (!ta && !tb) launch((gemm_short_k<false, false, EPI>), grid, dim3(256), 0, s, g);
+    else if (!ta) launch((gemm_short_k<false, true, EPI>), grid, dim3(256), 0, s, g);
+    else if (!tb) launch((gemm_short_k<true, false, EPI>), grid, dim3(256), 0, s, g);
+    else launch((gemm_short_k<true, true, EPI>), grid, dim3(256), 0, s, g);
+}
+
+static void launch_short_k(int ta, int tb, GemmArgs g, hipStream_t s) {
+    g.tiles_m = (g.M + 63) / 64;
+    g.tiles_n = (g.N + 63) / 64;
+    g.tiles = g.tiles_m * g.tiles_n;
+    const dim3 grid(static_cast<unsigned>(g.tiles));
+    if (g.bias || g.mask || g.relu) launch_short_k_as<kEpiAll>(ta, tb, g, grid, s);
+    else launch_short_k_as<kEpiNone>(ta, tb, g, grid, s);
+}
+
 }  // namespace tship
 
 using namespace tship;
@@ -829,7 +916,9 @@ static int gemm_launch(int trans_a, int trans_b, size_t M, size_t N, size_t K, c
     const size_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batches;
     const size_t mid_tiles = ((M + 127) / 128) * ((N + 127) / 128) * batches;
     const unsigned nb = static_cast<unsigned>(batches);
-    if (big_tiles >= static_cast<size_t>(device_cu_count())) {
+    if (K >= 1 && K <= static_cast<size_t>(kBK) && g.batch_rank == 0 && !g.colsum) {  // one k tile
+        launch_short_k(trans_a, trans_b, g, s);
+    } else if (big_tiles >= static_cast<size_t>(device_cu_count())) {
         if (!g.vec) launch_tiles<256, 256, 2, 4>(trans_a, trans_b, g, s, nb);
         else launch_dma_layout(trans_a, trans_b, g, s, nb);
     } else if (2 * mid_tiles >= static_cast<size_t>(device_cu_count())) {
@@ -842,9 +931,9 @@ static int gemm_launch(int trans_a, int trans_b, size_t M, size_t N, size_t K, c
 
 // ---- skinny products (N <= 16) -----------------------------------------------
 //
-// A product with at most 16 output columns (a layer with few outputs: config
-// 4's 1024x10 products) is a stream over A with N multiply-adds per element:
-// MFMA tiles would pad N to 32 or more.  A workgroup of 4 waves takes 64 rows,
+// A product with at most 16 output columns over few rows and a long K (the
+// narrow kernel below takes the rest) is a stream over A with N multiply-adds
+// per element.  A workgroup of 4 waves takes 64 rows,
 // a lane per row, and one slice of K (grid.y slices, enough row groups x
 // slices for every CU); its waves split the slice into 4 contiguous ranges.
 // A wave walks its range in chunks of 64 k: the chunk's B rows go to the
@@ -944,6 +1033,211 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny(GemmArgs g, flo
     }
 }
 
+// ---- narrow products (N <= 16) in one pass ------------------------------------
+//
+// v_mfma_f32_16x16x4f32: lane l supplies A[l%16][l/16] of a 16x4 block and
+// B[l/16][l%16] of a 4x16 block, and holds C[4*(l/16) + r][l%16] in its 4
+// accumulators.  A workgroup owns 16 rows of C with all of its (<= 16)
+// columns and all of K, split over its waves in contiguous ranges of whole
+// 64-row chunks (the column sum's); B's columns past N are read clamped to
+// column N-1 and feed outputs that are never stored.  A wave takes its range
+// a chunk per round: four 16-k blocks, all their loads at once, then 16
+// MFMAs.  Inside a block, lane group q = l/16 holds k = 4q .. 4q+3 and the
+// block's MFMA s takes k = 4q + s (A and B follow the same order), so a
+// row-major A row gives the lane its four k in one dwordx4.  The waves'
+// accumulators are added in wave order through LDS and the epilogue applied
+// at the store: one launch, no temporary.
+// Column sums of B (CS, trans_b == 0): workgroup 0 holds every row of B in
+// its registers, a chunk per wave round, so each round also adds its chunk's
+// rows in row order (lane j gathers column j's 64 values with cross-lane
+// reads, f64 from +0), the chunk sums go to LDS, and 16 threads add them in
+// the column sum's groups at the end.
+// Used while the row blocks spread over the chip or K is moderate (with
+// column sums in the kernel K <= kNarrowMaxK, the chunk table's size; past
+// it a column-sum pass follows); the sliced skinny kernel above takes long K
+// over few rows.
+constexpr int kNarrowRows = 16;
+constexpr int kNarrowMaxWaves = 16;
+constexpr size_t kNarrowMaxK = 8192;
+constexpr int kNarrowMaxChunks = static_cast<int>(kNarrowMaxK / kColsumRows);
+static_assert(kColsumRows == 64, "a narrow wave round is one column-sum chunk");
+
+// V: the k-contiguous operands (A unless TA, B when TB) take dwordx4 loads
+// (16-byte aligned, leading dimension % 4 == 0).
+template <bool TA, bool TB, bool V, bool CS>
+__global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) {
+    static_assert(!CS || !TB, "column sums of B need trans_b == 0");
+    __shared__ float red[kNarrowMaxWaves][256];
+    __shared__ double csum[CS ? kNarrowMaxChunks : 1][kSkinnyN];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int waves = blockDim.x >> 6;
+    const int m0 = blockIdx.x * kNarrowRows;
+    const int q = lane >> 4;
+    const int m = min(m0 + (lane & 15), g.M - 1);  // rows past M: never stored
+    const int n = min(lane & 15, g.N - 1);         // columns past N: never stored
+    const int kc = ((g.K + waves - 1) / waves + 63) & ~63;
+    const int kb = min(g.K, wave * kc), ke = min(g.K, kb + kc);
+    const bool cs_wg = CS && blockIdx.x == 0;  // uniform
+    const float *__restrict__ A = g.A;
+    const float *__restrict__ B = g.B;
+    auto a_at = [&](int k) { return TA ? A[(size_t)k * g.lda + m] : A[(size_t)m * g.lda + k]; };
+    auto b_at = [&](int k) { return TB ? B[(size_t)n * g.ldb + k] : B[(size_t)k * g.ldb + n]; };
+    // The epilogue's bias and mask values of the outputs this thread stores
+    // (output t = 64r + l: row 4*(l/16) + r, column l%16), loaded now at
+    // clamped addresses so they arrive with the operands.
+    constexpr int kOuts = 256 / 64;
+    float eb[kOuts] = {}, em[kOuts] = {};
+#pragma unroll
+    for (int o = 0; o < kOuts; ++o) {
+        if (o * static_cast<int>(blockDim.x) >= 256) break;  // uniform
+        const int t = static_cast<int>(threadIdx.x) + o * static_cast<int>(blockDim.x);
+        const int i = min(m0 + 4 * ((t & 63) >> 4) + ((t >> 6) & 3), g.M - 1), j = min(t & 15, g.N - 1);
+        eb[o] = g.bias ? g.bias[j] : 0.0f;
+        em[o] = g.mask ? g.mask[(size_t)i * g.ldc + j] : 1.0f;
+    }
+    f4v_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = kb; k0 < ke; k0 += 64) {
+        float av[4][4], bv[4][4];
+        if (k0 + 64 <= ke) {  // a whole chunk (uniform)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int k = k0 + 16 * u + 4 * q;
+                if (!TA && V) {
+                    const f4v_t x = *reinterpret_cast<const f4v_t *>(A + (size_t)m * g.lda + k);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) av[u][s] = x[s];
+                } else {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) av[u][s] = a_at(k + s);
+                }
+                if (TB && V) {
+                    const f4v_t x = *reinterpret_cast<const f4v_t *>(B + (size_t)n * g.ldb + k);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) bv[u][s] = x[s];
+                } else {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) bv[u][s] = b_at(k + s);
+                }
+            }
+        } else {  // the last chunk of K: k past its end reads zeros
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const int k = k0 + 16 * u + 4 * q + s;
+                    av[u][s] = k < ke ? a_at(k) : 0.0f;
+                    bv[u][s] = k < ke ? b_at(k) : 0.0f;
+                }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u][s], bv[u][s], acc, 0, 0, 0);
+        if (cs_wg) {
+            // chunk k0/64: row r = 16u + 4q + s sits in lane (column, q) as
+            // bv[u][s]; rows past K hold zeros, which add nothing to a sum
+            // that starts at +0
+            float v[64];
+#pragma unroll
+            for (int r = 0; r < 64; ++r) v[r] = __shfl(bv[r >> 4][r & 3], (lane & 15) + 16 * ((r >> 2) & 3));
+            double sum = 0.0;
+#pragma unroll
+            for (int r = 0; r < 64; ++r) sum += (double)v[r];
+            if (lane < kSkinnyN) csum[k0 >> 6][lane] = sum;
+        }
+    }
+    // The mask values stay floats in registers until here: compared as soon
+    // as they were loaded, each compare would wait for its load first.
+#pragma unroll
+    for (int o = 0; o < kOuts; ++o) asm volatile("" : "+v"(em[o]));
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][r * 64 + lane] = acc[r];
+    __syncthreads();
+#pragma unroll
+    for (int o = 0; o < kOuts; ++o) {
+        const int t = static_cast<int>(threadIdx.x) + o * static_cast<int>(blockDim.x);
+        if (t >= 256) break;  // uniform per wave
+        float v = red[0][t];
+        for (int w = 1; w < waves; ++w) v += red[w][t];
+        const int l = t & 63;
+        const int i = m0 + 4 * (l >> 4) + (t >> 6), j = l & 15;
+        if (g.bias) v = v + eb[o];  // epilogue()'s order: bias, relu, mask
+        if (g.relu) v = v > 0.0f ? v : 0.0f;
+        if (g.mask) v = em[o] > 0.0f ? v : 0.0f;
+        if (i < g.M && j < g.N) g.C[(size_t)i * g.ldc + j] = v;
+    }
+    if (cs_wg && static_cast<int>(threadIdx.x) < g.N) {
+        // the chunk sums in groups of kColsumGroup, each from +0
+        constexpr int G = static_cast<int>(kColsumGroup);
+        const int j = threadIdx.x, chunks = (g.K + 63) >> 6;
+        double total = 0.0;
+        for (int c0 = 0; c0 < chunks; c0 += G) {
+            double x[G];
+#pragma unroll
+            for (int i = 0; i < G; ++i) x[i] = csum[min(c0 + i, chunks - 1)][j];
+            double grp = 0.0;
+#pragma unroll
+            for (int i = 0; i < G; ++i)
+                if (c0 + i < chunks) grp += x[i];
+            total += grp;
+        }
+        g.colsum[j] = static_cast<float>(total);
+    }
+}
+
+// Waves per narrow workgroup: the largest power of two up to 16 that leaves
+// each wave at least 64 k.
+static int narrow_waves(size_t K) {
+    int w = 1;
+    while (w < kNarrowMaxWaves && static_cast<size_t>(2 * w) * 64 <= K) w *= 2;
+    return w;
+}
+
+static bool narrow_fits(size_t M, size_t K) {
+    const size_t blocks = (M + kNarrowRows - 1) / kNarrowRows;
+    return K <= kNarrowMaxK || 8 * blocks >= static_cast<size_t>(device_cu_count());
+}
+
+template <bool CS>
+static void launch_narrow_as(int trans_a, int trans_b, bool v, const GemmArgs &g, dim3 grid, dim3 block,
+                             hipStream_t s) {
+    if (!trans_a && !trans_b) {
+        if (v) launch((gemm_narrow<false, false, true, CS>), grid, block, 0, s, g);
+        else launch((gemm_narrow<false, false, false, CS>), grid, block, 0, s, g);
+    } else if (!trans_b) {
+        launch((gemm_narrow<true, false, false, CS>), grid, block, 0, s, g);
+    } else if (!CS) {  // column sums need trans_b == 0 (checked by the caller)
+        if (!trans_a) {
+            if (v) launch((gemm_narrow<false, true, true, false>), grid, block, 0, s, g);
+            else launch((gemm_narrow<false, true, false, false>), grid, block, 0, s, g);
+        } else {
+            if (v) launch((gemm_narrow<true, true, true, false>), grid, block, 0, s, g);
+            else launch((gemm_narrow<true, true, false, false>), grid, block, 0, s, g);
+        }
+    }
+}
+
+// g carries the epilogue and, optionally, colsum (trans_b == 0, K <= kNarrowMaxK).
+static int launch_narrow(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A, size_t lda,
+                         const float *B, size_t ldb, float *C, size_t ldc, GemmArgs g, void *stream) {
+    if (!A || !B) return TS_HIP_EINVAL;
+    if (lda < (trans_a ? M : K) || ldb < (trans_b ? K : N)) return TS_HIP_EINVAL;
+    const size_t lim = 0x7ffffe00ULL;
+    if (M > lim || K > lim || lda > lim || ldb > lim || ldc > lim) return TS_HIP_EINVAL;
+    if (g.colsum && (trans_b || K > kNarrowMaxK)) return TS_HIP_EINVAL;
+    g.A = A; g.B = B; g.C = C;
+    g.M = static_cast<int>(M); g.N = static_cast<int>(N); g.K = static_cast<int>(K);
+    g.lda = static_cast<int>(lda); g.ldb = static_cast<int>(ldb); g.ldc = static_cast<int>(ldc);
+    const bool va = trans_a || (aligned16(A) && lda % 4 == 0);
+    const bool vb = !trans_b || (aligned16(B) && ldb % 4 == 0);
+    const dim3 grid(static_cast<unsigned>((M + kNarrowRows - 1) / kNarrowRows)), block(64 * narrow_waves(K));
+    hipStream_t s = as_stream(stream);
+    if (g.colsum) launch_narrow_as<true>(trans_a, trans_b, va && vb, g, grid, block, s);
+    else launch_narrow_as<false>(trans_a, trans_b, va && vb, g, grid, block, s);
+    return launch_status();
+}
+
 static bool skinny(size_t N) { return N <= static_cast<size_t>(kSkinnyN); }
 
 // Slices of K for a skinny product: enough (row group x slice) workgroups for
@@ -1023,9 +1317,11 @@ static int split_slices(size_t M, size_t N, size_t K) {
 // Workspace of one product: the split temporary (slices * M * N floats) and,
 // with column sums of B, colsum_chunk_count(K) * N doubles of chunk sums after
 // it (8-byte aligned) -- written by the product's kernels (trans_a == 1,
-// unsplit or skinny) or by a column-sum pass after the product.
+// unsplit, or the sliced skinny kernel) or by a column-sum pass after the
+// product.  The narrow kernel needs neither.
 struct GemmPlan {
     bool skinny = false;
+    bool narrow = false;  // skinny, in one pass (no temporary; column sums in the kernel)
     int slices = 1;
     size_t split_floats = 0;
     size_t part_floats = 0;
@@ -1038,10 +1334,12 @@ static GemmPlan gemm_plan(int trans_a, int trans_b, size_t M, size_t N, size_t K
     GemmPlan p;
     if (M == 0 || N == 0 || K == 0) return p;
     p.skinny = skinny(N);
-    p.slices = p.skinny ? skinny_slices(M, K) : split_slices(M, N, K);
+    p.narrow = p.skinny && narrow_fits(M, K);  // the same kernel with or without column sums
+    p.slices = p.narrow ? 1 : p.skinny ? skinny_slices(M, K) : split_slices(M, N, K);
     p.split_floats = p.slices > 1 ? static_cast<size_t>(p.slices) * M * N : 0;
-    p.cs_kernel = colsum && !p.skinny && p.slices == 1 && trans_a && !trans_b;
-    p.part_floats = colsum ? 2 * colsum_chunk_count(K) * N : 0;
+    p.cs_kernel = colsum && (p.narrow ? K <= kNarrowMaxK : !p.skinny && p.slices == 1 && trans_a && !trans_b);
+    // chunk sums in the workspace, except where the narrow kernel keeps them in LDS
+    p.part_floats = colsum && !(p.narrow && p.cs_kernel) ? 2 * colsum_chunk_count(K) * N : 0;
     return p;
 }
 
@@ -1086,7 +1384,17 @@ static int gemm_plain(int trans_a, int trans_b, size_t M, size_t N, size_t K, co
     }
     double *part = plan.part_floats ? reinterpret_cast<double *>(W + plan.part_offset()) : nullptr;
     int status;
-    if (plan.skinny) {  // few output columns: the skinny kernel, K split over the CUs
+    if (plan.narrow) {  // few output columns, one pass
+        GemmArgs g{};
+        g.bias = bias;
+        g.mask = mask;
+        g.relu = relu;
+        if (plan.cs_kernel) g.colsum = colsum;
+        status = launch_narrow(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, g, stream);
+        if (status == TS_HIP_OK && colsum && !plan.cs_kernel)  // K past the kernel's chunk table
+            status = launch_colsum(B, nullptr, K, N, ldb, colsum, reinterpret_cast<float *>(part), plan.part_floats,
+                                   stream);
+    } else if (plan.skinny) {  // few output columns over few rows: K split over the CUs
         GemmArgs g{};
         g.bias = bias;
         g.mask = mask;
