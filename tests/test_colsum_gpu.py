@@ -18,6 +18,7 @@ pytestmark = pytest.mark.gpu
 # (trans_a, M, N, K, B row pitch, B offset in floats): the path each takes
 CASES = [
     (1, 4096, 4096, 8192, 4096, 0),   # 256x256 LDS-DMA tiles (config 5's dW)
+    (1, 4096, 4096, 1000, 4096, 0),   # LDS-DMA, 31 two-sub-tile stages and a partial last sub-tile
     (1, 784, 1024, 1024, 1024, 0),    # 64x64 register tiles (config 4's dW1)
     (1, 2048, 2048, 1000, 2048, 0),   # 128x128 tiles, K not a multiple of 16 or 64
     (1, 4096, 4096, 520, 4097, 1),    # unaligned B: 256x256 register tiles, element loads

@@ -546,15 +546,18 @@ struct DmaStage {
 
 // 256x256 tiles, WM x WN waves.  SCHED 1 spreads the next step pair's LDS
 // reads over the current pair's MFMAs; SCHED 0 issues them as one group
-// ahead of the MFMAs (measured per layout, see the launcher).
-template <bool TA, bool TB, int WM, int WN, int SCHED, int EPI, bool CS>
+// ahead of the MFMAs (measured per layout, see the launcher).  Each of the two
+// LDS stages holds SUB consecutive 16-k sub-tiles (one barrier per stage).
+template <bool TA, bool TB, int WM, int WN, int SCHED, int EPI, bool CS, int SUB = 1>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_lds_dma(GemmArgs g) {
     constexpr int BM = 256, BN = 256, NW = WM * WN;
     constexpr int TMW = BM / WM, TNW = BN / WN, FM = TMW / 32, FN = TNW / 32, PAIRS = kBK / 4;
+    constexpr int SPAIRS = SUB * PAIRS;  // step pairs per stage
+    static_assert(SUB == 1 || SUB == 2, "one or two sub-tiles per stage");
     using SA = DmaStage<!TA, NW>;
     using SB = DmaStage<TB, NW>;
-    __shared__ __attribute__((aligned(16))) float As[2][kBK * BM];
-    __shared__ __attribute__((aligned(16))) float Bs[2][kBK * BN];
+    __shared__ __attribute__((aligned(16))) float As[2][SUB * kBK * BM];
+    __shared__ __attribute__((aligned(16))) float Bs[2][SUB * kBK * BN];
 
     const float *Ap = g.A, *Bp = g.B;
     float *Cp = g.C;
@@ -610,17 +613,22 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_lds_dma(GemmArgs g) {
         cs_s = 0.0;
     };
 
-    const int nfull = g.K / kBK;  // whole k tiles; a partial one is done after the loop
+    const int nfull = g.K / (SUB * kBK);  // whole stages; the rest, sub-tile by sub-tile after the loop
     auto dma = [&](int kt, int buf) {
-        SA::dma(Ap, g.lda, g.M, i0, kt * kBK, As[buf], wave, lane);
-        SB::dma(Bp, g.ldb, g.N, j0, kt * kBK, Bs[buf], wave, lane);
+#pragma unroll
+        for (int s = 0; s < SUB; ++s) {
+            SA::dma(Ap, g.lda, g.M, i0, (kt * SUB + s) * kBK, As[buf] + s * kBK * BM, wave, lane);
+            SB::dma(Bp, g.ldb, g.N, j0, (kt * SUB + s) * kBK, Bs[buf] + s * kBK * BN, wave, lane);
+        }
     };
     f2v F[2][FM + FN];
-    auto rd = [&](int buf, int j, f2v (&f)[FM + FN]) {
+    auto rd = [&](int buf, int j, f2v (&f)[FM + FN]) {  // step pair j of a stage
+        const float *Sa = As[buf] + (j / PAIRS) * kBK * BM;
+        const float *Sb = Bs[buf] + (j / PAIRS) * kBK * BN;
 #pragma unroll
-        for (int a = 0; a < FM; ++a) f[a] = SA::frag(As[buf], j, lhalf, wm * TMW + a * 32 + lrow);
+        for (int a = 0; a < FM; ++a) f[a] = SA::frag(Sa, j % PAIRS, lhalf, wm * TMW + a * 32 + lrow);
 #pragma unroll
-        for (int b = 0; b < FN; ++b) f[FM + b] = SB::frag(Bs[buf], j, lhalf, wn * TNW + b * 32 + lrow);
+        for (int b = 0; b < FN; ++b) f[FM + b] = SB::frag(Sb, j % PAIRS, lhalf, wn * TNW + b * 32 + lrow);
     };
     auto mm = [&](const f2v (&f)[FM + FN]) {
 #pragma unroll
@@ -645,9 +653,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_lds_dma(GemmArgs g) {
         }
     };
 
-    // Pipeline: LDS buffer kt&1 holds tile kt; tile kt+1 is in flight into the
-    // other buffer; the registers F[j&1] hold step pair j.  Each wave waits for
-    // its own DMA (vmcnt) before the barrier that publishes the tile.
+    // Pipeline: LDS buffer kt&1 holds stage kt; stage kt+1 is in flight into
+    // the other buffer; the registers F[j&1] hold step pair j.  Each wave
+    // waits for its own DMA (vmcnt) before the barrier that publishes a stage.
+    // CS: the 4 k rows of B of step pair p of stage kt (sub-tile t16 of 16 k)
+    // are added before the barrier that frees the buffer; a chunk's fourth
+    // sub-tile closes it.
+    auto cs_pair = [&](int kt, int p) {
+        const int t16 = kt * SUB + p / PAIRS, jj = p % PAIRS;
+        if (cs_wave && cs_mine(t16)) {
+            cs_rows(Bs[kt & 1] + (p / PAIRS) * kBK * BN, 4 * jj, 4 * jj + 4);
+            if (jj == PAIRS - 1 && (t16 & 3) == 3) cs_flush(t16 >> 2);
+        }
+    };
     if (nfull > 0) {
         dma(0, 0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -658,51 +676,54 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_lds_dma(GemmArgs g) {
     for (int kt = 0; kt < nfull; ++kt) {
         const int cur = kt & 1;
 #pragma unroll
-        for (int j = 0; j < PAIRS - 1; ++j) {
+        for (int j = 0; j < SPAIRS - 1; ++j) {
             rd(cur, j + 1, F[(j + 1) & 1]);
             if (SCHED == 0) __builtin_amdgcn_sched_barrier(0);
             mm(F[j & 1]);
             order();
             __builtin_amdgcn_sched_barrier(0);
-            if (cs_wave && cs_mine(kt)) {  // this tile's rows, before the barrier that frees its buffer
-                cs_rows(Bs[cur], 4 * j, 4 * j + 4);
-                if (j == PAIRS - 2) {
-                    cs_rows(Bs[cur], 4 * j + 4, kBK);
-                    if ((kt & 3) == 3) cs_flush(kt >> 2);
-                }
+            if (CS) {
+                cs_pair(kt, j);
+                if (j == SPAIRS - 2) cs_pair(kt, j + 1);
             }
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        // Tile kt+1 is published and every read of buffer cur is done: read
-        // the next tile's first pair and start tile kt+2 into buffer cur, then
-        // run this tile's last pair.  On the last tiles the DMA repeats tile
-        // nfull-1 and the read takes an idle buffer: both stay in bounds.
+        // Stage kt+1 is published and every read of buffer cur is done: read
+        // the next stage's first pair and start stage kt+2 into buffer cur,
+        // then run this stage's last pair.  On the last stages the DMA repeats
+        // stage nfull-1 and the read takes an idle buffer: both stay in bounds.
         rd(cur ^ 1, 0, F[0]);
         dma(kt + 2 < nfull ? kt + 2 : nfull - 1, cur);
         if (SCHED == 0) __builtin_amdgcn_sched_barrier(0);
-        mm(F[(PAIRS - 1) & 1]);
+        mm(F[(SPAIRS - 1) & 1]);
         order();
         __builtin_amdgcn_sched_barrier(0);
     }
-    if (nfull * kBK < g.K) {
+    // the sub-tiles past the last whole stage (the last may be partial), one
+    // at a time through buffer nfull&1 (idle: every DMA has landed and every
+    // read passed the barrier)
+    const int buf = nfull & 1;
+    for (int t16 = nfull * SUB; t16 * kBK < g.K; ++t16) {  // uniform
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        const int buf = nfull & 1;
-        SA::guarded(Ap, g.lda, g.M, g.K, i0, nfull * kBK, As[buf], wave, lane);
-        SB::guarded(Bp, g.ldb, g.N, g.K, j0, nfull * kBK, Bs[buf], wave, lane);
+        SA::guarded(Ap, g.lda, g.M, g.K, i0, t16 * kBK, As[buf], wave, lane);
+        SB::guarded(Bp, g.ldb, g.N, g.K, j0, t16 * kBK, Bs[buf], wave, lane);
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < PAIRS; ++j) {
             rd(buf, j, F[0]);
             mm(F[0]);
         }
-        if (cs_wave && cs_mine(nfull)) cs_rows(Bs[buf], 0, kBK);  // zeros past K add nothing
+        if (cs_wave && cs_mine(t16)) {  // zeros past K add nothing
+            cs_rows(Bs[buf], 0, kBK);
+            if ((t16 & 3) == 3) cs_flush(t16 >> 2);
+        }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA outstanding at exit
-    if (CS) {  // the last chunk, unless the loop ended exactly on it
+    if (CS) {  // the last chunk, unless its fourth sub-tile closed it
         const int last = (g.K - 1) / kBK;
-        if (cs_wave && cs_mine(last) && !(last < nfull && (last & 3) == 3)) cs_flush(last >> 2);
+        if (cs_wave && cs_mine(last) && (last & 3) != 3) cs_flush(last >> 2);
     }
 
     store_tile<EPI, FM, FN>(g, acc, Cp, i0 + wm * TMW, j0 + wn * TNW, lrow, lhalf);
@@ -768,18 +789,20 @@ __global__ __launch_bounds__(kBlock) void splitk_sum(const float *__restrict__ P
     C[i * ldc + j] = epilogue(e, acc, static_cast<int>(i), static_cast<int>(j));
 }
 
-template <bool TA, bool TB, int WM, int WN, int SCHED, int EPI, bool CS = false>
+template <bool TA, bool TB, int WM, int WN, int SCHED, int EPI, bool CS = false, int SUB = 1>
 static void launch_dma(GemmArgs g, hipStream_t s, unsigned batches) {
     g.tiles_m = (g.M + 255) / 256;
     g.tiles_n = (g.N + 255) / 256;
     g.tiles = g.tiles_m * g.tiles_n;
     dim3 grid(static_cast<unsigned>(g.tiles) * batches);
     dim3 block(64 * WM * WN);
-    launch((gemm_f32_lds_dma<TA, TB, WM, WN, SCHED, EPI, CS>), grid, block, 0, s, g);
+    launch((gemm_f32_lds_dma<TA, TB, WM, WN, SCHED, EPI, CS, SUB>), grid, block, 0, s, g);
 }
 
-// The DMA kernel of one layout: wave grid and LDS-read order per layout, the
-// fastest measured at 8192x4096x4096 (only these instantiations exist).  A
+// The DMA kernel of one layout: wave grid, LDS-read order and sub-tiles per
+// stage per layout, the fastest measured at 8192x4096x4096 (only these
+// instantiations exist; two sub-tiles per stage measured slower for NN and NT,
+// about 1.5% faster for TN).  A
 // mask epilogue on NN takes the 8-wave grid: the 4-wave one holds its
 // accumulators in AGPRs and has no registers left for a row of mask values
 // (it spills); bias and relu alone fit.
@@ -792,10 +815,10 @@ static void launch_dma_layout(int ta, int tb, const GemmArgs &g, hipStream_t s, 
     } else if (!ta && tb) {
         if (epi) launch_dma<false, true, 2, 4, 0, kEpiAll>(g, s, nb);
         else launch_dma<false, true, 2, 4, 0, kEpiNone>(g, s, nb);
-    } else if (ta && !tb) {
-        if (g.colsum) launch_dma<true, false, 2, 4, 1, kEpiNone, true>(g, s, nb);  // dW with db
-        else if (epi) launch_dma<true, false, 2, 4, 1, kEpiAll>(g, s, nb);
-        else launch_dma<true, false, 2, 4, 1, kEpiNone>(g, s, nb);
+    } else if (ta && !tb) {  // two sub-tiles per stage: measured faster for this layout only
+        if (g.colsum) launch_dma<true, false, 2, 4, 1, kEpiNone, true, 2>(g, s, nb);  // dW with db
+        else if (epi) launch_dma<true, false, 2, 4, 1, kEpiAll, false, 2>(g, s, nb);
+        else launch_dma<true, false, 2, 4, 1, kEpiNone, false, 2>(g, s, nb);
     } else {
         if (epi) launch_dma<true, true, 2, 4, 1, kEpiAll>(g, s, nb);
         else launch_dma<true, true, 2, 4, 1, kEpiNone>(g, s, nb);
