@@ -83,13 +83,14 @@ struct GemmArgs {
     const float *mask;
     int relu;
     // Column sums of B (trans_b == 0; the bias gradient beside a weight
-    // gradient) in the column sum's fixed order.  The MFMA kernels write the
-    // sum of each chunk of kColsumRows rows to colsum_part[chunk][n] (f64)
-    // from the B tiles they stage anyway -- chunk c by the workgroups of tile
+    // gradient) in the column sum's fixed order.  The LDS-DMA kernel writes
+    // the sum of each chunk of kColsumRows rows to colsum_part[chunk][n] (f64)
+    // from the B tiles it stages anyway -- chunk c by the workgroups of tile
     // row c % tiles_m, so the work is spread over the grid -- and a pass after
-    // the product adds the chunks into colsum[n]; the narrow kernel and the
-    // skinny kernel's slice sum add B's columns in a workgroup of their own.
-    // Null: none.
+    // the product adds the chunks into colsum[n]; the register-staged tiles
+    // append a workgroup per 16 columns to their grid, the narrow kernel's
+    // first workgroup and the skinny kernel's slice sum add B's columns as
+    // they go.  Null: none.
     float *colsum;
     double *colsum_part;
     int kslice;  // skinny: k rows per slice
@@ -264,6 +265,50 @@ __device__ inline void tile_coords(int tiles_m, int tiles_n, int b, int &tm, int
     tn = in_group / gsz;
 }
 
+// Column sums of B ([K][N], trans_b == 0) for 16 columns, j0 .. j0+15, in
+// the column sum's order, by one workgroup of NT threads: in rounds of
+// NT/16 chunks, thread (chunk q, column j) adds its chunk's rows from +0 in
+// f64 (16 rows in flight at a time, rows past K read in bounds and not
+// added), then thread j adds the round's groups of chunk sums, each from +0,
+// into its running total, and finally stores it.
+constexpr int kStripCols = 16;
+
+template <int NT>
+__device__ void colsum_strip(const GemmArgs &g, int j0) {
+    constexpr int R = static_cast<int>(kColsumRows), G = static_cast<int>(kColsumGroup), RC = NT / kStripCols;
+    static_assert(RC * kStripCols == NT && RC % G == 0, "a round holds whole groups of chunks");
+    __shared__ double cs[RC][kStripCols];
+    const int t = static_cast<int>(threadIdx.x), q = t / kStripCols, j = t % kStripCols;
+    const int col = min(j0 + j, g.N - 1);
+    const int chunks = (g.K + R - 1) / R;
+    double total = 0.0;
+    for (int c0 = 0; c0 < chunks; c0 += RC) {  // uniform
+        const int r0 = (c0 + q) * R;
+        double sum = 0.0;
+        for (int rb = 0; rb < R; rb += 16) {
+            float v[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) v[r] = g.B[(size_t)min(r0 + rb + r, g.K - 1) * g.ldb + col];
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (r0 + rb + r < g.K) sum += (double)v[r];
+        }
+        cs[q][j] = sum;
+        __syncthreads();
+        if (t < kStripCols) {
+#pragma unroll
+            for (int h = 0; h < RC / G; ++h) {
+                double grp = 0.0;
+#pragma unroll
+                for (int i = 0; i < G; ++i) grp += cs[h * G + i][t];
+                total += grp;
+            }
+        }
+        __syncthreads();
+    }
+    if (t < kStripCols && j0 + t < g.N) g.colsum[j0 + t] = static_cast<float>(total);
+}
+
 // EPI: the epilogue kind applied at the store (a separate instantiation per
 // kind, so the bare product keeps its register allocation).  PF: operand tiles
 // prefetched into registers ahead of the LDS stage (deeper for small tiles,
@@ -272,9 +317,16 @@ __device__ inline void tile_coords(int tiles_m, int tiles_n, int b, int &tm, int
 // dwordx4 loads whose rows are clamped into the operand (rows past an M / N
 // edge feed outputs that are never stored), and a partial last tile follows
 // it with element loads; otherwise every tile takes bounds-checked element
-// loads (zeros outside).
+// loads (zeros outside).  CS (column sums of B): workgroups past the g.tiles
+// product tiles each take a strip of kStripCols columns (colsum_strip); the
+// grid has no other idle work for them.
 template <bool TA, bool TB, int BM, int BN, int WM, int WN, int EPI, int PF, bool VEC, bool CS = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
+    static_assert(!CS || !TB, "column sums of B need trans_b == 0");
+    if (CS && static_cast<int>(blockIdx.x) >= g.tiles) {  // uniform
+        colsum_strip<64 * WM * WN>(g, (static_cast<int>(blockIdx.x) - g.tiles) * kStripCols);
+        return;
+    }
     constexpr int NT = 64 * WM * WN;
     constexpr int TMW = BM / WM, TNW = BN / WN;  // wave tile
     constexpr int FM = TMW / 32, FN = TNW / 32;  // 32x32 accumulators per wave
@@ -320,24 +372,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
         for (int b = 0; b < FN; ++b)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
-
-    // CS: the chunk sums of B's columns (GemmArgs::colsum_part) by the first
-    // BN threads, one column each, from the B tiles in LDS; chunk c (four k
-    // tiles) by the workgroups of tile row c % tiles_m.
-    static_assert(!CS || !TB, "column sums of B need trans_b == 0");
-    const bool cs_thread = CS && static_cast<int>(threadIdx.x) < BN;
-    const int cs_c = static_cast<int>(threadIdx.x) % BN;
-    double cs_s = 0.0;
-    auto cs_mine = [&](int kt) { return ((kt >> 2) % g.tiles_m) == tm; };  // uniform
-    auto cs_flush = [&](int chunk) {
-        if (j0 + cs_c < g.N) g.colsum_part[(size_t)chunk * g.N + j0 + cs_c] = cs_s;
-        cs_s = 0.0;
-    };
-    auto cs_tile = [&](const float *Bc, int kt) {
-#pragma unroll
-        for (int k = 0; k < kBK; ++k) cs_s += (double)Bc[k * BN + (cs_c ^ swz(k))];
-        if ((kt & 3) == 3) cs_flush(kt >> 2);
-    };
 
     // One k tile from LDS: every operand read, then the MFMAs in k order
     // (the reads complete in order, so each MFMA waits only for its own).
@@ -397,7 +431,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
                 // scheduler can place the stores and loads in the MFMAs'
                 // shadow (a wave issues in order).
                 mma(As[cur], Bs[cur]);
-                if (cs_thread && cs_mine(kt)) cs_tile(Bs[cur], kt);
                 SA::store(As[cur ^ 1], ra[u]);
                 SB::store(Bs[cur ^ 1], rb[u]);
                 load(kt + 1 + PF, ra[u], rb[u]);
@@ -413,11 +446,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
         SB::store(Bs[0], pb);
         __syncthreads();
         mma(As[0], Bs[0]);
-        if (cs_thread && cs_mine(nt)) cs_tile(Bs[0], nt);  // zeros past K add nothing
-    }
-    if (CS) {  // the last chunk, unless a tile ended exactly on it
-        const int last = (g.K - 1) / kBK;
-        if (cs_thread && cs_mine(last) && (last & 3) != 3) cs_flush(last >> 2);
     }
     store_tile<EPI, FM, FN>(g, acc, Cp, i0 + wm * TMW, j0 + wn * TNW, lrow, lhalf);
 }
@@ -452,6 +480,8 @@ static void launch_tiles(int ta, int tb, GemmArgs g, hipStream_t s, unsigned bat
     g.tiles_n = (g.N + BN - 1) / BN;
     g.tiles = g.tiles_m * g.tiles_n;
     dim3 grid(static_cast<unsigned>(g.tiles) * batches);
+    // column sums (2-D dW with db): a strip workgroup per 16 columns after the tiles
+    if (g.colsum && ta && !tb) grid.x += static_cast<unsigned>((g.N + kStripCols - 1) / kStripCols);
     dim3 block(64 * WM * WN);
     if (g.bias || g.mask || g.relu) launch_tiles_as<BM, BN, WM, WN, kEpiAll>(ta, tb, g, grid, block, s);
     else launch_tiles_as<BM, BN, WM, WN, kEpiNone>(ta, tb, g, grid, block, s);
@@ -915,6 +945,16 @@ static void launch_short_k(int ta, int tb, GemmArgs g, hipStream_t s) {
 
 using namespace tship;
 
+// Enough 256x256 tiles to fill every CU: the LDS-DMA kernel when the operands
+// allow dwordx4 loads (vec), else 256x256 register-staged tiles.
+static bool big_grid(size_t M, size_t N, size_t batches) {
+    return ((M + 255) / 256) * ((N + 255) / 256) * batches >= static_cast<size_t>(device_cu_count());
+}
+
+static bool vec_operands(const float *A, size_t lda, const float *B, size_t ldb) {
+    return aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0);
+}
+
 // Argument checks and kernel selection shared by the plain and batched forms.
 static int gemm_launch(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A, size_t lda,
                        const float *B, size_t ldb, float *C, size_t ldc, GemmArgs g, size_t batches,
@@ -932,16 +972,15 @@ static int gemm_launch(int trans_a, int trans_b, size_t M, size_t N, size_t K, c
     g.tiles_m = g.tiles_n = 0;
     bool strides4 = true;
     for (int k = 0; k < g.batch_rank; ++k) strides4 = strides4 && g.sa[k] % 4 == 0 && g.sb[k] % 4 == 0;
-    g.vec = aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) && strides4;
+    g.vec = vec_operands(A, lda, B, ldb) && strides4;
     hipStream_t s = as_stream(stream);
     // 256x256 tiles once they alone fill every CU; 128x128 while those give at
     // least half as many workgroups as CUs; 64x64 (4 waves of 32x32) below.
-    const size_t big_tiles = ((M + 255) / 256) * ((N + 255) / 256) * batches;
     const size_t mid_tiles = ((M + 127) / 128) * ((N + 127) / 128) * batches;
     const unsigned nb = static_cast<unsigned>(batches);
     if (K >= 1 && K <= static_cast<size_t>(kBK) && g.batch_rank == 0 && !g.colsum) {  // one k tile
         launch_short_k(trans_a, trans_b, g, s);
-    } else if (big_tiles >= static_cast<size_t>(device_cu_count())) {
+    } else if (big_grid(M, N, batches)) {
         if (!g.vec) launch_tiles<256, 256, 2, 4>(trans_a, trans_b, g, s, nb);
         else launch_dma_layout(trans_a, trans_b, g, s, nb);
     } else if (2 * mid_tiles >= static_cast<size_t>(device_cu_count())) {
@@ -1339,9 +1378,10 @@ static int split_slices(size_t M, size_t N, size_t K) {
 
 // Workspace of one product: the split temporary (slices * M * N floats) and,
 // with column sums of B, colsum_chunk_count(K) * N doubles of chunk sums after
-// it (8-byte aligned) -- written by the product's kernels (trans_a == 1,
-// unsplit, or the sliced skinny kernel) or by a column-sum pass after the
-// product.  The narrow kernel needs neither.
+// it (8-byte aligned) -- written by the LDS-DMA kernel (then added by
+// colsum_final) or by a column-sum pass after the product.  The narrow kernel
+// and the register-staged tiles (column strips in their own grid) write the
+// column sums directly.
 struct GemmPlan {
     bool skinny = false;
     bool narrow = false;  // skinny, in one pass (no temporary; column sums in the kernel)
@@ -1361,8 +1401,10 @@ static GemmPlan gemm_plan(int trans_a, int trans_b, size_t M, size_t N, size_t K
     p.slices = p.narrow ? 1 : p.skinny ? skinny_slices(M, K) : split_slices(M, N, K);
     p.split_floats = p.slices > 1 ? static_cast<size_t>(p.slices) * M * N : 0;
     p.cs_kernel = colsum && (p.narrow ? K <= kNarrowMaxK : !p.skinny && p.slices == 1 && trans_a && !trans_b);
-    // chunk sums in the workspace, except where the narrow kernel keeps them in LDS
-    p.part_floats = colsum && !(p.narrow && p.cs_kernel) ? 2 * colsum_chunk_count(K) * N : 0;
+    // chunk sums in the workspace: a column-sum pass's, or the LDS-DMA kernel's
+    // (sized whenever the grid could take that kernel: alignment is not known here)
+    const bool dma_cs = p.cs_kernel && !p.narrow && big_grid(M, N, 1);
+    p.part_floats = colsum && (!p.cs_kernel || dma_cs) ? 2 * colsum_chunk_count(K) * N : 0;
     return p;
 }
 
@@ -1458,9 +1500,9 @@ static int gemm_plain(int trans_a, int trans_b, size_t M, size_t N, size_t K, co
             g.colsum_part = part;
         }
         status = gemm_launch(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, g, 1, stream);
-        if (status == TS_HIP_OK && plan.cs_kernel)
-            status = launch_colsum_final(part, colsum_chunk_count(K), N, colsum, st);
-        else if (status == TS_HIP_OK && colsum)
+        if (status == TS_HIP_OK && plan.cs_kernel && big_grid(M, N, 1) && vec_operands(A, lda, B, ldb))
+            status = launch_colsum_final(part, colsum_chunk_count(K), N, colsum, st);  // the DMA kernel's chunks
+        else if (status == TS_HIP_OK && colsum && !plan.cs_kernel)  // (register tiles: written by their strips)
             status = launch_colsum(B, nullptr, K, N, ldb, colsum, reinterpret_cast<float *>(part), plan.part_floats,
                                    stream);
     }
