@@ -15,11 +15,13 @@
  * caller can panic with a message from ts_hip_error_string().
  *
  * All tensor pointers are device pointers to contiguous row-major f32 data.
- * Launchers are asynchronous on `stream`.  They allocate nothing, with one
- * exception: ts_hip_gemm (and ts_hip_matmul, which calls it) takes a split-K
+ * Launchers are asynchronous on `stream`.  They allocate nothing, with two
+ * exceptions: ts_hip_gemm (and ts_hip_matmul, which calls it) takes a split-K
  * temporary from the stream-ordered allocator for few output tiles with a
- * long K.  ts_hip_gemm_fused (caller's workspace) and ts_hip_gemm_noalloc
- * (fixed device array) compute the same products without allocating.
+ * long K, and ts_hip_gemm_colsum given a NULL workspace takes its workspace
+ * from the same allocator.  ts_hip_gemm_fused (caller's workspace) and
+ * ts_hip_gemm_noalloc (fixed device array) compute ts_hip_gemm's products
+ * without allocating, and ts_hip_gemm_colsum does with a workspace.
  * No torch or HIP types appear in these signatures.
  */
 #ifndef TS_HIP_H
@@ -385,8 +387,10 @@ int ts_hip_gemm_fused(int trans_a, int trans_b, size_t M, size_t N, size_t K, co
  * grad_fn/utils.rs:23-60, i.e. sum_dims(&[0]) of reductions/sum.rs:225-306):
  *   C[M,N] = op(A)[M,K] . B[K,N]   as ts_hip_gemm(trans_a, 0, ...) computes it
  *   colsum[n] = sum over k of B[k*ldb + n]   with the bits of ts_hip_sum_dim0
- * With trans_a == 1 (dW = X^T . dY) the product's own workgroups add B's
- * columns from the tiles they stage, so dY is read once; other shapes take a
+ * With trans_a == 1 (dW = X^T . dY) the product's own launch adds B's
+ * columns: from the B tiles it stages (large aligned products, then a short
+ * combine pass), from workgroups appended to its grid (register-staged tiles),
+ * or from the rows its first workgroup holds (N <= 16); other shapes take a
  * column-sum pass after the product.  M == 0 gives the column sums alone.
  * Workspace as ts_hip_gemm_colsum_workspace_floats (8-byte aligned; NULL:
  * taken from the stream-ordered allocator). */
