@@ -28,8 +28,10 @@ CASES = [
     (1, 512, 12, 5000, 12, 0),        # narrow, 79 chunks: a partial last chunk and a partial last group
     (1, 64, 10, 16384, 10, 0),        # sliced skinny kernel (long K, few rows): the slice sum's extra workgroup
     (1, 16400, 3, 8256, 3, 0),        # narrow, K past its chunk table: the product, then a column-sum pass
-    (1, 32, 128, 784, 128, 0),        # MFMA split-K: the column sum runs as its own pass
-    (0, 512, 256, 640, 256, 0),       # trans_a == 0: product, then the column sum pass
+    (1, 32, 128, 784, 128, 0),        # narrow kernel, 8 column blocks (the README step's dW shape, transposed)
+    (1, 32, 128, 16384, 128, 0),      # MFMA split-K: the column sum runs as its own pass
+    (0, 512, 256, 640, 256, 0),       # trans_a == 0 through the narrow kernel
+    (0, 2048, 2048, 100, 2048, 0),    # trans_a == 0 on 128x128 tiles: product, then the column sum pass
     (1, 64, 64, 5, 64, 0),            # K shorter than one tile
     (1, 0, 33, 130, 33, 0),           # no product: the column sums alone
     (1, 50, 40, 0, 40, 0),            # empty contraction: C = 0, colsum = 0
@@ -92,13 +94,14 @@ def test_gemm_colsum_refuses_bad_arguments():
     init()
     a, b, c = Dev(64 * 64), Dev(64 * 64), Dev(64 * 64)
     cs = Dev(64)
-    ws = hip.ts_hip_gemm_colsum_workspace_floats(1, 32, 128, 784)
+    K = 16384  # a split-K product: it needs a workspace
+    ws = hip.ts_hip_gemm_colsum_workspace_floats(1, 32, 128, K)
     assert ws > 0
     small = Dev(ws)
     # no column-sum output; a workspace that is too small
     assert hip.ts_hip_gemm_colsum(1, 64, 64, 64, a.ptr, 64, b.ptr, 64, c.ptr, 64, None, None, 0, None) != 0
-    aa, bb, cc, cc2 = Dev(784 * 32), Dev(784 * 128), Dev(32 * 128), Dev(128)
-    assert hip.ts_hip_gemm_colsum(1, 32, 128, 784, aa.ptr, 32, bb.ptr, 128, cc.ptr, 128, cc2.ptr, small.ptr,
+    aa, bb, cc, cc2 = Dev(K * 32), Dev(K * 128), Dev(32 * 128), Dev(128)
+    assert hip.ts_hip_gemm_colsum(1, 32, 128, K, aa.ptr, 32, bb.ptr, 128, cc.ptr, 128, cc2.ptr, small.ptr,
                                   ws - 1, None) == 100003
 
 

@@ -35,10 +35,11 @@ def fusion():
 
 
 # (M, N, K, offset): offset 1 shifts A by one float so the operands are not
-# 16-byte aligned (register-staged kernel); N <= 16 takes the narrow kernel;
+# 16-byte aligned (register-staged kernel); N <= 16 and few tiles with a long
+# K (32x128x784) take the narrow kernel, a K past it split-K (32x128x16384);
 # 784 rows leave an edge tile (clamped loads)
 SHAPES = [(8192, 4096, 512, 0), (1024, 1024, 784, 0), (32, 128, 784, 0), (300, 260, 77, 0), (1024, 512, 256, 1),
-          (1024, 10, 1024, 0), (1000, 7, 333, 1), (784, 1024, 1024, 0)]
+          (1024, 10, 1024, 0), (1000, 7, 333, 1), (784, 1024, 1024, 0), (32, 128, 16384, 0)]
 
 
 @pytest.mark.parametrize("M,N,K,off", SHAPES)

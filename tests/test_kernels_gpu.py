@@ -198,7 +198,10 @@ GEMM_SHAPES = [(1, 1, 1), (2, 2, 2), (32, 128, 784), (784, 128, 32), (129, 127, 
                # N <= 16 over few rows with a long K: the sliced skinny kernel and its slice sum
                (64, 10, 16384),
                # K <= 16 (one k tile, operands straight to registers): ragged edges, K = 16 and 1
-               (129, 127, 16), (100, 33, 1)]
+               (129, 127, 16), (100, 33, 1),
+               # few output tiles and a long K: the narrow kernel's column blocks (ragged N), and
+               # split-K past its K
+               (40, 200, 1000), (32, 128, 16384)]
 
 
 def _gemm_case(oracle, ta, tb, M, N, K, seed, check_rows=None):

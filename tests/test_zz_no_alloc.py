@@ -17,10 +17,12 @@ pytestmark = pytest.mark.gpu
 
 SCRATCH_FLOATS = 1 << 21
 
-# (trans_a, trans_b, M, N, K): the first two split K (few output tiles, long
-# K: the README step's forward and dW shapes), the second smaller than the
-# first; then an unsplit product and an empty contraction
-CASES = [(0, 0, 32, 128, 784), (1, 0, 16, 64, 512), (0, 1, 300, 260, 130), (0, 0, 8, 8, 0)]
+# (trans_a, trans_b, M, N, K): the first two split K (few output tiles and a
+# K longer than the one-pass narrow kernel takes), the second's slices smaller
+# than the first's; then a product the narrow kernel takes (the README step's
+# forward shape: no scratch), an unsplit tiled product and an empty contraction
+CASES = [(0, 0, 32, 128, 16384), (1, 0, 16, 64, 8448), (0, 0, 32, 128, 784), (0, 1, 300, 260, 130),
+         (0, 0, 8, 8, 0)]
 
 
 def _operands(ta, tb, M, N, K, seed):

@@ -1099,25 +1099,28 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny(GemmArgs g, flo
 //
 // v_mfma_f32_16x16x4f32: lane l supplies A[l%16][l/16] of a 16x4 block and
 // B[l/16][l%16] of a 4x16 block, and holds C[4*(l/16) + r][l%16] in its 4
-// accumulators.  A workgroup owns 16 rows of C with all of its (<= 16)
-// columns and all of K, split over its waves in contiguous ranges of whole
-// 64-row chunks (the column sum's); B's columns past N are read clamped to
-// column N-1 and feed outputs that are never stored.  A wave takes its range
+// accumulators.  A workgroup owns a 16x16 block of C (grid.x over row blocks,
+// grid.y over 16-column blocks: one column block for N <= 16) and all of K,
+// split over its waves in contiguous ranges of whole 64-row chunks (the
+// column sum's); B's columns past N are read clamped to column N-1 and feed
+// outputs that are never stored.  A wave takes its range
 // a chunk per round: four 16-k blocks, all their loads at once, then 16
 // MFMAs.  Inside a block, lane group q = l/16 holds k = 4q .. 4q+3 and the
 // block's MFMA s takes k = 4q + s (A and B follow the same order), so a
 // row-major A row gives the lane its four k in one dwordx4.  The waves'
 // accumulators are added in wave order through LDS and the epilogue applied
 // at the store: one launch, no temporary.
-// Column sums of B (CS, trans_b == 0): workgroup 0 holds every row of B in
-// its registers, a chunk per wave round, so each round also adds its chunk's
-// rows in row order (lane j gathers column j's 64 values with cross-lane
-// reads, f64 from +0), the chunk sums go to LDS, and 16 threads add them in
-// the column sum's groups at the end.
-// Used while the row blocks spread over the chip or K is moderate (with
-// column sums in the kernel K <= kNarrowMaxK, the chunk table's size; past
-// it a column-sum pass follows); the sliced skinny kernel above takes long K
-// over few rows.
+// Column sums of B (CS, trans_b == 0): the first row block's workgroup of
+// each column block holds every row of its 16 columns of B in its registers,
+// a chunk per wave round, so each round also adds its chunk's rows in row
+// order (lane j gathers column j's 64 values with cross-lane reads, f64 from
+// +0), the chunk sums go to LDS, and 16 threads add them in the column sum's
+// groups at the end.
+// Used for N <= 16, and for products with few output tiles and a long K,
+// while the blocks spread over the chip or K is moderate (with column sums in
+// the kernel K <= kNarrowMaxK, the chunk table's size; past it a column-sum
+// pass follows); past that the sliced skinny kernel above (N <= 16) or split-K
+// takes them.
 constexpr int kNarrowRows = 16;
 constexpr int kNarrowMaxWaves = 16;
 constexpr size_t kNarrowMaxK = 8192;
@@ -1134,10 +1137,10 @@ __global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int waves = blockDim.x >> 6;
-    const int m0 = blockIdx.x * kNarrowRows;
+    const int m0 = blockIdx.x * kNarrowRows, n0 = blockIdx.y * kSkinnyN;
     const int q = lane >> 4;
     const int m = min(m0 + (lane & 15), g.M - 1);  // rows past M: never stored
-    const int n = min(lane & 15, g.N - 1);         // columns past N: never stored
+    const int n = min(n0 + (lane & 15), g.N - 1);  // columns past N: never stored
     const int kc = ((g.K + waves - 1) / waves + 63) & ~63;
     const int kb = min(g.K, wave * kc), ke = min(g.K, kb + kc);
     const bool cs_wg = CS && blockIdx.x == 0;  // uniform
@@ -1154,7 +1157,7 @@ __global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) 
     for (int o = 0; o < kOuts; ++o) {
         if (o * static_cast<int>(blockDim.x) >= 256) break;  // uniform
         const int t = static_cast<int>(threadIdx.x) + o * static_cast<int>(blockDim.x);
-        const int i = min(m0 + 4 * ((t & 63) >> 4) + ((t >> 6) & 3), g.M - 1), j = min(t & 15, g.N - 1);
+        const int i = min(m0 + 4 * ((t & 63) >> 4) + ((t >> 6) & 3), g.M - 1), j = min(n0 + (t & 15), g.N - 1);
         eb[o] = g.bias ? g.bias[j] : 0.0f;
         em[o] = g.mask ? g.mask[(size_t)i * g.ldc + j] : 1.0f;
     }
@@ -1223,13 +1226,13 @@ __global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) 
         float v = red[0][t];
         for (int w = 1; w < waves; ++w) v += red[w][t];
         const int l = t & 63;
-        const int i = m0 + 4 * (l >> 4) + (t >> 6), j = l & 15;
+        const int i = m0 + 4 * (l >> 4) + (t >> 6), j = n0 + (l & 15);
         if (g.bias) v = v + eb[o];  // epilogue()'s order: bias, relu, mask
         if (g.relu) v = v > 0.0f ? v : 0.0f;
         if (g.mask) v = em[o] > 0.0f ? v : 0.0f;
         if (i < g.M && j < g.N) g.C[(size_t)i * g.ldc + j] = v;
     }
-    if (cs_wg && static_cast<int>(threadIdx.x) < g.N) {
+    if (cs_wg && static_cast<int>(threadIdx.x) < kSkinnyN && n0 + static_cast<int>(threadIdx.x) < g.N) {
         // the chunk sums in groups of kColsumGroup, each from +0
         constexpr int G = static_cast<int>(kColsumGroup);
         const int j = threadIdx.x, chunks = (g.K + 63) >> 6;
@@ -1244,7 +1247,7 @@ __global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) 
                 if (c0 + i < chunks) grp += x[i];
             total += grp;
         }
-        g.colsum[j] = static_cast<float>(total);
+        g.colsum[n0 + j] = static_cast<float>(total);
     }
 }
 
@@ -1256,8 +1259,8 @@ static int narrow_waves(size_t K) {
     return w;
 }
 
-static bool narrow_fits(size_t M, size_t K) {
-    const size_t blocks = (M + kNarrowRows - 1) / kNarrowRows;
+static bool narrow_fits(size_t M, size_t N, size_t K) {
+    const size_t blocks = ((M + kNarrowRows - 1) / kNarrowRows) * ((N + kSkinnyN - 1) / kSkinnyN);
     return K <= kNarrowMaxK || 8 * blocks >= static_cast<size_t>(device_cu_count());
 }
 
@@ -1286,14 +1289,17 @@ static int launch_narrow(int trans_a, int trans_b, size_t M, size_t N, size_t K,
     if (!A || !B) return TS_HIP_EINVAL;
     if (lda < (trans_a ? M : K) || ldb < (trans_b ? K : N)) return TS_HIP_EINVAL;
     const size_t lim = 0x7ffffe00ULL;
-    if (M > lim || K > lim || lda > lim || ldb > lim || ldc > lim) return TS_HIP_EINVAL;
+    if (M > lim || N > lim || K > lim || lda > lim || ldb > lim || ldc > lim) return TS_HIP_EINVAL;
+    if ((N + kSkinnyN - 1) / kSkinnyN > 65535) return TS_HIP_EINVAL;  // grid.y
     if (g.colsum && (trans_b || K > kNarrowMaxK)) return TS_HIP_EINVAL;
     g.A = A; g.B = B; g.C = C;
     g.M = static_cast<int>(M); g.N = static_cast<int>(N); g.K = static_cast<int>(K);
     g.lda = static_cast<int>(lda); g.ldb = static_cast<int>(ldb); g.ldc = static_cast<int>(ldc);
     const bool va = trans_a || (aligned16(A) && lda % 4 == 0);
     const bool vb = !trans_b || (aligned16(B) && ldb % 4 == 0);
-    const dim3 grid(static_cast<unsigned>((M + kNarrowRows - 1) / kNarrowRows)), block(64 * narrow_waves(K));
+    const dim3 grid(static_cast<unsigned>((M + kNarrowRows - 1) / kNarrowRows),
+                    static_cast<unsigned>((N + kSkinnyN - 1) / kSkinnyN)),
+        block(64 * narrow_waves(K));
     hipStream_t s = as_stream(stream);
     if (g.colsum) launch_narrow_as<true>(trans_a, trans_b, va && vb, g, grid, block, s);
     else launch_narrow_as<false>(trans_a, trans_b, va && vb, g, grid, block, s);
@@ -1384,7 +1390,7 @@ static int split_slices(size_t M, size_t N, size_t K) {
 // column sums directly.
 struct GemmPlan {
     bool skinny = false;
-    bool narrow = false;  // skinny, in one pass (no temporary; column sums in the kernel)
+    bool narrow = false;  // the narrow kernel: one pass, no temporary (N <= 16, or few tiles and a long K)
     int slices = 1;
     size_t split_floats = 0;
     size_t part_floats = 0;
@@ -1397,7 +1403,11 @@ static GemmPlan gemm_plan(int trans_a, int trans_b, size_t M, size_t N, size_t K
     GemmPlan p;
     if (M == 0 || N == 0 || K == 0) return p;
     p.skinny = skinny(N);
-    p.narrow = p.skinny && narrow_fits(M, K);  // the same kernel with or without column sums
+    // the narrow kernel for N <= 16, and for the few-tile, long-K shapes split-K
+    // takes otherwise (the same kernel with or without column sums)
+    const size_t tiles64 = ((M + 63) / 64) * ((N + 63) / 64);
+    const bool few_tiles = !p.skinny && 4 * tiles64 < static_cast<size_t>(device_cu_count()) && K >= 512;
+    p.narrow = (p.skinny || few_tiles) && narrow_fits(M, N, K);
     p.slices = p.narrow ? 1 : p.skinny ? skinny_slices(M, K) : split_slices(M, N, K);
     p.split_floats = p.slices > 1 ? static_cast<size_t>(p.slices) * M * N : 0;
     p.cs_kernel = colsum && (p.narrow ? K <= kNarrowMaxK : !p.skinny && p.slices == 1 && trans_a && !trans_b);
@@ -1449,7 +1459,7 @@ static int gemm_plain(int trans_a, int trans_b, size_t M, size_t N, size_t K, co
     }
     double *part = plan.part_floats ? reinterpret_cast<double *>(W + plan.part_offset()) : nullptr;
     int status;
-    if (plan.narrow) {  // few output columns, one pass
+    if (plan.narrow) {  // few output columns, or few output tiles and a long K: one pass
         GemmArgs g{};
         g.bias = bias;
         g.mask = mask;
