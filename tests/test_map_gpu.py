@@ -127,7 +127,9 @@ def test_chain_multi_output_and_scalar_input():
     assert_bits_equal(gc.get(), want_c.get(), "gc")
 
 
-@pytest.mark.parametrize("n", [1, 5, 4096, 100003, 1 << 22])
+# up to 16 first-pass workgroups (n <= 16384) ts_hip_sum runs both passes in
+# one workgroup; the fused sum always takes two: the same bits either way
+@pytest.mark.parametrize("n", [1, 5, 4096, 10240, 16384, 16385, 100003, 1 << 22])
 @pytest.mark.parametrize("mean", [0, 1])
 def test_fused_sum_has_the_bits_of_ts_hip_sum(n, mean):
     from gpu_util import Dev, hip, hip_check, sync

@@ -62,6 +62,66 @@ int launch_sum_final(const double *partial, size_t nparts, size_t n, float *out,
     return launch_status();
 }
 
+// Both passes in one workgroup, for at most kSumSmallBlocks first-pass
+// workgroups and the float4 path (n4 == n / 4): the operations, and so the
+// bits, of sum_partial's workgroups and sum_final.  With that few workgroups
+// the grid stride covers every float4 group, so virtual thread (b, t) of
+// first-pass workgroup b has at most one group and one tail element; thread t
+// holds them for every b (all loads in flight at once), each b's wave sums are
+// formed as block_sum forms them and added in wave order from +0 (a partial),
+// and thread t then adds partials t, t + 256, ... from +0 as sum_final's
+// threads do, combined by block_sum.
+constexpr int kSumSmallBlocks = 16;
+
+template <bool PROD, bool MEAN>
+__global__ __launch_bounds__(kBlock) void sum_small(const float *__restrict__ x, const float *__restrict__ y,
+                                                    size_t n, size_t n4, int blocks, float *out) {
+    __shared__ double wsum[kSumSmallBlocks][kBlock / 64];
+    __shared__ double parts[kSumSmallBlocks];
+    const int t = static_cast<int>(threadIdx.x), lane = t & 63, wave = t >> 6;
+    double acc[kSumSmallBlocks];
+#pragma unroll
+    for (int b = 0; b < kSumSmallBlocks; ++b) {
+        acc[b] = 0.0;
+        if (b < blocks) {
+            const size_t v = static_cast<size_t>(b) * kBlock + t;
+            if (v < n4) {
+                const float4 q = reinterpret_cast<const float4 *>(x)[v];
+                if (PROD) {
+                    const float4 r = reinterpret_cast<const float4 *>(y)[v];
+                    acc[b] += (double)q.x * (double)r.x + (double)q.y * (double)r.y + (double)q.z * (double)r.z +
+                              (double)q.w * (double)r.w;
+                } else {
+                    acc[b] += (double)q.x + (double)q.y + (double)q.z + (double)q.w;
+                }
+            }
+            const size_t i = 4 * n4 + v;  // the tail: n - 4*n4 < 4 <= stride, so one element at most
+            if (i < n) acc[b] += PROD ? (double)x[i] * (double)y[i] : (double)x[i];
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < kSumSmallBlocks; ++b) {
+        if (b >= blocks) break;  // uniform
+        const double s = wave_sum(acc[b]);
+        if (lane == 0) wsum[b][wave] = s;
+    }
+    __syncthreads();
+    if (t < blocks) {
+        double r = 0.0;
+#pragma unroll
+        for (int w = 0; w < kBlock / 64; ++w) r += wsum[t][w];
+        parts[t] = r;
+    }
+    __syncthreads();
+    double a = 0.0;
+    if (t < blocks) a += parts[t];
+    const double r = block_sum(a);
+    if (t == 0) {
+        const float s = static_cast<float>(r);
+        out[0] = MEAN ? s / static_cast<float>(n) : s;
+    }
+}
+
 template <bool MEAN>
 static int launch_sum(const float *x, const float *y, size_t n, float *out, float *workspace, size_t ws,
                       void *stream) {
@@ -76,6 +136,12 @@ static int launch_sum(const float *x, const float *y, size_t n, float *out, floa
     if ((reinterpret_cast<uintptr_t>(workspace) & 7u) != 0) return TS_HIP_EINVAL;
     double *partial = reinterpret_cast<double *>(workspace);
     size_t n4 = (aligned16(x) && (!y || aligned16(y))) ? n / 4 : 0;
+    if (blocks <= static_cast<size_t>(kSumSmallBlocks) && n4 == n / 4) {  // one launch, the same bits
+        const int nb = static_cast<int>(blocks);
+        if (y) launch(sum_small<true, MEAN>, dim3(1), dim3(kBlock), 0, s, x, y, n, n4, nb, out);
+        else launch(sum_small<false, MEAN>, dim3(1), dim3(kBlock), 0, s, x, y, n, n4, nb, out);
+        return launch_status();
+    }
     if (y)
         launch(sum_partial<true>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, y, n,
                            n4, partial);
