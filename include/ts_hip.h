@@ -268,7 +268,12 @@ int ts_hip_softmax_backward(const float *y, const float *go, float *gi, size_t o
  *   divisor is checked as ts_hip_div does, from zero_check_start on, into
  *   zero_index), NEG (0-a before tail_start, -a after: ts_hip_neg), RELU,
  *   RELU_BWD (a > 0 ? b : +0: ts_hip_relu_backward with a the saved value, b
- *   the gradient), ADD_S / SUB_S / MUL_S / DIV_S (a op imm), SQUARE (a*a).
+ *   the gradient), ADD_S / SUB_S / MUL_S / DIV_S (a op imm), SQUARE (a*a),
+ *   CONST (imm for every element, as ts_hip_fill writes it; a and b are not
+ *   read and may be any register, e.g. 0).
+ * On an op without an immediate of its own (not the _S ops or CONST), flags &
+ * TS_HIP_MAP_IMM_A (IMM_B) makes operand a (b) the op's imm instead of a
+ * register (a constant folded into the op; the register is not read).
  * With sum_out != NULL, register reduce_reg is also added up into sum_out[0]
  * (divided by (float)n when mean) with the bits ts_hip_sum / ts_hip_mean give
  * over those values; the workspace is ts_hip_map_workspace_floats(n) floats,
@@ -277,10 +282,13 @@ int ts_hip_softmax_backward(const float *y, const float *go, float *gi, size_t o
 #define TS_HIP_MAP_MAX_OPS 11
 #define TS_HIP_MAP_MAX_OUTPUTS 4
 #define TS_HIP_MAP_CHECKED 1
+#define TS_HIP_MAP_IMM_A 2
+#define TS_HIP_MAP_IMM_B 4
 enum {
     TS_HIP_MAP_ADD = 0, TS_HIP_MAP_SUB = 1, TS_HIP_MAP_MUL = 2, TS_HIP_MAP_DIV = 3, TS_HIP_MAP_NEG = 4,
     TS_HIP_MAP_RELU = 5, TS_HIP_MAP_RELU_BWD = 6, TS_HIP_MAP_ADD_S = 7, TS_HIP_MAP_SUB_S = 8,
-    TS_HIP_MAP_MUL_S = 9, TS_HIP_MAP_DIV_S = 10, TS_HIP_MAP_SQUARE = 11
+    TS_HIP_MAP_MUL_S = 9, TS_HIP_MAP_DIV_S = 10, TS_HIP_MAP_SQUARE = 11,
+    TS_HIP_MAP_CONST = 12
 };
 typedef struct ts_hip_map_op {
     uint8_t code, a, b, flags;

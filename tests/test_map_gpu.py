@@ -75,6 +75,8 @@ def test_each_op_matches_its_kernel(n, offset):
         ("mul_s", -3.1, lambda o: hip.ts_hip_mul_scalar(da.ptr, ctypes.c_float(-3.1), o, n, None)),
         ("div_s", 7.0, lambda o: hip.ts_hip_div_scalar(da.ptr, ctypes.c_float(7.0), o, n, None)),
         ("square", 0.0, lambda o: hip.ts_hip_pow_scalar(da.ptr, ctypes.c_float(2.0), o, n, None)),
+        ("const", -0.0, lambda o: hip.ts_hip_fill(o, ctypes.c_float(-0.0), n, None)),
+        ("const", 0.37, lambda o: hip.ts_hip_fill(o, ctypes.c_float(0.37), n, None)),
     ]
     for code, imm, ref in cases:
         got, want = Dev(n, offset), Dev(n, offset)
@@ -155,6 +157,72 @@ def test_fused_sum_has_the_bits_of_ts_hip_sum(n, mean):
     assert_bits_equal(d.get(), (y - t).astype(np.float32), "stored difference")
 
 
+@pytest.mark.parametrize("n", [7, 4099])
+def test_immediate_operands_match_a_filled_operand(n):
+    # an operand flagged IMM_A / IMM_B is the op's imm: the same bits as the
+    # separate kernel reading a buffer filled with that value
+    from gpu_util import Dev, ZeroIndex, hip, hip_check, sync
+    F = _ffi()
+    print(f"[map imm] n={n}", flush=True)
+    a = normal(n, 11)
+    a[: 3] = np.array([0.0, -0.0, np.inf], np.float32)
+    da = Dev.of(a)
+    tail8, tail32 = 8 * (n // 8), 32 * (n // 32)
+    zi = ZeroIndex()
+    binary = {"add": hip.ts_hip_add, "sub": hip.ts_hip_sub, "mul": hip.ts_hip_mul,
+              "relu_bwd": hip.ts_hip_relu_backward}
+    for v in (1.0, -0.0, 0.625, -3.0):
+        filled = Dev(n)
+        hip_check(hip.ts_hip_fill(filled.ptr, ctypes.c_float(v), n, None))
+        for code in ("add", "sub", "mul", "div", "relu_bwd"):
+            for side in ("a", "b"):
+                got, want = Dev(n), Dev(n)
+                flag = F.MAP_IMM_A if side == "a" else F.MAP_IMM_B
+                x, y = (filled, da) if side == "a" else (da, filled)
+                prog = _program([da.ptr], [(code, 0, 0, v, flag)], [(got.ptr, R0)])
+                hip_check(hip.ts_hip_map(ctypes.byref(prog), n, tail8, tail32, None, None, 0, None, 0, None), code)
+                if code == "div":
+                    hip_check(hip.ts_hip_div(x.ptr, y.ptr, want.ptr, n, tail32, zi.ptr, None))
+                else:
+                    hip_check(binary[code](x.ptr, y.ptr, want.ptr, n, None))
+                sync()
+                zi.reset()
+                assert_bits_equal(got.get(), want.get(), f"{code} imm {side} = {v}")
+        # a unary op and both operands of a binary one
+        for code, ref in (("neg", lambda o: hip.ts_hip_neg(filled.ptr, o, n, tail8, None)),
+                          ("square", lambda o: hip.ts_hip_mul(filled.ptr, filled.ptr, o, n, None)),
+                          ("mul", lambda o: hip.ts_hip_mul(filled.ptr, filled.ptr, o, n, None))):
+            got, want = Dev(n), Dev(n)
+            prog = _program([da.ptr], [(code, 0, 0, v, F.MAP_IMM_A | F.MAP_IMM_B)], [(got.ptr, R0)])
+            hip_check(hip.ts_hip_map(ctypes.byref(prog), n, tail8, tail32, None, None, 0, None, 0, None), code)
+            hip_check(ref(want.ptr))
+            sync()
+            assert_bits_equal(got.get(), want.get(), f"{code} both imm = {v}")
+
+
+@pytest.mark.parametrize("n", [1, 4099, 100003])
+def test_program_without_inputs(n):
+    # a constant (the deferred gradient seed) and what is computed from it,
+    # stored and summed, with no input buffer at all
+    from gpu_util import Dev, hip, hip_check, sync
+    print(f"[map const] n={n}", flush=True)
+    stored, out = Dev(n), Dev(1)
+    ws = hip.ts_hip_map_workspace_floats(n)
+    dws = Dev(ws + 2)
+    prog = _program([], [("const", 0, 0, 1.5, 0), ("mul_s", R0, R0, 0.25, 0)], [(stored.ptr, R0 + 1)],
+                    reduce_reg=R0 + 1)
+    hip_check(hip.ts_hip_map(ctypes.byref(prog), n, 8 * (n // 8), 32 * (n // 32), None, out.ptr, 0, dws.ptr, ws,
+                             None), "map")
+    filled, want = Dev(n), Dev(1)
+    hip_check(hip.ts_hip_fill(filled.ptr, ctypes.c_float(0.375), n, None))
+    sw = hip.ts_hip_sum_workspace_floats(n)
+    dsw = Dev(sw + 2)
+    hip_check(hip.ts_hip_sum(filled.ptr, n, want.ptr, dsw.ptr, sw, None))
+    sync()
+    assert_bits_equal(stored.get(), np.full(n, 0.375, np.float32), "stored")
+    assert_bits_equal(out.get(), want.get(), "sum")
+
+
 def test_division_by_zero_index_is_reported_as_by_ts_hip_div():
     from gpu_util import Dev, ZeroIndex, hip, hip_check, sync
     n = 100
@@ -181,6 +249,9 @@ def test_bad_programs_are_refused():
     d = Dev(16)
     bad = [
         _program([d.ptr], [("add", 0, R0 + 1, 0.0, 0)], [(d.ptr, R0)]),    # reads a later register
+        _program([], [("const", 0, 0, 1.0, 0)], [(d.ptr, 0)]),              # stores an absent input
+        _program([d.ptr], [("add_s", 0, 0, 1.0, 2)], [(d.ptr, R0)]),       # imm operand on an _S op
+        _program([d.ptr], [("const", 0, 0, 1.0, 4)], [(d.ptr, R0)]),       # imm operand on CONST
         _program([d.ptr], [("add", 0, 3, 0.0, 0)], [(d.ptr, R0)]),         # input register past n_inputs
         _program([d.ptr], [("add", 0, 0, 0.0, 0)], [(d.ptr, R0 + 1)]),     # output of no op
         _program([d.ptr], [("add", 0, 0, 0.0, 0)], []),                    # nothing stored, no sum
@@ -228,9 +299,10 @@ def test_chain_bits_with_fusion_on_and_off(T, oracle, n):
 
 def test_chain_runs_as_few_fused_passes(T):
     # forward: one pass computing y (stored: relu saves it) and a + b (stored:
-    # mul saves it) with the sum's first pass; backward: the scalar seed and
-    # one pass writing the three gradients.  Bytes per element: 12 read + 8
-    # written, then 16 read (y, c, a, a + b) + 12 written.
+    # mul saves it) with the sum's first pass; backward: one pass writing the
+    # three gradients, the seed (ones) a constant of it and never written.
+    # Bytes per element: 12 read + 8 written, then 16 read (y, c, a, a + b) +
+    # 12 written.
     n = 1 << 20
     a, b = normal(n, 21), normal(n, 22)
     c = uniform(n, 0.5, 2.0, 23)
@@ -246,6 +318,8 @@ def test_chain_runs_as_few_fused_passes(T):
     ew = T.Profile.read(T.Profile.ELEMENTWISE)
     red = T.Profile.read(T.Profile.REDUCTION)
     assert red["launches"] == 0
-    assert ew["launches"] == 3, ew                      # forward pass, seed (ones), backward pass
-    per_elem = (ew["work"] - 4.0) / n
+    assert ew["launches"] == 2, ew                      # forward pass, backward pass
+    per_elem = ew["work"] / n
     assert per_elem == 20.0 + 28.0, per_elem
+    # the seed is still ones when read
+    assert_bits_equal(loss.grad().data(), np.ones(1, np.float32), "seed")

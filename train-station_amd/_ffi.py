@@ -38,8 +38,10 @@ def _load(name: str) -> ctypes.CDLL:
 MAP_MAX_INPUTS, MAP_MAX_OPS, MAP_MAX_OUTPUTS = 5, 11, 4
 # TS_HIP_MAP_* op codes and flags of include/ts_hip.h
 MAP_CODES = {"add": 0, "sub": 1, "mul": 2, "div": 3, "neg": 4, "relu": 5, "relu_bwd": 6, "add_s": 7, "sub_s": 8,
-             "mul_s": 9, "div_s": 10, "square": 11}
+             "mul_s": 9, "div_s": 10, "square": 11, "const": 12}
 MAP_CHECKED = 1
+MAP_IMM_A = 2
+MAP_IMM_B = 4
 
 
 class MapOp(ctypes.Structure):

@@ -70,7 +70,9 @@ const Tensor *accumulated_gradient(size_t id) {
 
 // engine.rs:962-1047
 void engine_backward(Tensor &root, const Tensor *grad_output) {
-    Tensor init = grad_output ? grad_output->alias() : Tensor::ones(root.dims());
+    // backward(None) seeds ones; deferred, the seed is a constant of the
+    // programs that read it and is written only if read elsewhere
+    Tensor init = grad_output ? grad_output->alias() : Tensor::constant(root.dims(), 1.0f);
     if (init.dims() != root.dims() && init.size() != root.size())
         throw Error("backward: gradient shape does not match the tensor");
     root.accumulate_grad(init.alias());
@@ -105,7 +107,10 @@ void engine_backward(Tensor &root, const Tensor *grad_output) {
     std::vector<std::shared_ptr<Allocation>> deferred;
     for (auto &kv : graph().gradients)
         if (kv.second.allocation() && kv.second.allocation()->map) deferred.push_back(kv.second.allocation());
-    if (root.grad_ref() && root.grad_ref()->allocation() && root.grad_ref()->allocation()->map)
+    // (the root's seed, a deferred constant, reads no buffer and stays
+    // deferred until read)
+    if (root.grad_ref() && root.grad_ref()->allocation() && root.grad_ref()->allocation()->map &&
+        !(root.grad_ref()->allocation()->map->leaves.empty() && root.grad_ref()->allocation()->map->nodes.size() == 1))
         deferred.push_back(root.grad_ref()->allocation());
     materialize_maps(deferred);
     // and the column sums (bias gradients) no weight-gradient product produced

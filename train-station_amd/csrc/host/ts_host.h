@@ -337,6 +337,10 @@ class Tensor {
     static Tensor zeros(std::vector<size_t> dims);
     static Tensor ones(std::vector<size_t> dims);
     static Tensor filled(std::vector<size_t> dims, float v);
+    // filled(dims, v), deferred with fusion on: the value becomes a constant
+    // of the elementwise program that reads it (the gradient seed of
+    // backward(None)), and is written only if something else reads it.
+    static Tensor constant(std::vector<size_t> dims, float v);
     static Tensor from_slice(const float *data, size_t len, std::vector<size_t> dims);
     // Tensor::randn (init/random.rs:231-235): XorShiftRng values generated on
     // the device; without a seed, one derived from the clock (random.rs:492-497)

@@ -55,8 +55,11 @@ __device__ __forceinline__ void run_program(const MapArgsK &a, size_t i0, unsign
         // operands read once, the op's values formed in temporaries, the
         // register file written once after the switch (writing it in every
         // case makes the compiler keep several copies of it)
-        const float x[W] = {r[op.a]...};
-        const float y[W] = {r[op.b]...};
+        // an operand flagged TS_HIP_MAP_IMM_A / _B is the op's immediate (a
+        // folded constant) instead of a register
+        const bool ia = (op.flags & TS_HIP_MAP_IMM_A) != 0, ib = (op.flags & TS_HIP_MAP_IMM_B) != 0;
+        const float x[W] = {(ia ? op.imm : r[op.a])...};
+        const float y[W] = {(ib ? op.imm : r[op.b])...};
         float v[W];
         switch (op.code) {
             case TS_HIP_MAP_ADD: ((v[C] = x[C] + y[C]), ...); break;
@@ -83,6 +86,7 @@ __device__ __forceinline__ void run_program(const MapArgsK &a, size_t i0, unsign
             case TS_HIP_MAP_SUB_S: ((v[C] = x[C] - op.imm), ...); break;
             case TS_HIP_MAP_MUL_S: ((v[C] = x[C] * op.imm), ...); break;
             case TS_HIP_MAP_DIV_S: ((v[C] = x[C] / op.imm), ...); break;
+            case TS_HIP_MAP_CONST: ((v[C] = op.imm), ...); break;  // ts_hip_fill's value
             default: ((v[C] = x[C] * x[C]), ...); break;  // TS_HIP_MAP_SQUARE: pow_scalar(2)
         }
         const int d = kMapIn + static_cast<int>(k);
@@ -290,11 +294,22 @@ extern "C" int ts_hip_map(const ts_hip_map_program *prog, size_t n, size_t tail_
     const bool reduce = sum_out != nullptr;
     if (reduce && (p.reduce_reg < 0 || p.reduce_reg >= static_cast<int>(kMapIn + p.n_ops))) return TS_HIP_EINVAL;
     if (!reduce && p.n_outputs == 0) return TS_HIP_EINVAL;
-    // every register read must be an input or an earlier op's value
+    // every register read must be an input or an earlier op's value (CONST
+    // and an immediate operand read none; their operand registers are only
+    // required to exist); immediate operands only on ops without an
+    // immediate of their own
     for (uint32_t k = 0; k < p.n_ops; ++k) {
         const ts_hip_map_op &op = p.ops[k];
-        auto ok = [&](int r) { return r < static_cast<int>(p.n_inputs) || (r >= kMapIn && r < kMapIn + static_cast<int>(k)); };
-        if (!ok(op.a) || !ok(op.b) || op.code > TS_HIP_MAP_SQUARE) return TS_HIP_EINVAL;
+        const bool own_imm = op.code == TS_HIP_MAP_CONST || (op.code >= TS_HIP_MAP_ADD_S && op.code <= TS_HIP_MAP_DIV_S);
+        const bool imm_ops = (op.flags & (TS_HIP_MAP_IMM_A | TS_HIP_MAP_IMM_B)) != 0;
+        auto ok = [&](int r, bool unread) {
+            if (unread) return r < kMapRegs;
+            return r < static_cast<int>(p.n_inputs) || (r >= kMapIn && r < kMapIn + static_cast<int>(k));
+        };
+        const bool konst = op.code == TS_HIP_MAP_CONST;
+        if (!ok(op.a, konst || (op.flags & TS_HIP_MAP_IMM_A)) || !ok(op.b, konst || (op.flags & TS_HIP_MAP_IMM_B)) ||
+            op.code > TS_HIP_MAP_CONST || (own_imm && imm_ops))
+            return TS_HIP_EINVAL;
     }
     for (uint32_t o = 0; o < p.n_outputs; ++o) {
         const int q = p.output_regs[o];
