@@ -81,3 +81,49 @@ def rel_l2(got, want) -> float:
     got = np.asarray(got, dtype=np.float64).reshape(-1)
     want = np.asarray(want, dtype=np.float64).reshape(-1)
     return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
+
+
+def sum_order_model(values, mean=False, aligned=True) -> np.float32:
+    """The fp32 result of ts_hip_sum / ts_hip_mean (and of a fused sum in
+    ts_hip_map) over `values`, in the partition's order, restated in numpy:
+    ceil(n / 1024) first-pass workgroups (at most 2048) of 256 threads; thread
+    t adds, in f64 from +0, each float4 group g = t, t + stride, ... as
+    ((x0 + x1) + x2) + x3 (no groups when the input is not 16-byte aligned),
+    then the elements 4 * n4 + t, ... past the groups; a workgroup's sum is the
+    xor butterfly over each wave's 64 lanes, the four wave sums added from +0;
+    the second pass's thread t adds partials t, t + 256, ... from +0, then the
+    same workgroup sum; one rounding to fp32 (divided by (float)n for the
+    mean).  Whatever kernels run, the bits are these."""
+    x = np.asarray(values, np.float32).astype(np.float64)
+    n = x.size
+    if n == 0:
+        return np.float32(0.0)
+    blocks = min(max((n + 1023) // 1024, 1), 2048)
+    threads = blocks * 256
+    n4 = n // 4 if aligned else 0
+    acc = np.zeros(threads)
+    q = x[: 4 * n4].reshape(n4, 4)
+    quad = ((q[:, 0] + q[:, 1]) + q[:, 2]) + q[:, 3]
+    for g0 in range(0, n4, threads):
+        part = quad[g0: g0 + threads]
+        acc[: part.size] += part
+    for i0 in range(4 * n4, n, threads):
+        part = x[i0: i0 + threads]
+        acc[: part.size] += part
+
+    def workgroup_sums(v):  # v: [workgroups, 256]
+        w = v.reshape(v.shape[0], 4, 64).copy()
+        for off in (32, 16, 8, 4, 2, 1):
+            w = w + w[:, :, np.arange(64) ^ off]
+        r = np.zeros(v.shape[0])
+        for k in range(4):
+            r = r + w[:, k, 0]
+        return r
+
+    partial = workgroup_sums(acc.reshape(blocks, 256))
+    acc2 = np.zeros(256)
+    for i0 in range(0, blocks, 256):
+        part = partial[i0: i0 + 256]
+        acc2[: part.size] += part
+    s = np.float32(workgroup_sums(acc2.reshape(1, 256))[0])
+    return np.float32(s / np.float32(n)) if mean else s

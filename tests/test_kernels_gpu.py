@@ -7,7 +7,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import assert_bits_equal, max_rel, normal, uniform
+from conftest import assert_bits_equal, max_rel, normal, sum_order_model, uniform
 from gpu_util import Dev, ZeroIndex, hip, hip_check, sync
 
 pytestmark = pytest.mark.gpu
@@ -164,6 +164,22 @@ def test_sum_and_mean(oracle, n):
         assert float(dout.get()[0]) == 0.0
     if n:  # too small a workspace is refused, not overrun
         assert hip.ts_hip_sum(dx.ptr, n, dout.ptr, dws.ptr, ws - 1, None) == 100003
+
+
+# the one-workgroup form (up to 16 first-pass workgroups, aligned) and the two
+# passes give the partition's bits, aligned or not
+@pytest.mark.parametrize("offset", [0, 1])
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 1024, 1027, 4096, 10240, 15361, 16384, 16385, 100003, 1 << 22])
+def test_sum_bits_follow_the_partition(n, offset):
+    print(f"[sum bits] n={n} offset={offset}", flush=True)
+    x = normal(n, 12)
+    dx = Dev.of(x, offset)
+    ws = hip.ts_hip_sum_workspace_floats(n)
+    dws, dout = Dev(ws), Dev(1)
+    for name, mean in (("ts_hip_sum", False), ("ts_hip_mean", True)):
+        _run(name, dx.ptr, n, dout.ptr, dws.ptr, ws, None)
+        want = sum_order_model(x, mean=mean, aligned=offset == 0)
+        assert_bits_equal(dout.get(), np.array([want], np.float32), f"{name} n={n} offset={offset}")
 
 
 def test_sum_known_answers():

@@ -12,7 +12,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from conftest import assert_bits_equal, normal, uniform
+from conftest import assert_bits_equal, normal, sum_order_model, uniform
 
 pytestmark = pytest.mark.gpu
 
@@ -130,8 +130,9 @@ def test_chain_multi_output_and_scalar_input():
 
 
 # up to 16 first-pass workgroups (n <= 16384) ts_hip_sum runs both passes in
-# one workgroup; the fused sum always takes two: the same bits either way
-@pytest.mark.parametrize("n", [1, 5, 4096, 10240, 16384, 16385, 100003, 1 << 22])
+# one workgroup; the fused sum always takes two: the same bits either way,
+# the partition's order
+@pytest.mark.parametrize("n", [1, 4, 5, 1024, 4096, 10240, 12288, 16384, 16385, 100003, 1 << 22])
 @pytest.mark.parametrize("mean", [0, 1])
 def test_fused_sum_has_the_bits_of_ts_hip_sum(n, mean):
     from gpu_util import Dev, hip, hip_check, sync
@@ -155,6 +156,10 @@ def test_fused_sum_has_the_bits_of_ts_hip_sum(n, mean):
     sync()
     assert_bits_equal(out.get(), want.get(), f"fused {'mean' if mean else 'sum'} n={n}")
     assert_bits_equal(d.get(), (y - t).astype(np.float32), "stored difference")
+    # and both have the partition's bits
+    dd = (y - t).astype(np.float32)
+    model = sum_order_model((dd * dd).astype(np.float32), mean=bool(mean))
+    assert_bits_equal(out.get(), np.array([model], np.float32), f"partition order n={n}")
 
 
 @pytest.mark.parametrize("n", [7, 4099])
@@ -200,7 +205,7 @@ def test_immediate_operands_match_a_filled_operand(n):
             assert_bits_equal(got.get(), want.get(), f"{code} both imm = {v}")
 
 
-@pytest.mark.parametrize("n", [1, 4099, 100003])
+@pytest.mark.parametrize("n", [1, 4096, 4099, 100003])
 def test_program_without_inputs(n):
     # a constant (the deferred gradient seed) and what is computed from it,
     # stored and summed, with no input buffer at all

@@ -299,3 +299,26 @@ def test_adam_velocity_tail_association(oracle):
     assert v[0] == np.float32(c2 * np.float32(g_diff * g_diff))
     assert v[8] == np.float32(np.float32(c2 * g_diff) * g_diff)
     assert v[0] != v[8]
+
+
+def test_sum_order_model_known_answers():
+    # the numpy restatement of the GPU sum's partition (the checker of the
+    # one-workgroup and two-pass kernels' bits): exact where the sum is, the
+    # reference's known answers, and within the f64 bound of math.fsum
+    import math
+    from conftest import sum_order_model
+    ka = golden("known_answers.json")
+    for key in ("sum_forward", "sum_21", "sum_276"):
+        case = ka[key]
+        assert abs(float(sum_order_model(case["x"])) - case["sum"]) <= case.get("tol", 0.0), key
+    for key in ("mean_forward", "mean_3_5"):
+        case = ka[key]
+        assert abs(float(sum_order_model(case["x"], mean=True)) - case["mean"]) <= case["tol"], key
+    for n in (1, 3, 1027, 300001):
+        ints = np.arange(n, dtype=np.float32) % 97 - 48
+        assert sum_order_model(ints) == np.float32(np.sum(ints.astype(np.int64)))
+        assert sum_order_model(ints, aligned=False) == np.float32(np.sum(ints.astype(np.int64)))
+    assert sum_order_model([]) == 0.0
+    x = normal(1 << 21, 5)
+    exact = math.fsum(x.astype(np.float64))
+    assert abs(float(sum_order_model(x)) - exact) <= 1e-6 * float(np.abs(x).sum(dtype=np.float64))

@@ -79,26 +79,37 @@ __global__ __launch_bounds__(kBlock) void sum_small(const float *__restrict__ x,
     __shared__ double wsum[kSumSmallBlocks][kBlock / 64];
     __shared__ double parts[kSumSmallBlocks];
     const int t = static_cast<int>(threadIdx.x), lane = t & 63, wave = t >> 6;
+    // every load issued before any is used (a load consumed in its own
+    // conditional block is waited for there, one latency per block):
+    // addresses clamped into the input, values past it not added.  The tail
+    // (n - 4*n4 < 4 elements) falls to threads 0..2 of block 0.
+    const size_t ti = 4 * n4 + t < n ? 4 * n4 + t : n - 1;
+    const float tx = x[ti], ty = PROD ? y[ti] : 0.0f;
+    float4 q[kSumSmallBlocks], qy[kSumSmallBlocks];
+#pragma unroll
+    for (int b = 0; b < kSumSmallBlocks; ++b) {
+        q[b] = qy[b] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (b < blocks && n4 > 0) {  // uniform
+            const size_t v = static_cast<size_t>(b) * kBlock + t;
+            const size_t vc = v < n4 ? v : n4 - 1;
+            q[b] = reinterpret_cast<const float4 *>(x)[vc];
+            if (PROD) qy[b] = reinterpret_cast<const float4 *>(y)[vc];
+        }
+    }
     double acc[kSumSmallBlocks];
 #pragma unroll
     for (int b = 0; b < kSumSmallBlocks; ++b) {
         acc[b] = 0.0;
-        if (b < blocks) {
-            const size_t v = static_cast<size_t>(b) * kBlock + t;
-            if (v < n4) {
-                const float4 q = reinterpret_cast<const float4 *>(x)[v];
-                if (PROD) {
-                    const float4 r = reinterpret_cast<const float4 *>(y)[v];
-                    acc[b] += (double)q.x * (double)r.x + (double)q.y * (double)r.y + (double)q.z * (double)r.z +
-                              (double)q.w * (double)r.w;
-                } else {
-                    acc[b] += (double)q.x + (double)q.y + (double)q.z + (double)q.w;
-                }
-            }
-            const size_t i = 4 * n4 + v;  // the tail: n - 4*n4 < 4 <= stride, so one element at most
-            if (i < n) acc[b] += PROD ? (double)x[i] * (double)y[i] : (double)x[i];
+        const size_t v = static_cast<size_t>(b) * kBlock + t;
+        if (b < blocks && v < n4) {
+            if (PROD)
+                acc[b] += (double)q[b].x * (double)qy[b].x + (double)q[b].y * (double)qy[b].y +
+                          (double)q[b].z * (double)qy[b].z + (double)q[b].w * (double)qy[b].w;
+            else
+                acc[b] += (double)q[b].x + (double)q[b].y + (double)q[b].z + (double)q[b].w;
         }
     }
+    if (4 * n4 + t < n) acc[0] += PROD ? (double)tx * (double)ty : (double)tx;
 #pragma unroll
     for (int b = 0; b < kSumSmallBlocks; ++b) {
         if (b >= blocks) break;  // uniform
