@@ -258,37 +258,32 @@ int ts_hip_softmax_backward(const float *y, const float *go, float *gi, size_t o
  * every op as its own pass) ---------------------------------------------------
  * One pass evaluates a short program of the elementwise ops above over up to
  * TS_HIP_MAP_MAX_INPUTS inputs of n elements (or one value used for every
- * element: bit k of scalar_inputs) and stores up to TS_HIP_MAP_MAX_OUTPUTS of
- * its values.  Registers 0 .. n_inputs-1 hold the inputs; op k writes register
- * TS_HIP_MAP_MAX_INPUTS + k and reads registers a and b (inputs or earlier
- * ops).  Each op's formula and fp32 operation order is that of the separate
+ * element: bit k of scalar_inputs reads inputs[k][0]; bit k of const_inputs
+ * takes const_values[k], and inputs[k] is not read) and stores up to
+ * TS_HIP_MAP_MAX_OUTPUTS of its values.  Registers 0 .. n_inputs-1 hold the
+ * inputs; op k writes register TS_HIP_MAP_MAX_INPUTS + k and reads registers a
+ * and b (inputs or earlier ops); an output or the summed register may be an
+ * input's.  Each op's formula and fp32 operation order is that of the separate
  * kernel of the same op, so every stored value has the bits the op-by-op
  * sequence gives:
  *   ADD a+b, SUB a-b, MUL a*b, DIV a/b (with flags & TS_HIP_MAP_CHECKED the
  *   divisor is checked as ts_hip_div does, from zero_check_start on, into
  *   zero_index), NEG (0-a before tail_start, -a after: ts_hip_neg), RELU,
  *   RELU_BWD (a > 0 ? b : +0: ts_hip_relu_backward with a the saved value, b
- *   the gradient), ADD_S / SUB_S / MUL_S / DIV_S (a op imm), SQUARE (a*a),
- *   CONST (imm for every element, as ts_hip_fill writes it; a and b are not
- *   read and may be any register, e.g. 0).
- * On an op without an immediate of its own (not the _S ops or CONST), flags &
- * TS_HIP_MAP_IMM_A (IMM_B) makes operand a (b) the op's imm instead of a
- * register (a constant folded into the op; the register is not read).
- * With sum_out != NULL, register reduce_reg is also added up into sum_out[0]
- * (divided by (float)n when mean) with the bits ts_hip_sum / ts_hip_mean give
- * over those values; the workspace is ts_hip_map_workspace_floats(n) floats,
- * 8-byte aligned. */
+ *   the gradient), ADD_S / SUB_S / MUL_S / DIV_S (a op imm), SQUARE (a*a).
+ * A constant input is the value ts_hip_fill would write into a buffer read in
+ * its place.  With sum_out != NULL, register reduce_reg is also added up into
+ * sum_out[0] (divided by (float)n when mean) with the bits ts_hip_sum /
+ * ts_hip_mean give over those values; the workspace is
+ * ts_hip_map_workspace_floats(n) floats, 8-byte aligned. */
 #define TS_HIP_MAP_MAX_INPUTS 5
 #define TS_HIP_MAP_MAX_OPS 11
 #define TS_HIP_MAP_MAX_OUTPUTS 4
 #define TS_HIP_MAP_CHECKED 1
-#define TS_HIP_MAP_IMM_A 2
-#define TS_HIP_MAP_IMM_B 4
 enum {
     TS_HIP_MAP_ADD = 0, TS_HIP_MAP_SUB = 1, TS_HIP_MAP_MUL = 2, TS_HIP_MAP_DIV = 3, TS_HIP_MAP_NEG = 4,
     TS_HIP_MAP_RELU = 5, TS_HIP_MAP_RELU_BWD = 6, TS_HIP_MAP_ADD_S = 7, TS_HIP_MAP_SUB_S = 8,
-    TS_HIP_MAP_MUL_S = 9, TS_HIP_MAP_DIV_S = 10, TS_HIP_MAP_SQUARE = 11,
-    TS_HIP_MAP_CONST = 12
+    TS_HIP_MAP_MUL_S = 9, TS_HIP_MAP_DIV_S = 10, TS_HIP_MAP_SQUARE = 11
 };
 typedef struct ts_hip_map_op {
     uint8_t code, a, b, flags;
@@ -301,6 +296,8 @@ typedef struct ts_hip_map_program {
     float *outputs[TS_HIP_MAP_MAX_OUTPUTS];
     uint8_t output_regs[TS_HIP_MAP_MAX_OUTPUTS];
     int32_t reduce_reg;
+    uint32_t const_inputs;
+    float const_values[TS_HIP_MAP_MAX_INPUTS];
 } ts_hip_map_program;
 size_t ts_hip_map_workspace_floats(size_t n);
 int ts_hip_map(const ts_hip_map_program *prog, size_t n, size_t tail_start, size_t zero_check_start,

@@ -24,15 +24,19 @@ def _ffi():
     return _ffi
 
 
-def _program(inputs, ops, outputs, scalar=0, reduce_reg=-1):
+def _program(inputs, ops, outputs, scalar=0, reduce_reg=-1, consts=None):
     """inputs: device pointers; ops: (code name, a, b, imm, flags) with
-    registers numbered as in include/ts_hip.h; outputs: (pointer, register)."""
+    registers numbered as in include/ts_hip.h; outputs: (pointer, register);
+    consts: {input index: value} for constant inputs (their pointer unused)."""
     F = _ffi()
     p = F.MapProgram()
     p.n_inputs = len(inputs)
     for k, ptr in enumerate(inputs):
         p.inputs[k] = ptr
     p.scalar_inputs = scalar
+    for k, v in (consts or {}).items():
+        p.const_inputs |= 1 << k
+        p.const_values[k] = v
     p.n_ops = len(ops)
     for k, (code, a, b, imm, flags) in enumerate(ops):
         p.ops[k] = F.MapOp(F.MAP_CODES[code], a, b, flags, imm)
@@ -75,8 +79,6 @@ def test_each_op_matches_its_kernel(n, offset):
         ("mul_s", -3.1, lambda o: hip.ts_hip_mul_scalar(da.ptr, ctypes.c_float(-3.1), o, n, None)),
         ("div_s", 7.0, lambda o: hip.ts_hip_div_scalar(da.ptr, ctypes.c_float(7.0), o, n, None)),
         ("square", 0.0, lambda o: hip.ts_hip_pow_scalar(da.ptr, ctypes.c_float(2.0), o, n, None)),
-        ("const", -0.0, lambda o: hip.ts_hip_fill(o, ctypes.c_float(-0.0), n, None)),
-        ("const", 0.37, lambda o: hip.ts_hip_fill(o, ctypes.c_float(0.37), n, None)),
     ]
     for code, imm, ref in cases:
         got, want = Dev(n, offset), Dev(n, offset)
@@ -163,59 +165,52 @@ def test_fused_sum_has_the_bits_of_ts_hip_sum(n, mean):
 
 
 @pytest.mark.parametrize("n", [7, 4099])
-def test_immediate_operands_match_a_filled_operand(n):
-    # an operand flagged IMM_A / IMM_B is the op's imm: the same bits as the
-    # separate kernel reading a buffer filled with that value
-    from gpu_util import Dev, ZeroIndex, hip, hip_check, sync
-    F = _ffi()
-    print(f"[map imm] n={n}", flush=True)
+def test_constant_inputs_match_a_filled_buffer(n):
+    # a constant input is the value ts_hip_fill writes: every op reading it,
+    # on either side, has the bits of its separate kernel reading a buffer
+    # filled with it (NEG's body / tail rule included)
+    from gpu_util import Dev, hip, hip_check, sync
+    print(f"[map constant inputs] n={n}", flush=True)
     a = normal(n, 11)
     a[: 3] = np.array([0.0, -0.0, np.inf], np.float32)
     da = Dev.of(a)
     tail8, tail32 = 8 * (n // 8), 32 * (n // 32)
-    zi = ZeroIndex()
     binary = {"add": hip.ts_hip_add, "sub": hip.ts_hip_sub, "mul": hip.ts_hip_mul,
+              "div": lambda x, y, o, m, s: hip.ts_hip_div(x, y, o, m, tail32, None, s),
               "relu_bwd": hip.ts_hip_relu_backward}
-    for v in (1.0, -0.0, 0.625, -3.0):
+    for v in (1.0, -0.0, 0.0, 0.625, -3.0):
         filled = Dev(n)
         hip_check(hip.ts_hip_fill(filled.ptr, ctypes.c_float(v), n, None))
-        for code in ("add", "sub", "mul", "div", "relu_bwd"):
-            for side in ("a", "b"):
+        for code, ref in binary.items():
+            for side in (0, 1):  # the constant as operand a (side 0) or b
                 got, want = Dev(n), Dev(n)
-                flag = F.MAP_IMM_A if side == "a" else F.MAP_IMM_B
-                x, y = (filled, da) if side == "a" else (da, filled)
-                prog = _program([da.ptr], [(code, 0, 0, v, flag)], [(got.ptr, R0)])
+                ins = [None, da.ptr] if side == 0 else [da.ptr, None]
+                k = side  # the constant's register
+                prog = _program(ins, [(code, 0, 1, 0.0, 0)], [(got.ptr, R0)], consts={k: v})
                 hip_check(hip.ts_hip_map(ctypes.byref(prog), n, tail8, tail32, None, None, 0, None, 0, None), code)
-                if code == "div":
-                    hip_check(hip.ts_hip_div(x.ptr, y.ptr, want.ptr, n, tail32, zi.ptr, None))
-                else:
-                    hip_check(binary[code](x.ptr, y.ptr, want.ptr, n, None))
+                x, y = (filled, da) if side == 0 else (da, filled)
+                hip_check(ref(x.ptr, y.ptr, want.ptr, n, None))
                 sync()
-                zi.reset()
-                assert_bits_equal(got.get(), want.get(), f"{code} imm {side} = {v}")
-        # a unary op and both operands of a binary one
-        for code, ref in (("neg", lambda o: hip.ts_hip_neg(filled.ptr, o, n, tail8, None)),
-                          ("square", lambda o: hip.ts_hip_mul(filled.ptr, filled.ptr, o, n, None)),
-                          ("mul", lambda o: hip.ts_hip_mul(filled.ptr, filled.ptr, o, n, None))):
-            got, want = Dev(n), Dev(n)
-            prog = _program([da.ptr], [(code, 0, 0, v, F.MAP_IMM_A | F.MAP_IMM_B)], [(got.ptr, R0)])
-            hip_check(hip.ts_hip_map(ctypes.byref(prog), n, tail8, tail32, None, None, 0, None, 0, None), code)
-            hip_check(ref(want.ptr))
-            sync()
-            assert_bits_equal(got.get(), want.get(), f"{code} both imm = {v}")
+                assert_bits_equal(got.get(), want.get(), f"{code} constant {v} as operand {'ab'[side]}")
+        got, want = Dev(n), Dev(n)
+        prog = _program([None], [("neg", 0, 0, 0.0, 0)], [(got.ptr, R0)], consts={0: v})
+        hip_check(hip.ts_hip_map(ctypes.byref(prog), n, tail8, tail32, None, None, 0, None, 0, None), "neg")
+        hip_check(hip.ts_hip_neg(filled.ptr, want.ptr, n, tail8, None))
+        sync()
+        assert_bits_equal(got.get(), want.get(), f"neg of constant {v}")
 
 
 @pytest.mark.parametrize("n", [1, 4096, 4099, 100003])
-def test_program_without_inputs(n):
-    # a constant (the deferred gradient seed) and what is computed from it,
-    # stored and summed, with no input buffer at all
+def test_program_of_a_constant_input(n):
+    # a constant input (the deferred gradient seed), stored as it is and
+    # scaled, the scaled value summed: no input buffer at all
     from gpu_util import Dev, hip, hip_check, sync
     print(f"[map const] n={n}", flush=True)
-    stored, out = Dev(n), Dev(1)
+    stored, both, out = Dev(n), Dev(n), Dev(1)
     ws = hip.ts_hip_map_workspace_floats(n)
     dws = Dev(ws + 2)
-    prog = _program([], [("const", 0, 0, 1.5, 0), ("mul_s", R0, R0, 0.25, 0)], [(stored.ptr, R0 + 1)],
-                    reduce_reg=R0 + 1)
+    prog = _program([None], [("mul_s", 0, 0, 0.25, 0)], [(stored.ptr, R0), (both.ptr, 0)], reduce_reg=R0,
+                    consts={0: 1.5})
     hip_check(hip.ts_hip_map(ctypes.byref(prog), n, 8 * (n // 8), 32 * (n // 32), None, out.ptr, 0, dws.ptr, ws,
                              None), "map")
     filled, want = Dev(n), Dev(1)
@@ -225,6 +220,7 @@ def test_program_without_inputs(n):
     hip_check(hip.ts_hip_sum(filled.ptr, n, want.ptr, dsw.ptr, sw, None))
     sync()
     assert_bits_equal(stored.get(), np.full(n, 0.375, np.float32), "stored")
+    assert_bits_equal(both.get(), np.full(n, 1.5, np.float32), "the constant itself")
     assert_bits_equal(out.get(), want.get(), "sum")
 
 
@@ -254,15 +250,20 @@ def test_bad_programs_are_refused():
     d = Dev(16)
     bad = [
         _program([d.ptr], [("add", 0, R0 + 1, 0.0, 0)], [(d.ptr, R0)]),    # reads a later register
-        _program([], [("const", 0, 0, 1.0, 0)], [(d.ptr, 0)]),              # stores an absent input
-        _program([d.ptr], [("add_s", 0, 0, 1.0, 2)], [(d.ptr, R0)]),       # imm operand on an _S op
-        _program([d.ptr], [("const", 0, 0, 1.0, 4)], [(d.ptr, R0)]),       # imm operand on CONST
+        _program([], [], [(d.ptr, 0)]),                                     # stores an absent input
+        _program([None], [("neg", 0, 0, 0.0, 0)], [(d.ptr, R0)]),          # no buffer, not constant
         _program([d.ptr], [("add", 0, 3, 0.0, 0)], [(d.ptr, R0)]),         # input register past n_inputs
         _program([d.ptr], [("add", 0, 0, 0.0, 0)], [(d.ptr, R0 + 1)]),     # output of no op
         _program([d.ptr], [("add", 0, 0, 0.0, 0)], []),                    # nothing stored, no sum
     ]
     for p in bad:
         assert hip.ts_hip_map(ctypes.byref(p), 16, 16, 0, None, None, 0, None, 0, None) == 100001
+    p = _program([d.ptr], [("add", 0, 0, 0.0, 0)], [(d.ptr, R0)])
+    p.ops[0].code = 12                                                   # no such op
+    assert hip.ts_hip_map(ctypes.byref(p), 16, 16, 0, None, None, 0, None, 0, None) == 100001
+    p = _program([d.ptr], [("add", 0, 0, 0.0, 0)], [(d.ptr, R0)], reduce_reg=2)  # sums an absent input
+    out = Dev(1)
+    assert hip.ts_hip_map(ctypes.byref(p), 16, 16, 0, None, out.ptr, 0, d.ptr, 16, None) == 100001
     p = _program([d.ptr], [("add", 0, 0, 0.0, 0)], [(d.ptr, R0)], reduce_reg=R0)
     out = Dev(1)
     assert hip.ts_hip_map(ctypes.byref(p), 16, 16, 0, None, out.ptr, 0, None, 0, None) == 100003  # no workspace
@@ -328,3 +329,30 @@ def test_chain_runs_as_few_fused_passes(T):
     assert per_elem == 20.0 + 28.0, per_elem
     # the seed is still ones when read
     assert_bits_equal(loss.grad().data(), np.ones(1, np.float32), "seed")
+
+
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
+@pytest.mark.parametrize("loss", ["sum", "mean"])
+@pytest.mark.parametrize("relu", [False, True])
+def test_seeded_gradients_equal_the_unfused_ones(T, op, loss, relu):
+    # backward(None) seeds a deferred constant, an input of the backward
+    # formulas' pass with no buffer: the gradients have the bits of the
+    # op-by-op sequence with a stored seed (fusion off)
+    n = 4099
+    av, bv = normal(n, 31), uniform(n, 0.5, 2.0, 32)
+
+    def run(fused):
+        T.set_fusion(fused)
+        a, b = (T.Tensor.from_slice(v, [n]).with_requires_grad() for v in (av, bv))
+        y = getattr(a, f"{op}_tensor")(b)
+        if relu:
+            y = y.relu()
+        getattr(y, loss)().backward()
+        out = [a.grad_by_value().data(), b.grad_by_value().data()]
+        T.clear_gradients()
+        return out
+
+    off = run(False)
+    on = run(True)
+    for name, u, v in zip(("ga", "gb"), on, off):
+        assert_bits_equal(u, v, f"{op} {loss} relu={relu} {name}")

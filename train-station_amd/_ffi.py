@@ -38,10 +38,8 @@ def _load(name: str) -> ctypes.CDLL:
 MAP_MAX_INPUTS, MAP_MAX_OPS, MAP_MAX_OUTPUTS = 5, 11, 4
 # TS_HIP_MAP_* op codes and flags of include/ts_hip.h
 MAP_CODES = {"add": 0, "sub": 1, "mul": 2, "div": 3, "neg": 4, "relu": 5, "relu_bwd": 6, "add_s": 7, "sub_s": 8,
-             "mul_s": 9, "div_s": 10, "square": 11, "const": 12}
+             "mul_s": 9, "div_s": 10, "square": 11}
 MAP_CHECKED = 1
-MAP_IMM_A = 2
-MAP_IMM_B = 4
 
 
 class MapOp(ctypes.Structure):
@@ -55,7 +53,8 @@ class MapProgram(ctypes.Structure):
     _fields_ = [("inputs", VP * MAP_MAX_INPUTS), ("scalar_inputs", _c.c_uint32), ("n_inputs", _c.c_uint32),
                 ("n_ops", _c.c_uint32), ("n_outputs", _c.c_uint32), ("ops", MapOp * MAP_MAX_OPS),
                 ("outputs", VP * MAP_MAX_OUTPUTS), ("output_regs", _c.c_uint8 * MAP_MAX_OUTPUTS),
-                ("reduce_reg", _c.c_int32)]
+                ("reduce_reg", _c.c_int32), ("const_inputs", _c.c_uint32),
+                ("const_values", _c.c_float * MAP_MAX_INPUTS)]
 
 
 # name -> (restype, argtypes); every symbol declared in include/ts_hip.h

@@ -110,7 +110,7 @@ void engine_backward(Tensor &root, const Tensor *grad_output) {
     // (the root's seed, a deferred constant, reads no buffer and stays
     // deferred until read)
     if (root.grad_ref() && root.grad_ref()->allocation() && root.grad_ref()->allocation()->map &&
-        !(root.grad_ref()->allocation()->map->leaves.empty() && root.grad_ref()->allocation()->map->nodes.size() == 1))
+        !root.grad_ref()->allocation()->map->constant())
         deferred.push_back(root.grad_ref()->allocation());
     materialize_maps(deferred);
     // and the column sums (bias gradients) no weight-gradient product produced

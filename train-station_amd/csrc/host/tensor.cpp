@@ -372,27 +372,46 @@ struct MapBuilder {
     int ops = 0;
     std::map<std::tuple<uint8_t, uint8_t, int, int, uint32_t>, int> cse;
 
-    int leaf(const std::shared_ptr<Allocation> &al, bool scalar) {
-        // a deferred constant is read as its value, whatever the element count
-        if (al->map && is_constant(*al->map)) return constant(al->map->nodes[0].imm);
-        for (size_t k = 0; k < p.leaves.size(); ++k)
-            if (p.leaves[k] == al && (((p.scalar >> k) & 1u) != 0) == scalar)
-                for (size_t j = 0; j < p.nodes.size(); ++j)
-                    if (p.nodes[j].code == MapNode::kLeaf && p.nodes[j].a == static_cast<int>(k)) return static_cast<int>(j);
-        const int k = static_cast<int>(p.leaves.size());
-        p.leaves.push_back(al);
-        if (scalar) p.scalar |= 1u << k;
+    int leaf_node(int k) {
+        for (size_t j = 0; j < p.nodes.size(); ++j)
+            if (p.nodes[j].code == MapNode::kLeaf && p.nodes[j].a == k) return static_cast<int>(j);
         MapNode nd;
         nd.a = static_cast<int16_t>(k);
         p.nodes.push_back(nd);
         return static_cast<int>(p.nodes.size()) - 1;
     }
+    int leaf(const std::shared_ptr<Allocation> &al, bool scalar) {
+        // a deferred constant is read as its value, whatever the element count
+        if (al->map && al->map->constant()) return constant(*al->map->constant());
+        for (size_t k = 0; k < p.leaves.size(); ++k)
+            if (p.leaves[k] == al && (((p.scalar >> k) & 1u) != 0) == scalar) return leaf_node(static_cast<int>(k));
+        const int k = static_cast<int>(p.leaves.size());
+        p.leaves.push_back(al);
+        p.values.push_back(0.0f);
+        if (scalar) p.scalar |= 1u << k;
+        return leaf_node(k);
+    }
+    // a constant: an input of the pass holding v for every element (one leaf
+    // per distinct value, no buffer, nothing read per element)
+    int constant(float v) {
+        for (size_t k = 0; k < p.leaves.size(); ++k)
+            if (((p.consts >> k) & 1u) && std::memcmp(&p.values[k], &v, 4) == 0) return leaf_node(static_cast<int>(k));
+        const int k = static_cast<int>(p.leaves.size());
+        p.leaves.push_back(nullptr);
+        p.values.push_back(v);
+        p.consts |= 1u << k;
+        p.scalar |= 1u << k;
+        return leaf_node(k);
+    }
+    bool is_const(int j, float v) const {
+        const MapNode &nd = p.nodes[j];
+        return nd.code == MapNode::kLeaf && ((p.consts >> nd.a) & 1u) && p.values[nd.a] == v;
+    }
     int op(uint8_t code, int a, int b, float imm = 0.0f, uint8_t flags = 0) {
         if (b < 0) b = a;
         // the constant one scaled by imm is imm exactly (the mean's gradient
         // of the seed)
-        if (code == TS_HIP_MAP_MUL_S && a >= 0 && p.nodes[a].code == TS_HIP_MAP_CONST && p.nodes[a].imm == 1.0f)
-            return constant(imm);
+        if (code == TS_HIP_MAP_MUL_S && a >= 0 && is_const(a, 1.0f)) return constant(imm);
         uint32_t bits;
         std::memcpy(&bits, &imm, 4);
         const auto key = std::make_tuple(code, flags, a, b, bits);
@@ -405,15 +424,10 @@ struct MapBuilder {
         nd.b = static_cast<int16_t>(b);
         nd.imm = imm;
         p.nodes.push_back(nd);
-        if (code != TS_HIP_MAP_CONST) ++ops;  // a constant takes an op only when it needs a register
+        ++ops;
         const int id = static_cast<int>(p.nodes.size()) - 1;
         cse.emplace(key, id);
         return id;
-    }
-    // a constant node (TS_HIP_MAP_CONST reads no operand)
-    int constant(float v) { return op(TS_HIP_MAP_CONST, -1, -1, v); }
-    static bool is_constant(const PendingMap &m) {
-        return m.leaves.empty() && m.nodes.size() == 1 && m.nodes[0].code == TS_HIP_MAP_CONST;
     }
     // m's program merged in; returns the node of its value, which records
     // `origin` (the allocation m was deferred for)
@@ -422,9 +436,8 @@ struct MapBuilder {
         for (size_t j = 0; j < m.nodes.size(); ++j) {
             const MapNode &nd = m.nodes[j];
             if (nd.code == MapNode::kLeaf) {
-                remap[j] = leaf(m.leaves[nd.a], ((m.scalar >> nd.a) & 1u) != 0);
-            } else if (nd.code == TS_HIP_MAP_CONST) {
-                remap[j] = constant(nd.imm);
+                remap[j] = ((m.consts >> nd.a) & 1u) ? constant(m.values[nd.a])
+                                                     : leaf(m.leaves[nd.a], ((m.scalar >> nd.a) & 1u) != 0);
             } else {
                 remap[j] = op(nd.code, remap[nd.a], remap[nd.b], nd.imm, nd.flags);
                 if (p.nodes[remap[j]].origin.expired() && !nd.origin.expired()) p.nodes[remap[j]].origin = nd.origin;
@@ -439,35 +452,8 @@ struct MapBuilder {
         if (al->map && al->map->n == n) return import(*al->map, al);
         return leaf(al, false);
     }
-    static bool own_immediate(uint8_t code) {
-        return code == TS_HIP_MAP_CONST || (code >= TS_HIP_MAP_ADD_S && code <= TS_HIP_MAP_DIV_S);
-    }
-    bool is_const(int j) const { return p.nodes[j].code == TS_HIP_MAP_CONST; }
-    // The constant nodes computed into a register by a TS_HIP_MAP_CONST op:
-    // those in `pinned` (stored or summed) and those read by an op that
-    // cannot take them as its immediate (an op with an immediate of its own,
-    // or the first of two different constants).  Every other read folds the
-    // constant into the op (TS_HIP_MAP_IMM_A / _B).
-    std::vector<char> const_registers(const std::vector<int> &pinned) const {
-        std::vector<char> in_reg(p.nodes.size(), 0);
-        for (int j : pinned)
-            if (j >= 0 && is_const(j)) in_reg[j] = 1;
-        for (const MapNode &nd : p.nodes) {
-            if (nd.code == MapNode::kLeaf || nd.code == TS_HIP_MAP_CONST) continue;
-            if (own_immediate(nd.code)) {
-                if (is_const(nd.a)) in_reg[nd.a] = 1;
-            } else if (is_const(nd.a) && is_const(nd.b) && nd.a != nd.b && !in_reg[nd.b]) {
-                in_reg[nd.a] = 1;
-            }
-        }
-        return in_reg;
-    }
-    // whether the program, storing or summing the nodes in `pinned`, is within
-    // the fused pass's limits
-    bool fits(const std::vector<int> &pinned) const {
-        int regs = ops;
-        for (char c : const_registers(pinned)) regs += c;
-        return p.leaves.size() <= static_cast<size_t>(TS_HIP_MAP_MAX_INPUTS) && regs <= TS_HIP_MAP_MAX_OPS;
+    bool fits() const {
+        return p.leaves.size() <= static_cast<size_t>(TS_HIP_MAP_MAX_INPUTS) && ops <= TS_HIP_MAP_MAX_OPS;
     }
 };
 
@@ -485,9 +471,8 @@ void launch_program(MapBuilder &b, std::vector<MapOutput> outs, int reduce = -1,
     for (size_t j = 0; j < b.p.nodes.size() && outs.size() < static_cast<size_t>(TS_HIP_MAP_MAX_OUTPUTS); ++j) {
         auto o = b.p.nodes[j].origin.lock();
         // still held (a saved operand, or its tensor): it may be read again,
-        // and this pass computes it anyway, so it stores it (a constant stays
-        // deferred: storing it saves nothing)
-        if (!o || !o->map || o.use_count() <= 1 || b.is_const(static_cast<int>(j))) continue;
+        // and this pass computes it anyway, so it stores it
+        if (!o || !o->map || o.use_count() <= 1) continue;
         bool listed = false;
         for (const MapOutput &m : outs) listed = listed || m.alloc == o;
         if (!listed) outs.push_back({o, static_cast<int>(j)});
@@ -496,15 +481,16 @@ void launch_program(MapBuilder &b, std::vector<MapOutput> outs, int reduce = -1,
     ts_hip_map_program prog{};
     prog.n_inputs = static_cast<uint32_t>(b.p.leaves.size());
     prog.scalar_inputs = b.p.scalar;
+    prog.const_inputs = b.p.consts;
     double bytes = 0.0;
     for (size_t k = 0; k < b.p.leaves.size(); ++k) {
+        if ((b.p.consts >> k) & 1u) {  // a constant: no buffer
+            prog.const_values[k] = b.p.values[k];
+            continue;
+        }
         prog.inputs[k] = b.p.leaves[k]->get();
         if (!((b.p.scalar >> k) & 1u)) bytes += 4.0 * n;
     }
-    std::vector<int> pinned;
-    for (const MapOutput &m : outs) pinned.push_back(m.node);
-    pinned.push_back(reduce);
-    const std::vector<char> in_reg = b.const_registers(pinned);
     std::vector<int> reg(b.p.nodes.size(), -1);
     for (size_t j = 0; j < b.p.nodes.size(); ++j) {
         const MapNode &nd = b.p.nodes[j];
@@ -512,28 +498,12 @@ void launch_program(MapBuilder &b, std::vector<MapOutput> outs, int reduce = -1,
             reg[j] = nd.a;
             continue;
         }
-        if (nd.code == TS_HIP_MAP_CONST && !in_reg[j]) continue;  // folded into the ops that read it
-        if (prog.n_ops >= static_cast<uint32_t>(TS_HIP_MAP_MAX_OPS))
-            throw Error("an elementwise program exceeds the fused pass's limits");
         ts_hip_map_op &op = prog.ops[prog.n_ops];
         op.code = nd.code;
+        op.a = static_cast<uint8_t>(reg[nd.a]);
+        op.b = static_cast<uint8_t>(reg[nd.b]);
         op.flags = nd.flags;
         op.imm = nd.imm;
-        // a register, or the folded constant as the op's immediate
-        auto operand = [&](int src, uint8_t flag) -> uint8_t {
-            if (b.is_const(src) && !in_reg[src]) {
-                op.flags |= flag;
-                op.imm = b.p.nodes[src].imm;
-                return 0;
-            }
-            return static_cast<uint8_t>(reg[src]);
-        };
-        if (nd.code == TS_HIP_MAP_CONST) {  // reads no register
-            op.a = op.b = 0;
-        } else {
-            op.a = operand(nd.a, TS_HIP_MAP_IMM_A);
-            op.b = operand(nd.b, TS_HIP_MAP_IMM_B);
-        }
         reg[j] = TS_HIP_MAP_MAX_INPUTS + static_cast<int>(prog.n_ops);
         ++prog.n_ops;
     }
@@ -573,7 +543,7 @@ std::shared_ptr<PendingMap> defer(size_t n, const std::vector<std::pair<std::sha
         std::vector<int> ids;
         for (const auto &o : operands) ids.push_back(o.second ? b.leaf(o.first, true) : b.value(o.first, n));
         b.p.root = build(b, ids);
-        if (b.fits({b.p.root})) return std::make_shared<PendingMap>(std::move(b.p));
+        if (b.fits()) return std::make_shared<PendingMap>(std::move(b.p));
         for (const auto &o : operands) o.first->get();
     }
     throw Error("an elementwise program exceeds the fused pass's limits");
@@ -629,9 +599,7 @@ void materialize_maps(const std::vector<std::shared_ptr<Allocation>> &allocs) {
         if (!outs.empty() && group.p.n == al->map->n && outs.size() < static_cast<size_t>(TS_HIP_MAP_MAX_OUTPUTS)) {
             MapBuilder trial = group;
             const int r = trial.import(*al->map, al);
-            std::vector<int> pinned{r};
-            for (const MapOutput &m : outs) pinned.push_back(m.node);
-            if (trial.fits(pinned)) {
+            if (trial.fits()) {
                 group = std::move(trial);
                 outs.push_back({al, r});
                 continue;
@@ -673,14 +641,10 @@ Tensor Tensor::filled(std::vector<size_t> dims, float v) {
 Tensor Tensor::constant(std::vector<size_t> dims, float v) {
     const size_t n = product(dims);
     if (!defer_ok(n)) return filled(std::move(dims), v);
-    auto p = std::make_shared<PendingMap>();
-    p->n = n;
-    MapNode nd;
-    nd.code = TS_HIP_MAP_CONST;
-    nd.imm = v;
-    p->nodes.push_back(nd);
-    p->root = 0;
-    return deferred_tensor(dims, std::move(p));
+    MapBuilder b;
+    b.p.n = n;
+    b.p.root = b.constant(v);
+    return deferred_tensor(dims, std::make_shared<PendingMap>(std::move(b.p)));
 }
 
 Tensor Tensor::zeros(std::vector<size_t> dims) { return filled(std::move(dims), 0.0f); }

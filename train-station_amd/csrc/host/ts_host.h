@@ -152,8 +152,15 @@ struct PendingMap {
     size_t n = 0;  // elements
     std::vector<std::shared_ptr<Allocation>> leaves;
     uint32_t scalar = 0;  // bit k: leaf k is one value used for every element
+    // bit k: leaf k is the constant values[k] (no buffer; leaves[k] is null)
+    uint32_t consts = 0;
+    std::vector<float> values;  // per leaf
     std::vector<MapNode> nodes;  // in evaluation order
     int root = -1;
+    // the whole program is one constant (a deferred fill): its value, or null
+    const float *constant() const {
+        return (leaves.size() == 1 && consts == 1u && nodes.size() == 1 && root == 0) ? &values[0] : nullptr;
+    }
 };
 
 // A deferred column sum out[n] = sum over r of src[r][n] of a [rows, cols]

@@ -55,11 +55,8 @@ __device__ __forceinline__ void run_program(const MapArgsK &a, size_t i0, unsign
         // operands read once, the op's values formed in temporaries, the
         // register file written once after the switch (writing it in every
         // case makes the compiler keep several copies of it)
-        // an operand flagged TS_HIP_MAP_IMM_A / _B is the op's immediate (a
-        // folded constant) instead of a register
-        const bool ia = (op.flags & TS_HIP_MAP_IMM_A) != 0, ib = (op.flags & TS_HIP_MAP_IMM_B) != 0;
-        const float x[W] = {(ia ? op.imm : r[op.a])...};
-        const float y[W] = {(ib ? op.imm : r[op.b])...};
+        const float x[W] = {r[op.a]...};
+        const float y[W] = {r[op.b]...};
         float v[W];
         switch (op.code) {
             case TS_HIP_MAP_ADD: ((v[C] = x[C] + y[C]), ...); break;
@@ -86,7 +83,6 @@ __device__ __forceinline__ void run_program(const MapArgsK &a, size_t i0, unsign
             case TS_HIP_MAP_SUB_S: ((v[C] = x[C] - op.imm), ...); break;
             case TS_HIP_MAP_MUL_S: ((v[C] = x[C] * op.imm), ...); break;
             case TS_HIP_MAP_DIV_S: ((v[C] = x[C] / op.imm), ...); break;
-            case TS_HIP_MAP_CONST: ((v[C] = op.imm), ...); break;  // ts_hip_fill's value
             default: ((v[C] = x[C] * x[C]), ...); break;  // TS_HIP_MAP_SQUARE: pow_scalar(2)
         }
         const int d = kMapIn + static_cast<int>(k);
@@ -102,7 +98,9 @@ __device__ __forceinline__ void load_inputs(const MapArgsK &a, size_t i0, bool v
     for (int k = 0; k < kMapIn; ++k) {
         if (k >= static_cast<int>(p.n_inputs)) break;
         const float *in = p.inputs[k];
-        if (p.scalar_inputs & (1u << k)) {
+        if (p.const_inputs & (1u << k)) {
+            ((r[k] = p.const_values[k]), ...);
+        } else if (p.scalar_inputs & (1u << k)) {
             const float s = in[0];
             ((r[k] = s), ...);
         } else if (vec4) {
@@ -157,10 +155,13 @@ __global__ __launch_bounds__(kBlock) void map_program_vec(MapArgsK a) {
     const auto seq = std::make_index_sequence<4>{};
     double acc = 0.0;
     unsigned long long zmin = ~0ull;
-    float sv[kMapIn];  // scalar inputs, read once
+    float sv[kMapIn];  // scalar and constant inputs, read once
 #pragma unroll
     for (int k = 0; k < kMapIn; ++k)
-        sv[k] = (k < static_cast<int>(a.p.n_inputs) && (a.p.scalar_inputs & (1u << k))) ? a.p.inputs[k][0] : 0.0f;
+        sv[k] = k >= static_cast<int>(a.p.n_inputs)           ? 0.0f
+                : (a.p.const_inputs & (1u << k))            ? a.p.const_values[k]
+                : (a.p.scalar_inputs & (1u << k))           ? a.p.inputs[k][0]
+                                                            : 0.0f;
     f4v_t nx[NV > 0 ? NV : 1];  // the next group's per-element inputs
     auto fetch = [&](size_t g) {
 #pragma unroll
@@ -292,34 +293,27 @@ extern "C" int ts_hip_map(const ts_hip_map_program *prog, size_t n, size_t tail_
     const ts_hip_map_program &p = *prog;
     if (p.n_inputs > kMapIn || p.n_ops > kMapOps || p.n_outputs > kMapOut) return TS_HIP_EINVAL;
     const bool reduce = sum_out != nullptr;
-    if (reduce && (p.reduce_reg < 0 || p.reduce_reg >= static_cast<int>(kMapIn + p.n_ops))) return TS_HIP_EINVAL;
+    auto holds_value = [&](int r) {  // an input's register or a computed op's
+        return (r >= 0 && r < static_cast<int>(p.n_inputs)) || (r >= kMapIn && r < kMapIn + static_cast<int>(p.n_ops));
+    };
+    if (reduce && !holds_value(p.reduce_reg)) return TS_HIP_EINVAL;
     if (!reduce && p.n_outputs == 0) return TS_HIP_EINVAL;
-    // every register read must be an input or an earlier op's value (CONST
-    // and an immediate operand read none; their operand registers are only
-    // required to exist); immediate operands only on ops without an
-    // immediate of their own
+    // every register read must be an input or an earlier op's value
     for (uint32_t k = 0; k < p.n_ops; ++k) {
         const ts_hip_map_op &op = p.ops[k];
-        const bool own_imm = op.code == TS_HIP_MAP_CONST || (op.code >= TS_HIP_MAP_ADD_S && op.code <= TS_HIP_MAP_DIV_S);
-        const bool imm_ops = (op.flags & (TS_HIP_MAP_IMM_A | TS_HIP_MAP_IMM_B)) != 0;
-        auto ok = [&](int r, bool unread) {
-            if (unread) return r < kMapRegs;
-            return r < static_cast<int>(p.n_inputs) || (r >= kMapIn && r < kMapIn + static_cast<int>(k));
-        };
-        const bool konst = op.code == TS_HIP_MAP_CONST;
-        if (!ok(op.a, konst || (op.flags & TS_HIP_MAP_IMM_A)) || !ok(op.b, konst || (op.flags & TS_HIP_MAP_IMM_B)) ||
-            op.code > TS_HIP_MAP_CONST || (own_imm && imm_ops))
-            return TS_HIP_EINVAL;
+        auto ok = [&](int r) { return r < static_cast<int>(p.n_inputs) || (r >= kMapIn && r < kMapIn + static_cast<int>(k)); };
+        if (!ok(op.a) || !ok(op.b) || op.code > TS_HIP_MAP_SQUARE) return TS_HIP_EINVAL;
     }
     for (uint32_t o = 0; o < p.n_outputs; ++o) {
         const int q = p.output_regs[o];
-        if (!p.outputs[o] || !(q < static_cast<int>(p.n_inputs) || (q >= kMapIn && q < kMapIn + static_cast<int>(p.n_ops))))
-            return TS_HIP_EINVAL;
+        if (!p.outputs[o] || !holds_value(q)) return TS_HIP_EINVAL;
     }
+    // per-element inputs: neither scalar nor constant
+    const uint32_t one_value = p.scalar_inputs | p.const_inputs;
     bool vec = true;
     for (uint32_t k = 0; k < p.n_inputs; ++k) {
-        if (!p.inputs[k]) return TS_HIP_EINVAL;
-        if (!(p.scalar_inputs & (1u << k))) vec = vec && aligned16(p.inputs[k]);
+        if (!(p.const_inputs & (1u << k)) && !p.inputs[k]) return TS_HIP_EINVAL;
+        if (!(one_value & (1u << k))) vec = vec && aligned16(p.inputs[k]);
     }
     for (uint32_t o = 0; o < p.n_outputs; ++o) vec = vec && aligned16(p.outputs[o]);
     hipStream_t s = as_stream(stream);
@@ -336,7 +330,7 @@ extern "C" int ts_hip_map(const ts_hip_map_program *prog, size_t n, size_t tail_
     a.vec = vec;
     int nv = 0;
     for (uint32_t k = 0; k < p.n_inputs; ++k)
-        if (!(p.scalar_inputs & (1u << k))) {
+        if (!(one_value & (1u << k))) {
             a.vin[nv] = p.inputs[k];
             a.vreg[nv] = static_cast<int>(k);
             ++nv;
