@@ -83,7 +83,7 @@ def rel_l2(got, want) -> float:
     return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
 
 
-def sum_order_model(values, mean=False, aligned=True) -> np.float32:
+def sum_order_model(values, mean=False, aligned=True, times=None) -> np.float32:
     """The fp32 result of ts_hip_sum / ts_hip_mean (and of a fused sum in
     ts_hip_map) over `values`, in the partition's order, restated in numpy:
     ceil(n / 1024) first-pass workgroups (at most 2048) of 256 threads; thread
@@ -93,8 +93,12 @@ def sum_order_model(values, mean=False, aligned=True) -> np.float32:
     xor butterfly over each wave's 64 lanes, the four wave sums added from +0;
     the second pass's thread t adds partials t, t + 256, ... from +0, then the
     same workgroup sum; one rounding to fp32 (divided by (float)n for the
-    mean).  Whatever kernels run, the bits are these."""
+    mean).  With `times`, the sum of products x[i] * times[i] (ts_hip_dot),
+    each product formed in f64 (exact).  Whatever kernels run, the bits are
+    these."""
     x = np.asarray(values, np.float32).astype(np.float64)
+    if times is not None:
+        x = x * np.asarray(times, np.float32).astype(np.float64)
     n = x.size
     if n == 0:
         return np.float32(0.0)

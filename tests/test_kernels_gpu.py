@@ -182,6 +182,19 @@ def test_sum_bits_follow_the_partition(n, offset):
         assert_bits_equal(dout.get(), np.array([want], np.float32), f"{name} n={n} offset={offset}")
 
 
+@pytest.mark.parametrize("offset", [0, 1])
+@pytest.mark.parametrize("n", [1, 5, 1024, 4096, 8192, 8193, 16384, 100003])
+def test_dot_bits_follow_the_partition(n, offset):
+    print(f"[dot bits] n={n} offset={offset}", flush=True)
+    a, b = normal(n, 13), normal(n, 14)
+    da, db = Dev.of(a, offset), Dev.of(b, offset)
+    ws = hip.ts_hip_sum_workspace_floats(n)
+    dws, dout = Dev(ws), Dev(1)
+    _run("ts_hip_dot", da.ptr, db.ptr, n, dout.ptr, dws.ptr, ws, None)
+    want = sum_order_model(a, aligned=offset == 0, times=b)
+    assert_bits_equal(dout.get(), np.array([want], np.float32), f"dot n={n} offset={offset}")
+
+
 def test_sum_known_answers():
     for xs, want in (([i * 0.5 for i in range(6)], 7.5), ([1, 2, 3, 4, 5, 6], 21.0),
                      (list(range(24)), 276.0)):

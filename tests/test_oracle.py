@@ -318,6 +318,8 @@ def test_sum_order_model_known_answers():
         ints = np.arange(n, dtype=np.float32) % 97 - 48
         assert sum_order_model(ints) == np.float32(np.sum(ints.astype(np.int64)))
         assert sum_order_model(ints, aligned=False) == np.float32(np.sum(ints.astype(np.int64)))
+        sq = np.sum(ints.astype(np.int64) ** 2)
+        assert sum_order_model(ints, times=ints) == np.float32(sq)  # products exact in f64
     assert sum_order_model([]) == 0.0
     x = normal(1 << 21, 5)
     exact = math.fsum(x.astype(np.float64))

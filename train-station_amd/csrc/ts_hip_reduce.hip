@@ -72,10 +72,14 @@ int launch_sum_final(const double *partial, size_t nparts, size_t n, float *out,
 // and thread t then adds partials t, t + 256, ... from +0 as sum_final's
 // threads do, combined by block_sum.
 constexpr int kSumSmallBlocks = 16;
+// a product's two operands take twice the registers: half as many workgroups
+template <bool PROD>
+constexpr int small_blocks() { return PROD ? kSumSmallBlocks / 2 : kSumSmallBlocks; }
 
 template <bool PROD, bool MEAN>
 __global__ __launch_bounds__(kBlock) void sum_small(const float *__restrict__ x, const float *__restrict__ y,
                                                     size_t n, size_t n4, int blocks, float *out) {
+    constexpr int kSumSmallBlocks = small_blocks<PROD>();
     __shared__ double wsum[kSumSmallBlocks][kBlock / 64];
     __shared__ double parts[kSumSmallBlocks];
     const int t = static_cast<int>(threadIdx.x), lane = t & 63, wave = t >> 6;
@@ -112,9 +116,10 @@ __global__ __launch_bounds__(kBlock) void sum_small(const float *__restrict__ x,
     if (4 * n4 + t < n) acc[0] += PROD ? (double)tx * (double)ty : (double)tx;
 #pragma unroll
     for (int b = 0; b < kSumSmallBlocks; ++b) {
-        if (b >= blocks) break;  // uniform
-        const double s = wave_sum(acc[b]);
-        if (lane == 0) wsum[b][wave] = s;
+        if (b < blocks) {  // uniform
+            const double s = wave_sum(acc[b]);
+            if (lane == 0) wsum[b][wave] = s;
+        }
     }
     __syncthreads();
     if (t < blocks) {
@@ -147,7 +152,8 @@ static int launch_sum(const float *x, const float *y, size_t n, float *out, floa
     if ((reinterpret_cast<uintptr_t>(workspace) & 7u) != 0) return TS_HIP_EINVAL;
     double *partial = reinterpret_cast<double *>(workspace);
     size_t n4 = (aligned16(x) && (!y || aligned16(y))) ? n / 4 : 0;
-    if (blocks <= static_cast<size_t>(kSumSmallBlocks) && n4 == n / 4) {  // one launch, the same bits
+    if (blocks <= static_cast<size_t>(y ? small_blocks<true>() : small_blocks<false>()) && n4 == n / 4) {
+        // one launch, the same bits
         const int nb = static_cast<int>(blocks);
         if (y) launch(sum_small<true, MEAN>, dim3(1), dim3(kBlock), 0, s, x, y, n, n4, nb, out);
         else launch(sum_small<false, MEAN>, dim3(1), dim3(kBlock), 0, s, x, y, n, n4, nb, out);
