@@ -404,6 +404,44 @@ int ts_hip_gemm_colsum(int trans_a, size_t M, size_t N, size_t K, const float *A
                        size_t ldb, float *C, size_t ldc, float *colsum, float *workspace, size_t workspace_floats,
                        void *stream);
 
+/* Operand transforms (no counterpart in the reference, which stores the
+ * elementwise op's result and then multiplies it: e.g. relu's backward,
+ * grad_fn/ops/relu.rs:4-17, or the MSE's gradient, grad_fn/ops/pow.rs:5-27,
+ * before the matmul backward of grad_fn/ops/matmul.rs:68-80).  A
+ * ts_hip_operand_xf is applied to each element of its operand as the product
+ * loads it: n_ops ops in order, each x = op(x, imm[i]) as one fp32 operation
+ * with the bits of the elementwise kernel of that op:
+ *   ADD_S x+imm, SUB_S x-imm, MUL_S x*imm, DIV_S x/imm, RSUB_S imm-x,
+ *   RDIV_S imm/x, RELU (x > 0 ? x : +0), RELU_BWD_S (x > 0 ? imm : +0: relu's
+ *   backward with a gradient of imm everywhere), SQUARE (x*x).
+ * The chain must map +0 to +0 (the zeros that pad a k tile stay zeros);
+ * TS_HIP_EINVAL otherwise.  The product, its epilogue and its column sums
+ * then have the bits of the same call on an operand holding the transformed
+ * values.  Only the kernels of products that ts_hip_gemm_takes_xf accepts
+ * apply transforms (register-staged tiles, few-column and one-k-tile
+ * kernels: products with fewer than one 256x256 tile per compute unit and
+ * no split of K); the _xf calls refuse the rest with TS_HIP_EINVAL.  xa / xb
+ * NULL: no transform of that operand. */
+#define TS_HIP_XF_MAX_OPS 4
+enum {
+    TS_HIP_XF_ADD_S = 0, TS_HIP_XF_SUB_S = 1, TS_HIP_XF_MUL_S = 2, TS_HIP_XF_DIV_S = 3, TS_HIP_XF_RSUB_S = 4,
+    TS_HIP_XF_RDIV_S = 5, TS_HIP_XF_RELU = 6, TS_HIP_XF_RELU_BWD_S = 7, TS_HIP_XF_SQUARE = 8
+};
+typedef struct ts_hip_operand_xf {
+    uint32_t n_ops;
+    uint8_t code[TS_HIP_XF_MAX_OPS];
+    float imm[TS_HIP_XF_MAX_OPS];
+} ts_hip_operand_xf;
+int ts_hip_gemm_takes_xf(int trans_a, int trans_b, size_t M, size_t N, size_t K, int colsum);
+int ts_hip_gemm_fused_xf(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A, size_t lda,
+                         const ts_hip_operand_xf *xa, const float *B, size_t ldb, const ts_hip_operand_xf *xb,
+                         const float *bias, int relu, const float *mask, float *C, size_t ldc, float *workspace,
+                         size_t workspace_floats, void *stream);
+int ts_hip_gemm_colsum_xf(int trans_a, size_t M, size_t N, size_t K, const float *A, size_t lda,
+                          const ts_hip_operand_xf *xa, const float *B, size_t ldb, const ts_hip_operand_xf *xb,
+                          float *C, size_t ldc, float *colsum, float *workspace, size_t workspace_floats,
+                          void *stream);
+
 /* Batched C[b] = op(A[b]) . op(B[b]) (matmul/mod.rs:634-760 batched_matmul and
  * the batched backward of grad_fn/ops/matmul.rs:150-219) on the same MFMA
  * tiles: a batch grid of batch_rank axes (<= 6) with sizes batch_dims; the A /

@@ -42,6 +42,17 @@ MAP_CODES = {"add": 0, "sub": 1, "mul": 2, "div": 3, "neg": 4, "relu": 5, "relu_
 MAP_CHECKED = 1
 
 
+XF_MAX_OPS = 4
+# TS_HIP_XF_* operand-transform op codes of include/ts_hip.h
+XF_CODES = {"add_s": 0, "sub_s": 1, "mul_s": 2, "div_s": 3, "rsub_s": 4, "rdiv_s": 5, "relu": 6, "relu_bwd_s": 7,
+            "square": 8}
+
+
+class OperandXf(ctypes.Structure):
+    """struct ts_hip_operand_xf of include/ts_hip.h"""
+    _fields_ = [("n_ops", _c.c_uint32), ("code", _c.c_uint8 * XF_MAX_OPS), ("imm", _c.c_float * XF_MAX_OPS)]
+
+
 class MapOp(ctypes.Structure):
     """struct ts_hip_map_op of include/ts_hip.h"""
     _fields_ = [("code", _c.c_uint8), ("a", _c.c_uint8), ("b", _c.c_uint8), ("flags", _c.c_uint8),
@@ -137,6 +148,10 @@ HIP_SIGNATURES = {
     "ts_hip_gemm_noalloc": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, SZ, VP]),
     "ts_hip_gemm_colsum_workspace_floats": (SZ, [_c.c_int, SZ, SZ, SZ]),
     "ts_hip_gemm_colsum": (_c.c_int, [_c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, SZ, VP, VP, SZ, VP]),
+    "ts_hip_gemm_takes_xf": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, _c.c_int]),
+    "ts_hip_gemm_fused_xf": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, VP, SZ, VP, VP, SZ, VP, VP, _c.c_int, VP,
+                                        VP, SZ, VP, SZ, VP]),
+    "ts_hip_gemm_colsum_xf": (_c.c_int, [_c.c_int, SZ, SZ, SZ, VP, SZ, VP, VP, SZ, VP, VP, SZ, VP, VP, SZ, VP]),
     "ts_hip_gemm_workspace_floats": (SZ, [SZ, SZ, SZ]),
     "ts_hip_gemm_batched": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, SZ, SZ,
                                        _c.POINTER(SZ), _c.POINTER(SZ), _c.POINTER(SZ), SZ, VP]),

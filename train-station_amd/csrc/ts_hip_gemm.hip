@@ -41,6 +41,7 @@
 // current two run, across tile boundaries too.  Its k order per MFMA differs
 // (k of step s, lane half h = 4*(s/2) + 2h + s%2) so that a k-contiguous
 // operand gives two steps' values in one 8-byte LDS read.
+#include <cstring>
 #include <mutex>
 #include <vector>
 
@@ -58,6 +59,59 @@ constexpr int kXcds = 8;
 __device__ __forceinline__ int swz(int k) { return (((k >> 2) & 3) << 4) ^ ((k & 1) << 5); }
 
 constexpr int kMaxBatchRank = 6;
+
+// An elementwise transform of one operand, applied to each element as it is
+// loaded (ts_hip_operand_xf; n == 0: none).  It maps +0 to +0, so the zeros
+// that pad a partial k tile stay zeros.
+struct OperandXf {
+    int n;
+    uint8_t code[TS_HIP_XF_MAX_OPS];
+    float imm[TS_HIP_XF_MAX_OPS];
+};
+
+// The ops of ts_hip_operand_xf in order on every element of v (V: an
+// indexable set of floats, E of them), each one fp32 operation as the
+// elementwise kernel of the same op computes it.  The op's case is chosen
+// once per op (a uniform branch) and the elements are looped inside it:
+// per element, the switch multiplied the kernels' code (and compile time)
+// by the element count.
+#define TS_XF_EACH(expr) \
+    _Pragma("unroll") for (int e = 0; e < E; ++e) { float &x = at(e); x = (expr); } break
+template <int E, class At>
+__device__ __forceinline__ void xf_each(const OperandXf &xf, At &&at) {
+    for (int i = 0; i < TS_HIP_XF_MAX_OPS; ++i) {
+        if (i >= xf.n) break;  // uniform
+        const float c = xf.imm[i];
+        switch (xf.code[i]) {
+            case TS_HIP_XF_ADD_S: TS_XF_EACH(x + c);
+            case TS_HIP_XF_SUB_S: TS_XF_EACH(x - c);
+            case TS_HIP_XF_MUL_S: TS_XF_EACH(x * c);
+            case TS_HIP_XF_DIV_S: TS_XF_EACH(x / c);
+            case TS_HIP_XF_RSUB_S: TS_XF_EACH(c - x);
+            case TS_HIP_XF_RDIV_S: TS_XF_EACH(c / x);
+            case TS_HIP_XF_RELU: TS_XF_EACH(x > 0.0f ? x : 0.0f);
+            case TS_HIP_XF_RELU_BWD_S: TS_XF_EACH(x > 0.0f ? c : 0.0f);
+            default: TS_XF_EACH(x * x);  // TS_HIP_XF_SQUARE
+        }
+    }
+}
+#undef TS_XF_EACH
+
+template <int N>
+__device__ __forceinline__ void xf_array(const OperandXf &xf, float (&v)[N]) {
+    if (xf.n) xf_each<N>(xf, [&](int e) -> float & { return v[e]; });
+}
+
+template <int NF>
+__device__ __forceinline__ void xf_regs(const OperandXf &xf, f4v_t (&reg)[NF]) {
+    if (!xf.n) return;  // uniform
+    float v[4 * NF];
+#pragma unroll
+    for (int e = 0; e < 4 * NF; ++e) v[e] = reg[e / 4][e % 4];
+    xf_each<4 * NF>(xf, [&](int e) -> float & { return v[e]; });
+#pragma unroll
+    for (int e = 0; e < 4 * NF; ++e) reg[e / 4][e % 4] = v[e];
+}
 
 struct GemmArgs {
     const float *A;
@@ -94,6 +148,9 @@ struct GemmArgs {
     float *colsum;
     double *colsum_part;
     int kslice;  // skinny: k rows per slice
+    // operand transforms (register-staged tiles, the narrow and one-k-tile
+    // kernels and the column strips apply them; the others take none)
+    OperandXf xa, xb;
 };
 
 // Store of a wave's FM x FN accumulator blocks, the wave tile's corner at
@@ -273,8 +330,8 @@ __device__ inline void tile_coords(int tiles_m, int tiles_n, int b, int &tm, int
 // into its running total, and finally stores it.
 constexpr int kStripCols = 16;
 
-template <int NT>
-__device__ void colsum_strip(const GemmArgs &g, int j0) {
+template <int NT, bool XF>
+__device__ __forceinline__ void colsum_strip(const GemmArgs &g, int j0) {
     constexpr int R = static_cast<int>(kColsumRows), G = static_cast<int>(kColsumGroup), RC = NT / kStripCols;
     static_assert(RC * kStripCols == NT && RC % G == 0, "a round holds whole groups of chunks");
     __shared__ double cs[RC][kStripCols];
@@ -289,6 +346,7 @@ __device__ void colsum_strip(const GemmArgs &g, int j0) {
             float v[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) v[r] = g.B[(size_t)min(r0 + rb + r, g.K - 1) * g.ldb + col];
+            if constexpr (XF) xf_array(g.xb, v);  // the rows past K are transformed too, and not added
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 if (r0 + rb + r < g.K) sum += (double)v[r];
@@ -320,11 +378,12 @@ __device__ void colsum_strip(const GemmArgs &g, int j0) {
 // loads (zeros outside).  CS (column sums of B): workgroups past the g.tiles
 // product tiles each take a strip of kStripCols columns (colsum_strip); the
 // grid has no other idle work for them.
-template <bool TA, bool TB, int BM, int BN, int WM, int WN, int EPI, int PF, bool VEC, bool CS = false>
+template <bool TA, bool TB, int BM, int BN, int WM, int WN, int EPI, int PF, bool VEC, bool CS = false,
+          bool XF = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
     static_assert(!CS || !TB, "column sums of B need trans_b == 0");
     if (CS && static_cast<int>(blockIdx.x) >= g.tiles) {  // uniform
-        colsum_strip<64 * WM * WN>(g, (static_cast<int>(blockIdx.x) - g.tiles) * kStripCols);
+        colsum_strip<64 * WM * WN, XF>(g, (static_cast<int>(blockIdx.x) - g.tiles) * kStripCols);
         return;
     }
     constexpr int NT = 64 * WM * WN;
@@ -412,6 +471,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
 
     if (nt > 0) {
         load(0, ra[0], rb[0]);
+        if constexpr (XF) {
+            xf_regs(g.xa, ra[0]);
+            xf_regs(g.xb, rb[0]);
+        }
         SA::store(As[0], ra[0]);
         SB::store(Bs[0], rb[0]);
 #pragma unroll
@@ -431,6 +494,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
                 // scheduler can place the stores and loads in the MFMAs'
                 // shadow (a wave issues in order).
                 mma(As[cur], Bs[cur]);
+                if constexpr (XF) {
+                    xf_regs(g.xa, ra[u]);
+                    xf_regs(g.xb, rb[u]);
+                }
                 SA::store(As[cur ^ 1], ra[u]);
                 SB::store(Bs[cur ^ 1], rb[u]);
                 load(kt + 1 + PF, ra[u], rb[u]);
@@ -442,6 +509,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
         f4v_t pa[SA::NF], pb[SB::NF];
         SA::load_guarded(Ap, g.lda, g.M, g.K, i0, nt * kBK, pa);
         SB::load_guarded(Bp, g.ldb, g.N, g.K, j0, nt * kBK, pb);
+        if constexpr (XF) {
+            xf_regs(g.xa, pa);
+            xf_regs(g.xb, pb);
+        }
         SA::store(As[0], pa);
         SB::store(Bs[0], pb);
         __syncthreads();
@@ -455,17 +526,30 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
 template <int BM>
 constexpr int prefetch_tiles() { return BM >= 256 ? 1 : 4; }
 
-template <int BM, int BN, int WM, int WN, int EPI, bool VEC>
-static void launch_tiles_vec(int ta, int tb, const GemmArgs &g, dim3 grid, dim3 block, hipStream_t s) {
+template <int BM, int BN, int WM, int WN, int EPI, bool VEC, bool XF>
+static void launch_tiles_xf(int ta, int tb, const GemmArgs &g, dim3 grid, dim3 block, hipStream_t s) {
     constexpr int PF = prefetch_tiles<BM>();
     if (g.colsum && ta && !tb) {  // dW with db (no epilogue)
-        launch((gemm_f32_mfma<true, false, BM, BN, WM, WN, kEpiNone, PF, VEC, true>), grid, block, 0, s, g);
+        launch((gemm_f32_mfma<true, false, BM, BN, WM, WN, kEpiNone, PF, VEC, true, XF>), grid, block, 0, s, g);
         return;
     }
-    if (!ta && !tb) launch((gemm_f32_mfma<false, false, BM, BN, WM, WN, EPI, PF, VEC>), grid, block, 0, s, g);
-    else if (!ta && tb) launch((gemm_f32_mfma<false, true, BM, BN, WM, WN, EPI, PF, VEC>), grid, block, 0, s, g);
-    else if (ta && !tb) launch((gemm_f32_mfma<true, false, BM, BN, WM, WN, EPI, PF, VEC>), grid, block, 0, s, g);
-    else launch((gemm_f32_mfma<true, true, BM, BN, WM, WN, EPI, PF, VEC>), grid, block, 0, s, g);
+    if (!ta && !tb) launch((gemm_f32_mfma<false, false, BM, BN, WM, WN, EPI, PF, VEC, false, XF>), grid, block, 0, s, g);
+    else if (!ta && tb) launch((gemm_f32_mfma<false, true, BM, BN, WM, WN, EPI, PF, VEC, false, XF>), grid, block, 0, s, g);
+    else if (ta && !tb) launch((gemm_f32_mfma<true, false, BM, BN, WM, WN, EPI, PF, VEC, false, XF>), grid, block, 0, s, g);
+    else launch((gemm_f32_mfma<true, true, BM, BN, WM, WN, EPI, PF, VEC, false, XF>), grid, block, 0, s, g);
+}
+
+// Operand transforms only on the 64x64 and 128x128 tiles (products with a
+// 256x256 grid that fills the chip take none).
+template <int BM, int BN, int WM, int WN, int EPI, bool VEC>
+static void launch_tiles_vec(int ta, int tb, const GemmArgs &g, dim3 grid, dim3 block, hipStream_t s) {
+    if constexpr (BM < 256) {
+        if (g.xa.n || g.xb.n) {
+            launch_tiles_xf<BM, BN, WM, WN, EPI, VEC, true>(ta, tb, g, grid, block, s);
+            return;
+        }
+    }
+    launch_tiles_xf<BM, BN, WM, WN, EPI, VEC, false>(ta, tb, g, grid, block, s);
 }
 
 template <int BM, int BN, int WM, int WN, int EPI>
@@ -865,7 +949,7 @@ static void launch_dma_layout(int ta, int tb, const GemmArgs &g, hipStream_t s, 
 // takes k = 2s + (lane half), as a tiled kernel's k tile does, and stops at
 // the last MFMA that holds a k < K (the tiled kernels add the zero products
 // of the rest), so the stored values are the same.
-template <bool TA, bool TB, int EPI>
+template <bool TA, bool TB, int EPI, bool XF = false>
 __global__ __launch_bounds__(256) void gemm_short_k(GemmArgs g) {
     int tm, tn;
     tile_coords(g.tiles_m, g.tiles_n, blockIdx.x, tm, tn);
@@ -891,6 +975,10 @@ __global__ __launch_bounds__(256) void gemm_short_k(GemmArgs g) {
         const bool in = 2 * s + lhalf < g.K;
         af[s] = in ? a : 0.0f;
         bf[s] = in ? b : 0.0f;
+    }
+    if constexpr (XF) {
+        xf_array(g.xa, af);
+        xf_array(g.xb, bf);
     }
     float mk[16], bj = 0.0f;
     if (EPI != kEpiNone) {
@@ -924,12 +1012,18 @@ __global__ __launch_bounds__(256) void gemm_short_k(GemmArgs g) {
     }
 }
 
+template <int EPI, bool XF>
+static void launch_short_k_xf(int ta, int tb, const GemmArgs &g, dim3 grid, hipStream_t s) {
+    if (!ta && !tb) launch((gemm_short_k<false, false, EPI, XF>), grid, dim3(256), 0, s, g);
+    else if (!ta) launch((gemm_short_k<false, true, EPI, XF>), grid, dim3(256), 0, s, g);
+    else if (!tb) launch((gemm_short_k<true, false, EPI, XF>), grid, dim3(256), 0, s, g);
+    else launch((gemm_short_k<true, true, EPI, XF>), grid, dim3(256), 0, s, g);
+}
+
 template <int EPI>
 static void launch_short_k_as(int ta, int tb, const GemmArgs &g, dim3 grid, hipStream_t s) {
-    if (!ta && !tb) launch((gemm_short_k<false, false, EPI>), grid, dim3(256), 0, s, g);
-    else if (!ta) launch((gemm_short_k<false, true, EPI>), grid, dim3(256), 0, s, g);
-    else if (!tb) launch((gemm_short_k<true, false, EPI>), grid, dim3(256), 0, s, g);
-    else launch((gemm_short_k<true, true, EPI>), grid, dim3(256), 0, s, g);
+    if (g.xa.n || g.xb.n) launch_short_k_xf<EPI, true>(ta, tb, g, grid, s);
+    else launch_short_k_xf<EPI, false>(ta, tb, g, grid, s);
 }
 
 static void launch_short_k(int ta, int tb, GemmArgs g, hipStream_t s) {
@@ -1129,7 +1223,7 @@ static_assert(kColsumRows == 64, "a narrow wave round is one column-sum chunk");
 
 // V: the k-contiguous operands (A unless TA, B when TB) take dwordx4 loads
 // (16-byte aligned, leading dimension % 4 == 0).
-template <bool TA, bool TB, bool V, bool CS>
+template <bool TA, bool TB, bool V, bool CS, bool XF = false>
 __global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) {
     static_assert(!CS || !TB, "column sums of B need trans_b == 0");
     __shared__ float red[kNarrowMaxWaves][256];
@@ -1194,6 +1288,10 @@ __global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) 
                     av[u][s] = k < ke ? a_at(k) : 0.0f;
                     bv[u][s] = k < ke ? b_at(k) : 0.0f;
                 }
+        }
+        if constexpr (XF) {
+            if (g.xa.n) xf_each<16>(g.xa, [&](int e) -> float & { return av[e / 4][e % 4]; });
+            if (g.xb.n) xf_each<16>(g.xb, [&](int e) -> float & { return bv[e / 4][e % 4]; });
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u)
@@ -1264,23 +1362,30 @@ static bool narrow_fits(size_t M, size_t N, size_t K) {
     return K <= kNarrowMaxK || 8 * blocks >= static_cast<size_t>(device_cu_count());
 }
 
+template <bool CS, bool XF>
+static void launch_narrow_xf(int trans_a, int trans_b, bool v, const GemmArgs &g, dim3 grid, dim3 block,
+                             hipStream_t s) {
+    if (!trans_a && !trans_b) {
+        if (v) launch((gemm_narrow<false, false, true, CS, XF>), grid, block, 0, s, g);
+        else launch((gemm_narrow<false, false, false, CS, XF>), grid, block, 0, s, g);
+    } else if (!trans_b) {
+        launch((gemm_narrow<true, false, false, CS, XF>), grid, block, 0, s, g);
+    } else if (!CS) {  // column sums need trans_b == 0 (checked by the caller)
+        if (!trans_a) {
+            if (v) launch((gemm_narrow<false, true, true, false, XF>), grid, block, 0, s, g);
+            else launch((gemm_narrow<false, true, false, false, XF>), grid, block, 0, s, g);
+        } else {
+            if (v) launch((gemm_narrow<true, true, true, false, XF>), grid, block, 0, s, g);
+            else launch((gemm_narrow<true, true, false, false, XF>), grid, block, 0, s, g);
+        }
+    }
+}
+
 template <bool CS>
 static void launch_narrow_as(int trans_a, int trans_b, bool v, const GemmArgs &g, dim3 grid, dim3 block,
                              hipStream_t s) {
-    if (!trans_a && !trans_b) {
-        if (v) launch((gemm_narrow<false, false, true, CS>), grid, block, 0, s, g);
-        else launch((gemm_narrow<false, false, false, CS>), grid, block, 0, s, g);
-    } else if (!trans_b) {
-        launch((gemm_narrow<true, false, false, CS>), grid, block, 0, s, g);
-    } else if (!CS) {  // column sums need trans_b == 0 (checked by the caller)
-        if (!trans_a) {
-            if (v) launch((gemm_narrow<false, true, true, false>), grid, block, 0, s, g);
-            else launch((gemm_narrow<false, true, false, false>), grid, block, 0, s, g);
-        } else {
-            if (v) launch((gemm_narrow<true, true, true, false>), grid, block, 0, s, g);
-            else launch((gemm_narrow<true, true, false, false>), grid, block, 0, s, g);
-        }
-    }
+    if (g.xa.n || g.xb.n) launch_narrow_xf<CS, true>(trans_a, trans_b, v, g, grid, block, s);
+    else launch_narrow_xf<CS, false>(trans_a, trans_b, v, g, grid, block, s);
 }
 
 // g carries the epilogue and, optionally, colsum (trans_b == 0, K <= kNarrowMaxK).
@@ -1418,16 +1523,60 @@ static GemmPlan gemm_plan(int trans_a, int trans_b, size_t M, size_t N, size_t K
     return p;
 }
 
+// Whether the kernels a product takes apply operand transforms: one pass of
+// the narrow, one-k-tile or register-staged kernels (fewer 256x256 tiles
+// than CUs, so never the LDS-DMA kernel), with its column sums (if any)
+// written by that pass.
+static bool xf_plan_ok(const GemmPlan &p, size_t M, size_t N, size_t K, bool colsum) {
+    if (M == 0 || N == 0 || K == 0) return true;
+    return !big_grid(M, N, 1) && p.slices == 1 && (p.narrow || !p.skinny) && (!colsum || p.cs_kernel);
+}
+
+// A caller's transform checked (codes, op count, +0 -> +0) and copied.
+static bool xf_from(const ts_hip_operand_xf *x, OperandXf &out) {
+    out = OperandXf{};
+    if (!x || x->n_ops == 0) return true;
+    if (x->n_ops > TS_HIP_XF_MAX_OPS) return false;
+    float v = 0.0f;
+    for (uint32_t i = 0; i < x->n_ops; ++i) {
+        const float c = x->imm[i];
+        switch (x->code[i]) {
+            case TS_HIP_XF_ADD_S: v = v + c; break;
+            case TS_HIP_XF_SUB_S: v = v - c; break;
+            case TS_HIP_XF_MUL_S: v = v * c; break;
+            case TS_HIP_XF_DIV_S: v = v / c; break;
+            case TS_HIP_XF_RSUB_S: v = c - v; break;
+            case TS_HIP_XF_RDIV_S: v = c / v; break;
+            case TS_HIP_XF_RELU: v = v > 0.0f ? v : 0.0f; break;
+            case TS_HIP_XF_RELU_BWD_S: v = v > 0.0f ? c : 0.0f; break;
+            case TS_HIP_XF_SQUARE: v = v * v; break;
+            default: return false;
+        }
+        out.code[i] = x->code[i];
+        out.imm[i] = c;
+    }
+    uint32_t bits;
+    std::memcpy(&bits, &v, 4);
+    if (bits != 0) return false;  // +0 must stay +0
+    out.n = static_cast<int>(x->n_ops);
+    return true;
+}
+
 // One 2-D product with an optional epilogue (GemmArgs::bias / mask / relu)
-// and optional column sums of B (colsum, trans_b == 0, no epilogue).  The
-// workspace is `ws` when given (at least gemm_plan(...).total() floats),
-// else it comes from the stream-ordered allocator.
+// and optional column sums of B (colsum, trans_b == 0, no epilogue), its
+// operands optionally transformed as loaded (xa, xb: null or n == 0 for
+// none).  The workspace is `ws` when given (at least gemm_plan(...).total()
+// floats), else it comes from the stream-ordered allocator.
 static int gemm_plain(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A, size_t lda,
                       const float *B, size_t ldb, float *C, size_t ldc, const float *bias, const float *mask,
-                      int relu, float *colsum, float *ws, size_t ws_floats, void *stream) {
+                      int relu, float *colsum, float *ws, size_t ws_floats, void *stream,
+                      const OperandXf *xa = nullptr, const OperandXf *xb = nullptr) {
     if (M == 0 || N == 0) return TS_HIP_OK;
     if (!C || ldc < N) return TS_HIP_EINVAL;
     if (colsum && (trans_b || bias || mask || relu)) return TS_HIP_EINVAL;
+    const bool xf = (xa && xa->n) || (xb && xb->n);
+    if (xf && !xf_plan_ok(gemm_plan(trans_a, trans_b, M, N, K, colsum != nullptr), M, N, K, colsum != nullptr))
+        return TS_HIP_EINVAL;
     if (K == 0) {  // empty contraction: C = 0, then the epilogue
         if (ldc != N) return TS_HIP_EINVAL;
         int st = ts_hip_fill(C, 0.0f, M * N, stream);
@@ -1464,6 +1613,8 @@ static int gemm_plain(int trans_a, int trans_b, size_t M, size_t N, size_t K, co
         g.bias = bias;
         g.mask = mask;
         g.relu = relu;
+        if (xa) g.xa = *xa;
+        if (xb) g.xb = *xb;
         if (plan.cs_kernel) g.colsum = colsum;
         status = launch_narrow(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, g, stream);
         if (status == TS_HIP_OK && colsum && !plan.cs_kernel)  // K past the kernel's chunk table
@@ -1505,6 +1656,8 @@ static int gemm_plain(int trans_a, int trans_b, size_t M, size_t N, size_t K, co
         g.bias = bias;
         g.mask = mask;
         g.relu = relu;
+        if (xa) g.xa = *xa;
+        if (xb) g.xb = *xb;
         if (plan.cs_kernel) {
             g.colsum = colsum;
             g.colsum_part = part;
@@ -1624,6 +1777,33 @@ extern "C" int ts_hip_gemm_colsum(int trans_a, size_t M, size_t N, size_t K, con
     }
     return gemm_plain(trans_a, 0, M, N, K, A, lda, B, ldb, C, ldc, nullptr, nullptr, 0, colsum, workspace,
                       workspace_floats, stream);
+}
+
+extern "C" int ts_hip_gemm_takes_xf(int trans_a, int trans_b, size_t M, size_t N, size_t K, int colsum) {
+    return xf_plan_ok(gemm_plan(trans_a, trans_b, M, N, K, colsum != 0), M, N, K, colsum != 0) ? 1 : 0;
+}
+
+extern "C" int ts_hip_gemm_fused_xf(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
+                                    size_t lda, const ts_hip_operand_xf *xa, const float *B, size_t ldb,
+                                    const ts_hip_operand_xf *xb, const float *bias, int relu, const float *mask,
+                                    float *C, size_t ldc, float *workspace, size_t workspace_floats,
+                                    void *stream) {
+    OperandXf fa, fb;
+    if (!xf_from(xa, fa) || !xf_from(xb, fb)) return TS_HIP_EINVAL;
+    return gemm_plain(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, bias, mask, relu != 0, nullptr, workspace,
+                      workspace_floats, stream, &fa, &fb);
+}
+
+extern "C" int ts_hip_gemm_colsum_xf(int trans_a, size_t M, size_t N, size_t K, const float *A, size_t lda,
+                                     const ts_hip_operand_xf *xa, const float *B, size_t ldb,
+                                     const ts_hip_operand_xf *xb, float *C, size_t ldc, float *colsum,
+                                     float *workspace, size_t workspace_floats, void *stream) {
+    OperandXf fa, fb;
+    if (!xf_from(xa, fa) || !xf_from(xb, fb)) return TS_HIP_EINVAL;
+    if (!colsum || M == 0) return TS_HIP_EINVAL;  // the column sums alone take no transform
+    if (N == 0) return TS_HIP_OK;
+    return gemm_plain(trans_a, 0, M, N, K, A, lda, B, ldb, C, ldc, nullptr, nullptr, 0, colsum, workspace,
+                      workspace_floats, stream, &fa, &fb);
 }
 
 extern "C" int ts_hip_gemm_batched(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
