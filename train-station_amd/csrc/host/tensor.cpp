@@ -288,14 +288,136 @@ std::vector<std::shared_ptr<Allocation>> pending_members(const Allocation &a, co
     return out;
 }
 
+// A deferred elementwise value that is a single chain of ops over one
+// per-element buffer, each op's other operand a constant (relu's backward of
+// the seed, the MSE's gradient 2 * d * (1/n)): that buffer, and the chain as
+// a GEMM operand transform (ts_hip_operand_xf), so a product reads the buffer
+// and the value itself is never stored.  False for anything else, or a chain
+// that does not keep +0 (the transform's condition).  The ops map one to
+// one: x op c is the _S op, c - x and c / x the reversed ones, c * x and
+// c + x the _S op (c not a NaN, so the operands' order cannot show); a
+// division checked for zero divisors, relu's backward with a constant
+// input and negation (whose sign rule depends on the index) do not map.
+bool operand_xf(const std::shared_ptr<Allocation> &al, std::shared_ptr<Allocation> &leaf, ts_hip_operand_xf &xf) {
+    if (!fusion_enabled() || !al || !al->map) return false;
+    const PendingMap &m = *al->map;
+    int vl = -1;  // the per-element buffer
+    for (size_t k = 0; k < m.leaves.size(); ++k) {
+        if ((m.consts >> k) & 1u) continue;
+        if (((m.scalar >> k) & 1u) || vl >= 0) return false;
+        vl = static_cast<int>(k);
+    }
+    if (vl < 0 || m.root < 0) return false;
+    auto const_of = [&](int j, float &c) {
+        const MapNode &nd = m.nodes[j];
+        if (nd.code != MapNode::kLeaf || !((m.consts >> nd.a) & 1u)) return false;
+        c = m.values[nd.a];
+        return true;
+    };
+    auto chain_op = [&](int j, uint8_t &code, float &c, int &next) {
+        const MapNode &nd = m.nodes[j];
+        next = nd.a;
+        c = nd.imm;
+        switch (nd.code) {
+            case TS_HIP_MAP_ADD_S: code = TS_HIP_XF_ADD_S; return true;
+            case TS_HIP_MAP_SUB_S: code = TS_HIP_XF_SUB_S; return true;
+            case TS_HIP_MAP_MUL_S: code = TS_HIP_XF_MUL_S; return true;
+            case TS_HIP_MAP_DIV_S: code = TS_HIP_XF_DIV_S; return true;
+            case TS_HIP_MAP_RELU: code = TS_HIP_XF_RELU; return true;
+            case TS_HIP_MAP_SQUARE: code = TS_HIP_XF_SQUARE; return true;
+            case TS_HIP_MAP_ADD:
+            case TS_HIP_MAP_MUL:
+                code = nd.code == TS_HIP_MAP_ADD ? TS_HIP_XF_ADD_S : TS_HIP_XF_MUL_S;
+                if (const_of(nd.b, c)) return true;
+                next = nd.b;
+                return const_of(nd.a, c) && !std::isnan(c);
+            case TS_HIP_MAP_SUB:
+                code = TS_HIP_XF_SUB_S;
+                if (const_of(nd.b, c)) return true;
+                code = TS_HIP_XF_RSUB_S;
+                next = nd.b;
+                return const_of(nd.a, c);
+            case TS_HIP_MAP_DIV:
+                if (nd.flags & TS_HIP_MAP_CHECKED) return false;
+                code = TS_HIP_XF_DIV_S;
+                if (const_of(nd.b, c)) return true;
+                code = TS_HIP_XF_RDIV_S;
+                next = nd.b;
+                return const_of(nd.a, c);
+            case TS_HIP_MAP_RELU_BWD:
+                code = TS_HIP_XF_RELU_BWD_S;
+                return const_of(nd.b, c);
+            default:
+                return false;
+        }
+    };
+    uint8_t codes[TS_HIP_XF_MAX_OPS];
+    float imms[TS_HIP_XF_MAX_OPS];
+    int len = 0;
+    for (int j = m.root; !(m.nodes[j].code == MapNode::kLeaf && m.nodes[j].a == vl);) {
+        if (m.nodes[j].code == MapNode::kLeaf || len == TS_HIP_XF_MAX_OPS) return false;
+        int next;
+        if (!chain_op(j, codes[len], imms[len], next)) return false;
+        ++len;
+        j = next;
+    }
+    int ops = 0;  // nothing else computed in the program
+    for (const MapNode &nd : m.nodes) ops += nd.code != MapNode::kLeaf;
+    if (ops != len || len == 0) return false;
+    xf = ts_hip_operand_xf{};
+    xf.n_ops = static_cast<uint32_t>(len);
+    float z = 0.0f;  // +0 through the chain, innermost op first
+    for (int i = 0; i < len; ++i) {
+        xf.code[i] = codes[len - 1 - i];
+        xf.imm[i] = imms[len - 1 - i];
+        const float c = xf.imm[i];
+        switch (xf.code[i]) {
+            case TS_HIP_XF_ADD_S: z = z + c; break;
+            case TS_HIP_XF_SUB_S: z = z - c; break;
+            case TS_HIP_XF_MUL_S: z = z * c; break;
+            case TS_HIP_XF_DIV_S: z = z / c; break;
+            case TS_HIP_XF_RSUB_S: z = c - z; break;
+            case TS_HIP_XF_RDIV_S: z = c / z; break;
+            case TS_HIP_XF_RELU: z = z > 0.0f ? z : 0.0f; break;
+            case TS_HIP_XF_RELU_BWD_S: z = z > 0.0f ? c : 0.0f; break;
+            default: z = z * z; break;
+        }
+    }
+    uint32_t bits;
+    std::memcpy(&bits, &z, 4);
+    if (bits != 0) return false;
+    leaf = m.leaves[vl];
+    return true;
+}
+
+// gemm2d with operand transforms (null: none)
+int gemm2d_xf(int ta, int tb, size_t M, size_t N, size_t K, const float *A, size_t lda, const ts_hip_operand_xf *xa,
+              const float *B, size_t ldb, const ts_hip_operand_xf *xb, const float *bias, bool relu,
+              const float *mask, float *C, size_t ldc) {
+    const size_t ws = ts_hip_gemm_workspace_floats(M, N, K);
+    std::unique_ptr<Allocation> work;
+    if (ws) work = std::make_unique<Allocation>(ws);
+    return ts_hip_gemm_fused_xf(ta, tb, M, N, K, A, lda, xa, B, ldb, xb, bias, relu ? 1 : 0, mask, C, ldc,
+                                work ? work->get() : nullptr, ws, S());
+}
+
 void launch_product(const PendingGemm &p, float *C, bool with_epilogue) {
+    // an operand that is a deferred chain over one buffer is read as that
+    // buffer, the chain applied as it is loaded
+    ts_hip_operand_xf xa{}, xb{};
+    std::shared_ptr<Allocation> la, lb;
+    const bool takes = ts_hip_gemm_takes_xf(p.ta, p.tb, p.M, p.N, p.K, 0) != 0;
+    const bool fa = takes && operand_xf(p.A, la, xa), fb = takes && operand_xf(p.B, lb, xb);
     // inputs first (they may be deferred themselves), outside this launch's window
-    const float *A = p.A->get(), *B = p.B->get();
+    const float *A = fa ? la->get() : p.A->get(), *B = fb ? lb->get() : p.B->get();
     const float *bias = with_epilogue && p.bias ? p.bias->get() : nullptr;
     const float *mask = with_epilogue && p.mask ? p.mask->get() : nullptr;
     const bool relu = with_epilogue && p.relu;
     DevicePool::get().note_use(C);  // a step being recorded writes it on every replay
     launch(KernelClass::Gemm, 2.0 * p.M * p.N * p.K, "ts_hip_gemm_fused", [&] {
+        if (fa || fb)
+            return gemm2d_xf(p.ta, p.tb, p.M, p.N, p.K, A, p.lda, fa ? &xa : nullptr, B, p.ldb, fb ? &xb : nullptr,
+                             bias, relu, mask, C, p.N);
         return gemm2d(p.ta, p.tb, p.M, p.N, p.K, A, p.lda, B, p.ldb, bias, relu, mask, C, p.N);
     });
 }
@@ -1453,21 +1575,29 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
                                 break;
                             }
                         }
+                    // go deferred as a chain over one buffer (relu's backward of the
+                    // seed, the MSE's gradient): the product reads that buffer and
+                    // applies the chain as it loads it; go is never stored
+                    ts_hip_operand_xf xb{};
+                    std::shared_ptr<Allocation> leaf;
+                    const bool fx = ts_hip_gemm_takes_xf(1, 0, Kd, N, M, db ? 1 : 0) &&
+                                    operand_xf(go.allocation(), leaf, xb);
                     if (db) {
                         db->colsum.reset();
-                        const float *A = a.ptr(), *B = go.dev();
+                        const float *A = a.ptr(), *B = fx ? leaf->get() : go.dev();
                         float *C = t.dev_mut();
                         const size_t ws = ts_hip_gemm_colsum_workspace_floats(1, Kd, N, M);
                         std::unique_ptr<Allocation> work;  // from the pool: the launch allocates nothing
                         if (ws) work = std::make_unique<Allocation>(ws);
                         launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm_colsum(dW, db)", [&] {
-                            return ts_hip_gemm_colsum(1, Kd, N, M, A, Kd, B, N, C, N, db->raw(),
-                                                      work ? work->get() : nullptr, ws, S());
+                            return ts_hip_gemm_colsum_xf(1, Kd, N, M, A, Kd, nullptr, B, N, fx ? &xb : nullptr, C, N,
+                                                         db->raw(), work ? work->get() : nullptr, ws, S());
                         });
                     } else {
+                        const float *B = fx ? leaf->get() : go.dev();
                         launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm(dW)", [&] {
-                            return gemm2d(1, 0, Kd, N, M, a.ptr(), Kd, go.dev(), N, nullptr, false, nullptr,
-                                          t.dev_mut(), N);
+                            return gemm2d_xf(1, 0, Kd, N, M, a.ptr(), Kd, nullptr, B, N, fx ? &xb : nullptr, nullptr,
+                                             false, nullptr, t.dev_mut(), N);
                         });
                     }
                     gr = std::move(t);

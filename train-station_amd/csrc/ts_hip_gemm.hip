@@ -69,20 +69,38 @@ struct OperandXf {
     float imm[TS_HIP_XF_MAX_OPS];
 };
 
-// The ops of ts_hip_operand_xf in order on every element of v (V: an
-// indexable set of floats, E of them), each one fp32 operation as the
-// elementwise kernel of the same op computes it.  The op's case is chosen
-// once per op (a uniform branch) and the elements are looped inside it:
-// per element, the switch multiplied the kernels' code (and compile time)
-// by the element count.
+// A transform read once into scalar registers (the op codes packed in one
+// word), so applying it reads no memory.
+struct XfRegs {
+    int n;
+    uint32_t codes;
+    float c0, c1, c2, c3;
+};
+__device__ __forceinline__ XfRegs xf_load(const OperandXf &x) {
+    XfRegs r;
+    r.n = x.n;
+    r.codes = static_cast<uint32_t>(x.code[0]) | (static_cast<uint32_t>(x.code[1]) << 8) |
+              (static_cast<uint32_t>(x.code[2]) << 16) | (static_cast<uint32_t>(x.code[3]) << 24);
+    r.c0 = x.imm[0];
+    r.c1 = x.imm[1];
+    r.c2 = x.imm[2];
+    r.c3 = x.imm[3];
+    return r;
+}
+
+// The ops of the transform in order on every element (at(e), E of them),
+// each one fp32 operation as the elementwise kernel of the same op computes
+// it.  The op's case is chosen once per op (a uniform branch) with the
+// elements looped inside it: a switch per element multiplied the kernels'
+// code (and compile time) by the element count.
 #define TS_XF_EACH(expr) \
     _Pragma("unroll") for (int e = 0; e < E; ++e) { float &x = at(e); x = (expr); } break
 template <int E, class At>
-__device__ __forceinline__ void xf_each(const OperandXf &xf, At &&at) {
-    for (int i = 0; i < TS_HIP_XF_MAX_OPS; ++i) {
-        if (i >= xf.n) break;  // uniform
-        const float c = xf.imm[i];
-        switch (xf.code[i]) {
+__device__ __forceinline__ void xf_each(const XfRegs &xf, At &&at) {
+    for (int i = 0; i < xf.n; ++i) {  // uniform
+        const uint32_t code = (xf.codes >> (8 * i)) & 255u;
+        const float c = i == 0 ? xf.c0 : i == 1 ? xf.c1 : i == 2 ? xf.c2 : xf.c3;
+        switch (code) {
             case TS_HIP_XF_ADD_S: TS_XF_EACH(x + c);
             case TS_HIP_XF_SUB_S: TS_XF_EACH(x - c);
             case TS_HIP_XF_MUL_S: TS_XF_EACH(x * c);
@@ -98,12 +116,12 @@ __device__ __forceinline__ void xf_each(const OperandXf &xf, At &&at) {
 #undef TS_XF_EACH
 
 template <int N>
-__device__ __forceinline__ void xf_array(const OperandXf &xf, float (&v)[N]) {
+__device__ __forceinline__ void xf_array(const XfRegs &xf, float (&v)[N]) {
     if (xf.n) xf_each<N>(xf, [&](int e) -> float & { return v[e]; });
 }
 
 template <int NF>
-__device__ __forceinline__ void xf_regs(const OperandXf &xf, f4v_t (&reg)[NF]) {
+__device__ __forceinline__ void xf_regs(const XfRegs &xf, f4v_t (&reg)[NF]) {
     if (!xf.n) return;  // uniform
     float v[4 * NF];
 #pragma unroll
@@ -338,6 +356,7 @@ __device__ __forceinline__ void colsum_strip(const GemmArgs &g, int j0) {
     const int t = static_cast<int>(threadIdx.x), q = t / kStripCols, j = t % kStripCols;
     const int col = min(j0 + j, g.N - 1);
     const int chunks = (g.K + R - 1) / R;
+    const XfRegs xfb = xf_load(g.xb);
     double total = 0.0;
     for (int c0 = 0; c0 < chunks; c0 += RC) {  // uniform
         const int r0 = (c0 + q) * R;
@@ -346,7 +365,7 @@ __device__ __forceinline__ void colsum_strip(const GemmArgs &g, int j0) {
             float v[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) v[r] = g.B[(size_t)min(r0 + rb + r, g.K - 1) * g.ldb + col];
-            if constexpr (XF) xf_array(g.xb, v);  // the rows past K are transformed too, and not added
+            if constexpr (XF) xf_array(xfb, v);  // the rows past K are transformed too, and not added
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 if (r0 + rb + r < g.K) sum += (double)v[r];
@@ -423,6 +442,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WN, wn = wave % WN;
     const int lrow = lane & 31, lhalf = lane >> 5;
+    const XfRegs xfa = XF ? xf_load(g.xa) : XfRegs{}, xfb = XF ? xf_load(g.xb) : XfRegs{};
 
     floatx16 acc[FM][FN];
 #pragma unroll
@@ -472,8 +492,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
     if (nt > 0) {
         load(0, ra[0], rb[0]);
         if constexpr (XF) {
-            xf_regs(g.xa, ra[0]);
-            xf_regs(g.xb, rb[0]);
+            xf_regs(xfa, ra[0]);
+            xf_regs(xfb, rb[0]);
         }
         SA::store(As[0], ra[0]);
         SB::store(Bs[0], rb[0]);
@@ -495,8 +515,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
                 // shadow (a wave issues in order).
                 mma(As[cur], Bs[cur]);
                 if constexpr (XF) {
-                    xf_regs(g.xa, ra[u]);
-                    xf_regs(g.xb, rb[u]);
+                    xf_regs(xfa, ra[u]);
+                    xf_regs(xfb, rb[u]);
                 }
                 SA::store(As[cur ^ 1], ra[u]);
                 SB::store(Bs[cur ^ 1], rb[u]);
@@ -510,8 +530,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
         SA::load_guarded(Ap, g.lda, g.M, g.K, i0, nt * kBK, pa);
         SB::load_guarded(Bp, g.ldb, g.N, g.K, j0, nt * kBK, pb);
         if constexpr (XF) {
-            xf_regs(g.xa, pa);
-            xf_regs(g.xb, pb);
+            xf_regs(xfa, pa);
+            xf_regs(xfb, pb);
         }
         SA::store(As[0], pa);
         SB::store(Bs[0], pb);
@@ -977,8 +997,8 @@ __global__ __launch_bounds__(256) void gemm_short_k(GemmArgs g) {
         bf[s] = in ? b : 0.0f;
     }
     if constexpr (XF) {
-        xf_array(g.xa, af);
-        xf_array(g.xb, bf);
+        xf_array(xf_load(g.xa), af);
+        xf_array(xf_load(g.xb), bf);
     }
     float mk[16], bj = 0.0f;
     if (EPI != kEpiNone) {
@@ -1238,6 +1258,7 @@ __global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) 
     const int kc = ((g.K + waves - 1) / waves + 63) & ~63;
     const int kb = min(g.K, wave * kc), ke = min(g.K, kb + kc);
     const bool cs_wg = CS && blockIdx.x == 0;  // uniform
+    const XfRegs xfa = XF ? xf_load(g.xa) : XfRegs{}, xfb = XF ? xf_load(g.xb) : XfRegs{};
     const float *__restrict__ A = g.A;
     const float *__restrict__ B = g.B;
     auto a_at = [&](int k) { return TA ? A[(size_t)k * g.lda + m] : A[(size_t)m * g.lda + k]; };
@@ -1290,8 +1311,8 @@ __global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) 
                 }
         }
         if constexpr (XF) {
-            if (g.xa.n) xf_each<16>(g.xa, [&](int e) -> float & { return av[e / 4][e % 4]; });
-            if (g.xb.n) xf_each<16>(g.xb, [&](int e) -> float & { return bv[e / 4][e % 4]; });
+            xf_each<16>(xfa, [&](int e) -> float & { return av[e / 4][e % 4]; });
+            xf_each<16>(xfb, [&](int e) -> float & { return bv[e / 4][e % 4]; });
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u)
@@ -1800,6 +1821,9 @@ extern "C" int ts_hip_gemm_colsum_xf(int trans_a, size_t M, size_t N, size_t K, 
                                      float *workspace, size_t workspace_floats, void *stream) {
     OperandXf fa, fb;
     if (!xf_from(xa, fa) || !xf_from(xb, fb)) return TS_HIP_EINVAL;
+    if (!fa.n && !fb.n)  // no transform: the plain call
+        return ts_hip_gemm_colsum(trans_a, M, N, K, A, lda, B, ldb, C, ldc, colsum, workspace, workspace_floats,
+                                  stream);
     if (!colsum || M == 0) return TS_HIP_EINVAL;  // the column sums alone take no transform
     if (N == 0) return TS_HIP_OK;
     return gemm_plain(trans_a, 0, M, N, K, A, lda, B, ldb, C, ldc, nullptr, nullptr, 0, colsum, workspace,
