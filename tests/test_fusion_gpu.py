@@ -319,3 +319,40 @@ def test_bias_gradient_without_a_weight_product_runs_on_its_own(fusion):
         vals[on] = b.grad_by_value().data()
         T.clear_gradients()
     assert_bits_equal(vals[True], vals[False], "bias grad")
+
+
+@pytest.mark.parametrize("readme", [True, False])
+def test_gradient_chains_are_applied_in_the_products(fusion, readme):
+    """With fusion on, an output gradient that is a chain of elementwise ops
+    over one buffer -- relu's backward of the seed in the README step
+    (README.md:71-79), the MSE's gradient 2 * d * (1/n) of config 4 -- is
+    applied by the products that read it, as an operand transform of that
+    buffer (ts_hip_gemm_*_xf): the backward launches no elementwise pass, the
+    same products, and every gradient has the bits of the op-by-op run."""
+    T = fusion
+    widths, batch = ([784, 128], 32) if readme else ([784, 1024, 10], 1024)
+    grads, counts = {}, {}
+    for on in (True, False):
+        T.set_fusion(on)
+        ps, x, t = _mlp(T, widths, batch, 13)
+        h = x
+        n = len(ps) // 2
+        for i in range(n):
+            h = h.matmul(ps[2 * i]).add_tensor(ps[2 * i + 1])
+            if readme or i < n - 1:
+                h = h.relu()
+        loss = h.sum() if readme else h.sub_tensor(t).pow_scalar(2.0).mean()
+        loss.value()
+        T.synchronize()
+        T.Profile.reset()
+        T.Profile.enable(True)
+        loss.backward()
+        T.synchronize()
+        T.Profile.enable(False)
+        counts[on] = (T.Profile.read(T.Profile.GEMM)["launches"], T.Profile.read(T.Profile.ELEMENTWISE)["launches"])
+        grads[on] = [p.grad_by_value().data() for p in ps]
+        T.clear_gradients()
+    for i, (a, b) in enumerate(zip(grads[True], grads[False])):
+        assert_bits_equal(a, b, f"grad {i}")
+    assert counts[True][1] == 0, counts
+    assert counts[True][0] == (1 if readme else 3), counts   # dW (+db) per layer, and dX2 in config 4

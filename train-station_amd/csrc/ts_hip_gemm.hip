@@ -996,10 +996,6 @@ __global__ __launch_bounds__(256) void gemm_short_k(GemmArgs g) {
         af[s] = in ? a : 0.0f;
         bf[s] = in ? b : 0.0f;
     }
-    if constexpr (XF) {
-        xf_array(xf_load(g.xa), af);
-        xf_array(xf_load(g.xb), bf);
-    }
     float mk[16], bj = 0.0f;
     if (EPI != kEpiNone) {
         if (g.bias) bj = g.bias[jb];  // uniform
@@ -1010,6 +1006,10 @@ __global__ __launch_bounds__(256) void gemm_short_k(GemmArgs g) {
                 mk[r] = g.mask[(size_t)i * g.ldc + jb];
             }
         }
+    }
+    if constexpr (XF) {  // after the mask loads are issued: transforming waits for the operands
+        xf_array(xf_load(g.xa), af);
+        xf_array(xf_load(g.xb), bf);
     }
     floatx16 acc;
 #pragma unroll
