@@ -18,10 +18,10 @@
  * Launchers are asynchronous on `stream`.  They allocate nothing, with two
  * exceptions: ts_hip_gemm (and ts_hip_matmul, which calls it) takes a split-K
  * temporary from the stream-ordered allocator for few output tiles with a
- * long K, and ts_hip_gemm_colsum given a NULL workspace takes its workspace
- * from the same allocator.  ts_hip_gemm_fused (caller's workspace) and
- * ts_hip_gemm_noalloc (fixed device array) compute ts_hip_gemm's products
- * without allocating, and ts_hip_gemm_colsum does with a workspace.
+ * long K, and ts_hip_gemm_fused / ts_hip_gemm_colsum (and their _xf forms)
+ * given a NULL workspace take it from the same allocator.  With the caller's
+ * workspace they allocate nothing, and ts_hip_gemm_noalloc (fixed device
+ * array) computes ts_hip_gemm's products without allocating.
  * No torch or HIP types appear in these signatures.
  */
 #ifndef TS_HIP_H

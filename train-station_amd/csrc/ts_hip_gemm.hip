@@ -33,6 +33,12 @@
 // tiles, ordered in groups of 8 tile-rows so neighbouring tiles share A rows
 // and B columns in that L2.
 //
+// Operand transforms (ts_hip_gemm_*_xf): the register-staged tiles, the
+// narrow and one-k-tile kernels and the column strips can apply a short
+// elementwise chain to an operand as they load it (in registers, before the
+// LDS store or the MFMA), in instantiations of their own (XF), so a deferred
+// gradient such as relu's backward of a constant is never stored.
+//
 // Large aligned problems (both operands 16-byte aligned, leading dimensions
 // % 4 == 0, enough 256x256 tiles to fill the chip) take gemm_f32_lds_dma
 // instead: operand tiles go from global memory straight into LDS with
