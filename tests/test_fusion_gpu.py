@@ -356,3 +356,40 @@ def test_gradient_chains_are_applied_in_the_products(fusion, readme):
         assert_bits_equal(a, b, f"grad {i}")
     assert counts[True][1] == 0, counts
     assert counts[True][0] == (1 if readme else 3), counts   # dW (+db) per layer, and dX2 in config 4
+
+
+@pytest.mark.parametrize("op", ["mul", "div"])
+@pytest.mark.parametrize("loss", ["sum", "mean"])
+def test_product_gradient_times_a_constant_buffer(fusion, op, loss):
+    """y = (x . W) op B with B a buffer that needs no gradient: W's gradient
+    reads go * B (or go / B) with go the seed's constant, a chain over B that
+    the dW product applies to B as it loads it when the division is not
+    checked for zeros (mul; a checked division runs its pass); the gradients
+    have the bits of the op-by-op run either way."""
+    T = fusion
+    rng = np.random.default_rng(17)
+    M, K, N = 96, 784, 128
+    xv = rng.standard_normal((M, K)).astype(np.float32)
+    wv = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
+    bv = rng.uniform(0.5, 2.0, (M, N)).astype(np.float32)
+    grads, ew = {}, {}
+    for on in (True, False):
+        T.set_fusion(on)
+        x = T.Tensor.from_slice(xv, [M, K])
+        w = T.Tensor.from_slice(wv, [K, N]).with_requires_grad()
+        b = T.Tensor.from_slice(bv, [M, N])
+        y = getattr(x.matmul(w), f"{op}_tensor")(b)
+        lv = getattr(y, loss)()
+        lv.value()
+        T.synchronize()
+        T.Profile.reset()
+        T.Profile.enable(True)
+        lv.backward()
+        T.synchronize()
+        T.Profile.enable(False)
+        ew[on] = T.Profile.read(T.Profile.ELEMENTWISE)["launches"]
+        grads[on] = w.grad_by_value().data()
+        T.clear_gradients()
+    assert_bits_equal(grads[True], grads[False], f"{op} {loss} dW")
+    if op == "mul":
+        assert ew[True] == 0, ew
