@@ -262,9 +262,15 @@ def run_bandwidth(TS, cfg: str, steps: int, warmup: int, cpu: bool) -> dict:
         data = "synthetic (numpy default_rng(0))"
     else:
         n = ADAM_P
-        log(f"config c3: Adam on {n} parameters; generating on the device")
-        p = TS.Tensor.randn([n], seed=1).with_requires_grad()
-        g = TS.Tensor.randn([n], seed=2).mul_scalar(0.1)
+        log(f"config c3: Adam on {n} parameters; p ~N(0,1), g ~N(0,1e-2) (sigma 0.1) from numpy, uploaded")
+        rng = np.random.default_rng(0)
+        pv = rng.standard_normal(n, dtype=np.float32)
+        p = TS.Tensor.from_slice(pv, [n]).with_requires_grad()
+        del pv
+        gv = rng.standard_normal(n, dtype=np.float32)
+        gv *= np.float32(0.1)
+        g = TS.Tensor.from_slice(gv, [n])
+        del gv
         p.set_grad(g)
         opt = TS.Adam.with_learning_rate(1e-3)
         opt.add_parameter(p)
@@ -276,7 +282,7 @@ def run_bandwidth(TS, cfg: str, steps: int, warmup: int, cpu: bool) -> dict:
         classes = ("adam",)
         workload = ("BASELINE config 3: Adam::step alone on 2^28 fp32 params, grads ~N(0, 1e-2) set once, "
                     "m=v=0 initially, lr=1e-3, betas (0.9, 0.999), eps 1e-8")
-        data = "synthetic (device XorShiftRng randn: p seed 1, g = 0.1 * randn seed 2)"
+        data = "synthetic (numpy default_rng(0): p ~N(0,1), g = 0.1 * N(0,1), float32)"
 
     for i in range(warmup):
         step()

@@ -84,6 +84,24 @@ ts_tensor *ts_tensor_softmax(const ts_tensor *a, size_t dim);
 ts_tensor *ts_tensor_sum_dims(const ts_tensor *a, const size_t *dims, size_t ndims, int keepdim);
 ts_tensor *ts_tensor_mean_dims(const ts_tensor *a, const size_t *dims, size_t ndims, int keepdim);
 
+/* transpose(dim0, dim1) / t() (transform/transpose.rs:156-208, :283-291): a
+ * transposed view, recorded (Transpose GradFn, grad_fn/mod.rs:243-249, :575)
+ * whenever the input requires grad.  The view's values are copied only when
+ * something reads them; a 2-D view given to matmul is read by the product
+ * with its transpose flag instead (forward and backward), never copied.
+ * contiguous() (transform/contiguous.rs:123-157): a view's copy, anything
+ * else's clone (Contiguous GradFn: identity).  is_contiguous(): 0 for a
+ * transposed view of a contiguous tensor.  Panics as the reference: "dim0 2
+ * out of bounds for tensor with rank 2", "Matrix transpose requires at least
+ * 2 dimensions, got 1". */
+ts_tensor *ts_tensor_transpose(const ts_tensor *a, size_t dim0, size_t dim1);
+ts_tensor *ts_tensor_t(const ts_tensor *a);
+ts_tensor *ts_tensor_contiguous(const ts_tensor *a);
+int ts_tensor_is_contiguous(const ts_tensor *a);
+/* Tensor::fill (init/basic.rs:304-326): every element set to value, in place
+ * (through a view not yet copied, into its source, which it shares) */
+int ts_tensor_fill(ts_tensor *t, float value);
+
 /* Tensor::backward(Option<Tensor>) (utils.rs:634-636); grad_output may be NULL */
 int ts_tensor_backward(ts_tensor *t, const ts_tensor *grad_output);
 /* Tensor::grad (utils.rs:491-506): the gradient stored on the tensor itself

@@ -212,6 +212,12 @@ int ts_hip_softmax(const float *x, float *y, size_t outer, size_t reduce, size_t
 int ts_hip_broadcast_copy(const float *src, const size_t *src_dims, size_t src_rank, float *out,
                           const size_t *out_dims, size_t out_rank, float scale, int use_scale,
                           void *stream);
+/* transform/transpose.rs:156-208 and contiguous.rs:123-157 (the reference's
+ * strided view, materialised): out = src (dims, rank) with axes d0 and d1
+ * swapped, both row-major; d0 == d1 copies.  A matrix operand of a product
+ * is never transposed this way: the GEMM entries read it transposed. */
+int ts_hip_transpose(const float *src, const size_t *dims, size_t rank, size_t d0, size_t d1, float *out,
+                     void *stream);
 /* Sum of x (dims, rank) over the axes whose bit is set in reduce_mask, into
  * out laid out with those axes of size 1 (keepdim); f64 accumulation in a
  * fixed order, rounded once, then times scale (fp32) when use_scale. */
@@ -274,7 +280,9 @@ int ts_hip_softmax_backward(const float *y, const float *go, float *gi, size_t o
  * A constant input is the value ts_hip_fill would write into a buffer read in
  * its place.  With sum_out != NULL, register reduce_reg is also added up into
  * sum_out[0] (divided by (float)n when mean) with the bits ts_hip_sum /
- * ts_hip_mean give over those values; the workspace is
+ * ts_hip_mean give over a 16-byte-aligned buffer holding those values (the
+ * pass groups by four whatever its outputs' alignment; ts_hip_sum over an
+ * unaligned buffer adds element by element); the workspace is
  * ts_hip_map_workspace_floats(n) floats, 8-byte aligned. */
 #define TS_HIP_MAP_MAX_INPUTS 5
 #define TS_HIP_MAP_MAX_OPS 11

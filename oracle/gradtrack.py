@@ -251,6 +251,41 @@ class OTensor:
                                                 dims=tuple(sorted(set(dims))), keepdim=keepdim))
         return out
 
+    def transpose(self, dim0: int, dim1: int):
+        """transform/transpose.rs:156-208: axes dim0 and dim1 swapped (the
+        reference's strided view, here a copy: the values are the same); the
+        same axis twice is a clone that tracks no gradient (:171-173); records
+        whenever the input requires grad."""
+        rank = self.data.ndim
+        if dim0 >= rank:
+            raise ValueError(f"dim0 {dim0} out of bounds for tensor with rank {rank}")
+        if dim1 >= rank:
+            raise ValueError(f"dim1 {dim1} out of bounds for tensor with rank {rank}")
+        if dim0 == dim1:
+            return OTensor(self.data.copy())
+        out = OTensor(np.ascontiguousarray(np.swapaxes(self.data, dim0, dim1)))
+        if self.requires_grad:
+            self._record(out, [self.id], GradFn("transpose", shapes=(self.shape,), dims=(dim0, dim1)))
+        return out
+
+    def t(self):
+        """transpose.rs:283-291: the last two axes."""
+        if self.data.ndim < 2:
+            raise ValueError(f"Matrix transpose requires at least 2 dimensions, got {self.data.ndim}")
+        return self.transpose(self.data.ndim - 2, self.data.ndim - 1)
+
+    def contiguous(self):
+        """transform/contiguous.rs:123-157: a copy; records (identity
+        gradient) whenever the input requires grad."""
+        out = OTensor(self.data.copy())
+        if self.requires_grad:
+            self._record(out, [self.id], GradFn("contiguous", shapes=(self.shape,)))
+        return out
+
+    def fill(self, value: float) -> None:
+        """init/basic.rs:304-326: every element set to value, in place."""
+        self.data[...] = np.float32(value)
+
     def backward(self, grad_output: Optional[np.ndarray] = None) -> None:
         backward(self, grad_output)
 
@@ -348,6 +383,10 @@ def _apply(fn: GradFn, go: np.ndarray) -> list[Optional[np.ndarray]]:
         if fn.shapes is None:
             return [ga, gb]
         return [_reduce_to(ga, fn.shapes[0]), _reduce_to(gb, fn.shapes[1])]
+    if k == "transpose":                             # grad_fn/transforms/transpose.rs
+        return [np.ascontiguousarray(np.swapaxes(go, fn.dims[0], fn.dims[1]))]
+    if k == "contiguous":                            # grad_fn/mod.rs:534-537: identity
+        return [go]
     if k in ("add_scalar", "sub_scalar"):
         return [go]
     if k == "mul_scalar":

@@ -120,16 +120,21 @@ def test_adam_libtorch_cases_on_device(TS, G, case):
 # the ReLU backward then routes an O(1) gradient differently.  The MLP tests
 # therefore (1) assert that device and oracle masks differ only where
 # |z| <= 1e-5 * max|z| and (2) hand the device's masks to the oracle's ReLU
-# backward, so every remaining difference is arithmetic.
+# backward, so every remaining difference is arithmetic.  The device's mask
+# is read from its ReLU output (relu(z) > 0 exactly where z > 0), which the
+# step stores anyway for the backward; the pre-activation itself is never
+# read, so the device runs the step as the bench does, with bias and ReLU in
+# the product's store.
 
 def _relu_both(z, zo, stats):
-    zg = z.data()
-    mism = (zg > 0) != (zo.data > 0)
+    h = z.relu()
+    hg = h.data()
+    mism = (hg > 0) != (zo.data > 0)
     if mism.any():
         scale = float(np.max(np.abs(zo.data)))
         assert np.all(np.abs(zo.data[mism]) <= 1e-5 * scale), "mask differs away from zero"
         stats["flips"] = stats.get("flips", 0) + int(mism.sum())
-    return z.relu(), zo.relu(mask_source=zg)
+    return h, zo.relu(mask_source=hg)
 
 
 def _mlp_both(xd, td, pd, xo, to, po, stats, readme=False):
@@ -143,11 +148,32 @@ def _mlp_both(xd, td, pd, xo, to, po, stats, readme=False):
         else:
             h, ho = z, zo
     if readme:
-        return h.sum(), ho.sum()
-    return h.sub_tensor(td).pow_scalar(2.0).mean(), ho.sub_tensor(to).pow_scalar(2.0).mean()
+        return h.sum(), ho.sum(), float(np.sum(ho.data, dtype=np.float64))
+    sq = ho.sub_tensor(to).pow_scalar(2.0)
+    # the loss's exact value: the oracle's per-element terms summed in f64
+    # (the reference's sequential fp32 sum drifts at these sizes)
+    return (h.sub_tensor(td).pow_scalar(2.0).mean(), sq.mean(),
+            float(np.sum(sq.data, dtype=np.float64)) / sq.size())
 
 
 EPS32 = 2.0 ** -23
+EXCLUDED_MAX_ABS = 1e-4
+
+
+def _assert_elementwise(got, want, what, rel=1e-4):
+    """Per-element bar with an RMS floor: |got - want| <= rel * max(|want|,
+    rms(want)) for every element.  A matmul-derived value that is the small
+    result of a long cancelling sum carries rounding of the size of the
+    tensor's typical entries, not of its own size; the floor states that."""
+    g = np.asarray(got, np.float64).reshape(-1)
+    w = np.asarray(want, np.float64).reshape(-1)
+    assert g.shape == w.shape, (what, g.shape, w.shape)
+    tol = rel * np.maximum(np.abs(w), np.sqrt(np.mean(w * w)))
+    d = np.abs(g - w)
+    bad = np.flatnonzero(~(d <= tol))
+    assert bad.size == 0, (f"{what}: {bad.size} of {g.size} elements over the bar; first at {bad[0]}: "
+                           f"got {g[bad[0]]!r} want {w[bad[0]]!r} tol {tol[bad[0]]!r}")
+    return float(np.max(d / tol)) if g.size else 0.0
 
 
 def _train_both(TS, G, ws, x, t, steps, readme=False, lr=1e-3, max_excluded=0.01):
@@ -191,13 +217,12 @@ def _train_both(TS, G, ws, x, t, steps, readme=False, lr=1e-3, max_excluded=0.01
     try:
         for step in range(steps):
             bound.clear()
-            loss, lo = _mlp_both(xd, td, pd, xo, to, po, stats, readme)
+            loss, lo, exact = _mlp_both(xd, td, pd, xo, to, po, stats, readme)
             loss.backward()
             lo.backward()
             if step == 0:
-                for d, o in zip(pd, po):
-                    assert max_rel(d.grad_by_value().data(), o.grad_by_value()) <= 1e-4
-            exact = lo.value()
+                for k, (d, o) in enumerate(zip(pd, po)):
+                    _assert_elementwise(d.grad_by_value().data(), o.grad_by_value(), f"step-0 gradient {k}")
             assert abs(loss.value() - exact) <= 1e-4 * abs(exact), (step, loss.value(), exact)
             for k, o in enumerate(po):
                 g = o.grad_by_value().reshape(-1).astype(np.float64)
@@ -229,7 +254,10 @@ def _train_both(TS, G, ws, x, t, steps, readme=False, lr=1e-3, max_excluded=0.01
         print(f"[train {steps} steps] param {k} {entry}", flush=True)
         assert not fail.any(), (k, int(fail.sum()), np.flatnonzero(fail)[:5], diff[fail][:5], tol[fail][:5])
         assert ex.mean() <= max_excluded, (k, float(ex.mean()))
-        assert entry["excluded_max_abs"] <= steps * lr, (k, entry["excluded_max_abs"])
+        # an excluded element could move up to ~2 lr per step the wrong way;
+        # the worst-case rounding bound that selects them is far above the
+        # rounding actually seen, so in practice they stay within this
+        assert entry["excluded_max_abs"] <= EXCLUDED_MAX_ABS, (k, entry["excluded_max_abs"])
     print(f"[train] mask flips conditioned on: {report['mask_flips_conditioned_on']}", flush=True)
     return report
 
@@ -279,6 +307,42 @@ def test_division_by_zero_is_reported(TS):
     assert np.isinf(q.data()[3])
     with pytest.raises(TS.TsError, match="zero scalar"):
         a.div_scalar(0.0)
+
+
+@pytest.mark.parametrize("keep", [True, False])
+def test_division_by_zero_is_reported_when_the_quotient_is_never_read(TS, keep):
+    # ops/div.rs:383-416 panics inside div_tensor; a deferred quotient that is
+    # never read (held, or dropped at once) still reports the zero divisor at
+    # the next synchronisation, once
+    n = 40
+    a = TS.Tensor.from_slice(np.ones(n, np.float32), [n])
+    z = np.ones(n, np.float32)
+    z[35] = 0.0
+    q = a.div_tensor(TS.Tensor.from_slice(z, [n]))
+    if not keep:
+        del q
+    with pytest.raises(TS.TsError, match="Division by zero detected at index 35"):
+        TS.synchronize()
+    TS.synchronize()
+    # inside a longer recorded chain whose value is dropped
+    x = TS.Tensor.from_slice(np.full(n, 2.0, np.float32), [n]).with_requires_grad()
+    d = TS.Tensor.from_slice(z, [n]).with_requires_grad()
+    y = x.div_tensor(d).add_scalar(1.0)
+    del y
+    with pytest.raises(TS.TsError, match="Division by zero detected at index 35"):
+        TS.synchronize()
+    # no zero in the tail: nothing is reported, and a dropped quotient costs
+    # no pass of its own once a pass that read it has run
+    z[35] = 1.0
+    q = a.div_tensor(TS.Tensor.from_slice(z, [n]))
+    s = q.add_scalar(1.0).sum().value()
+    assert s == 2.0 * n
+    del q
+    TS.Profile.reset()
+    TS.Profile.enable(True)
+    TS.synchronize()
+    TS.Profile.enable(False)
+    assert TS.Profile.read(TS.Profile.ELEMENTWISE)["launches"] == 0
 
 
 # ---- config 3: Adam alone -----------------------------------------------------------------------
@@ -353,6 +417,19 @@ def test_config5_scaled_mlp_100_steps(TS, G):
     _train_both(TS, G, ws, x, t, 100, max_excluded=0.02)
 
 
+@pytest.mark.timeout(900)
+def test_wide_mlp_10_steps_on_the_lds_dma_kernel(TS, G):
+    # 2 x Linear(4096, 4096) at batch 4096, ReLU after the first, MSE: every
+    # product (forward, dX, dW) has 256 output tiles of 256 x 256, one per CU,
+    # so each takes the LDS-DMA kernel that carries config 5 (with its fused
+    # bias + ReLU store, the ReLU-backward mask in the dX store and the bias
+    # gradient in the dW product); 10 steps, per-element parameter bar
+    ws, rng = _mlp_weights([4096] * 3, 3, "normal")
+    x = rng.standard_normal((4096, 4096)).astype(np.float32)
+    t = rng.standard_normal((4096, 4096)).astype(np.float32)
+    _train_both(TS, G, ws, x, t, 10, max_excluded=0.02)
+
+
 def _mlp(lib_tensor, x, t, params, relu_last=False):
     h = x
     n = len(params) // 2
@@ -363,52 +440,71 @@ def _mlp(lib_tensor, x, t, params, relu_last=False):
     return h.sub_tensor(t).pow_scalar(2.0).mean()
 
 
+@pytest.mark.timeout(900)
 def test_config5_full_size_step(TS, oracle):
     # The bench workload at its real size (B = 8192, 6 x 4096^2, ReLU on 1-5,
-    # MSE), checked through size-independent properties: sampled output rows
-    # against an f64 forward pass, the loss against f64 over the downloaded
-    # output, the last bias gradient against 2/n * colsum(y - t) in f64, and
-    # Adam's first step, which moves every weight by lr * |g| / (|g| + eps).
+    # MSE; small nonzero biases so the fused bias store is exercised), one
+    # step, every element of every product checked:
+    # * forward: each layer's stored output against relu(h_in . W + b) in f64
+    #   from the device's own input to that layer (all 6 products, every tile);
+    # * backward: the f64 backward from the device's output, through the
+    #   device's ReLU masks (read from the stored outputs, exactly the masks
+    #   the device applies), against every element of all 6 dW and db
+    #   (the dX products enter every dW below the last layer);
+    # * Adam: the first step on all 12 tensors bit-exact against the oracle's
+    #   Adam applied to the device's gradients.
     rng = np.random.default_rng(2)
     D, B, L = 4096, 8192, 6
     ws = [rng.standard_normal((D, D), dtype=np.float32) * np.float32(1 / 64) for _ in range(L)]
+    bs = [rng.standard_normal(D, dtype=np.float32) * np.float32(0.01) for _ in range(L)]
     x = rng.standard_normal((B, D), dtype=np.float32)
     t = rng.standard_normal((B, D), dtype=np.float32)
     ps = []
-    for w in ws:
-        ps += [TS.Tensor.from_slice(w, w.shape).with_requires_grad(), TS.Tensor.zeros([D]).with_requires_grad()]
+    for w, b in zip(ws, bs):
+        ps += [TS.Tensor.from_slice(w, w.shape).with_requires_grad(),
+               TS.Tensor.from_slice(b, b.shape).with_requires_grad()]
     xd, td = TS.Tensor.from_slice(x, [B, D]), TS.Tensor.from_slice(t, [B, D])
     opt = TS.Adam.new()
     opt.add_parameters(ps)
-    h = xd
+    h, hs = xd, []
     for i in range(L):
         h = h.matmul(ps[2 * i]).add_tensor(ps[2 * i + 1])
         if i < L - 1:
             h = h.relu()
-    y = h
-    loss = y.sub_tensor(td).pow_scalar(2.0).mean()
+        hs.append(h)
+    loss = hs[-1].sub_tensor(td).pow_scalar(2.0).mean()
     loss.backward()
-    yg = y.data()
-    rows = np.array([0, 1, 4095, 8191])
-    hr = x[rows]
-    for i, w in enumerate(ws):
-        hr = oracle.gemm_f64(hr, w).astype(np.float32)
-        if i < L - 1:
-            hr = oracle.relu(hr)
-    assert max_rel(yg[rows], hr) <= 1e-4
-    d = yg.astype(np.float64) - t.astype(np.float64)
+    print("[c5 full] step ran; downloading activations and gradients", flush=True)
+    hd = [x] + [v.data() for v in hs]
+    grads = [p.grad_by_value().data() for p in ps]
+
+    for i in range(L):
+        z = oracle.gemm_f64(hd[i], ws[i]) + bs[i].astype(np.float64)
+        want = np.maximum(z, 0.0) if i < L - 1 else z
+        r = _assert_elementwise(hd[i + 1], want, f"forward layer {i + 1}")
+        print(f"[c5 full] forward layer {i + 1}: max err / tol {r:.3f}", flush=True)
+    del z, want
+
+    d = hd[L].astype(np.float64) - t.astype(np.float64)
     want_loss = float(np.mean(d * d))
     assert abs(loss.value() - want_loss) <= 1e-5 * want_loss
-    want_db = 2.0 / (B * D) * d.sum(axis=0)
-    assert max_rel(ps[-1].grad_by_value().data(), want_db) <= 1e-4
-    g1 = ps[0].grad_by_value().data().astype(np.float64)
+    g = (2.0 / (B * D)) * d
+    del d
+    for i in reversed(range(L)):
+        r = _assert_elementwise(grads[2 * i], oracle.gemm_f64(hd[i], g, ta=True), f"dW layer {i + 1}")
+        rb = _assert_elementwise(grads[2 * i + 1], g.sum(axis=0), f"db layer {i + 1}")
+        print(f"[c5 full] layer {i + 1}: dW max err / tol {r:.3f}, db {rb:.3f}", flush=True)
+        if i > 0:
+            g = (g @ ws[i].astype(np.float64).T) * (hd[i] > 0)
+    del g
+
     opt.step(ps)
-    # first step: m_hat = g and v_hat = g^2 (to a few ulp), so each weight
-    # moves by lr * |g| / (|g| + eps); the remaining error is the f32 rounding
-    # of the updated weight (|w| < 0.1, ulp <= 7.5e-9)
-    moved = np.abs(ps[0].data().astype(np.float64) - ws[0].astype(np.float64))
-    expected = 1e-3 * np.abs(g1) / (np.abs(g1) + 1e-8)
-    assert float(np.max(np.abs(moved - expected))) <= 2e-8
+    for k, (v0, gk) in enumerate(zip([a for wb in zip(ws, bs) for a in wb], grads)):
+        p = v0.reshape(-1).copy()
+        m = np.zeros_like(p)
+        vv = np.zeros_like(p)
+        oracle.adam_step(p, np.ascontiguousarray(gk.reshape(-1)), m, vv, 1)
+        assert_bits_equal(ps[k].data().reshape(-1), p, f"parameter {k} after the first Adam step")
     opt.zero_grad(ps)
 
 

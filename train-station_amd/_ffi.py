@@ -128,6 +128,7 @@ HIP_SIGNATURES = {
     "ts_hip_broadcast_copy": (_c.c_int, [VP, _c.POINTER(SZ), SZ, VP, _c.POINTER(SZ), SZ, _c.c_float,
                                          _c.c_int, VP]),
     "ts_hip_reduce_sum": (_c.c_int, [VP, _c.POINTER(SZ), SZ, _c.c_uint, VP, _c.c_float, _c.c_int, VP]),
+    "ts_hip_transpose": (_c.c_int, [VP, _c.POINTER(SZ), SZ, SZ, SZ, VP, VP]),
     "ts_hip_log_backward": (_c.c_int, [VP, VP, VP, SZ, VP]),
     "ts_hip_sqrt_backward": (_c.c_int, [VP, VP, VP, SZ, VP]),
     "ts_hip_tanh_backward": (_c.c_int, [VP, VP, VP, SZ, VP]),
@@ -226,6 +227,11 @@ GRADTRACK_SIGNATURES = {
     "ts_tensor_softmax": (TP, [TP, SZ]),
     "ts_tensor_sum_dims": (TP, [TP, _c.POINTER(SZ), SZ, _c.c_int]),
     "ts_tensor_mean_dims": (TP, [TP, _c.POINTER(SZ), SZ, _c.c_int]),
+    "ts_tensor_transpose": (TP, [TP, SZ, SZ]),
+    "ts_tensor_t": (TP, [TP]),
+    "ts_tensor_contiguous": (TP, [TP]),
+    "ts_tensor_is_contiguous": (_c.c_int, [TP]),
+    "ts_tensor_fill": (_c.c_int, [TP, _c.c_float]),
     "ts_tensor_sum": (TP, [TP]),
     "ts_tensor_mean": (TP, [TP]),
     "ts_tensor_backward": (_c.c_int, [TP, TP]),

@@ -177,6 +177,20 @@ ts_tensor *ts_tensor_sum_dims(const ts_tensor *a, const size_t *dims, size_t ndi
 ts_tensor *ts_tensor_mean_dims(const ts_tensor *a, const size_t *dims, size_t ndims, int keepdim) {
     return guard_ptr([&] { return wrap(T(a).mean_dims(dims_of(dims, ndims), keepdim != 0)); });
 }
+ts_tensor *ts_tensor_transpose(const ts_tensor *a, size_t dim0, size_t dim1) {
+    return guard_ptr([&] { return wrap(T(a).transpose(dim0, dim1)); });
+}
+ts_tensor *ts_tensor_t(const ts_tensor *a) { return guard_ptr([&] { return wrap(T(a).t()); }); }
+ts_tensor *ts_tensor_contiguous(const ts_tensor *a) {
+    return guard_ptr([&] { return wrap(T(a).contiguous()); });
+}
+int ts_tensor_is_contiguous(const ts_tensor *a) { return a && a->t.is_contiguous() ? 1 : 0; }
+int ts_tensor_fill(ts_tensor *t, float value) {
+    return guard_int([&] {
+        if (!t) throw ts::Error("tensor handle is NULL");
+        t->t.fill(value);
+    });
+}
 ts_tensor *ts_tensor_sum(const ts_tensor *a) {
     return guard_ptr([&] { return wrap(T(a).sum()); });
 }

@@ -35,6 +35,7 @@ Runtime &Runtime::get() {
 void Runtime::sync() {
     if (StepRecorder::get().open())
         throw Error("a step being recorded cannot wait for or read device results: end the recording first");
+    run_division_checks();  // quotients never read still check their divisors
     check(ts_hip_stream_synchronize(stream_), "ts_hip_stream_synchronize");
     unsigned long long idx = kNoZero;
     check(ts_hip_memcpy(reinterpret_cast<float *>(&idx),
@@ -169,6 +170,7 @@ float *Allocation::get() {
     if (pending) materialize(*this);
     else if (map) materialize_map(*this);
     else if (colsum) materialize_colsum(*this);
+    else if (transpose) materialize_transpose(*this);
     DevicePool::get().note_use(ptr_);
     return ptr_;
 }
@@ -181,6 +183,7 @@ void Allocation::before_write() {
             if (r->pending) materialize(*r);
             else if (r->map) materialize_map(*r);
             else if (r->colsum) materialize_colsum(*r);
+            else if (r->transpose) materialize_transpose(*r);
         }
 }
 

@@ -529,7 +529,10 @@ struct MapBuilder {
         const MapNode &nd = p.nodes[j];
         return nd.code == MapNode::kLeaf && ((p.consts >> nd.a) & 1u) && p.values[nd.a] == v;
     }
-    int op(uint8_t code, int a, int b, float imm = 0.0f, uint8_t flags = 0) {
+    // `inherit`: the checks of a checked division copied from another
+    // program (none: a new division, which gets a check of its own)
+    int op(uint8_t code, int a, int b, float imm = 0.0f, uint8_t flags = 0,
+           const std::vector<std::shared_ptr<DivCheck>> *inherit = nullptr) {
         if (b < 0) b = a;
         // the constant one scaled by imm is imm exactly (the mean's gradient
         // of the seed)
@@ -538,14 +541,23 @@ struct MapBuilder {
         std::memcpy(&bits, &imm, 4);
         const auto key = std::make_tuple(code, flags, a, b, bits);
         auto it = cse.find(key);
-        if (it != cse.end()) return it->second;
+        if (it != cse.end()) {
+            if (inherit) {
+                auto &mine = p.nodes[it->second].checks;
+                for (const auto &c : *inherit)
+                    if (std::find(mine.begin(), mine.end(), c) == mine.end()) mine.push_back(c);
+            }
+            return it->second;
+        }
         MapNode nd;
         nd.code = code;
         nd.flags = flags;
         nd.a = static_cast<int16_t>(a);
         nd.b = static_cast<int16_t>(b);
         nd.imm = imm;
-        p.nodes.push_back(nd);
+        if (inherit) nd.checks = *inherit;
+        else if (flags & TS_HIP_MAP_CHECKED) nd.checks.push_back(std::make_shared<DivCheck>());
+        p.nodes.push_back(std::move(nd));
         ++ops;
         const int id = static_cast<int>(p.nodes.size()) - 1;
         cse.emplace(key, id);
@@ -561,7 +573,7 @@ struct MapBuilder {
                 remap[j] = ((m.consts >> nd.a) & 1u) ? constant(m.values[nd.a])
                                                      : leaf(m.leaves[nd.a], ((m.scalar >> nd.a) & 1u) != 0);
             } else {
-                remap[j] = op(nd.code, remap[nd.a], remap[nd.b], nd.imm, nd.flags);
+                remap[j] = op(nd.code, remap[nd.a], remap[nd.b], nd.imm, nd.flags, &nd.checks);
                 if (p.nodes[remap[j]].origin.expired() && !nd.origin.expired()) p.nodes[remap[j]].origin = nd.origin;
             }
         }
@@ -579,6 +591,49 @@ struct MapBuilder {
     }
 };
 
+// true when something besides `own` local references (and the division-check
+// list) holds the allocation
+bool held_elsewhere(const std::shared_ptr<Allocation> &a, long own) {
+    return a.use_count() > own + (a->check_hold ? 1 : 0);
+}
+
+bool open_checks(const PendingMap &m) {
+    for (const MapNode &nd : m.nodes)
+        for (const auto &c : nd.checks)
+            if (!c->done) return true;
+    return false;
+}
+
+// This thread's deferred values whose programs hold a checked division that
+// no pass has computed yet (only sizes with a tail: the check is on the
+// elements past 32 * floor(n / 32)).  Held here so they run, before the next
+// synchronisation reads the zero-divisor word, even when nothing else reads
+// them; being registered readers of their inputs, they also run before an
+// input is overwritten in place.
+std::vector<std::shared_ptr<Allocation>> &check_holds() {
+    static thread_local std::vector<std::shared_ptr<Allocation>> v;
+    return v;
+}
+
+void prune_check_holds() {
+    auto &v = check_holds();
+    size_t k = 0;
+    for (size_t i = 0; i < v.size(); ++i) {
+        if (v[i]->map && open_checks(*v[i]->map)) v[k++] = std::move(v[i]);
+        else v[i]->check_hold = false;
+    }
+    v.resize(k);
+}
+
+constexpr size_t kMaxCheckHolds = 256;  // past this the held programs run (bounds what they keep alive)
+
+void hold_for_check(const std::shared_ptr<Allocation> &al) {
+    if (al->check_hold) return;
+    if (check_holds().size() >= kMaxCheckHolds) run_division_checks();
+    check_holds().push_back(al);
+    al->check_hold = true;
+}
+
 struct MapOutput {
     std::shared_ptr<Allocation> alloc;
     int node;
@@ -594,7 +649,7 @@ void launch_program(MapBuilder &b, std::vector<MapOutput> outs, int reduce = -1,
         auto o = b.p.nodes[j].origin.lock();
         // still held (a saved operand, or its tensor): it may be read again,
         // and this pass computes it anyway, so it stores it
-        if (!o || !o->map || o.use_count() <= 1) continue;
+        if (!o || !o->map || !held_elsewhere(o, 1)) continue;
         bool listed = false;
         for (const MapOutput &m : outs) listed = listed || m.alloc == o;
         if (!listed) outs.push_back({o, static_cast<int>(j)});
@@ -650,6 +705,10 @@ void launch_program(MapBuilder &b, std::vector<MapOutput> outs, int reduce = -1,
                           work ? work->get() : nullptr, wsf, S());
     });
     for (const MapOutput &m : outs) m.alloc->map.reset();
+    bool checked = false;
+    for (const MapNode &nd : b.p.nodes)
+        for (const auto &c : nd.checks) c->done = checked = true;
+    if (checked) prune_check_holds();
 }
 
 // The deferred value of `dims` computed by build(builder, operand nodes) from
@@ -677,6 +736,7 @@ Tensor deferred_tensor(const std::vector<size_t> &dims, std::shared_ptr<PendingM
     const auto &al = out.allocation();
     for (const auto &l : p->leaves) add_reader(l, al);
     al->map = std::move(p);
+    if (tail32(al->map->n) < al->map->n && open_checks(*al->map)) hold_for_check(al);
     return out;
 }
 
@@ -699,6 +759,14 @@ Tensor map_unary(uint8_t code, const Tensor &x, float imm = 0.0f) {
 }  // namespace
 
 void materialize_map(Allocation &a) { materialize_maps({a.shared_from_this()}); }
+
+void run_division_checks() {
+    std::vector<std::shared_ptr<Allocation>> open;
+    for (const auto &a : check_holds())
+        if (a->map && open_checks(*a->map)) open.push_back(a);
+    if (!open.empty()) materialize_maps(open);
+    prune_check_holds();
+}
 
 Tensor add_gradients(const Tensor &existing, const Tensor &g) {
     if (defer_ok(existing.size()) && existing.size() == g.size()) return map_binary(TS_HIP_MAP_ADD, existing, g);
@@ -837,7 +905,134 @@ Tensor Tensor::view() const {
     t.size_ = size_;
     t.id_ = id_;
     t.requires_grad_ = requires_grad_;
+    t.strided_ = strided_;
     return t;
+}
+
+// ---- transpose, contiguous, fill (transform/transpose.rs, contiguous.rs,
+// init/basic.rs) ---------------------------------------------------------------------
+
+void materialize_transpose(Allocation &a) {
+    const std::shared_ptr<PendingTranspose> p = a.transpose;
+    const float *src = p->src->get();
+    float *C = a.raw();
+    DevicePool::get().note_use(C);
+    launch(KernelClass::Elementwise, 8.0 * a.n, "ts_hip_transpose", [&] {
+        return ts_hip_transpose(src, p->dims.data(), p->dims.size(), p->d0, p->d1, C, S());
+    });
+    a.transpose.reset();
+}
+
+namespace {
+// A deferred copy of src (dims) with axes d0 and d1 swapped (d0 == d1: a
+// plain copy) for `out`; a view reads src as it is when read, a copy is a
+// reader of src and so runs before src is written in place.
+void defer_transpose(const std::shared_ptr<Allocation> &out, const std::shared_ptr<Allocation> &src,
+                     const std::vector<size_t> &dims, size_t d0, size_t d1, bool view) {
+    auto t = std::make_shared<PendingTranspose>();
+    t->src = src;
+    t->dims = dims;
+    t->d0 = d0;
+    t->d1 = d1;
+    t->view = view;
+    if (!view) add_reader(src, out);
+    out->transpose = std::move(t);
+}
+
+bool same_axes(const PendingTranspose &t, size_t d0, size_t d1) {
+    return (t.d0 == d0 && t.d1 == d1) || (t.d0 == d1 && t.d1 == d0);
+}
+}  // namespace
+
+Tensor transposed_value(const Tensor &x, size_t d0, size_t d1, bool view) {
+    std::vector<size_t> od = x.dims();
+    std::swap(od[d0], od[d1]);
+    Tensor out = Tensor::new_uninit(od);
+    const auto &a = x.allocation();
+    if (!a || !out.size()) return out;
+    if (a->transpose && a->transpose->d0 != a->transpose->d1 && same_axes(*a->transpose, d0, d1) &&
+        a->transpose->dims == od) {
+        // transposed back: the source's values (a copy, as the reference's
+        // transpose of a strided view is, transpose.rs:187-190)
+        defer_transpose(out.allocation(), a->transpose->src, od, 0, 0, false);
+    } else if (od.size() == 2 && a->pending && a->pending->bare()) {
+        // C = op(A) . op(B) not yet run: C^T = op(B)^T . op(A)^T, written
+        // transposed by the product itself
+        const PendingGemm &p = *a->pending;
+        auto q = new_product(out.allocation());
+        q->ta = p.tb ? 0 : 1;
+        q->tb = p.ta ? 0 : 1;
+        q->M = p.N;
+        q->N = p.M;
+        q->K = p.K;
+        q->lda = p.ldb;
+        q->ldb = p.lda;
+        q->A = p.B;
+        q->B = p.A;
+        set_pending(out.allocation(), std::move(q));
+    } else {
+        defer_transpose(out.allocation(), a, x.dims(), d0, d1, view);
+    }
+    return out;
+}
+
+Tensor Tensor::transpose(size_t dim0, size_t dim1) const {
+    const size_t rank = dims_.size();
+    if (dim0 >= rank)  // transpose.rs:157-168
+        throw Error("dim0 " + std::to_string(dim0) + " out of bounds for tensor with rank " + std::to_string(rank));
+    if (dim1 >= rank)
+        throw Error("dim1 " + std::to_string(dim1) + " out of bounds for tensor with rank " + std::to_string(rank));
+    if (dim0 == dim1) return clone();  // :171-173: a clone, which tracks no gradient
+    // a view of a contiguous tensor, a copy of a strided one (:181-186)
+    const bool view = !strided_;
+    Tensor out = transposed_value(*this, dim0, dim1, view);
+    out.strided_ = view;
+    if (requires_grad_) {  // :189-202, whatever is_grad_enabled() says
+        GradFn fn{GradFn::Kind::Transpose};
+        fn.dim0 = dim0;
+        fn.dim1 = dim1;
+        fn.input_shape = dims_;
+        record(out, {id_}, std::move(fn));
+    }
+    return out;
+}
+
+Tensor Tensor::t() const {
+    if (dims_.size() < 2)  // transpose.rs:283-291
+        throw Error("Matrix transpose requires at least 2 dimensions, got " + std::to_string(dims_.size()));
+    return transpose(dims_.size() - 2, dims_.size() - 1);
+}
+
+bool Tensor::is_contiguous() const { return !strided_; }
+
+Tensor Tensor::contiguous() const {
+    Tensor out;
+    if (strided_ && alloc_ && alloc_->transpose && alloc_->transpose->view) {
+        // the view's values as they are now, copied when first read
+        const PendingTranspose &v = *alloc_->transpose;
+        out = new_uninit(dims_);
+        defer_transpose(out.alloc_, v.src, v.dims, v.d0, v.d1, false);
+    } else {
+        out = clone();  // contiguous.rs:124-137 (or a view already copied)
+    }
+    if (requires_grad_) {  // :125-157, whatever is_grad_enabled() says
+        GradFn fn{GradFn::Kind::Contiguous};
+        fn.input_shape = dims_;
+        record(out, {id_}, std::move(fn));
+    }
+    return out;
+}
+
+void Tensor::fill(float value) {
+    if (!size_) return;  // basic.rs:305-307
+    Allocation *target = alloc_.get();
+    // a view not yet copied writes through to its source, as the reference's
+    // strided view shares its storage (every element of the source is one of
+    // the view's)
+    while (target->transpose && target->transpose->view) target = target->transpose->src.get();
+    target->before_write();
+    float *p = target->get();
+    launch(KernelClass::Elementwise, 4.0 * size_, "ts_hip_fill", [&] { return ts_hip_fill(p, value, size_, S()); });
 }
 
 Tensor Tensor::from_saved(const SavedTensor &s) {
@@ -1041,6 +1236,16 @@ Tensor Tensor::pow_scalar(float e) const {
     return out;
 }
 
+// A matrix operand as a product reads it: a 2-D transposed view (or copy)
+// not yet written is its source read with the trans flag (transposes of the
+// last two axes, transform/transpose.rs:283-291, are folded into the
+// product's loads, never materialised); anything else as stored.
+MatOperand mat_operand(const std::shared_ptr<Allocation> &a) {
+    if (a && a->transpose && a->transpose->dims.size() == 2 && !a->pending && !a->map && !a->colsum)
+        return {a->transpose->src, a->transpose->d0 != a->transpose->d1 ? 1 : 0};
+    return {a, 0};
+}
+
 namespace {
 
 // Output batch axes of batched_matmul (matmul/mod.rs:660-690): the batch
@@ -1136,15 +1341,20 @@ Tensor Tensor::matmul(const Tensor &o) const {
         if (k != o.dims_[0])
             throw Error("Inner dimensions must match: " + std::to_string(k) + " vs " + std::to_string(o.dims_[0]));
         out = new_uninit({m, n});
+        // a transposed view is read as its source with the trans flag
+        const MatOperand va = mat_operand(alloc_), vb = mat_operand(o.alloc_);
+        const size_t lda = va.trans ? m : k, ldb = vb.trans ? k : n;
         if (fusion_enabled() && out.size_ && k) {  // deferred: a following bias add / relu joins it
             auto p = new_product(out.alloc_);
-            p->M = m; p->N = n; p->K = k; p->lda = k; p->ldb = n;
-            p->A = alloc_;
-            p->B = o.alloc_;
+            p->ta = va.trans; p->tb = vb.trans;
+            p->M = m; p->N = n; p->K = k; p->lda = lda; p->ldb = ldb;
+            p->A = va.buf;
+            p->B = vb.buf;
             set_pending(out.alloc_, std::move(p));
-        } else {
+        } else if (out.size_) {
+            const float *A = k ? va.buf->get() : nullptr, *B = k ? vb.buf->get() : nullptr;
             launch(KernelClass::Gemm, 2.0 * m * n * k, "ts_hip_gemm", [&] {
-                return gemm2d(0, 0, m, n, k, dev(), k, o.dev(), n, nullptr, false, nullptr, out.dev_mut(), n);
+                return gemm2d(va.trans, vb.trans, m, n, k, A, lda, B, ldb, nullptr, false, nullptr, out.dev_mut(), n);
             });
         }
     } else {  // batched_matmul (:634-760)
@@ -1175,7 +1385,7 @@ void fused_sum(const std::shared_ptr<Allocation> &x, float *out, bool mean) {
     b.p.n = x->map->n;
     const int r = b.import(*x->map, x);
     std::vector<MapOutput> outs;
-    if (x.use_count() > 1) outs.push_back({x, r});
+    if (held_elsewhere(x, 1)) outs.push_back({x, r});
     else b.p.nodes[r].origin.reset();  // not stored: it stays deferred
     launch_program(b, outs, r, out, mean);
 }
@@ -1542,25 +1752,45 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
                 if (req_right) gr = gemv(1, a.ptr(), a.dims[0], a.dims[1], go.dev());
             } else if (ra == 2 && rb == 2) {
                 const size_t M = a.dims[0], Kd = a.dims[1], N = b.dims[1];
+                // b (or a) a transposed view: its source, with the flag flipped
+                const MatOperand va = mat_operand(a.alloc), vb = mat_operand(b.alloc);
                 if (req_left) {  // go[M,N] . b[Kd,N]^T -> [M,Kd]
                     Tensor t = Tensor::new_uninit({M, Kd});
-                    if (fusion_enabled() && t.size() && N && go.allocation() && b.alloc) {
+                    const int tb = vb.trans ? 0 : 1;
+                    const size_t ldb = vb.trans ? Kd : N;
+                    if (fusion_enabled() && t.size() && N && go.allocation() && vb.buf) {
                         // deferred: relu's backward, usually next, joins it as a mask
                         auto p = new_product(t.allocation());
-                        p->ta = 0; p->tb = 1;
-                        p->M = M; p->N = Kd; p->K = N; p->lda = N; p->ldb = N;
+                        p->ta = 0; p->tb = tb;
+                        p->M = M; p->N = Kd; p->K = N; p->lda = N; p->ldb = ldb;
                         p->A = go.allocation();
-                        p->B = b.alloc;
+                        p->B = vb.buf;
                         set_pending(t.allocation(), std::move(p));
                     } else {
+                        const float *B = vb.buf ? vb.buf->get() : nullptr;
                         launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm(dX)", [&] {
-                            return gemm2d(0, 1, M, Kd, N, go.dev(), N, b.ptr(), N, nullptr, false, nullptr,
+                            return gemm2d(0, tb, M, Kd, N, go.dev(), N, B, ldb, nullptr, false, nullptr,
                                           t.dev_mut(), Kd);
                         });
                     }
                     gl = std::move(t);
                 }
-                if (req_right) {  // a[M,Kd]^T . go[M,N] -> [Kd,N]
+                const int ta = va.trans ? 0 : 1;
+                const size_t lda = va.trans ? M : Kd;
+                const bool b_view = b.alloc && b.alloc->transpose && b.alloc->transpose->view;
+                if (req_right && b_view && Kd && N && M && go.allocation() && va.buf) {
+                    // b is a transposed view, so this gradient goes on through
+                    // its Transpose: deferred, the product is then run with its
+                    // operands swapped and writes the source's gradient directly
+                    Tensor t = Tensor::new_uninit({Kd, N});
+                    auto p = new_product(t.allocation());
+                    p->ta = ta; p->tb = 0;
+                    p->M = Kd; p->N = N; p->K = M; p->lda = lda; p->ldb = N;
+                    p->A = va.buf;
+                    p->B = go.allocation();
+                    set_pending(t.allocation(), std::move(p));
+                    gr = std::move(t);
+                } else if (req_right) {  // a[M,Kd]^T . go[M,N] -> [Kd,N]
                     Tensor t = Tensor::new_uninit({Kd, N});
                     // A bias gradient still waiting to sum go's rows (the
                     // add before this product, grad_fn/ops/add.rs:4-28)
@@ -1580,23 +1810,24 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
                     // applies the chain as it loads it; go is never stored
                     ts_hip_operand_xf xb{};
                     std::shared_ptr<Allocation> leaf;
-                    const bool fx = ts_hip_gemm_takes_xf(1, 0, Kd, N, M, db ? 1 : 0) &&
+                    const bool fx = ts_hip_gemm_takes_xf(ta, 0, Kd, N, M, db ? 1 : 0) &&
                                     operand_xf(go.allocation(), leaf, xb);
+                    const float *A = va.buf ? va.buf->get() : nullptr;
                     if (db) {
                         db->colsum.reset();
-                        const float *A = a.ptr(), *B = fx ? leaf->get() : go.dev();
+                        const float *B = fx ? leaf->get() : go.dev();
                         float *C = t.dev_mut();
-                        const size_t ws = ts_hip_gemm_colsum_workspace_floats(1, Kd, N, M);
+                        const size_t ws = ts_hip_gemm_colsum_workspace_floats(ta, Kd, N, M);
                         std::unique_ptr<Allocation> work;  // from the pool: the launch allocates nothing
                         if (ws) work = std::make_unique<Allocation>(ws);
                         launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm_colsum(dW, db)", [&] {
-                            return ts_hip_gemm_colsum_xf(1, Kd, N, M, A, Kd, nullptr, B, N, fx ? &xb : nullptr, C, N,
+                            return ts_hip_gemm_colsum_xf(ta, Kd, N, M, A, lda, nullptr, B, N, fx ? &xb : nullptr, C, N,
                                                          db->raw(), work ? work->get() : nullptr, ws, S());
                         });
                     } else {
                         const float *B = fx ? leaf->get() : go.dev();
                         launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm(dW)", [&] {
-                            return gemm2d_xf(1, 0, Kd, N, M, a.ptr(), Kd, nullptr, B, N, fx ? &xb : nullptr, nullptr,
+                            return gemm2d_xf(ta, 0, Kd, N, M, A, lda, nullptr, B, N, fx ? &xb : nullptr, nullptr,
                                              false, nullptr, t.dev_mut(), N);
                         });
                     }
@@ -1614,6 +1845,12 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
             r.emplace_back(std::move(gr));
             break;
         }
+        case K::Transpose:  // grad_fn/transforms/transpose.rs: the same two axes swapped back
+            r.emplace_back(transposed_value(go, dim0, dim1, false));
+            break;
+        case K::Contiguous:  // grad_fn/mod.rs:534-537: the gradient passes through
+            r.emplace_back(go.alias());
+            break;
         case K::Exp: {  // grad_fn/ops/exp.rs: go * y
             Tensor g = Tensor::new_uninit(go.dims());
             launch(KernelClass::Elementwise, 12.0 * n, "exp grad",

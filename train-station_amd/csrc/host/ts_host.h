@@ -129,6 +129,15 @@ struct PendingGemm {
     bool bare() const { return !src && !bias && !mask && !relu; }
 };
 
+// One division checked for zero divisors (the reference's panic in
+// div_tensor, ops/div.rs:383-416) recorded in a deferred program: done once a
+// pass has computed the division, and so checked it.  A program that is
+// copied into a larger one shares its checks, so the check is made once,
+// by whichever pass computes the division first.
+struct DivCheck {
+    bool done = false;
+};
+
 // A deferred elementwise value: a chain of same-shape elementwise ops (and
 // their backward formulas) recorded as a small program over leaf buffers and
 // run by ts_hip_map when the value is first needed.  An op whose operands are
@@ -146,6 +155,9 @@ struct MapNode {
     // program computes it anyway and the allocation is still pending and held
     // elsewhere, the same pass stores it
     std::weak_ptr<Allocation> origin;
+    // a checked division: the checks it stands for (several when equal
+    // divisions were merged into one node)
+    std::vector<std::shared_ptr<DivCheck>> checks;
 };
 
 struct PendingMap {
@@ -174,6 +186,22 @@ struct PendingColsum {
     size_t rows = 0, cols = 0;
 };
 
+// A deferred transposed copy: the contents are src (dims) with axes d0 and d1
+// swapped, written by ts_hip_transpose when first read.  A product reads a
+// transposed matrix through its trans flag instead (the copy is never made),
+// and transposing it back gives src itself.  `view`: the result of
+// Tensor::transpose / t(), which, like the reference's strided view
+// (transform/transpose.rs:183-186), reads src as src is when it is read (no
+// reader link, so an in-place write of src is not held back for it); not a
+// view: contiguous()'s copy, which keeps src's values at the call (a reader
+// of src, run before src is written in place).
+struct PendingTranspose {
+    std::shared_ptr<Allocation> src;
+    std::vector<size_t> dims;  // src's
+    size_t d0 = 0, d1 = 1;
+    bool view = true;
+};
+
 // Device variant of tensor/core/allocation.rs:43-187: owns one pooled device
 // buffer; shared (Arc-like) by tensors, saved graph operands and gradients.
 struct Allocation : std::enable_shared_from_this<Allocation> {
@@ -191,9 +219,14 @@ struct Allocation : std::enable_shared_from_this<Allocation> {
     std::shared_ptr<PendingGemm> pending;
     std::shared_ptr<PendingMap> map;                 // deferred elementwise value
     std::shared_ptr<PendingColsum> colsum;           // deferred column sum
-    bool deferred() const { return pending || map || colsum; }
+    std::shared_ptr<PendingTranspose> transpose;     // deferred transposed copy
+    bool deferred() const { return pending || map || colsum || transpose; }
     std::vector<std::weak_ptr<Allocation>> readers;  // pending allocations reading this one
     size_t n = 0, rounded = 0;
+    // held by this thread's list of deferred programs with a checked
+    // division not yet computed (run_division_checks), one reference more
+    // than its users hold
+    bool check_hold = false;
 
   private:
     float *ptr_ = nullptr;
@@ -205,9 +238,25 @@ void materialize(Allocation &a);
 void materialize_map(Allocation &a);
 // Runs a's deferred column sum (tensor.cpp).
 void materialize_colsum(Allocation &a);
+// Runs a's deferred transposed copy (tensor.cpp).
+void materialize_transpose(Allocation &a);
+// A matrix operand as a product reads it: a 2-D transposed view or copy not
+// yet written is its source with the trans flag set (tensor.cpp).
+struct MatOperand {
+    std::shared_ptr<Allocation> buf;
+    int trans = 0;
+};
+MatOperand mat_operand(const std::shared_ptr<Allocation> &a);
 // Runs the deferred elementwise programs of several allocations, merged into
 // as few passes as the program limits allow (tensor.cpp).
 void materialize_maps(const std::vector<std::shared_ptr<Allocation>> &allocs);
+// Runs every deferred program of this thread that holds a checked division
+// no pass has computed yet, whether or not its value is still held, so a
+// zero divisor is reported by the next synchronisation even when the
+// quotient is never read (Runtime::sync calls it first).  Only divisions
+// with a tail are tracked: the check covers the elements past the last
+// whole 32-element block, as the reference's does (ops/div.rs:378-417).
+void run_division_checks();
 // Makes `out` pending on p and records it as a reader of p's inputs.
 void set_pending(const std::shared_ptr<Allocation> &out, std::shared_ptr<PendingGemm> p);
 // A new deferred product C = op(A) . op(B) for `out`, the first member of
@@ -312,7 +361,8 @@ struct GradFn {
     enum class Kind {
         Add, Sub, Mul, Div, AddScalar, SubScalar, MulScalar, DivScalar,
         Relu, PowScalar, MatMul, ReduceSum, ReduceMean,
-        Exp, Log, Sqrt, Tanh, Sigmoid, LeakyRelu, Softmax, ReduceSumDims, ReduceMeanDims
+        Exp, Log, Sqrt, Tanh, Sigmoid, LeakyRelu, Softmax, ReduceSumDims, ReduceMeanDims,
+        Transpose, Contiguous
     };
     explicit GradFn(Kind k) : kind(k) {}
     Kind kind;
@@ -326,6 +376,7 @@ struct GradFn {
     std::vector<size_t> reduce_dims;   // sum_dims / mean_dims: sorted, deduplicated
     bool keepdim = false;
     size_t axis = 0;                   // softmax
+    size_t dim0 = 0, dim1 = 0;         // transpose: the axes swapped
 
     // GradFn::apply (grad_fn/mod.rs:490-789): gradients by operand position.
     std::vector<std::optional<Tensor>> apply(const Tensor &grad_output) const;
@@ -423,6 +474,17 @@ class Tensor {
     // reductions/sum.rs:225-306, reductions/mean.rs:186-230
     Tensor sum_dims(const std::vector<size_t> &dims, bool keepdim) const;
     Tensor mean_dims(const std::vector<size_t> &dims, bool keepdim) const;
+    // transform/transpose.rs:156-291, contiguous.rs:123-157: a transposed
+    // view (deferred copy, see PendingTranspose), t() = the last two axes;
+    // contiguous() of a view is its copy, of anything else a clone; both
+    // record their GradFn whenever the input requires grad (no
+    // is_grad_enabled check, as there)
+    Tensor transpose(size_t dim0, size_t dim1) const;
+    Tensor t() const;
+    Tensor contiguous() const;
+    bool is_contiguous() const;
+    // init/basic.rs:304-326: every element set to value, in place
+    void fill(float value);
 
     // host access (synchronises)
     std::vector<float> data() const;
@@ -442,8 +504,17 @@ class Tensor {
     size_t size_ = 0;
     size_t id_ = 0;
     bool requires_grad_ = false;
+    // a transposed view of a contiguous tensor (transform/transpose.rs:
+    // 182-186): is_contiguous() is false, as for the reference's strided view
+    bool strided_ = false;
     std::shared_ptr<Tensor> grad_;
 };
+
+// x with axes d0 != d1 swapped, deferred (no recording): a deferred bare
+// matrix product becomes the product of its swapped operands; a pending view
+// transposed back, a deferred copy of its source; anything else a
+// PendingTranspose of x (a view when `view`).
+Tensor transposed_value(const Tensor &x, size_t d0, size_t d1, bool view);
 
 size_t next_tensor_id();
 

@@ -1794,9 +1794,10 @@ extern "C" int ts_hip_gemm_colsum(int trans_a, size_t M, size_t N, size_t K, con
         }
         hipStream_t st = as_stream(stream);
         float *W = nullptr;
-        if (hipMallocAsync(reinterpret_cast<void **>(&W), need * sizeof(float), st) != hipSuccess) {
+        const hipError_t ae = hipMallocAsync(reinterpret_cast<void **>(&W), need * sizeof(float), st);
+        if (ae != hipSuccess) {
             (void)hipGetLastError();
-            return TS_HIP_EINVAL;
+            return static_cast<int>(ae);  // hipErrorOutOfMemory when the device is full
         }
         const int status = launch_colsum(B, nullptr, K, N, ldb, colsum, W, need, stream);
         const hipError_t fe = hipFreeAsync(W, st);

@@ -93,11 +93,106 @@ __global__ __launch_bounds__(kBlock) void reduce_axes(const float *__restrict__ 
     }
 }
 
+// ---- transposing two axes (transform/transpose.rs:156-208, materialised) ----
+//
+// out = src with axes d0 < d1 swapped, both row-major.  Viewing the source as
+// [P, D0, M, D1, Q], the output is [P, D1, M, D0, Q].
+//
+// Q == 1 (d1 is the last axis, as in a matrix transpose): each (p, m) plane
+// moves in 64 x 64 tiles through LDS, so a wave reads 64 consecutive floats
+// of a source row and writes 64 consecutive floats of an output row; the LDS
+// row pitch of 65 floats keeps the column reads conflict-free.  HBM-bound:
+// 8 B per element.  Q > 1: runs of Q contiguous floats keep their order, a
+// thread per element, reads and writes both along q.
+
+struct TransposeDims {
+    uint64_t P, D0, M, D1, Q;
+    uint64_t tiles0, tiles1;  // 64-wide tiles along D0 and D1
+};
+
+__global__ __launch_bounds__(256) void transpose_tiles(const float *__restrict__ src, float *__restrict__ out,
+                                                       TransposeDims T) {
+    __shared__ float tile[64][65];
+    const uint64_t per_plane = T.tiles0 * T.tiles1;
+    const uint64_t b = blockIdx.x;
+    const uint64_t plane = b / per_plane, t = b - plane * per_plane;
+    const uint64_t i0 = (t / T.tiles1) * 64, j0 = (t % T.tiles1) * 64;
+    const uint64_t p = plane / T.M, m = plane - p * T.M;
+    const int c = static_cast<int>(threadIdx.x & 63u), r = static_cast<int>(threadIdx.x >> 6);
+    // src[p, i, m, j] at ((p * D0 + i) * M + m) * D1 + j
+    const float *sb = src + (p * T.D0 * T.M + m) * T.D1;
+    const uint64_t in_row = T.M * T.D1;
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const uint64_t i = i0 + r + 4 * k, j = j0 + c;
+        v[k] = (i < T.D0 && j < T.D1) ? sb[i * in_row + j] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) tile[r + 4 * k][c] = v[k];
+    __syncthreads();
+    // out[p, j, m, i] at ((p * D1 + j) * M + m) * D0 + i
+    float *ob = out + (p * T.D1 * T.M + m) * T.D0;
+    const uint64_t out_row = T.M * T.D0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const uint64_t j = j0 + r + 4 * k, i = i0 + c;
+        if (i < T.D0 && j < T.D1) ob[j * out_row + i] = tile[c][r + 4 * k];
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void transpose_runs(const float *__restrict__ src, float *__restrict__ out,
+                                                         TransposeDims T, uint64_t n) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kBlock;
+    for (uint64_t o = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x; o < n; o += stride) {
+        uint64_t rest = o / T.Q;
+        const uint64_t q = o - rest * T.Q;
+        const uint64_t i = rest % T.D0;
+        rest /= T.D0;
+        const uint64_t m = rest % T.M;
+        rest /= T.M;
+        const uint64_t j = rest % T.D1, p = rest / T.D1;
+        out[o] = src[(((p * T.D0 + i) * T.M + m) * T.D1 + j) * T.Q + q];
+    }
+}
+
 }  // namespace tship
 
 using namespace tship;
 
 extern "C" {
+
+int ts_hip_transpose(const float *src, const size_t *dims, size_t rank, size_t d0, size_t d1, float *out,
+                     void *stream) {
+    if (rank > 0 && !dims) return TS_HIP_EINVAL;
+    if (d0 >= rank || d1 >= rank) return TS_HIP_EINVAL;
+    uint64_t n = 1;
+    for (size_t k = 0; k < rank; ++k) n *= dims[k];
+    if (n == 0) return TS_HIP_OK;
+    if (!src || !out) return TS_HIP_EINVAL;
+    if (d0 == d1) return ts_hip_copy(src, out, n, stream);
+    if (d0 > d1) {
+        const size_t t = d0;
+        d0 = d1;
+        d1 = t;
+    }
+    TransposeDims T{1, dims[d0], 1, dims[d1], 1, 0, 0};
+    for (size_t k = 0; k < d0; ++k) T.P *= dims[k];
+    for (size_t k = d0 + 1; k < d1; ++k) T.M *= dims[k];
+    for (size_t k = d1 + 1; k < rank; ++k) T.Q *= dims[k];
+    hipStream_t s = as_stream(stream);
+    if (T.Q == 1) {
+        T.tiles0 = (T.D0 + 63) / 64;
+        T.tiles1 = (T.D1 + 63) / 64;
+        const uint64_t blocks = T.P * T.M * T.tiles0 * T.tiles1;
+        if (blocks > 0x7fffffffULL) return TS_HIP_EINVAL;
+        launch(transpose_tiles, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, src, out, T);
+    } else {
+        launch(transpose_runs, dim3(grid_for(n)), dim3(kBlock), 0, s, src, out, T, n);
+    }
+    return launch_status();
+}
+
 
 int ts_hip_broadcast_copy(const float *src, const size_t *src_dims, size_t src_rank, float *out,
                           const size_t *out_dims, size_t out_rank, float scale, int use_scale,

@@ -189,6 +189,23 @@ class Tensor:
         d, r = _dims(dims)
         return _wrap(_G.ts_tensor_mean_dims(self._h, d, r, int(bool(keepdim))))
 
+    # -- transform/{transpose,contiguous}.rs ----------------------------------------
+    def transpose(self, dim0: int, dim1: int) -> "Tensor":
+        return _wrap(_G.ts_tensor_transpose(self._h, dim0, dim1))
+
+    def t(self) -> "Tensor":
+        return _wrap(_G.ts_tensor_t(self._h))
+
+    def contiguous(self) -> "Tensor":
+        return _wrap(_G.ts_tensor_contiguous(self._h))
+
+    def is_contiguous(self) -> bool:
+        return bool(_G.ts_tensor_is_contiguous(self._h))
+
+    def fill(self, value: float) -> None:
+        """Tensor::fill (init/basic.rs:304-326), in place."""
+        _ok(_G.ts_tensor_fill(self._h, value))
+
     def sum(self) -> "Tensor":
         return _wrap(_G.ts_tensor_sum(self._h))
 
