@@ -266,10 +266,14 @@ int ts_hip_softmax_backward(const float *y, const float *go, float *gi, size_t o
  * TS_HIP_MAP_MAX_INPUTS inputs of n elements (or one value used for every
  * element: bit k of scalar_inputs reads inputs[k][0]; bit k of const_inputs
  * takes const_values[k], and inputs[k] is not read) and stores up to
- * TS_HIP_MAP_MAX_OUTPUTS of its values.  Registers 0 .. n_inputs-1 hold the
- * inputs; op k writes register TS_HIP_MAP_MAX_INPUTS + k and reads registers a
- * and b (inputs or earlier ops); an output or the summed register may be an
- * input's.  Each op's formula and fp32 operation order is that of the separate
+ * TS_HIP_MAP_MAX_OUTPUTS of its values.  The pass has TS_HIP_MAP_REGS
+ * registers per element: registers 0 .. n_inputs-1 start with the inputs; op k
+ * reads registers a and b and writes register d (any register, an input's or
+ * an earlier op's included: the op reads its operands first), so a program of
+ * up to TS_HIP_MAP_MAX_OPS ops fits the file when its values' lifetimes do
+ * (every register read must have been written, by the inputs or an earlier
+ * op).  Outputs and the summed register are read after the last op.  Each op's
+ * formula and fp32 operation order is that of the separate
  * kernel of the same op, so every stored value has the bits the op-by-op
  * sequence gives:
  *   ADD a+b, SUB a-b, MUL a*b, DIV a/b (with flags & TS_HIP_MAP_CHECKED the
@@ -285,8 +289,9 @@ int ts_hip_softmax_backward(const float *y, const float *go, float *gi, size_t o
  * unaligned buffer adds element by element); the workspace is
  * ts_hip_map_workspace_floats(n) floats, 8-byte aligned. */
 #define TS_HIP_MAP_MAX_INPUTS 5
-#define TS_HIP_MAP_MAX_OPS 11
+#define TS_HIP_MAP_MAX_OPS 24
 #define TS_HIP_MAP_MAX_OUTPUTS 4
+#define TS_HIP_MAP_REGS 16
 #define TS_HIP_MAP_CHECKED 1
 enum {
     TS_HIP_MAP_ADD = 0, TS_HIP_MAP_SUB = 1, TS_HIP_MAP_MUL = 2, TS_HIP_MAP_DIV = 3, TS_HIP_MAP_NEG = 4,
@@ -296,6 +301,7 @@ enum {
 typedef struct ts_hip_map_op {
     uint8_t code, a, b, flags;
     float imm;
+    uint8_t d; /* destination register */
 } ts_hip_map_op;
 typedef struct ts_hip_map_program {
     const float *inputs[TS_HIP_MAP_MAX_INPUTS];
@@ -311,6 +317,24 @@ size_t ts_hip_map_workspace_floats(size_t n);
 int ts_hip_map(const ts_hip_map_program *prog, size_t n, size_t tail_start, size_t zero_check_start,
                unsigned long long *zero_index, float *sum_out, int mean, float *workspace, size_t workspace_floats,
                void *stream);
+/* Compiled programs (no counterpart in the reference).  ts_hip_map runs a
+ * program whose operands are all 16-byte aligned as a kernel compiled at run
+ * time for its shape -- its ops, registers, inputs read per element, stored
+ * values and reduction; not the pointers, constants or immediates -- with the
+ * interpreter's loop and fp32 operations written out as straight-line code
+ * (hipRTC, the library's numerics flags), so with the same bits; compiled
+ * kernels are cached for the process, per device.  mode 0: never; 1: from a
+ * shape's second use (the default); 2: from its first.  Returns the previous
+ * mode, or -1 for a bad one.  A shape whose compilation fails runs
+ * interpreted, counted in *failed, with the compiler's log in
+ * ts_hip_map_jit_log(). */
+int ts_hip_map_jit_mode(int mode);
+int ts_hip_map_jit_stats(size_t *compiled, size_t *failed);
+const char *ts_hip_map_jit_log(void);
+/* The source compiled for a program with its operands aligned (reduce: with
+ * its sum), NUL-terminated into buf (at most cap bytes); returns its length
+ * + 1, or 0 for a malformed program. */
+size_t ts_hip_map_jit_source(const ts_hip_map_program *prog, int reduce, char *buf, size_t cap);
 
 /* ---- reductions ------------------------------------------------------------- */
 

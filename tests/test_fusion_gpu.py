@@ -220,7 +220,7 @@ def test_product_with_several_consumers(fusion):
         c = h.mul_scalar(2.0)               # reads the bare product
         d = b2.add_tensor(h).relu()         # a second fused chain on the same product
         loss = a.add_tensor(c).mul_tensor(d).sum()
-        T.synchronize()
+        loss.value()                        # the sum is deferred until read (or until backward's pass)
         T.Profile.enable(False)
         assert T.Profile.read(T.Profile.GEMM)["launches"] == 1, on   # the forward product, once
         T.Profile.reset()

@@ -25,8 +25,9 @@ def _ffi():
 
 
 def _program(inputs, ops, outputs, scalar=0, reduce_reg=-1, consts=None):
-    """inputs: device pointers; ops: (code name, a, b, imm, flags) with
-    registers numbered as in include/ts_hip.h; outputs: (pointer, register);
+    """inputs: device pointers; ops: (code name, a, b, imm, flags[, d]) with
+    registers numbered as in include/ts_hip.h, op k writing register d
+    (default R0 + k, one register per op); outputs: (pointer, register);
     consts: {input index: value} for constant inputs (their pointer unused)."""
     F = _ffi()
     p = F.MapProgram()
@@ -38,8 +39,9 @@ def _program(inputs, ops, outputs, scalar=0, reduce_reg=-1, consts=None):
         p.const_inputs |= 1 << k
         p.const_values[k] = v
     p.n_ops = len(ops)
-    for k, (code, a, b, imm, flags) in enumerate(ops):
-        p.ops[k] = F.MapOp(F.MAP_CODES[code], a, b, flags, imm)
+    for k, op in enumerate(ops):
+        code, a, b, imm, flags = op[:5]
+        p.ops[k] = F.MapOp(F.MAP_CODES[code], a, b, flags, imm, op[5] if len(op) > 5 else R0 + k)
     p.n_outputs = len(outputs)
     for k, (ptr, reg) in enumerate(outputs):
         p.outputs[k] = ptr
@@ -255,6 +257,8 @@ def test_bad_programs_are_refused():
         _program([d.ptr], [("add", 0, 3, 0.0, 0)], [(d.ptr, R0)]),         # input register past n_inputs
         _program([d.ptr], [("add", 0, 0, 0.0, 0)], [(d.ptr, R0 + 1)]),     # output of no op
         _program([d.ptr], [("add", 0, 0, 0.0, 0)], []),                    # nothing stored, no sum
+        _program([d.ptr], [("add", 0, 0, 0.0, 0, 16)], [(d.ptr, 0)]),      # writes past the register file
+        _program([d.ptr], [("add", 0, 0, 0.0, 0, 7), ("neg", R0, R0, 0.0, 0, 8)], [(d.ptr, 8)]),  # reads an unwritten register
     ]
     for p in bad:
         assert hip.ts_hip_map(ctypes.byref(p), 16, 16, 0, None, None, 0, None, 0, None) == 100001
@@ -303,15 +307,58 @@ def test_chain_bits_with_fusion_on_and_off(T, oracle, n):
         assert_bits_equal(u, v, name)
 
 
-def test_chain_runs_as_few_fused_passes(T):
-    # forward: one pass computing y (stored: relu saves it) and a + b (stored:
-    # mul saves it) with the sum's first pass; backward: one pass writing the
-    # three gradients, the seed (ones) a constant of it and never written.
-    # Bytes per element: 12 read + 8 written, then 16 read (y, c, a, a + b) +
-    # 12 written.
+def _chain_profiled(T, ta, tb, tc, read_loss_first):
+    T.synchronize()
+    T.Profile.reset()
+    T.Profile.enable(True)
+    y = ta.add_tensor(tb).mul_tensor(tc).sub_tensor(ta.div_tensor(tc)).relu()
+    loss = y.sum()
+    first = loss.value() if read_loss_first else None
+    loss.backward()
+    T.synchronize()
+    T.Profile.enable(False)
+    ew = T.Profile.read(T.Profile.ELEMENTWISE)
+    red = T.Profile.read(T.Profile.REDUCTION)
+    out = (loss.value(), y.data(), ta.grad_by_value().data(), tb.grad_by_value().data(),
+           tc.grad_by_value().data())
+    assert first is None or first == out[0]
+    assert_bits_equal(loss.grad().data(), np.ones(1, np.float32), "seed")  # still ones when read
+    T.clear_gradients()
+    return ew, red, out
+
+
+def test_chain_runs_as_one_fused_pass(T, oracle):
+    # the loss not read before backward: one pass reads a, b, c, recomputes the
+    # forward values, writes the three gradients and adds y up into the loss
+    # (the seed, ones, a constant of it): 12 B read + 12 B written per element,
+    # the fused floor.  Read before backward: a forward pass with the sum
+    # (storing y and a + b, held for the backward) and a backward pass, 20 + 28
+    # B.  Both give every value the bits of the op-by-op run.
     n = 1 << 20
     a, b = normal(n, 21), normal(n, 22)
     c = uniform(n, 0.5, 2.0, 23)
+    T.set_fusion(True)
+    ta, tb, tc = (T.Tensor.from_slice(v, [n]).with_requires_grad() for v in (a, b, c))
+    ew, red, one = _chain_profiled(T, ta, tb, tc, False)
+    assert red["launches"] == 0
+    assert ew["launches"] == 1, ew                      # the fused pass (y is recomputed when read after)
+    assert ew["work"] / n == 24.0
+    ew, red, two = _chain_profiled(T, ta, tb, tc, True)
+    assert red["launches"] == 0
+    assert ew["launches"] == 2, ew                      # forward pass, backward pass
+    assert ew["work"] / n == 20.0 + 28.0
+    for name, u, v in zip(("loss", "y", "ga", "gb", "gc"), one, two):
+        assert_bits_equal(u, v, name)
+    T.set_fusion(False)
+    _, _, off = _chain_profiled(T, ta, tb, tc, False)
+    for name, u, v in zip(("loss", "y", "ga", "gb", "gc"), one, off):
+        assert_bits_equal(u, v, name + " (fusion off)")
+
+
+def test_chain_pass_moves_the_fused_floor(T):
+    n = 1 << 20
+    a, b = normal(n, 24), normal(n, 25)
+    c = uniform(n, 0.5, 2.0, 26)
     T.set_fusion(True)
     ta, tb, tc = (T.Tensor.from_slice(v, [n]).with_requires_grad() for v in (a, b, c))
     T.synchronize()
@@ -322,13 +369,16 @@ def test_chain_runs_as_few_fused_passes(T):
     T.synchronize()
     T.Profile.enable(False)
     ew = T.Profile.read(T.Profile.ELEMENTWISE)
-    red = T.Profile.read(T.Profile.REDUCTION)
-    assert red["launches"] == 0
-    assert ew["launches"] == 2, ew                      # forward pass, backward pass
-    per_elem = ew["work"] / n
-    assert per_elem == 20.0 + 28.0, per_elem
-    # the seed is still ones when read
-    assert_bits_equal(loss.grad().data(), np.ones(1, np.float32), "seed")
+    assert ew["launches"] == 1, ew
+    assert ew["work"] / n == 24.0
+    exact = float(np.sum(oracle_chain_y(a, b, c), dtype=np.float64))
+    assert abs(loss.value() - exact) <= 1e-6 * abs(exact)
+    T.clear_gradients()
+
+
+def oracle_chain_y(a, b, c):
+    import oracle as O
+    return O.relu(O.sub(O.mul(O.add(a, b), c), O.div(a, c)))
 
 
 @pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])

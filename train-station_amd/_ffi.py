@@ -35,7 +35,7 @@ def _load(name: str) -> ctypes.CDLL:
 
 # --- include/ts_hip.h ------------------------------------------------------------
 
-MAP_MAX_INPUTS, MAP_MAX_OPS, MAP_MAX_OUTPUTS = 5, 11, 4
+MAP_MAX_INPUTS, MAP_MAX_OPS, MAP_MAX_OUTPUTS, MAP_REGS = 5, 24, 4, 16
 # TS_HIP_MAP_* op codes and flags of include/ts_hip.h
 MAP_CODES = {"add": 0, "sub": 1, "mul": 2, "div": 3, "neg": 4, "relu": 5, "relu_bwd": 6, "add_s": 7, "sub_s": 8,
              "mul_s": 9, "div_s": 10, "square": 11}
@@ -56,7 +56,7 @@ class OperandXf(ctypes.Structure):
 class MapOp(ctypes.Structure):
     """struct ts_hip_map_op of include/ts_hip.h"""
     _fields_ = [("code", _c.c_uint8), ("a", _c.c_uint8), ("b", _c.c_uint8), ("flags", _c.c_uint8),
-                ("imm", _c.c_float)]
+                ("imm", _c.c_float), ("d", _c.c_uint8)]
 
 
 class MapProgram(ctypes.Structure):
@@ -129,6 +129,10 @@ HIP_SIGNATURES = {
                                          _c.c_int, VP]),
     "ts_hip_reduce_sum": (_c.c_int, [VP, _c.POINTER(SZ), SZ, _c.c_uint, VP, _c.c_float, _c.c_int, VP]),
     "ts_hip_transpose": (_c.c_int, [VP, _c.POINTER(SZ), SZ, SZ, SZ, VP, VP]),
+    "ts_hip_map_jit_mode": (_c.c_int, [_c.c_int]),
+    "ts_hip_map_jit_stats": (_c.c_int, [_c.POINTER(SZ), _c.POINTER(SZ)]),
+    "ts_hip_map_jit_log": (_c.c_char_p, []),
+    "ts_hip_map_jit_source": (SZ, [VP, _c.c_int, _c.c_char_p, SZ]),
     "ts_hip_log_backward": (_c.c_int, [VP, VP, VP, SZ, VP]),
     "ts_hip_sqrt_backward": (_c.c_int, [VP, VP, VP, SZ, VP]),
     "ts_hip_tanh_backward": (_c.c_int, [VP, VP, VP, SZ, VP]),

@@ -68,8 +68,19 @@ const Tensor *accumulated_gradient(size_t id) {
     return it == grads.end() ? nullptr : &it->second;
 }
 
+namespace {
+thread_local int g_backward_depth = 0;  // backward calls running on this thread
+struct BackwardScope {
+    BackwardScope() { ++g_backward_depth; }
+    ~BackwardScope() { --g_backward_depth; }
+};
+}  // namespace
+
+bool in_backward() { return g_backward_depth > 0; }
+
 // engine.rs:962-1047
 void engine_backward(Tensor &root, const Tensor *grad_output) {
+    const BackwardScope scope;
     // backward(None) seeds ones; deferred, the seed is a constant of the
     // programs that read it and is written only if read elsewhere
     Tensor init = grad_output ? grad_output->alias() : Tensor::constant(root.dims(), 1.0f);

@@ -171,6 +171,7 @@ float *Allocation::get() {
     else if (map) materialize_map(*this);
     else if (colsum) materialize_colsum(*this);
     else if (transpose) materialize_transpose(*this);
+    else if (reduce) materialize_reduce(*this);
     DevicePool::get().note_use(ptr_);
     return ptr_;
 }
@@ -184,6 +185,7 @@ void Allocation::before_write() {
             else if (r->map) materialize_map(*r);
             else if (r->colsum) materialize_colsum(*r);
             else if (r->transpose) materialize_transpose(*r);
+            else if (r->reduce) materialize_reduce(*r);
         }
 }
 

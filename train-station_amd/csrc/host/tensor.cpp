@@ -487,11 +487,62 @@ void materialize(Allocation &a) {
 
 namespace {
 
+// The registers of a pass over program p: reg[j] for every node the pass
+// computes, -1 for a node it need not (read by no computed op, not kept, no
+// division to check).  Input k sits in register k from the start until its
+// last use; each op then takes the lowest free register, after the registers
+// of operands it reads for the last time are freed (an op reads its operands
+// before it writes).  Nodes in `keep` -- the stored values and the summed one
+// -- stay live to the end.  False when the computed ops exceed
+// TS_HIP_MAP_MAX_OPS or more than TS_HIP_MAP_REGS values would be live at once.
+bool allocate_registers(const PendingMap &p, const std::vector<int> &keep, std::vector<int> &reg) {
+    const int n = static_cast<int>(p.nodes.size());
+    constexpr int kEnd = 1 << 30;
+    std::vector<int> last(n, -1);
+    std::vector<char> need(n, 0);
+    for (int j : keep) {
+        need[j] = 1;
+        last[j] = kEnd;
+    }
+    int ops = 0;
+    for (int j = n - 1; j >= 0; --j) {
+        const MapNode &nd = p.nodes[j];
+        if (nd.code == MapNode::kLeaf || (!need[j] && nd.checks.empty())) continue;
+        need[j] = 1;
+        ++ops;
+        for (const int o : {static_cast<int>(nd.a), static_cast<int>(nd.b)}) {
+            need[o] = 1;
+            if (last[o] < j) last[o] = j;
+        }
+    }
+    if (ops > TS_HIP_MAP_MAX_OPS) return false;
+    reg.assign(n, -1);
+    uint32_t busy = 0;
+    for (int j = 0; j < n; ++j) {
+        const MapNode &nd = p.nodes[j];
+        if (nd.code == MapNode::kLeaf && need[j]) {
+            reg[j] = nd.a;
+            busy |= 1u << nd.a;
+        }
+    }
+    for (int j = 0; j < n; ++j) {
+        const MapNode &nd = p.nodes[j];
+        if (nd.code == MapNode::kLeaf || !need[j]) continue;
+        if (last[nd.a] == j) busy &= ~(1u << reg[nd.a]);
+        if (last[nd.b] == j) busy &= ~(1u << reg[nd.b]);
+        int d = 0;
+        while (d < TS_HIP_MAP_REGS && ((busy >> d) & 1u)) ++d;
+        if (d == TS_HIP_MAP_REGS) return false;
+        reg[j] = d;
+        if (last[j] >= 0) busy |= 1u << d;  // a checked division nothing reads frees its register at once
+    }
+    return true;
+}
+
 // One program under construction: its leaves and nodes, common
 // subexpressions shared (the same op on the same operands is one node).
 struct MapBuilder {
     PendingMap p;
-    int ops = 0;
     std::map<std::tuple<uint8_t, uint8_t, int, int, uint32_t>, int> cse;
 
     int leaf_node(int k) {
@@ -558,7 +609,6 @@ struct MapBuilder {
         if (inherit) nd.checks = *inherit;
         else if (flags & TS_HIP_MAP_CHECKED) nd.checks.push_back(std::make_shared<DivCheck>());
         p.nodes.push_back(std::move(nd));
-        ++ops;
         const int id = static_cast<int>(p.nodes.size()) - 1;
         cse.emplace(key, id);
         return id;
@@ -586,8 +636,10 @@ struct MapBuilder {
         if (al->map && al->map->n == n) return import(*al->map, al);
         return leaf(al, false);
     }
-    bool fits() const {
-        return p.leaves.size() <= static_cast<size_t>(TS_HIP_MAP_MAX_INPUTS) && ops <= TS_HIP_MAP_MAX_OPS;
+    // one pass can compute the program with the nodes of `keep` stored
+    bool fits(const std::vector<int> &keep) const {
+        std::vector<int> reg;
+        return p.leaves.size() <= static_cast<size_t>(TS_HIP_MAP_MAX_INPUTS) && allocate_registers(p, keep, reg);
     }
 };
 
@@ -639,20 +691,79 @@ struct MapOutput {
     int node;
 };
 
-// Runs one program: stores `outs` (and any still-deferred origin the program
-// computes on the way that something else holds), and with sum_out set adds
-// node `reduce` up as ts_hip_sum / ts_hip_mean would.
+// This thread's deferred sums and means (outputs whose `reduce` is pending),
+// for passes to take up as their reduction.
+std::vector<std::weak_ptr<Allocation>> &pending_reduces() {
+    static thread_local std::vector<std::weak_ptr<Allocation>> v;
+    return v;
+}
+
+// A pass with no reduction of its own takes up a deferred sum of a value it
+// can compute from the inputs it reads anyway (its program merged in, within
+// the pass's limits): the sum costs the pass no extra reads.  `keep` gains the
+// summed node.
+void attach_reduce(MapBuilder &b, std::vector<int> &keep, int &reduce, float *&sum_out, bool &mean) {
+    auto &v = pending_reduces();
+    size_t live = 0;
+    for (size_t i = 0; i < v.size(); ++i) {
+        auto o = v[i].lock();
+        if (!o || !o->reduce) continue;  // gone or computed: off the list
+        const PendingReduce &r = *o->reduce;
+        if (reduce < 0 && r.x->map && r.x->map->n == b.p.n) {
+            MapBuilder trial = b;
+            const int node = trial.import(*r.x->map, r.x);
+            bool reads_more = trial.p.leaves.size() > static_cast<size_t>(TS_HIP_MAP_MAX_INPUTS);
+            for (size_t q = b.p.leaves.size(); q < trial.p.leaves.size(); ++q)
+                reads_more = reads_more || !((trial.p.consts >> q) & 1u);
+            keep.push_back(node);
+            std::vector<int> reg;
+            if (!reads_more && allocate_registers(trial.p, keep, reg)) {
+                b = std::move(trial);
+                reduce = node;
+                sum_out = o->raw();
+                mean = r.mean;
+                DevicePool::get().note_use(sum_out);
+                o->reduce.reset();
+                continue;
+            }
+            keep.pop_back();
+        }
+        v[live++] = v[i];
+    }
+    v.resize(live);
+}
+
+// Runs one program: stores `outs` (and, outside backward, any still-deferred
+// origin the program computes on the way that something else holds, as far
+// as the registers allow), and with sum_out set adds node `reduce` up as
+// ts_hip_sum / ts_hip_mean would.
 void launch_program(MapBuilder &b, std::vector<MapOutput> outs, int reduce = -1, float *sum_out = nullptr,
                     bool mean = false) {
     const size_t n = b.p.n;
-    for (size_t j = 0; j < b.p.nodes.size() && outs.size() < static_cast<size_t>(TS_HIP_MAP_MAX_OUTPUTS); ++j) {
+    std::vector<int> keep, reg;
+    for (const MapOutput &m : outs) keep.push_back(m.node);
+    if (reduce >= 0) keep.push_back(reduce);
+    else attach_reduce(b, keep, reduce, sum_out, mean);
+    if (!allocate_registers(b.p, keep, reg)) throw Error("an elementwise program exceeds the fused pass's limits");
+    // A value still held (a saved operand, or its tensor) may be read again,
+    // and this pass computes it anyway, so it stores it -- except during
+    // backward, whose passes run after the forward values' last graph use:
+    // there a value read later is computed again from its inputs.
+    for (size_t j = 0; !in_backward() && j < b.p.nodes.size() && outs.size() < static_cast<size_t>(TS_HIP_MAP_MAX_OUTPUTS);
+         ++j) {
         auto o = b.p.nodes[j].origin.lock();
-        // still held (a saved operand, or its tensor): it may be read again,
-        // and this pass computes it anyway, so it stores it
         if (!o || !o->map || !held_elsewhere(o, 1)) continue;
         bool listed = false;
         for (const MapOutput &m : outs) listed = listed || m.alloc == o;
-        if (!listed) outs.push_back({o, static_cast<int>(j)});
+        if (listed) continue;
+        keep.push_back(static_cast<int>(j));
+        std::vector<int> trial;
+        if (allocate_registers(b.p, keep, trial)) {
+            outs.push_back({o, static_cast<int>(j)});
+            reg = std::move(trial);
+        } else {
+            keep.pop_back();
+        }
     }
     // leaves first: deferred ones run before, outside this launch's window
     ts_hip_map_program prog{};
@@ -660,28 +771,29 @@ void launch_program(MapBuilder &b, std::vector<MapOutput> outs, int reduce = -1,
     prog.scalar_inputs = b.p.scalar;
     prog.const_inputs = b.p.consts;
     double bytes = 0.0;
+    std::vector<char> read(b.p.leaves.size(), 0);  // inputs a computed op or an output reads
+    for (size_t j = 0; j < b.p.nodes.size(); ++j)
+        if (b.p.nodes[j].code == MapNode::kLeaf && reg[j] >= 0) read[b.p.nodes[j].a] = 1;
     for (size_t k = 0; k < b.p.leaves.size(); ++k) {
-        if ((b.p.consts >> k) & 1u) {  // a constant: no buffer
-            prog.const_values[k] = b.p.values[k];
+        if (((b.p.consts >> k) & 1u) || !read[k]) {  // a constant (or an input nothing reads): no buffer
+            prog.const_inputs |= 1u << k;
+            prog.scalar_inputs |= 1u << k;
+            prog.const_values[k] = read[k] ? b.p.values[k] : 0.0f;
             continue;
         }
         prog.inputs[k] = b.p.leaves[k]->get();
         if (!((b.p.scalar >> k) & 1u)) bytes += 4.0 * n;
     }
-    std::vector<int> reg(b.p.nodes.size(), -1);
     for (size_t j = 0; j < b.p.nodes.size(); ++j) {
         const MapNode &nd = b.p.nodes[j];
-        if (nd.code == MapNode::kLeaf) {
-            reg[j] = nd.a;
-            continue;
-        }
+        if (nd.code == MapNode::kLeaf || reg[j] < 0) continue;  // an input, or a value nothing needs
         ts_hip_map_op &op = prog.ops[prog.n_ops];
         op.code = nd.code;
         op.a = static_cast<uint8_t>(reg[nd.a]);
         op.b = static_cast<uint8_t>(reg[nd.b]);
         op.flags = nd.flags;
         op.imm = nd.imm;
-        reg[j] = TS_HIP_MAP_MAX_INPUTS + static_cast<int>(prog.n_ops);
+        op.d = static_cast<uint8_t>(reg[j]);
         ++prog.n_ops;
     }
     for (const MapOutput &m : outs) {
@@ -724,7 +836,7 @@ std::shared_ptr<PendingMap> defer(size_t n, const std::vector<std::pair<std::sha
         std::vector<int> ids;
         for (const auto &o : operands) ids.push_back(o.second ? b.leaf(o.first, true) : b.value(o.first, n));
         b.p.root = build(b, ids);
-        if (b.fits()) return std::make_shared<PendingMap>(std::move(b.p));
+        if (b.fits({b.p.root})) return std::make_shared<PendingMap>(std::move(b.p));
         for (const auto &o : operands) o.first->get();
     }
     throw Error("an elementwise program exceeds the fused pass's limits");
@@ -789,7 +901,9 @@ void materialize_maps(const std::vector<std::shared_ptr<Allocation>> &allocs) {
         if (!outs.empty() && group.p.n == al->map->n && outs.size() < static_cast<size_t>(TS_HIP_MAP_MAX_OUTPUTS)) {
             MapBuilder trial = group;
             const int r = trial.import(*al->map, al);
-            if (trial.fits()) {
+            std::vector<int> keep{r};
+            for (const MapOutput &m : outs) keep.push_back(m.node);
+            if (trial.fits(keep)) {
                 group = std::move(trial);
                 outs.push_back({al, r});
                 continue;
@@ -1389,13 +1503,47 @@ void fused_sum(const std::shared_ptr<Allocation> &x, float *out, bool mean) {
     else b.p.nodes[r].origin.reset();  // not stored: it stays deferred
     launch_program(b, outs, r, out, mean);
 }
+
+// sum / mean of a deferred elementwise value, deferred in turn (x is the
+// summed tensor's allocation); out reads x, so an in-place write of x's
+// buffer runs it first
+Tensor deferred_reduce(const std::shared_ptr<Allocation> &x, size_t n, bool mean) {
+    Tensor out = Tensor::new_uninit({1});
+    auto r = std::make_shared<PendingReduce>();
+    r->x = x;
+    r->n = n;
+    r->mean = mean;
+    add_reader(x, out.allocation());
+    out.allocation()->reduce = std::move(r);
+    pending_reduces().push_back(out.allocation());
+    return out;
+}
 }  // namespace
 
-Tensor Tensor::sum() const {
-    Tensor out = new_uninit({1});
-    if (alloc_ && alloc_->map && fusion_enabled()) {
-        fused_sum(alloc_, out.dev_mut(), false);
+void materialize_reduce(Allocation &a) {
+    const std::shared_ptr<PendingReduce> r = a.reduce;
+    float *out = a.raw();
+    DevicePool::get().note_use(out);
+    if (r->x->map && r->x->map->n == r->n) {
+        fused_sum(r->x, out, r->mean);  // x's program with its sum; x stored only if held elsewhere
     } else {
+        const float *x = r->x->get();
+        const size_t ws = ts_hip_sum_workspace_floats(r->n);
+        Allocation work(ws);
+        launch(KernelClass::Reduction, 4.0 * r->n + 4.0, r->mean ? "ts_hip_mean" : "ts_hip_sum", [&] {
+            return r->mean ? ts_hip_mean(x, r->n, out, work.get(), ws, S())
+                           : ts_hip_sum(x, r->n, out, work.get(), ws, S());
+        });
+    }
+    a.reduce.reset();
+}
+
+Tensor Tensor::sum() const {
+    Tensor out;
+    if (alloc_ && alloc_->map && fusion_enabled()) {
+        out = deferred_reduce(alloc_, size_, false);
+    } else {
+        out = new_uninit({1});
         const size_t ws = ts_hip_sum_workspace_floats(size_);
         Allocation work(ws);
         launch(KernelClass::Reduction, 4.0 * size_ + 4.0, "ts_hip_sum",
@@ -1410,10 +1558,11 @@ Tensor Tensor::sum() const {
 }
 
 Tensor Tensor::mean() const {
-    Tensor out = new_uninit({1});
+    Tensor out;
     if (alloc_ && alloc_->map && fusion_enabled()) {
-        fused_sum(alloc_, out.dev_mut(), true);
+        out = deferred_reduce(alloc_, size_, true);
     } else {
+        out = new_uninit({1});
         const size_t ws = ts_hip_sum_workspace_floats(size_);
         Allocation work(ws);
         launch(KernelClass::Reduction, 4.0 * size_ + 4.0, "ts_hip_mean",

@@ -202,6 +202,17 @@ struct PendingTranspose {
     bool view = true;
 };
 
+// A deferred sum or mean of a deferred elementwise value x (reductions/
+// sum.rs:80-141, mean.rs:48-109): out[0] = sum(x), divided by (float)n for
+// the mean, with the bits of ts_hip_sum / ts_hip_mean over x's values.  The
+// first pass that reads x's inputs anyway adds x up as its reduction (backward
+// of the loss usually is that pass); otherwise it runs when out is read.
+struct PendingReduce {
+    std::shared_ptr<Allocation> x;
+    size_t n = 0;
+    bool mean = false;
+};
+
 // Device variant of tensor/core/allocation.rs:43-187: owns one pooled device
 // buffer; shared (Arc-like) by tensors, saved graph operands and gradients.
 struct Allocation : std::enable_shared_from_this<Allocation> {
@@ -220,7 +231,8 @@ struct Allocation : std::enable_shared_from_this<Allocation> {
     std::shared_ptr<PendingMap> map;                 // deferred elementwise value
     std::shared_ptr<PendingColsum> colsum;           // deferred column sum
     std::shared_ptr<PendingTranspose> transpose;     // deferred transposed copy
-    bool deferred() const { return pending || map || colsum || transpose; }
+    std::shared_ptr<PendingReduce> reduce;           // deferred sum / mean
+    bool deferred() const { return pending || map || colsum || transpose || reduce; }
     std::vector<std::weak_ptr<Allocation>> readers;  // pending allocations reading this one
     size_t n = 0, rounded = 0;
     // held by this thread's list of deferred programs with a checked
@@ -240,6 +252,8 @@ void materialize_map(Allocation &a);
 void materialize_colsum(Allocation &a);
 // Runs a's deferred transposed copy (tensor.cpp).
 void materialize_transpose(Allocation &a);
+// Runs a's deferred sum / mean (tensor.cpp).
+void materialize_reduce(Allocation &a);
 // A matrix operand as a product reads it: a 2-D transposed view or copy not
 // yet written is its source with the trans flag set (tensor.cpp).
 struct MatOperand {
@@ -531,6 +545,10 @@ bool gradients_pending();           // the gradient map holds at least one gradi
 void register_operation(size_t output_id, std::vector<size_t> input_ids, GradFn fn);
 const Tensor *accumulated_gradient(size_t id);
 void engine_backward(Tensor &root, const Tensor *grad_output);
+// true while engine_backward runs on this thread: its passes store only the
+// values they run for (the forward values they recompute are past their last
+// graph use)
+bool in_backward();
 
 // ---- optimizer -----------------------------------------------------------------------
 

@@ -7,10 +7,9 @@
 #include <stdint.h>
 
 #include "ts_hip.h"
+#include "ts_hip_device_common.h"
 
 namespace tship {
-
-constexpr int kBlock = 256;  // 4 wave64 per workgroup
 
 // Status of a launch: the error the runtime recorded for it, if any.
 inline int launch_status() {
@@ -43,6 +42,17 @@ inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds
     ++w->kernels;
 }
 
+// The same for a kernel of a code object compiled at run time (the compiled
+// elementwise programs of ts_hip_map): blocks workgroups of `threads`.
+inline hipError_t launch_module(hipFunction_t f, unsigned blocks, unsigned threads, hipStream_t s, void **params) {
+    TimingWindow *w = timing_window();
+    if (!w) return hipModuleLaunchKernel(f, blocks, 1, 1, threads, 1, 1, 0, s, params, nullptr);
+    const hipError_t e = hipExtModuleLaunchKernel(f, blocks * threads, 1, 1, threads, 1, 1, 0, s, params, nullptr,
+                                                  w->kernels == 0 ? w->start : nullptr, w->stop, 0u);
+    if (e == hipSuccess) ++w->kernels;
+    return e;
+}
+
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 
@@ -58,8 +68,6 @@ inline unsigned grid_for(size_t units, size_t per_thread = 1) {
 }
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
-typedef float f4v_t __attribute__((ext_vector_type(4)));
 
 // Non-temporal 16-byte store / load (the nt cache policy): for streams that
 // are written, or read, once per kernel.
@@ -82,27 +90,6 @@ inline size_t sum_blocks(size_t n) {
     size_t b = (n + kSumChunk - 1) / kSumChunk;
     if (b > kSumMaxBlocks) b = kSumMaxBlocks;
     return b < 1 ? 1 : b;
-}
-
-__device__ inline double wave_sum(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-// Sum of a workgroup's per-thread values, returned to thread 0.
-__device__ inline double block_sum(double v) {
-    __shared__ double lds[kBlock / 64];
-    v = wave_sum(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) lds[wave] = v;
-    __syncthreads();
-    double r = 0.0;
-    if (threadIdx.x == 0) {
-#pragma unroll
-        for (int w = 0; w < kBlock / 64; ++w) r += lds[w];
-    }
-    return r;
 }
 
 // The sum's second pass: one workgroup adds the nparts f64 partials in a fixed

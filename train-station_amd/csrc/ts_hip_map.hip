@@ -7,246 +7,106 @@
 // so intermediates nobody reads are never written and shared inputs are read
 // once.
 //
-// Registers: r[0 .. n_inputs) hold the inputs, r[kMapIn + k] the value of op
-// k.  Each thread evaluates four consecutive elements at once; the register
-// file is four arrays indexed by uniform (scalar) indices, which the compiler
-// keeps in VGPRs (indexed moves), and each op's code selects its formula by a
-// uniform branch.  An indexed array takes a power-of-two register tuple, so
-// the limits (5 inputs + 11 ops = 16 registers, the config-2 backward as one
-// program) keep the file at 4 x 16 VGPRs and the kernel at 4 waves per SIMD.
-#include <utility>
+// Two ways to run a program, with the same bits (the same fp32 operations in
+// the same order over the same loop, ts_hip_map_body.h):
+// * the interpreter below: r[0 .. n_inputs) start with the inputs; op k
+//   writes r[d_k], the register the host assigned it.  Each thread evaluates
+//   four consecutive elements at once; the register file is four arrays
+//   indexed by uniform (scalar) indices, which the compiler keeps in VGPRs
+//   (indexed moves), and each op's code selects its formula by a uniform
+//   branch.  An indexed array takes a power-of-two register tuple: 16
+//   registers keep the file at 4 x 16 VGPRs and the kernel at 4 waves per
+//   SIMD.
+// * a compiled program: for a program shape (ops, registers, inputs read per
+//   element, stored values, reduction) met again, the same loop with the ops
+//   written out as straight-line code is compiled at run time (hipRTC) and
+//   cached for the process; its registers are plain registers, and no op is
+//   dispatched per element (ts_hip_map_jit_mode).
+#include <hip/hiprtc.h>
+
+#include <atomic>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
 
 #include "ts_hip_internal.h"
+#include "ts_hip_map_body.h"
 
 namespace tship {
 
-constexpr int kMapIn = TS_HIP_MAP_MAX_INPUTS;
-constexpr int kMapOps = TS_HIP_MAP_MAX_OPS;
-constexpr int kMapOut = TS_HIP_MAP_MAX_OUTPUTS;
-constexpr int kMapRegs = kMapIn + kMapOps;
+// The interpreter: every field of the program read at run time.
+struct Interp {
+    __device__ static int in_reg(const MapArgsK &a, int j) { return a.vreg[j]; }
+    __device__ static int out_reg(const MapArgsK &a, int o) { return a.p.output_regs[o]; }
+    __device__ static int red_reg(const MapArgsK &a) { return a.p.reduce_reg; }
 
-struct MapArgsK {
-    ts_hip_map_program p;
-    size_t n, n4, tail_start, check_start;
-    unsigned long long *zero_index;
-    bool vec;  // every input and output is 16-byte aligned
-    double *partial;  // reduce: one f64 partial per workgroup
-    // the inputs read per element (not scalar), compacted: pointer and register
-    const float *vin[kMapIn];
-    int vreg[kMapIn];
-};
-
-// The register file of W consecutive elements: one local array per element,
-// passed as a parameter pack so every element's array is named at compile
-// time (a pointer chosen at run time, a 2-D array or arrays wrapped in one
-// struct go to scratch; separate arrays with uniform indices stay in VGPRs,
-// read and written with indexed moves).  C... are the elements' offsets.
-template <size_t... C, class... R>
-__device__ __forceinline__ void run_program(const MapArgsK &a, size_t i0, unsigned long long &zmin,
-                                            std::index_sequence<C...>, R &...r) {
-    constexpr int W = sizeof...(C);
-    const ts_hip_map_program &p = a.p;
-    // The compiler keeps this a loop (each op's fields read from the kernel
-    // arguments, its result written with an indexed move).  Forced unrolled
-    // (a compile-time op index: fields in scalar registers, static
-    // destinations) and with the fields read one op ahead, the config-2
-    // programs both ran 7% slower; unrolled, the kernel's code is ~6x larger.
-#pragma unroll
-    for (int k = 0; k < kMapOps; ++k) {
-        if (k >= static_cast<int>(p.n_ops)) break;
-        const ts_hip_map_op op = p.ops[k];
-        // operands read once, the op's values formed in temporaries, the
-        // register file written once after the switch (writing it in every
-        // case makes the compiler keep several copies of it)
-        const float x[W] = {r[op.a]...};
-        const float y[W] = {r[op.b]...};
-        float v[W];
-        switch (op.code) {
-            case TS_HIP_MAP_ADD: ((v[C] = x[C] + y[C]), ...); break;
-            case TS_HIP_MAP_SUB: ((v[C] = x[C] - y[C]), ...); break;
-            case TS_HIP_MAP_MUL: ((v[C] = x[C] * y[C]), ...); break;
-            case TS_HIP_MAP_DIV: {
-                if ((op.flags & TS_HIP_MAP_CHECKED) && a.zero_index) {
+    // The register file of W consecutive elements: one local array per
+    // element, passed as a parameter pack so every element's array is named
+    // at compile time (a pointer chosen at run time, a 2-D array or arrays
+    // wrapped in one struct go to scratch; separate arrays with uniform
+    // indices stay in VGPRs, read and written with indexed moves).  C... are
+    // the elements' offsets.
+    template <unsigned long... C, class... R>
+    __device__ static __forceinline__ void run(const MapArgsK &a, size_t i0, unsigned long long &zmin, Seq<C...>,
+                                               R &...r) {
+        constexpr int W = sizeof...(C);
+        const ts_hip_map_program &p = a.p;
+        // The compiler keeps this a loop (each op's fields read from the kernel
+        // arguments, its result written with an indexed move).  Forced unrolled
+        // (a compile-time op index: fields in scalar registers, static
+        // destinations) and with the fields read one op ahead, the config-2
+        // programs both ran 7% slower; unrolled, the kernel's code is ~6x larger.
+    #pragma unroll
+        for (int k = 0; k < kMapOps; ++k) {
+            if (k >= static_cast<int>(p.n_ops)) break;
+            const ts_hip_map_op op = p.ops[k];
+            // operands read once, the op's values formed in temporaries, the
+            // register file written once after the switch (writing it in every
+            // case makes the compiler keep several copies of it)
+            const float x[W] = {r[op.a]...};
+            const float y[W] = {r[op.b]...};
+            float v[W];
+            switch (op.code) {
+                case TS_HIP_MAP_ADD: ((v[C] = x[C] + y[C]), ...); break;
+                case TS_HIP_MAP_SUB: ((v[C] = x[C] - y[C]), ...); break;
+                case TS_HIP_MAP_MUL: ((v[C] = x[C] * y[C]), ...); break;
+                case TS_HIP_MAP_DIV: ((v[C] = x[C] / y[C]), ...); break;
+                case kMapDivChecked: {
                     // the first zero divisor this thread sees (reported once, after its loop)
                     auto check = [&](float d, size_t i) {
                         if (i >= a.check_start && d == 0.0f && i < zmin) zmin = i;
                     };
                     (check(y[C], i0 + C), ...);
+                    ((v[C] = x[C] / y[C]), ...);
+                    break;
                 }
-                ((v[C] = x[C] / y[C]), ...);
-                break;
+                case TS_HIP_MAP_NEG:  // core/utils.rs:847-870: 0 - x on the AVX2 body, -x on the tail
+                    ((v[C] = (i0 + C < a.tail_start) ? 0.0f - x[C] : -x[C]), ...);
+                    break;
+                case TS_HIP_MAP_RELU: ((v[C] = x[C] > 0.0f ? x[C] : 0.0f), ...); break;
+                // grad_fn/ops/relu.rs: x > 0 ? go : 0 (a = x, b = go)
+                case TS_HIP_MAP_RELU_BWD: ((v[C] = x[C] > 0.0f ? y[C] : 0.0f), ...); break;
+                case TS_HIP_MAP_ADD_S: ((v[C] = x[C] + op.imm), ...); break;
+                case TS_HIP_MAP_SUB_S: ((v[C] = x[C] - op.imm), ...); break;
+                case TS_HIP_MAP_MUL_S: ((v[C] = x[C] * op.imm), ...); break;
+                case TS_HIP_MAP_DIV_S: ((v[C] = x[C] / op.imm), ...); break;
+                default: ((v[C] = x[C] * x[C]), ...); break;  // TS_HIP_MAP_SQUARE: pow_scalar(2)
             }
-            case TS_HIP_MAP_NEG:  // core/utils.rs:847-870: 0 - x on the AVX2 body, -x on the tail
-                ((v[C] = (i0 + C < a.tail_start) ? 0.0f - x[C] : -x[C]), ...);
-                break;
-            case TS_HIP_MAP_RELU: ((v[C] = x[C] > 0.0f ? x[C] : 0.0f), ...); break;
-            // grad_fn/ops/relu.rs: x > 0 ? go : 0 (a = x, b = go)
-            case TS_HIP_MAP_RELU_BWD: ((v[C] = x[C] > 0.0f ? y[C] : 0.0f), ...); break;
-            case TS_HIP_MAP_ADD_S: ((v[C] = x[C] + op.imm), ...); break;
-            case TS_HIP_MAP_SUB_S: ((v[C] = x[C] - op.imm), ...); break;
-            case TS_HIP_MAP_MUL_S: ((v[C] = x[C] * op.imm), ...); break;
-            case TS_HIP_MAP_DIV_S: ((v[C] = x[C] / op.imm), ...); break;
-            default: ((v[C] = x[C] * x[C]), ...); break;  // TS_HIP_MAP_SQUARE: pow_scalar(2)
-        }
-        const int d = kMapIn + static_cast<int>(k);
-        ((r[d] = v[C]), ...);
-    }
-}
-
-template <size_t... C, class... R>
-__device__ __forceinline__ void load_inputs(const MapArgsK &a, size_t i0, bool vec4, std::index_sequence<C...>,
-                                            R &...r) {
-    const ts_hip_map_program &p = a.p;
-#pragma unroll
-    for (int k = 0; k < kMapIn; ++k) {
-        if (k >= static_cast<int>(p.n_inputs)) break;
-        const float *in = p.inputs[k];
-        if (p.const_inputs & (1u << k)) {
-            ((r[k] = p.const_values[k]), ...);
-        } else if (p.scalar_inputs & (1u << k)) {
-            const float s = in[0];
-            ((r[k] = s), ...);
-        } else if (vec4) {
-            const float4 q = *reinterpret_cast<const float4 *>(in + i0);
-            const float v[4] = {q.x, q.y, q.z, q.w};
-            ((r[k] = v[C]), ...);
-        } else {
-            ((r[k] = in[i0 + C]), ...);
+            const int d = op.d;
+            ((r[d] = v[C]), ...);
         }
     }
-}
+};
 
-template <size_t... C, class... R>
-__device__ __forceinline__ void store_outputs(const MapArgsK &a, size_t i0, bool vec4, std::index_sequence<C...>,
-                                              R &...r) {
-    const ts_hip_map_program &p = a.p;
-#pragma unroll
-    for (int o = 0; o < kMapOut; ++o) {
-        if (o >= static_cast<int>(p.n_outputs)) break;
-        const int q = p.output_regs[o];
-        float *out = p.outputs[o];
-        if (vec4) {
-            // ordinary stores: the value is usually read again soon (a
-            // gradient by the next op, a forward value by its consumer)
-            float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            ((v[C] = r[q]), ...);
-            *reinterpret_cast<float4 *>(out + i0) = make_float4(v[0], v[1], v[2], v[3]);
-        } else {
-            ((out[i0 + C] = r[q]), ...);
-        }
-    }
-}
-
-// Groups of four elements, grid-stride: thread t takes groups t, t + stride,
-// ... (with a reduction the grid and order of ts_hip_sum's first pass: each
-// group's four values added in f64 left to right, then the remainder, so the
-// sum has the bits of ts_hip_sum over the stored values), the next group's
-// inputs loaded before the current group is evaluated, so a wave keeps loads
-// in flight while it computes.
-//
-// map_program_vec: 16-byte aligned operands, NV inputs read per element and NO
-// stored values known at compile time.  Every iteration then issues exactly
-// NV loads and NO stores (the next group's index clamped into range, a
-// division's zero check kept in a register and reported after the loop), so
-// the compiler's load counters are exact: the loop waits only for the next
-// group's loads, never for its own stores to complete.
 template <bool REDUCE, int NV, int NO>
 __global__ __launch_bounds__(kBlock) void map_program_vec(MapArgsK a) {
-    const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
-    const int rq = a.p.reduce_reg;
-    const auto seq = std::make_index_sequence<4>{};
-    double acc = 0.0;
-    unsigned long long zmin = ~0ull;
-    float sv[kMapIn];  // scalar and constant inputs, read once
-#pragma unroll
-    for (int k = 0; k < kMapIn; ++k)
-        sv[k] = k >= static_cast<int>(a.p.n_inputs)           ? 0.0f
-                : (a.p.const_inputs & (1u << k))            ? a.p.const_values[k]
-                : (a.p.scalar_inputs & (1u << k))           ? a.p.inputs[k][0]
-                                                            : 0.0f;
-    f4v_t nx[NV > 0 ? NV : 1];  // the next group's per-element inputs
-    auto fetch = [&](size_t g) {
-#pragma unroll
-        for (int j = 0; j < NV; ++j) nx[j] = *reinterpret_cast<const f4v_t *>(a.vin[j] + 4 * g);
-    };
-    if (t < a.n4) fetch(t);
-    for (size_t g = t; g < a.n4; g += stride) {
-        float r0[kMapRegs], r1[kMapRegs], r2[kMapRegs], r3[kMapRegs];
-#pragma unroll
-        for (int k = 0; k < kMapIn; ++k) {
-            r0[k] = sv[k];
-            r1[k] = sv[k];
-            r2[k] = sv[k];
-            r3[k] = sv[k];
-        }
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const int k = a.vreg[j];
-            r0[k] = nx[j][0];
-            r1[k] = nx[j][1];
-            r2[k] = nx[j][2];
-            r3[k] = nx[j][3];
-        }
-        const size_t gn = g + stride < a.n4 ? g + stride : a.n4 - 1;  // in range: the same loads every step
-        fetch(gn);
-        run_program(a, 4 * g, zmin, seq, r0, r1, r2, r3);
-#pragma unroll
-        for (int o = 0; o < NO; ++o) {
-            const int q = a.p.output_regs[o];
-            f4v_t v;
-            v[0] = r0[q];
-            v[1] = r1[q];
-            v[2] = r2[q];
-            v[3] = r3[q];
-            *reinterpret_cast<f4v_t *>(a.p.outputs[o] + 4 * g) = v;
-        }
-        if (REDUCE) acc += (double)r0[rq] + (double)r1[rq] + (double)r2[rq] + (double)r3[rq];
-    }
-    for (size_t i = 4 * a.n4 + t; i < a.n; i += stride) {
-        float r0[kMapRegs];
-        const auto one = std::make_index_sequence<1>{};
-        load_inputs(a, i, false, one, r0);
-        run_program(a, i, zmin, one, r0);
-        store_outputs(a, i, false, one, r0);
-        if (REDUCE) acc += (double)r0[rq];
-    }
-    if (zmin != ~0ull) atomicMin(a.zero_index, zmin);
-    if (REDUCE) {
-        const double s = block_sum(acc);
-        if (threadIdx.x == 0) a.partial[blockIdx.x] = s;
-    }
+    map_vec_body<REDUCE, NV, NO, Interp>(a);
 }
 
-// Any alignment and counts: the same evaluation with element loads.
 template <bool REDUCE>
 __global__ __launch_bounds__(kBlock) void map_program_kernel(MapArgsK a) {
-    const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-    const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
-    const int rq = a.p.reduce_reg;
-    const auto seq = std::make_index_sequence<4>{};
-    double acc = 0.0;
-    unsigned long long zmin = ~0ull;
-    for (size_t g = t; g < a.n4; g += stride) {
-        float r0[kMapRegs], r1[kMapRegs], r2[kMapRegs], r3[kMapRegs];
-        load_inputs(a, 4 * g, a.vec, seq, r0, r1, r2, r3);
-        run_program(a, 4 * g, zmin, seq, r0, r1, r2, r3);
-        store_outputs(a, 4 * g, a.vec, seq, r0, r1, r2, r3);
-        if (REDUCE) acc += (double)r0[rq] + (double)r1[rq] + (double)r2[rq] + (double)r3[rq];
-    }
-    for (size_t i = 4 * a.n4 + t; i < a.n; i += stride) {
-        float r0[kMapRegs];
-        const auto one = std::make_index_sequence<1>{};
-        load_inputs(a, i, false, one, r0);
-        run_program(a, i, zmin, one, r0);
-        store_outputs(a, i, false, one, r0);
-        if (REDUCE) acc += (double)r0[rq];
-    }
-    if (zmin != ~0ull) atomicMin(a.zero_index, zmin);
-    if (REDUCE) {
-        const double s = block_sum(acc);
-        if (threadIdx.x == 0) a.partial[blockIdx.x] = s;
-    }
+    map_any_body<REDUCE, Interp>(a);
 }
 
 // The launch: the counted form for aligned operands, the general one else.
@@ -283,34 +143,247 @@ static void launch_map(const MapArgsK &a, int nv, dim3 grid, hipStream_t s) {
     }
 }
 
+// ---- programs compiled at run time ----------------------------------------------
+
+// The headers the compiled source includes, as text (generated from the files
+// at build time), and the two C headers hipRTC lacks, as aliases of its own
+// fixed-width types.
+#include "ts_hip_jit_headers.inc"
+
+constexpr char kRtcStdint[] =
+    "#pragma once\n"
+    "typedef __hip_internal::uint8_t uint8_t;\ntypedef __hip_internal::uint16_t uint16_t;\n"
+    "typedef __hip_internal::uint32_t uint32_t;\ntypedef __hip_internal::uint64_t uint64_t;\n"
+    "typedef __hip_internal::int8_t int8_t;\ntypedef __hip_internal::int16_t int16_t;\n"
+    "typedef __hip_internal::int32_t int32_t;\ntypedef __hip_internal::int64_t int64_t;\n"
+    "typedef unsigned long uintptr_t;\n";
+constexpr char kRtcStddef[] = "#pragma once\n";
+
+// The straight-line form of one op, for W elements: the interpreter's formula
+// of its code, with the registers and the op's index fixed.
+static std::string jit_op(const ts_hip_map_op &op, int k) {
+    const std::string a = std::to_string(op.a), b = std::to_string(op.b), d = std::to_string(op.d);
+    const std::string imm = "a.p.ops[" + std::to_string(k) + "].imm";
+    std::string v;
+    switch (op.code) {
+        case TS_HIP_MAP_ADD: v = "((v[C] = x[C] + y[C]), ...);"; break;
+        case TS_HIP_MAP_SUB: v = "((v[C] = x[C] - y[C]), ...);"; break;
+        case TS_HIP_MAP_MUL: v = "((v[C] = x[C] * y[C]), ...);"; break;
+        case TS_HIP_MAP_DIV: v = "((v[C] = x[C] / y[C]), ...);"; break;
+        case kMapDivChecked:
+            v = "auto check = [&](float q, size_t i) { if (i >= a.check_start && q == 0.0f && i < zmin) zmin = i; };\n"
+                "        (check(y[C], i0 + C), ...);\n        ((v[C] = x[C] / y[C]), ...);";
+            break;
+        case TS_HIP_MAP_NEG: v = "((v[C] = (i0 + C < a.tail_start) ? 0.0f - x[C] : -x[C]), ...);"; break;
+        case TS_HIP_MAP_RELU: v = "((v[C] = x[C] > 0.0f ? x[C] : 0.0f), ...);"; break;
+        case TS_HIP_MAP_RELU_BWD: v = "((v[C] = x[C] > 0.0f ? y[C] : 0.0f), ...);"; break;
+        case TS_HIP_MAP_ADD_S: v = "((v[C] = x[C] + " + imm + "), ...);"; break;
+        case TS_HIP_MAP_SUB_S: v = "((v[C] = x[C] - " + imm + "), ...);"; break;
+        case TS_HIP_MAP_MUL_S: v = "((v[C] = x[C] * " + imm + "), ...);"; break;
+        case TS_HIP_MAP_DIV_S: v = "((v[C] = x[C] / " + imm + "), ...);"; break;
+        default: v = "((v[C] = x[C] * x[C]), ...);"; break;  // TS_HIP_MAP_SQUARE
+    }
+    return "    {  // op " + std::to_string(k) + "\n        const float x[W] = {r[" + a + "]...};\n" +
+           "        const float y[W] = {r[" + b + "]...};\n        float v[W];\n        " + v +
+           "\n        ((r[" + d + "] = v[C]), ...);\n    }\n";
+}
+
+// A register table as a constant expression of its index: j == 0 ? r0 : ...
+static std::string jit_table(const int *regs, int count) {
+    std::string s;
+    for (int i = 0; i + 1 < count; ++i) s += "j == " + std::to_string(i) + " ? " + std::to_string(regs[i]) + " : ";
+    return s + std::to_string(count > 0 ? regs[count - 1] : 0);
+}
+
+// The source of the compiled form of a's program (aligned operands; NV
+// inputs read per element, NO stored values, a reduction or not).
+static std::string jit_source(const MapArgsK &a, bool reduce, int nv, int no) {
+    int outs[kMapOut];
+    for (int o = 0; o < kMapOut; ++o) outs[o] = o < no ? a.p.output_regs[o] : 0;
+    std::string s =
+        "#include \"ts_hip_map_body.h\"\n"
+        "namespace tship {\n"
+        "struct Compiled {\n"
+        "    __device__ static constexpr int in_reg(const MapArgsK &, int j) { return " + jit_table(a.vreg, nv) + "; }\n"
+        "    __device__ static constexpr int out_reg(const MapArgsK &, int j) { return " + jit_table(outs, no) + "; }\n"
+        "    __device__ static constexpr int red_reg(const MapArgsK &) { return " +
+        std::to_string(reduce ? a.p.reduce_reg : 0) + "; }\n"
+        "    template <unsigned long... C, class... R>\n"
+        "    __device__ static __forceinline__ void run(const MapArgsK &a, size_t i0, unsigned long long &zmin,\n"
+        "                                               Seq<C...>, R &...r) {\n"
+        "    constexpr int W = sizeof...(C);\n";
+    for (uint32_t k = 0; k < a.p.n_ops; ++k) s += jit_op(a.p.ops[k], static_cast<int>(k));
+    s += "    (void)a; (void)i0; (void)zmin;\n    }\n};\n}  // namespace tship\n"
+         "extern \"C\" __global__ __launch_bounds__(256) void ts_hip_map_compiled(tship::MapArgsK a) {\n"
+         "    tship::map_vec_body<" + std::string(reduce ? "true" : "false") + ", " + std::to_string(nv) + ", " +
+         std::to_string(no) + ", tship::Compiled>(a);\n}\n";
+    return s;
+}
+
+// hipRTC options: the library's own numerics (no contraction, IEEE division
+// and square root, denormals kept, no packed fp32 instructions).
+static const char *const kRtcOptions[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
+                                          "-fhip-fp32-correctly-rounded-divide-sqrt",
+                                          "-fno-gpu-flush-denormals-to-zero", "-Xclang", "-target-feature",
+                                          "-Xclang", "-packed-fp32-ops"};
+
+// A compiled program's code object, or empty with the compiler's log in *log.
+static std::vector<char> jit_compile(const std::string &src, std::string *log) {
+    const char *headers[] = {kJitHeaderTsHip, kJitHeaderDeviceCommon, kJitHeaderMapBody, kRtcStdint, kRtcStddef};
+    const char *names[] = {"ts_hip.h", "ts_hip_device_common.h", "ts_hip_map_body.h", "stdint.h", "stddef.h"};
+    hiprtcProgram prog;
+    std::vector<char> code;
+    if (hiprtcCreateProgram(&prog, src.c_str(), "ts_hip_map_compiled.hip", 5, headers, names) != HIPRTC_SUCCESS) {
+        *log = "hiprtcCreateProgram failed";
+        return code;
+    }
+    const int nopt = static_cast<int>(sizeof(kRtcOptions) / sizeof(kRtcOptions[0]));
+    if (hiprtcCompileProgram(prog, nopt, kRtcOptions) == HIPRTC_SUCCESS) {
+        size_t size = 0;
+        if (hiprtcGetCodeSize(prog, &size) == HIPRTC_SUCCESS && size > 0) {
+            code.resize(size);
+            if (hiprtcGetCode(prog, code.data()) != HIPRTC_SUCCESS) code.clear();
+        }
+    } else {
+        size_t size = 0;
+        hiprtcGetProgramLogSize(prog, &size);
+        log->assign(size, '\0');
+        if (size) hiprtcGetProgramLog(prog, &(*log)[0]);
+    }
+    hiprtcDestroyProgram(&prog);
+    return code;
+}
+
+struct JitEntry {
+    int uses = 0;
+    bool tried = false;
+    hipModule_t module = nullptr;
+    hipFunction_t function = nullptr;  // null: not compiled (yet, or it failed)
+};
+
+static std::mutex g_jit_mutex;
+static std::unordered_map<std::string, JitEntry> g_jit;  // by device and program shape
+static std::atomic<int> g_jit_mode{1};
+static std::atomic<size_t> g_jit_compiled{0}, g_jit_failed{0};
+static std::string g_jit_log;  // the last failure's compiler log
+
+// The program shape the compiled form depends on: everything but the
+// pointers, the constants' values and the immediates (read at run time).
+static std::string jit_key(int device, const MapArgsK &a, bool reduce, int nv, int no) {
+    std::string k;
+    auto put = [&](unsigned v) { k.push_back(static_cast<char>(v & 0xffu)); };
+    put(static_cast<unsigned>(device));
+    put(reduce);
+    put(static_cast<unsigned>(nv));
+    put(static_cast<unsigned>(no));
+    put(a.p.n_inputs);
+    put(a.p.scalar_inputs);
+    put(a.p.const_inputs);
+    put(static_cast<unsigned>(reduce ? a.p.reduce_reg : 0));
+    for (int j = 0; j < nv; ++j) put(static_cast<unsigned>(a.vreg[j]));
+    for (int o = 0; o < no; ++o) put(a.p.output_regs[o]);
+    for (uint32_t i = 0; i < a.p.n_ops; ++i) {
+        put(a.p.ops[i].code);
+        put(a.p.ops[i].a);
+        put(a.p.ops[i].b);
+        put(a.p.ops[i].d);
+    }
+    return k;
+}
+
+// The compiled kernel for a's program, compiling it on its second use (mode
+// 1) or first (mode 2); null: run the interpreter.
+static hipFunction_t jit_function(const MapArgsK &a, bool reduce, int nv, int no) {
+    const int mode = g_jit_mode.load(std::memory_order_relaxed);
+    if (mode == 0 || !a.vec) return nullptr;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lock(g_jit_mutex);
+    JitEntry &c = g_jit[jit_key(device, a, reduce, nv, no)];
+    ++c.uses;
+    if (!c.tried && c.uses >= (mode == 2 ? 1 : 2)) {
+        c.tried = true;
+        std::string log;
+        const std::vector<char> code = jit_compile(jit_source(a, reduce, nv, no), &log);
+        if (!code.empty() && hipModuleLoadData(&c.module, code.data()) == hipSuccess &&
+            hipModuleGetFunction(&c.function, c.module, "ts_hip_map_compiled") == hipSuccess) {
+            g_jit_compiled.fetch_add(1);
+        } else {
+            (void)hipGetLastError();
+            c.function = nullptr;
+            g_jit_failed.fetch_add(1);
+            g_jit_log = log.empty() ? "code object load failed" : log;
+        }
+    }
+    return c.function;
+}
+
+// The program is well formed: counts within the limits, known op codes, every
+// register read written first (by the inputs, or by an earlier op), something
+// stored or summed, and every stored or summed register written.
+static bool program_ok(const ts_hip_map_program &p, bool reduce) {
+    if (p.n_inputs > kMapIn || p.n_ops > kMapOps || p.n_outputs > kMapOut) return false;
+    uint32_t written = (1u << p.n_inputs) - 1u;
+    auto holds_value = [&](int r) { return r >= 0 && r < kMapRegs && ((written >> r) & 1u); };
+    for (uint32_t k = 0; k < p.n_ops; ++k) {
+        const ts_hip_map_op &op = p.ops[k];
+        if (!holds_value(op.a) || !holds_value(op.b) || op.d >= kMapRegs || op.code > TS_HIP_MAP_SQUARE) return false;
+        written |= 1u << op.d;
+    }
+    if (reduce ? !holds_value(p.reduce_reg) : p.n_outputs == 0) return false;
+    for (uint32_t o = 0; o < p.n_outputs; ++o)
+        if (!holds_value(p.output_regs[o])) return false;
+    return true;
+}
+
 }  // namespace tship
 
 using namespace tship;
+
+extern "C" int ts_hip_map_jit_mode(int mode) {
+    if (mode < 0 || mode > 2) return -1;
+    return g_jit_mode.exchange(mode);
+}
+
+extern "C" int ts_hip_map_jit_stats(size_t *compiled, size_t *failed) {
+    if (compiled) *compiled = g_jit_compiled.load();
+    if (failed) *failed = g_jit_failed.load();
+    return TS_HIP_OK;
+}
+
+extern "C" const char *ts_hip_map_jit_log(void) {
+    std::lock_guard<std::mutex> lock(g_jit_mutex);
+    return g_jit_log.c_str();
+}
+
+extern "C" size_t ts_hip_map_jit_source(const ts_hip_map_program *prog, int reduce, char *buf, size_t cap) {
+    if (!prog || !program_ok(*prog, reduce != 0)) return 0;
+    MapArgsK a{};
+    a.p = *prog;
+    for (uint32_t k = 0; k < a.p.n_ops; ++k)
+        if (a.p.ops[k].code == TS_HIP_MAP_DIV && (a.p.ops[k].flags & TS_HIP_MAP_CHECKED)) a.p.ops[k].code = kMapDivChecked;
+    int nv = 0;
+    for (uint32_t k = 0; k < a.p.n_inputs; ++k)
+        if (!((a.p.scalar_inputs | a.p.const_inputs) & (1u << k))) a.vreg[nv++] = static_cast<int>(k);
+    const std::string s = jit_source(a, reduce != 0, nv, static_cast<int>(a.p.n_outputs));
+    if (buf && cap) {
+        const size_t m = s.size() < cap - 1 ? s.size() : cap - 1;
+        s.copy(buf, m);
+        buf[m] = '\0';
+    }
+    return s.size() + 1;
+}
 
 extern "C" size_t ts_hip_map_workspace_floats(size_t n) { return 2 * sum_blocks(n); }
 
 extern "C" int ts_hip_map(const ts_hip_map_program *prog, size_t n, size_t tail_start, size_t zero_check_start,
                           unsigned long long *zero_index, float *sum_out, int mean, float *workspace,
                           size_t workspace_floats, void *stream) {
-    if (!prog) return TS_HIP_EINVAL;
+    if (!prog || !program_ok(*prog, sum_out != nullptr)) return TS_HIP_EINVAL;
     const ts_hip_map_program &p = *prog;
-    if (p.n_inputs > kMapIn || p.n_ops > kMapOps || p.n_outputs > kMapOut) return TS_HIP_EINVAL;
     const bool reduce = sum_out != nullptr;
-    auto holds_value = [&](int r) {  // an input's register or a computed op's
-        return (r >= 0 && r < static_cast<int>(p.n_inputs)) || (r >= kMapIn && r < kMapIn + static_cast<int>(p.n_ops));
-    };
-    if (reduce && !holds_value(p.reduce_reg)) return TS_HIP_EINVAL;
-    if (!reduce && p.n_outputs == 0) return TS_HIP_EINVAL;
-    // every register read must be an input or an earlier op's value
-    for (uint32_t k = 0; k < p.n_ops; ++k) {
-        const ts_hip_map_op &op = p.ops[k];
-        auto ok = [&](int r) { return r < static_cast<int>(p.n_inputs) || (r >= kMapIn && r < kMapIn + static_cast<int>(k)); };
-        if (!ok(op.a) || !ok(op.b) || op.code > TS_HIP_MAP_SQUARE) return TS_HIP_EINVAL;
-    }
-    for (uint32_t o = 0; o < p.n_outputs; ++o) {
-        const int q = p.output_regs[o];
-        if (!p.outputs[o] || !holds_value(q)) return TS_HIP_EINVAL;
-    }
+    for (uint32_t o = 0; o < p.n_outputs; ++o)
+        if (!p.outputs[o]) return TS_HIP_EINVAL;
     // per-element inputs: neither scalar nor constant
     const uint32_t one_value = p.scalar_inputs | p.const_inputs;
     bool vec = true;
@@ -323,6 +396,9 @@ extern "C" int ts_hip_map(const ts_hip_map_program *prog, size_t n, size_t tail_
     if (n == 0) return reduce ? ts_hip_fill(sum_out, 0.0f, 1, stream) : TS_HIP_OK;
     MapArgsK a{};
     a.p = p;
+    for (uint32_t k = 0; k < p.n_ops; ++k)
+        if (p.ops[k].code == TS_HIP_MAP_DIV && (p.ops[k].flags & TS_HIP_MAP_CHECKED) && zero_index)
+            a.p.ops[k].code = kMapDivChecked;
     a.n = n;
     // the group structure is n / 4 whatever the alignment (loads and stores
     // fall back to single elements), so a fused sum keeps ts_hip_sum's order
@@ -338,22 +414,33 @@ extern "C" int ts_hip_map(const ts_hip_map_program *prog, size_t n, size_t tail_
             a.vreg[nv] = static_cast<int>(k);
             ++nv;
         }
+    unsigned blocks;
     if (!reduce) {
         const size_t rest = n - 4 * a.n4;
         const size_t threads = a.n4 > rest ? a.n4 : rest;
         // a group per thread up to 16 workgroups per CU, then several per
         // thread (the prefetch overlaps them): a small program is one short
         // round of loads, not a chain of them
-        const unsigned blocks = grid_for(threads, 1);
-        launch_map<false>(a, nv, dim3(blocks), s);
-        return launch_status();
+        blocks = grid_for(threads, 1);
+    } else {
+        blocks = static_cast<unsigned>(sum_blocks(n));
+        if (!workspace || workspace_floats < 2 * static_cast<size_t>(blocks)) return TS_HIP_EWORKSPACE;
+        if ((reinterpret_cast<uintptr_t>(workspace) & 7u) != 0) return TS_HIP_EINVAL;
+        a.partial = reinterpret_cast<double *>(workspace);
     }
-    const size_t blocks = sum_blocks(n);
-    if (!workspace || workspace_floats < 2 * blocks) return TS_HIP_EWORKSPACE;
-    if ((reinterpret_cast<uintptr_t>(workspace) & 7u) != 0) return TS_HIP_EINVAL;
-    a.partial = reinterpret_cast<double *>(workspace);
-    launch_map<true>(a, nv, dim3(static_cast<unsigned>(blocks)), s);
+    if (hipFunction_t f = jit_function(a, reduce, nv, static_cast<int>(p.n_outputs))) {
+        void *params[] = {&a};
+        const hipError_t e = launch_module(f, blocks, kBlock, s, params);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return static_cast<int>(e);
+        }
+    } else if (reduce) {
+        launch_map<true>(a, nv, dim3(blocks), s);
+    } else {
+        launch_map<false>(a, nv, dim3(blocks), s);
+    }
     const int st = launch_status();
-    if (st != TS_HIP_OK) return st;
+    if (st != TS_HIP_OK || !reduce) return st;
     return launch_sum_final(a.partial, blocks, n, sum_out, mean != 0, s);
 }
