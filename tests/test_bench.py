@@ -42,9 +42,11 @@ def test_gemm_flops_per_step_are_the_closed_forms():
 
 
 def test_bandwidth_work_per_unit():
-    # forward add/mul/div/sub 12 B each, relu 8, sum 4; backward fill 4, relu mask 12,
-    # neg 8, div 20, mul 20, two accumulations 12 + 12
-    assert bench.CHAIN_BYTES_PER_ELEM == 4 * 12 + 8 + 4 + 4 + 12 + 8 + 20 + 20 + 12 + 12
+    # config 2's fused floor: a, b, c read once, ga, gb, gc written once (the
+    # reference's op-by-op sequence moves 148: forward add/mul/div/sub 12 B each,
+    # relu 8, sum 4; backward fill 4, relu mask 12, neg 8, div 20, mul 20, two
+    # accumulations 12 + 12)
+    assert bench.CHAIN_BYTES_PER_ELEM == 3 * 4 + 3 * 4
     assert bench.ADAM_BYTES_PER_PARAM == 4 * 4 + 3 * 4
 
 
