@@ -474,6 +474,23 @@ int ts_hip_gemm_colsum_xf(int trans_a, size_t M, size_t N, size_t K, const float
                           float *C, size_t ldc, float *colsum, float *workspace, size_t workspace_floats,
                           void *stream);
 
+/* ts_hip_gemm_colsum_xf with ldb == N that also adds up B as stored (before
+ * xb) in the same launch (no counterpart in the reference, which sums the
+ * loss in a pass of its own, reductions/sum.rs:80-141 and
+ * reductions/mean.rs:48-109, before its backward reads the same values: the
+ * README step's relu(x W + b).sum(), README.md:71-79, whose weight gradient
+ * reads relu's output through relu's backward):
+ *   bsum[0] = the sum of B's K*N values, divided by (float)(K*N) when mean,
+ * with the bits of ts_hip_sum / ts_hip_mean(B, K*N), from one workgroup
+ * appended to the product's grid.  Only where ts_hip_gemm_takes_bsum accepts
+ * (trans_a == 1; the products whose column sums come from the register-staged
+ * tiles' own launch, with no workspace; K*N <= 16384), with B 16-byte
+ * aligned; TS_HIP_EINVAL otherwise.  Allocates nothing. */
+int ts_hip_gemm_takes_bsum(int trans_a, size_t M, size_t N, size_t K);
+int ts_hip_gemm_colsum_bsum(int trans_a, size_t M, size_t N, size_t K, const float *A, size_t lda,
+                            const ts_hip_operand_xf *xa, const float *B, const ts_hip_operand_xf *xb, float *C,
+                            size_t ldc, float *colsum, float *bsum, int mean, void *stream);
+
 /* Batched C[b] = op(A[b]) . op(B[b]) (matmul/mod.rs:634-760 batched_matmul and
  * the batched backward of grad_fn/ops/matmul.rs:150-219) on the same MFMA
  * tiles: a batch grid of batch_rank axes (<= 6) with sizes batch_dims; the A /

@@ -4,8 +4,8 @@ roofline divides by, and the CPU-baseline record (nothing here touches a GPU).
 The work figures are closed forms of the configurations: 17 products of
 2*8192*4096*4096 FLOP for config 5 (6 forward, 6 dW, 5 dX: the input needs no
 gradient), 3.351 GFLOP for config 4 and 12.85 MFLOP for config 1 (forward and
-dW only), 148 bytes per element for the config-2 chain and 28 per parameter
-for Adam (read p, g, m, v; write p, m, v).
+dW only), 24 bytes per element for the config-2 chain (its fused floor) and
+28 per parameter for Adam (read p, g, m, v; write p, m, v).
 """
 from __future__ import annotations
 
@@ -69,7 +69,11 @@ def test_traffic_from_the_committed_counters():
     assert abs(traffic / (28 * 2 ** 28) - 1.0) < 0.01
     traffic, src = bench.pmc_traffic("c5")
     assert src == "profiles/c5_gemm_pmc.md" and traffic > 0
-    assert bench.pmc_traffic("c2") == (None, None)
+    # config 2: the one compiled pass per step moves the fused floor, 24 B
+    # per element of 2^26
+    traffic, src = bench.pmc_traffic("c2")
+    assert src == "profiles/c2_map_pmc.md"
+    assert abs(traffic / (24 * 2 ** 26) - 1.0) < 0.01
 
 
 def test_a_default_run_covers_every_baseline_config():

@@ -401,6 +401,17 @@ int gemm2d_xf(int ta, int tb, size_t M, size_t N, size_t K, const float *A, size
                                 work ? work->get() : nullptr, ws, S());
 }
 
+std::vector<std::weak_ptr<Allocation>> &pending_reduces();
+
+// A deferred sum / mean of all n values of x still to be formed, or null.
+std::shared_ptr<Allocation> pending_sum_of(const Allocation *x, size_t n) {
+    for (auto &w : pending_reduces()) {
+        auto o = w.lock();
+        if (o && o->reduce && o->reduce->x.get() == x && o->reduce->n == n) return o;
+    }
+    return nullptr;
+}
+
 void launch_product(const PendingGemm &p, float *C, bool with_epilogue) {
     // an operand that is a deferred chain over one buffer is read as that
     // buffer, the chain applied as it is loaded
@@ -1504,9 +1515,19 @@ void fused_sum(const std::shared_ptr<Allocation> &x, float *out, bool mean) {
     launch_program(b, outs, r, out, mean);
 }
 
-// sum / mean of a deferred elementwise value, deferred in turn (x is the
-// summed tensor's allocation); out reads x, so an in-place write of x's
-// buffer runs it first
+// Whether a sum of all n values of a, a deferred product, is deferred too:
+// a weight-gradient product that reads a as its right operand (the README
+// step's dW reads relu's output through relu's backward) then forms it in
+// its own launch (ts_hip_gemm_colsum_bsum); otherwise it runs when read,
+// with the same bits.  Only sums one workgroup covers.
+bool sum_fits_product(const Allocation &a, size_t n) {
+    constexpr size_t kOneWorkgroupSum = 16 * 1024;  // ts_hip_gemm_takes_bsum's limit
+    return a.pending && !a.pending->src && n == a.pending->M * a.pending->N && n <= kOneWorkgroupSum;
+}
+
+// sum / mean of a deferred elementwise value or product, deferred in turn (x
+// is the summed tensor's allocation); out reads x, so an in-place write of
+// x's buffer runs it first
 Tensor deferred_reduce(const std::shared_ptr<Allocation> &x, size_t n, bool mean) {
     Tensor out = Tensor::new_uninit({1});
     auto r = std::make_shared<PendingReduce>();
@@ -1540,7 +1561,7 @@ void materialize_reduce(Allocation &a) {
 
 Tensor Tensor::sum() const {
     Tensor out;
-    if (alloc_ && alloc_->map && fusion_enabled()) {
+    if (alloc_ && (alloc_->map || sum_fits_product(*alloc_, size_)) && fusion_enabled()) {
         out = deferred_reduce(alloc_, size_, false);
     } else {
         out = new_uninit({1});
@@ -1559,7 +1580,7 @@ Tensor Tensor::sum() const {
 
 Tensor Tensor::mean() const {
     Tensor out;
-    if (alloc_ && alloc_->map && fusion_enabled()) {
+    if (alloc_ && (alloc_->map || sum_fits_product(*alloc_, size_)) && fusion_enabled()) {
         out = deferred_reduce(alloc_, size_, true);
     } else {
         out = new_uninit({1});
@@ -1962,7 +1983,24 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
                     const bool fx = ts_hip_gemm_takes_xf(ta, 0, Kd, N, M, db ? 1 : 0) &&
                                     operand_xf(go.allocation(), leaf, xb);
                     const float *A = va.buf ? va.buf->get() : nullptr;
-                    if (db) {
+                    // a deferred sum of the buffer read as B (the README step's
+                    // loss, over relu's output) comes out of this launch too
+                    const std::shared_ptr<Allocation> bsum =
+                        db && ts_hip_gemm_takes_bsum(ta, Kd, N, M)
+                            ? pending_sum_of(fx ? leaf.get() : go.allocation().get(), M * N)
+                            : nullptr;
+                    if (bsum) {
+                        db->colsum.reset();
+                        const float *B = fx ? leaf->get() : go.dev();
+                        float *C = t.dev_mut();
+                        float *sum = bsum->raw();
+                        DevicePool::get().note_use(sum);
+                        launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm_colsum_bsum(dW, db, loss)", [&] {
+                            return ts_hip_gemm_colsum_bsum(ta, Kd, N, M, A, lda, nullptr, B, fx ? &xb : nullptr, C, N,
+                                                           db->raw(), sum, bsum->reduce->mean ? 1 : 0, S());
+                        });
+                        bsum->reduce.reset();
+                    } else if (db) {
                         db->colsum.reset();
                         const float *B = fx ? leaf->get() : go.dev();
                         float *C = t.dev_mut();

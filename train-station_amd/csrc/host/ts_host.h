@@ -202,11 +202,13 @@ struct PendingTranspose {
     bool view = true;
 };
 
-// A deferred sum or mean of a deferred elementwise value x (reductions/
-// sum.rs:80-141, mean.rs:48-109): out[0] = sum(x), divided by (float)n for
-// the mean, with the bits of ts_hip_sum / ts_hip_mean over x's values.  The
-// first pass that reads x's inputs anyway adds x up as its reduction (backward
-// of the loss usually is that pass); otherwise it runs when out is read.
+// A deferred sum or mean of a deferred elementwise value or product x
+// (reductions/sum.rs:80-141, mean.rs:48-109): out[0] = sum(x), divided by
+// (float)n for the mean, with the bits of ts_hip_sum / ts_hip_mean over x's
+// values.  The first pass that reads x's inputs anyway adds x up as its
+// reduction (backward of the loss usually is that pass), and a weight-gradient
+// product that reads x as its right operand can add it up in its own launch
+// (ts_hip_gemm_colsum_bsum); otherwise it runs when out is read.
 struct PendingReduce {
     std::shared_ptr<Allocation> x;
     size_t n = 0;

@@ -175,6 +175,15 @@ struct GemmArgs {
     // operand transforms (register-staged tiles, the narrow and one-k-tile
     // kernels and the column strips apply them; the others take none)
     OperandXf xa, xb;
+    // The sum (mean: / (float)sum_n) of sum_n floats at sum_x into
+    // sum_out[0], with the bits of ts_hip_sum: one workgroup appended after
+    // the column strips runs sum_small_body over sum_blocks first-pass
+    // workgroups (register-staged tiles with column sums only; the caller
+    // passes B as stored).  Null sum_out: none.
+    const float *sum_x;
+    float *sum_out;
+    size_t sum_n;
+    int sum_mean, sum_blocks;
 };
 
 // Store of a wave's FM x FN accumulator blocks, the wave tile's corner at
@@ -407,8 +416,16 @@ template <bool TA, bool TB, int BM, int BN, int WM, int WN, int EPI, int PF, boo
           bool XF = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
     static_assert(!CS || !TB, "column sums of B need trans_b == 0");
+    static_assert(64 * WM * WN >= kBlock, "the appended sum takes a workgroup of at least kBlock threads");
     if (CS && static_cast<int>(blockIdx.x) >= g.tiles) {  // uniform
-        colsum_strip<64 * WM * WN, XF>(g, (static_cast<int>(blockIdx.x) - g.tiles) * kStripCols);
+        const int j0 = (static_cast<int>(blockIdx.x) - g.tiles) * kStripCols;
+        if (j0 < g.N) {
+            colsum_strip<64 * WM * WN, XF>(g, j0);
+        } else if (g.sum_mean) {  // the workgroup after the strips: GemmArgs::sum_out
+            sum_small_body<false, true>(g.sum_x, nullptr, g.sum_n, g.sum_n / 4, g.sum_blocks, g.sum_out);
+        } else {
+            sum_small_body<false, false>(g.sum_x, nullptr, g.sum_n, g.sum_n / 4, g.sum_blocks, g.sum_out);
+        }
         return;
     }
     constexpr int NT = 64 * WM * WN;
@@ -590,8 +607,12 @@ static void launch_tiles(int ta, int tb, GemmArgs g, hipStream_t s, unsigned bat
     g.tiles_n = (g.N + BN - 1) / BN;
     g.tiles = g.tiles_m * g.tiles_n;
     dim3 grid(static_cast<unsigned>(g.tiles) * batches);
-    // column sums (2-D dW with db): a strip workgroup per 16 columns after the tiles
-    if (g.colsum && ta && !tb) grid.x += static_cast<unsigned>((g.N + kStripCols - 1) / kStripCols);
+    // column sums (2-D dW with db): a strip workgroup per 16 columns after the
+    // tiles, and one for the sum of B after them
+    if (g.colsum && ta && !tb) {
+        grid.x += static_cast<unsigned>((g.N + kStripCols - 1) / kStripCols);
+        if (g.sum_out) grid.x += 1;
+    }
     dim3 block(64 * WM * WN);
     if (g.bias || g.mask || g.relu) launch_tiles_as<BM, BN, WM, WN, kEpiAll>(ta, tb, g, grid, block, s);
     else launch_tiles_as<BM, BN, WM, WN, kEpiNone>(ta, tb, g, grid, block, s);
@@ -1805,6 +1826,36 @@ extern "C" int ts_hip_gemm_colsum(int trans_a, size_t M, size_t N, size_t K, con
     }
     return gemm_plain(trans_a, 0, M, N, K, A, lda, B, ldb, C, ldc, nullptr, nullptr, 0, colsum, workspace,
                       workspace_floats, stream);
+}
+
+extern "C" int ts_hip_gemm_takes_bsum(int trans_a, size_t M, size_t N, size_t K) {
+    if (!trans_a || M == 0 || N == 0 || K == 0) return 0;
+    const GemmPlan p = gemm_plan(1, 0, M, N, K, true);
+    // the register-staged tiles with their column strips (one pass, no
+    // temporary), and a B that one workgroup's sum covers
+    const bool strips = !p.narrow && !p.skinny && p.slices == 1 && p.cs_kernel && !big_grid(M, N, 1) && p.total() == 0;
+    const size_t n = K * N;
+    return strips && n / K == N && sum_blocks(n) <= static_cast<size_t>(small_blocks<false>()) ? 1 : 0;
+}
+
+extern "C" int ts_hip_gemm_colsum_bsum(int trans_a, size_t M, size_t N, size_t K, const float *A, size_t lda,
+                                       const ts_hip_operand_xf *xa, const float *B, const ts_hip_operand_xf *xb,
+                                       float *C, size_t ldc, float *colsum, float *bsum, int mean, void *stream) {
+    if (!ts_hip_gemm_takes_bsum(trans_a, M, N, K) || !A || !B || !C || !colsum || !bsum || ldc < N)
+        return TS_HIP_EINVAL;
+    if (!aligned16(B) && K * N >= 4) return TS_HIP_EINVAL;  // the sum's float4 loads
+    OperandXf fa, fb;
+    if (!xf_from(xa, fa) || !xf_from(xb, fb)) return TS_HIP_EINVAL;
+    GemmArgs g{};
+    g.xa = fa;
+    g.xb = fb;
+    g.colsum = colsum;
+    g.sum_x = B;  // as stored: the transform applies to the product's loads only
+    g.sum_out = bsum;
+    g.sum_n = K * N;
+    g.sum_mean = mean != 0;
+    g.sum_blocks = static_cast<int>(sum_blocks(K * N));
+    return gemm_launch(1, 0, M, N, K, A, lda, B, N, C, ldc, g, 1, stream);
 }
 
 extern "C" int ts_hip_gemm_takes_xf(int trans_a, int trans_b, size_t M, size_t N, size_t K, int colsum) {

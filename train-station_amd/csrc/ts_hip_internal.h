@@ -92,6 +92,97 @@ inline size_t sum_blocks(size_t n) {
     return b < 1 ? 1 : b;
 }
 
+// Both passes of the sum in one workgroup, for at most small_blocks<PROD>()
+// first-pass workgroups and the float4 path (n4 == n / 4): the operations,
+// and so the bits, of the first pass's workgroups and the second pass.  With
+// that few workgroups the grid stride covers every float4 group, so virtual
+// thread (b, t) of first-pass workgroup b has at most one group and one tail
+// element; thread t holds them for every b (all loads in flight at once),
+// each b's wave sums are formed as block_sum forms them and added in wave
+// order from +0 (a partial), and thread t then adds partials t, t + 256, ...
+// from +0 as the second pass's threads do, combined as block_sum combines
+// them.  Run by every thread of a workgroup of at least kBlock threads: the
+// threads past kBlock take no values but reach the barriers.  out[0] is
+// written by thread 0.  Used by ts_hip_sum's one-launch path and by the
+// narrow product kernel, which adds up its own output with it.
+constexpr int kSumSmallBlocks = 16;
+// a product's two operands take twice the registers: half as many workgroups
+template <bool PROD>
+constexpr int small_blocks() { return PROD ? kSumSmallBlocks / 2 : kSumSmallBlocks; }
+
+template <bool PROD, bool MEAN>
+__device__ __forceinline__ void sum_small_body(const float *x, const float *y, size_t n, size_t n4, int blocks,
+                                               float *out) {
+    constexpr int NB = small_blocks<PROD>();
+    constexpr int kWaves = kBlock / 64;
+    __shared__ double wsum[NB][kWaves];
+    __shared__ double parts[NB];
+    __shared__ double fin[kWaves];
+    const int t = static_cast<int>(threadIdx.x), lane = t & 63, wave = t >> 6;
+    if (wave < kWaves) {  // uniform per wave
+        // every load issued before any is used (a load consumed in its own
+        // conditional block is waited for there, one latency per block):
+        // addresses clamped into the input, values past it not added.  The
+        // tail (n - 4*n4 < 4 elements) falls to threads 0..2 of block 0.
+        const size_t ti = 4 * n4 + t < n ? 4 * n4 + t : n - 1;
+        const float tx = x[ti], ty = PROD ? y[ti] : 0.0f;
+        float4 q[NB], qy[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            q[b] = qy[b] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (b < blocks && n4 > 0) {  // uniform
+                const size_t v = static_cast<size_t>(b) * kBlock + t;
+                const size_t vc = v < n4 ? v : n4 - 1;
+                q[b] = reinterpret_cast<const float4 *>(x)[vc];
+                if (PROD) qy[b] = reinterpret_cast<const float4 *>(y)[vc];
+            }
+        }
+        double acc[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            acc[b] = 0.0;
+            const size_t v = static_cast<size_t>(b) * kBlock + t;
+            if (b < blocks && v < n4) {
+                if (PROD)
+                    acc[b] += (double)q[b].x * (double)qy[b].x + (double)q[b].y * (double)qy[b].y +
+                              (double)q[b].z * (double)qy[b].z + (double)q[b].w * (double)qy[b].w;
+                else
+                    acc[b] += (double)q[b].x + (double)q[b].y + (double)q[b].z + (double)q[b].w;
+            }
+        }
+        if (4 * n4 + t < n) acc[0] += PROD ? (double)tx * (double)ty : (double)tx;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            if (b < blocks) {  // uniform
+                const double s = wave_sum(acc[b]);
+                if (lane == 0) wsum[b][wave] = s;
+            }
+        }
+    }
+    __syncthreads();
+    if (t < blocks) {
+        double r = 0.0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) r += wsum[t][w];
+        parts[t] = r;
+    }
+    __syncthreads();
+    if (wave < kWaves) {  // block_sum over the first kBlock threads
+        double a = 0.0;
+        if (t < blocks) a += parts[t];
+        a = wave_sum(a);
+        if (lane == 0) fin[wave] = a;
+    }
+    __syncthreads();
+    if (t == 0) {
+        double r = 0.0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) r += fin[w];
+        const float s = static_cast<float>(r);
+        out[0] = MEAN ? s / static_cast<float>(n) : s;
+    }
+}
+
 // The sum's second pass: one workgroup adds the nparts f64 partials in a fixed
 // order and writes the fp32 sum (divided by (float)n when mean) to out[0].
 int launch_sum_final(const double *partial, size_t nparts, size_t n, float *out, bool mean, hipStream_t s);
