@@ -104,7 +104,7 @@ inline size_t sum_blocks(size_t n) {
 // them.  Run by every thread of a workgroup of at least kBlock threads: the
 // threads past kBlock take no values but reach the barriers.  out[0] is
 // written by thread 0.  Used by ts_hip_sum's one-launch path and by the
-// narrow product kernel, which adds up its own output with it.
+// workgroup a weight-gradient product appends to add up its B operand.
 constexpr int kSumSmallBlocks = 16;
 // a product's two operands take twice the registers: half as many workgroups
 template <bool PROD>
@@ -151,13 +151,15 @@ __device__ __forceinline__ void sum_small_body(const float *x, const float *y, s
             }
         }
         if (4 * n4 + t < n) acc[0] += PROD ? (double)tx * (double)ty : (double)tx;
+        // every workgroup's butterfly formed (independent chains the compiler
+        // interleaves; one behind a branch each would run one after another),
+        // the unused ones dropped
+        double ws[NB];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            if (b < blocks) {  // uniform
-                const double s = wave_sum(acc[b]);
-                if (lane == 0) wsum[b][wave] = s;
-            }
-        }
+        for (int b = 0; b < NB; ++b) ws[b] = wave_sum(acc[b]);
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+            if (b < blocks && lane == 0) wsum[b][wave] = ws[b];
     }
     __syncthreads();
     if (t < blocks) {
