@@ -565,6 +565,18 @@ int ts_hip_adam_step_multi(const ts_hip_adam_param *params, size_t count, float 
 int ts_hip_adam_step_multi_table(const ts_hip_adam_param *params, size_t count, float lr, float beta1,
                                  float beta2, float eps, float weight_decay, const float *bias_corrections,
                                  const unsigned *slot, void *stream);
+/* The same with self-advancing replay counters (no counterpart in the
+ * reference): tickets holds one uint32 per wave of the launch
+ * (ts_hip_adam_multi_waves of the same list; device memory, 4-byte aligned,
+ * zero before the first launch); wave w adds 1 to tickets[w] and uses pair
+ * s = its value before the add, so the r-th launch since the tickets were
+ * cleared uses pair r with no counter-advancing launch of its own.  Launches
+ * that share tickets must run one after another (one stream) with the same
+ * parameter sizes and alignments. */
+size_t ts_hip_adam_multi_waves(const ts_hip_adam_param *params, size_t count);
+int ts_hip_adam_step_multi_ticket(const ts_hip_adam_param *params, size_t count, float lr, float beta1,
+                                  float beta2, float eps, float weight_decay, const float *bias_corrections,
+                                  unsigned *tickets, void *stream);
 /* Host: the bias corrections of steps first_step .. first_step + count - 1 as
  * ts_hip_adam_step_multi computes them (adam/mod.rs:524-531, bias_correct
  * :790-833): out[2i] = 1 / (1 - beta1^t), out[2i+1] = 1 / (1 - beta2^t), the

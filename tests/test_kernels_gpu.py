@@ -418,3 +418,43 @@ def test_adam_multi_matches_per_parameter(oracle):
             assert_bits_equal(dev[i][0].get(), host[i][0], f"p[{i}] wd={wd} ams={ams}")
             assert_bits_equal(dev[i][2].get(), host[i][2], f"v[{i}] wd={wd} ams={ams}")
     assert hip.ts_hip_adam_step_multi(None, 17, 1e-3, 0.9, 0.999, 1e-8, 0.0, 1, None) == 100001
+
+
+def test_adam_ticket_launches_read_their_own_table_entries():
+    # five launches on one set of tickets read table entries 0..4: the bits
+    # of eager steps 3..7
+    import ctypes
+    from train_station_amd._ffi import AdamParam
+    sizes = [4099, 10, (1 << 17) + 5]
+    first = 3
+    table = np.zeros(2 * 5, np.float32)
+    table_c = table.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+    hip_check(hip.ts_hip_adam_bias_corrections(ctypes.c_float(0.9), ctypes.c_float(0.999), first, 5, table_c))
+    dtable = Dev.of(table)
+    res = {}
+    for mode in ("eager", "ticket"):
+        ps = [Dev.of(normal(n, 400 + i)) for i, n in enumerate(sizes)]
+        ms = [Dev.of(np.zeros(n, np.float32)) for n in sizes]
+        vs = [Dev.of(np.zeros(n, np.float32)) for n in sizes]
+        for k in range(5):
+            gs = [Dev.of(normal(n, 500 + 10 * k + i, 0.1)) for i, n in enumerate(sizes)]
+            arr = (AdamParam * len(sizes))()
+            for i, n in enumerate(sizes):
+                arr[i] = AdamParam(ps[i].ptr, gs[i].ptr, ms[i].ptr, vs[i].ptr, None, n, 0)
+            if k == 0:
+                nw = hip.ts_hip_adam_multi_waves(ctypes.cast(arr, ctypes.c_void_p), len(sizes))
+                ticket = Dev.of(np.zeros(nw, np.float32))
+            if mode == "eager":
+                _run("ts_hip_adam_step_multi", ctypes.cast(arr, ctypes.c_void_p), len(sizes), 1e-3, 0.9, 0.999,
+                     1e-8, 0.0, first + k, None)
+            else:
+                _run("ts_hip_adam_step_multi_ticket", ctypes.cast(arr, ctypes.c_void_p), len(sizes), 1e-3, 0.9,
+                     0.999, 1e-8, 0.0, dtable.ptr, ticket.ptr, None)
+            sync()
+        res[mode] = [p.get() for p in ps] + [v.get() for v in vs]
+    for i, (a, b) in enumerate(zip(res["ticket"], res["eager"])):
+        assert_bits_equal(a, b, f"array {i}")
+    # every wave counted the 5 launches in its own word
+    counts = np.frombuffer(ticket.get().tobytes(), np.uint32)
+    assert counts.size >= len(sizes) * 4 and np.all(counts == 5)
+    assert hip.ts_hip_adam_step_multi_ticket(None, 1, 1e-3, 0.9, 0.999, 1e-8, 0.0, dtable.ptr, None, None) != 0

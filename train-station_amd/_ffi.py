@@ -173,6 +173,9 @@ HIP_SIGNATURES = {
                                           _c.c_float, _c.c_uint64, VP]),
     "ts_hip_adam_step_multi_table": (_c.c_int, [VP, SZ, _c.c_float, _c.c_float, _c.c_float, _c.c_float,
                                                 _c.c_float, VP, VP, VP]),
+    "ts_hip_adam_step_multi_ticket": (_c.c_int, [VP, SZ, _c.c_float, _c.c_float, _c.c_float, _c.c_float,
+                                                 _c.c_float, VP, VP, VP]),
+    "ts_hip_adam_multi_waves": (SZ, [VP, SZ]),
     "ts_hip_adam_bias_corrections": (_c.c_int, [_c.c_float, _c.c_float, _c.c_uint64, SZ, VP]),
     "ts_hip_slot_advance": (_c.c_int, [VP, VP]),
     "ts_hip_module_load_data": (_c.c_int, [VP, _c.POINTER(VP)]),

@@ -80,9 +80,11 @@ void Adam::step(const std::vector<Tensor *> &params) {
         launch(KernelClass::Adam, bytes, "ts_hip_adam_step_multi", [&] {
             void *st = Runtime::get().stream();
             if (slot)
-                return ts_hip_adam_step_multi_table(batch.data(), batch.size(), config_.learning_rate,
-                                                    config_.beta1, config_.beta2, config_.eps,
-                                                    config_.weight_decay, slot->table, slot->slot, st);
+                return ts_hip_adam_step_multi_ticket(batch.data(), batch.size(), config_.learning_rate,
+                                                     config_.beta1, config_.beta2, config_.eps,
+                                                     config_.weight_decay, slot->table,
+                                                     rec.adam_tickets(ts_hip_adam_multi_waves(batch.data(), batch.size())),
+                                                     st);
             return ts_hip_adam_step_multi(batch.data(), batch.size(), config_.learning_rate, config_.beta1,
                                           config_.beta2, config_.eps, config_.weight_decay, step_count, st);
         });

@@ -9,9 +9,11 @@
 // life: the pool pins every block acquired or used while recording and
 // parks, instead of reusing, any of them released meanwhile.  Adam's bias
 // corrections depend on the step count, so a recorded Adam::step reads them
-// from a device table indexed by a replay counter that the graph's last node
-// advances; before each run of replays the host fills the table with the
-// values eager steps would use from the optimizer's count at that moment.
+// from a device table: each wave of a recorded Adam launch counts its own
+// launches in a ticket word and reads the entry of its replay, so no launch of
+// its own advances a counter; before each run of replays the host clears the
+// tickets and fills the table with the values eager steps would use from the
+// optimizer's count at that moment.
 #include <algorithm>
 
 #include "ts_hip.h"
@@ -42,7 +44,6 @@ void StepRecorder::begin() {
 
 StepRecorder::AdamSlot StepRecorder::adam_step(float beta1, float beta2, const std::shared_ptr<AdamLedger> &ledger) {
     if (!graph_) throw Error("no step recording is open");
-    if (!graph_->slot) graph_->slot = std::make_shared<Allocation>(1);  // pinned: acquired while recording
     StepGraph::AdamUse u;
     u.table = std::make_shared<Allocation>(2 * kReplayChunk);
     u.beta1 = beta1;
@@ -52,7 +53,13 @@ StepRecorder::AdamSlot StepRecorder::adam_step(float beta1, float beta2, const s
         if (o.ledger == ledger) ++u.order;
     graph_->adams.push_back(std::move(u));
     const StepGraph::AdamUse &b = graph_->adams.back();
-    return {b.table->get(), reinterpret_cast<const unsigned *>(graph_->slot->get()), graph_->adams.size() - 1};
+    return {b.table->get(), graph_->adams.size() - 1};
+}
+
+unsigned *StepRecorder::adam_tickets(size_t waves) {
+    if (!graph_) throw Error("no step recording is open");
+    graph_->tickets.push_back(std::make_shared<Allocation>(waves));  // pinned: acquired while recording
+    return reinterpret_cast<unsigned *>(graph_->tickets.back()->get());
 }
 
 void StepRecorder::adam_param(size_t use, size_t param_id) {
@@ -77,16 +84,13 @@ StepGraph *StepRecorder::end() {
     std::unique_ptr<StepGraph> g = std::move(graph_);
     take_back(*g);
     void *stream = Runtime::get().stream();
-    // the last node moves the replay counter on to the next table entry
-    const int adv = g->slot ? ts_hip_slot_advance(reinterpret_cast<unsigned *>(g->slot->get()), stream)
-                            : TS_HIP_OK;
     void *exec = nullptr;
     const int st = ts_hip_stream_end_capture(stream, &exec);
     DevicePool::get().pin_end();
     g->exec = exec;
-    if (adv != TS_HIP_OK || st != TS_HIP_OK) {
+    if (st != TS_HIP_OK) {
         g.reset();  // unpins
-        check(adv != TS_HIP_OK ? adv : st, "recording the step");
+        check(st, "recording the step");
     }
     return g.release();
 }
@@ -117,8 +121,8 @@ void StepGraph::replay(size_t times) {
     std::vector<float> cf;
     for (size_t done = 0; done < times;) {
         const size_t chunk = std::min(times - done, StepRecorder::kReplayChunk);
-        if (slot) {
-            rt.sync();  // earlier replays have read their tables
+        if (!adams.empty()) {
+            rt.sync();  // earlier replays have read their tables and tickets
             cf.resize(2 * chunk);
             for (AdamUse &u : adams) {
                 // replay i runs this optimizer's recorded steps as its steps
@@ -137,8 +141,10 @@ void StepGraph::replay(size_t times) {
                 }
                 check(ts_hip_memcpy(u.table->get(), cf.data(), 2 * chunk, 0), "ts_hip_memcpy");
             }
-            const unsigned zero = 0;
-            check(ts_hip_memcpy(slot->get(), reinterpret_cast<const float *>(&zero), 1, 0), "ts_hip_memcpy");
+            for (auto &t : tickets) {
+                const std::vector<float> zeros(t->n, 0.0f);  // all bits 0: tickets of 0
+                check(ts_hip_memcpy(t->get(), zeros.data(), t->n, 0), "ts_hip_memcpy");
+            }
         }
         for (size_t i = 0; i < chunk; ++i) check(ts_hip_graph_launch(exec, rt.stream()), "ts_hip_graph_launch");
         executed += chunk;

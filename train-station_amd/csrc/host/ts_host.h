@@ -644,16 +644,19 @@ class Adam {
 
 // One recorded step: a HIP graph of the library stream's work between
 // StepRecorder::begin and end, the blocks it pinned, and per recorded
-// Adam::step a table of bias corrections indexed by a device replay counter.
-// A recording itself runs nothing, so it leaves every step counter as it was;
-// each replay then counts as many steps as it ran.
+// Adam::step a table of bias corrections, which each recorded Adam launch
+// indexes by device tickets of its own (ts_hip_adam_step_multi_ticket: the
+// r-th launch since the tickets were cleared reads entry r, so a replay needs
+// no counter-advancing launch).  A recording itself runs nothing, so it leaves
+// every step counter as it was; each replay then counts as many steps as it
+// ran.
 struct StepGraph {
     ~StepGraph();
     // Runs the recorded work `times` times in stream order.
     void replay(size_t times);
     void *exec = nullptr;
     std::vector<float *> pins;
-    std::shared_ptr<Allocation> slot;  // replay counter (one unsigned)
+    std::vector<std::shared_ptr<Allocation>> tickets;  // per recorded Adam launch, one unsigned per wave
     struct AdamUse {
         std::shared_ptr<Allocation> table;  // kReplayChunk [cf1, cf2] pairs
         float beta1 = 0, beta2 = 0;
@@ -677,14 +680,16 @@ class StepRecorder {
     StepGraph *end();
     void abort();
     // Called by Adam::step while recording, before it counts the step: the
-    // table and counter its launch reads; `use` names the step for
-    // adam_param, which records each parameter as soon as it is stepped.
+    // table its launches read; `use` names the step for adam_param, which
+    // records each parameter as soon as it is stepped.
     struct AdamSlot {
         const float *table;
-        const unsigned *slot;
         size_t use;
     };
     AdamSlot adam_step(float beta1, float beta2, const std::shared_ptr<AdamLedger> &ledger);
+    // The tickets of one recorded Adam launch of `waves` waves (cleared
+    // before each run of replays).
+    unsigned *adam_tickets(size_t waves);
     void adam_param(size_t use, size_t param_id);
 
   private:

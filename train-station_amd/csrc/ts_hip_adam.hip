@@ -118,9 +118,14 @@ struct MultiArgs {
     int count;
     float b1, c1, b2, c2, cf1, cf2, lr, eps, wd;
     // When set, the bias corrections are cf_table[2*s], cf_table[2*s+1] with
-    // s = *cf_slot instead of cf1 / cf2 (a step recorded once and replayed).
+    // s = *cf_slot instead of cf1 / cf2 (a step recorded once and replayed);
+    // with cf_ticket instead of cf_slot, wave w of the launch adds 1 to
+    // cf_ticket[w] and s = its value before the add (the launches it has run
+    // since the tickets were cleared: one word per wave, so no two waves
+    // contend for an address).
     const float *cf_table;
     const unsigned *cf_slot;
+    unsigned *cf_ticket;
 };
 
 // One flat grid over all tensors: workgroup b finds its tensor in the
@@ -138,7 +143,15 @@ __global__ __launch_bounds__(kBlock) void adam_multi_kernel(MultiArgs A) {
     a.b1 = A.b1; a.c1 = A.c1; a.b2 = A.b2; a.c2 = A.c2;
     a.cf1 = A.cf1; a.cf2 = A.cf2; a.lr = A.lr; a.eps = A.eps; a.wd = A.wd;
     if (A.cf_table) {  // vector loads at device scope: the slot changes between launches
-        const unsigned sl = __hip_atomic_load(A.cf_slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        unsigned sl;
+        if (A.cf_ticket) {  // one vector atomic per wave on its own word, its result read from lane 0
+            unsigned tk = 0;
+            const unsigned w = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+            if ((threadIdx.x & 63) == 0) tk = atomicAdd(A.cf_ticket + w, 1u);
+            sl = static_cast<unsigned>(__builtin_amdgcn_readfirstlane(static_cast<int>(tk)));
+        } else {
+            sl = __hip_atomic_load(A.cf_slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         a.cf1 = __hip_atomic_load(A.cf_table + 2 * sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         a.cf2 = __hip_atomic_load(A.cf_table + 2 * sl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -187,9 +200,22 @@ extern "C" int ts_hip_adam_step(float *p, const float *g, float *m, float *v, fl
     return launch_status();
 }
 
+// Workgroups of the one multi-tensor launch over params (0 for a bad list).
+static size_t adam_multi_blocks(const ts_hip_adam_param *params, size_t count) {
+    if (!params || count == 0 || count > TS_HIP_ADAM_MAX_PARAMS) return 0;
+    size_t blocks = 0;
+    for (size_t i = 0; i < count; ++i) {
+        const ts_hip_adam_param &q = params[i];
+        const bool vec = aligned16(q.p) && aligned16(q.g) && aligned16(q.m) && aligned16(q.v) &&
+                         (!q.v_hat_max || aligned16(q.v_hat_max));
+        blocks += (adam_threads(q.n, vec ? q.n / 4 : 0) + kBlock - 1) / kBlock;
+    }
+    return blocks;
+}
+
 static int adam_multi(const ts_hip_adam_param *params, size_t count, float lr, float beta1, float beta2,
                       float eps, float weight_decay, float cf1, float cf2, const float *cf_table,
-                      const unsigned *cf_slot, void *stream) {
+                      const unsigned *cf_slot, void *stream, unsigned *cf_ticket = nullptr) {
     if (count == 0) return TS_HIP_OK;
     if (!params || count > TS_HIP_ADAM_MAX_PARAMS) return TS_HIP_EINVAL;
     MultiArgs A{};
@@ -214,6 +240,7 @@ static int adam_multi(const ts_hip_adam_param *params, size_t count, float lr, f
     A.cf2 = cf2;
     A.cf_table = cf_table;
     A.cf_slot = cf_slot;
+    A.cf_ticket = cf_ticket;
     A.lr = lr; A.eps = eps; A.wd = weight_decay;
     launch(adam_multi_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0,
                        as_stream(stream), A);
@@ -234,6 +261,19 @@ extern "C" int ts_hip_adam_step_multi_table(const ts_hip_adam_param *params, siz
     if (!bias_corrections || !slot) return TS_HIP_EINVAL;
     return adam_multi(params, count, lr, beta1, beta2, eps, weight_decay, 0.0f, 0.0f, bias_corrections, slot,
                       stream);
+}
+
+extern "C" size_t ts_hip_adam_multi_waves(const ts_hip_adam_param *params, size_t count) {
+    return adam_multi_blocks(params, count) * (kBlock / 64);
+}
+
+extern "C" int ts_hip_adam_step_multi_ticket(const ts_hip_adam_param *params, size_t count, float lr,
+                                             float beta1, float beta2, float eps, float weight_decay,
+                                             const float *bias_corrections, unsigned *tickets, void *stream) {
+    if (!bias_corrections || !tickets) return TS_HIP_EINVAL;
+    if ((reinterpret_cast<uintptr_t>(tickets) & 3u) != 0) return TS_HIP_EINVAL;
+    return adam_multi(params, count, lr, beta1, beta2, eps, weight_decay, 0.0f, 0.0f, bias_corrections, nullptr,
+                      stream, tickets);
 }
 
 extern "C" int ts_hip_adam_bias_corrections(float beta1, float beta2, uint64_t first_step, size_t count,
