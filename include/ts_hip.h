@@ -418,6 +418,21 @@ int ts_hip_gemm_fused(int trans_a, int trans_b, size_t M, size_t N, size_t K, co
                       const float *B, size_t ldb, const float *bias, int relu, const float *mask, float *C,
                       size_t ldc, float *workspace, size_t workspace_floats, void *stream);
 
+/* ts_hip_gemm_fused with a subtraction in the epilogue (no counterpart in
+ * the reference, whose MSE subtracts the target in a pass of its own:
+ * feedforward_network.rs:478-479 through ops/sub.rs's sub_tensor of
+ * same-shape tensors).  Per output element, after the bias:
+ *   v = v - sub[i*ldc + j]   (sub laid out as C)
+ * then relu and mask as in ts_hip_gemm_fused: the bits of ts_hip_gemm_fused
+ * (bias only) followed by ts_hip_sub, then the rest.  Only for products that
+ * ts_hip_gemm_takes_sub accepts (the one-pass narrow kernel: at most 16
+ * output columns, or few output tiles and a long K); TS_HIP_EINVAL otherwise.
+ * Allocates nothing. */
+int ts_hip_gemm_takes_sub(int trans_a, int trans_b, size_t M, size_t N, size_t K);
+int ts_hip_gemm_fused_sub(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A, size_t lda,
+                          const float *B, size_t ldb, const float *bias, const float *sub, int relu,
+                          const float *mask, float *C, size_t ldc, void *stream);
+
 /* The weight gradient of a linear layer together with its bias gradient (no
  * counterpart in the reference, which reduces the bias gradient in a pass of
  * its own: grad_fn/ops/add.rs:4-28 through reduce_gradient_to_shape,
@@ -474,22 +489,27 @@ int ts_hip_gemm_colsum_xf(int trans_a, size_t M, size_t N, size_t K, const float
                           float *C, size_t ldc, float *colsum, float *workspace, size_t workspace_floats,
                           void *stream);
 
-/* ts_hip_gemm_colsum_xf with ldb == N that also adds up B as stored (before
- * xb) in the same launch (no counterpart in the reference, which sums the
- * loss in a pass of its own, reductions/sum.rs:80-141 and
+/* ts_hip_gemm_colsum_xf with ldb == N that also adds up B as stored, each
+ * value put through xs first (NULL: none; the ops and fp32 semantics of
+ * ts_hip_operand_xf), in the same launch (no counterpart in the reference,
+ * which sums the loss in a pass of its own, reductions/sum.rs:80-141 and
  * reductions/mean.rs:48-109, before its backward reads the same values: the
  * README step's relu(x W + b).sum(), README.md:71-79, whose weight gradient
- * reads relu's output through relu's backward):
- *   bsum[0] = the sum of B's K*N values, divided by (float)(K*N) when mean,
- * with the bits of ts_hip_sum / ts_hip_mean(B, K*N), from one workgroup
- * appended to the product's grid.  Only where ts_hip_gemm_takes_bsum accepts
- * (trans_a == 1; the products whose column sums come from the register-staged
- * tiles' own launch, with no workspace; K*N <= 16384), with B 16-byte
- * aligned; TS_HIP_EINVAL otherwise.  Allocates nothing. */
+ * reads relu's output through relu's backward, or an MSE's mean of d * d,
+ * feedforward_network.rs:478-479, whose last weight gradient reads d):
+ *   bsum[0] = the sum of xs(B)'s K*N values, divided by (float)(K*N) when
+ *   mean, with the bits of ts_hip_sum / ts_hip_mean over those values,
+ * from one workgroup appended to the product's grid.  Only where
+ * ts_hip_gemm_takes_bsum accepts (trans_a == 1; the products whose column
+ * sums come from the product's own launch with no workspace -- the
+ * register-staged tiles, or the narrow kernel at its widest workgroups,
+ * K >= 1024; K*N <= 16384), with B 16-byte aligned; TS_HIP_EINVAL otherwise.
+ * Allocates nothing. */
 int ts_hip_gemm_takes_bsum(int trans_a, size_t M, size_t N, size_t K);
 int ts_hip_gemm_colsum_bsum(int trans_a, size_t M, size_t N, size_t K, const float *A, size_t lda,
                             const ts_hip_operand_xf *xa, const float *B, const ts_hip_operand_xf *xb, float *C,
-                            size_t ldc, float *colsum, float *bsum, int mean, void *stream);
+                            size_t ldc, float *colsum, const ts_hip_operand_xf *xs, float *bsum, int mean,
+                            void *stream);
 
 /* Batched C[b] = op(A[b]) . op(B[b]) (matmul/mod.rs:634-760 batched_matmul and
  * the batched backward of grad_fn/ops/matmul.rs:150-219) on the same MFMA

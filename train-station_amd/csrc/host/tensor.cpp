@@ -239,6 +239,7 @@ void set_pending(const std::shared_ptr<Allocation> &out, std::shared_ptr<Pending
     add_reader(p->B, out);
     add_reader(p->src, out);
     add_reader(p->bias, out);
+    add_reader(p->sub, out);
     add_reader(p->mask, out);
     out->pending = std::move(p);
 }
@@ -403,16 +404,35 @@ int gemm2d_xf(int ta, int tb, size_t M, size_t N, size_t K, const float *A, size
 
 std::vector<std::weak_ptr<Allocation>> &pending_reduces();
 
-// A deferred sum / mean of all n values of x still to be formed, or null.
-std::shared_ptr<Allocation> pending_sum_of(const Allocation *x, size_t n) {
+// A deferred sum / mean still to be formed of all n values of x, or of a
+// chain of ops over x alone that a transform expresses (xs: that chain, or
+// no ops), or null.
+std::shared_ptr<Allocation> pending_sum_of(const std::shared_ptr<Allocation> &x, size_t n, ts_hip_operand_xf &xs) {
     for (auto &w : pending_reduces()) {
         auto o = w.lock();
-        if (o && o->reduce && o->reduce->x.get() == x && o->reduce->n == n) return o;
+        if (!o || !o->reduce || o->reduce->n != n) continue;
+        xs = ts_hip_operand_xf{};
+        if (o->reduce->x == x) return o;
+        std::shared_ptr<Allocation> leaf;
+        if (operand_xf(o->reduce->x, leaf, xs) && leaf == x) return o;
     }
+    xs = ts_hip_operand_xf{};
     return nullptr;
 }
 
 void launch_product(const PendingGemm &p, float *C, bool with_epilogue) {
+    if (with_epilogue && p.sub) {  // the narrow kernel's subtraction (no operand transforms)
+        const float *A = p.A->get(), *B = p.B->get();
+        const float *bias = p.bias ? p.bias->get() : nullptr;
+        const float *sub = p.sub->get();
+        const float *mask = p.mask ? p.mask->get() : nullptr;
+        DevicePool::get().note_use(C);
+        launch(KernelClass::Gemm, 2.0 * p.M * p.N * p.K, "ts_hip_gemm_fused_sub", [&] {
+            return ts_hip_gemm_fused_sub(p.ta, p.tb, p.M, p.N, p.K, A, p.lda, B, p.ldb, bias, sub, p.relu ? 1 : 0,
+                                         mask, C, p.N, S());
+        });
+        return;
+    }
     // an operand that is a deferred chain over one buffer is read as that
     // buffer, the chain applied as it is loaded
     ts_hip_operand_xf xa{}, xb{};
@@ -444,12 +464,17 @@ void materialize(Allocation &a) {
     if (p->src) {  // epilogue only: the separate kernels, in the fused epilogue's order
         const float *x = p->src->get();
         const float *bias = p->bias ? p->bias->get() : nullptr;
+        const float *sub = p->sub ? p->sub->get() : nullptr;
         const float *mask = p->mask ? p->mask->get() : nullptr;
         DevicePool::get().note_use(C);
         const size_t n = p->M * p->N;
         if (bias) {
             launch(KernelClass::Elementwise, 8.0 * n + 4.0 * p->N, "ts_hip_bias_add",
                    [&] { return ts_hip_bias_add(x, bias, C, p->M, p->N, 0, S()); });
+            x = C;
+        }
+        if (sub) {
+            launch(KernelClass::Elementwise, 12.0 * n, "ts_hip_sub", [&] { return ts_hip_sub(x, sub, C, n, S()); });
             x = C;
         }
         if (p->relu) {
@@ -487,6 +512,7 @@ void materialize(Allocation &a) {
         e->N = old->N;
         e->src = prod;
         e->bias = old->bias;
+        e->sub = old->sub;
         e->relu = old->relu;
         e->mask = old->mask;
         set_pending(m, e);
@@ -1219,6 +1245,17 @@ static bool fuse_bias(const Tensor &mat, const Tensor &vec) {
            is_row_broadcast(mat.dims(), vec.dims());
 }
 
+// A deferred product [M, N] (bare or with its bias) minus a same-shape
+// tensor becomes the product with a subtraction in its store, where the
+// narrow kernel takes the product (ts_hip_gemm_takes_sub).
+static bool fuse_sub(const Tensor &mat, const Tensor &o) {
+    const auto &a = mat.allocation();
+    if (!fusion_enabled() || !a || !a->pending || !o.allocation() || mat.dims() != o.dims()) return false;
+    const PendingGemm &p = *a->pending;
+    return !p.src && !p.sub && !p.relu && !p.mask && a.get() != o.allocation().get() &&
+           ts_hip_gemm_takes_sub(p.ta, p.tb, p.M, p.N, p.K) != 0;
+}
+
 Tensor Tensor::binary(const Tensor &o, GradFn::Kind kind) const {
     const bool same = dims_ == o.dims_;
     const int op = opcode(kind);
@@ -1226,7 +1263,12 @@ Tensor Tensor::binary(const Tensor &o, GradFn::Kind kind) const {
     const bool fuse_self = kind == GradFn::Kind::Add && fuse_bias(*this, o);
     const bool fuse_other = !fuse_self && kind == GradFn::Kind::Add && fuse_bias(o, *this);
     std::shared_ptr<PendingGemm> fused;
-    if (fuse_self || fuse_other) {
+    if (kind == GradFn::Kind::Sub && fuse_sub(*this, o)) {
+        out = new_uninit(dims_);
+        fused = fork_pending(alloc_, out.alloc_);  // a record: fuse_sub found it pending
+        fused->sub = o.alloc_;
+        set_pending(out.alloc_, std::move(fused));
+    } else if (fuse_self || fuse_other) {
         const Tensor &mat = fuse_self ? *this : o, &vec = fuse_self ? o : *this;
         out = new_uninit(mat.dims_);
         fused = fork_pending(mat.alloc_, out.alloc_);
@@ -1983,11 +2025,13 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
                     const bool fx = ts_hip_gemm_takes_xf(ta, 0, Kd, N, M, db ? 1 : 0) &&
                                     operand_xf(go.allocation(), leaf, xb);
                     const float *A = va.buf ? va.buf->get() : nullptr;
-                    // a deferred sum of the buffer read as B (the README step's
-                    // loss, over relu's output) comes out of this launch too
+                    // a deferred sum of the buffer read as B, or of a chain over
+                    // it (the README step's loss over relu's output; an MSE's
+                    // mean of d * d), comes out of this launch too
+                    ts_hip_operand_xf xs{};
                     const std::shared_ptr<Allocation> bsum =
                         db && ts_hip_gemm_takes_bsum(ta, Kd, N, M)
-                            ? pending_sum_of(fx ? leaf.get() : go.allocation().get(), M * N)
+                            ? pending_sum_of(fx ? leaf : go.allocation(), M * N, xs)
                             : nullptr;
                     if (bsum) {
                         db->colsum.reset();
@@ -1997,7 +2041,8 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
                         DevicePool::get().note_use(sum);
                         launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm_colsum_bsum(dW, db, loss)", [&] {
                             return ts_hip_gemm_colsum_bsum(ta, Kd, N, M, A, lda, nullptr, B, fx ? &xb : nullptr, C, N,
-                                                           db->raw(), sum, bsum->reduce->mean ? 1 : 0, S());
+                                                           db->raw(), xs.n_ops ? &xs : nullptr, sum,
+                                                           bsum->reduce->mean ? 1 : 0, S());
                         });
                         bsum->reduce.reset();
                     } else if (db) {

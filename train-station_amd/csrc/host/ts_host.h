@@ -123,10 +123,13 @@ struct PendingGemm {
     int ta = 0, tb = 0;
     size_t M = 0, N = 0, K = 0, lda = 0, ldb = 0;
     std::shared_ptr<Allocation> A, B, bias, mask;
+    // after the bias: minus a same-shape buffer (the MSE's prediction minus
+    // target, ts_hip_gemm_fused_sub; products on the narrow kernel only)
+    std::shared_ptr<Allocation> sub;
     std::shared_ptr<Allocation> src;  // epilogue-only: the produced [M, N] buffer the epilogue reads
     bool relu = false;
     std::shared_ptr<ProductGroup> group;
-    bool bare() const { return !src && !bias && !mask && !relu; }
+    bool bare() const { return !src && !bias && !sub && !mask && !relu; }
 };
 
 // One division checked for zero divisors (the reference's panic in

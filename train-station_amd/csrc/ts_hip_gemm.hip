@@ -175,15 +175,20 @@ struct GemmArgs {
     // operand transforms (register-staged tiles, the narrow and one-k-tile
     // kernels and the column strips apply them; the others take none)
     OperandXf xa, xb;
-    // The sum (mean: / (float)sum_n) of sum_n floats at sum_x into
-    // sum_out[0], with the bits of ts_hip_sum: one workgroup appended after
-    // the column strips runs sum_small_body over sum_blocks first-pass
-    // workgroups (register-staged tiles with column sums only; the caller
-    // passes B as stored).  Null sum_out: none.
+    // The sum (mean: / (float)sum_n) of the sum_n floats at sum_x, each put
+    // through sum_xf first, into sum_out[0] with the bits of ts_hip_sum over
+    // the transformed values: one workgroup appended to the grid of a product
+    // with column sums (after the register-staged tiles' strips, or as the
+    // narrow kernel's last row block) runs sum_in_workgroup over sum_blocks
+    // first-pass workgroups.  Null sum_out: none.
     const float *sum_x;
     float *sum_out;
     size_t sum_n;
     int sum_mean, sum_blocks;
+    OperandXf sum_xf;
+    // Epilogue subtraction (narrow kernel only): after the bias, v = v -
+    // sub[i*ldc + j] (laid out as C).  Null: none.
+    const float *sub;
 };
 
 // Store of a wave's FM x FN accumulator blocks, the wave tile's corner at
@@ -401,6 +406,85 @@ __device__ __forceinline__ void colsum_strip(const GemmArgs &g, int j0) {
     if (t < kStripCols && j0 + t < g.N) g.colsum[j0 + t] = static_cast<float>(total);
 }
 
+// The sum of GemmArgs::sum_x (sum_n values, each put through sum_xf first,
+// one fp32 operation per op as the operand transforms apply them) into
+// sum_out[0] with the bits of ts_hip_sum over the transformed values, by one
+// workgroup of NT threads (a multiple of kBlock): it plays the sum's
+// sum_blocks <= kSumSmallBlocks first-pass workgroups and its second pass.
+// Thread T takes the first pass's virtual threads v = T + r*NT (workgroup
+// v / kBlock, wave (T % kBlock) / 64, the same lane), each with at most one
+// float4 group (and the tail, n - 4*(n/4) < 4 values, on virtual threads
+// 0..2), so every wave sum is that pass's; the partials are then combined as
+// the second pass combines them (thread t adds partial t from +0, block_sum).
+// All loads are issued before any value is used.
+template <int NT>
+__device__ __forceinline__ void sum_in_workgroup(const GemmArgs &g) {
+    static_assert(NT % kBlock == 0, "whole first-pass workgroups per round");
+    constexpr int R = kSumSmallBlocks * kBlock / NT;  // rounds
+    constexpr int kWaves = kBlock / 64;
+    __shared__ double wsum[kSumSmallBlocks][kWaves];
+    __shared__ double parts[kSumSmallBlocks];
+    __shared__ double fin[kWaves];
+    const float *x = g.sum_x;
+    const size_t n = g.sum_n, n4 = n / 4;
+    const int blocks = g.sum_blocks;
+    const int T = static_cast<int>(threadIdx.x), lane = T & 63, wave = T >> 6;
+    const XfRegs xs = xf_load(g.sum_xf);
+    const size_t ti = 4 * n4 + T < n ? 4 * n4 + T : n - 1;
+    float tx[1] = {x[ti]};
+    f4v_t q[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        q[r] = f4v_t{0.0f, 0.0f, 0.0f, 0.0f};
+        if (r * NT < blocks * kBlock && n4 > 0) {  // uniform
+            const size_t v = static_cast<size_t>(T) + static_cast<size_t>(r) * NT;
+            q[r] = *reinterpret_cast<const f4v_t *>(x + 4 * (v < n4 ? v : n4 - 1));
+        }
+    }
+    xf_regs(xs, q);
+    xf_array(xs, tx);
+    double acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        acc[r] = 0.0;
+        const size_t v = static_cast<size_t>(T) + static_cast<size_t>(r) * NT;
+        if (v < n4) acc[r] += (double)q[r][0] + (double)q[r][1] + (double)q[r][2] + (double)q[r][3];
+    }
+    if (4 * n4 + T < n) acc[0] += (double)tx[0];
+    // every round's butterfly formed together (independent chains), each
+    // stored for its first-pass workgroup
+    double ws[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) ws[r] = wave_sum(acc[r]);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int b = (T + r * NT) / kBlock;
+        if (b < blocks && lane == 0) wsum[b][(T % kBlock) / 64] = ws[r];
+    }
+    __syncthreads();
+    if (T < blocks) {
+        double s = 0.0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) s += wsum[T][w];
+        parts[T] = s;
+    }
+    __syncthreads();
+    if (wave < kWaves) {  // block_sum over the first kBlock threads
+        double a = 0.0;
+        if (T < blocks) a += parts[T];
+        a = wave_sum(a);
+        if (lane == 0) fin[wave] = a;
+    }
+    __syncthreads();
+    if (T == 0) {
+        double s = 0.0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) s += fin[w];
+        const float f = static_cast<float>(s);
+        g.sum_out[0] = g.sum_mean ? f / static_cast<float>(n) : f;
+    }
+}
+
 // EPI: the epilogue kind applied at the store (a separate instantiation per
 // kind, so the bare product keeps its register allocation).  PF: operand tiles
 // prefetched into registers ahead of the LDS stage (deeper for small tiles,
@@ -416,16 +500,11 @@ template <bool TA, bool TB, int BM, int BN, int WM, int WN, int EPI, int PF, boo
           bool XF = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_mfma(GemmArgs g) {
     static_assert(!CS || !TB, "column sums of B need trans_b == 0");
-    static_assert(64 * WM * WN >= kBlock, "the appended sum takes a workgroup of at least kBlock threads");
+
     if (CS && static_cast<int>(blockIdx.x) >= g.tiles) {  // uniform
         const int j0 = (static_cast<int>(blockIdx.x) - g.tiles) * kStripCols;
-        if (j0 < g.N) {
-            colsum_strip<64 * WM * WN, XF>(g, j0);
-        } else if (g.sum_mean) {  // the workgroup after the strips: GemmArgs::sum_out
-            sum_small_body<false, true>(g.sum_x, nullptr, g.sum_n, g.sum_n / 4, g.sum_blocks, g.sum_out);
-        } else {
-            sum_small_body<false, false>(g.sum_x, nullptr, g.sum_n, g.sum_n / 4, g.sum_blocks, g.sum_out);
-        }
+        if (j0 < g.N) colsum_strip<64 * WM * WN, XF>(g, j0);
+        else sum_in_workgroup<64 * WM * WN>(g);  // the workgroup after the strips: GemmArgs::sum_out
         return;
     }
     constexpr int NT = 64 * WM * WN;
@@ -1273,6 +1352,14 @@ static_assert(kColsumRows == 64, "a narrow wave round is one column-sum chunk");
 template <bool TA, bool TB, bool V, bool CS, bool XF = false>
 __global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) {
     static_assert(!CS || !TB, "column sums of B need trans_b == 0");
+    if constexpr (CS) {
+        // the row of workgroups appended for GemmArgs::sum_out (launched with
+        // kNarrowMaxWaves waves): its first workgroup forms the sum
+        if (g.sum_out && blockIdx.x == gridDim.x - 1) {  // uniform
+            if (blockIdx.y == 0) sum_in_workgroup<64 * kNarrowMaxWaves>(g);
+            return;
+        }
+    }
     __shared__ float red[kNarrowMaxWaves][256];
     __shared__ double csum[CS ? kNarrowMaxChunks : 1][kSkinnyN];
     const int lane = threadIdx.x & 63;
@@ -1294,7 +1381,7 @@ __global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) 
     // (output t = 64r + l: row 4*(l/16) + r, column l%16), loaded now at
     // clamped addresses so they arrive with the operands.
     constexpr int kOuts = 256 / 64;
-    float eb[kOuts] = {}, em[kOuts] = {};
+    float eb[kOuts] = {}, em[kOuts] = {}, es[kOuts] = {};
 #pragma unroll
     for (int o = 0; o < kOuts; ++o) {
         if (o * static_cast<int>(blockDim.x) >= 256) break;  // uniform
@@ -1302,6 +1389,7 @@ __global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) 
         const int i = min(m0 + 4 * ((t & 63) >> 4) + ((t >> 6) & 3), g.M - 1), j = min(n0 + (t & 15), g.N - 1);
         eb[o] = g.bias ? g.bias[j] : 0.0f;
         em[o] = g.mask ? g.mask[(size_t)i * g.ldc + j] : 1.0f;
+        es[o] = g.sub ? g.sub[(size_t)i * g.ldc + j] : 0.0f;
     }
     f4v_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int k0 = kb; k0 < ke; k0 += 64) {
@@ -1373,7 +1461,8 @@ __global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) 
         for (int w = 1; w < waves; ++w) v += red[w][t];
         const int l = t & 63;
         const int i = m0 + 4 * (l >> 4) + (t >> 6), j = n0 + (l & 15);
-        if (g.bias) v = v + eb[o];  // epilogue()'s order: bias, relu, mask
+        if (g.bias) v = v + eb[o];  // epilogue()'s order: bias, sub, relu, mask
+        if (g.sub) v = v - es[o];
         if (g.relu) v = v > 0.0f ? v : 0.0f;
         if (g.mask) v = em[o] > 0.0f ? v : 0.0f;
         if (i < g.M && j < g.N) g.C[(size_t)i * g.ldc + j] = v;
@@ -1450,7 +1539,9 @@ static int launch_narrow(int trans_a, int trans_b, size_t M, size_t N, size_t K,
     g.lda = static_cast<int>(lda); g.ldb = static_cast<int>(ldb); g.ldc = static_cast<int>(ldc);
     const bool va = trans_a || (aligned16(A) && lda % 4 == 0);
     const bool vb = !trans_b || (aligned16(B) && ldb % 4 == 0);
-    const dim3 grid(static_cast<unsigned>((M + kNarrowRows - 1) / kNarrowRows),
+    // the sum's workgroup: a row block appended (full width, kNarrowMaxWaves waves)
+    if (g.sum_out && (!g.colsum || narrow_waves(K) != kNarrowMaxWaves)) return TS_HIP_EINVAL;
+    const dim3 grid(static_cast<unsigned>((M + kNarrowRows - 1) / kNarrowRows + (g.sum_out ? 1 : 0)),
                     static_cast<unsigned>((N + kSkinnyN - 1) / kSkinnyN)),
         block(64 * narrow_waves(K));
     hipStream_t s = as_stream(stream);
@@ -1828,33 +1919,54 @@ extern "C" int ts_hip_gemm_colsum(int trans_a, size_t M, size_t N, size_t K, con
                       workspace_floats, stream);
 }
 
+extern "C" int ts_hip_gemm_takes_sub(int trans_a, int trans_b, size_t M, size_t N, size_t K) {
+    if (M == 0 || N == 0 || K == 0) return 0;
+    return gemm_plan(trans_a, trans_b, M, N, K, false).narrow ? 1 : 0;
+}
+
+extern "C" int ts_hip_gemm_fused_sub(int trans_a, int trans_b, size_t M, size_t N, size_t K, const float *A,
+                                     size_t lda, const float *B, size_t ldb, const float *bias, const float *sub,
+                                     int relu, const float *mask, float *C, size_t ldc, void *stream) {
+    if (!ts_hip_gemm_takes_sub(trans_a, trans_b, M, N, K) || !sub || !C || ldc < N) return TS_HIP_EINVAL;
+    GemmArgs g{};
+    g.bias = bias;
+    g.sub = sub;
+    g.relu = relu != 0;
+    g.mask = mask;
+    return launch_narrow(trans_a, trans_b, M, N, K, A, lda, B, ldb, C, ldc, g, stream);
+}
+
 extern "C" int ts_hip_gemm_takes_bsum(int trans_a, size_t M, size_t N, size_t K) {
     if (!trans_a || M == 0 || N == 0 || K == 0) return 0;
     const GemmPlan p = gemm_plan(1, 0, M, N, K, true);
     // the register-staged tiles with their column strips (one pass, no
-    // temporary), and a B that one workgroup's sum covers
+    // temporary), or the narrow kernel with its column sums and its widest
+    // workgroups; and a B that one workgroup's sum covers
     const bool strips = !p.narrow && !p.skinny && p.slices == 1 && p.cs_kernel && !big_grid(M, N, 1) && p.total() == 0;
+    const bool narrow = p.narrow && p.cs_kernel && narrow_waves(K) == kNarrowMaxWaves;
     const size_t n = K * N;
-    return strips && n / K == N && sum_blocks(n) <= static_cast<size_t>(small_blocks<false>()) ? 1 : 0;
+    return (strips || narrow) && n / K == N && sum_blocks(n) <= static_cast<size_t>(kSumSmallBlocks) ? 1 : 0;
 }
 
 extern "C" int ts_hip_gemm_colsum_bsum(int trans_a, size_t M, size_t N, size_t K, const float *A, size_t lda,
                                        const ts_hip_operand_xf *xa, const float *B, const ts_hip_operand_xf *xb,
-                                       float *C, size_t ldc, float *colsum, float *bsum, int mean, void *stream) {
+                                       float *C, size_t ldc, float *colsum, const ts_hip_operand_xf *xs,
+                                       float *bsum, int mean, void *stream) {
     if (!ts_hip_gemm_takes_bsum(trans_a, M, N, K) || !A || !B || !C || !colsum || !bsum || ldc < N)
         return TS_HIP_EINVAL;
     if (!aligned16(B) && K * N >= 4) return TS_HIP_EINVAL;  // the sum's float4 loads
     OperandXf fa, fb;
-    if (!xf_from(xa, fa) || !xf_from(xb, fb)) return TS_HIP_EINVAL;
     GemmArgs g{};
+    if (!xf_from(xa, fa) || !xf_from(xb, fb) || !xf_from(xs, g.sum_xf)) return TS_HIP_EINVAL;
     g.xa = fa;
     g.xb = fb;
     g.colsum = colsum;
-    g.sum_x = B;  // as stored: the transform applies to the product's loads only
+    g.sum_x = B;  // as stored: xb applies to the product's loads, xs to the summed values
     g.sum_out = bsum;
     g.sum_n = K * N;
     g.sum_mean = mean != 0;
     g.sum_blocks = static_cast<int>(sum_blocks(K * N));
+    if (gemm_plan(1, 0, M, N, K, true).narrow) return launch_narrow(1, 0, M, N, K, A, lda, B, N, C, ldc, g, stream);
     return gemm_launch(1, 0, M, N, K, A, lda, B, N, C, ldc, g, 1, stream);
 }
 
