@@ -347,14 +347,17 @@ int ts_hip_sum(const float *x, size_t n, float *out, float *workspace, size_t wo
 /* reductions/mean.rs:48-109: out[0] = sum(x) / (float)n */
 int ts_hip_mean(const float *x, size_t n, float *out, float *workspace, size_t workspace_floats,
                 void *stream);
-/* Workspace (device floats) needed by ts_hip_sum_dim0 for [rows,cols]. */
+/* Workspace (device floats) needed by ts_hip_sum_dim0 for [rows,cols]: one
+ * f64 sum per 64-row chunk and column, 2 * ceil(rows/64) * cols floats, so it
+ * grows with the row count (32 MiB for [2^24, 16]). */
 size_t ts_hip_sum_dim0_workspace_floats(size_t rows, size_t cols);
 /* reductions/sum.rs:225-306 sum_dims(&[0]) on [rows,cols] -> [cols]; the
  * bias-gradient column reduction of grad_fn/utils.rs:23-60.  Fixed order:
- * chunks of 64 rows, each added row by row in f64 from +0, the chunk sums
- * added in chunk order in f64 from +0, rounded to fp32 once (not the
+ * chunks of 64 rows, each added row by row in f64 from +0; groups of 8
+ * consecutive chunk sums, each added in chunk order in f64 from +0; the group
+ * sums added in group order in f64 from +0; rounded to fp32 once (not the
  * reference's fp32 row order; within 1e-4 of it, within f64 rounding of the
- * exact sum). */
+ * exact sum).  The last sum is one dependent add per group of 512 rows. */
 int ts_hip_sum_dim0(const float *x, size_t rows, size_t cols, float *out, float *workspace,
                     size_t workspace_floats, void *stream);
 

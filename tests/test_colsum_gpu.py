@@ -154,3 +154,28 @@ def da_ptr(Dev, a):
     d = Dev.of(a)
     _keep.append(d)  # alive until the test module ends
     return d.ptr
+
+
+# tall inputs: past 16 groups of 8 chunks the group sums run as a pass of
+# their own, then one dependent add per group (the order is unchanged)
+@pytest.mark.parametrize("rows,cols", [(8192, 7), (8193, 3), (9 * 8192 + 5, 5), ((1 << 17) + 37, 16),
+                                       (40000, 259)])
+def test_tall_column_sums(oracle, rows, cols):
+    from gpu_util import Dev, hip, hip_check, init, sync
+
+    init()
+    print(f"[colsum tall] {rows}x{cols}", flush=True)
+    x = normal((rows, cols), 31)
+    # large terms that cancel across groups, and a small one they would
+    # swallow if a group's sum were formed in another order
+    x[64 * 8 * 3, 0] = 2.0 ** 50
+    x[64 * 8 * 7, 0] = -(2.0 ** 50)
+    x[64 * 8 * 5 + 1, 0] = 1.5
+    want = oracle.sum_dim0_chunked(x)
+    dx, out = Dev.of(x), Dev(cols)
+    ws = hip.ts_hip_sum_dim0_workspace_floats(rows, cols)
+    assert ws == 2 * ((rows + 63) // 64) * cols
+    dws = Dev(ws)
+    hip_check(hip.ts_hip_sum_dim0(dx.ptr, rows, cols, out.ptr, dws.ptr, ws, None), "ts_hip_sum_dim0")
+    sync()
+    assert_bits_equal(out.get(), want, f"tall column sums {rows}x{cols}")

@@ -210,6 +210,6 @@ int launch_colsum(const float *x, const float *w, size_t rows, size_t cols, size
 
 // The column sum's second pass: out[c] = the chunk sums partial[k * cols + c]
 // added by groups as above, rounded to fp32.
-int launch_colsum_final(const double *partial, size_t chunks, size_t cols, float *out, hipStream_t s);
+int launch_colsum_final(double *partial, size_t chunks, size_t cols, float *out, hipStream_t s);
 
 }  // namespace tship

@@ -192,9 +192,75 @@ __global__ __launch_bounds__(kBlock) void colsum_final(const double *__restrict_
     if (gl == 0 && c < cols) out[c] = static_cast<float>(total);
 }
 
-int launch_colsum_final(const double *partial, size_t chunks, size_t cols, float *out, hipStream_t s) {
-    launch(colsum_final, dim3(static_cast<unsigned>((cols + 15) / 16)), dim3(kBlock), 0, s, partial, chunks, cols,
-           out);
+// Many groups (tall inputs): the group sums first, in parallel -- thread
+// (group g, column c) adds chunk sums 8g .. 8g+7 in order from +0, as
+// colsum_final's lanes do, and writes the result over chunk sum 8g (only that
+// thread reads or writes those slots) -- then colsum_groups_final adds them in
+// group order.  The same additions in the same order, so the same bits; the
+// serial part is one dependent add per group instead of a round of loads,
+// two barriers and 16 adds per 16 groups.
+__global__ __launch_bounds__(kBlock) void colsum_groups(double *__restrict__ partial, size_t chunks, size_t cols) {
+    constexpr int G = static_cast<int>(kColsumGroup);
+    const size_t groups = (chunks + G - 1) / G;
+    const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (t >= groups * cols) return;
+    const size_t g = t / cols, c = t % cols;
+    double v[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) v[j] = g * G + j < chunks ? partial[(g * G + j) * cols + c] : 0.0;
+    double sum = 0.0;
+#pragma unroll
+    for (int j = 0; j < G; ++j) sum += v[j];
+    partial[g * G * cols + c] = sum;
+}
+
+// A workgroup takes 16 columns; in rounds of 256 groups thread (gl, cl)
+// loads the group sums of groups g0 + 16*gl .. +15 (16 in flight) into LDS,
+// and the first lane of each column adds the round's 256 in group order.
+constexpr int kGroupsPerLane = 16;
+__global__ __launch_bounds__(kBlock) void colsum_groups_final(const double *__restrict__ partial, size_t chunks,
+                                                              size_t cols, float *__restrict__ out) {
+    constexpr int G = static_cast<int>(kColsumGroup), R = 16 * kGroupsPerLane;
+    __shared__ double gs[R][17];
+    const int cl = threadIdx.x & 15, gl = threadIdx.x >> 4;
+    const size_t c = static_cast<size_t>(blockIdx.x) * 16 + cl;
+    const size_t groups = (chunks + G - 1) / G;
+    double total = 0.0;
+    for (size_t g0 = 0; g0 < groups; g0 += R) {  // uniform
+        double v[kGroupsPerLane];
+#pragma unroll
+        for (int k = 0; k < kGroupsPerLane; ++k) {
+            const size_t g = g0 + static_cast<size_t>(gl) * kGroupsPerLane + k;
+            v[k] = (c < cols && g < groups) ? partial[g * G * cols + c] : 0.0;
+        }
+#pragma unroll
+        for (int k = 0; k < kGroupsPerLane; ++k) gs[gl * kGroupsPerLane + k][cl] = v[k];
+        __syncthreads();
+        if (gl == 0)
+            for (int j = 0; j < R; ++j) total += gs[j][cl];  // groups past the end add +0
+        __syncthreads();
+    }
+    if (gl == 0 && c < cols) out[c] = static_cast<float>(total);
+}
+
+// Past this many groups of chunk sums the group sums run as a pass of their own.
+constexpr size_t kColsumSerialGroups = 16;
+
+int launch_colsum_final(double *partial, size_t chunks, size_t cols, float *out, hipStream_t s) {
+    const size_t groups = (chunks + kColsumGroup - 1) / kColsumGroup;
+    const dim3 grid(static_cast<unsigned>((cols + 15) / 16));
+    if (groups <= kColsumSerialGroups) {
+        launch(colsum_final, grid, dim3(kBlock), 0, s, partial, chunks, cols, out);
+        return launch_status();
+    }
+    const size_t threads = groups * cols;
+    if ((threads + kBlock - 1) / kBlock > 0x7fffffffULL) return TS_HIP_EINVAL;
+    // the group sums overwrite chunk sums in place (partial is the caller's workspace)
+    launch(colsum_groups, dim3(static_cast<unsigned>((threads + kBlock - 1) / kBlock)), dim3(kBlock), 0, s, partial,
+           chunks, cols);
+    const int st = launch_status();
+    if (st) return st;
+    launch(colsum_groups_final, grid, dim3(kBlock), 0, s, partial, chunks, cols, out);
     return launch_status();
 }
 
