@@ -137,3 +137,29 @@ def test_training_chain_compiled_equals_interpreted(jit, oracle, n):
     for name, u, v in zip(("loss", "y", "ga", "gb", "gc"), got, want):
         assert_bits_equal(u, v, name)
     assert _stats(jit)[1] == 0, jit.ts_hip_map_jit_log()
+
+
+def test_a_training_loop_compiles_nothing_after_its_warm_up(jit):
+    # the step builds the same programs every time (the leaf gradients merge
+    # in a fixed order), so a loop with no synchronisation between steps
+    # compiles nothing after the warm-up
+    import train_station_amd as T
+    n = (1 << 20) + 64
+    a = T.Tensor.from_slice(normal(n, 51), [n]).with_requires_grad()
+    b = T.Tensor.from_slice(normal(n, 52), [n]).with_requires_grad()
+    c = T.Tensor.from_slice(uniform(n, 0.5, 2.0, 53), [n]).with_requires_grad()
+
+    def step():
+        loss = a.add_tensor(b).mul_tensor(c).sub_tensor(a.div_tensor(c)).relu().sum()
+        loss.backward()
+        T.clear_gradients()
+
+    jit.ts_hip_map_jit_mode(1)
+    for _ in range(3):
+        step()
+    T.synchronize()
+    before = _stats(jit)
+    for _ in range(60):
+        step()
+    T.synchronize()
+    assert _stats(jit) == before

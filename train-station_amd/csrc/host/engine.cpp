@@ -1,5 +1,6 @@
 // gradtrack engine: the recorded graph, the no-grad switch and the backward
 // worklist (gradtrack/engine.rs, gradtrack/no_grad_track.rs).
+#include <algorithm>
 #include <unordered_map>
 #include <utility>
 #include <vector>
@@ -114,10 +115,17 @@ void engine_backward(Tensor &root, const Tensor *grad_output) {
     }
     // The gradients left are the leaves'; those still deferred run now, in as
     // few passes as they fit (they share their inputs): backward returns with
-    // every gradient computed, as the reference's does.
-    std::vector<std::shared_ptr<Allocation>> deferred;
+    // every gradient computed, as the reference's does.  They are merged in
+    // tensor-id order: the map's own order follows its bucket history, and a
+    // different merge order is a different program (and, for the programs
+    // compiled at run time, a new compile) for the same step.
+    std::vector<std::pair<size_t, std::shared_ptr<Allocation>>> leaves;
     for (auto &kv : graph().gradients)
-        if (kv.second.allocation() && kv.second.allocation()->map) deferred.push_back(kv.second.allocation());
+        if (kv.second.allocation() && kv.second.allocation()->map) leaves.emplace_back(kv.first, kv.second.allocation());
+    std::sort(leaves.begin(), leaves.end(),
+              [](const auto &x, const auto &y) { return x.first < y.first; });
+    std::vector<std::shared_ptr<Allocation>> deferred;
+    for (auto &l : leaves) deferred.push_back(std::move(l.second));
     // (the root's seed, a deferred constant, reads no buffer and stays
     // deferred until read)
     if (root.grad_ref() && root.grad_ref()->allocation() && root.grad_ref()->allocation()->map &&
