@@ -715,36 +715,34 @@ struct DmaStage {
     static constexpr int NI = kBK / NW;  // DMA instructions per wave and operand tile
     static_assert(NI * NW == kBK, "waves must divide the 16 DMA instructions of a tile");
 
-    // Interior k tile.  Rows (columns) past the matrix edge are clamped to the
-    // last one: they only feed outputs that are never stored.
-    static __device__ __forceinline__ void dma(const float *__restrict__ P, int ld, int rows, int r0, int k0,
-                                               float *S, int wave, int lane) {
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int q = NI * wave + i;
-            const float *src;
-            if (KCONTIG) {
-                int row = r0 + q * 16 + (lane & 15);
-                row = row < rows ? row : rows - 1;
-                src = P + (size_t)row * ld + k0 + (lane >> 4) * 4;
-            } else {
-                const int last = (rows - 1) & ~3;  // ld % 4 == 0, so the chunk stays inside the row
-                int col = r0 + 4 * (lane ^ dswz(q));
-                col = col <= last ? col : last;
-                src = P + (size_t)(k0 + q) * ld + col;
-            }
-            // Issued as inline assembly: through the builtin the compiler makes
-            // every later LDS read wait for this load.  Completion is awaited
-            // explicitly (vmcnt) before the barrier that publishes the tile.
-            // M0 is listed as clobbered although the compiler treats it as
-            // reserved (and warns); nothing else in these kernels uses M0.
-            const unsigned lds = static_cast<unsigned>(reinterpret_cast<size_t>((lds_void *)(S + q * 256)));
+    // DMA instruction i (of NI) of a wave for an interior k tile.  Rows
+    // (columns) past the matrix edge are clamped to the last one: they only
+    // feed outputs that are never stored.
+    static __device__ __forceinline__ void one(const float *__restrict__ P, int ld, int rows, int r0, int k0,
+                                               float *S, int wave, int lane, int i) {
+        const int q = NI * wave + i;
+        const float *src;
+        if (KCONTIG) {
+            int row = r0 + q * 16 + (lane & 15);
+            row = row < rows ? row : rows - 1;
+            src = P + (size_t)row * ld + k0 + (lane >> 4) * 4;
+        } else {
+            const int last = (rows - 1) & ~3;  // ld % 4 == 0, so the chunk stays inside the row
+            int col = r0 + 4 * (lane ^ dswz(q));
+            col = col <= last ? col : last;
+            src = P + (size_t)(k0 + q) * ld + col;
+        }
+        // Issued as inline assembly: through the builtin the compiler makes
+        // every later LDS read wait for this load.  Completion is awaited
+        // explicitly (vmcnt) before the barrier that publishes the tile.
+        // M0 is listed as clobbered although the compiler treats it as
+        // reserved (and warns); nothing else in these kernels uses M0.
+        const unsigned lds = static_cast<unsigned>(reinterpret_cast<size_t>((lds_void *)(S + q * 256)));
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-            asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
-                         : "memory", "m0");
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+                     : "memory", "m0");
 #pragma clang diagnostic pop
-        }
     }
 
     // Partial last k tile: element loads with bounds checks, zeros outside.
@@ -784,20 +782,28 @@ struct DmaStage {
     }
 };
 
-// 256x256 tiles, WM x WN waves.  SCHED 1 spreads the next step pair's LDS
-// reads over the current pair's MFMAs; SCHED 0 issues them as one group
-// ahead of the MFMAs (measured per layout, see the launcher).  Each of the two
-// LDS stages holds SUB consecutive 16-k sub-tiles (one barrier per stage).
-template <bool TA, bool TB, int WM, int WN, int SCHED, int EPI, bool CS, int SUB = 1>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_f32_lds_dma(GemmArgs g) {
-    constexpr int BM = 256, BN = 256, NW = WM * WN;
+// 256x256 tiles, 2x4 waves (128x64 each, two per SIMD), three LDS stages of
+// 16 k.  A DMA or LDS read instruction waits at issue until the CU's address
+// unit or LDS takes it (about 16 cycles per 1 KB DMA instruction when one
+// wave issues, 45-60 when four do), and a wave issues in order, so with one
+// wave per SIMD each such stall idles the matrix core; two waves per SIMD
+// cover each other's.  Stage kt+2's DMA goes out during stage kt, one
+// instruction per 16 MFMAs, into the buffer stage kt-1 freed at the last
+// barrier, and is awaited a whole stage later.  A step pair is 4 groups of 4
+// MFMAs in (half, a, b) order; its first six MFMAs each carry one fragment
+// read of the next pair, and each pair's first group one DMA instruction.
+template <bool TA, bool TB, int EPI, bool CS>
+__global__ __launch_bounds__(512) void gemm_f32_lds_dma(GemmArgs g) {
+    constexpr int BM = 256, BN = 256, WM = 2, WN = 4, NW = WM * WN, NB = 3;
     constexpr int TMW = BM / WM, TNW = BN / WN, FM = TMW / 32, FN = TNW / 32, PAIRS = kBK / 4;
-    constexpr int SPAIRS = SUB * PAIRS;  // step pairs per stage
-    static_assert(SUB == 1 || SUB == 2, "one or two sub-tiles per stage");
+    constexpr int NI = kBK / NW, ND = 2 * NI;  // DMA instructions per wave and stage: A's, then B's
+    constexpr int GP = 2 * FM * FN / 4;        // groups of 4 MFMAs per step pair
+    static_assert(FM == 4 && FN == 2 && ND == PAIRS && GP == 4,
+                  "one DMA instruction per step pair; the next pair's six reads in the first six MFMAs");
     using SA = DmaStage<!TA, NW>;
     using SB = DmaStage<TB, NW>;
-    __shared__ __attribute__((aligned(16))) float As[2][SUB * kBK * BM];
-    __shared__ __attribute__((aligned(16))) float Bs[2][SUB * kBK * BN];
+    __shared__ __attribute__((aligned(16))) float As[NB][kBK * BM];
+    __shared__ __attribute__((aligned(16))) float Bs[NB][kBK * BN];
 
     const float *Ap = g.A, *Bp = g.B;
     float *Cp = g.C;
@@ -852,116 +858,117 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f32_lds_dma(GemmArgs g) {
         if (j0 + cs_c < g.N) g.colsum_part[(size_t)chunk * g.N + j0 + cs_c] = cs_s;
         cs_s = 0.0;
     };
-
-    const int nfull = g.K / (SUB * kBK);  // whole stages; the rest, sub-tile by sub-tile after the loop
-    auto dma = [&](int kt, int buf) {
-#pragma unroll
-        for (int s = 0; s < SUB; ++s) {
-            SA::dma(Ap, g.lda, g.M, i0, (kt * SUB + s) * kBK, As[buf] + s * kBK * BM, wave, lane);
-            SB::dma(Bp, g.ldb, g.N, j0, (kt * SUB + s) * kBK, Bs[buf] + s * kBK * BN, wave, lane);
+    // the 4 k rows of B of step pair p of k tile kt (in buffer buf), added
+    // before the barrier that frees the buffer; a chunk's fourth k tile closes it
+    auto cs_pair = [&](int kt, int buf, int p) {
+        if (cs_wave && cs_mine(kt)) {
+            cs_rows(Bs[buf], 4 * p, 4 * p + 4);
+            if (p == PAIRS - 1 && (kt & 3) == 3) cs_flush(kt >> 2);
         }
+    };
+
+    const int nfull = g.K / kBK;  // whole k tiles; a partial last one after the loop
+    auto dma1 = [&](int kt, int buf, int i) {
+        if (i < NI) SA::one(Ap, g.lda, g.M, i0, kt * kBK, As[buf], wave, lane, i);
+        else SB::one(Bp, g.ldb, g.N, j0, kt * kBK, Bs[buf], wave, lane, i - NI);
     };
     f2v F[2][FM + FN];
-    auto rd = [&](int buf, int j, f2v (&f)[FM + FN]) {  // step pair j of a stage
-        const float *Sa = As[buf] + (j / PAIRS) * kBK * BM;
-        const float *Sb = Bs[buf] + (j / PAIRS) * kBK * BN;
-#pragma unroll
-        for (int a = 0; a < FM; ++a) f[a] = SA::frag(Sa, j % PAIRS, lhalf, wm * TMW + a * 32 + lrow);
-#pragma unroll
-        for (int b = 0; b < FN; ++b) f[FM + b] = SB::frag(Sb, j % PAIRS, lhalf, wn * TNW + b * 32 + lrow);
+    auto rd1 = [&](int buf, int j, f2v (&f)[FM + FN], int k) {  // fragment k of step pair j
+        if (k < FM) f[k] = SA::frag(As[buf], j, lhalf, wm * TMW + k * 32 + lrow);
+        else f[k] = SB::frag(Bs[buf], j, lhalf, wn * TNW + (k - FM) * 32 + lrow);
     };
-    auto mm = [&](const f2v (&f)[FM + FN]) {
-#pragma unroll
-        for (int a = 0; a < FM; ++a)
-#pragma unroll
-            for (int b = 0; b < FN; ++b)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(f[a].x, f[FM + b].x, acc[a][b], 0, 0, 0);
-#pragma unroll
-        for (int a = 0; a < FM; ++a)
-#pragma unroll
-            for (int b = 0; b < FN; ++b)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(f[a].y, f[FM + b].y, acc[a][b], 0, 0, 0);
+    auto mfma = [&](const f2v (&f)[FM + FN], int idx) {  // MFMA idx of a step pair, (half, a, b) order
+        const int h = idx / (FM * FN), a = (idx / FN) % FM, b = idx % FN;
+        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(h ? f[a].y : f[a].x, h ? f[FM + b].y : f[FM + b].x,
+                                                         acc[a][b], 0, 0, 0);
     };
-    auto order = [&]() {
-        if (SCHED == 1) {
+    // Step pair p of the current k tile from registers f; fragments of step
+    // pair jn of buffer rb into n; DMA instruction p of k tile ks into dst.
+    auto pair = [&](const f2v (&f)[FM + FN], f2v (&n)[FM + FN], int rb, int jn, int p, int ks, int dst) {
 #pragma unroll
-            for (int i = 0; i < FM + FN; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        for (int grp = 0; grp < GP; ++grp) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                mfma(f, grp * 4 + m);
+                if (grp * 4 + m < FM + FN) rd1(rb, jn, n, grp * 4 + m);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, 2 * FM * FN - (FM + FN), 0);
+            if (grp == 0) {
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+                }
+            } else if (grp == 1) {
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    if (4 + m < FM + FN) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (grp == 0) dma1(ks, dst, p);
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    // Pipeline: LDS buffer kt&1 holds stage kt; stage kt+1 is in flight into
-    // the other buffer; the registers F[j&1] hold step pair j.  Each wave
-    // waits for its own DMA (vmcnt) before the barrier that publishes a stage.
-    // CS: the 4 k rows of B of step pair p of stage kt (sub-tile t16 of 16 k)
-    // are added before the barrier that frees the buffer; a chunk's fourth
-    // sub-tile closes it.
-    auto cs_pair = [&](int kt, int p) {
-        const int t16 = kt * SUB + p / PAIRS, jj = p % PAIRS;
-        if (cs_wave && cs_mine(t16)) {
-            cs_rows(Bs[kt & 1] + (p / PAIRS) * kBK * BN, 4 * jj, 4 * jj + 4);
-            if (jj == PAIRS - 1 && (t16 & 3) == 3) cs_flush(t16 >> 2);
-        }
-    };
+    // Pipeline: buffer kt % 3 holds k tile kt; k tile kt+1 has landed or is
+    // landing in the next; k tile kt+2 is loaded into the third during this
+    // one (its buffer held kt-1, whose reads all precede the last barrier).
+    // Each wave waits for its own DMA (vmcnt, loads complete in order) before
+    // the barrier that publishes a k tile: of the 2*ND instructions in flight
+    // there, the last ND-1 are k tile kt+2's.
     if (nfull > 0) {
-        dma(0, 0);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (nfull > 1) dma(1, 1);
-        rd(0, 0, F[0]);
-    }
-    for (int kt = 0; kt < nfull; ++kt) {
-        const int cur = kt & 1;
 #pragma unroll
-        for (int j = 0; j < SPAIRS - 1; ++j) {
-            rd(cur, j + 1, F[(j + 1) & 1]);
-            if (SCHED == 0) __builtin_amdgcn_sched_barrier(0);
-            mm(F[j & 1]);
-            order();
-            __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < ND; ++i) dma1(0, 0, i);
+#pragma unroll
+        for (int i = 0; i < ND; ++i) dma1(nfull > 1 ? 1 : 0, 1, i);
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // ND: k tile 0 has landed
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < FM + FN; ++k) rd1(0, 0, F[0], k);
+    }
+    int cur = 0;
+    for (int kt = 0; kt < nfull; ++kt) {
+        const int nxt = cur == NB - 1 ? 0 : cur + 1, dst = nxt == NB - 1 ? 0 : nxt + 1;
+        // past the end the DMA repeats the last k tile into the free buffer
+        // and the last read takes it: both stay in bounds, neither is used
+        const int ks = kt + 2 < nfull ? kt + 2 : nfull - 1;
+#pragma unroll
+        for (int j = 0; j < PAIRS - 1; ++j) {
+            pair(F[j & 1], F[(j + 1) & 1], cur, j + 1, j, ks, dst);
             if (CS) {
-                cs_pair(kt, j);
-                if (j == SPAIRS - 2) cs_pair(kt, j + 1);
+                cs_pair(kt, cur, j);
+                if (j == PAIRS - 2) cs_pair(kt, cur, j + 1);
             }
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(3)" ::: "memory");  // ND - 1
         __syncthreads();
-        // Stage kt+1 is published and every read of buffer cur is done: read
-        // the next stage's first pair and start stage kt+2 into buffer cur,
-        // then run this stage's last pair.  On the last stages the DMA repeats
-        // stage nfull-1 and the read takes an idle buffer: both stay in bounds.
-        rd(cur ^ 1, 0, F[0]);
-        dma(kt + 2 < nfull ? kt + 2 : nfull - 1, cur);
-        if (SCHED == 0) __builtin_amdgcn_sched_barrier(0);
-        mm(F[(SPAIRS - 1) & 1]);
-        order();
-        __builtin_amdgcn_sched_barrier(0);
+        pair(F[(PAIRS - 1) & 1], F[0], nxt, 0, PAIRS - 1, ks, dst);
+        cur = nxt;
     }
-    // the sub-tiles past the last whole stage (the last may be partial), one
-    // at a time through buffer nfull&1 (idle: every DMA has landed and every
-    // read passed the barrier)
-    const int buf = nfull & 1;
-    for (int t16 = nfull * SUB; t16 * kBK < g.K; ++t16) {  // uniform
+    // the partial last k tile (K % 16), with bounds checks, through buffer 0
+    // (idle: every DMA has landed and every read passed the barrier)
+    if (nfull * kBK < g.K) {  // uniform
+        const int t16 = nfull;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        SA::guarded(Ap, g.lda, g.M, g.K, i0, t16 * kBK, As[buf], wave, lane);
-        SB::guarded(Bp, g.ldb, g.N, g.K, j0, t16 * kBK, Bs[buf], wave, lane);
+        SA::guarded(Ap, g.lda, g.M, g.K, i0, t16 * kBK, As[0], wave, lane);
+        SB::guarded(Bp, g.ldb, g.N, g.K, j0, t16 * kBK, Bs[0], wave, lane);
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < PAIRS; ++j) {
-            rd(buf, j, F[0]);
-            mm(F[0]);
+#pragma unroll
+            for (int k = 0; k < FM + FN; ++k) rd1(0, j, F[0], k);
+#pragma unroll
+            for (int m = 0; m < 2 * FM * FN; ++m) mfma(F[0], m);
         }
         if (cs_wave && cs_mine(t16)) {  // zeros past K add nothing
-            cs_rows(Bs[buf], 0, kBK);
+            cs_rows(Bs[0], 0, kBK);
             if ((t16 & 3) == 3) cs_flush(t16 >> 2);
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA outstanding at exit
-    if (CS) {  // the last chunk, unless its fourth sub-tile closed it
+    if (CS) {  // the last chunk, unless its fourth k tile closed it
         const int last = (g.K - 1) / kBK;
         if (cs_wave && cs_mine(last) && (last & 3) != 3) cs_flush(last >> 2);
     }
@@ -1029,39 +1036,33 @@ __global__ __launch_bounds__(kBlock) void splitk_sum(const float *__restrict__ P
     C[i * ldc + j] = epilogue(e, acc, static_cast<int>(i), static_cast<int>(j));
 }
 
-template <bool TA, bool TB, int WM, int WN, int SCHED, int EPI, bool CS = false, int SUB = 1>
+template <bool TA, bool TB, int EPI, bool CS = false>
 static void launch_dma(GemmArgs g, hipStream_t s, unsigned batches) {
     g.tiles_m = (g.M + 255) / 256;
     g.tiles_n = (g.N + 255) / 256;
     g.tiles = g.tiles_m * g.tiles_n;
     dim3 grid(static_cast<unsigned>(g.tiles) * batches);
-    dim3 block(64 * WM * WN);
-    launch((gemm_f32_lds_dma<TA, TB, WM, WN, SCHED, EPI, CS, SUB>), grid, block, 0, s, g);
+    dim3 block(512);
+    launch((gemm_f32_lds_dma<TA, TB, EPI, CS>), grid, block, 0, s, g);
 }
 
-// The DMA kernel of one layout: wave grid, LDS-read order and sub-tiles per
-// stage per layout, the fastest measured at 8192x4096x4096 (only these
-// instantiations exist; two sub-tiles per stage measured slower for NN and NT,
-// about 1.5% faster for TN).  A
-// mask epilogue on NN takes the 8-wave grid: the 4-wave one holds its
-// accumulators in AGPRs and has no registers left for a row of mask values
-// (it spills); bias and relu alone fit.
+// The DMA kernel of one layout and epilogue (only these instantiations exist).
 static void launch_dma_layout(int ta, int tb, const GemmArgs &g, hipStream_t s, unsigned nb) {
     const bool epi = g.bias || g.mask || g.relu;
     if (!ta && !tb) {
-        if (g.mask) launch_dma<false, false, 2, 4, 1, kEpiAll>(g, s, nb);
-        else if (epi) launch_dma<false, false, 2, 2, 1, kEpiBiasRelu>(g, s, nb);
-        else launch_dma<false, false, 2, 2, 1, kEpiNone>(g, s, nb);
+        if (g.mask) launch_dma<false, false, kEpiAll>(g, s, nb);
+        else if (epi) launch_dma<false, false, kEpiBiasRelu>(g, s, nb);
+        else launch_dma<false, false, kEpiNone>(g, s, nb);
     } else if (!ta && tb) {
-        if (epi) launch_dma<false, true, 2, 4, 0, kEpiAll>(g, s, nb);
-        else launch_dma<false, true, 2, 4, 0, kEpiNone>(g, s, nb);
-    } else if (ta && !tb) {  // two sub-tiles per stage: measured faster for this layout only
-        if (g.colsum) launch_dma<true, false, 2, 4, 1, kEpiNone, true, 2>(g, s, nb);  // dW with db
-        else if (epi) launch_dma<true, false, 2, 4, 1, kEpiAll, false, 2>(g, s, nb);
-        else launch_dma<true, false, 2, 4, 1, kEpiNone, false, 2>(g, s, nb);
+        if (epi) launch_dma<false, true, kEpiAll>(g, s, nb);
+        else launch_dma<false, true, kEpiNone>(g, s, nb);
+    } else if (ta && !tb) {
+        if (g.colsum) launch_dma<true, false, kEpiNone, true>(g, s, nb);  // dW with db
+        else if (epi) launch_dma<true, false, kEpiAll>(g, s, nb);
+        else launch_dma<true, false, kEpiNone>(g, s, nb);
     } else {
-        if (epi) launch_dma<true, true, 2, 4, 1, kEpiAll>(g, s, nb);
-        else launch_dma<true, true, 2, 4, 1, kEpiNone>(g, s, nb);
+        if (epi) launch_dma<true, true, kEpiAll>(g, s, nb);
+        else launch_dma<true, true, kEpiNone>(g, s, nb);
     }
 }
 
