@@ -782,28 +782,36 @@ struct DmaStage {
     }
 };
 
-// 256x256 tiles, 2x4 waves (128x64 each, two per SIMD), three LDS stages of
-// 16 k.  A DMA or LDS read instruction waits at issue until the CU's address
-// unit or LDS takes it (about 16 cycles per 1 KB DMA instruction when one
-// wave issues, 45-60 when four do), and a wave issues in order, so with one
-// wave per SIMD each such stall idles the matrix core; two waves per SIMD
-// cover each other's.  Stage kt+2's DMA goes out during stage kt, one
-// instruction per 16 MFMAs, into the buffer stage kt-1 freed at the last
-// barrier, and is awaited a whole stage later.  A step pair is 4 groups of 4
-// MFMAs in (half, a, b) order; its first six MFMAs each carry one fragment
-// read of the next pair, and each pair's first group one DMA instruction.
-template <bool TA, bool TB, int EPI, bool CS>
+// 256x256 tiles, 2x4 waves (128x64 each, two per SIMD).  A DMA or LDS read
+// instruction waits at issue until the CU's address unit or LDS takes it
+// (about 16 cycles per 1 KB DMA instruction when one wave issues, 45-60 when
+// four do), and a wave issues in order, so with one wave per SIMD each such
+// stall idles the matrix core; two waves per SIMD cover each other's.  A step
+// pair is 4 groups of 4 MFMAs in (half, a, b) order; its first six MFMAs each
+// carry one fragment read of the next pair.  The DMA instructions are spread
+// over the MFMAs:
+//   SUB 1: three LDS stages of one 16-k tile; k tile kt+2's DMA goes out
+//     during k tile kt, one instruction in each step pair's first group, into
+//     the buffer k tile kt-1 freed at the last barrier, and is awaited a
+//     whole stage later.
+//   SUB 2: two stages of two 16-k tiles (half the barriers, for long k);
+//     stage kt+1's DMA goes out during the first half of stage kt, two
+//     instructions per step pair, into the other buffer, and is awaited at
+//     the stage's end (half a stage after the last instruction).
+template <bool TA, bool TB, int EPI, bool CS, int SUB>
 __global__ __launch_bounds__(512) void gemm_f32_lds_dma(GemmArgs g) {
-    constexpr int BM = 256, BN = 256, WM = 2, WN = 4, NW = WM * WN, NB = 3;
+    constexpr int BM = 256, BN = 256, WM = 2, WN = 4, NW = WM * WN, NB = SUB == 1 ? 3 : 2;
     constexpr int TMW = BM / WM, TNW = BN / WN, FM = TMW / 32, FN = TNW / 32, PAIRS = kBK / 4;
-    constexpr int NI = kBK / NW, ND = 2 * NI;  // DMA instructions per wave and stage: A's, then B's
+    constexpr int SP = SUB * PAIRS;            // step pairs per stage
+    constexpr int NI = kBK / NW, ND = 2 * NI;  // DMA instructions per wave and k tile: A's, then B's
     constexpr int GP = 2 * FM * FN / 4;        // groups of 4 MFMAs per step pair
+    static_assert(SUB == 1 || SUB == 2, "one or two k tiles per stage");
     static_assert(FM == 4 && FN == 2 && ND == PAIRS && GP == 4,
-                  "one DMA instruction per step pair; the next pair's six reads in the first six MFMAs");
+                  "DMA slots: one per step pair (SUB 1) or two in each of the first half's (SUB 2)");
     using SA = DmaStage<!TA, NW>;
     using SB = DmaStage<TB, NW>;
-    __shared__ __attribute__((aligned(16))) float As[NB][kBK * BM];
-    __shared__ __attribute__((aligned(16))) float Bs[NB][kBK * BN];
+    __shared__ __attribute__((aligned(16))) float As[NB][SUB * kBK * BM];
+    __shared__ __attribute__((aligned(16))) float Bs[NB][SUB * kBK * BN];
 
     const float *Ap = g.A, *Bp = g.B;
     float *Cp = g.C;
@@ -858,32 +866,36 @@ __global__ __launch_bounds__(512) void gemm_f32_lds_dma(GemmArgs g) {
         if (j0 + cs_c < g.N) g.colsum_part[(size_t)chunk * g.N + j0 + cs_c] = cs_s;
         cs_s = 0.0;
     };
-    // the 4 k rows of B of step pair p of k tile kt (in buffer buf), added
+    // the 4 k rows of B of step pair p of stage st (in buffer buf), added
     // before the barrier that frees the buffer; a chunk's fourth k tile closes it
-    auto cs_pair = [&](int kt, int buf, int p) {
-        if (cs_wave && cs_mine(kt)) {
-            cs_rows(Bs[buf], 4 * p, 4 * p + 4);
-            if (p == PAIRS - 1 && (kt & 3) == 3) cs_flush(kt >> 2);
+    auto cs_pair = [&](int st, int buf, int p) {
+        const int t16 = st * SUB + p / PAIRS, jj = p % PAIRS;
+        if (cs_wave && cs_mine(t16)) {
+            cs_rows(Bs[buf] + (p / PAIRS) * kBK * BN, 4 * jj, 4 * jj + 4);
+            if (jj == PAIRS - 1 && (t16 & 3) == 3) cs_flush(t16 >> 2);
         }
     };
 
-    const int nfull = g.K / kBK;  // whole k tiles; a partial last one after the loop
-    auto dma1 = [&](int kt, int buf, int i) {
-        if (i < NI) SA::one(Ap, g.lda, g.M, i0, kt * kBK, As[buf], wave, lane, i);
-        else SB::one(Bp, g.ldb, g.N, j0, kt * kBK, Bs[buf], wave, lane, i - NI);
+    const int nfull = g.K / (SUB * kBK);  // whole stages; the k tiles past them after the loop
+    auto dma1 = [&](int st, int buf, int i) {  // instruction i of stage st: k tile i / ND, A's then B's
+        const int s = i / ND, q = i % ND, k0 = (st * SUB + s) * kBK;
+        if (q < NI) SA::one(Ap, g.lda, g.M, i0, k0, As[buf] + s * kBK * BM, wave, lane, q);
+        else SB::one(Bp, g.ldb, g.N, j0, k0, Bs[buf] + s * kBK * BN, wave, lane, q - NI);
     };
     f2v F[2][FM + FN];
-    auto rd1 = [&](int buf, int j, f2v (&f)[FM + FN], int k) {  // fragment k of step pair j
-        if (k < FM) f[k] = SA::frag(As[buf], j, lhalf, wm * TMW + k * 32 + lrow);
-        else f[k] = SB::frag(Bs[buf], j, lhalf, wn * TNW + (k - FM) * 32 + lrow);
+    auto rd1 = [&](int buf, int j, f2v (&f)[FM + FN], int k) {  // fragment k of step pair j of a stage
+        const float *Sa = As[buf] + (j / PAIRS) * kBK * BM, *Sb = Bs[buf] + (j / PAIRS) * kBK * BN;
+        if (k < FM) f[k] = SA::frag(Sa, j % PAIRS, lhalf, wm * TMW + k * 32 + lrow);
+        else f[k] = SB::frag(Sb, j % PAIRS, lhalf, wn * TNW + (k - FM) * 32 + lrow);
     };
     auto mfma = [&](const f2v (&f)[FM + FN], int idx) {  // MFMA idx of a step pair, (half, a, b) order
         const int h = idx / (FM * FN), a = (idx / FN) % FM, b = idx % FN;
         acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(h ? f[a].y : f[a].x, h ? f[FM + b].y : f[FM + b].x,
                                                          acc[a][b], 0, 0, 0);
     };
-    // Step pair p of the current k tile from registers f; fragments of step
-    // pair jn of buffer rb into n; DMA instruction p of k tile ks into dst.
+    // Step pair p of the current stage from registers f; fragments of step
+    // pair jn of buffer rb into n; this pair's DMA instructions of stage ks
+    // into dst.
     auto pair = [&](const f2v (&f)[FM + FN], f2v (&n)[FM + FN], int rb, int jn, int p, int ks, int dst) {
 #pragma unroll
         for (int grp = 0; grp < GP; ++grp) {
@@ -906,50 +918,60 @@ __global__ __launch_bounds__(512) void gemm_f32_lds_dma(GemmArgs g) {
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
-            if (grp == 0) dma1(ks, dst, p);
+            if (SUB == 1 && grp == 0) dma1(ks, dst, p);
+            if (SUB == 2 && p < PAIRS && (grp == 0 || grp == 2)) dma1(ks, dst, 2 * p + grp / 2);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    // Pipeline: buffer kt % 3 holds k tile kt; k tile kt+1 has landed or is
-    // landing in the next; k tile kt+2 is loaded into the third during this
-    // one (its buffer held kt-1, whose reads all precede the last barrier).
-    // Each wave waits for its own DMA (vmcnt, loads complete in order) before
-    // the barrier that publishes a k tile: of the 2*ND instructions in flight
-    // there, the last ND-1 are k tile kt+2's.
+    // Pipeline (SUB 1): buffer kt % 3 holds k tile kt; k tile kt+1 has landed
+    // or is landing in the next; k tile kt+2 is loaded into the third during
+    // this one (its buffer held kt-1, whose reads all precede the last
+    // barrier).  Each wave waits for its own DMA (vmcnt; loads complete in
+    // order) before the barrier that publishes a stage: of the 2*ND
+    // instructions in flight there, the last ND-1 are k tile kt+2's.
+    // (SUB 2): buffer kt & 1 holds stage kt, stage kt+1 is loaded into the
+    // other during its first half, and all of it is awaited (vmcnt(0)).
     if (nfull > 0) {
 #pragma unroll
-        for (int i = 0; i < ND; ++i) dma1(0, 0, i);
+        for (int i = 0; i < SUB * ND; ++i) dma1(0, 0, i);
+        if (SUB == 1) {
 #pragma unroll
-        for (int i = 0; i < ND; ++i) dma1(nfull > 1 ? 1 : 0, 1, i);
-        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // ND: k tile 0 has landed
+            for (int i = 0; i < ND; ++i) dma1(nfull > 1 ? 1 : 0, 1, i);
+            asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // ND: k tile 0 has landed
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < FM + FN; ++k) rd1(0, 0, F[0], k);
     }
     int cur = 0;
     for (int kt = 0; kt < nfull; ++kt) {
-        const int nxt = cur == NB - 1 ? 0 : cur + 1, dst = nxt == NB - 1 ? 0 : nxt + 1;
-        // past the end the DMA repeats the last k tile into the free buffer
+        const int nxt = cur == NB - 1 ? 0 : cur + 1;
+        const int dst = SUB == 1 ? (nxt == NB - 1 ? 0 : nxt + 1) : nxt;
+        // past the end the DMA repeats the last stage into the free buffer
         // and the last read takes it: both stay in bounds, neither is used
-        const int ks = kt + 2 < nfull ? kt + 2 : nfull - 1;
+        const int ahead = kt + (SUB == 1 ? 2 : 1);
+        const int ks = ahead < nfull ? ahead : nfull - 1;
 #pragma unroll
-        for (int j = 0; j < PAIRS - 1; ++j) {
+        for (int j = 0; j < SP - 1; ++j) {
             pair(F[j & 1], F[(j + 1) & 1], cur, j + 1, j, ks, dst);
             if (CS) {
                 cs_pair(kt, cur, j);
-                if (j == PAIRS - 2) cs_pair(kt, cur, j + 1);
+                if (j == SP - 2) cs_pair(kt, cur, j + 1);
             }
         }
-        asm volatile("s_waitcnt vmcnt(3)" ::: "memory");  // ND - 1
+        if (SUB == 1) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");  // ND - 1
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        pair(F[(PAIRS - 1) & 1], F[0], nxt, 0, PAIRS - 1, ks, dst);
+        pair(F[(SP - 1) & 1], F[0], nxt, 0, SP - 1, ks, dst);
         cur = nxt;
     }
-    // the partial last k tile (K % 16), with bounds checks, through buffer 0
-    // (idle: every DMA has landed and every read passed the barrier)
-    if (nfull * kBK < g.K) {  // uniform
-        const int t16 = nfull;
+    // the k tiles past the last whole stage (the last may be partial), one at
+    // a time with bounds checks through buffer 0 (idle: every DMA has landed
+    // and every read passed the barrier)
+    for (int t16 = nfull * SUB; t16 * kBK < g.K; ++t16) {  // uniform
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         SA::guarded(Ap, g.lda, g.M, g.K, i0, t16 * kBK, As[0], wave, lane);
@@ -1036,17 +1058,19 @@ __global__ __launch_bounds__(kBlock) void splitk_sum(const float *__restrict__ P
     C[i * ldc + j] = epilogue(e, acc, static_cast<int>(i), static_cast<int>(j));
 }
 
-template <bool TA, bool TB, int EPI, bool CS = false>
+template <bool TA, bool TB, int EPI, bool CS = false, int SUB = 1>
 static void launch_dma(GemmArgs g, hipStream_t s, unsigned batches) {
     g.tiles_m = (g.M + 255) / 256;
     g.tiles_n = (g.N + 255) / 256;
     g.tiles = g.tiles_m * g.tiles_n;
     dim3 grid(static_cast<unsigned>(g.tiles) * batches);
     dim3 block(512);
-    launch((gemm_f32_lds_dma<TA, TB, EPI, CS>), grid, block, 0, s, g);
+    launch((gemm_f32_lds_dma<TA, TB, EPI, CS, SUB>), grid, block, 0, s, g);
 }
 
-// The DMA kernel of one layout and epilogue (only these instantiations exist).
+// The DMA kernel of one layout and epilogue (only these instantiations exist):
+// two k tiles per stage for TN, whose k is the batch (long), one otherwise,
+// the faster measured per layout.
 static void launch_dma_layout(int ta, int tb, const GemmArgs &g, hipStream_t s, unsigned nb) {
     const bool epi = g.bias || g.mask || g.relu;
     if (!ta && !tb) {
@@ -1057,9 +1081,9 @@ static void launch_dma_layout(int ta, int tb, const GemmArgs &g, hipStream_t s, 
         if (epi) launch_dma<false, true, kEpiAll>(g, s, nb);
         else launch_dma<false, true, kEpiNone>(g, s, nb);
     } else if (ta && !tb) {
-        if (g.colsum) launch_dma<true, false, kEpiNone, true>(g, s, nb);  // dW with db
-        else if (epi) launch_dma<true, false, kEpiAll>(g, s, nb);
-        else launch_dma<true, false, kEpiNone>(g, s, nb);
+        if (g.colsum) launch_dma<true, false, kEpiNone, true, 2>(g, s, nb);  // dW with db
+        else if (epi) launch_dma<true, false, kEpiAll, false, 2>(g, s, nb);
+        else launch_dma<true, false, kEpiNone, false, 2>(g, s, nb);
     } else {
         if (epi) launch_dma<true, true, kEpiAll>(g, s, nb);
         else launch_dma<true, true, kEpiNone>(g, s, nb);
