@@ -514,6 +514,27 @@ int ts_hip_gemm_colsum_bsum(int trans_a, size_t M, size_t N, size_t K, const flo
                             size_t ldc, float *colsum, const ts_hip_operand_xf *xs, float *bsum, int mean,
                             void *stream);
 
+/* Launch groups (no counterpart in the reference, whose matmul backward,
+ * grad_fn/ops/matmul.rs:68-80, runs its two products one after the other).
+ * Between ts_hip_launch_group_begin(stream) and ts_hip_launch_group_end(stream)
+ * the calling thread's products on `stream` that take the narrow kernel (few
+ * output columns: ts_hip_gemm_takes_sub, or the column-sum / bsum forms there)
+ * or the one-k-tile kernel (K <= 16) are held, at most two; any other work on
+ * the stream -- another launch, a copy, an event, a synchronisation -- runs
+ * them first, in the order they were issued.  At the end one of each runs as
+ * one launch, their workgroups side by side, when the pair is one the library
+ * builds (an MLP backward's dW with its bias gradient and, at its widest
+ * workgroups, K >= 1024, its dX with relu's backward mask); otherwise what is
+ * held is launched as issued.  Same results either way.  The products of a
+ * group must not read each other's outputs (the caller's contract: a matmul
+ * backward's dX and dW read only the forward's values and the incoming
+ * gradient).  Entry points called inside a group return TS_HIP_OK for a held
+ * launch; errors of the launch come from _end.  One group per thread at a
+ * time: _begin inside an open group and _end on another stream are
+ * TS_HIP_EINVAL.  Allocates nothing. */
+int ts_hip_launch_group_begin(void *stream);
+int ts_hip_launch_group_end(void *stream);
+
 /* Batched C[b] = op(A[b]) . op(B[b]) (matmul/mod.rs:634-760 batched_matmul and
  * the batched backward of grad_fn/ops/matmul.rs:150-219) on the same MFMA
  * tiles: a batch grid of batch_rank axes (<= 6) with sizes batch_dims; the A /

@@ -296,10 +296,11 @@ def _mse_loss(x, t, ps):
 
 @pytest.mark.parametrize("read_first", [False, True])
 def test_config4_step_launches(T, read_first):
-    # the loss read after backward: six launches (two forward products, the
-    # last with the MSE's subtraction; dX2, dW2 with db2 and the loss, dW1
-    # with db1; Adam), no elementwise pass; read before backward: its own
-    # pass.  The same bits as the op-by-op run either way.
+    # the loss read after backward: five launches (two forward products, the
+    # last with the MSE's subtraction; dX2 and dW2 with db2 and the loss as
+    # one launch of a launch group; dW1 with db1; Adam), no elementwise pass;
+    # read before backward: its own pass.  The same bits as the op-by-op run
+    # either way.
     out, counts = {}, {}
     for on in (True, False):
         T.set_fusion(on)
@@ -326,9 +327,9 @@ def test_config4_step_launches(T, read_first):
                 losses.append(loss.value())
         out[on] = (losses, [p.data() for p in ps])
     if read_first:
-        assert counts[True]["GEMM"] == 5 and counts[True]["ADAM"] == 1, counts
+        assert counts[True]["GEMM"] == 4 and counts[True]["ADAM"] == 1, counts
     else:
-        assert counts[True] == {"GEMM": 5, "ELEMENTWISE": 0, "REDUCTION": 0, "ADAM": 1}, counts
+        assert counts[True] == {"GEMM": 4, "ELEMENTWISE": 0, "REDUCTION": 0, "ADAM": 1}, counts
     assert out[True][0] == out[False][0]
     for i, (a, b) in enumerate(zip(out[True][1], out[False][1])):
         assert_bits_equal(a, b, f"param {i} after 3 steps")

@@ -154,6 +154,8 @@ HIP_SIGNATURES = {
     "ts_hip_gemm_colsum_workspace_floats": (SZ, [_c.c_int, SZ, SZ, SZ]),
     "ts_hip_gemm_colsum": (_c.c_int, [_c.c_int, SZ, SZ, SZ, VP, SZ, VP, SZ, VP, SZ, VP, VP, SZ, VP]),
     "ts_hip_gemm_takes_xf": (_c.c_int, [_c.c_int, _c.c_int, SZ, SZ, SZ, _c.c_int]),
+    "ts_hip_launch_group_begin": (_c.c_int, [VP]),
+    "ts_hip_launch_group_end": (_c.c_int, [VP]),
     "ts_hip_gemm_takes_bsum": (_c.c_int, [_c.c_int, SZ, SZ, SZ]),
     "ts_hip_gemm_colsum_bsum": (_c.c_int, [_c.c_int, SZ, SZ, SZ, VP, SZ, VP, VP, VP, VP, SZ, VP, VP, VP,
                                            _c.c_int, VP]),

@@ -172,6 +172,7 @@ float *Allocation::get() {
     else if (colsum) materialize_colsum(*this);
     else if (transpose) materialize_transpose(*this);
     else if (reduce) materialize_reduce(*this);
+    else if (sibling) run_sibling(*this);
     DevicePool::get().note_use(ptr_);
     return ptr_;
 }
@@ -186,6 +187,7 @@ void Allocation::before_write() {
             else if (r->colsum) materialize_colsum(*r);
             else if (r->transpose) materialize_transpose(*r);
             else if (r->reduce) materialize_reduce(*r);
+            else if (r->sibling) run_sibling(*r);
         }
 }
 

@@ -420,40 +420,122 @@ std::shared_ptr<Allocation> pending_sum_of(const std::shared_ptr<Allocation> &x,
     return nullptr;
 }
 
-void launch_product(const PendingGemm &p, float *C, bool with_epilogue) {
+// A product's operands as its launch reads them: fetched (deferred inputs
+// run now), an operand that is a deferred chain over one buffer read as that
+// buffer with the chain applied as it is loaded.
+struct ProductOperands {
+    const float *A = nullptr, *B = nullptr, *bias = nullptr, *sub = nullptr, *mask = nullptr;
+    ts_hip_operand_xf xa{}, xb{};
+    bool fa = false, fb = false;
+};
+
+ProductOperands product_operands(const PendingGemm &p, bool with_epilogue) {
+    ProductOperands o;
     if (with_epilogue && p.sub) {  // the narrow kernel's subtraction (no operand transforms)
-        const float *A = p.A->get(), *B = p.B->get();
-        const float *bias = p.bias ? p.bias->get() : nullptr;
-        const float *sub = p.sub->get();
-        const float *mask = p.mask ? p.mask->get() : nullptr;
-        DevicePool::get().note_use(C);
+        o.A = p.A->get();
+        o.B = p.B->get();
+        o.bias = p.bias ? p.bias->get() : nullptr;
+        o.sub = p.sub->get();
+        o.mask = p.mask ? p.mask->get() : nullptr;
+        return o;
+    }
+    std::shared_ptr<Allocation> la, lb;
+    const bool takes = ts_hip_gemm_takes_xf(p.ta, p.tb, p.M, p.N, p.K, 0) != 0;
+    o.fa = takes && operand_xf(p.A, la, o.xa);
+    o.fb = takes && operand_xf(p.B, lb, o.xb);
+    o.A = o.fa ? la->get() : p.A->get();
+    o.B = o.fb ? lb->get() : p.B->get();
+    o.bias = with_epilogue && p.bias ? p.bias->get() : nullptr;
+    o.mask = with_epilogue && p.mask ? p.mask->get() : nullptr;
+    return o;
+}
+
+void issue_product(const PendingGemm &p, const ProductOperands &o, float *C, bool with_epilogue) {
+    DevicePool::get().note_use(C);  // a step being recorded writes it on every replay
+    if (with_epilogue && p.sub) {
         launch(KernelClass::Gemm, 2.0 * p.M * p.N * p.K, "ts_hip_gemm_fused_sub", [&] {
-            return ts_hip_gemm_fused_sub(p.ta, p.tb, p.M, p.N, p.K, A, p.lda, B, p.ldb, bias, sub, p.relu ? 1 : 0,
-                                         mask, C, p.N, S());
+            return ts_hip_gemm_fused_sub(p.ta, p.tb, p.M, p.N, p.K, o.A, p.lda, o.B, p.ldb, o.bias, o.sub,
+                                         p.relu ? 1 : 0, o.mask, C, p.N, S());
         });
         return;
     }
-    // an operand that is a deferred chain over one buffer is read as that
-    // buffer, the chain applied as it is loaded
-    ts_hip_operand_xf xa{}, xb{};
-    std::shared_ptr<Allocation> la, lb;
-    const bool takes = ts_hip_gemm_takes_xf(p.ta, p.tb, p.M, p.N, p.K, 0) != 0;
-    const bool fa = takes && operand_xf(p.A, la, xa), fb = takes && operand_xf(p.B, lb, xb);
-    // inputs first (they may be deferred themselves), outside this launch's window
-    const float *A = fa ? la->get() : p.A->get(), *B = fb ? lb->get() : p.B->get();
-    const float *bias = with_epilogue && p.bias ? p.bias->get() : nullptr;
-    const float *mask = with_epilogue && p.mask ? p.mask->get() : nullptr;
     const bool relu = with_epilogue && p.relu;
-    DevicePool::get().note_use(C);  // a step being recorded writes it on every replay
     launch(KernelClass::Gemm, 2.0 * p.M * p.N * p.K, "ts_hip_gemm_fused", [&] {
-        if (fa || fb)
-            return gemm2d_xf(p.ta, p.tb, p.M, p.N, p.K, A, p.lda, fa ? &xa : nullptr, B, p.ldb, fb ? &xb : nullptr,
-                             bias, relu, mask, C, p.N);
-        return gemm2d(p.ta, p.tb, p.M, p.N, p.K, A, p.lda, B, p.ldb, bias, relu, mask, C, p.N);
+        if (o.fa || o.fb)
+            return gemm2d_xf(p.ta, p.tb, p.M, p.N, p.K, o.A, p.lda, o.fa ? &o.xa : nullptr, o.B, p.ldb,
+                             o.fb ? &o.xb : nullptr, o.bias, relu, o.mask, C, p.N);
+        return gemm2d(p.ta, p.tb, p.M, p.N, p.K, o.A, p.lda, o.B, p.ldb, o.bias, relu, o.mask, C, p.N);
     });
 }
 
+// inputs first (they may be deferred themselves), outside this launch's window
+void launch_product(const PendingGemm &p, float *C, bool with_epilogue) {
+    const ProductOperands o = product_operands(p, with_epilogue);
+    issue_product(p, o, C, with_epilogue);
+}
+
+void finish_sibling(SiblingLaunch &s) {
+    s.done = true;
+    for (auto &w : s.outputs)
+        if (auto o = w.lock())
+            if (o->sibling.get() == &s) o->sibling.reset();
+}
+
+// The product of p, with the weight-gradient product held beside it (if any,
+// and unless a group is already forming on this thread) in one launch group:
+// the two run as one launch, timed as one.
+void launch_product_grouped(const PendingGemm &p, float *C, bool with_epilogue) {
+    const std::shared_ptr<SiblingLaunch> sib = p.sibling;
+    LaunchCollector *&cur = launch_collector();
+    if (!sib || sib->done || cur) {
+        launch_product(p, C, with_epilogue);
+        return;
+    }
+    // every input of both first (deferred ones run here, outside the group)
+    const ProductOperands o = product_operands(p, with_epilogue);
+    for (auto &in : sib->inputs)
+        if (in) in->get();
+    Profiler &P = Profiler::get();
+    LaunchCollector col;
+    P.begin(KernelClass::Gemm);
+    const int st = ts_hip_launch_group_begin(S());
+    if (st != TS_HIP_OK) {
+        P.abort();
+        check(st, "ts_hip_launch_group_begin");
+    }
+    cur = &col;
+    try {
+        issue_product(p, o, C, with_epilogue);
+        sib->run();
+    } catch (...) {
+        cur = nullptr;
+        (void)ts_hip_launch_group_end(S());  // what was held is launched
+        P.abort();
+        throw;
+    }
+    cur = nullptr;
+    const int end = ts_hip_launch_group_end(S());
+    if (end != TS_HIP_OK) {
+        P.abort();
+        check(end, "ts_hip_launch_group_end");
+    }
+    P.end(KernelClass::Gemm, col.work);
+    finish_sibling(*sib);
+}
+
 }  // namespace
+
+LaunchCollector *&launch_collector() {
+    static thread_local LaunchCollector *c = nullptr;
+    return c;
+}
+
+void run_sibling(Allocation &a) {
+    // the record stays until the launch has succeeded (as for a product)
+    const std::shared_ptr<SiblingLaunch> s = a.sibling;
+    if (!s->done) s->run();
+    finish_sibling(*s);
+}
 
 void materialize(Allocation &a) {
     // The record stays until the launch has succeeded: after a failed launch
@@ -490,7 +572,7 @@ void materialize(Allocation &a) {
     }
     const std::vector<std::shared_ptr<Allocation>> others = pending_members(a, *p);
     if (others.empty()) {  // the only consumer: the product with its epilogue, in one launch
-        launch_product(*p, C, true);
+        launch_product_grouped(*p, C, true);
         a.pending.reset();
         return;
     }
@@ -500,7 +582,7 @@ void materialize(Allocation &a) {
     std::shared_ptr<Allocation> prod = p->group->bare.lock();
     if (!prod || !prod->pending || !prod->pending->bare() || prod->pending->group != p->group)
         prod = std::make_shared<Allocation>(p->M * p->N);
-    launch_product(*p, prod->raw(), false);
+    launch_product_grouped(*p, prod->raw(), false);
     if (prod->pending) prod->pending.reset();
     std::vector<std::shared_ptr<Allocation>> all = others;
     all.push_back(a.shared_from_this());
@@ -1966,6 +2048,7 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
                 const size_t M = a.dims[0], Kd = a.dims[1], N = b.dims[1];
                 // b (or a) a transposed view: its source, with the flag flipped
                 const MatOperand va = mat_operand(a.alloc), vb = mat_operand(b.alloc);
+                std::shared_ptr<PendingGemm> dx_pending;  // the dX product, when deferred
                 if (req_left) {  // go[M,N] . b[Kd,N]^T -> [M,Kd]
                     Tensor t = Tensor::new_uninit({M, Kd});
                     const int tb = vb.trans ? 0 : 1;
@@ -1977,6 +2060,7 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
                         p->M = M; p->N = Kd; p->K = N; p->lda = N; p->ldb = ldb;
                         p->A = go.allocation();
                         p->B = vb.buf;
+                        dx_pending = p;
                         set_pending(t.allocation(), std::move(p));
                     } else {
                         const float *B = vb.buf ? vb.buf->get() : nullptr;
@@ -2024,7 +2108,6 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
                     std::shared_ptr<Allocation> leaf;
                     const bool fx = ts_hip_gemm_takes_xf(ta, 0, Kd, N, M, db ? 1 : 0) &&
                                     operand_xf(go.allocation(), leaf, xb);
-                    const float *A = va.buf ? va.buf->get() : nullptr;
                     // a deferred sum of the buffer read as B, or of a chain over
                     // it (the README step's loss over relu's output; an MSE's
                     // mean of d * d), comes out of this launch too
@@ -2033,35 +2116,58 @@ std::vector<std::optional<Tensor>> GradFn::apply(const Tensor &go) const {
                         db && ts_hip_gemm_takes_bsum(ta, Kd, N, M)
                             ? pending_sum_of(fx ? leaf : go.allocation(), M * N, xs)
                             : nullptr;
-                    if (bsum) {
-                        db->colsum.reset();
-                        const float *B = fx ? leaf->get() : go.dev();
-                        float *C = t.dev_mut();
-                        float *sum = bsum->raw();
-                        DevicePool::get().note_use(sum);
-                        launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm_colsum_bsum(dW, db, loss)", [&] {
-                            return ts_hip_gemm_colsum_bsum(ta, Kd, N, M, A, lda, nullptr, B, fx ? &xb : nullptr, C, N,
-                                                           db->raw(), xs.n_ops ? &xs : nullptr, sum,
-                                                           bsum->reduce->mean ? 1 : 0, S());
-                        });
-                        bsum->reduce.reset();
-                    } else if (db) {
-                        db->colsum.reset();
-                        const float *B = fx ? leaf->get() : go.dev();
-                        float *C = t.dev_mut();
-                        const size_t ws = ts_hip_gemm_colsum_workspace_floats(ta, Kd, N, M);
-                        std::unique_ptr<Allocation> work;  // from the pool: the launch allocates nothing
-                        if (ws) work = std::make_unique<Allocation>(ws);
-                        launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm_colsum(dW, db)", [&] {
-                            return ts_hip_gemm_colsum_xf(ta, Kd, N, M, A, lda, nullptr, B, N, fx ? &xb : nullptr, C, N,
-                                                         db->raw(), work ? work->get() : nullptr, ws, S());
-                        });
+                    const bool mean = bsum && bsum->reduce->mean;
+                    if (db) db->colsum.reset();
+                    if (bsum) bsum->reduce.reset();
+                    // the launcher, from the buffers alone: run now, or held
+                    // beside the deferred dX product (below)
+                    const std::shared_ptr<Allocation> Ab = va.buf, Bb = fx ? leaf : go.allocation(),
+                                                      out = t.allocation();
+                    auto dw = [=]() {
+                        const float *A = Ab ? Ab->get() : nullptr;
+                        const float *B = Bb->get();
+                        float *C = out->raw();
+                        DevicePool::get().note_use(C);
+                        if (bsum) {
+                            float *sum = bsum->raw();
+                            DevicePool::get().note_use(sum);
+                            launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm_colsum_bsum(dW, db, loss)", [&] {
+                                return ts_hip_gemm_colsum_bsum(ta, Kd, N, M, A, lda, nullptr, B, fx ? &xb : nullptr, C,
+                                                               N, db->raw(), xs.n_ops ? &xs : nullptr, sum,
+                                                               mean ? 1 : 0, S());
+                            });
+                        } else if (db) {
+                            const size_t ws = ts_hip_gemm_colsum_workspace_floats(ta, Kd, N, M);
+                            std::unique_ptr<Allocation> work;  // from the pool: the launch allocates nothing
+                            if (ws) work = std::make_unique<Allocation>(ws);
+                            launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm_colsum(dW, db)", [&] {
+                                return ts_hip_gemm_colsum_xf(ta, Kd, N, M, A, lda, nullptr, B, N, fx ? &xb : nullptr,
+                                                             C, N, db->raw(), work ? work->get() : nullptr, ws, S());
+                            });
+                        } else {
+                            launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm(dW)", [&] {
+                                return gemm2d_xf(ta, 0, Kd, N, M, A, lda, nullptr, B, N, fx ? &xb : nullptr, nullptr,
+                                                 false, nullptr, C, N);
+                            });
+                        }
+                    };
+                    // A layer with few outputs (N <= 16): dX (K = N, one k tile)
+                    // and dW (the narrow kernel) are both latency-bound; dW is
+                    // held until dX runs, and the two run as one launch.
+                    if (dx_pending && N <= 16 && ts_hip_gemm_takes_sub(ta, 0, Kd, N, M)) {
+                        auto sib = std::make_shared<SiblingLaunch>();
+                        sib->run = dw;
+                        sib->inputs = {Ab, Bb};
+                        for (const auto &o : {out, db, bsum})
+                            if (o) {
+                                o->sibling = sib;
+                                sib->outputs.push_back(o);
+                            }
+                        add_reader(Ab, out);  // an in-place write of an input runs it first
+                        add_reader(Bb, out);
+                        dx_pending->sibling = std::move(sib);
                     } else {
-                        const float *B = fx ? leaf->get() : go.dev();
-                        launch(KernelClass::Gemm, 2.0 * M * N * Kd, "ts_hip_gemm(dW)", [&] {
-                            return gemm2d_xf(ta, 0, Kd, N, M, A, lda, nullptr, B, N, fx ? &xb : nullptr, nullptr,
-                                             false, nullptr, t.dev_mut(), N);
-                        });
+                        dw();
                     }
                     gr = std::move(t);
                 }

@@ -19,6 +19,7 @@
 #include <atomic>
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <memory>
 #include <optional>
 #include <stdexcept>
@@ -119,6 +120,21 @@ struct ProductGroup {
     std::vector<std::weak_ptr<Allocation>> members;  // it and every fork
 };
 
+// A weight-gradient product held beside its matmul backward's deferred dX
+// product (grad_fn/ops/matmul.rs:68-80 computes both; here for a layer with
+// few outputs, whose dW takes the narrow kernel and dX the one-k-tile kernel,
+// both latency-bound): when the dX product runs, the two are issued in one
+// launch group (ts_hip_launch_group_begin / _end) and run as one launch.
+// When one of its outputs (dW, the bias gradient, a loss summed in its
+// launch) is read first, or an input is about to be written in place, it
+// runs by itself.  Same bits either way.
+struct SiblingLaunch {
+    std::function<void()> run;                    // the product's launcher, through launch()
+    std::vector<std::shared_ptr<Allocation>> inputs;  // fetched before the group forms
+    bool done = false;
+    std::vector<std::weak_ptr<Allocation>> outputs;
+};
+
 struct PendingGemm {
     int ta = 0, tb = 0;
     size_t M = 0, N = 0, K = 0, lda = 0, ldb = 0;
@@ -129,6 +145,7 @@ struct PendingGemm {
     std::shared_ptr<Allocation> src;  // epilogue-only: the produced [M, N] buffer the epilogue reads
     bool relu = false;
     std::shared_ptr<ProductGroup> group;
+    std::shared_ptr<SiblingLaunch> sibling;  // run in the same launch group as this product
     bool bare() const { return !src && !bias && !sub && !mask && !relu; }
 };
 
@@ -237,7 +254,8 @@ struct Allocation : std::enable_shared_from_this<Allocation> {
     std::shared_ptr<PendingColsum> colsum;           // deferred column sum
     std::shared_ptr<PendingTranspose> transpose;     // deferred transposed copy
     std::shared_ptr<PendingReduce> reduce;           // deferred sum / mean
-    bool deferred() const { return pending || map || colsum || transpose || reduce; }
+    std::shared_ptr<SiblingLaunch> sibling;          // written by a held weight-gradient product
+    bool deferred() const { return pending || map || colsum || transpose || reduce || sibling; }
     std::vector<std::weak_ptr<Allocation>> readers;  // pending allocations reading this one
     size_t n = 0, rounded = 0;
     // held by this thread's list of deferred programs with a checked
@@ -259,6 +277,8 @@ void materialize_colsum(Allocation &a);
 void materialize_transpose(Allocation &a);
 // Runs a's deferred sum / mean (tensor.cpp).
 void materialize_reduce(Allocation &a);
+// Runs the held product that writes a, by itself (tensor.cpp).
+void run_sibling(Allocation &a);
 // A matrix operand as a product reads it: a 2-D transposed view or copy not
 // yet written is its source with the trans flag set (tensor.cpp).
 struct MatOperand {
@@ -352,8 +372,21 @@ class Profiler {
 // when it is enabled; a failed status throws with `what` in the message.
 // Operands should be fetched before the call (a deferred operand that runs
 // inside the window is charged to its own class all the same).
+// While a launch group forms (a dX product and its held sibling), the
+// launchers' GEMM calls are issued into the group with no profiler window of
+// their own: the group's one launch is timed once, with their work summed.
+struct LaunchCollector {
+    double work = 0.0;
+};
+LaunchCollector *&launch_collector();
+
 template <class F>
 void launch(KernelClass k, double work, const char *what, F &&f) {
+    if (LaunchCollector *c = launch_collector(); c && k == KernelClass::Gemm) {
+        check(f(), what);
+        c->work += work;
+        return;
+    }
     Profiler &P = Profiler::get();
     P.begin(k);
     try {

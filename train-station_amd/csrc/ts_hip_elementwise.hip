@@ -370,6 +370,7 @@ int ts_hip_fill(float *out, float value, size_t n, void *stream) {
 int ts_hip_copy(const float *src, float *dst, size_t n, void *stream) {
     if (n == 0) return TS_HIP_OK;
     if (!src || !dst) return TS_HIP_EINVAL;
+    if (launch_group_holding()) flush_launch_group();  // after the products a launch group holds
     return static_cast<int>(
         hipMemcpyAsync(dst, src, n * sizeof(float), hipMemcpyDeviceToDevice, as_stream(stream)));
 }

@@ -1090,6 +1090,61 @@ static void launch_dma_layout(int ta, int tb, const GemmArgs &g, hipStream_t s, 
     }
 }
 
+// ---- launch groups -------------------------------------------------------------
+//
+// Between ts_hip_launch_group_begin(stream) and ts_hip_launch_group_end(stream)
+// the calling thread's products on that stream that run on the narrow or the
+// one-k-tile kernel are held (at most two); any other launch on the stream
+// launches them first, in the order they were issued.  At the end, one of each
+// runs as one launch when their pair is instantiated (gemm_narrow_short_k: an
+// MLP backward's dW with its bias gradient and dX of a layer with few outputs,
+// both latency-bound), otherwise what is held is launched as issued.
+namespace {
+enum : int { kHeldNarrow = 1, kHeldShortK = 2 };
+struct HeldLaunch {
+    int kind, variant;
+    void (*kernel)(GemmArgs);
+    dim3 grid, block;
+    GemmArgs g;
+};
+struct LaunchGroupState {
+    bool open = false;
+    hipStream_t stream = nullptr;
+    int n = 0;
+    HeldLaunch held[2];
+};
+thread_local LaunchGroupState t_group;
+
+// held when a group is open on s with room, else launched (after any held)
+void hold_or_launch(int kind, int variant, void (*k)(GemmArgs), dim3 grid, dim3 block, hipStream_t s,
+                    const GemmArgs &g) {
+    LaunchGroupState &lg = t_group;
+    if (lg.open && lg.stream == s && lg.n < 2) {
+        lg.held[lg.n++] = HeldLaunch{kind, variant, k, grid, block, g};
+        return;
+    }
+    launch(k, grid, block, 0, s, g);
+}
+}  // namespace
+
+bool launch_group_holding() { return t_group.n > 0; }
+
+void flush_launch_group() {
+    LaunchGroupState &lg = t_group;
+    const int n = lg.n;
+    lg.n = 0;
+    for (int i = 0; i < n; ++i) launch_now(lg.held[i].kernel, lg.held[i].grid, lg.held[i].block, 0, lg.stream, lg.held[i].g);
+}
+
+template <bool TA, bool TB, bool V, bool CS, bool XF>
+constexpr int narrow_variant() {
+    return int(TA) | int(TB) << 1 | int(V) << 2 | int(CS) << 3 | int(XF) << 4;
+}
+template <bool TA, bool TB, int EPI, bool XF>
+constexpr int short_k_variant() {
+    return int(TA) | int(TB) << 1 | EPI << 2 | int(XF) << 4;
+}
+
 // ---- short contractions (K <= 16) --------------------------------------------
 //
 // One k tile: a wave's 32x32 block takes at most 8 MFMAs, so its operands go
@@ -1100,11 +1155,12 @@ static void launch_dma_layout(int ta, int tb, const GemmArgs &g, hipStream_t s, 
 // takes k = 2s + (lane half), as a tiled kernel's k tile does, and stops at
 // the last MFMA that holds a k < K (the tiled kernels add the zero products
 // of the rest), so the stored values are the same.
-template <bool TA, bool TB, int EPI, bool XF = false>
-__global__ __launch_bounds__(256) void gemm_short_k(GemmArgs g) {
+// Tile `tile` of the grid, by the 256 threads numbered tid (4 waves).
+template <bool TA, bool TB, int EPI, bool XF>
+__device__ __forceinline__ void short_k_tile(const GemmArgs &g, int tile, int tid) {
     int tm, tn;
-    tile_coords(g.tiles_m, g.tiles_n, blockIdx.x, tm, tn);
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    tile_coords(g.tiles_m, g.tiles_n, tile, tm, tn);
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lrow = lane & 31, lhalf = lane >> 5;
     const int i0 = tm * 64 + (wave >> 1) * 32, j = tn * 64 + (wave & 1) * 32 + lrow;
     const float *__restrict__ A = g.A;
@@ -1163,12 +1219,23 @@ __global__ __launch_bounds__(256) void gemm_short_k(GemmArgs g) {
     }
 }
 
+template <bool TA, bool TB, int EPI, bool XF = false>
+__global__ __launch_bounds__(256) void gemm_short_k(GemmArgs g) {
+    short_k_tile<TA, TB, EPI, XF>(g, blockIdx.x, threadIdx.x);
+}
+
+template <bool TA, bool TB, int EPI, bool XF>
+static void short_k_launch(dim3 grid, hipStream_t s, const GemmArgs &g) {
+    hold_or_launch(kHeldShortK, short_k_variant<TA, TB, EPI, XF>(), gemm_short_k<TA, TB, EPI, XF>, grid, dim3(256), s,
+                   g);
+}
+
 template <int EPI, bool XF>
 static void launch_short_k_xf(int ta, int tb, const GemmArgs &g, dim3 grid, hipStream_t s) {
-    if (!ta && !tb) launch((gemm_short_k<false, false, EPI, XF>), grid, dim3(256), 0, s, g);
-    else if (!ta) launch((gemm_short_k<false, true, EPI, XF>), grid, dim3(256), 0, s, g);
-    else if (!tb) launch((gemm_short_k<true, false, EPI, XF>), grid, dim3(256), 0, s, g);
-    else launch((gemm_short_k<true, true, EPI, XF>), grid, dim3(256), 0, s, g);
+    if (!ta && !tb) short_k_launch<false, false, EPI, XF>(grid, s, g);
+    else if (!ta) short_k_launch<false, true, EPI, XF>(grid, s, g);
+    else if (!tb) short_k_launch<true, false, EPI, XF>(grid, s, g);
+    else short_k_launch<true, true, EPI, XF>(grid, s, g);
 }
 
 template <int EPI>
@@ -1374,14 +1441,16 @@ static_assert(kColsumRows == 64, "a narrow wave round is one column-sum chunk");
 
 // V: the k-contiguous operands (A unless TA, B when TB) take dwordx4 loads
 // (16-byte aligned, leading dimension % 4 == 0).
-template <bool TA, bool TB, bool V, bool CS, bool XF = false>
-__global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) {
+// Workgroup (bx, by) of a gx-wide grid of narrow workgroups of
+// blockDim.x threads (whole waves).
+template <bool TA, bool TB, bool V, bool CS, bool XF>
+__device__ __forceinline__ void narrow_block(const GemmArgs &g, int bx, int by, int gx) {
     static_assert(!CS || !TB, "column sums of B need trans_b == 0");
     if constexpr (CS) {
         // the row of workgroups appended for GemmArgs::sum_out (launched with
         // kNarrowMaxWaves waves): its first workgroup forms the sum
-        if (g.sum_out && blockIdx.x == gridDim.x - 1) {  // uniform
-            if (blockIdx.y == 0) sum_in_workgroup<64 * kNarrowMaxWaves>(g);
+        if (g.sum_out && bx == gx - 1) {  // uniform
+            if (by == 0) sum_in_workgroup<64 * kNarrowMaxWaves>(g);
             return;
         }
     }
@@ -1390,13 +1459,13 @@ __global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int waves = blockDim.x >> 6;
-    const int m0 = blockIdx.x * kNarrowRows, n0 = blockIdx.y * kSkinnyN;
+    const int m0 = bx * kNarrowRows, n0 = by * kSkinnyN;
     const int q = lane >> 4;
     const int m = min(m0 + (lane & 15), g.M - 1);  // rows past M: never stored
     const int n = min(n0 + (lane & 15), g.N - 1);  // columns past N: never stored
     const int kc = ((g.K + waves - 1) / waves + 63) & ~63;
     const int kb = min(g.K, wave * kc), ke = min(g.K, kb + kc);
-    const bool cs_wg = CS && blockIdx.x == 0;  // uniform
+    const bool cs_wg = CS && bx == 0;  // uniform
     const XfRegs xfa = XF ? xf_load(g.xa) : XfRegs{}, xfb = XF ? xf_load(g.xb) : XfRegs{};
     const float *__restrict__ A = g.A;
     const float *__restrict__ B = g.B;
@@ -1511,6 +1580,28 @@ __global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) 
     }
 }
 
+template <bool TA, bool TB, bool V, bool CS, bool XF = false>
+__global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow(GemmArgs g) {
+    narrow_block<TA, TB, V, CS, XF>(g, blockIdx.x, blockIdx.y, gridDim.x);
+}
+
+// A narrow product and a one-k-tile product in one launch (a launch group of
+// the two; ts_hip_launch_group_begin): the first nb workgroups are the narrow
+// product's (one row of column blocks, kNarrowMaxWaves waves), each later one
+// runs tpw (1-4) of the other's 64x64 tiles, one per 256 threads.  The two
+// write different outputs and read only inputs written before the launch.
+template <bool NTA, bool NTB, bool NV, bool NCS, bool NXF, bool STA, bool STB, int SEPI, bool SXF>
+__global__ __launch_bounds__(64 * kNarrowMaxWaves) void gemm_narrow_short_k(GemmArgs gn, GemmArgs gs, int nb,
+                                                                             int tpw) {
+    if (static_cast<int>(blockIdx.x) < nb) {  // uniform
+        narrow_block<NTA, NTB, NV, NCS, NXF>(gn, blockIdx.x, 0, nb);
+        return;
+    }
+    const int part = static_cast<int>(threadIdx.x >> 8);  // uniform per wave
+    const int tile = (static_cast<int>(blockIdx.x) - nb) * tpw + part;
+    if (part < tpw && tile < gs.tiles) short_k_tile<STA, STB, SEPI, SXF>(gs, tile, threadIdx.x & 255);
+}
+
 // Waves per narrow workgroup: the largest power of two up to 16 that leaves
 // each wave at least 64 k.
 static int narrow_waves(size_t K) {
@@ -1524,21 +1615,26 @@ static bool narrow_fits(size_t M, size_t N, size_t K) {
     return K <= kNarrowMaxK || 8 * blocks >= static_cast<size_t>(device_cu_count());
 }
 
+template <bool TA, bool TB, bool V, bool CS, bool XF>
+static void narrow_launch(dim3 grid, dim3 block, hipStream_t s, const GemmArgs &g) {
+    hold_or_launch(kHeldNarrow, narrow_variant<TA, TB, V, CS, XF>(), gemm_narrow<TA, TB, V, CS, XF>, grid, block, s, g);
+}
+
 template <bool CS, bool XF>
 static void launch_narrow_xf(int trans_a, int trans_b, bool v, const GemmArgs &g, dim3 grid, dim3 block,
                              hipStream_t s) {
     if (!trans_a && !trans_b) {
-        if (v) launch((gemm_narrow<false, false, true, CS, XF>), grid, block, 0, s, g);
-        else launch((gemm_narrow<false, false, false, CS, XF>), grid, block, 0, s, g);
+        if (v) narrow_launch<false, false, true, CS, XF>(grid, block, s, g);
+        else narrow_launch<false, false, false, CS, XF>(grid, block, s, g);
     } else if (!trans_b) {
-        launch((gemm_narrow<true, false, false, CS, XF>), grid, block, 0, s, g);
+        narrow_launch<true, false, false, CS, XF>(grid, block, s, g);
     } else if (!CS) {  // column sums need trans_b == 0 (checked by the caller)
         if (!trans_a) {
-            if (v) launch((gemm_narrow<false, true, true, false, XF>), grid, block, 0, s, g);
-            else launch((gemm_narrow<false, true, false, false, XF>), grid, block, 0, s, g);
+            if (v) narrow_launch<false, true, true, false, XF>(grid, block, s, g);
+            else narrow_launch<false, true, false, false, XF>(grid, block, s, g);
         } else {
-            if (v) launch((gemm_narrow<true, true, true, false, XF>), grid, block, 0, s, g);
-            else launch((gemm_narrow<true, true, false, false, XF>), grid, block, 0, s, g);
+            if (v) narrow_launch<true, true, true, false, XF>(grid, block, s, g);
+            else narrow_launch<true, true, false, false, XF>(grid, block, s, g);
         }
     }
 }
@@ -1572,6 +1668,56 @@ static int launch_narrow(int trans_a, int trans_b, size_t M, size_t N, size_t K,
     hipStream_t s = as_stream(stream);
     if (g.colsum) launch_narrow_as<true>(trans_a, trans_b, va && vb, g, grid, block, s);
     else launch_narrow_as<false>(trans_a, trans_b, va && vb, g, grid, block, s);
+    return launch_status();
+}
+
+using PairKernel = void (*)(GemmArgs, GemmArgs, int, int);
+
+// The instantiated pairs: an MLP backward's dW of a layer with few outputs
+// (narrow, A transposed, with the bias gradient's column sums) and its dX
+// (one k tile, B transposed, relu-backward mask), with and without operand
+// transforms on the gradient they share.
+static PairKernel pair_kernel(int nv, int sv) {
+    if (nv == narrow_variant<true, false, false, true, true>() && sv == short_k_variant<false, true, kEpiAll, true>())
+        return gemm_narrow_short_k<true, false, false, true, true, false, true, kEpiAll, true>;
+    if (nv == narrow_variant<true, false, false, true, false>() && sv == short_k_variant<false, true, kEpiAll, false>())
+        return gemm_narrow_short_k<true, false, false, true, false, false, true, kEpiAll, false>;
+    return nullptr;
+}
+
+extern "C" int ts_hip_launch_group_begin(void *stream) {
+    tship::LaunchGroupState &lg = tship::t_group;
+    if (lg.open) return TS_HIP_EINVAL;
+    lg.open = true;
+    lg.stream = tship::as_stream(stream);
+    lg.n = 0;
+    return TS_HIP_OK;
+}
+
+extern "C" int ts_hip_launch_group_end(void *stream) {
+    using namespace tship;
+    LaunchGroupState &lg = t_group;
+    if (!lg.open || lg.stream != as_stream(stream)) return TS_HIP_EINVAL;
+    lg.open = false;
+    if (lg.n == 2 && lg.held[0].kind != lg.held[1].kind) {
+        const HeldLaunch &nr = lg.held[0].kind == kHeldNarrow ? lg.held[0] : lg.held[1];
+        const HeldLaunch &sk = lg.held[0].kind == kHeldNarrow ? lg.held[1] : lg.held[0];
+        const PairKernel k = pair_kernel(nr.variant, sk.variant);
+        if (k && nr.grid.y == 1 && nr.block.x == 64 * kNarrowMaxWaves) {
+            lg.n = 0;
+            // one workgroup of either kind per CU (the narrow one holds a CU
+            // at its register count): the one-k-tile product's tiles over the
+            // CUs the narrow product leaves, up to four per workgroup
+            const int nb = static_cast<int>(nr.grid.x), free = device_cu_count() - nb;
+            int tpw = 1;
+            while (tpw < 4 && (free <= 0 || static_cast<long long>(free) * tpw < sk.g.tiles)) tpw *= 2;
+            const unsigned sb = static_cast<unsigned>((sk.g.tiles + tpw - 1) / tpw);
+            launch_now(k, dim3(static_cast<unsigned>(nb) + sb), dim3(64 * kNarrowMaxWaves), 0, lg.stream, nr.g, sk.g,
+                       nb, tpw);
+            return launch_status();
+        }
+    }
+    flush_launch_group();
     return launch_status();
 }
 

@@ -26,12 +26,30 @@ struct TimingWindow {
 };
 TimingWindow *timing_window();
 
+// Products held by the calling thread's open launch group
+// (ts_hip_launch_group_begin): true while any is held.  A kernel launched
+// while they are held is launched after them (flush_launch_group first), so
+// the stream sees every launch in the order it was issued.
+bool launch_group_holding();
+void flush_launch_group();
+
+template <typename... KArgs, typename... Args>
+inline void launch_now(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds, hipStream_t s,
+                       Args... args);
+
 // Every kernel of the library is launched through here: a plain launch, or,
 // inside a timing window, one that carries the window's events in its
 // dispatch (the first kernel the start event, each kernel the stop event).
 template <typename... KArgs, typename... Args>
 inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds, hipStream_t s,
                    Args... args) {
+    if (launch_group_holding()) flush_launch_group();
+    launch_now(kernel, grid, block, lds, s, args...);
+}
+
+template <typename... KArgs, typename... Args>
+inline void launch_now(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds, hipStream_t s,
+                       Args... args) {
     TimingWindow *w = timing_window();
     if (!w) {
         kernel<<<grid, block, lds, s>>>(args...);
@@ -45,6 +63,7 @@ inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds
 // The same for a kernel of a code object compiled at run time (the compiled
 // elementwise programs of ts_hip_map): blocks workgroups of `threads`.
 inline hipError_t launch_module(hipFunction_t f, unsigned blocks, unsigned threads, hipStream_t s, void **params) {
+    if (launch_group_holding()) flush_launch_group();
     TimingWindow *w = timing_window();
     if (!w) return hipModuleLaunchKernel(f, blocks, 1, 1, threads, 1, 1, 0, s, params, nullptr);
     const hipError_t e = hipExtModuleLaunchKernel(f, blocks * threads, 1, 1, threads, 1, 1, 0, s, params, nullptr,

@@ -55,6 +55,14 @@ static hipMemcpyKind copy_kind(int kind, bool *ok) {
 
 using namespace tship;
 
+namespace {
+// Stream work below that is not a kernel launch (copies, synchronisation,
+// events, graphs, module kernels) goes after any products a launch group holds.
+void flush_held() {
+    if (tship::launch_group_holding()) tship::flush_launch_group();
+}
+}  // namespace
+
 extern "C" {
 
 int ts_hip_initialize(void) {
@@ -72,7 +80,10 @@ int ts_hip_initialize(void) {
     return TS_HIP_OK;
 }
 
-void ts_hip_cleanup(void) { (void)hipDeviceSynchronize(); }
+void ts_hip_cleanup(void) {
+    flush_held();
+    (void)hipDeviceSynchronize();
+}
 
 int ts_hip_get_device_count(int *count) {
     if (!count) return TS_HIP_EINVAL;
@@ -102,6 +113,7 @@ int ts_hip_free(float *ptr) {
 }
 
 int ts_hip_memcpy(float *dst, const float *src, size_t n_floats, int kind) {
+    flush_held();
     bool ok;
     hipMemcpyKind k = copy_kind(kind, &ok);
     if (!ok || (n_floats && (!dst || !src))) return TS_HIP_EINVAL;
@@ -110,6 +122,7 @@ int ts_hip_memcpy(float *dst, const float *src, size_t n_floats, int kind) {
 }
 
 int ts_hip_memcpy_async(float *dst, const float *src, size_t n_floats, int kind, void *stream) {
+    flush_held();
     bool ok;
     hipMemcpyKind k = copy_kind(kind, &ok);
     if (!ok || (n_floats && (!dst || !src))) return TS_HIP_EINVAL;
@@ -119,6 +132,7 @@ int ts_hip_memcpy_async(float *dst, const float *src, size_t n_floats, int kind,
 }
 
 int ts_hip_memcpy_bytes(void *dst, const void *src, size_t bytes, int kind, void *stream) {
+    flush_held();
     bool ok;
     hipMemcpyKind k = copy_kind(kind, &ok);
     if (!ok || (bytes && (!dst || !src))) return TS_HIP_EINVAL;
@@ -152,10 +166,14 @@ int ts_hip_stream_destroy(void *stream) {
 }
 
 int ts_hip_stream_synchronize(void *stream) {
+    flush_held();
     return tship::status_of(hipStreamSynchronize(as_stream(stream)));
 }
 
-int ts_hip_device_synchronize(void) { return tship::status_of(hipDeviceSynchronize()); }
+int ts_hip_device_synchronize(void) {
+    flush_held();
+    return tship::status_of(hipDeviceSynchronize());
+}
 
 int ts_hip_event_create(void **event) {
     if (!event) return TS_HIP_EINVAL;
@@ -171,6 +189,7 @@ int ts_hip_event_destroy(void *event) {
 }
 
 int ts_hip_event_record(void *event, void *stream) {
+    flush_held();
     if (!event) return TS_HIP_EINVAL;
     return tship::status_of(hipEventRecord(reinterpret_cast<hipEvent_t>(event), as_stream(stream)));
 }
@@ -224,6 +243,7 @@ int ts_hip_module_get_function(void *module, const char *name, void **function) 
 int ts_hip_module_launch(void *function, unsigned grid_x, unsigned grid_y, unsigned grid_z, unsigned block_x,
                          unsigned block_y, unsigned block_z, unsigned lds_bytes, void *stream,
                          void **kernel_params) {
+    flush_held();
     if (!function || !grid_x || !grid_y || !grid_z || !block_x || !block_y || !block_z) return TS_HIP_EINVAL;
     if (static_cast<unsigned long long>(block_x) * block_y * block_z > 1024) return TS_HIP_EINVAL;
     return tship::status_of(hipModuleLaunchKernel(reinterpret_cast<hipFunction_t>(function), grid_x, grid_y,
@@ -237,6 +257,7 @@ int ts_hip_stream_begin_capture(void *stream) {
 }
 
 int ts_hip_stream_end_capture(void *stream, void **graph_exec) {
+    flush_held();
     if (!stream || !graph_exec) return TS_HIP_EINVAL;
     *graph_exec = nullptr;
     hipGraph_t graph = nullptr;
@@ -259,6 +280,7 @@ int ts_hip_stream_is_capturing(void *stream, int *capturing) {
 }
 
 int ts_hip_graph_launch(void *graph_exec, void *stream) {
+    flush_held();
     if (!graph_exec) return TS_HIP_EINVAL;
     return tship::status_of(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph_exec), as_stream(stream)));
 }
