@@ -190,3 +190,81 @@ def test_group_calls_out_of_order_are_refused():
     finally:
         hip_check(hip.ts_hip_stream_synchronize(s))
         hip_check(hip.ts_hip_stream_destroy(s))
+
+
+@pytest.fixture
+def T():
+    import train_station_amd as T
+    yield T
+    T.set_fusion(True)
+    T.clear_gradients()
+
+
+def _narrow_mlp(T, seed, frozen_first):
+    """784 -> 1024 -> 10 at batch 1024 with an MSE: the second layer's dW and
+    dX are held for one launch.  frozen_first: W1 and b1 constant and x
+    requiring a gradient instead, so nothing reads dX2 before x.grad does."""
+    rng = np.random.default_rng(seed)
+    ps = []
+    for fi, fo in ((784, 1024), (1024, 10)):
+        bound = np.float32(np.sqrt(6.0 / fi))
+        w = T.Tensor.from_slice(rng.uniform(-bound, bound, (fi, fo)).astype(np.float32), [fi, fo])
+        b = T.Tensor.from_slice((0.1 * rng.standard_normal(fo)).astype(np.float32), [fo])
+        if not (frozen_first and fi == 784):
+            w, b = w.with_requires_grad(), b.with_requires_grad()
+        ps += [w, b]
+    x = T.Tensor.from_slice(rng.standard_normal((1024, 784)).astype(np.float32), [1024, 784])
+    if frozen_first:
+        x = x.with_requires_grad()
+    t = T.Tensor.from_slice(rng.standard_normal((1024, 10)).astype(np.float32), [1024, 10])
+    return ps, x, t
+
+
+@pytest.mark.parametrize("order", ["dw_first", "dx_first", "loss_first"])
+def test_held_weight_gradient_read_before_its_pair_runs_by_itself(T, order):
+    # W1 constant, x requiring a gradient: after backward dX2 is still
+    # deferred (only x.grad reads it), so reading W2's gradient, b2's or the
+    # loss first runs the held dW2 by itself; x.grad then runs dX2 alone.
+    # Every value equals the unfused run's.
+    got = {}
+    for on in (True, False):
+        T.set_fusion(on)
+        ps, x, t = _narrow_mlp(T, 23, True)
+        h = x.matmul(ps[0]).add_tensor(ps[1]).relu()
+        loss = h.matmul(ps[2]).add_tensor(ps[3]).sub_tensor(t).pow_scalar(2.0).mean()
+        loss.backward()
+        vals = {}
+        reads = {"dw_first": ("w2", "b2", "loss", "x"), "dx_first": ("x", "w2", "b2", "loss"),
+                 "loss_first": ("loss", "x", "b2", "w2")}[order]
+        for r in reads:
+            if r == "w2":
+                vals[r] = ps[2].grad_by_value().data()
+            elif r == "b2":
+                vals[r] = ps[3].grad_by_value().data()
+            elif r == "x":
+                vals[r] = x.grad_by_value().data()
+            else:
+                vals[r] = np.array([loss.value()], dtype=np.float32)
+        got[on] = vals
+        T.clear_gradients()
+    for k in got[True]:
+        assert_bits_equal(got[True][k], got[False][k], f"{order}: {k}")
+
+
+def test_held_weight_gradient_runs_before_its_input_is_written_in_place(T):
+    # the held dW2 reads relu's output h; writing h in place (fill) before
+    # anything reads dW2 runs the held product first, with the old h
+    got = {}
+    for on in (True, False):
+        T.set_fusion(on)
+        ps, x, t = _narrow_mlp(T, 29, True)
+        h = x.matmul(ps[0]).add_tensor(ps[1]).relu()
+        loss = h.matmul(ps[2]).add_tensor(ps[3]).sub_tensor(t).pow_scalar(2.0).mean()
+        loss.backward()
+        h.fill(0.5)
+        got[on] = (ps[2].grad_by_value().data(), ps[3].grad_by_value().data(), x.grad_by_value().data(),
+                   loss.value())
+        T.clear_gradients()
+    for name, a, b in zip(("w2", "b2", "x"), got[True][:3], got[False][:3]):
+        assert_bits_equal(a, b, name)
+    assert got[True][3] == got[False][3]
