@@ -79,6 +79,8 @@ def lib() -> ctypes.CDLL:
         L.o_libm_cr_check.restype = ctypes.c_long
         L.o_libm_glibc_diff.argtypes = [ctypes.c_int]
         L.o_libm_glibc_diff.restype = ctypes.c_long
+        L.o_glibc_restated_diff.argtypes = [ctypes.c_int, ctypes.c_uint, ctypes.c_uint]
+        L.o_glibc_restated_diff.restype = ctypes.c_long
         _LIB = L
     return _LIB
 
@@ -326,12 +328,29 @@ def build() -> None:
                    stdout=subprocess.DEVNULL if not os.environ.get("TS_VERBOSE") else None)
 
 
-def randn(n: int, seed: int, correctly_rounded: bool = False) -> np.ndarray:
+def _libm_mode(correctly_rounded: bool, restated: bool) -> int:
+    """0: the host libm, as the reference; 1: f64 rounded once; 2: glibc 2.35's
+    evaluation restated in ts_oracle.c (the host libm's bits on this image)."""
+    return 1 if correctly_rounded else (2 if restated else 0)
+
+
+def randn(n: int, seed: int, correctly_rounded: bool = False, restated: bool = False) -> np.ndarray:
     """Tensor::randn(n, Some(seed)) values.  ``correctly_rounded`` evaluates ln
-    and cos in f64 and rounds once; otherwise the host libm's logf / cosf."""
+    and cos in f64 and rounds once; ``restated`` takes glibc 2.35's logf / cosf
+    restated; otherwise the host libm's logf / cosf."""
     out = np.empty(n, dtype=np.float32)
-    lib().o_randn(_p(out), n, ctypes.c_uint64(seed), int(correctly_rounded))
+    lib().o_randn(_p(out), n, ctypes.c_uint64(seed), _libm_mode(correctly_rounded, restated))
     return out
+
+
+GLIBC_RESTATED = {"exp": 0, "log": 1, "tanh": 2, "cos": 3, "expm1": 4}
+
+
+def glibc_restated_diff(fn: str, stride: int, offset: int = 0) -> int:
+    """Inputs (f32 bit patterns offset + k * stride; cos below 120 only) where
+    ts_oracle.c's restatement of glibc 2.35's expf / logf / tanhf / cosf /
+    expm1f differs from the host libm's."""
+    return int(lib().o_glibc_restated_diff(GLIBC_RESTATED[fn], stride, offset))
 
 
 def xorshift_next(s: int) -> int:
@@ -356,12 +375,13 @@ def libm_glibc_diff(which: int) -> int:
 UNARY = {"exp": 0, "log": 1, "sqrt": 2, "tanh": 3, "sigmoid": 4, "leaky_relu": 5}
 
 
-def unary(op: str, x, slope: float = 0.0, correctly_rounded: bool = False) -> np.ndarray:
+def unary(op: str, x, slope: float = 0.0, correctly_rounded: bool = False, restated: bool = False) -> np.ndarray:
     """tensor/ops/{exp,log,sqrt,tanh,sigmoid,leaky_relu}.rs forward.  exp / ln /
-    tanh come from the host libm unless ``correctly_rounded``."""
+    tanh come from the host libm unless ``correctly_rounded`` (f64 rounded
+    once) or ``restated`` (glibc 2.35's evaluation restated)."""
     x = _f32(x)
     out = np.empty_like(x)
-    lib().o_unary(UNARY[op], _p(x), _p(out), x.size, ctypes.c_float(slope), int(correctly_rounded))
+    lib().o_unary(UNARY[op], _p(x), _p(out), x.size, ctypes.c_float(slope), _libm_mode(correctly_rounded, restated))
     return out
 
 
@@ -380,11 +400,11 @@ def _axis_view(shape, dim):
     return outer, int(shape[dim]), inner
 
 
-def softmax(x, dim: int, correctly_rounded: bool = False) -> np.ndarray:
+def softmax(x, dim: int, correctly_rounded: bool = False, restated: bool = False) -> np.ndarray:
     x = _f32(x)
     y = np.empty_like(x)
     outer, red, inner = _axis_view(x.shape, dim)
-    lib().o_softmax(_p(x), _p(y), outer, red, inner, int(correctly_rounded))
+    lib().o_softmax(_p(x), _p(y), outer, red, inner, _libm_mode(correctly_rounded, restated))
     return y
 
 

@@ -39,7 +39,8 @@ import oracle as O
 _ids = itertools.count(1)
 
 # exp / ln / tanh in the recorded ops: False = the host libm (what the
-# reference computes), True = correctly rounded (what the device computes)
+# reference computes; the device restates glibc 2.35's evaluations, with
+# the same bits), True = f64 rounded once (correctly rounded)
 CORRECTLY_ROUNDED = False
 
 # thread-local GradGraph of the reference (engine.rs:697-699); one per process here

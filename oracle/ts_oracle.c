@@ -329,12 +329,262 @@ static float xs_unit(uint64_t *s) {
     return f;
 }
 
+/* ---- glibc 2.35's f32 exp / log / cos / tanh, restated (mode 2) ----------
+ *
+ * The reference takes these from the host libm (Rust's f32::exp / ln / cos /
+ * tanh call expf / logf / cosf / tanhf); the pinned libm is glibc 2.35 (the
+ * image's, Ubuntu 2.35-0ubuntu3).  Its algorithms are published:
+ *   expf, logf, cosf: Arm optimized-routines (MIT / Apache-2.0), shipped as
+ *     glibc's sysdeps/ieee754/flt-32/e_expf.c, e_logf.c, s_cosf.c with the
+ *     tables of e_exp2f_data.c, e_logf_data.c, s_sincosf_data.c; on an x86-64
+ *     CPU with FMA glibc selects the builds compiled with FMA (multiarch
+ *     e_expf-fma, e_logf-fma, s_cosf-fma), in which every product whose only
+ *     uses are additions is fused;
+ *   tanhf (with expm1f): fdlibm's s_tanhf.c / s_expm1f.c (Sun Microsystems,
+ *     "permission to use, copy, modify, and distribute this software is
+ *     freely granted, provided that this notice is preserved"), compiled
+ *     for plain x86-64, in f32 with no fused operations.
+ * Each function below restates that evaluation step by step in this file's
+ * own code, with the published constants (the exp table is 2^(i/32)
+ * rounded to double, computed here).  Pinned: o_glibc_restated_diff counts
+ * inputs where a restatement differs from the host libm; on every one of
+ * the 2^32 f32 inputs (|x| < 120 for cos, the only range used) the count is
+ * 0 on this image with FMA (tests/test_ops_oracle.py runs strided and dense
+ * sweeps).  Without FMA glibc's expf differs from this on 2 inputs of 2^32
+ * and cosf on 22 below 120. */
+static uint64_t d_bits(double x) { uint64_t u; memcpy(&u, &x, 8); return u; }
+static double d_of(uint64_t u) { double x; memcpy(&x, &u, 8); return x; }
+static uint32_t f_bits(float x) { uint32_t u; memcpy(&u, &x, 4); return u; }
+static float f_of(uint32_t u) { float x; memcpy(&x, &u, 4); return x; }
+
+/* expf: x = (k + r)/32 * ln2 with integer k (ties to even through the
+ * 1.5*2^52 shift) and |r| <= 1/2; exp(x) = 2^(k/32) * 2^(r/32), the first a
+ * table entry with k/32's integer part added to its exponent, the second a
+ * degree-3 polynomial, all in double, rounded to f32 once. */
+static uint64_t gl_exp_tab[32];
+static int gl_exp_ready;
+static void gl_exp_init(void) {
+    for (int i = 0; i < 32; ++i) /* 2^(i/32) rounded to double, less i/32 in the exponent field */
+        gl_exp_tab[i] = d_bits((double)exp2l((long double)i / 32)) - ((uint64_t)i << 52) / 32;
+    gl_exp_ready = 1;
+}
+static float gl_expf(float x) {
+    if (!gl_exp_ready) gl_exp_init();
+    const double InvLn2N = 0x1.71547652b82fep+0 * 32, SHIFT = 0x1.8p+52;
+    const double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, C1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                 C2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const uint32_t abstop = (f_bits(x) >> 20) & 0x7ff;
+    if (abstop >= 0x42b) { /* |x| >= 88, inf, nan */
+        if (f_bits(x) == f_bits(-INFINITY)) return 0.0f;
+        if (abstop >= 0x7f8) return x + x;
+        if (x > 0x1.62e42ep6f) return INFINITY;
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double xd = (double)x;
+    double kd = fma(InvLn2N, xd, SHIFT);
+    const uint64_t ki = d_bits(kd);
+    kd -= SHIFT;
+    const double r = fma(InvLn2N, xd, -kd);
+    const double s = d_of(gl_exp_tab[ki % 32] + (ki << 47));
+    const double z = fma(C0, r, C1), r2 = r * r;
+    double y = fma(C2, r, 1.0);
+    y = fma(z, r2, y);
+    return (float)(y * s);
+}
+
+/* logf: x = 2^k z with z in [0x3f330000, 2 * that) as bits; z's subinterval
+ * (16 of them) gives c ~ its centre: log(x) = log1p(z/c - 1) + log(c) + k ln2,
+ * log1p by a degree-4 polynomial, in double, rounded once. */
+static const double gl_log_invc[16] = {
+    0x1.661ec79f8f3bep+0, 0x1.571ed4aaf883dp+0, 0x1.49539f0f010bp+0,  0x1.3c995b0b80385p+0,
+    0x1.30d190c8864a5p+0, 0x1.25e227b0b8eap+0,  0x1.1bb4a4a1a343fp+0, 0x1.12358f08ae5bap+0,
+    0x1.0953f419900a7p+0, 0x1p+0,               0x1.e608cfd9a47acp-1, 0x1.ca4b31f026aap-1,
+    0x1.b2036576afce6p-1, 0x1.9c2d163a1aa2dp-1, 0x1.886e6037841edp-1, 0x1.767dcf5534862p-1};
+static const double gl_log_logc[16] = {
+    -0x1.57bf7808caadep-2, -0x1.2bef0a7c06ddbp-2, -0x1.01eae7f513a67p-2, -0x1.b31d8a68224e9p-3,
+    -0x1.6574f0ac07758p-3, -0x1.1aa2bc79c81p-3,  -0x1.a4e76ce8c0e5ep-4, -0x1.1973c5a611cccp-4,
+    -0x1.252f438e10c1ep-5, 0x0p+0,               0x1.aa5aa5df25984p-5,  0x1.c5e53aa362eb4p-4,
+    0x1.526e57720db08p-3,  0x1.bc2860d22477p-3,   0x1.1058bc8a07ee1p-2,  0x1.4043057b6ee09p-2};
+static float gl_logf(float x) {
+    const double A0 = -0x1.00ea348b88334p-2, A1 = 0x1.5575b0be00b6ap-2, A2 = -0x1.ffffef20a4123p-2,
+                 Ln2 = 0x1.62e42fefa39efp-1;
+    uint32_t ix = f_bits(x);
+    if (ix == 0x3f800000) return 0.0f;
+    if (ix - 0x00800000 >= 0x7f800000 - 0x00800000) { /* zero, subnormal, negative, inf, nan */
+        if (ix * 2 == 0) return -INFINITY;
+        if (ix == 0x7f800000) return x;
+        if ((ix & 0x80000000) || ix * 2 >= 0xff000000) return NAN;
+        ix = f_bits(x * 0x1p23f); /* normalise a subnormal */
+        ix -= 23u << 23;
+    }
+    const uint32_t tmp = ix - 0x3f330000;
+    const int i = (int)((tmp >> 19) % 16);
+    const int32_t k = (int32_t)tmp >> 23;
+    const double z = (double)f_of(ix - (tmp & 0xff800000u));
+    const double r = fma(z, gl_log_invc[i], -1.0);
+    const double y0 = fma((double)k, Ln2, gl_log_logc[i]);
+    const double r2 = r * r;
+    double y = fma(A1, r, A2);
+    y = fma(A0, r2, y);
+    y = fma(y, r2, y0 + r);
+    return (float)y;
+}
+
+/* cosf for |x| < 120: below pi/4 the even polynomial directly; else x less
+ * n * pi/2 (n from the 2/pi * 2^24 scaled product, rounded), the sign and
+ * the sin or cos polynomial by n's low bits; in double, rounded once. */
+typedef struct { double sign[4], hpi_inv, hpi, c0, c1, c2, c3, c4, s1, s2, s3; } gl_sincos_t;
+static const gl_sincos_t gl_sincos[2] = {
+    {{1.0, -1.0, -1.0, 1.0}, 0x1.45F306DC9C883p+23, 0x1.921FB54442D18p0, 0x1p0, -0x1.ffffffd0c621cp-2,
+     0x1.55553e1068f19p-5, -0x1.6c087e89a359dp-10, 0x1.99343027bf8c3p-16, -0x1.555545995a603p-3,
+     0x1.1107605230bc4p-7, -0x1.994eb3774cf24p-13},
+    {{1.0, -1.0, -1.0, 1.0}, 0x1.45F306DC9C883p+23, 0x1.921FB54442D18p0, -0x1p0, 0x1.ffffffd0c621cp-2,
+     -0x1.55553e1068f19p-5, 0x1.6c087e89a359dp-10, -0x1.99343027bf8c3p-16, -0x1.555545995a603p-3,
+     0x1.1107605230bc4p-7, -0x1.994eb3774cf24p-13}};
+static float gl_sincos_poly(double x, double x2, const gl_sincos_t *p, int n) {
+    if ((n & 1) == 0) { /* sin */
+        const double x3 = x * x2, s1 = fma(x2, p->s3, p->s2), x7 = x3 * x2, s = fma(x3, p->s1, x);
+        return (float)fma(x7, s1, s);
+    }
+    const double x4 = x2 * x2, c2 = fma(x2, p->c4, p->c3), c1 = fma(x2, p->c1, p->c0), x6 = x4 * x2,
+                 c = fma(x4, p->c2, c1);
+    return (float)fma(x6, c2, c);
+}
+static float gl_cosf(float y) { /* |y| < 120 */
+    const uint32_t top = (f_bits(y) >> 20) & 0x7ff;
+    const gl_sincos_t *p = &gl_sincos[0];
+    double x = (double)y;
+    if (top < ((f_bits(0x1.921FB6p-1f) >> 20) & 0x7ff)) { /* |y| < pi/4 */
+        if (top < ((f_bits(0x1p-12f) >> 20) & 0x7ff)) return 1.0f;
+        return gl_sincos_poly(x, x * x, p, 1);
+    }
+    const int n = (((int32_t)(x * p->hpi_inv)) + 0x800000) >> 24;
+    x = fma(-(double)n, p->hpi, x);
+    const double sgn = p->sign[n & 3];
+    if (n & 2) p = &gl_sincos[1];
+    return gl_sincos_poly(x * sgn, x * x, p, n ^ 1);
+}
+
+/* expm1f (fdlibm s_expm1f.c): x = k ln2 + r with |r| <= ln2/2 split into
+ * hi - lo, expm1(r) from a rational form with a degree-5 polynomial in
+ * r^2/2, then the exponent k applied; all in f32. */
+static float gl_expm1f(float x) {
+    const float one = 1.0f, huge = 1.0e+30f, tiny = 1.0e-30f, o_threshold = f_of(0x42b17180),
+                ln2_hi = f_of(0x3f317180), ln2_lo = f_of(0x3717f7d1), invln2 = f_of(0x3fb8aa3b),
+                Q1 = f_of(0xbd088889), Q2 = f_of(0x3ad00d01), Q3 = f_of(0xb8a670cd), Q4 = f_of(0x36867e54),
+                Q5 = f_of(0xb457edbb);
+    float y, hi, lo, c = 0.0f, t, e, hxs, hfx, r1;
+    int32_t k;
+    uint32_t hx = f_bits(x);
+    const uint32_t xsb = hx & 0x80000000u;
+    hx &= 0x7fffffff;
+    if (hx >= 0x4195b844) { /* |x| >= 27 ln2 */
+        if (hx >= 0x42b17218) {
+            if (hx > 0x7f800000) return x + x;
+            if (hx == 0x7f800000) return xsb == 0 ? x : -1.0f;
+            if (x > o_threshold) return huge * huge;
+        }
+        if (xsb != 0 && x + tiny < 0.0f) return tiny - one;
+    }
+    if (hx > 0x3eb17218) { /* |x| > ln2/2 */
+        if (hx < 0x3F851592) { /* and < 3 ln2/2 */
+            if (xsb == 0) { hi = x - ln2_hi; lo = ln2_lo; k = 1; }
+            else { hi = x + ln2_hi; lo = -ln2_lo; k = -1; }
+        } else {
+            k = (int32_t)(invln2 * x + (xsb == 0 ? 0.5f : -0.5f));
+            t = (float)k;
+            hi = x - t * ln2_hi;
+            lo = t * ln2_lo;
+        }
+        x = hi - lo;
+        c = (hi - x) - lo;
+    } else if (hx < 0x33000000) { /* |x| < 2^-25 */
+        t = huge + x;
+        return x - (t - (huge + x));
+    } else {
+        k = 0;
+    }
+    hfx = 0.5f * x;
+    hxs = x * hfx;
+    r1 = one + hxs * (Q1 + hxs * (Q2 + hxs * (Q3 + hxs * (Q4 + hxs * Q5))));
+    t = 3.0f - r1 * hfx;
+    e = hxs * ((r1 - t) / (6.0f - x * t));
+    if (k == 0) return x - (x * e - hxs);
+    e = x * (e - c) - c;
+    e -= hxs;
+    if (k == -1) return 0.5f * (x - e) - 0.5f;
+    if (k == 1) return x < -0.25f ? -2.0f * (e - (x + 0.5f)) : one + 2.0f * (x - e);
+    if (k <= -2 || k > 56) {
+        y = one - (e - x);
+        if (k == 128) y = y * 2.0f * f_of(0x7f000000);
+        else y = f_of(f_bits(y) + ((uint32_t)k << 23));
+        return y - one;
+    }
+    if (k < 23) {
+        t = f_of(0x3f800000 - (0x1000000u >> k)); /* 1 - 2^-k */
+        y = t - (e - x);
+    } else {
+        t = f_of((uint32_t)(0x7f - k) << 23); /* 2^-k */
+        y = x - (e + t);
+        y += one;
+    }
+    return f_of(f_bits(y) + ((uint32_t)k << 23));
+}
+
+/* tanhf (fdlibm s_tanhf.c): 1 - 2/(expm1(2|x|) + 2) for |x| >= 1,
+ * -t/(t + 2) with t = expm1(-2|x|) below, 1 past 22, the sign restored. */
+static float gl_tanhf(float x) {
+    const float one = 1.0f, two = 2.0f, tiny = 1.0e-30f;
+    float t, z;
+    const int32_t jx = (int32_t)f_bits(x), ix = jx & 0x7fffffff;
+    if (ix >= 0x7f800000) return jx >= 0 ? one / x + one : one / x - one;
+    if (ix < 0x41b00000) { /* |x| < 22 */
+        if (ix == 0) return x;
+        if (ix < 0x24000000) return x * (one + x); /* |x| < 2^-55 */
+        if (ix >= 0x3f800000) {
+            t = gl_expm1f(two * fabsf(x));
+            z = one - two / (t + two);
+        } else {
+            t = gl_expm1f(-two * fabsf(x));
+            z = -t / (t + two);
+        }
+    } else {
+        z = one - tiny;
+    }
+    return jx >= 0 ? z : -z;
+}
+
+/* Inputs x = offset + k * stride (as f32 bit patterns) where the
+ * restatement of op (0 exp, 1 log, 2 tanh, 3 cos below 120, 4 expm1)
+ * differs from the host libm's (any two NaNs agree). */
+EXPORT long o_glibc_restated_diff(int op, unsigned stride, unsigned offset) {
+    long diff = 0;
+    for (uint64_t u = offset; u < (1ull << 32); u += stride) {
+        const float x = f_of((uint32_t)u);
+        float a, b;
+        switch (op) {
+            case 0: a = expf(x); b = gl_expf(x); break;
+            case 1: a = logf(x); b = gl_logf(x); break;
+            case 2: a = tanhf(x); b = gl_tanhf(x); break;
+            case 3: if (!(fabsf(x) < 120.0f)) continue; a = cosf(x); b = gl_cosf(x); break;
+            default: a = expm1f(x); b = gl_expm1f(x); break;
+        }
+        if (f_bits(a) != f_bits(b) && !(isnan(a) && isnan(b))) ++diff;
+    }
+    return diff;
+}
+
 /* f32 natural log and cosine.  mode 0 calls the host libm's logf / cosf, as
  * Rust's f32::ln / f32::cos do; mode 1 evaluates in f64 and rounds once,
  * which is correctly rounded on every input next_normal can produce
- * (checked against long double by o_libm_cr_check). */
-static float ln_f32(float x, int mode) { return mode ? (float)log((double)x) : logf(x); }
-static float cos_f32(float x, int mode) { return mode ? (float)cos((double)x) : cosf(x); }
+ * (checked against long double by o_libm_cr_check); mode 2 is glibc 2.35's
+ * evaluation restated (above), mode 0's bits without the host libm. */
+static float ln_f32(float x, int mode) {
+    return mode == 1 ? (float)log((double)x) : mode == 2 ? gl_logf(x) : logf(x);
+}
+static float cos_f32(float x, int mode) {
+    return mode == 1 ? (float)cos((double)x) : mode == 2 ? gl_cosf(x) : cosf(x);
+}
 
 /* 2*PI in fp32: std::f32::consts::PI (0x40490FDB) doubled exactly. */
 static const float kTwoPiF = 6.28318548202514648438f;
@@ -401,10 +651,13 @@ EXPORT long o_libm_glibc_diff(int which) {
 /* ---- other recorded ops (tensor/ops/{exp,log,sqrt,tanh,sigmoid,leaky_relu,softmax}.rs) ---- */
 
 /* f32 exp / ln / tanh: mode 0 is the host libm (expf, logf, tanhf), which
- * Rust's f32::exp / ln / tanh call; mode 1 evaluates in f64 and rounds once. */
-static float f_exp(float x, int mode) { return mode ? (float)exp((double)x) : expf(x); }
-static float f_log(float x, int mode) { return mode ? (float)log((double)x) : logf(x); }
-static float f_tanh(float x, int mode) { return mode ? (float)tanh((double)x) : tanhf(x); }
+ * Rust's f32::exp / ln / tanh call; mode 1 evaluates in f64 and rounds once;
+ * mode 2 is glibc 2.35's evaluation restated (above). */
+static float f_exp(float x, int mode) { return mode == 1 ? (float)exp((double)x) : mode == 2 ? gl_expf(x) : expf(x); }
+static float f_log(float x, int mode) { return mode == 1 ? (float)log((double)x) : mode == 2 ? gl_logf(x) : logf(x); }
+static float f_tanh(float x, int mode) {
+    return mode == 1 ? (float)tanh((double)x) : mode == 2 ? gl_tanhf(x) : tanhf(x);
+}
 
 /* op: 0 exp (exp.rs scalar loop), 1 log (log.rs), 2 sqrt (sqrt.rs; AVX2
  * sqrt_ps and f32::sqrt are both correctly rounded), 3 tanh (tanh.rs),

@@ -185,3 +185,37 @@ def test_matmul_ranks_against_torch_autograd(sa, sb):
 def test_matmul_shape_errors(sa, sb, msg):
     with pytest.raises(ValueError, match=msg):
         G.OTensor(normal(sa, 1)).matmul(G.OTensor(normal(sb, 2)))
+
+
+def _glibc_2_35():
+    import platform
+    return platform.libc_ver() == ("glibc", "2.35")
+
+
+@pytest.mark.skipif(not _glibc_2_35(), reason="the restatement pins glibc 2.35, the image's libm")
+@pytest.mark.parametrize("fn", ["exp", "log", "tanh", "cos", "expm1"])
+def test_glibc_restatement_equals_the_host_libm(fn):
+    # ts_oracle.c's restatement of glibc 2.35's expf / logf / tanhf / cosf
+    # (below 120) / expm1f against the host libm on every 17th f32 bit
+    # pattern from two offsets (about 5e8 inputs; every one of the 2^32 was
+    # checked once, with 0 differences)
+    for off in (0, 8):
+        assert O.glibc_restated_diff(fn, 17, off) == 0, (fn, off)
+
+
+@pytest.mark.skipif(not _glibc_2_35(), reason="the restatement pins glibc 2.35, the image's libm")
+def test_glibc_restatement_through_the_ops_and_randn():
+    # the modes end to end: unary ops, softmax and randn in the restated mode
+    # equal the host-libm mode bit for bit, and the two differ from f64
+    # rounded once (a mutation that made the restated mode call the f64
+    # path would fail the last check)
+    x = normal(1 << 18, 11, 8.0)
+    for op in ("exp", "tanh", "sigmoid"):
+        assert_bits_equal(O.unary(op, x, restated=True), O.unary(op, x), op)
+    assert_bits_equal(O.unary("log", np.abs(x), restated=True), O.unary("log", np.abs(x)), "log")
+    y = normal((64, 257), 12, 5.0)
+    assert_bits_equal(O.softmax(y, 1, restated=True), O.softmax(y, 1), "softmax")
+    r = O.randn(1 << 20, 77, restated=True)
+    assert_bits_equal(r, O.randn(1 << 20, 77), "randn")
+    assert np.any(r != O.randn(1 << 20, 77, correctly_rounded=True))
+    assert np.any(O.unary("tanh", x, restated=True) != O.unary("tanh", x, correctly_rounded=True))

@@ -4,6 +4,7 @@
 // order, with no contraction (-ffp-contract=off) and IEEE division/sqrt, so
 // results are bit-identical to train-station's CPU path.
 #include "ts_hip_internal.h"
+#include "ts_hip_libm.h"
 
 namespace tship {
 
@@ -72,31 +73,26 @@ struct FillFromOp {
 
 // ---- activations (tensor/ops/{exp,log,sqrt,tanh,sigmoid,leaky_relu}.rs) ----
 // The reference calls f32::exp / ln / tanh, i.e. the host libm's expf / logf /
-// tanhf.  Here each is evaluated in f64 and rounded once: the correctly
-// rounded value, which those libm functions return on all but a small share
-// of inputs (where the two differ in the last place).
-__device__ inline float exp_cr(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
-__device__ inline float log_cr(float x) { return static_cast<float>(log(static_cast<double>(x))); }
-__device__ inline float tanh_cr(float x) { return static_cast<float>(tanh(static_cast<double>(x))); }
-
+// tanhf: glibc's evaluations, restated in ts_hip_libm.h, so every value has
+// the host libm's bits.
 struct ExpOp { static constexpr int NIN = 1, NOUT = 1;
-    __device__ void operator()(size_t, const float *x, float *y) const { y[0] = exp_cr(x[0]); } };
+    __device__ void operator()(size_t, const float *x, float *y) const { y[0] = libm::expf_glibc(x[0]); } };
 struct LogOp { static constexpr int NIN = 1, NOUT = 1;
-    __device__ void operator()(size_t, const float *x, float *y) const { y[0] = log_cr(x[0]); } };
+    __device__ void operator()(size_t, const float *x, float *y) const { y[0] = libm::logf_glibc(x[0]); } };
 // sqrt.rs: _mm256_sqrt_ps / f32::sqrt, both correctly rounded, as sqrtf is here
 struct SqrtOp { static constexpr int NIN = 1, NOUT = 1;
     __device__ void operator()(size_t, const float *x, float *y) const { y[0] = sqrtf(x[0]); } };
 struct TanhOp { static constexpr int NIN = 1, NOUT = 1;
-    __device__ void operator()(size_t, const float *x, float *y) const { y[0] = tanh_cr(x[0]); } };
+    __device__ void operator()(size_t, const float *x, float *y) const { y[0] = libm::tanhf_fdlibm(x[0]); } };
 // sigmoid.rs:9-21, the two-branch stable form
 struct SigmoidOp { static constexpr int NIN = 1, NOUT = 1;
     __device__ void operator()(size_t, const float *x, float *y) const {
         const float v = x[0];
         if (v >= 0.0f) {
-            const float z = exp_cr(-v);
+            const float z = libm::expf_glibc(-v);
             y[0] = 1.0f / (1.0f + z);
         } else {
-            const float z = exp_cr(v);
+            const float z = libm::expf_glibc(v);
             y[0] = z / (1.0f + z);
         }
     } };

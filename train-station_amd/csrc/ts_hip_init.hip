@@ -16,6 +16,7 @@
 // where those are not correctly rounded the two differ in the last place of
 // that intermediate.
 #include "ts_hip_internal.h"
+#include "ts_hip_libm.h"
 
 namespace tship {
 
@@ -79,9 +80,11 @@ __device__ inline float next_normal(uint64_t &s) {
     const float u2 = unit_of(s);
     if (u1 <= 0.0f) u1 = 1e-7f;
     else if (u1 >= 1.0f) u1 = 1.0f - 1e-7f;
-    const float l = static_cast<float>(log(static_cast<double>(u1)));
+    // f32::ln / f32::cos of the reference: the host libm's logf / cosf,
+    // restated (ts_hip_libm.h; 2*pi*u2 is in [0, 2*pi), the range restated)
+    const float l = libm::logf_glibc(u1);
     const float r = sqrtf(-2.0f * l);
-    const float c = static_cast<float>(cos(static_cast<double>(kTwoPiF * u2)));
+    const float c = libm::cosf_glibc_small(kTwoPiF * u2);
     const float z = r * c;
     return (__builtin_isnan(z) || __builtin_isinf(z)) ? 0.0f : z;
 }

@@ -5,10 +5,12 @@
 // scale by 1/sum; backward a sequential fp32 dot then y * (go - dot) -- so
 // the results are those of the reference's loops, element for element.
 #include "ts_hip_internal.h"
+#include "ts_hip_libm.h"
 
 namespace tship {
 
-__device__ inline float softmax_exp(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
+// f32::exp of the reference: the host libm's expf, restated (ts_hip_libm.h)
+__device__ inline float softmax_exp(float x) { return libm::expf_glibc(x); }
 
 __global__ __launch_bounds__(kBlock) void softmax_fwd(const float *__restrict__ x, float *__restrict__ y,
                                                       size_t outer, size_t reduce, size_t inner) {
