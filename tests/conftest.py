@@ -86,10 +86,13 @@ def rel_l2(got, want) -> float:
 def sum_order_model(values, mean=False, aligned=True, times=None) -> np.float32:
     """The fp32 result of ts_hip_sum / ts_hip_mean (and of a fused sum in
     ts_hip_map) over `values`, in the partition's order, restated in numpy:
-    ceil(n / 1024) first-pass workgroups (at most 2048) of 256 threads; thread
-    t adds, in f64 from +0, each float4 group g = t, t + stride, ... as
+    R float4 groups per thread (1 while ceil(n / 1024) <= 2048, else
+    max(4, ceil(n / 2^26))) and ceil(n / (1024 R)) first-pass workgroups of
+    256 threads; thread t of workgroup b adds, in f64 from +0, the groups
+    g = 256 R b + t + 256 j, j = 0 .. R - 1 (those below n4), each as
     ((x0 + x1) + x2) + x3 (no groups when the input is not 16-byte aligned),
-    then the elements 4 * n4 + t, ... past the groups; a workgroup's sum is the
+    then the elements 4 * n4 + T, T + 256 * blocks, ... past the groups
+    (T = 256 b + t); a workgroup's sum is the
     xor butterfly over each wave's 64 lanes, the four wave sums added from +0;
     the second pass's thread t adds partials t, t + 256, ... from +0, then the
     same workgroup sum; one rounding to fp32 (divided by (float)n for the
@@ -102,15 +105,18 @@ def sum_order_model(values, mean=False, aligned=True, times=None) -> np.float32:
     n = x.size
     if n == 0:
         return np.float32(0.0)
-    blocks = min(max((n + 1023) // 1024, 1), 2048)
+    run = 1 if (n + 1023) // 1024 <= 2048 else max(4, -(-n // (1024 * 65536)))
+    blocks = max(-(-n // (1024 * run)), 1)
     threads = blocks * 256
     n4 = n // 4 if aligned else 0
-    acc = np.zeros(threads)
     q = x[: 4 * n4].reshape(n4, 4)
-    quad = ((q[:, 0] + q[:, 1]) + q[:, 2]) + q[:, 3]
-    for g0 in range(0, n4, threads):
-        part = quad[g0: g0 + threads]
-        acc[: part.size] += part
+    quad = np.zeros(threads * run)  # padded with +0: adding it to an f64 sum from +0 changes nothing
+    quad[:n4] = ((q[:, 0] + q[:, 1]) + q[:, 2]) + q[:, 3]
+    runs = quad.reshape(blocks, run, 256)
+    acc = np.zeros((blocks, 256))
+    for j in range(run):
+        acc += runs[:, j, :]
+    acc = acc.reshape(threads)
     for i0 in range(4 * n4, n, threads):
         part = x[i0: i0 + threads]
         acc[: part.size] += part

@@ -169,7 +169,8 @@ def test_sum_and_mean(oracle, n):
 # the one-workgroup form (up to 16 first-pass workgroups, aligned) and the two
 # passes give the partition's bits, aligned or not
 @pytest.mark.parametrize("offset", [0, 1])
-@pytest.mark.parametrize("n", [1, 3, 4, 5, 1024, 1027, 4096, 10240, 15361, 16384, 16385, 100003, 1 << 22])
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 1024, 1027, 4096, 10240, 15361, 16384, 16385, 100003, 1 << 21,
+                               (1 << 21) + 4, 1 << 22, (1 << 22) + 5, 1 << 26])
 def test_sum_bits_follow_the_partition(n, offset):
     print(f"[sum bits] n={n} offset={offset}", flush=True)
     x = normal(n, 12)
@@ -182,8 +183,23 @@ def test_sum_bits_follow_the_partition(n, offset):
         assert_bits_equal(dout.get(), np.array([want], np.float32), f"{name} n={n} offset={offset}")
 
 
+def test_sum_bits_with_longer_runs():
+    # past 2^28 inputs a first-pass thread takes more than four groups (five here)
+    n = (1 << 28) + 12
+    print(f"[sum bits] n={n}", flush=True)
+    x = normal(n, 15)
+    dx = Dev.of(x)
+    ws = hip.ts_hip_sum_workspace_floats(n)
+    dws, dout = Dev(ws), Dev(1)
+    want = sum_order_model(x)
+    _run("ts_hip_sum", dx.ptr, n, dout.ptr, dws.ptr, ws, None)
+    assert_bits_equal(dout.get(), np.array([want], np.float32), f"sum n={n}")
+    _run("ts_hip_mean", dx.ptr, n, dout.ptr, dws.ptr, ws, None)
+    assert_bits_equal(dout.get(), np.array([want / np.float32(n)], np.float32), f"mean n={n}")
+
+
 @pytest.mark.parametrize("offset", [0, 1])
-@pytest.mark.parametrize("n", [1, 5, 1024, 4096, 8192, 8193, 16384, 100003])
+@pytest.mark.parametrize("n", [1, 5, 1024, 4096, 8192, 8193, 16384, 100003, (1 << 22) + 3])
 def test_dot_bits_follow_the_partition(n, offset):
     print(f"[dot bits] n={n} offset={offset}", flush=True)
     a, b = normal(n, 13), normal(n, 14)

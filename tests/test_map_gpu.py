@@ -136,7 +136,8 @@ def test_chain_multi_output_and_scalar_input():
 # up to 16 first-pass workgroups (n <= 16384) ts_hip_sum runs both passes in
 # one workgroup; the fused sum always takes two: the same bits either way,
 # the partition's order
-@pytest.mark.parametrize("n", [1, 4, 5, 1024, 4096, 10240, 12288, 16384, 16385, 100003, 1 << 22])
+@pytest.mark.parametrize("n", [1, 4, 5, 1024, 4096, 10240, 12288, 16384, 16385, 100003, 1 << 22, (1 << 22) + 13,
+                               1 << 26])
 @pytest.mark.parametrize("mean", [0, 1])
 def test_fused_sum_has_the_bits_of_ts_hip_sum(n, mean):
     from gpu_util import Dev, hip, hip_check, sync

@@ -321,6 +321,31 @@ def test_sum_order_model_known_answers():
         sq = np.sum(ints.astype(np.int64) ** 2)
         assert sum_order_model(ints, times=ints) == np.float32(sq)  # products exact in f64
     assert sum_order_model([]) == 0.0
+    # past 2048 workgroups a thread takes R consecutive groups of its
+    # workgroup's run (R = 4 up to 2^28 inputs; the longer runs past that are
+    # pinned on the device against this model): every element counted once
+    # (exact integer sums, ragged tails, unaligned) ...
+    for n in ((1 << 21) + 4, (1 << 22) + 7, (1 << 24) + 12):
+        ints = (np.arange(n, dtype=np.int32) % 97 - 48).astype(np.float32)
+        want = np.float32(np.sum(ints, dtype=np.float64))  # exact: integers far below 2^53
+        assert sum_order_model(ints) == want, n
+        assert sum_order_model(ints, aligned=False) == want, n
+        del ints
+    # ... and added one after another in that thread: 2^60 + 1 rounds back to
+    # 2^60 in f64, so 1, 2^60, -2^60, 1 in a thread's last four groups give
+    # exactly 1 (a tree, (1 + 2^60) + (-2^60 + 1), gives 0) and 2^60, -2^60,
+    # 1, 1 exactly 2
+    big = np.float32(2.0 ** 60)
+    for n, run, b, threads in (((1 << 22) + 4, 4, 3, (0, 77, 255)), ((1 << 24) + 12, 4, 4000, (129,))):
+        assert -(-n // (1024 * run)) > b  # workgroup b exists
+        for t in threads:
+            g = 256 * run * b + t  # thread t of workgroup b: groups g, g + 256, ...
+            for vals, want in (((1.0, big, -big, 1.0), 1.0), ((big, -big, 1.0, 1.0), 2.0)):
+                x = np.zeros(n, np.float32)
+                for j, v in enumerate(vals):
+                    x[4 * (g + 256 * (run - 4 + j)) + j] = v  # any lane of a group: its quad is v
+                assert sum_order_model(x) == np.float32(want), (n, t, vals)
+                del x
     x = normal(1 << 21, 5)
     exact = math.fsum(x.astype(np.float64))
     assert abs(float(sum_order_model(x)) - exact) <= 1e-6 * float(np.abs(x).sum(dtype=np.float64))

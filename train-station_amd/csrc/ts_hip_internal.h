@@ -102,12 +102,37 @@ __device__ __forceinline__ float4 load_nt(const float4 *p) {
 // ---- the scalar sum's partition (ts_hip_sum, and the fused sum of ts_hip_map,
 // which must give the same bits) ----------------------------------------------
 
-constexpr size_t kSumChunk = 1024;  // inputs per first-pass workgroup (minimum): one group of 4 per thread
-constexpr size_t kSumMaxBlocks = 2048;
+//
+// First-pass workgroup b takes the float4 groups [b * 256R, (b + 1) * 256R)
+// (those below n4), R = sum_run(n) groups per thread: thread t adds groups
+// b * 256R + t, + 256, ... in order, then the single elements past the groups,
+// 4 * n4 + T, T + 256 * blocks, ... (T = 256b + t, a grid stride).  Up to
+// kSumFlatBlocks workgroups a thread takes one group; past that four, in as
+// many workgroups as that takes (at most kSumMaxBlocks, then more groups per
+// thread).  Each workgroup covers a contiguous range and ends after a few
+// groups, so the hardware hands the next one to whichever CU frees first.
+// With a fixed grid striding over the whole input (2048 workgroups, a group
+// per thread per step), workgroups of one launch took from 0.3x to 1.5x
+// their median time and the launch ended with the slowest: the same
+// 24 B/element pass over 2^26 elements with its sum took 334 us that way and
+// 297 us with four groups per thread here.
+constexpr size_t kSumChunk = 1024;  // inputs per first-pass workgroup at one group of 4 per thread
+constexpr size_t kSumFlatBlocks = 2048;
+constexpr size_t kSumRun = 4;
+constexpr size_t kSumMaxBlocks = 65536;
 
+// Groups per thread of the first pass over n inputs.
+inline size_t sum_run(size_t n) {
+    if ((n + kSumChunk - 1) / kSumChunk <= kSumFlatBlocks) return 1;
+    const size_t r = (n + kSumChunk * kSumMaxBlocks - 1) / (kSumChunk * kSumMaxBlocks);
+    return r < kSumRun ? kSumRun : r;
+}
+
+// First-pass workgroups over n inputs (every group and element covered:
+// 1024 * R * blocks >= n).
 inline size_t sum_blocks(size_t n) {
-    size_t b = (n + kSumChunk - 1) / kSumChunk;
-    if (b > kSumMaxBlocks) b = kSumMaxBlocks;
+    const size_t per = kSumChunk * sum_run(n);
+    const size_t b = (n + per - 1) / per;
     return b < 1 ? 1 : b;
 }
 

@@ -414,16 +414,12 @@ extern "C" int ts_hip_map(const ts_hip_map_program *prog, size_t n, size_t tail_
             a.vreg[nv] = static_cast<int>(k);
             ++nv;
         }
-    unsigned blocks;
-    if (!reduce) {
-        const size_t rest = n - 4 * a.n4;
-        const size_t threads = a.n4 > rest ? a.n4 : rest;
-        // a group per thread up to 16 workgroups per CU, then several per
-        // thread (the prefetch overlaps them): a small program is one short
-        // round of loads, not a chain of them
-        blocks = grid_for(threads, 1);
-    } else {
-        blocks = static_cast<unsigned>(sum_blocks(n));
+    // the sum's partition with or without a sum: a group per thread up to
+    // 2048 workgroups, then four per thread in short workgroups (a fixed grid
+    // striding over the input ends with its slowest workgroup)
+    const unsigned blocks = static_cast<unsigned>(sum_blocks(n));
+    a.run = sum_run(n);
+    if (reduce) {
         if (!workspace || workspace_floats < 2 * static_cast<size_t>(blocks)) return TS_HIP_EWORKSPACE;
         if ((reinterpret_cast<uintptr_t>(workspace) & 7u) != 0) return TS_HIP_EINVAL;
         a.partial = reinterpret_cast<double *>(workspace);

@@ -34,6 +34,7 @@ using Seq4 = Seq<0, 1, 2, 3>;
 struct MapArgsK {
     ts_hip_map_program p;
     size_t n, n4, tail_start, check_start;
+    size_t run;  // float4 groups per thread (the sum's partition, sum_run)
     unsigned long long *zero_index;
     bool vec;  // every input and output is 16-byte aligned
     double *partial;  // reduce: one f64 partial per workgroup
@@ -86,12 +87,13 @@ __device__ __forceinline__ void store_outputs(const MapArgsK &a, size_t i0, bool
     }
 }
 
-// Groups of four elements, grid-stride: thread t takes groups t, t + stride,
-// ... (with a reduction the grid and order of ts_hip_sum's first pass: each
-// group's four values added in f64 left to right, then the remainder, so the
-// sum has the bits of ts_hip_sum over the stored values), the next group's
-// inputs loaded before the current group is evaluated, so a wave keeps loads
-// in flight while it computes.
+// Groups of four elements in ts_hip_sum's partition: workgroup b takes the
+// groups [b * 256R, (b + 1) * 256R), R = a.run, thread t groups b * 256R + t,
+// + 256, ..., then the elements past the groups with a grid stride (with a
+// reduction each group's four values added in f64 left to right, then the
+// remaining elements, so the sum has the bits of ts_hip_sum over the stored
+// values); the next group's inputs loaded before the current group is
+// evaluated, so a wave keeps loads in flight while it computes.
 //
 // 16-byte aligned operands, NV inputs read per element and NO stored values
 // known at compile time: every iteration then issues exactly NV loads and NO
@@ -103,6 +105,9 @@ template <bool REDUCE, int NV, int NO, class P>
 __device__ __forceinline__ void map_vec_body(const MapArgsK &a) {
     const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
     const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    const size_t base = static_cast<size_t>(blockIdx.x) * kBlock * a.run;
+    const size_t end = base + kBlock * a.run < a.n4 ? base + kBlock * a.run : a.n4;
+    const size_t g0 = base + threadIdx.x;
     const int rq = P::red_reg(a);
     double acc = 0.0;
     unsigned long long zmin = ~0ull;
@@ -118,8 +123,8 @@ __device__ __forceinline__ void map_vec_body(const MapArgsK &a) {
 #pragma unroll
         for (int j = 0; j < NV; ++j) nx[j] = *reinterpret_cast<const f4v_t *>(a.vin[j] + 4 * g);
     };
-    if (t < a.n4) fetch(t);
-    for (size_t g = t; g < a.n4; g += stride) {
+    if (g0 < end) fetch(g0);
+    for (size_t g = g0; g < end; g += kBlock) {
         float r0[kMapRegs], r1[kMapRegs], r2[kMapRegs], r3[kMapRegs];
 #pragma unroll
         for (int k = 0; k < kMapIn; ++k) {
@@ -136,7 +141,7 @@ __device__ __forceinline__ void map_vec_body(const MapArgsK &a) {
             r2[k] = nx[j][2];
             r3[k] = nx[j][3];
         }
-        const size_t gn = g + stride < a.n4 ? g + stride : a.n4 - 1;  // in range: the same loads every step
+        const size_t gn = g + kBlock < end ? g + kBlock : end - 1;  // in range: the same loads every step
         fetch(gn);
         P::run(a, 4 * g, zmin, Seq4{}, r0, r1, r2, r3);
 #pragma unroll
@@ -170,10 +175,12 @@ template <bool REDUCE, class P>
 __device__ __forceinline__ void map_any_body(const MapArgsK &a) {
     const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
     const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
+    const size_t base = static_cast<size_t>(blockIdx.x) * kBlock * a.run;
+    const size_t end = base + kBlock * a.run < a.n4 ? base + kBlock * a.run : a.n4;
     const int rq = P::red_reg(a);
     double acc = 0.0;
     unsigned long long zmin = ~0ull;
-    for (size_t g = t; g < a.n4; g += stride) {
+    for (size_t g = base + threadIdx.x; g < end; g += kBlock) {
         float r0[kMapRegs], r1[kMapRegs], r2[kMapRegs], r3[kMapRegs];
         load_inputs(a, 4 * g, a.vec, Seq4{}, r0, r1, r2, r3);
         P::run(a, 4 * g, zmin, Seq4{}, r0, r1, r2, r3);

@@ -8,18 +8,23 @@
 
 namespace tship {
 
-// Pass 1: workgroup b sums the float4 groups b, b+G, b+2G, ... (all threads
-// of the grid stride together) and writes one f64 partial.  PROD: the terms
-// are x[i] * y[i] formed in f64 (a dot product).
+// Pass 1: workgroup b sums its run of float4 groups [b * 256R, (b + 1) * 256R)
+// (thread t: b * 256R + t, + 256, ...), then the elements past the groups
+// with a grid stride, and writes one f64 partial (the partition of
+// sum_blocks / sum_run).  PROD: the terms are x[i] * y[i] formed in f64 (a
+// dot product).
 template <bool PROD>
 __global__ __launch_bounds__(kBlock) void sum_partial(const float *__restrict__ x, const float *__restrict__ y,
-                                                      size_t n, size_t n4, double *__restrict__ partial) {
+                                                      size_t n, size_t n4, size_t run,
+                                                      double *__restrict__ partial) {
     const size_t stride = static_cast<size_t>(gridDim.x) * kBlock;
     const size_t t = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const size_t base = static_cast<size_t>(blockIdx.x) * kBlock * run;
+    const size_t end = base + kBlock * run < n4 ? base + kBlock * run : n4;
     double acc = 0.0;
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
     const float4 *y4 = reinterpret_cast<const float4 *>(y);
-    for (size_t v = t; v < n4; v += stride) {
+    for (size_t v = base + threadIdx.x; v < end; v += kBlock) {
         const float4 q = x4[v];
         if (PROD) {
             const float4 r = y4[v];
@@ -41,13 +46,25 @@ __global__ __launch_bounds__(kBlock) void sum_final(const double *__restrict__ p
                                                     size_t nparts, size_t n, float *out) {
     double acc = 0.0;
     size_t i = threadIdx.x;
-    for (; i + kBlock * 7 < nparts; i += kBlock * 8) {  // eight loads in flight
-        double v[8];
+    // partials t, t + 256, ... added in order; loads issued D at a time before
+    // any is added (the partials come from every XCD's L2 through memory: one
+    // latency per round, so 16384 partials take one round of 64)
+    auto rounds = [&](auto d) {
+        constexpr int D = decltype(d)::value;
+        for (; i + kBlock * (D - 1) < nparts; i += kBlock * D) {
+            double v[D];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = partial[i + kBlock * j];
+            for (int j = 0; j < D; ++j) v[j] = partial[i + kBlock * j];
+            // every load issued before the first add (left to itself the
+            // scheduler moves each load down to its add, a few in flight)
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc += v[j];
-    }
+            for (int j = 0; j < D; ++j) acc += v[j];
+        }
+    };
+    rounds(std::integral_constant<int, 64>{});
+    rounds(std::integral_constant<int, 16>{});
+    rounds(std::integral_constant<int, 4>{});
     for (; i < nparts; i += kBlock) acc += partial[i];
     double r = block_sum(acc);
     if (threadIdx.x == 0) {
@@ -91,12 +108,13 @@ static int launch_sum(const float *x, const float *y, size_t n, float *out, floa
         else launch(sum_small<false, MEAN>, dim3(1), dim3(kBlock), 0, s, x, y, n, n4, nb, out);
         return launch_status();
     }
+    const size_t run = sum_run(n);
     if (y)
-        launch(sum_partial<true>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, y, n,
-                           n4, partial);
+        launch(sum_partial<true>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, y, n, n4, run,
+               partial);
     else
-        launch(sum_partial<false>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, y, n,
-                           n4, partial);
+        launch(sum_partial<false>, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, x, y, n, n4, run,
+               partial);
     int st = launch_status();
     if (st) return st;
     return launch_sum_final(partial, blocks, n, out, MEAN, s);
