@@ -1058,6 +1058,274 @@ __global__ __launch_bounds__(kBlock) void splitk_sum(const float *__restrict__ P
     C[i * ldc + j] = epilogue(e, acc, static_cast<int>(i), static_cast<int>(j));
 }
 
+// ---------------------------------------------------------------------------
+// 16x16x4 path for exact tilings (M and N multiples of 256, K of 32, no batch
+// rank): 256x256 tiles, 8 waves of 128x64, each 8x4 blocks of
+// v_mfma_f32_16x16x4_f32, two LDS stages of 32 k rows fed by LDS DMA.
+//
+// Every operand read is a 16-byte ds_read_b128 that feeds four MFMAs:
+//   k-major operand (stored [K][rows]): LDS stage [k][256]; lane (i, q) reads
+//     the 4 consecutive rows (columns) 64g + 4i .. +3 at k row kk, the operand
+//     of blocks 4g + 0 .. 4g + 3 (block b's lane i is row 64g + 4i + b);
+//   k-contiguous operand (stored [rows][K]): 16-byte chunks of 4 k, chunk
+//     (rho >> 4) * 128 + kq * 16 + (rho & 15) for LDS row rho and k quad kq,
+//     and LDS row rho holds matrix row w16_perm(rho) (the same interleave:
+//     block 4g + b's lane i is row 64g + 4i + b); lane (i, q) reads 4 k of
+//     one block, its operand for 4 k steps.
+// K step ks of a stage takes, in lane group q, k row 16 (ks / 4) + 4q + ks % 4
+// (the k-contiguous reads fix that order; the k-major reads follow it), so a
+// block's 16 k of a super step are added in another order than the 32x32
+// kernels' (a different rounding of the same sum).  A lane's accumulator
+// element v of blocks (4g + b, c) is C[64g + 16q + 4v + b][4i + c]: four
+// adjacent columns, stored as one 16-byte store.
+//
+// The DMA uses the scalar-base form (a wave-uniform row base in SGPRs plus a
+// 32-bit lane offset shared by all of a wave's instructions of one operand):
+// with a 64-bit address per instruction the compiler kept all eight live
+// across the loop and spilled.  The stage barrier comes before a stage's last
+// k step (vmcnt and lgkmcnt at zero first: the next stage has landed, and
+// every read of this buffer is done), so that k step's MFMAs cover the first
+// reads of the next stage.  SCHED picks where a stage's 8 DMA instructions go:
+// 0 two per k step over the first four, 1 one per k step over the first six
+// and two more in the first two.
+constexpr int kW16K = 32;
+__device__ __forceinline__ int w16_perm(int r) { return (r & ~63) | (4 * (r & 15) + ((r >> 4) & 3)); }
+
+template <bool KC>
+struct W16Op {
+    static __device__ __forceinline__ unsigned lane_off(int ld, int lane) {
+        return KC ? static_cast<unsigned>((4 * (lane & 15) * ld + 4 * (lane >> 4)) * 4)
+                  : static_cast<unsigned>(16 * lane);
+    }
+    // DMA instruction r (0..31) of the stage at k0 into S
+    static __device__ __forceinline__ void dma(const float *__restrict__ P, int ld, int r0, int k0, float *S, int r,
+                                               unsigned voff) {
+        const float *base;
+        float *dst;
+        if (KC) {
+            const int rb = r >> 1, hh = r & 1;
+            base = P + (size_t)(r0 + 64 * (rb >> 2) + (rb & 3)) * ld + k0 + 16 * hh;
+            dst = S + (rb * 128 + hh * 64) * 4;
+        } else {
+            base = P + (size_t)(k0 + r) * ld + r0;
+            dst = S + r * 256;
+        }
+        const unsigned lds = static_cast<unsigned>(reinterpret_cast<size_t>((lds_void *)dst));
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+                     : "memory", "m0");
+#pragma clang diagnostic pop
+    }
+    // k-contiguous: block x (LDS rows base + 16x ..) for super step sg
+    static __device__ __forceinline__ f4v_t kc(const float *S, int base, int x, int sg, int li, int lq) {
+        const int rho = base + 16 * x + li, kq = 4 * sg + lq;
+        return *reinterpret_cast<const f4v_t *>(S + ((rho >> 4) * 128 + kq * 16 + (rho & 15)) * 4);
+    }
+    // k-major: group gi (blocks 4gi .. 4gi+3) at k row kk
+    static __device__ __forceinline__ f4v_t km(const float *S, int base, int gi, int kk, int li) {
+        return *reinterpret_cast<const f4v_t *>(S + kk * 256 + base + 64 * gi + 4 * li);
+    }
+};
+
+// CS (TN only): B's column chunk sums as gemm_f32_lds_dma forms them (chunk c
+// of 64 k rows by the workgroups of tile row c % tiles_m, each column's rows
+// added in order from +0 in f64) by the first four waves from the B stages
+// in LDS: a stage's 32 rows over its first six k steps (5, 5, 5, 5, 6, 6),
+// each k step's rows read at its 5th MFMA and added at its 21st (read and
+// added at once, the waits for the reads made those four waves late at every
+// barrier: 22 us per 4096x4096x8192 product, against 6 us so).
+template <bool TA, bool TB, int EPI, bool CS, int SCHED>
+__global__ __launch_bounds__(512) void gemm_f32_w16(GemmArgs g) {
+    constexpr bool KCA = !TA, KCB = TB;
+    static_assert(!CS || (TA && !TB), "column sums on the TN layout only");
+    __shared__ __attribute__((aligned(16))) float As[2][kW16K * 256];
+    __shared__ __attribute__((aligned(16))) float Bs[2][kW16K * 256];
+    int tm, tn;
+    tile_coords(g.tiles_m, g.tiles_n, blockIdx.x, tm, tn);
+    const int i0 = tm * 256, j0 = tn * 256;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 2, wn = wave & 3;
+    const int li = lane & 15, lq = lane >> 4;
+    const int abase = wm * 128, bbase = wn * 64;
+    f4v_t acc[8][4];
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = f4v_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const bool cs_wave = CS && wave < 4;  // uniform
+    const int cs_c = threadIdx.x & 255;
+    double cs_s = 0.0;
+    float cs_v[6];
+    auto cs_first = [](int ks) { return ks < 4 ? 5 * ks : 20 + 6 * (ks - 4); };
+    auto cs_count = [](int ks) { return ks < 4 ? 5 : 6; };
+    auto cs_load = [&](int buf, int st, int ks) {
+        if (cs_wave && ((st >> 1) % g.tiles_m) == tm)
+#pragma unroll
+            for (int r = 0; r < cs_count(ks); ++r) cs_v[r] = Bs[buf][(cs_first(ks) + r) * 256 + cs_c];
+    };
+    auto cs_add = [&](int st, int ks) {
+        if (cs_wave && ((st >> 1) % g.tiles_m) == tm)
+#pragma unroll
+            for (int r = 0; r < cs_count(ks); ++r) cs_s += (double)cs_v[r];
+    };
+    auto cs_flush = [&](int st) {
+        if (cs_wave && ((st >> 1) % g.tiles_m) == tm) {
+            g.colsum_part[(size_t)(st >> 1) * g.N + j0 + cs_c] = cs_s;
+            cs_s = 0.0;
+        }
+    };
+
+    const unsigned voff = wave < 4 ? W16Op<KCA>::lane_off(g.lda, lane) : W16Op<KCB>::lane_off(g.ldb, lane);
+    auto dma = [&](int st, int buf, int i) {  // instruction i (0..7) of this wave: A's 32, then B's
+        const int r = wave * 8 + i;
+        if (r < 32) W16Op<KCA>::dma(g.A, g.lda, i0, st * kW16K, As[buf], r, voff);
+        else W16Op<KCB>::dma(g.B, g.ldb, j0, st * kW16K, Bs[buf], r - 32, voff);
+    };
+    f4v_t FAm[2][2], FAc[8], FBm[2], FBc[2][4];
+    auto kk_of = [&](int ks) { return 16 * (ks >> 2) + 4 * lq + (ks & 3); };
+    auto rd_km = [&](int buf, int ks, int slot) {
+        if (!KCA) {
+            FAm[slot][0] = W16Op<false>::km(As[buf], abase, 0, kk_of(ks), li);
+            FAm[slot][1] = W16Op<false>::km(As[buf], abase, 1, kk_of(ks), li);
+        }
+        if (!KCB) FBm[slot] = W16Op<false>::km(Bs[buf], bbase, 0, kk_of(ks), li);
+    };
+    auto rd_kcb = [&](int buf, int sg, int slot) {
+        if (KCB)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) FBc[slot][c] = W16Op<true>::kc(Bs[buf], bbase, c, sg, li, lq);
+    };
+    auto rd_kca = [&](int buf, int sg, int x) {
+        if (KCA) FAc[x] = W16Op<true>::kc(As[buf], abase, x, sg, li, lq);
+    };
+    auto mf = [&](int ks, int idx) {  // A block x = idx / 4, B block c = idx % 4
+        const int x = idx >> 2, c = idx & 3, s = ks & 3, slot = ks & 1, bslot = (ks >> 2) & 1;
+        const float a = KCA ? FAc[x][s] : FAm[slot][x >> 2][x & 3];
+        const float b = KCB ? FBc[bslot][c][s] : FBm[slot][c];
+        acc[x][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc[x][c], 0, 0, 0);
+    };
+
+    const int nst = g.K / kW16K;  // >= 1
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dma(0, 0, i);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    rd_km(0, 0, 0);
+    rd_kcb(0, 0, 0);
+#pragma unroll
+    for (int x = 0; x < 8; ++x) rd_kca(0, 0, x);
+    for (int st = 0; st < nst; ++st) {
+        const int buf = st & 1, nb = buf ^ 1;
+        // past the last stage the DMA reloads it into the free buffer (in bounds, never read)
+        const int sn = st + 1 < nst ? st + 1 : st;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            if (ks == 7) {
+                asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+                __syncthreads();
+            }
+            const int rbuf = ks == 7 ? nb : buf;  // the reads issued in this k step: the next one's
+#pragma unroll
+            for (int idx = 0; idx < 32; ++idx) {
+                mf(ks, idx);
+                if (idx == 1) rd_km(rbuf, (ks + 1) & 7, (ks + 1) & 1);
+                if (KCB && (ks & 3) == 3 && idx == 3) rd_kcb(rbuf, ((ks + 1) >> 2) & 1, ((ks >> 2) + 1) & 1);
+                if (KCA && (ks & 3) == 3 && (idx & 3) == 3) rd_kca(rbuf, ((ks + 1) >> 2) & 1, idx >> 2);
+                if (SCHED == 1) {
+                    if (ks < 6 && idx == 16) dma(sn, nb, ks);
+                    if (ks < 2 && idx == 24) dma(sn, nb, 6 + ks);
+                } else {
+                    if (ks < 4 && (idx == 8 || idx == 24)) dma(sn, nb, 2 * ks + (idx >> 4));
+                }
+                if (CS && idx == 4 && ks < 6) cs_load(buf, st, ks);
+                if (CS && idx == 20 && ks < 6) cs_add(st, ks);
+                __builtin_amdgcn_sched_barrier(0);  // reads and DMA stay where they are written
+            }
+        }
+        if (CS && (st & 1)) cs_flush(st);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA outstanding at exit
+    if (CS && (nst & 1)) cs_flush(nst - 1);            // a last chunk of one stage
+
+    // store, with the epilogue of store_tile (bias, relu, then the mask); the
+    // bias loaded once and each row group's 16 mask vectors before its first
+    // store, each batch awaited once (awaited one by one, the NT product with
+    // its mask ran 5% slower)
+    float *Cp = g.C;
+    const bool vec = ((reinterpret_cast<uintptr_t>(Cp) & 15) == 0) && (g.ldc % 4 == 0) &&
+                     (EPI != kEpiAll || !g.mask || (reinterpret_cast<uintptr_t>(g.mask) & 15) == 0);
+    const int col = j0 + bbase + 4 * li;
+    float bj[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (EPI != kEpiNone && g.bias) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) bj[c] = g.bias[col + c];
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    }
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg) {
+        f4v_t mk[4][4];
+        if (EPI == kEpiAll && g.mask) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const size_t at = (size_t)(i0 + abase + 64 * gg + 16 * lq + 4 * v + b) * g.ldc + col;
+                    if (vec) {
+                        mk[v][b] = *reinterpret_cast<const f4v_t *>(g.mask + at);
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) mk[v][b][c] = g.mask[at + c];
+                    }
+                }
+            __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int x = 4 * gg + b;
+                const size_t at = (size_t)(i0 + abase + 64 * gg + 16 * lq + 4 * v + b) * g.ldc + col;
+                float o[4] = {acc[x][0][v], acc[x][1][v], acc[x][2][v], acc[x][3][v]};
+                if (EPI != kEpiNone) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        float val = o[c];
+                        if (g.bias) val = val + bj[c];
+                        if (g.relu) val = val > 0.0f ? val : 0.0f;
+                        if (EPI == kEpiAll && g.mask) val = mk[v][b][c] > 0.0f ? val : 0.0f;
+                        o[c] = val;
+                    }
+                }
+                if (vec) {
+                    *reinterpret_cast<f4v_t *>(Cp + at) = f4v_t{o[0], o[1], o[2], o[3]};
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) Cp[at + c] = o[c];
+                }
+            }
+        if (EPI == kEpiAll) __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+template <bool TA, bool TB, int EPI, bool CS, int SCHED>
+static void launch_w16(GemmArgs g, hipStream_t s) {
+    g.tiles_m = g.M / 256;
+    g.tiles_n = g.N / 256;
+    g.tiles = g.tiles_m * g.tiles_n;
+    launch((gemm_f32_w16<TA, TB, EPI, CS, SCHED>), dim3(static_cast<unsigned>(g.tiles)), dim3(512), 0, s, g);
+}
+
+// The 16x16x4 kernel takes a product when its tiling is exact, it has no
+// batch rank and the lane offsets of its DMA fit 32 bits.
+static bool w16_fits(const GemmArgs &g, unsigned batches) {
+    const long long lim = 1LL << 31;
+    return batches == 1 && g.batch_rank == 0 && g.M % 256 == 0 && g.N % 256 == 0 && g.K % kW16K == 0 &&
+           g.K >= kW16K && 64LL * g.lda * 4 < lim && 64LL * g.ldb * 4 < lim;
+}
+
 template <bool TA, bool TB, int EPI, bool CS = false, int SUB = 1>
 static void launch_dma(GemmArgs g, hipStream_t s, unsigned batches) {
     g.tiles_m = (g.M + 255) / 256;
@@ -1073,6 +1341,21 @@ static void launch_dma(GemmArgs g, hipStream_t s, unsigned batches) {
 // the faster measured per layout.
 static void launch_dma_layout(int ta, int tb, const GemmArgs &g, hipStream_t s, unsigned nb) {
     const bool epi = g.bias || g.mask || g.relu;
+    // the 16x16x4 kernel for NN and TN (its DMA spread measured per layout);
+    // NT stays on the 32x32x2 kernel, 0.3-0.5% faster there (same box, with
+    // and without the relu mask)
+    if (!tb && w16_fits(g, nb)) {
+        if (!ta) {
+            if (g.mask) launch_w16<false, false, kEpiAll, false, 1>(g, s);
+            else if (epi) launch_w16<false, false, kEpiBiasRelu, false, 1>(g, s);
+            else launch_w16<false, false, kEpiNone, false, 1>(g, s);
+        } else {
+            if (g.colsum) launch_w16<true, false, kEpiNone, true, 0>(g, s);
+            else if (epi) launch_w16<true, false, kEpiAll, false, 0>(g, s);
+            else launch_w16<true, false, kEpiNone, false, 0>(g, s);
+        }
+        return;
+    }
     if (!ta && !tb) {
         if (g.mask) launch_dma<false, false, kEpiAll>(g, s, nb);
         else if (epi) launch_dma<false, false, kEpiBiasRelu>(g, s, nb);
