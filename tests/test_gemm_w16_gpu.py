@@ -1,6 +1,7 @@
 """The 16x16x4 kernel (gemm_f32_w16: M and N multiples of 256, K of 32, at
-least one 256x256 tile per CU; the NN and TN layouts): its corners against the
-f64 product, the column sums' fixed order and the separate epilogue kernels."""
+least one 256x256 tile per CU; the NN, NT and TN layouts, TT keeping the 32x32
+kernel): its corners against the f64 product, the column sums' fixed order and
+the separate epilogue kernels."""
 from __future__ import annotations
 
 import numpy as np
@@ -10,39 +11,49 @@ from conftest import assert_bits_equal, max_rel, normal
 
 pytestmark = pytest.mark.gpu
 
-# (trans_a, M, N, K, operand pitch pad, output pitch pad, C offset in floats)
+# (trans_a, trans_b, M, N, K, operand pitch pad, output pitch pad, C offset in floats)
 CASES = [
-    (0, 4096, 4096, 32, 0, 0, 0),     # one stage
-    (0, 4096, 4096, 96, 0, 0, 0),     # an odd stage count
-    (1, 4096, 4096, 32, 0, 0, 0),
-    (1, 4096, 4096, 160, 0, 0, 0),
-    (0, 4096, 4096, 64, 4, 8, 0),     # operand and output pitches past the matrix
-    (1, 4096, 4096, 64, 12, 4, 0),
-    (0, 4096, 4096, 64, 0, 0, 1),     # C not 16-byte aligned: element stores
-    (1, 4096, 4096, 64, 0, 0, 1),
-    (0, 256, 65536, 64, 0, 0, 0),     # one tile row
-    (0, 65536, 256, 64, 0, 0, 0),     # one tile column
+    (0, 0, 4096, 4096, 32, 0, 0, 0),     # one stage
+    (0, 0, 4096, 4096, 96, 0, 0, 0),     # an odd stage count
+    (1, 0, 4096, 4096, 32, 0, 0, 0),
+    (1, 0, 4096, 4096, 160, 0, 0, 0),
+    (0, 1, 4096, 4096, 32, 0, 0, 0),
+    (0, 1, 4096, 4096, 96, 0, 0, 0),
+    (0, 0, 4096, 4096, 64, 4, 8, 0),     # operand and output pitches past the matrix
+    (1, 0, 4096, 4096, 64, 12, 4, 0),
+    (0, 1, 4096, 4096, 64, 8, 4, 0),
+    (0, 0, 4096, 4096, 64, 0, 0, 1),     # C not 16-byte aligned: element stores
+    (1, 0, 4096, 4096, 64, 0, 0, 1),
+    (0, 1, 4096, 4096, 64, 0, 0, 1),
+    (0, 0, 256, 65536, 64, 0, 0, 0),     # one tile row
+    (0, 0, 65536, 256, 64, 0, 0, 0),     # one tile column
+    (0, 1, 256, 65536, 64, 0, 0, 0),
+    (0, 1, 65536, 256, 64, 0, 0, 0),
 ]
 
 
-@pytest.mark.parametrize("ta,M,N,K,pad,cpad,coff", CASES)
-def test_w16_products(oracle, ta, M, N, K, pad, cpad, coff):
+@pytest.mark.parametrize("ta,tb,M,N,K,pad,cpad,coff", CASES)
+def test_w16_products(oracle, ta, tb, M, N, K, pad, cpad, coff):
     from gpu_util import Dev, hip, hip_check, sync
 
-    print(f"[w16] ta={ta} M={M} N={N} K={K} pad={pad} cpad={cpad} coff={coff}", flush=True)
+    print(f"[w16] ta={ta} tb={tb} M={M} N={N} K={K} pad={pad} cpad={cpad} coff={coff}", flush=True)
     a = normal((K, M) if ta else (M, K), 21)
-    b = normal((K, N), 22)
-    lda = a.shape[1] + pad
-    apad = np.zeros((a.shape[0], lda), np.float32)
-    apad[:, : a.shape[1]] = a
+    b = normal((N, K) if tb else (K, N), 22)
+
+    def padded(x):  # the matrix in a buffer whose row pitch is `pad` floats longer
+        out = np.zeros((x.shape[0], x.shape[1] + pad), np.float32)
+        out[:, : x.shape[1]] = x
+        return out
+
+    lda, ldb = a.shape[1] + pad, b.shape[1] + pad
     ldc = N + cpad
     c0 = np.full((M, ldc), np.nan, np.float32)
-    da, db, dc = Dev.of(apad), Dev.of(b), Dev.of(c0, offset=coff)
-    hip_check(hip.ts_hip_gemm(ta, 0, M, N, K, da.ptr, lda, db.ptr, N, dc.ptr, ldc, None), "ts_hip_gemm")
+    da, db, dc = Dev.of(padded(a)), Dev.of(padded(b)), Dev.of(c0, offset=coff)
+    hip_check(hip.ts_hip_gemm(ta, tb, M, N, K, da.ptr, lda, db.ptr, ldb, dc.ptr, ldc, None), "ts_hip_gemm")
     sync()
     out = dc.get((M, ldc))
     got = out[:, :N]
-    want = oracle.gemm_f64(a, b, ta=bool(ta), tb=False)
+    want = oracle.gemm_f64(a, b, ta=bool(ta), tb=bool(tb))
     assert max_rel(got, want) <= 1e-4
     tol = 1e-4 * np.maximum(np.abs(want), np.sqrt(np.mean(want * want)))
     assert np.all(np.abs(got.astype(np.float64) - want) <= tol)

@@ -1117,10 +1117,13 @@ struct W16Op {
                      : "memory", "m0");
 #pragma clang diagnostic pop
     }
-    // k-contiguous: block x (LDS rows base + 16x ..) for super step sg
-    static __device__ __forceinline__ f4v_t kc(const float *S, int base, int x, int sg, int li, int lq) {
-        const int rho = base + 16 * x + li, kq = 4 * sg + lq;
-        return *reinterpret_cast<const f4v_t *>(S + ((rho >> 4) * 128 + kq * 16 + (rho & 15)) * 4);
+    // k-contiguous: block x (LDS rows base + 16x .., base a multiple of 16)
+    // for super step sg: chunk ((base >> 4) + x) * 128 + (4 sg + q) * 16 + i,
+    // i.e. the lane index times 4 floats past a wave-uniform offset (written
+    // so: from the chunk formula the compiler kept an address per block,
+    // super step and buffer)
+    static __device__ __forceinline__ f4v_t kc(const float *S, int base, int x, int sg, int lane) {
+        return *reinterpret_cast<const f4v_t *>(S + ((base >> 4) + x) * 512 + sg * 256 + lane * 4);
     }
     // k-major: group gi (blocks 4gi .. 4gi+3) at k row kk
     static __device__ __forceinline__ f4v_t km(const float *S, int base, int gi, int kk, int li) {
@@ -1196,10 +1199,10 @@ __global__ __launch_bounds__(512) void gemm_f32_w16(GemmArgs g) {
     auto rd_kcb = [&](int buf, int sg, int slot) {
         if (KCB)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) FBc[slot][c] = W16Op<true>::kc(Bs[buf], bbase, c, sg, li, lq);
+            for (int c = 0; c < 4; ++c) FBc[slot][c] = W16Op<true>::kc(Bs[buf], bbase, c, sg, lane);
     };
     auto rd_kca = [&](int buf, int sg, int x) {
-        if (KCA) FAc[x] = W16Op<true>::kc(As[buf], abase, x, sg, li, lq);
+        if (KCA) FAc[x] = W16Op<true>::kc(As[buf], abase, x, sg, lane);
     };
     auto mf = [&](int ks, int idx) {  // A block x = idx / 4, B block c = idx % 4
         const int x = idx >> 2, c = idx & 3, s = ks & 3, slot = ks & 1, bslot = (ks >> 2) & 1;
@@ -1341,11 +1344,14 @@ static void launch_dma(GemmArgs g, hipStream_t s, unsigned batches) {
 // the faster measured per layout.
 static void launch_dma_layout(int ta, int tb, const GemmArgs &g, hipStream_t s, unsigned nb) {
     const bool epi = g.bias || g.mask || g.relu;
-    // the 16x16x4 kernel for NN and TN (its DMA spread measured per layout);
-    // NT stays on the 32x32x2 kernel, 0.3-0.5% faster there (same box, with
-    // and without the relu mask)
-    if (!tb && w16_fits(g, nb)) {
-        if (!ta) {
+    // the 16x16x4 kernel for NN, NT and TN (its DMA spread measured per
+    // layout; NT alone ran as fast on either kernel, in config 5's step 44 us
+    // faster per launch on this one)
+    if (!(ta && tb) && w16_fits(g, nb)) {
+        if (!ta && tb) {
+            if (epi) launch_w16<false, true, kEpiAll, false, 0>(g, s);
+            else launch_w16<false, true, kEpiNone, false, 0>(g, s);
+        } else if (!ta) {
             if (g.mask) launch_w16<false, false, kEpiAll, false, 1>(g, s);
             else if (epi) launch_w16<false, false, kEpiBiasRelu, false, 1>(g, s);
             else launch_w16<false, false, kEpiNone, false, 1>(g, s);
