@@ -455,7 +455,7 @@ def run_mlp(TS, hip, hip_check, cfg: str, steps: int, warmup: int, cpu: bool, cp
         "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
-                     "kernel": ("gemm_f32_lds_dma (all 3 layouts, every launch of the roofline pass)" if cfg == "c5"
+                     "kernel": ("gemm_f32_w16 (all 3 layouts, every launch of the roofline pass)" if cfg == "c5"
                                 else "every GEMM launch of the roofline pass (gemm_f32_mfma tiles, the skinny "
                                      "kernel for N <= 16, split-K where the output has few tiles)"),
                      "flop_per_launch": per_launch_flops,
