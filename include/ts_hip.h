@@ -375,7 +375,11 @@ int ts_hip_matmul(const float *a, const float *b, float *c, size_t m, size_t n, 
  *   trans_b == 0: B(k,j) = B[k*ldb + j]   (B stored [K][ldb])
  *   trans_b == 1: B(k,j) = B[j*ldb + k]   (B stored [N][ldb], i.e. B^T view)
  *   C(i,j) = C[i*ldc + j]
- * fp32 inputs, fp32 MFMA accumulation (v_mfma_f32_32x32x2_f32).  M, N, K and
+ * fp32 inputs, fp32 MFMA accumulation (v_mfma_f32_16x16x4_f32 when M and N
+ * are multiples of 256, K of 32 and the grid has a 256x256 tile per CU; else
+ * v_mfma_f32_32x32x2_f32: the two add k in different groupings, so a product's
+ * last bits depend on which it takes; every entry point below takes the same
+ * one for the same shape, layout and alignment).  M, N, K and
  * the leading dimensions must be below 2^31 (TS_HIP_EINVAL otherwise).  For
  * few output tiles with a long K (e.g. M = 32, K = 784) the call splits K and
  * takes a temporary of up to 16*M*N floats from the stream-ordered allocator
