@@ -194,7 +194,9 @@ def _train_both(TS, G, ws, x, t, steps, readme=False, lr=1e-3, max_excluded=0.01
     fp32-determined sign, so two correct implementations move the element by
     up to ~lr in opposite directions.  The set is computed from the oracle
     alone; its size must stay below `max_excluded` of the elements and each
-    excluded element within steps * lr of the oracle.  Returns the report."""
+    excluded element within EXCLUDED_MAX_ABS of the oracle (the bound that
+    selects them is a worst case far above the rounding seen).  Returns the
+    report."""
     pd = [TS.Tensor.from_slice(v, v.shape).with_requires_grad() for v in ws]
     po = [G.OTensor(v.copy()).with_requires_grad() for v in ws]
     opt, oopt = TS.Adam.with_learning_rate(lr), G.OAdam(lr)
@@ -421,7 +423,8 @@ def test_config5_scaled_mlp_100_steps(TS, G):
 def test_wide_mlp_10_steps_on_the_lds_dma_kernel(TS, G):
     # 2 x Linear(4096, 4096) at batch 4096, ReLU after the first, MSE: every
     # product (forward, dX, dW) has 256 output tiles of 256 x 256, one per CU,
-    # so each takes the LDS-DMA kernel that carries config 5 (with its fused
+    # so each takes the LDS-DMA kernel that carries config 5 (gemm_f32_w16,
+    # its exact tiling; with its fused
     # bias + ReLU store, the ReLU-backward mask in the dX store and the bias
     # gradient in the dW product); 10 steps, per-element parameter bar
     ws, rng = _mlp_weights([4096] * 3, 3, "normal")
