@@ -82,23 +82,33 @@ def test_w16_column_sums(oracle, K):
     assert_bits_equal(c_new.get(), c_ref.get(), "product with and without the column sums")
 
 
-def test_w16_tn_epilogue():
-    # bias, relu and the mask in the TN kernel's stores: the separate kernels' bits
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+@pytest.mark.parametrize("bias,relu,mask", [(1, 1, 1), (1, 0, 0), (0, 1, 0), (0, 0, 1), (1, 1, 0)])
+def test_w16_epilogues(ta, tb, bias, relu, mask):
+    # bias, relu and the relu-backward mask in the kernel's stores, every
+    # combination on every layout it takes: the separate kernels' bits
     from gpu_util import Dev, hip, hip_check, sync
 
     M = N = 4096
     K = 64
-    a, b = normal((K, M), 25), normal((K, N), 26)
-    bias, mask = normal(N, 27), normal((M, N), 28)
-    da, db, dbias, dmask = Dev.of(a), Dev.of(b), Dev.of(bias), Dev.of(mask)
+    print(f"[w16 epilogue] ta={ta} tb={tb} bias={bias} relu={relu} mask={mask}", flush=True)
+    a = normal((K, M) if ta else (M, K), 25)
+    b = normal((N, K) if tb else (K, N), 26)
+    vb, vm = normal(N, 27), normal((M, N), 28)
+    da, db, dbias, dmask = Dev.of(a), Dev.of(b), Dev.of(vb), Dev.of(vm)
+    lda, ldb = a.shape[1], b.shape[1]
     fused, ref = Dev(M * N), Dev(M * N)
     ws = hip.ts_hip_gemm_workspace_floats(M, N, K)
     dws = Dev(max(ws, 1))
-    hip_check(hip.ts_hip_gemm_fused(1, 0, M, N, K, da.ptr, M, db.ptr, N, dbias.ptr, 1, dmask.ptr, fused.ptr, N,
-                                    dws.ptr if ws else None, ws, None), "ts_hip_gemm_fused")
-    hip_check(hip.ts_hip_gemm(1, 0, M, N, K, da.ptr, M, db.ptr, N, ref.ptr, N, None), "ts_hip_gemm")
-    hip_check(hip.ts_hip_bias_add(ref.ptr, dbias.ptr, ref.ptr, M, N, 0, None), "bias")
-    hip_check(hip.ts_hip_relu(ref.ptr, ref.ptr, M * N, None), "relu")
-    hip_check(hip.ts_hip_relu_backward(dmask.ptr, ref.ptr, ref.ptr, M * N, None), "mask")
+    hip_check(hip.ts_hip_gemm_fused(ta, tb, M, N, K, da.ptr, lda, db.ptr, ldb, dbias.ptr if bias else None, relu,
+                                    dmask.ptr if mask else None, fused.ptr, N, dws.ptr if ws else None, ws, None),
+              "ts_hip_gemm_fused")
+    hip_check(hip.ts_hip_gemm(ta, tb, M, N, K, da.ptr, lda, db.ptr, ldb, ref.ptr, N, None), "ts_hip_gemm")
+    if bias:
+        hip_check(hip.ts_hip_bias_add(ref.ptr, dbias.ptr, ref.ptr, M, N, 0, None), "bias")
+    if relu:
+        hip_check(hip.ts_hip_relu(ref.ptr, ref.ptr, M * N, None), "relu")
+    if mask:
+        hip_check(hip.ts_hip_relu_backward(dmask.ptr, ref.ptr, ref.ptr, M * N, None), "mask")
     sync()
-    assert_bits_equal(fused.get(), ref.get(), "TN with bias, relu and mask")
+    assert_bits_equal(fused.get(), ref.get(), f"ta={ta} tb={tb} bias={bias} relu={relu} mask={mask}")
