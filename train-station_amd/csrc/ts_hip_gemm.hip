@@ -1255,8 +1255,8 @@ __global__ __launch_bounds__(512) void gemm_f32_w16(GemmArgs g) {
 
     // store, with the epilogue of store_tile (bias, relu, then the mask); the
     // bias loaded once and each row group's 16 mask vectors before its first
-    // store, each batch awaited once (awaited one by one, the NT product with
-    // its mask ran 5% slower)
+    // store, each batch awaited once (each vector loaded just before its
+    // store, every load's latency was waited out in turn)
     float *Cp = g.C;
     const bool vec = ((reinterpret_cast<uintptr_t>(Cp) & 15) == 0) && (g.ldc % 4 == 0) &&
                      (EPI != kEpiAll || !g.mask || (reinterpret_cast<uintptr_t>(g.mask) & 15) == 0);
