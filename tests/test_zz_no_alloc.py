@@ -20,9 +20,10 @@ SCRATCH_FLOATS = 1 << 21
 # (trans_a, trans_b, M, N, K): the first two split K (few output tiles and a
 # K longer than the one-pass narrow kernel takes), the second's slices smaller
 # than the first's; then a product the narrow kernel takes (the README step's
-# forward shape: no scratch), an unsplit tiled product and an empty contraction
+# forward shape: no scratch), an unsplit tiled product, two on the 16x16x4
+# kernel of exact 256x256 tilings and an empty contraction
 CASES = [(0, 0, 32, 128, 16384), (1, 0, 16, 64, 8448), (0, 0, 32, 128, 784), (0, 1, 300, 260, 130),
-         (0, 0, 8, 8, 0)]
+         (1, 0, 4096, 4096, 64), (0, 1, 4096, 4096, 64), (0, 0, 8, 8, 0)]
 
 
 def _operands(ta, tb, M, N, K, seed):
