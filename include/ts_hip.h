@@ -452,7 +452,8 @@ int ts_hip_gemm_fused_sub(int trans_a, int trans_b, size_t M, size_t N, size_t K
  * or from the rows its first workgroup holds (N <= 16); other shapes take a
  * column-sum pass after the product.  M == 0 gives the column sums alone.
  * Workspace as ts_hip_gemm_colsum_workspace_floats (8-byte aligned; NULL:
- * taken from the stream-ordered allocator). */
+ * taken from the stream-ordered allocator, whose error is returned when it
+ * cannot give it: hipErrorOutOfMemory for a full device). */
 size_t ts_hip_gemm_colsum_workspace_floats(int trans_a, size_t M, size_t N, size_t K);
 int ts_hip_gemm_colsum(int trans_a, size_t M, size_t N, size_t K, const float *A, size_t lda, const float *B,
                        size_t ldb, float *C, size_t ldc, float *colsum, float *workspace, size_t workspace_floats,

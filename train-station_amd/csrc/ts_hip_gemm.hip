@@ -2194,15 +2194,16 @@ static int gemm_plain(int trans_a, int trans_b, size_t M, size_t N, size_t K, co
     if (need && ws && (ws_floats < need || (plan.part_floats && (reinterpret_cast<uintptr_t>(ws) & 7u))))
         return TS_HIP_EWORKSPACE;
     if (need && !W) {
-        if (hipMallocAsync(reinterpret_cast<void **>(&W), need * sizeof(float), st) == hipSuccess) {
+        const hipError_t ae = hipMallocAsync(reinterpret_cast<void **>(&W), need * sizeof(float), st);
+        if (ae == hipSuccess) {
             owned = true;
         } else {
             (void)hipGetLastError();
             W = nullptr;
-            // no stream-ordered allocator: an MFMA split runs unsplit; the
-            // rest needs the caller's workspace
-            if (plan.skinny && plan.slices > 1) return TS_HIP_EINVAL;
-            if (plan.part_floats) return TS_HIP_EINVAL;
+            // no stream-ordered memory: an MFMA split runs unsplit; the rest
+            // needs memory, and the allocator's error is returned
+            // (hipErrorOutOfMemory when the device is full)
+            if ((plan.skinny && plan.slices > 1) || plan.part_floats) return static_cast<int>(ae);
         }
     }
     double *part = plan.part_floats ? reinterpret_cast<double *>(W + plan.part_offset()) : nullptr;
