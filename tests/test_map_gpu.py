@@ -167,6 +167,29 @@ def test_fused_sum_has_the_bits_of_ts_hip_sum(n, mean):
     assert_bits_equal(out.get(), np.array([model], np.float32), f"partition order n={n}")
 
 
+def test_fused_sum_with_longer_runs():
+    # past 2^28 elements a first-pass thread of the sum's partition takes five
+    # float4 groups: the fused sum keeps ts_hip_sum's bits and the model's
+    from gpu_util import Dev, hip, hip_check, sync
+    n = (1 << 28) + 8
+    print(f"[map fused sum] n={n}", flush=True)
+    y = normal(n, 9)
+    dy, d, out = Dev.of(y), Dev(n), Dev(1)
+    ws = hip.ts_hip_map_workspace_floats(n)
+    dws = Dev(ws + 2)
+    # d = y * y stored; the sum of d
+    prog = _program([dy.ptr], [("square", 0, 0, 0.0, 0)], [(d.ptr, R0)], reduce_reg=R0)
+    hip_check(hip.ts_hip_map(ctypes.byref(prog), n, 8 * (n // 8), 32 * (n // 32), None, out.ptr, 0, dws.ptr, ws,
+                             None), "map")
+    want = Dev(1)
+    sw = hip.ts_hip_sum_workspace_floats(n)
+    dsw = Dev(sw + 2)
+    hip_check(hip.ts_hip_sum(d.ptr, n, want.ptr, dsw.ptr, sw, None), "sum")
+    sync()
+    assert_bits_equal(out.get(), want.get(), "fused sum vs ts_hip_sum")
+    assert_bits_equal(out.get(), np.array([sum_order_model((y * y).astype(np.float32))], np.float32), "model")
+
+
 @pytest.mark.parametrize("n", [7, 4099])
 def test_constant_inputs_match_a_filled_buffer(n):
     # a constant input is the value ts_hip_fill writes: every op reading it,
